@@ -1,0 +1,268 @@
+#!/usr/bin/env python3
+"""Benchmark of the SSLA hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Headline workload: chunked GLA forward, B=8 sequences x
+T=4096 tokens, H=8, K=V=64, chunk 64, bf16 q/k/v/o, fp32 g/h0/ht.  One
+"step" = one call of ssla_gla_chunk_fwd over the whole batch with inputs
+already resident in HBM.  Two input sets (2 x 203 MB, more than the 256 MB
+Infinity Cache) alternate so that the timed loop streams from HBM.
+
+Secondary lines (same JSON object): the per-site sparse GLA scan (config 3,
+64 bins per step) and the scatter-max pooling (config 4, 1e6 events).
+
+Prints ONE JSON line.  Kernel durations come from HIP events recorded on
+the stream the kernels are launched on (torch's current stream, which is
+the stream handed to the C-ABI).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+
+C2 = dict(B=8, T=4096, H=8, D=64)
+
+
+def c2_bytes():
+    Tt, H, D = C2["B"] * C2["T"], C2["H"], C2["D"]
+    # q, k, v bf16 + g fp32 read, o bf16 written, h0 read + ht written fp32
+    return 3 * Tt * H * D * 2 + Tt * H * D * 4 + Tt * H * D * 2 + 2 * C2["B"] * H * D * D * 4
+
+
+def c2_flops():
+    Tt, H, D = C2["B"] * C2["T"], C2["H"], C2["D"]
+    BT = 64
+    # causal-useful: T*H*[(BT+1)(K+V) + 4KV]
+    return Tt * H * ((BT + 1) * (D + D) + 4 * D * D)
+
+
+def _traffic_from_profile(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration), read from the
+    committed summary profiles/<name>; None if absent."""
+    p = ROOT / "profiles" / name
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].strip().split()[0])
+            except ValueError:
+                return None
+    return None
+
+
+def bench_chunk(torch, lib, steps, warmup, dev):
+    from ssla_amd import _lib, synthetic
+    sets = []
+    for seed in (0, 1):
+        x = synthetic.chunk_gla_inputs(seed=seed, device=dev)
+        x["o"] = torch.empty_like(x["v"])
+        x["ht"] = torch.empty_like(x["initial_state"])
+        sets.append(x)
+    Tt, H, D = C2["B"] * C2["T"], C2["H"], C2["D"]
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def launch(x):
+        st = lib.ssla_gla_chunk_fwd(
+            x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(), _lib.SSLA_F32,
+            x["cu_seqlens"].data_ptr(), C2["B"], Tt, H, D, D, float(x["scale"]),
+            x["initial_state"].data_ptr(), x["o"].data_ptr(), x["ht"].data_ptr(), _lib.SSLA_BF16,
+            None, 0, sh)
+        _lib.check(st, "ssla_gla_chunk_fwd")
+
+    for i in range(warmup):
+        launch(sets[i % 2])
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        launch(sets[i % 2])
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    avg_ms = sum(kern_ms) / len(kern_ms)
+    return dict(wall_s=wall, kernel_avg_ms=avg_ms, kernel_median_ms=kern_ms[len(kern_ms) // 2],
+                tokens=Tt, sample=sets[0])
+
+
+def bench_sparse(torch, lib, reps, dev):
+    """Config 3: 64 bins of per-site GLA updates, bin by bin."""
+    from ssla_amd import _lib, synthetic
+    sb = synthetic.sparse_scan_bins()
+    state = sb.state0.to(dev).contiguous()
+    bins = []
+    for b in range(len(sb.sites)):
+        bins.append(dict(s=torch.from_numpy(sb.sites[b]).to(dev), q=sb.q[b].to(dev), k=sb.k[b].to(dev),
+                         v=sb.v[b].to(dev), g=sb.g[b].to(dev),
+                         o=torch.empty(sb.sites[b].size, 4, 32, device=dev)))
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def one_pass():
+        for x in bins:
+            st = lib.ssla_sparse_gla_step(x["s"].data_ptr(), x["s"].numel(), x["q"].data_ptr(),
+                                          x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
+                                          state.data_ptr(), sb.n_sites, 4, 32, 32, float(sb.scale),
+                                          x["o"].data_ptr(), sh)
+            _lib.check(st, "ssla_sparse_gla_step")
+
+    one_pass()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        one_pass()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    steps = sb.site_steps
+    per_step_bytes = 4 * (2 * 4 * 32 * 32 + 3 * 4 * 32 + 2 * 4 * 32) + 4
+    gbs = steps * per_step_bytes / (ms * 1e-3) / 1e9
+    return {"workload": "sparse_gla_step config 3: 76x60 sites, 64 bins, H=4, K=V=32, fp32",
+            "metric": "sparse scan site-steps/s", "value": steps / (ms * 1e-3), "unit": "site-steps/s",
+            "ms_per_pass": ms, "site_steps_per_pass": steps, "launches_per_pass": len(bins),
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "bytes_per_site_step": per_step_bytes,
+                         "note": "per-pass average over 64 launches, launch gaps included"}}
+
+
+def bench_pool(torch, lib, reps, dev):
+    """Config 4: scatter_max of 1e6 clustered events (C=64) into 152x120 cells."""
+    from ssla_amd import _lib, synthetic
+    sets = []
+    for seed in (0, 1):
+        src, index, n_out = synthetic.pooling_events(seed=seed)
+        sets.append(dict(src=src.to(dev), idx=index.to(dev)))
+    E, C = sets[0]["src"].shape
+    ws_bytes = lib.ssla_scatter_workspace_size(E, C, n_out)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(n_out, C, device=dev)
+    arg = torch.empty(n_out, C, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def call(x):
+        st = lib.ssla_scatter_max(x["src"].data_ptr(), x["idx"].data_ptr(), E, C, n_out, 0,
+                                  out.data_ptr(), arg.data_ptr(), ws.data_ptr(), ws_bytes, sh)
+        _lib.check(st, "ssla_scatter_max")
+
+    for i in range(3):
+        call(sets[i % 2])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        call(sets[i % 2])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    alg = E * (4 * C + 4) + n_out * C * (4 + 8)
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": "scatter_max config 4: 1e6 shuffled events, C=64, 18240 cells",
+            "metric": "pooling events/s", "value": E / (ms * 1e-3), "unit": "events/s",
+            "ms_per_call": ms,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes": alg,
+                         "note": "whole call (bucketing + reduce), not one kernel"}}
+
+
+def cpu_baseline(x, budget_s=20.0):
+    """The fp64 C restatement of naive_gla_recurrent (oracle/) on this host,
+    over whole sequences of the same C2 batch until ~budget_s of work."""
+    import numpy as np
+    import oracle
+    q = x["q"].float().cpu().numpy()
+    k = x["k"].float().cpu().numpy()
+    v = x["v"].float().cpu().numpy()
+    g = x["g"].cpu().numpy()
+    h0 = x["initial_state"].cpu().numpy()
+    cu = x["cu_seqlens"].cpu().numpy()
+    T = int(cu[1] - cu[0])
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    oracle.load()
+    done_tok, t_used, n = 0, 0.0, 0
+    while n < len(cu) - 1 and t_used < budget_s:
+        s, e = int(cu[n]), int(cu[n + 1])
+        t0 = time.perf_counter()
+        oracle.gla_recurrent(q[s:e], k[s:e], v[s:e], g[s:e], np.array([0, e - s]), float(x["scale"]),
+                             h0[n:n + 1], True)
+        t_used += time.perf_counter() - t0
+        done_tok += e - s
+        n += 1
+    rate = done_tok / t_used / 1e6
+    return {"value": rate, "unit": "Mtok/s", "cores": min(threads, 8),
+            "kind": "port",
+            "sample": f"{n} of {len(cu) - 1} sequences ({done_tok} tokens x 8 heads) of the same batch, "
+                      f"fp64 C restatement of naive_gla_recurrent, OpenMP over heads, {t_used:.2f} s",
+            "host_cpus": os.cpu_count()}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the hot path is single-GPU; "
+              "see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+    from ssla_amd import _lib
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    lib = _lib.load()
+    r = bench_chunk(torch, lib, args.steps, args.warmup, dev)
+    ms_step = r["wall_s"] * 1e3 / args.steps
+    value = r["tokens"] / (r["wall_s"] / args.steps) / 1e6
+    kern_s = r["kernel_avg_ms"] * 1e-3
+    alg_bytes = c2_bytes()
+    achieved = alg_bytes / kern_s / 1e9
+    traffic = _traffic_from_profile("gla_chunk_fwd_c2_pmc.txt")
+    tflops = c2_flops() / kern_s / 1e12
+    line = {
+        "metric": "GLA chunk fwd Mtok/s (%bf16 MFMA peak); sparse scan site-steps/s (%HBM BW)",
+        "value": value, "unit": "Mtok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "chunk_gla_fwd (BASELINE config 2): B=8, H=8, T=4096, K=V=64, chunk 64; "
+                               "bf16 q/k/v/o, fp32 g/h0/ht; 2 input sets alternating (> MALL)",
+                   "global_batch": C2["B"], "seq_len": C2["T"], "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": "gla_chunk_fwd_kernel", "kernel_avg_us": r["kernel_avg_ms"] * 1e3,
+                     "algorithmic_bytes": alg_bytes},
+        "mfma": {"achieved": tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                 "frac": tflops / BF16_PEAK_TFLOPS, "flops_per_launch": c2_flops(),
+                 "note": "causal-useful flops; the shape is HBM-bound (31.8 flop/B < 312 ridge)"},
+    }
+    if not args.no_secondary:
+        line["secondary"] = [bench_sparse(torch, lib, 10, dev), bench_pool(torch, lib, 20, dev)]
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(r["sample"])
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,213 @@
+/*
+ * oracle.c -- CPU restatement of the reference (haohq19/ssla) hot-path
+ * arithmetic, used ONLY as the checker in tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg.  Nothing in the product (ssla_amd/)
+ * links or calls it.
+ *
+ * All GLA / scan arithmetic is done in double precision on fp32 inputs, so
+ * the oracle is more accurate than both the reference and the GPU path.
+ * Build: python -m oracle.build  (gcc -O2 -shared -fPIC, -fopenmp).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define IDX3(t, h, d, H, D) (((int64_t)(t) * (H) + (h)) * (D) + (d))
+
+/* naive_gla_recurrent (reference ops/gla/naive.py:50-111):
+ *   S_t = exp(g_t)[:, None] * S_{t-1} + k_t v_t^T ;  o_t = (q_t * scale) . S_t
+ * o_t uses the UPDATED state (naive.py:97-100).  h0 may be NULL (zeros,
+ * naive.py:84-90); ht may be NULL (naive.py:103-104).  Parallel over
+ * (sequence, head). */
+void oracle_gla_recurrent(const float *q, const float *k, const float *v, const float *g,
+                          const int64_t *cu, int n_seq, int H, int K, int V, double scale,
+                          const float *h0, double *o, double *ht) {
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int n = 0; n < n_seq; ++n) {
+    for (int h = 0; h < H; ++h) {
+      double *S = (double *)malloc(sizeof(double) * K * V);
+      for (int i = 0; i < K * V; ++i)
+        S[i] = h0 ? (double)h0[((int64_t)n * H + h) * K * V + i] : 0.0;
+      for (int64_t t = cu[n]; t < cu[n + 1]; ++t) {
+        for (int kk = 0; kk < K; ++kk) {
+          const double d = exp((double)g[IDX3(t, h, kk, H, K)]);
+          const double kv = (double)k[IDX3(t, h, kk, H, K)];
+          for (int vv = 0; vv < V; ++vv)
+            S[kk * V + vv] = d * S[kk * V + vv] + kv * (double)v[IDX3(t, h, vv, H, V)];
+        }
+        for (int vv = 0; vv < V; ++vv) {
+          double acc = 0.0;
+          for (int kk = 0; kk < K; ++kk)
+            acc += (double)q[IDX3(t, h, kk, H, K)] * scale * S[kk * V + vv];
+          o[IDX3(t, h, vv, H, V)] = acc;
+        }
+      }
+      if (ht)
+        for (int i = 0; i < K * V; ++i) ht[((int64_t)n * H + h) * K * V + i] = S[i];
+      free(S);
+    }
+  }
+}
+
+/* Chunked form of the same map, restating the reference forward pipeline
+ * chunk_gla_fwd (reference ops/gla/chunk.py:906-960) with fp64 everywhere:
+ *   1. G = chunk-local inclusive cumsum of g, restarting every BT rows of each
+ *      sequence (ops/utils/cumsum.py:61-90, chunk indices ops/utils/index.py:69-77);
+ *   2. entering state per chunk h[c]; S <- diag(e^{G_last}) S + (K e^{G_last-G})^T V
+ *      (ops/common/chunk_h.py:66-123, chunk_h_naive.py:58-87);
+ *   3. A_ij = scale sum_k q_ik k_jk e^{G_ik - G_jk}, j <= i (ops/gla/chunk.py:33-176);
+ *   4. o = (q scale e^{G}) h[c] + tril(A) v (ops/gla/chunk.py:189-249).
+ * Used to cross-check oracle_gla_recurrent (a different algorithm). */
+void oracle_gla_chunk(const float *q, const float *k, const float *v, const float *g,
+                      const int64_t *cu, int n_seq, int H, int K, int V, double scale,
+                      const float *h0, int BT, double *o, double *ht) {
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int n = 0; n < n_seq; ++n) {
+    for (int h = 0; h < H; ++h) {
+      double *S = (double *)malloc(sizeof(double) * K * V);
+      double *G = (double *)malloc(sizeof(double) * BT * K);
+      double *A = (double *)malloc(sizeof(double) * BT * BT);
+      for (int i = 0; i < K * V; ++i)
+        S[i] = h0 ? (double)h0[((int64_t)n * H + h) * K * V + i] : 0.0;
+      const int64_t bos = cu[n], eos = cu[n + 1];
+      for (int64_t c0 = bos; c0 < eos; c0 += BT) {
+        const int L = (int)((eos - c0) < BT ? (eos - c0) : BT);
+        for (int kk = 0; kk < K; ++kk) {
+          double run = 0.0;
+          for (int i = 0; i < L; ++i) {
+            run += (double)g[IDX3(c0 + i, h, kk, H, K)];
+            G[i * K + kk] = run;
+          }
+        }
+        for (int i = 0; i < L; ++i)
+          for (int j = 0; j < L; ++j) {
+            double a = 0.0;
+            if (j <= i)
+              for (int kk = 0; kk < K; ++kk)
+                a += (double)q[IDX3(c0 + i, h, kk, H, K)] * (double)k[IDX3(c0 + j, h, kk, H, K)] *
+                     exp(G[i * K + kk] - G[j * K + kk]);
+            A[i * BT + j] = a * scale;
+          }
+        for (int i = 0; i < L; ++i)
+          for (int vv = 0; vv < V; ++vv) {
+            double acc = 0.0;
+            for (int kk = 0; kk < K; ++kk)
+              acc += (double)q[IDX3(c0 + i, h, kk, H, K)] * scale * exp(G[i * K + kk]) * S[kk * V + vv];
+            for (int j = 0; j <= i; ++j) acc += A[i * BT + j] * (double)v[IDX3(c0 + j, h, vv, H, V)];
+            o[IDX3(c0 + i, h, vv, H, V)] = acc;
+          }
+        const int last = L - 1;
+        for (int kk = 0; kk < K; ++kk) {
+          const double gl = G[last * K + kk];
+          const double d = exp(gl);
+          for (int vv = 0; vv < V; ++vv) {
+            double acc = d * S[kk * V + vv];
+            for (int j = 0; j < L; ++j)
+              acc += (double)k[IDX3(c0 + j, h, kk, H, K)] * exp(gl - G[j * K + kk]) *
+                     (double)v[IDX3(c0 + j, h, vv, H, V)];
+            S[kk * V + vv] = acc;
+          }
+        }
+      }
+      if (ht)
+        for (int i = 0; i < K * V; ++i) ht[((int64_t)n * H + h) * K * V + i] = S[i];
+      free(S);
+      free(G);
+      free(A);
+    }
+  }
+}
+
+/* sequential_scan_fwd (reference ops/common/scan.py:20-43, :93-114):
+ * h = zeros_like(u); per sequence and channel h_t = h_{t-1} * g_t + u_t with
+ * h_{bos-1} = 0.  Rows outside all sequences stay 0. */
+void oracle_diag_scan(const float *u, const float *g, const int64_t *cu, int n_seq, int64_t T,
+                      int C, double *h) {
+  memset(h, 0, sizeof(double) * (size_t)T * C);
+#pragma omp parallel for schedule(dynamic)
+  for (int n = 0; n < n_seq; ++n) {
+    for (int c = 0; c < C; ++c) {
+      double s = 0.0;
+      for (int64_t t = cu[n]; t < cu[n + 1]; ++t) {
+        s = s * (double)g[t * C + c] + (double)u[t * C + c];
+        h[t * C + c] = s;
+      }
+    }
+  }
+}
+
+/* One bin of the per-site state update (naive_gla_recurrent on a length-1
+ * sequence per active site, initial state = stored fp32 state, final state
+ * stored back as fp32).  Inactive rows of `state` are not touched. */
+void oracle_sparse_gla_step(const int32_t *site, int n_active, const float *q, const float *k,
+                            const float *v, const float *g, float *state, int H, int K, int V,
+                            double scale, double *o) {
+#pragma omp parallel for collapse(2)
+  for (int i = 0; i < n_active; ++i) {
+    for (int h = 0; h < H; ++h) {
+      float *S = state + ((int64_t)site[i] * H + h) * K * V;
+      const int64_t io = (int64_t)i * H + h;
+      double acc[256];
+      for (int vv = 0; vv < V; ++vv) acc[vv] = 0.0;
+      for (int kk = 0; kk < K; ++kk) {
+        const double d = exp((double)g[io * K + kk]);
+        const double kv = (double)k[io * K + kk];
+        const double qs = (double)q[io * K + kk] * scale;
+        for (int vv = 0; vv < V; ++vv) {
+          const double s = d * (double)S[kk * V + vv] + kv * (double)v[io * V + vv];
+          acc[vv] += qs * s;
+          S[kk * V + vv] = (float)s;
+        }
+      }
+      for (int vv = 0; vv < V; ++vv) o[io * V + vv] = acc[vv];
+    }
+  }
+}
+
+/* torch_scatter.scatter_max along dim 0 with a row index (documented
+ * semantics; called at reference layers/sparse_pooling.py:33): events are
+ * visited in index order, a strictly greater value replaces the running
+ * maximum, so among equal maxima (floating-point ==) the smallest event
+ * index wins.  Empty rows: out = 0, argmax = E.  out gets src[argmax]'s
+ * bits. */
+void oracle_scatter_max(const float *src, const int64_t *index, int64_t E, int C, int64_t n_out,
+                        float *out, int64_t *argmax) {
+  for (int64_t i = 0; i < n_out * C; ++i) {
+    out[i] = 0.f;
+    argmax[i] = -1;
+  }
+  for (int64_t e = 0; e < E; ++e) {
+    const int64_t r = index[e];
+    for (int c = 0; c < C; ++c) {
+      const float x = src[e * C + c];
+      int64_t *a = &argmax[r * C + c];
+      if (*a < 0 || x > src[*a * C + c]) *a = e;
+    }
+  }
+  for (int64_t i = 0; i < n_out * C; ++i) {
+    if (argmax[i] < 0) {
+      argmax[i] = E;
+      out[i] = 0.f;
+    } else {
+      out[i] = src[argmax[i] * C + (i % C)];
+    }
+  }
+}
+
+/* torch_scatter.scatter_mean along dim 0: sum / max(count, 1) (fp64 sum). */
+void oracle_scatter_mean(const float *src, const int64_t *index, int64_t E, int C, int64_t n_out,
+                         double *out) {
+  int64_t *cnt = (int64_t *)calloc((size_t)(n_out > 0 ? n_out : 1), sizeof(int64_t));
+  for (int64_t i = 0; i < n_out * C; ++i) out[i] = 0.0;
+  for (int64_t e = 0; e < E; ++e) {
+    const int64_t r = index[e];
+    cnt[r] += 1;
+    for (int c = 0; c < C; ++c) out[r * C + c] += (double)src[e * C + c];
+  }
+  for (int64_t r = 0; r < n_out; ++r) {
+    const double d = (double)(cnt[r] > 0 ? cnt[r] : 1);
+    for (int c = 0; c < C; ++c) out[r * C + c] /= d;
+  }
+  free(cnt);
+}

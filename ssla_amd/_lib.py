@@ -1,0 +1,114 @@
+"""ctypes binding of libssla_amd.so (the C-ABI declared in include/ssla_amd.h).
+
+Only plain pointers, sizes and a stream handle cross this boundary.  The
+library is loaded lazily on first use; when it is missing or cannot be
+loaded every entry point raises -- there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libssla_amd.so"
+
+SSLA_OK = 0
+SSLA_ERR_ARG = -1
+SSLA_ERR_DTYPE = -2
+SSLA_ERR_WORKSPACE = -3
+SSLA_ERR_LAUNCH = -4
+SSLA_ERR_UNSUPPORTED = -5
+
+SSLA_F32, SSLA_BF16, SSLA_F16 = 0, 1, 2
+DTYPE_CODE = {torch.float32: SSLA_F32, torch.bfloat16: SSLA_BF16, torch.float16: SSLA_F16}
+
+_vp, _i32, _i64, _f32, _sz = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
+
+# name -> (restype, argtypes); must match include/ssla_amd.h
+SIGNATURES = {
+    "ssla_version": (_i32, []),
+    "ssla_last_error": (C.c_char_p, []),
+    "ssla_gla_chunk_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32,
+                                  _f32, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
+    "ssla_gla_recurrent_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32,
+                                      _f32, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
+    "ssla_diag_scan_fwd": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _vp, _vp]),
+    "ssla_sparse_gla_step": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
+                                    _f32, _vp, _vp]),
+    "ssla_scatter_workspace_size": (_sz, [_i64, _i32, _i64]),
+    "ssla_scatter_max": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "ssla_scatter_mean": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _sz, _vp]),
+    "ssla_scatter_check": (_i32, [_vp, C.POINTER(_i32), _vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class SslaError(RuntimeError):
+    """Launch or workspace failure reported by libssla_amd."""
+
+
+def load() -> C.CDLL:
+    """Load (once) and return the library; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = Path(os.environ.get("SSLA_AMD_LIB", LIB_PATH))
+            if not path.exists():
+                raise ImportError(
+                    f"{path} is missing: build it with `python -m ssla_amd.build` "
+                    "(the HIP path has no fallback)")
+            lib = C.CDLL(str(path))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status == SSLA_OK:
+        return
+    msg = load().ssla_last_error().decode(errors="replace") or what
+    if status == SSLA_ERR_ARG:
+        raise ValueError(msg)
+    if status == SSLA_ERR_DTYPE:
+        raise TypeError(msg)
+    if status == SSLA_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise SslaError(f"{msg} (status {status})")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_cuda(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("ssla_amd kernels need device tensors (got a CPU tensor)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def require_no_grad(name: str, *tensors: torch.Tensor) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise NotImplementedError(f"{name}: only the forward pass is implemented "
+                                  "(call it under torch.no_grad())")

@@ -1,0 +1,149 @@
+"""Gated linear attention (GLA) forward on MI355X.
+
+Drop-in for the reference's GLA API (haohq19/ssla ``ops/gla``):
+
+* :func:`chunk_gla` -- ``chunk_gla(q, k, v, g, cu_seqlens, scale=None,
+  initial_state=None, output_final_state=False) -> (o, final_state)``
+  (reference ops/gla/chunk.py:1119-1167).
+* :func:`fused_recurrent_gla` (alias :func:`naive_gla_recurrent`) -- the
+  recurrent form with the signature of ``naive_gla_recurrent``
+  (reference ops/gla/naive.py:50-111).
+
+Both are forward-only and run hand-written gfx950 kernels through
+libssla_amd.so; there is no CPU or Triton fallback.  Layouts are the
+reference's packed varlen layouts: q, k, g ``[T, H, K]``, v ``[T, H, V]``,
+``cu_seqlens`` int64 ``[N + 1]``, states ``[N, H, K, V]`` fp32.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+__all__ = ["chunk_gla", "fused_recurrent_gla", "naive_gla_recurrent", "chunk_kernel_supports"]
+
+
+def chunk_kernel_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
+    """True when the fused MFMA chunk kernel handles this dtype/shape
+    (bf16/fp16, K == 64, V a multiple of 16 up to 256)."""
+    return (q.dtype in (torch.bfloat16, torch.float16) and q.shape[-1] == 64
+            and v.shape[-1] % 16 == 0 and v.shape[-1] <= 256)
+
+
+def _prep(name, q, k, v, g, cu_seqlens, initial_state):
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (g, "g")):
+        if t.dim() != 3:
+            raise ValueError(f"{name}: {nm} must be [T, H, D], got shape {tuple(t.shape)}")
+    if q.shape != k.shape or q.shape != g.shape:
+        raise ValueError(f"{name}: q, k, g shapes differ: {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{tuple(g.shape)}")
+    if v.shape[:2] != q.shape[:2]:
+        raise ValueError(f"{name}: v shape {tuple(v.shape)} does not match q {tuple(q.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"{name}: q, k, v must share a dtype ({q.dtype}, {k.dtype}, {v.dtype})")
+    if q.dtype not in _lib.DTYPE_CODE:
+        raise TypeError(f"{name}: unsupported dtype {q.dtype}")
+    dev = _lib.require_cuda(q, k, v, g, initial_state)
+    _lib.require_no_grad(name, q, k, v, g, initial_state)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if g.dtype != torch.float32 and g.dtype != q.dtype:
+        g = g.float()
+    g = g.contiguous()
+    cu = cu_seqlens.to(device=dev, dtype=torch.int64).contiguous()
+    h0 = None
+    if initial_state is not None:
+        h0 = initial_state.to(dtype=torch.float32).contiguous()
+    return q, k, v, g, cu, h0
+
+
+def chunk_gla(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    cu_seqlens: torch.LongTensor,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Chunked GLA forward (reference ops/gla/chunk.py:1119-1167).
+
+    Returns ``o`` (dtype of v, ``[T, H, V]``) and the fp32 final state
+    ``[N, H, K, V]`` when ``output_final_state`` (else None).  Rows of o
+    outside ``[cu_seqlens[0], cu_seqlens[-1])`` are unspecified, as in the
+    reference (``torch.empty_like``).
+
+    bf16/fp16 inputs with K == 64 run the fused MFMA chunk kernel; other
+    shapes and fp32 inputs run the fused recurrent kernel (same math, fp32
+    state, serial over time).
+    """
+    if initial_state is not None and initial_state.shape[0] != len(cu_seqlens) - 1:
+        raise ValueError(
+            f"The number of initial states is expected to be equal to the number of input sequences, "
+            f"i.e., {len(cu_seqlens) - 1} rather than {initial_state.shape[0]}."
+        )
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    q, k, v, g, cu, h0 = _prep("chunk_gla", q, k, v, g, cu_seqlens, initial_state)
+    T, H, K = q.shape
+    V = v.shape[-1]
+    N = cu.numel() - 1
+    if h0 is not None and h0.shape != (N, H, K, V):
+        raise ValueError(f"chunk_gla: initial_state must be {(N, H, K, V)}, got {tuple(h0.shape)}")
+    o = torch.empty_like(v)
+    ht = torch.empty(N, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
+    if not chunk_kernel_supports(q, v):
+        return _recurrent(q, k, v, g, cu, float(scale), h0, o, ht, None, 0)
+    lib = _lib.load()
+    st = lib.ssla_gla_chunk_fwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.DTYPE_CODE[g.dtype],
+        _lib.ptr(cu), N, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(o), _lib.ptr(ht),
+        _lib.DTYPE_CODE[q.dtype], None, 0, _lib.stream_of(q))
+    _lib.check(st, "ssla_gla_chunk_fwd")
+    return o, ht
+
+
+def _recurrent(q, k, v, g, cu, scale, h0, o, ht, state_idx, n_rows):
+    T, H, K = q.shape
+    V = v.shape[-1]
+    N = cu.numel() - 1
+    lib = _lib.load()
+    st = lib.ssla_gla_recurrent_fwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.DTYPE_CODE[g.dtype],
+        _lib.ptr(cu), N, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(o), _lib.ptr(ht),
+        _lib.ptr(state_idx), int(n_rows), _lib.DTYPE_CODE[q.dtype], _lib.stream_of(q))
+    _lib.check(st, "ssla_gla_recurrent_fwd")
+    return o, ht
+
+
+def fused_recurrent_gla(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    cu_seqlens: torch.LongTensor,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Recurrent GLA forward with the signature and semantics of
+    ``naive_gla_recurrent`` (reference ops/gla/naive.py:50-111):
+    ``S_t = exp(g_t) * S_{t-1} + k_t v_t^T``, ``o_t = (scale q_t) . S_t``;
+    o has q's dtype, the final state is fp32."""
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    q, k, v, g, cu, h0 = _prep("fused_recurrent_gla", q, k, v, g, cu_seqlens, initial_state)
+    T, H, K = q.shape
+    V = v.shape[-1]
+    N = cu.numel() - 1
+    if h0 is not None and h0.shape != (N, H, K, V):
+        raise ValueError(f"fused_recurrent_gla: initial_state must be {(N, H, K, V)}, "
+                         f"got {tuple(h0.shape)}")
+    o = torch.empty(T, H, V, device=q.device, dtype=q.dtype)
+    ht = torch.empty(N, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
+    return _recurrent(q, k, v, g, cu, float(scale), h0, o, ht, None, 0)
+
+
+naive_gla_recurrent = fused_recurrent_gla

@@ -1,0 +1,78 @@
+"""CPU checks of the drop-in boundary: libssla_amd.so loads, exports every
+symbol include/ssla_amd.h declares, and rejects bad arguments before any
+device work (no GPU needed)."""
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "ssla_amd.h").read_text()
+    # function declarations start a line: "<type> [*]ssla_name("
+    return sorted(set(re.findall(r"^(?:const\s+)?[a-z_0-9]+\s*\*?\s*(ssla_[a-z0-9_]+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from ssla_amd import _lib
+    lib = _lib.load()
+    names = _declared()
+    assert "ssla_gla_chunk_fwd" in names and len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/ssla_amd.h but not exported"
+    # the ctypes table covers the header exactly
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_version():
+    from ssla_amd import _lib
+    assert _lib.load().ssla_version() >= 100
+
+
+def test_argument_errors_without_device_work():
+    from ssla_amd import _lib
+    lib = _lib.load()
+    # negative sizes -> SSLA_ERR_ARG
+    st = lib.ssla_gla_chunk_fwd(None, None, None, None, 0, None, -1, 0, 1, 64, 64, 1.0, None, None,
+                                None, _lib.SSLA_BF16, None, 0, None)
+    assert st == _lib.SSLA_ERR_ARG
+    assert b"bad sizes" in lib.ssla_last_error()
+    # K != 64 on the chunk kernel -> SSLA_ERR_UNSUPPORTED
+    st = lib.ssla_gla_chunk_fwd(None, None, None, None, 0, None, 1, 0, 1, 32, 64, 1.0, None, None,
+                                None, _lib.SSLA_BF16, None, 0, None)
+    assert st == _lib.SSLA_ERR_UNSUPPORTED
+    # K > 256 on the recurrent kernel
+    st = lib.ssla_gla_recurrent_fwd(None, None, None, None, 0, None, 1, 0, 1, 300, 64, 1.0, None, None,
+                                    None, None, 0, _lib.SSLA_F32, None)
+    assert st == _lib.SSLA_ERR_UNSUPPORTED
+    # unsupported sparse-step shape
+    st = lib.ssla_sparse_gla_step(None, 1, None, None, None, None, None, 1, 1, 48, 48, 1.0, None, None)
+    assert st == _lib.SSLA_ERR_ARG  # null pointers are rejected first
+    # scatter: C not a multiple of 4, and a missing workspace
+    st = lib.ssla_scatter_max(None, None, 10, 3, 4, 0, None, None, None, 0, None)
+    assert st == _lib.SSLA_ERR_UNSUPPORTED
+    st = lib.ssla_scatter_max(None, None, 10, 4, 4, 0, None, None, None, 0, None)
+    assert st == _lib.SSLA_ERR_WORKSPACE
+
+
+def test_workspace_size_monotone():
+    from ssla_amd import _lib
+    lib = _lib.load()
+    a = lib.ssla_scatter_workspace_size(1000, 64, 100)
+    b = lib.ssla_scatter_workspace_size(2000, 64, 100)
+    c = lib.ssla_scatter_workspace_size(2000, 64, 200)
+    assert 0 < a < b < c
+    assert lib.ssla_scatter_workspace_size(-1, 64, 10) == 0
+
+
+def test_python_wrappers_reject_cpu_tensors():
+    import torch
+    from ssla_amd.gla import chunk_gla
+    from ssla_amd.scan import scan
+    x = torch.zeros(4, 1, 64)
+    with pytest.raises(ValueError, match="device tensors"):
+        chunk_gla(x, x, x, x, torch.tensor([0, 4]))
+    with pytest.raises(ValueError, match="device tensors"):
+        scan(torch.zeros(4, 3), torch.zeros(4, 3), torch.tensor([0, 4]))

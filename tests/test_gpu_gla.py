@@ -1,0 +1,166 @@
+"""GPU parity: chunked and recurrent GLA forward (HIP, via the C-ABI) vs the
+fp64 CPU oracle (restating reference ops/gla/naive.py:50-111).
+
+Tolerances (north star): bf16 inputs with fp32 accumulation rtol 2e-2,
+fp32 inputs rtol 1e-4, both with atol = rtol * rms(reference) -- see
+tests/conftest.assert_close.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from tests.conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+RTOL_BF16 = 2e-2
+RTOL_F16 = 1e-2
+RTOL_F32 = 1e-4
+
+
+def _inputs(lens, H, K, V, dtype, seed=0, gate="logsig", h0=True, qscale=None):
+    gen = torch.Generator().manual_seed(seed)
+    T = int(sum(lens))
+    q = torch.randn(T, H, K, generator=gen)
+    if qscale is not None:
+        q = q * qscale
+    k = torch.randn(T, H, K, generator=gen)
+    v = torch.randn(T, H, V, generator=gen)
+    if gate == "logsig":
+        g = F.logsigmoid(torch.randn(T, H, K, generator=gen) / 16)
+    elif gate == "randn-1":          # reference self-check gates (ops/gla/naive.py:121)
+        g = torch.randn(T, H, K, generator=gen) - 1.0
+    elif gate == "strong":           # block decays far below the factorised range
+        g = -5.0 - torch.rand(T, H, K, generator=gen)
+    elif gate == "zero":
+        g = torch.zeros(T, H, K)
+    else:
+        raise ValueError(gate)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64)
+    s0 = torch.randn(len(lens), H, K, V, generator=gen) * 0.1 if h0 else None
+    return q.to(dtype), k.to(dtype), v.to(dtype), g, cu, s0
+
+
+def _oracle(q, k, v, g, cu, s0, scale):
+    return oracle.gla_recurrent(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                g.float().numpy(), cu.numpy(), scale,
+                                None if s0 is None else s0.numpy(), True)
+
+
+def _run(fn, q, k, v, g, cu, s0, scale, dev):
+    with torch.no_grad():
+        o, ht = fn(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev), scale=scale,
+                   initial_state=None if s0 is None else s0.to(dev), output_final_state=True)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), ht.cpu().numpy()
+
+
+def test_recurrent_c1_fp32(dev):
+    """N=1, H=4, T=256, K=V=32, fp32, q pre-scaled by
+    1/sqrt(32) and scale=1.0, zero initial state."""
+    from ssla_amd.gla import fused_recurrent_gla
+    torch.manual_seed(0)
+    q, k, v, g, cu, s0 = _inputs([256], 4, 32, 32, torch.float32, h0=False, qscale=32 ** -0.5)
+    o, ht = _run(fused_recurrent_gla, q, k, v, g, cu, None, 1.0, dev)
+    ro, rht = _oracle(q, k, v, g, cu, None, 1.0)
+    assert_close(o, ro, RTOL_F32, "o")
+    assert_close(ht, rht, RTOL_F32, "ht")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("K,V", [(32, 32), (64, 64), (16, 48), (100, 20), (256, 256)])
+def test_recurrent_varlen(dev, dtype, K, V):
+    from ssla_amd.gla import fused_recurrent_gla
+    lens = [0, 1, 17, 64, 130]
+    q, k, v, g, cu, s0 = _inputs(lens, 3, K, V, dtype, seed=K + V)
+    o, ht = _run(fused_recurrent_gla, q, k, v, g, cu, s0, K ** -0.5, dev)
+    ro, rht = _oracle(q, k, v, g, cu, s0, K ** -0.5)
+    rtol = {torch.float32: RTOL_F32, torch.bfloat16: RTOL_BF16, torch.float16: RTOL_F16}[dtype]
+    # o is rounded to the input dtype; the state stays fp32
+    assert_close(o, ro, rtol, "o")
+    assert_close(ht, rht, RTOL_F32 if dtype == torch.float32 else 1e-3, "ht")
+
+
+@pytest.mark.parametrize("V", [16, 64, 128])
+@pytest.mark.parametrize("gate", ["logsig", "randn-1", "strong", "zero"])
+def test_chunk_varlen(dev, V, gate):
+    """Ragged sequences (empty, 1, chunk-1, chunk, chunk+1, long), every
+    gate regime including the exact-mode chunks (strong / positive gates)."""
+    from ssla_amd.gla import chunk_gla
+    lens = [0, 1, 63, 64, 65, 200, 7]
+    q, k, v, g, cu, s0 = _inputs(lens, 3, 64, V, torch.bfloat16, seed=V, gate=gate)
+    o, ht = _run(chunk_gla, q, k, v, g, cu, s0, 64 ** -0.5, dev)
+    ro, rht = _oracle(q, k, v, g, cu, s0, 64 ** -0.5)
+    assert_close(o, ro, RTOL_BF16, f"o[{gate}]", ratio_mode=True)
+    assert_close(ht, rht, RTOL_BF16, f"ht[{gate}]", ratio_mode=True)
+
+
+def test_chunk_fp16_and_bf16_gates(dev):
+    from ssla_amd.gla import chunk_gla
+    lens = [100, 300]
+    for dtype, rtol in ((torch.float16, RTOL_F16), (torch.bfloat16, RTOL_BF16)):
+        q, k, v, g, cu, s0 = _inputs(lens, 2, 64, 64, dtype, seed=3)
+        g_lp = g.to(dtype)           # g in the input dtype
+        o, ht = _run(chunk_gla, q, k, v, g_lp, cu, s0, 0.125, dev)
+        ro, rht = _oracle(q, k, v, g_lp.float(), cu, s0, 0.125)
+        assert_close(o, ro, rtol, f"o[{dtype}]", ratio_mode=True)
+        assert_close(ht, rht, rtol, f"ht[{dtype}]", ratio_mode=True)
+
+
+def test_chunk_no_initial_state_no_final(dev):
+    from ssla_amd.gla import chunk_gla
+    q, k, v, g, cu, _ = _inputs([150], 2, 64, 32, torch.bfloat16, seed=5, h0=False)
+    with torch.no_grad():
+        o, ht = chunk_gla(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev))
+    assert ht is None
+    ro, _ = _oracle(q, k, v, g, cu, None, 64 ** -0.5)
+    assert_close(o.float().cpu().numpy(), ro, RTOL_BF16, "o", ratio_mode=True)
+
+
+def test_chunk_matches_recurrent_kernel(dev):
+    """The two HIP kernels agree (same math, different algorithms)."""
+    from ssla_amd.gla import chunk_gla, fused_recurrent_gla
+    q, k, v, g, cu, s0 = _inputs([500, 12, 333], 4, 64, 64, torch.bfloat16, seed=9)
+    o1, h1 = _run(chunk_gla, q, k, v, g, cu, s0, 0.125, dev)
+    o2, h2 = _run(fused_recurrent_gla, q, k, v, g, cu, s0, 0.125, dev)
+    assert_close(o1, o2, RTOL_BF16, "o", ratio_mode=True)
+    assert_close(h1, h2, RTOL_BF16, "ht", ratio_mode=True)
+
+
+def test_chunk_c2_full(dev):
+    """BASELINE config 2 at full size: B=8, H=8, T=4096, D=64, bf16,
+    h0 ~ N(0, 0.1), vs the fp64 naive recurrence."""
+    from ssla_amd import synthetic
+    from ssla_amd.gla import chunk_gla
+    x = synthetic.chunk_gla_inputs()
+    with torch.no_grad():
+        o, ht = chunk_gla(x["q"].to(dev), x["k"].to(dev), x["v"].to(dev), x["g"].to(dev),
+                          x["cu_seqlens"].to(dev), scale=x["scale"],
+                          initial_state=x["initial_state"].to(dev), output_final_state=True)
+    torch.cuda.synchronize()
+    ro, rht = oracle.gla_recurrent(x["q"].float().numpy(), x["k"].float().numpy(),
+                                   x["v"].float().numpy(), x["g"].numpy(), x["cu_seqlens"].numpy(),
+                                   x["scale"], x["initial_state"].numpy(), True)
+    assert_close(o.float().cpu().numpy(), ro, RTOL_BF16, "o", ratio_mode=True)
+    assert_close(ht.cpu().numpy(), rht, RTOL_BF16, "ht")
+
+
+def test_chunk_repeatable(dev):
+    """Same inputs, same bits (no atomics or races in the kernel)."""
+    from ssla_amd.gla import chunk_gla
+    q, k, v, g, cu, s0 = _inputs([700, 64], 2, 64, 64, torch.bfloat16, seed=11)
+    a = _run(chunk_gla, q, k, v, g, cu, s0, 0.125, dev)
+    b = _run(chunk_gla, q, k, v, g, cu, s0, 0.125, dev)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_chunk_errors(dev):
+    from ssla_amd.gla import chunk_gla
+    q, k, v, g, cu, s0 = _inputs([10, 20], 2, 64, 64, torch.bfloat16)
+    with pytest.raises(ValueError, match="number of initial states"):
+        chunk_gla(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev), initial_state=s0[:1].to(dev))
+    qg = q.to(dev).requires_grad_(True)
+    with pytest.raises(NotImplementedError):
+        chunk_gla(qg, k.to(dev), v.to(dev), g.to(dev), cu.to(dev))
