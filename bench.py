@@ -74,13 +74,15 @@ def bench_chunk(torch, lib, steps, warmup, dev):
     Tt, H, D = C2["B"] * C2["T"], C2["H"], C2["D"]
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
+    ws_bytes = lib.ssla_gla_chunk_workspace_size(C2["B"], Tt, H, D, D)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
 
     def launch(x):
         st = lib.ssla_gla_chunk_fwd(
             x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(), _lib.SSLA_F32,
             x["cu_seqlens"].data_ptr(), C2["B"], Tt, H, D, D, float(x["scale"]),
             x["initial_state"].data_ptr(), x["o"].data_ptr(), x["ht"].data_ptr(), _lib.SSLA_BF16,
-            None, 0, sh)
+            ws.data_ptr(), ws_bytes, sh)
         _lib.check(st, "ssla_gla_chunk_fwd")
 
     for i in range(warmup):

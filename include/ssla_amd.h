@@ -69,9 +69,14 @@ const char *ssla_last_error(void);
  *   (reference ops/gla/chunk.py:1119-1167, :1056-1094, :906-960)
  * together with chunk_local_cumsum (ops/utils/cumsum.py:346-364),
  * chunk_fwd_h (ops/common/chunk_h.py:242-294) and the intra-chunk /
- * output kernels (ops/gla/chunk.py:33-249, :644-743), fused into one
- * launch.  Supported: dtype BF16 or F16, K == 64, V a multiple of 16
- * (<= 256).  Workspace: none (pass NULL, 0). */
+ * output kernels (ops/gla/chunk.py:33-249, :644-743).  Supported: dtype
+ * BF16 or F16, K == 64, V a multiple of 16 (<= 256).
+ * Each sequence is split into segments processed in parallel; the
+ * workspace (ssla_gla_chunk_workspace_size bytes, 16-byte aligned, no
+ * initialisation needed) holds one fp32 state per segment.  A size of 0
+ * means no workspace is needed for this shape (pass NULL, 0). */
+size_t ssla_gla_chunk_workspace_size(int n_seq, int64_t T, int H, int K, int V);
+
 int ssla_gla_chunk_fwd(const void *q, const void *k, const void *v,
                        const void *g, int g_dtype,
                        const int64_t *cu_seqlens, int n_seq, int64_t T,

@@ -31,6 +31,7 @@ _vp, _i32, _i64, _f32, _sz = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size
 SIGNATURES = {
     "ssla_version": (_i32, []),
     "ssla_last_error": (C.c_char_p, []),
+    "ssla_gla_chunk_workspace_size": (_sz, [_i32, _i64, _i32, _i32, _i32]),
     "ssla_gla_chunk_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32,
                                   _f32, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
     "ssla_gla_recurrent_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32,

@@ -97,10 +97,12 @@ def chunk_gla(
     if not chunk_kernel_supports(q, v):
         return _recurrent(q, k, v, g, cu, float(scale), h0, o, ht, None, 0)
     lib = _lib.load()
+    ws_bytes = lib.ssla_gla_chunk_workspace_size(N, T, H, K, V)
+    ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
     st = lib.ssla_gla_chunk_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.DTYPE_CODE[g.dtype],
         _lib.ptr(cu), N, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(o), _lib.ptr(ht),
-        _lib.DTYPE_CODE[q.dtype], None, 0, _lib.stream_of(q))
+        _lib.DTYPE_CODE[q.dtype], _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
     _lib.check(st, "ssla_gla_chunk_fwd")
     return o, ht
 
