@@ -215,6 +215,20 @@ def cpu_baseline(x, budget_s=20.0):
             "host_cpus": os.cpu_count()}
 
 
+def calibrate_copy(torch, dev, mib=256, reps=3):
+    """Plain device-to-device copies of a known size.  Profiled with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, the counter value per copy
+    dispatch divided by mib MiB is the factor that turns those counters into
+    bytes for the kernels of this path."""
+    n = mib * 2**20 // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n * 4, "reps": reps}), flush=True)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -222,10 +236,12 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 256 MiB device copies (counter calibration) and exit")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the hot path is single-GPU; "
-              "see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py: this build measures one GPU only; the hot path is not sharded "
+              "across GPUs here. Run with --gpus 1.", file=sys.stderr)
         return 2
     import torch
     from ssla_amd import _lib
@@ -233,6 +249,9 @@ def main(argv=None):
         print("bench.py: no GPU visible", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        calibrate_copy(torch, dev)
+        return 0
     lib = _lib.load()
     r = bench_chunk(torch, lib, args.steps, args.warmup, dev)
     ms_step = r["wall_s"] * 1e3 / args.steps

@@ -101,11 +101,12 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 // ------------------------------------------------------------------- DPP --
 // Shift right by N lanes inside each 16-lane DPP row; lanes whose source
-// lies outside the row receive 0.
+// lies outside the row read 0 (bound_ctrl), so an add of the result folds
+// into a single v_add_f32 with a DPP source.
 template <int N>
 __device__ __forceinline__ float row_shr(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-      0, __builtin_bit_cast(int, x), 0x110 + N, 0xf, 0xf, false));
+      0, __builtin_bit_cast(int, x), 0x110 + N, 0xf, 0xf, true));
 }
 
 // Inclusive prefix sum across the 16 lanes of each DPP row.
