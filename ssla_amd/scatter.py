@@ -77,7 +77,7 @@ def _run(name, fn, src, index, n_out, sorted_index, out, argmax, check):
                              + (" or not sorted" if sorted_index else ""))
 
 
-def scatter_max(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
+def scatter_max(src: torch.Tensor, index: torch.Tensor, dim: int = -1,
                 out: Optional[torch.Tensor] = None, dim_size: Optional[int] = None,
                 sorted_index: bool = False, check: bool = True
                 ) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -98,7 +98,7 @@ def scatter_max(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
     return res, arg
 
 
-def scatter_mean(src: torch.Tensor, index: torch.Tensor, dim: int = 0,
+def scatter_mean(src: torch.Tensor, index: torch.Tensor, dim: int = -1,
                  out: Optional[torch.Tensor] = None, dim_size: Optional[int] = None,
                  sorted_index: bool = False, check: bool = True) -> torch.Tensor:
     """Row-wise mean (sum / max(count, 1))."""

@@ -63,7 +63,7 @@ def test_empty_and_single(dev):
     from ssla_amd.scatter import scatter_max
     with torch.no_grad():
         out, arg = scatter_max(torch.zeros(0, 8, device=dev), torch.zeros(0, dtype=torch.int64, device=dev),
-                               dim_size=4)
+                               dim=0, dim_size=4)
     assert (out == 0).all() and (arg == 0).all()
 
 
@@ -71,10 +71,12 @@ def test_out_of_range_index_raises(dev):
     from ssla_amd.scatter import scatter_max
     src = torch.randn(10, 8, device=dev)
     idx = torch.arange(10, device=dev)
+    with pytest.raises(NotImplementedError):
+        scatter_max(src, idx, dim_size=10)          # torch_scatter's default dim=-1
     with pytest.raises(ValueError):
-        scatter_max(src, idx, dim_size=5)
+        scatter_max(src, idx, dim=0, dim_size=5)
     with pytest.raises(ValueError):
-        scatter_max(src, idx.flip(0), dim_size=10, sorted_index=True)
+        scatter_max(src, idx.flip(0), dim=0, dim_size=10, sorted_index=True)
 
 
 def test_c4_full(dev):
