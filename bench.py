@@ -236,6 +236,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--only", choices=["chunk", "sparse", "pool"], default=None,
+                    help="run one workload and print its line (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 256 MiB device copies (counter calibration) and exit")
     args = ap.parse_args(argv)
@@ -253,6 +255,12 @@ def main(argv=None):
         calibrate_copy(torch, dev)
         return 0
     lib = _lib.load()
+    if args.only == "sparse":
+        print(json.dumps(bench_sparse(torch, lib, args.steps, dev)), flush=True)
+        return 0
+    if args.only == "pool":
+        print(json.dumps(bench_pool(torch, lib, args.steps, dev)), flush=True)
+        return 0
     r = bench_chunk(torch, lib, args.steps, args.warmup, dev)
     ms_step = r["wall_s"] * 1e3 / args.steps
     value = r["tokens"] / (r["wall_s"] / args.steps) / 1e6
@@ -277,7 +285,7 @@ def main(argv=None):
                  "frac": tflops / BF16_PEAK_TFLOPS, "flops_per_launch": c2_flops(),
                  "note": "causal-useful flops; the shape is HBM-bound (31.8 flop/B < 312 ridge)"},
     }
-    if not args.no_secondary:
+    if not args.no_secondary and args.only is None:
         line["secondary"] = [bench_sparse(torch, lib, 10, dev), bench_pool(torch, lib, 20, dev)]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(r["sample"])

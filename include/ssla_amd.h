@@ -146,12 +146,16 @@ int ssla_sparse_gla_step(const int32_t *site_idx, int n_active,
  *   argmax[n, c] = the SMALLEST such e attaining the maximum (floating-point
  *   comparison, so -0.0 == +0.0; out takes the bits of src[argmax]).
  *   Empty rows: out = 0, argmax = E.
- * scatter_mean: out[n, c] = sum / max(count, 1); empty rows give 0.
+ *   NaN values never win the comparison (a row whose values are all NaN
+ *   reports out = 0, argmax = E).
+ * scatter_mean: out[n, c] = sum / max(count, 1), summed in fp64 and
+ *   rounded once; empty rows give 0.
  *
  * `index_sorted` = 1 promises index is non-decreasing (the segment ids that
  * unique_consecutive produces); the kernels then skip the bucketing pass.
- * Workspace: ssla_scatter_workspace_size(E, C, n_out) bytes (16-byte aligned).
- * C must be a multiple of 4; E and n_out below 2^31.
+ * Workspace: ssla_scatter_workspace_size(E, C, n_out) bytes (16-byte aligned,
+ * no initialisation needed).  Any C >= 1; E below 2^31, n_out below 2^30.
+ * Concurrent calls must use distinct workspaces.
  * ------------------------------------------------------------------------ */
 size_t ssla_scatter_workspace_size(int64_t E, int C, int64_t n_out);
 

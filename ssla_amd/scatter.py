@@ -50,11 +50,7 @@ def _prep(name, src, index, dim, dim_size):
     index = index.to(torch.int64).contiguous()
     if dim_size is None:
         dim_size = int(index.max().item()) + 1 if E > 0 else 0
-    pad = (-Cc) % 4
-    src_c = src.contiguous()
-    if pad:
-        src_c = torch.nn.functional.pad(src_c, (0, pad))
-    return src_c, index, int(dim_size), Cc, squeeze
+    return src.contiguous(), index, int(dim_size), Cc, squeeze
 
 
 def _run(name, fn, src, index, n_out, sorted_index, out, argmax, check):
@@ -85,11 +81,9 @@ def scatter_max(src: torch.Tensor, index: torch.Tensor, dim: int = -1,
     promises a non-decreasing index (e.g. a ``unique_consecutive`` inverse);
     ``check`` reports out-of-range (or unsorted) indices as ValueError."""
     src_c, idx, n_out, Cc, squeeze = _prep("scatter_max", src, index, dim, dim_size)
-    Cp = src_c.shape[1]
-    res = torch.empty(n_out, Cp, device=src.device, dtype=torch.float32)
-    arg = torch.empty(n_out, Cp, device=src.device, dtype=torch.int64)
+    res = torch.empty(n_out, Cc, device=src.device, dtype=torch.float32)
+    arg = torch.empty(n_out, Cc, device=src.device, dtype=torch.int64)
     _run("scatter_max", _lib.load().ssla_scatter_max, src_c, idx, n_out, sorted_index, res, arg, check)
-    res, arg = res[:, :Cc], arg[:, :Cc]
     if squeeze:
         res, arg = res[:, 0], arg[:, 0]
     if out is not None:
@@ -103,10 +97,8 @@ def scatter_mean(src: torch.Tensor, index: torch.Tensor, dim: int = -1,
                  sorted_index: bool = False, check: bool = True) -> torch.Tensor:
     """Row-wise mean (sum / max(count, 1))."""
     src_c, idx, n_out, Cc, squeeze = _prep("scatter_mean", src, index, dim, dim_size)
-    Cp = src_c.shape[1]
-    res = torch.empty(n_out, Cp, device=src.device, dtype=torch.float32)
+    res = torch.empty(n_out, Cc, device=src.device, dtype=torch.float32)
     _run("scatter_mean", _lib.load().ssla_scatter_mean, src_c, idx, n_out, sorted_index, res, None, check)
-    res = res[:, :Cc]
     if squeeze:
         res = res[:, 0]
     if out is not None:

@@ -50,10 +50,12 @@ def test_argument_errors_without_device_work():
     # unsupported sparse-step shape
     st = lib.ssla_sparse_gla_step(None, 1, None, None, None, None, None, 1, 1, 48, 48, 1.0, None, None)
     assert st == _lib.SSLA_ERR_ARG  # null pointers are rejected first
-    # scatter: C not a multiple of 4, and a missing workspace
+    # scatter: non-positive C, n_out beyond 2^30, and a missing workspace
+    st = lib.ssla_scatter_max(None, None, 10, 0, 4, 0, None, None, None, 0, None)
+    assert st == _lib.SSLA_ERR_ARG
+    st = lib.ssla_scatter_max(None, None, 10, 4, 1 << 30, 0, None, None, None, 0, None)
+    assert st == _lib.SSLA_ERR_ARG
     st = lib.ssla_scatter_max(None, None, 10, 3, 4, 0, None, None, None, 0, None)
-    assert st == _lib.SSLA_ERR_UNSUPPORTED
-    st = lib.ssla_scatter_max(None, None, 10, 4, 4, 0, None, None, None, 0, None)
     assert st == _lib.SSLA_ERR_WORKSPACE
 
 

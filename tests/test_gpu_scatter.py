@@ -26,7 +26,7 @@ def _check(dev, src, index, n_out, sorted_index=False):
                  "scatter_mean", atol_scale=1e-6)
 
 
-@pytest.mark.parametrize("C", [4, 12, 64, 100, 256, 300])
+@pytest.mark.parametrize("C", [1, 3, 4, 12, 64, 65, 100, 256, 300])
 def test_random_unsorted(dev, C):
     gen = torch.Generator().manual_seed(C)
     E, n_out = 5000, 300
@@ -55,6 +55,27 @@ def test_sorted_segments(dev):
     src = torch.randn(E, C, generator=gen)
     _check(dev, src, index, 1000, sorted_index=True)
     _check(dev, src, index, 1000, sorted_index=False)
+
+
+def test_many_rows_global_counting(dev):
+    """More output rows than the LDS histogram holds (global-counter path),
+    plus a row with several pieces."""
+    gen = torch.Generator().manual_seed(3)
+    E, C, n_out = 60000, 8, 40000
+    src = torch.randn(E, C, generator=gen)
+    index = torch.randint(0, n_out, (E,), generator=gen)
+    index[:1000] = 7
+    _check(dev, src, index, n_out)
+
+
+def test_repeated_calls_reuse_workspace(dev):
+    """Calls of different shapes back to back (stale workspace contents from
+    the previous call must not leak into the next)."""
+    gen = torch.Generator().manual_seed(4)
+    for E, C, n_out in [(20000, 16, 50), (3000, 16, 2000), (20000, 16, 50), (0, 16, 10)]:
+        src = torch.randn(E, C, generator=gen)
+        index = torch.randint(0, n_out, (E,), generator=gen)
+        _check(dev, src, index, n_out)
 
 
 def test_empty_and_single(dev):
