@@ -10,43 +10,39 @@
 //   S_c+1 = diag(exp(G_last)) S_c + (k_c * exp(G_last - G))^T v_c
 // with S_0 = h0 (or 0) and ht = S after the last chunk.
 //
-// Schedule (two launches; the only intermediate is one state per segment):
-// * Each sequence is cut into P segments of whole chunks (P picked so that
-//   about two workgroups run per CU; no work is repeated across them).
-// * Kernel S ("state pass"): for segments 0..P-2, one workgroup walks the
-//   chunks of its (sequence, head, segment) computing only the state update
-//   (from h0 for segment 0, from zero otherwise) and leaves the final state
-//   and the total log-decay in the workspace.  It reads k, g, v only.
-// * Kernel A ("segment"): one workgroup per (sequence, head, segment) folds
-//   the earlier segments into its entering state
-//     S_e(1) = slot 0,  S_e(s+1) = 2^D(s) S_e(s) + slot s,
-//   then runs the full chunk loop below and writes o (and ht for the last
-//   segment).  Its k, g, v re-reads of segments 0..P-2 are served mostly by
-//   the Infinity Cache right after kernel S.
-//   P = 1 (no workspace) runs kernel A alone.
+// Schedule (three launches; the only intermediates are per-segment states):
+// * Each (sequence, head, V group) chain is cut into P segments of whole
+//   chunks (P chosen so that about two workgroups run per CU).
+// * state pass  : segments 0..P-2 run the state recurrence only (reads k, g,
+//   v) from h0 (segment 0) or zero, leaving the segment's final state and
+//   total log2-decay D in a workspace slot.
+// * prefix fold : E(1) = slot 0, E(s+1) = 2^D(s) E(s) + slot s, written back
+//   in place, so slot s-1 holds the state entering segment s.
+// * segment pass: every segment runs the full chunk loop from its entering
+//   state and writes o (and ht for the last segment).
 //
-// Kernel A per chunk:
-// * Wavefront I owns the 16 chunk rows 16I..16I+15 ("block" I) and the
-//   state rows 16I..16I+15 (as MFMA accumulators).  All products use
-//   v_mfma_f32_16x16x32_{bf16,f16}; every wavefront runs the same code,
-//   block-dependent work is predicated on the (uniform) index.  Within a
-//   lane the 64 keys are held as k = 32*jj + 8*(lane/16) + e (jj = 0,1;
-//   e = 0..7): the operand layout of the two K=32 halves of a K=64 product.
-// * Decay factorisation (log2 units, G2 = G * log2(e)): with R = G2 at the
-//   middle of the chunk (end of row 31),
-//     exp(G_i - G_j) = 2^(G2_i - R) * 2^(R - G2_j),
-//   so every block of A uses the same two operands q~ = q 2^(G2 - R) and
-//   k~ = k 2^(R - G2).  Both stay inside 2^(+-50) when neither half of the
-//   chunk decays by more than 2^-50 (typical GLA gates decay ~2^-1 per row
-//   per key, i.e. 2^-32 per half chunk).  A chunk outside that range, or with
-//   any positive log-gate, is computed in "exact" mode: the diagonal 16x16
-//   blocks elementwise and the off-diagonal blocks re-referenced to the row
-//   block, as the reference does (ops/gla/chunk.py:80-92, :160-166).  The
-//   mode is chosen per chunk, uniformly for the workgroup.
-// * The state enters the output product split into high and low 16-bit
-//   parts (written once by the wavefront that owns the rows), so S
-//   contributes with ~16 mantissa bits (the reference rounds its per-chunk
-//   states to bf16, ops/gla/chunk.py:933).  scale is applied to o at the end.
+// Inside a workgroup (256 threads, 4 wavefronts): wavefront I owns chunk
+// rows 16I..16I+15 ("block" I) and state rows (keys) 16I..16I+15 as MFMA
+// accumulators.  All products are v_mfma_f32_16x16x32_{bf16,f16}.  Within a
+// lane the 64 keys are held as k = 32*jj + 8*(lane/16) + e (jj = 0,1; e =
+// 0..7), the operand layout of the two K=32 halves of a K=64 product.
+// Products that contract over time (A v, k^T v) read their operands from
+// row-major LDS tiles with ds_read_b64_tr_b16 (transposing 16-bit loads),
+// so no transposed copies are written.
+//
+// Decay factorisation (log2 units, G2 = G * log2(e)), per key and block I
+// with block boundary values E_J (G2 at the last row of block J, E_-1 = 0)
+// and M_I = (E_I-1 + E_I) / 2:
+//   diagonal block     : 2^(G_i - G_j) = 2^(G_i - M_I) 2^(M_I - G_j)
+//   block J < I        : 2^(G_i - G_j) = [2^(G_i - M_I) 2^(M_I - E_J)] [2^(E_J - G_j)]
+// For non-positive gates the off-diagonal factors are all <= 1 (exact up to
+// underflow of values that are themselves below 2^-126), and the diagonal
+// factors stay inside 2^(+-x) with x the decay over half a block (8 rows);
+// exponents are clamped to +-126, which only matters when a key decays by
+// more than 2^-126 within 8 steps.  The state enters the output product in
+// the input dtype, as the reference's per-chunk states do
+// (states_in_fp32=False, ops/gla/chunk.py:933).  scale is applied to o at
+// the end.
 #include "common.h"
 
 namespace ssla {
@@ -54,16 +50,15 @@ namespace {
 
 constexpr int BT = 64;    // chunk rows
 constexpr int KD = 64;    // key width
-constexpr float kRangeLimit = 50.f;    // |G2 - R| bound of the fast path, log2 units
-
-// LDS row pitches (elements); padding breaks power-of-two bank strides.
-constexpr int kKP = KD + 8;    // [row][key] 16-bit
-constexpr int kTP = BT + 8;    // transposed [key or column][row] 16-bit
-constexpr int kXP = KD + 4;    // exact-mode G rows: [row][key] fp32
+constexpr float kExpClamp = 126.f;
+#ifndef SSLA_GC_SEG_WAVES
+#define SSLA_GC_SEG_WAVES 2
+#endif
 
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-// MFMA of the input dtype (value products: S q~, A v, k~s^T v).
+// MFMA of the input dtype (value products: S^T q0, V^T A^T, k^T v).
 template <int DT> struct Mfma;
 template <> struct Mfma<SSLA_BF16> {
   typedef bf16x8 Vec;
@@ -82,7 +77,7 @@ template <> struct Mfma<SSLA_F16> {
   static __device__ __forceinline__ f32x8 widen(Vec x) { return __builtin_convertvector(x, f32x8); }
 };
 // The decayed q~ k~^T products always run in bf16: its fp32 exponent range
-// holds the factors 2^(+-50) that fp16 cannot.
+// holds factors that fp16 cannot.
 typedef Mfma<SSLA_BF16> QK;
 
 template <class V8>
@@ -90,26 +85,59 @@ __device__ __forceinline__ V8 from_bits(const uint4 &x) { return __builtin_bit_c
 template <class V8>
 __device__ __forceinline__ uint4 to_bits(const V8 &x) { return __builtin_bit_cast(uint4, x); }
 
-template <int NVT>
+// ------------------------------------------------------------ LDS tiles --
+// A tile is [64 rows][64 columns] of 16-bit values, rows of 128 bytes, with
+// the 16-byte segments of row r permuted by XOR (r & 7) so that the column
+// reads of the MFMA operand layouts spread over the banks.
+__device__ __forceinline__ int swz(int row, int col) {
+  return row * 64 + ((((col >> 3) ^ (row & 7)) << 3) | (col & 7));
+}
+
+// 16 bytes (8 consecutive columns from col, col % 8 == 0) of one row.
+__device__ __forceinline__ uint4 tile_row8(const uint16_t *t, int row, int col) {
+  return *reinterpret_cast<const uint4 *>(t + swz(row, col));
+}
+__device__ __forceinline__ void tile_store8(uint16_t *t, int row, int col, const uint4 &x) {
+  *reinterpret_cast<uint4 *>(t + swz(row, col)) = x;
+}
+
+// ds_read_b64_tr_b16 lane mapping (16-lane groups): lane i receives element
+// (i % 4) of the 8-byte loads of source lanes i/4, 4 + i/4, 8 + i/4 and
+// 12 + i/4.  With source lane s of group G reading row rb(G) + s/4,
+// columns c0 + 4 (s % 4) .. +3, lane i of group G receives
+//   T[rb(G) + 0..3][c0 + i].
+__device__ __forceinline__ s16x4 tr_read4(const uint16_t *t, int row_base, int c0, int lane) {
+  const int s = lane & 15;
+  const uint16_t *p = t + swz(row_base + (s >> 2), c0 + 4 * (s & 3));
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<__attribute__((address_space(3))) s16x4 *>(
+          reinterpret_cast<uintptr_t>(p)));
+}
+
+// MFMA operand (16 x 32 with K = rows) whose lane 16G + i holds the column
+// c0 + i of rows ra(G) + 0..3 and rb(G) + 0..3.
+template <class V8>
+__device__ __forceinline__ V8 tr_operand(const uint16_t *t, int ra, int rb, int c0, int lane) {
+  const s16x4 a = tr_read4(t, ra, c0, lane);
+  const s16x4 b = tr_read4(t, rb, c0, lane);
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  return from_bits<V8>(make_uint4(ua.x, ua.y, ub.x, ub.y));
+}
+
 struct __align__(16) SmemA {
-  uint16_t sth[16 * NVT][kKP];   // S^T high part (column v, key k)
-  uint16_t stl[16 * NVT][kKP];   // S^T low part
-  uint16_t kt[BT][kKP];          // bf16 k~ rows (fast) / raw k rows (exact)
-  uint16_t kst[KD][kTP];         // k~s transposed (key k, row j), input dtype
-  uint16_t vt[16 * NVT][kTP];    // V tile transposed (column v, row j)
-  float tot[4][KD];              // per-block column sums of g (log2 units)
-  float fac[4][6][KD];           // per-wavefront per-key values (slots below)
-  int flag[4];                   // per-wavefront "saw a positive log-gate"
-  uint16_t xq[BT][kKP];          // exact mode: raw q rows
-  float xg[BT][kXP];             // exact mode: G2 rows
+  uint16_t sth[64 * 64];   // S^T (column v, key k), input dtype
+  uint16_t kt[64 * 64];    // k 2^(E_J - G) rows (bf16), blocks read by later wavefronts
+  uint16_t kh[64 * 64];    // k 2^(G_last - G) rows (input dtype)
+  uint16_t vs[64 * 64];    // v rows of the V group (input dtype)
+  float tot[4][KD];        // per-block column sums of g (log2 units)
+  float fac[4][8][KD];     // per-wavefront per-key factors (slots below)
 };
-// fac[I][.] slots, lane = key
-constexpr int kFacRel = 0;    // R_I - R         (R_I = G2 at the end of block I-1)
-constexpr int kFacKs = 1;     // 2^(G_last - R)
-constexpr int kFacQ0 = 2;     // 2^(R)
-constexpr int kFacDecay = 3;  // 2^(G_last)
-constexpr int kFacLast = 4;   // G_last          (exact mode)
-constexpr int kFacOwn = 5;    // R_I             (exact mode)
+constexpr int kFacHalf = 0;  // M_I - E_I-1          (G2 - it = G_abs - M_I)
+constexpr int kFacQ0 = 1;    // 2^M_I                (q0 = q~ 2^M_I)
+constexpr int kFacKh = 2;    // 2^(G_last - M_I)     (k^ = k~ 2^(G_last - M_I))
+constexpr int kFacKt = 3;    // 2^(E_I - M_I)        (kt = k~ 2^(E_I - M_I))
+constexpr int kFacDec = 4;   // 2^G_last             (state decay)
+constexpr int kFacQJ = 5;    // 2^(M_I - E_J), J < I (q~ for block J)
 
 __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -148,27 +176,30 @@ __device__ __forceinline__ void row_scan16(f32x8 (&x)[2]) {
   row_scan_step<8>(x);
 }
 
-// Raw global loads for one chunk row of this lane (q, k, g) and 4*NVT values
-// of one V row.
-template <int NVT>
+__device__ __forceinline__ float clamp_exp(float x) { return fminf(fmaxf(x, -kExpClamp), kExpClamp); }
+
+// Raw global loads of one chunk row of this lane: q, k, g at keys
+// {kq..kq+7, 32+kq..32+kq+7} and v at columns {kq.., 32+kq..} (columns
+// beyond the V group are not loaded).
 struct ChunkRegs {
-  uint4 q[2], k[2];   // 2 x 8 keys of this lane's row (16-bit)
-  float4 g[4];        // 16 log-gates (fp32 g) ...
+  uint4 q[2], k[2];   // 16-bit
+  float4 g[4];        // fp32 g ...
   uint4 g16[2];       // ... or 16-bit g
-  uint2 v[NVT];       // 4*NVT values of one V-tile row
+  uint4 v[2];
 };
 
-template <bool GF32, int NVT>
-__device__ __forceinline__ void load_chunk(ChunkRegs<NVT> &R, const uint16_t *__restrict__ q,
+template <bool LOADQ, bool GF32>
+__device__ __forceinline__ void load_chunk(ChunkRegs &R, const uint16_t *__restrict__ q,
                                            const uint16_t *__restrict__ k,
                                            const uint16_t *__restrict__ v, const void *__restrict__ g,
-                                           int64_t t_row, bool row_ok, int64_t t_vrow, bool vrow_ok,
-                                           int H, int V, int h, int kq, int vcol) {
+                                           int64_t t_row, bool row_ok, int H, int V, int h, int kq, int v0,
+                                           int vw) {
   const int64_t base = (t_row * H + h) * KD;
-  if (row_ok) {
+  const uint16_t *vp = v + (t_row * H + h) * V + v0;
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      R.q[jj] = *reinterpret_cast<const uint4 *>(q + base + 32 * jj + kq);
+  for (int jj = 0; jj < 2; ++jj) {
+    if (row_ok) {
+      if (LOADQ) R.q[jj] = *reinterpret_cast<const uint4 *>(q + base + 32 * jj + kq);
       R.k[jj] = *reinterpret_cast<const uint4 *>(k + base + 32 * jj + kq);
       if (GF32) {
         const float *gp = static_cast<const float *>(g) + base + 32 * jj + kq;
@@ -177,26 +208,21 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<NVT> &R, const uint16_t *__
       } else {
         R.g16[jj] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g) + base + 32 * jj + kq);
       }
-    }
-  } else {
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      R.q[jj] = make_uint4(0, 0, 0, 0);
+      R.v[jj] = (32 * jj + kq < vw) ? *reinterpret_cast<const uint4 *>(vp + 32 * jj + kq) : make_uint4(0, 0, 0, 0);
+    } else {
+      if (LOADQ) R.q[jj] = make_uint4(0, 0, 0, 0);
       R.k[jj] = make_uint4(0, 0, 0, 0);
       R.g[2 * jj] = make_float4(0.f, 0.f, 0.f, 0.f);
       R.g[2 * jj + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
       R.g16[jj] = make_uint4(0, 0, 0, 0);
+      R.v[jj] = make_uint4(0, 0, 0, 0);
     }
   }
-  const uint16_t *vp = v + (t_vrow * H + h) * V + vcol;
-#pragma unroll
-  for (int p = 0; p < NVT; ++p)
-    R.v[p] = vrow_ok ? *reinterpret_cast<const uint2 *>(vp + 4 * p) : make_uint2(0, 0);
 }
 
 // Unpack 16 gates (log2 units) of this lane.
-template <int DT, bool GF32, class R_>
-__device__ __forceinline__ void unpack_gates(const R_ &R, f32x8 (&gs)[2]) {
+template <int DT, bool GF32>
+__device__ __forceinline__ void unpack_gates(const ChunkRegs &R, f32x8 (&gs)[2]) {
   typedef Mfma<DT> M;
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
@@ -209,17 +235,14 @@ __device__ __forceinline__ void unpack_gates(const R_ &R, f32x8 (&gs)[2]) {
   }
 }
 
-// Split an fp32 state tile (4 values) into 16-bit high/low parts and store
-// them transposed into the S^T buffers.
-template <int DT, class SM>
-__device__ __forceinline__ void store_state(SM &sm, int vcolumn, int krow, const f32x4 &S) {
+// S (fp32 accumulator tile: keys krow..krow+3, column vcol) -> S^T tile in
+// the input dtype.
+template <int DT>
+__device__ __forceinline__ void store_state(uint16_t *sth, int vcol, int krow, const f32x4 &S) {
   typedef Mfma<DT> M;
   const f32x8 s8 = {S[0], S[1], S[2], S[3], 0.f, 0.f, 0.f, 0.f};
-  const typename M::Vec hi = M::cvt(s8);
-  const typename M::Vec lo = M::cvt(s8 - M::widen(hi));
-  const uint4 hb = to_bits(hi), lb = to_bits(lo);
-  *reinterpret_cast<uint2 *>(&sm.sth[vcolumn][krow]) = make_uint2(hb.x, hb.y);
-  *reinterpret_cast<uint2 *>(&sm.stl[vcolumn][krow]) = make_uint2(lb.x, lb.y);
+  const uint4 b = to_bits(M::cvt(s8));
+  *reinterpret_cast<uint2 *>(sth + swz(vcol, krow)) = make_uint2(b.x, b.y);
 }
 
 struct ChunkArgs {
@@ -228,11 +251,10 @@ struct ChunkArgs {
   const float *h0;
   uint16_t *o;
   float *ht;
-  float *ws_state;   // [n_seq, H, P, K, V] fp32 (P > 1)
-  float *ws_decay;   // [n_seq, H, P, K] fp32, log2 units (P > 1)
-  int64_t bos;       // first row of the sequence
-  int64_t len;       // rows of the sequence
-  int c_beg, c_end;  // chunk range of the segment
+  const float *ws_state;   // [n_seq, H, P, K, V] fp32: slot s-1 = state entering segment s
+  int64_t bos;             // first row of the sequence
+  int64_t len;             // rows of the sequence
+  int c_beg, c_end;        // chunk range of the segment
   int H, V, h, n, v0, seg, P;
   float scale;
 };
@@ -244,282 +266,150 @@ __device__ __forceinline__ void segment_range(int nch, int P, int seg, int &c0, 
   c1 = min(c0 + per, nch);
 }
 
-// Entering state of segment seg >= 1 from the state-pass slots of its
-// (sequence, head): slot 0 is the state after segment 0 (started from h0),
-// slot s >= 1 the state segment s reaches from zero, with total log2 decay
-// D(s):  S_e(1) = slot 0,  S_e(s+1) = 2^D(s) S_e(s) + slot s.
-template <int NVT>
-__device__ __forceinline__ void fold_entering_state(f32x4 (&S)[NVT], const float *__restrict__ ws_state,
-                                                    const float *__restrict__ ws_decay, int64_t slot0,
-                                                    int seg, int krow, int r, int V, int v0) {
-#pragma unroll
-  for (int t = 0; t < NVT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) S[t][i] = ws_state[(slot0 * KD + krow + i) * V + v0 + 16 * t + r];
-  for (int s = 1; s < seg; ++s) {
-    const float *src = ws_state + (slot0 + s) * KD * V;
-    f32x4 d;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) d[i] = fast_exp2(ws_decay[(slot0 + s) * KD + krow + i]);
-#pragma unroll
-    for (int t = 0; t < NVT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        S[t][i] = fmaf(d[i], S[t][i], src[static_cast<int64_t>(krow + i) * V + v0 + 16 * t + r]);
-  }
-}
-
-// Kernel A body.  Wavefront wv (uniform) owns rows 16wv..16wv+15 of every
-// chunk of the segment; the four wavefronts meet at two barriers per chunk.
+// --------------------------------------------------------- segment pass --
 template <int DT, bool GF32, int NVT>
-__device__ __forceinline__ void segment_loop(SmemA<NVT> &sm, const ChunkArgs &a, const int wv, int lane) {
+__device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, const int wv, int lane) {
   typedef Mfma<DT> M;
   typedef typename M::Vec MV;
   const int r = lane & 15;        // row within block / MFMA column index
   const int gq = lane >> 4;       // lane group
   const int kq = 8 * gq;          // key offset of this lane inside each K=32 half
   const int H = a.H, V = a.V, h = a.h, v0 = a.v0;
+  const int vw = 16 * NVT;        // columns of the V group
   const int64_t len = a.len;
 
-  // ---- entering state: rows 16wv + 4gq + i, columns v0 + 16t + r ----------
+  // ---- entering state: keys 16wv + 4gq + i, columns v0 + 16t + r ---------
   const int64_t sbase = (static_cast<int64_t>(a.n) * H + h) * KD;
   const int krow = 16 * wv + 4 * gq;
   f32x4 S[NVT];
-  if (a.seg == 0) {
+  {
+    const float *src = nullptr;
+    if (a.seg == 0) src = a.h0 ? a.h0 + sbase * V : nullptr;
+    else src = a.ws_state + ((static_cast<int64_t>(a.n) * H + h) * a.P + (a.seg - 1)) * KD * V;
 #pragma unroll
     for (int t = 0; t < NVT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) S[t][i] = a.h0 ? a.h0[(sbase + krow + i) * V + v0 + 16 * t + r] : 0.f;
-  } else {
-    fold_entering_state<NVT>(S, a.ws_state, a.ws_decay, (static_cast<int64_t>(a.n) * H + h) * a.P, a.seg,
-                             krow, r, V, v0);
+      for (int i = 0; i < 4; ++i)
+        S[t][i] = src ? src[static_cast<int64_t>(krow + i) * V + v0 + 16 * t + r] : 0.f;
   }
-#pragma unroll
-  for (int t = 0; t < NVT; ++t) store_state<DT>(sm, 16 * t + r, krow, S[t]);
 
-  // V rows staged by this lane: row 16wv + lane/4, columns (lane%4)*4*NVT ..
-  const int vrow = 16 * wv + (lane >> 2);
-  const int vcl = (lane & 3) * 4 * NVT;
-  const int vcol = v0 + vcl;
   const int row = 16 * wv + r;
-
-  ChunkRegs<NVT> buf[2];
+  ChunkRegs buf;
   if (a.c_beg < a.c_end) {
     const int64_t rem0 = len - static_cast<int64_t>(a.c_beg) * BT;
-    const int64_t tb = a.bos + static_cast<int64_t>(a.c_beg) * BT;
-    load_chunk<GF32, NVT>(buf[0], a.q, a.k, a.v, a.g, tb + row, row < rem0, tb + vrow, vrow < rem0, H, V,
-                          h, kq, vcol);
+    load_chunk<true, GF32>(buf, a.q, a.k, a.v, a.g, a.bos + static_cast<int64_t>(a.c_beg) * BT + row, row < rem0,
+                           H, V, h, kq, v0, vw);
   }
 
-  for (int c2 = a.c_beg; c2 < a.c_end; c2 += 2) {
-#pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int c = c2 + par;
-    if (c >= a.c_end) break;
+  for (int c = a.c_beg; c < a.c_end; ++c) {
     const int64_t t0 = a.bos + static_cast<int64_t>(c) * BT;
     const int64_t rem = len - static_cast<int64_t>(c) * BT;   // valid rows in this chunk (>0)
 
-    // ---- unpack: element e of half jj is key 32*jj + kq + e ---------------
-    // The current buffer is consumed before the next prefetch is issued, so
-    // the wait for it (at the loop head the compiler waits for every
-    // outstanding load) never covers the prefetch.
-    f32x8 qf[2], kf[2], gs[2];
-    uint2 vv[NVT];
-    {
-      const ChunkRegs<NVT> &R = buf[par];
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        qf[jj] = M::widen(from_bits<MV>(R.q[jj]));
-        kf[jj] = M::widen(from_bits<MV>(R.k[jj]));
-      }
-      unpack_gates<DT, GF32>(R, gs);
-#pragma unroll
-      for (int p = 0; p < NVT; ++p) vv[p] = R.v[p];
-    }
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    if (c + 1 < a.c_end) {
-      const int64_t rem2 = rem - BT;
-      load_chunk<GF32, NVT>(buf[par ^ 1], a.q, a.k, a.v, a.g, t0 + BT + row, row < rem2, t0 + BT + vrow,
-                            vrow < rem2, H, V, h, kq, vcol);
-    }
-    float gmax = fmaxf(gs[0][0], gs[1][0]);
-#pragma unroll
-    for (int e = 1; e < 8; ++e) gmax = fmaxf(gmax, fmaxf(gs[0][e], gs[1][e]));
     // ---- block-local inclusive cumsum over the 16 rows (DPP row scan) ------
+    f32x8 gs[2];
+    unpack_gates<DT, GF32>(buf, gs);
     row_scan16(gs);
     if (r == 15) {
       *reinterpret_cast<f32x8 *>(&sm.tot[wv][kq]) = gs[0];
       *reinterpret_cast<f32x8 *>(&sm.tot[wv][32 + kq]) = gs[1];
     }
-    const bool wpos = __builtin_amdgcn_ballot_w64(gmax > 0.f) != 0;
-    if (lane == 0) sm.flag[wv] = wpos ? 1 : 0;
     lds_barrier();  // --------------------------------------------- barrier 1
+    // Every wavefront finished chunk c-1, so sth / kt / kh / vs are free.
 
-    // ---- per-key references and factors (lane = key) -----------------------
-    bool exact;
+    // ---- per-key factors (lane = key) --------------------------------------
     {
       const int kk = lane;
-      const float t0_ = sm.tot[0][kk], t1_ = sm.tot[1][kk], t2_ = sm.tot[2][kk], t3_ = sm.tot[3][kk];
-      const float R1 = t0_, R2 = t0_ + t1_, R3 = R2 + t2_, GL = R3 + t3_;
-      const float own = wv == 0 ? 0.f : wv == 1 ? R1 : wv == 2 ? R2 : R3;
-      // without positive gates G2 falls monotonically, so |G2 - R| is largest
-      // at the chunk ends: R (first half) and R - G_last (second half).
-      const bool far = fmaxf(-R2, R2 - GL) > kRangeLimit;
-      exact = (sm.flag[0] | sm.flag[1] | sm.flag[2] | sm.flag[3]) != 0 ||
-              __builtin_amdgcn_ballot_w64(far) != 0;
-      sm.fac[wv][kFacRel][kk] = own - R2;
-      sm.fac[wv][kFacKs][kk] = fast_exp2(GL - R2);
-      sm.fac[wv][kFacQ0][kk] = fast_exp2(R2);
-      sm.fac[wv][kFacDecay][kk] = fast_exp2(GL);
-      sm.fac[wv][kFacLast][kk] = GL;
-      sm.fac[wv][kFacOwn][kk] = own;
+      const float E0 = sm.tot[0][kk];
+      const float E1 = E0 + sm.tot[1][kk];
+      const float E2 = E1 + sm.tot[2][kk];
+      const float E3 = E2 + sm.tot[3][kk];
+      const float Ep = wv == 0 ? 0.f : wv == 1 ? E0 : wv == 2 ? E1 : E2;
+      const float Eo = wv == 0 ? E0 : wv == 1 ? E1 : wv == 2 ? E2 : E3;
+      const float Mi = 0.5f * (Ep + Eo);
+      sm.fac[wv][kFacHalf][kk] = Mi - Ep;
+      sm.fac[wv][kFacQ0][kk] = fast_exp2(clamp_exp(Mi));
+      sm.fac[wv][kFacKh][kk] = fast_exp2(clamp_exp(E3 - Mi));
+      sm.fac[wv][kFacKt][kk] = fast_exp2(clamp_exp(Eo - Mi));
+      sm.fac[wv][kFacDec][kk] = fast_exp2(clamp_exp(E3));
+      if (wv > 0) sm.fac[wv][kFacQJ + 0][kk] = fast_exp2(clamp_exp(Mi - E0));
+      if (wv > 1) sm.fac[wv][kFacQJ + 1][kk] = fast_exp2(clamp_exp(Mi - E1));
+      if (wv > 2) sm.fac[wv][kFacQJ + 2][kk] = fast_exp2(clamp_exp(Mi - E2));
     }
-    // the state entering this chunk (computed at the end of the previous one);
-    // every reader of the previous state passed barrier 1 already
-    if (c > a.c_beg) {
+    // the state entering this chunk (S^T in the input dtype) and the V rows
 #pragma unroll
-      for (int t = 0; t < NVT; ++t) store_state<DT>(sm, 16 * t + r, krow, S[t]);
-    }
+    for (int t = 0; t < NVT; ++t) store_state<DT>(sm.sth, 16 * t + r, krow, S[t]);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+      if (32 * jj + kq < vw) tile_store8(sm.vs, row, 32 * jj + kq, buf.v[jj]);
     wave_sync_lds();
-    // own-row decays of the state rows 16wv + 4gq + i
-    const f32x4 sdec = *reinterpret_cast<const f32x4 *>(&sm.fac[wv][kFacDecay][krow]);
 
     // ---- operands ------------------------------------------------------------
-    // fast: q~ = q 2^(G2 - R) (MFMA B operand of A^T), q~0 = q~ 2^R (of o_inter),
-    //       k~ = k 2^(R - G2) (to LDS), k~s = k~ 2^(G_last - R) (to LDS, transposed)
-    QK::Vec qtb[2];    // q~ as bf16 (fast) / q 2^(G2 - R_I) (exact, off-diagonal blocks)
-    MV q0b[2];         // q~0 in the input dtype
-    {
-      f32x8 ks[2];
-      if (!exact) {
-        f32x8 rel[2], fks[2], fq0[2];
-        lds_keys(sm.fac[wv][kFacRel], kq, rel);
-        lds_keys(sm.fac[wv][kFacKs], kq, fks);
-        lds_keys(sm.fac[wv][kFacQ0], kq, fq0);
-        f32x8 kt[2];
+    // q~ = q 2^(G - M), k~ = k 2^(M - G) with G relative to the block start
+    // (G2 - (M - E_I-1) = G_abs - M); q0 = q~ 2^M, k^ = k~ 2^(G_last - M),
+    // kt = k~ 2^(E_I - M).  One K=32 half at a time keeps few registers live.
+    QK::Vec qd[2], kd[2];   // diagonal-block operands (bf16)
+    MV q0b[2];
+    auto operand_half = [&](const int jj) {
+      const f32x8 half = *reinterpret_cast<const f32x8 *>(&sm.fac[wv][kFacHalf][32 * jj + kq]);
+      const f32x8 qf = M::widen(from_bits<MV>(buf.q[jj]));
+      const f32x8 kf = M::widen(from_bits<MV>(buf.k[jj]));
+      f32x8 eq, ek;
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const f32x8 x = gs[jj] + rel[jj];             // G2 - R
-          f32x8 eq, ek;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            eq[e] = fast_exp2(x[e]);
-            ek[e] = fast_exp2(-x[e]);
-          }
-          const f32x8 qt = qf[jj] * eq;
-          kt[jj] = kf[jj] * ek;
-          ks[jj] = kt[jj] * fks[jj];
-          qtb[jj] = QK::cvt(qt);
-          q0b[jj] = M::cvt(qt * fq0[jj]);
-        }
-        *reinterpret_cast<uint4 *>(&sm.kt[row][kq]) = to_bits(QK::cvt(kt[0]));
-        *reinterpret_cast<uint4 *>(&sm.kt[row][32 + kq]) = to_bits(QK::cvt(kt[1]));
-      } else {
-        f32x8 own8[2], gl[2];
-        lds_keys(sm.fac[wv][kFacOwn], kq, own8);
-        lds_keys(sm.fac[wv][kFacLast], kq, gl);
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const f32x8 gabs = gs[jj] + own8[jj];
-          f32x8 eq, e0, ek;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            eq[e] = fast_exp2(gs[jj][e]);                 // 2^(G2_i - R_I)
-            e0[e] = fast_exp2(gabs[e]);                   // 2^(G2_i)
-            ek[e] = fast_exp2(gl[jj][e] - gabs[e]);       // 2^(G_last - G2_j)
-          }
-          qtb[jj] = QK::cvt(qf[jj] * eq);
-          q0b[jj] = M::cvt(qf[jj] * e0);
-          ks[jj] = kf[jj] * ek;
-          *reinterpret_cast<uint4 *>(&sm.xq[row][32 * jj + kq]) = to_bits(M::cvt(qf[jj]));
-          *reinterpret_cast<uint4 *>(&sm.kt[row][32 * jj + kq]) = to_bits(M::cvt(kf[jj]));
-          *reinterpret_cast<f32x8 *>(&sm.xg[row][32 * jj + kq]) = gabs;
-        }
+      for (int e = 0; e < 8; ++e) {
+        const float x = clamp_exp(gs[jj][e] - half[e]);
+        eq[e] = fast_exp2(x);
+        ek[e] = fast_exp2(-x);
       }
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const uint4 kb = to_bits(M::cvt(ks[jj]));
-        const uint32_t w4[4] = {kb.x, kb.y, kb.z, kb.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          sm.kst[32 * jj + kq + e][row] =
-              static_cast<uint16_t>((e & 1) ? (w4[e >> 1] >> 16) : (w4[e >> 1] & 0xffffu));
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < NVT; ++p) {
-      sm.vt[vcl + 4 * p + 0][vrow] = static_cast<uint16_t>(vv[p].x & 0xffffu);
-      sm.vt[vcl + 4 * p + 1][vrow] = static_cast<uint16_t>(vv[p].x >> 16);
-      sm.vt[vcl + 4 * p + 2][vrow] = static_cast<uint16_t>(vv[p].y & 0xffffu);
-      sm.vt[vcl + 4 * p + 3][vrow] = static_cast<uint16_t>(vv[p].y >> 16);
-    }
+      const f32x8 qt = qf * eq, kt = kf * ek;
+      qd[jj] = QK::cvt(qt);
+      kd[jj] = QK::cvt(kt);
+      q0b[jj] = M::cvt(qt * *reinterpret_cast<const f32x8 *>(&sm.fac[wv][kFacQ0][32 * jj + kq]));
+      tile_store8(sm.kh, row, 32 * jj + kq,
+                  to_bits(M::cvt(kt * *reinterpret_cast<const f32x8 *>(&sm.fac[wv][kFacKh][32 * jj + kq]))));
+      tile_store8(sm.kt, row, 32 * jj + kq,
+                  to_bits(QK::cvt(kt * *reinterpret_cast<const f32x8 *>(&sm.fac[wv][kFacKt][32 * jj + kq]))));
+    };
+    operand_half(0);
+    __builtin_amdgcn_sched_barrier(0);
+    operand_half(1);
     lds_barrier();  // --------------------------------------------- barrier 2
+
+    // the registers of chunk c are consumed: prefetch chunk c+1
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < a.c_end)
+      load_chunk<true, GF32>(buf, a.q, a.k, a.v, a.g, t0 + BT + row, row < rem - BT, H, V, h, kq, v0, vw);
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- A^T blocks (rows j of block J, columns i of this block) ------------
     // blocks J > wv are zero, block J == wv is causally masked.
     f32x4 at[4];
-    if (!exact) {
 #pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        at[J] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        if (J <= wv) {
-          const QK::Vec a0 = from_bits<QK::Vec>(*reinterpret_cast<const uint4 *>(&sm.kt[16 * J + r][kq]));
-          const QK::Vec a1 = from_bits<QK::Vec>(*reinterpret_cast<const uint4 *>(&sm.kt[16 * J + r][32 + kq]));
-          at[J] = QK::mma(a0, qtb[0], at[J]);
-          at[J] = QK::mma(a1, qtb[1], at[J]);
+    for (int J = 0; J < 4; ++J) at[J] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int J = 0; J < 3; ++J) {
+      if (J < wv) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const f32x8 fj = *reinterpret_cast<const f32x8 *>(&sm.fac[wv][kFacQJ + J][32 * jj + kq]);
+          const QK::Vec aj = from_bits<QK::Vec>(tile_row8(sm.kt, 16 * J + r, 32 * jj + kq));
+          const QK::Vec bj = QK::cvt(QK::widen(qd[jj]) * fj);
+          at[J] = QK::mma(aj, bj, at[J]);
         }
-      }
-    } else {
-      f32x8 own8[2];
-      lds_keys(sm.fac[wv][kFacOwn], kq, own8);
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        at[J] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        if (J < wv) {   // off-diagonal: k re-referenced to R_I (<= 1 for decays)
-          const int jrow = 16 * J + r;
-          QK::Vec kj[2];
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
-            const f32x8 kr = M::widen(from_bits<MV>(*reinterpret_cast<const uint4 *>(&sm.kt[jrow][32 * jj + kq])));
-            const f32x8 gr = *reinterpret_cast<const f32x8 *>(&sm.xg[jrow][32 * jj + kq]);
-            f32x8 e2;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) e2[e] = fast_exp2(own8[jj][e] - gr[e]);
-            kj[jj] = QK::cvt(kr * e2);
-          }
-          at[J] = QK::mma(kj[0], qtb[0], at[J]);
-          at[J] = QK::mma(kj[1], qtb[1], at[J]);
-        }
-      }
-      // diagonal block elementwise: lane holds A[i = r][j = 4gq + ii]
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int j = 4 * gq + ii;
-        const int jrow = 16 * wv + j;
-        float acc = 0.f;
-        if (j <= r) {
-#pragma unroll 1
-          for (int k8 = 0; k8 < KD; k8 += 8) {
-            const f32x8 qv = M::widen(from_bits<MV>(*reinterpret_cast<const uint4 *>(&sm.xq[row][k8])));
-            const f32x8 kv = M::widen(from_bits<MV>(*reinterpret_cast<const uint4 *>(&sm.kt[jrow][k8])));
-            const f32x8 gi = *reinterpret_cast<const f32x8 *>(&sm.xg[row][k8]);
-            const f32x8 gj = *reinterpret_cast<const f32x8 *>(&sm.xg[jrow][k8]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc += qv[e] * kv[e] * fast_exp2(gi[e] - gj[e]);
-          }
-        }
-#pragma unroll
-        for (int J = 0; J < 4; ++J)
-          if (J == wv) at[J][ii] = acc;
       }
     }
-    // causal mask on the diagonal block (row i = r, column j = 4gq + ii)
-#pragma unroll
-    for (int J = 0; J < 4; ++J)
+    {
+      f32x4 dg = (f32x4){0.f, 0.f, 0.f, 0.f};
+      dg = QK::mma(kd[0], qd[0], dg);
+      dg = QK::mma(kd[1], qd[1], dg);
+      // causal mask on the diagonal block (row i = r, column j = 4gq + ii)
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
-        if (J == wv && 4 * gq + ii > r) at[J][ii] = 0.f;
+        if (4 * gq + ii > r) dg[ii] = 0.f;
+#pragma unroll
+      for (int J = 0; J < 4; ++J)
+        if (J == wv) at[J] = dg;
+    }
     // A as the B operand of V^T A^T: K slots 0-3 <- block 2pr, 4-7 <- block 2pr+1
     MV ab[2];
 #pragma unroll
@@ -529,24 +419,18 @@ __device__ __forceinline__ void segment_loop(SmemA<NVT> &sm, const ChunkArgs &a,
       ab[pr] = M::cvt(av);
     }
 
-    // ---- per V tile: o^T = S^T q~0^T + V^T A^T, store, state update ----------
+    // ---- per V tile: o^T = S^T q0^T + V^T A^T, store ---------------------------
 #pragma unroll
     for (int t = 0; t < NVT; ++t) {
-      const int vc = 16 * t + r;
       f32x4 oacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const MV shi = from_bits<MV>(*reinterpret_cast<const uint4 *>(&sm.sth[vc][32 * jj + kq]));
-        const MV slo = from_bits<MV>(*reinterpret_cast<const uint4 *>(&sm.stl[vc][32 * jj + kq]));
-        oacc = M::mma(shi, q0b[jj], oacc);
-        oacc = M::mma(slo, q0b[jj], oacc);
-      }
+      for (int jj = 0; jj < 2; ++jj)
+        oacc = M::mma(from_bits<MV>(tile_row8(sm.sth, 16 * t + r, 32 * jj + kq)), q0b[jj], oacc);
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) {
         if (2 * pr <= wv) {
-          const uint2 va = *reinterpret_cast<const uint2 *>(&sm.vt[vc][32 * pr + 4 * gq]);
-          const uint2 vb = *reinterpret_cast<const uint2 *>(&sm.vt[vc][32 * pr + 16 + 4 * gq]);
-          oacc = M::mma(from_bits<MV>(make_uint4(va.x, va.y, vb.x, vb.y)), ab[pr], oacc);
+          const MV va = tr_operand<MV>(sm.vs, 32 * pr + 4 * gq, 32 * pr + 16 + 4 * gq, 16 * t, lane);
+          oacc = M::mma(va, ab[pr], oacc);
         }
       }
       if (row < rem) {
@@ -556,16 +440,21 @@ __device__ __forceinline__ void segment_loop(SmemA<NVT> &sm, const ChunkArgs &a,
         *reinterpret_cast<uint2 *>(a.o + ((t0 + row) * H + h) * V + v0 + 16 * t + 4 * gq) =
             make_uint2(ob.x, ob.y);
       }
-      // S <- 2^(G_last) S + Ks^T V for the state rows of this wavefront
-      S[t] *= sdec;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- S <- 2^(G_last) S + k^^T V for the state rows of this wavefront ------
+    {
+      const f32x4 sdec = *reinterpret_cast<const f32x4 *>(&sm.fac[wv][kFacDec][krow]);
+      const MV ka0 = tr_operand<MV>(sm.kh, 8 * gq, 8 * gq + 4, 16 * wv, lane);
+      const MV ka1 = tr_operand<MV>(sm.kh, 32 + 8 * gq, 32 + 8 * gq + 4, 16 * wv, lane);
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const MV ka = from_bits<MV>(*reinterpret_cast<const uint4 *>(&sm.kst[row][32 * jj + kq]));
-        const MV vb = from_bits<MV>(*reinterpret_cast<const uint4 *>(&sm.vt[vc][32 * jj + kq]));
-        S[t] = M::mma(ka, vb, S[t]);
+      for (int t = 0; t < NVT; ++t) {
+        S[t] *= sdec;
+        S[t] = M::mma(ka0, tr_operand<MV>(sm.vs, 8 * gq, 8 * gq + 4, 16 * t, lane), S[t]);
+        S[t] = M::mma(ka1, tr_operand<MV>(sm.vs, 32 + 8 * gq, 32 + 8 * gq + 4, 16 * t, lane), S[t]);
       }
     }
-  }
   }
 
   // ---- final state of the sequence -----------------------------------------
@@ -578,13 +467,13 @@ __device__ __forceinline__ void segment_loop(SmemA<NVT> &sm, const ChunkArgs &a,
 }
 
 template <int DT, bool GF32, int NVT>
-__global__ __launch_bounds__(256, 2) void gla_chunk_segment_kernel(
+__global__ __launch_bounds__(256, SSLA_GC_SEG_WAVES) void gla_chunk_segment_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
     const uint16_t *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int64_t T, int H, int V, float scale,
     const float *__restrict__ h0, uint16_t *__restrict__ o, float *__restrict__ ht, int P,
-    float *__restrict__ ws_state, float *__restrict__ ws_decay) {
-  __shared__ SmemA<NVT> sm;
+    const float *__restrict__ ws_state) {
+  __shared__ SmemA sm;
   const int nvg = V / (16 * NVT);
   // block -> (sequence, head, V group, segment); the segments of one
   // (sequence, head) are consecutive
@@ -598,7 +487,7 @@ __global__ __launch_bounds__(256, 2) void gla_chunk_segment_kernel(
   a.h = static_cast<int>(b % H);
   a.n = static_cast<int>(b / H);
   a.q = q; a.k = k; a.v = v; a.g = g; a.h0 = h0; a.o = o; a.ht = ht;
-  a.ws_state = ws_state; a.ws_decay = ws_decay;
+  a.ws_state = ws_state;
   a.H = H; a.V = V; a.scale = scale;
   a.v0 = vg * 16 * NVT;
   a.bos = min(max(cu_seqlens[a.n], (int64_t)0), T);
@@ -608,12 +497,12 @@ __global__ __launch_bounds__(256, 2) void gla_chunk_segment_kernel(
   segment_loop<DT, GF32, NVT>(sm, a, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), threadIdx.x & 63);
 }
 
-// ------------------------------------------------------------ kernel S ----
-template <int NVT>
+// ----------------------------------------------------------- state pass --
 struct __align__(16) SmemS {
-  uint16_t kst[KD][kTP];         // k~s transposed (key k, row j), input dtype
-  uint16_t vt[16 * NVT][kTP];    // V tile transposed (column v, row j)
-  float tot[2][4][KD];           // per-block column sums of g, by chunk parity
+  uint16_t kh[64 * 64];    // k 2^(G_last - G) rows
+  uint16_t vs[64 * 64];    // v rows of the V group
+  float tot[2][4][KD];     // per-block column sums of g, by chunk parity
+  float fac[4][2][KD];     // per-wavefront per-key: G_last - E_I-1, 2^G_last
 };
 
 // State-only walk over segment seg (< P - 1) of one (sequence, head, V
@@ -621,13 +510,13 @@ struct __align__(16) SmemS {
 // for segment 0 and from zero otherwise.  Writes the workspace slot and,
 // for seg >= 1, the segment's total log2 decay.
 template <int DT, bool GF32, int NVT>
-__global__ __launch_bounds__(256, 2) void gla_chunk_state_kernel(
+__global__ __launch_bounds__(256, 4) void gla_chunk_state_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int64_t T, int H, int V,
     const float *__restrict__ h0, int P, float *__restrict__ ws_state, float *__restrict__ ws_decay) {
   typedef Mfma<DT> M;
   typedef typename M::Vec MV;
-  __shared__ SmemS<NVT> sm;
+  __shared__ SmemS sm;
   const int nvg = V / (16 * NVT);
   int64_t b = blockIdx.x;
   const int seg = static_cast<int>(b % (P - 1));
@@ -637,13 +526,12 @@ __global__ __launch_bounds__(256, 2) void gla_chunk_state_kernel(
   const int h = static_cast<int>(b % H);
   const int n = static_cast<int>(b / H);
   const int v0 = vg * 16 * NVT;
+  const int vw = 16 * NVT;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, gq = lane >> 4, kq = 8 * gq;
   const int krow = 16 * wv + 4 * gq;
   const int row = 16 * wv + r;
-  const int vrow = 16 * wv + (lane >> 2);
-  const int vcl = (lane & 3) * 4 * NVT;
 
   const int64_t sbase = (static_cast<int64_t>(n) * H + h) * KD;
   f32x4 S[NVT];
@@ -660,131 +548,66 @@ __global__ __launch_bounds__(256, 2) void gla_chunk_state_kernel(
   segment_range(static_cast<int>((len + BT - 1) / BT), P, seg, c_beg, c_end);
   float dsum = 0.f;   // lane = key
 
-  struct StateRegs {
-    uint4 k[2];
-    float4 g[4];
-    uint4 g16[2];
-    uint2 v[NVT];
-  };
-  auto load_state = [&](StateRegs &R, int c) {
+  ChunkRegs buf;
+  if (c_beg < c_end) {
+    const int64_t rem0 = len - static_cast<int64_t>(c_beg) * BT;
+    load_chunk<false, GF32>(buf, nullptr, k, v, g, bos + static_cast<int64_t>(c_beg) * BT + row, row < rem0, H, V,
+                            h, kq, v0, vw);
+  }
+  for (int c = c_beg; c < c_end; ++c) {
+    const int par = (c - c_beg) & 1;
     const int64_t t0 = bos + static_cast<int64_t>(c) * BT;
     const int64_t rem = len - static_cast<int64_t>(c) * BT;
-    const bool ok = row < rem;
-    const int64_t base = ((t0 + row) * H + h) * KD;
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      R.k[jj] = ok ? *reinterpret_cast<const uint4 *>(k + base + 32 * jj + kq) : make_uint4(0, 0, 0, 0);
-      if (GF32) {
-        const float *gp = static_cast<const float *>(g) + base + 32 * jj + kq;
-        R.g[2 * jj] = ok ? *reinterpret_cast<const float4 *>(gp) : make_float4(0.f, 0.f, 0.f, 0.f);
-        R.g[2 * jj + 1] = ok ? *reinterpret_cast<const float4 *>(gp + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-      } else {
-        R.g16[jj] = ok ? *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g) + base + 32 * jj + kq)
-                       : make_uint4(0, 0, 0, 0);
-      }
-    }
-    const bool vok = vrow < rem;
-    const uint16_t *vp = v + ((t0 + vrow) * H + h) * V + v0 + vcl;
-#pragma unroll
-    for (int p = 0; p < NVT; ++p)
-      R.v[p] = vok ? *reinterpret_cast<const uint2 *>(vp + 4 * p) : make_uint2(0, 0);
-  };
-
-  StateRegs sb[2];
-  if (c_beg < c_end) load_state(sb[0], c_beg);
-  for (int c2 = c_beg; c2 < c_end; c2 += 2) {
-#pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int c = c2 + par;
-    if (c >= c_end) break;
-    f32x8 kf[2], gs[2];
-    uint2 vv[NVT];
-    {
-      const StateRegs &R = sb[par];
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) kf[jj] = M::widen(from_bits<MV>(R.k[jj]));
-      unpack_gates<DT, GF32>(R, gs);
-#pragma unroll
-      for (int p = 0; p < NVT; ++p) vv[p] = R.v[p];
-    }
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    if (c + 1 < c_end) load_state(sb[par ^ 1], c + 1);
+    f32x8 gs[2];
+    unpack_gates<DT, GF32>(buf, gs);
     row_scan16(gs);
     if (r == 15) {
       *reinterpret_cast<f32x8 *>(&sm.tot[par][wv][kq]) = gs[0];
       *reinterpret_cast<f32x8 *>(&sm.tot[par][wv][32 + kq]) = gs[1];
     }
-    lds_barrier();  // ------------------------------ barrier 1 (totals ready)
-    // G_abs - G_last for this lane's keys; state decay of its rows
-    f32x8 off[2], gl[2];
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      off[jj] = (f32x8){0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      gl[jj] = off[jj];
-    }
-#pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      f32x8 tj[2];
-      lds_keys(sm.tot[par][J], kq, tj);
-      if (J < wv) {
-        off[0] += tj[0];
-        off[1] += tj[1];
-      }
-      gl[0] += tj[0];
-      gl[1] += tj[1];
-    }
-    f32x4 sdec;
+    lds_barrier();  // ------------------- barrier 1 (totals ready; kh, vs free)
     {
-      float d4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int J = 0; J < 4; ++J) {
-        const f32x4 tj = *reinterpret_cast<const f32x4 *>(&sm.tot[par][J][krow]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d4[i] += tj[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sdec[i] = fast_exp2(d4[i]);
-      if (wv == 0 && seg > 0) {
-        float dl = 0.f;
-#pragma unroll
-        for (int J = 0; J < 4; ++J) dl += sm.tot[par][J][lane];
-        dsum += dl;
-      }
+      // lane = key: G_last - E_(wv-1) and 2^G_last
+      const int kk = lane;
+      const float E0 = sm.tot[par][0][kk];
+      const float E1 = E0 + sm.tot[par][1][kk];
+      const float E2 = E1 + sm.tot[par][2][kk];
+      const float E3 = E2 + sm.tot[par][3][kk];
+      const float Ep = wv == 0 ? 0.f : wv == 1 ? E0 : wv == 2 ? E1 : E2;
+      sm.fac[wv][0][kk] = E3 - Ep;
+      sm.fac[wv][1][kk] = fast_exp2(clamp_exp(E3));
+      if (wv == 0 && seg > 0) dsum += E3;
     }
 #pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+      if (32 * jj + kq < vw) tile_store8(sm.vs, row, 32 * jj + kq, buf.v[jj]);
+    wave_sync_lds();
+#pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
+      const f32x8 lg = *reinterpret_cast<const f32x8 *>(&sm.fac[wv][0][32 * jj + kq]);
       f32x8 e2;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) e2[e] = fast_exp2(gl[jj][e] - (gs[jj][e] + off[jj][e]));
-      const uint4 kb = to_bits(M::cvt(kf[jj] * e2));
-      const uint32_t w4[4] = {kb.x, kb.y, kb.z, kb.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        sm.kst[32 * jj + kq + e][row] =
-            static_cast<uint16_t>((e & 1) ? (w4[e >> 1] >> 16) : (w4[e >> 1] & 0xffffu));
+      for (int e = 0; e < 8; ++e) e2[e] = fast_exp2(clamp_exp(lg[e] - gs[jj][e]));
+      const f32x8 kf = M::widen(from_bits<MV>(buf.k[jj]));
+      tile_store8(sm.kh, row, 32 * jj + kq, to_bits(M::cvt(kf * e2)));
     }
-#pragma unroll
-    for (int p = 0; p < NVT; ++p) {
-      sm.vt[vcl + 4 * p + 0][vrow] = static_cast<uint16_t>(vv[p].x & 0xffffu);
-      sm.vt[vcl + 4 * p + 1][vrow] = static_cast<uint16_t>(vv[p].x >> 16);
-      sm.vt[vcl + 4 * p + 2][vrow] = static_cast<uint16_t>(vv[p].y & 0xffffu);
-      sm.vt[vcl + 4 * p + 3][vrow] = static_cast<uint16_t>(vv[p].y >> 16);
-    }
-    lds_barrier();  // ------------------------------ barrier 2 (k~s, V ready)
+    const f32x4 sdec = *reinterpret_cast<const f32x4 *>(&sm.fac[wv][1][krow]);
+    lds_barrier();  // ------------------------------ barrier 2 (k^, V ready)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < c_end)
+      load_chunk<false, GF32>(buf, nullptr, k, v, g, t0 + BT + row, row < rem - BT, H, V, h, kq, v0, vw);
+    __builtin_amdgcn_sched_barrier(0);
+    const MV ka0 = tr_operand<MV>(sm.kh, 8 * gq, 8 * gq + 4, 16 * wv, lane);
+    const MV ka1 = tr_operand<MV>(sm.kh, 32 + 8 * gq, 32 + 8 * gq + 4, 16 * wv, lane);
 #pragma unroll
     for (int t = 0; t < NVT; ++t) {
       S[t] *= sdec;
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const MV ka = from_bits<MV>(*reinterpret_cast<const uint4 *>(&sm.kst[row][32 * jj + kq]));
-        const MV vb = from_bits<MV>(*reinterpret_cast<const uint4 *>(&sm.vt[16 * t + r][32 * jj + kq]));
-        S[t] = M::mma(ka, vb, S[t]);
-      }
+      S[t] = M::mma(ka0, tr_operand<MV>(sm.vs, 8 * gq, 8 * gq + 4, 16 * t, lane), S[t]);
+      S[t] = M::mma(ka1, tr_operand<MV>(sm.vs, 32 + 8 * gq, 32 + 8 * gq + 4, 16 * t, lane), S[t]);
     }
-    // kst / vt are rewritten after the next chunk's barrier 1, which every
-    // wavefront reaches only after these reads
-  }
+    // kh / vs / fac are rewritten after the next chunk's barrier 1, which
+    // every wavefront reaches only after these reads
   }
 
   const int64_t slot = (static_cast<int64_t>(n) * H + h) * P + seg;
@@ -796,6 +619,40 @@ __global__ __launch_bounds__(256, 2) void gla_chunk_state_kernel(
   if (wv == 0 && v0 == 0) ws_decay[slot * KD + lane] = dsum;
 }
 
+// ----------------------------------------------------------- prefix fold --
+// One thread per (sequence, head, key, column): E(1) = slot 0 and
+// E(s+1) = 2^D(s) E(s) + slot s for s = 1..P-2, written back in place.
+// Slots are read eight at a time ahead of the serial fold.
+__global__ __launch_bounds__(256) void gla_chunk_fold_kernel(float *__restrict__ ws_state,
+                                                             const float *__restrict__ ws_decay, int64_t n_elems,
+                                                             int V, int P) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_elems) return;
+  const int64_t kv = static_cast<int64_t>(KD) * V;
+  const int64_t chain = i / kv, e = i % kv;
+  const int key = static_cast<int>(e / V);
+  float *base = ws_state + chain * P * kv + e;
+  const float *dec = ws_decay + chain * P * KD + key;
+  float acc = base[0];
+  for (int s0 = 1; s0 < P - 1; s0 += 8) {
+    float x[8], d[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + u;
+      x[u] = s < P - 1 ? base[s * kv] : 0.f;
+      d[u] = s < P - 1 ? dec[static_cast<int64_t>(s) * KD] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int s = s0 + u;
+      if (s < P - 1) {
+        acc = fmaf(fast_exp2(clamp_exp(d[u])), acc, x[u]);
+        base[s * kv] = acc;
+      }
+    }
+  }
+}
+
 inline int pick_nvt(int V) {
   const int tiles = V / 16;
   for (int nvt = 4; nvt >= 1; --nvt)
@@ -803,8 +660,9 @@ inline int pick_nvt(int V) {
   return 1;
 }
 
-// Segments per sequence: about two workgroups per CU (256 CUs), at least two
-// chunks per segment on average, at most 64 segments.
+// Segments per sequence: about two workgroups per CU (256 CUs), at least
+// two chunks per segment on average, at most 64 segments, and a count that
+// leaves no segment empty (P = ceil(chunks / ceil(chunks / P))).
 inline int pick_segments(int n_seq, int64_t T, int H, int V) {
   const int nvg = V / (16 * pick_nvt(V));
   const int64_t chains = static_cast<int64_t>(n_seq) * H * nvg;
@@ -813,7 +671,12 @@ inline int pick_segments(int n_seq, int64_t T, int H, int V) {
   const int64_t avg_chunks = (T / std::max<int64_t>(n_seq, 1) + BT - 1) / BT;
   p = std::min<int64_t>(p, std::max<int64_t>(1, avg_chunks / 2));
   p = std::min<int64_t>(p, 64);
-  return static_cast<int>(std::max<int64_t>(p, 1));
+  p = std::max<int64_t>(p, 1);
+  if (avg_chunks > 0) {
+    const int64_t per = (avg_chunks + p - 1) / p;
+    p = (avg_chunks + per - 1) / per;
+  }
+  return static_cast<int>(p);
 }
 
 inline size_t workspace_bytes_for(int n_seq, int H, int V, int P) {
@@ -839,11 +702,16 @@ int launch_nvt(const void *q, const void *k, const void *v, const void *g, const
     hipLaunchKernelGGL((gla_chunk_state_kernel<DT, GF32, NVT>), dim3(static_cast<unsigned>(blocks_s)),
                        dim3(256), 0, st, static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
                        g, cu, n_seq, T, H, V, h0, P, ws_state, ws_decay);
+    if (P > 2) {
+      const int64_t n_elems = static_cast<int64_t>(n_seq) * H * KD * V;
+      hipLaunchKernelGGL(gla_chunk_fold_kernel, dim3(static_cast<unsigned>((n_elems + 255) / 256)), dim3(256), 0,
+                         st, ws_state, ws_decay, n_elems, V, P);
+    }
   }
   hipLaunchKernelGGL((gla_chunk_segment_kernel<DT, GF32, NVT>), dim3(static_cast<unsigned>(blocks_a)),
                      dim3(256), 0, st, q16, static_cast<const uint16_t *>(k),
                      static_cast<const uint16_t *>(v), g, cu, n_seq, T, H, V, scale, h0, o16, ht, P,
-                     ws_state, ws_decay);
+                     ws_state);
   return launch_status("gla_chunk_fwd");
 }
 
@@ -883,8 +751,8 @@ extern "C" int ssla_gla_chunk_fwd(const void *q, const void *k, const void *v, c
   if (n_seq == 0) return SSLA_OK;
   SSLA_CHECK_ARG(cu_seqlens != nullptr, "gla_chunk_fwd: cu_seqlens is NULL");
   SSLA_CHECK_ARG(T == 0 || (q && k && v && g && o), "gla_chunk_fwd: null tensor pointer");
-  SSLA_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(g, 16) && aligned(v, 8) && aligned(o, 8),
-                 "gla_chunk_fwd: q/k/g must be 16-byte and v/o 8-byte aligned");
+  SSLA_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(g, 16) && aligned(v, 16) && aligned(o, 8),
+                 "gla_chunk_fwd: q/k/g/v must be 16-byte and o 8-byte aligned");
   if (dtype != SSLA_BF16 && dtype != SSLA_F16) {
     set_error("gla_chunk_fwd: dtype %d not supported (bf16 or fp16)", dtype);
     return SSLA_ERR_DTYPE;
