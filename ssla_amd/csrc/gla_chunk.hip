@@ -51,6 +51,9 @@ namespace {
 constexpr int BT = 64;    // chunk rows
 constexpr int KD = 64;    // key width
 constexpr float kExpClamp = 126.f;
+#ifndef SSLA_GC_STATE_WAVES
+#define SSLA_GC_STATE_WAVES 3
+#endif
 #ifndef SSLA_GC_SEG_WAVES
 #define SSLA_GC_SEG_WAVES 2
 #endif
@@ -151,12 +154,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// 16 per-key values of this lane's key set from an LDS row of 64.
-__device__ __forceinline__ void lds_keys(const float *row, int kq, f32x8 out[2]) {
-  out[0] = *reinterpret_cast<const f32x8 *>(row + kq);
-  out[1] = *reinterpret_cast<const f32x8 *>(row + 32 + kq);
-}
-
 // 16 independent inclusive row scans, step-major so that consecutive DPP
 // instructions never depend on each other.
 template <int N>
@@ -188,27 +185,28 @@ struct ChunkRegs {
   uint4 v[2];
 };
 
+// off: element offset of this lane's row and first key in q, k, g
+// ([T, H, 64] layout); offv: element offset of its row and first column in
+// v ([T, H, V] layout, V group applied).  Both advance by a constant per
+// chunk, so no address is recomputed inside the chunk loops.
 template <bool LOADQ, bool GF32>
 __device__ __forceinline__ void load_chunk(ChunkRegs &R, const uint16_t *__restrict__ q,
                                            const uint16_t *__restrict__ k,
                                            const uint16_t *__restrict__ v, const void *__restrict__ g,
-                                           int64_t t_row, bool row_ok, int H, int V, int h, int kq, int v0,
-                                           int vw) {
-  const int64_t base = (t_row * H + h) * KD;
-  const uint16_t *vp = v + (t_row * H + h) * V + v0;
+                                           int64_t off, int64_t offv, bool row_ok, int kq, int vw) {
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
     if (row_ok) {
-      if (LOADQ) R.q[jj] = *reinterpret_cast<const uint4 *>(q + base + 32 * jj + kq);
-      R.k[jj] = *reinterpret_cast<const uint4 *>(k + base + 32 * jj + kq);
+      if (LOADQ) R.q[jj] = *reinterpret_cast<const uint4 *>(q + off + 32 * jj);
+      R.k[jj] = *reinterpret_cast<const uint4 *>(k + off + 32 * jj);
       if (GF32) {
-        const float *gp = static_cast<const float *>(g) + base + 32 * jj + kq;
+        const float *gp = static_cast<const float *>(g) + off + 32 * jj;
         R.g[2 * jj] = *reinterpret_cast<const float4 *>(gp);
         R.g[2 * jj + 1] = *reinterpret_cast<const float4 *>(gp + 4);
       } else {
-        R.g16[jj] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g) + base + 32 * jj + kq);
+        R.g16[jj] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g) + off + 32 * jj);
       }
-      R.v[jj] = (32 * jj + kq < vw) ? *reinterpret_cast<const uint4 *>(vp + 32 * jj + kq) : make_uint4(0, 0, 0, 0);
+      R.v[jj] = (32 * jj + kq < vw) ? *reinterpret_cast<const uint4 *>(v + offv + 32 * jj) : make_uint4(0, 0, 0, 0);
     } else {
       if (LOADQ) R.q[jj] = make_uint4(0, 0, 0, 0);
       R.k[jj] = make_uint4(0, 0, 0, 0);
@@ -294,20 +292,30 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
   }
 
   const int row = 16 * wv + r;
+  const int64_t strk = static_cast<int64_t>(BT) * H * KD, strv = static_cast<int64_t>(BT) * H * V;
+  int64_t off = ((a.bos + static_cast<int64_t>(a.c_beg) * BT + row) * H + h) * KD + kq;
+  int64_t offv = ((a.bos + static_cast<int64_t>(a.c_beg) * BT + row) * H + h) * V + v0;   // row start
   ChunkRegs buf;
-  if (a.c_beg < a.c_end) {
-    const int64_t rem0 = len - static_cast<int64_t>(a.c_beg) * BT;
-    load_chunk<true, GF32>(buf, a.q, a.k, a.v, a.g, a.bos + static_cast<int64_t>(a.c_beg) * BT + row, row < rem0,
-                           H, V, h, kq, v0, vw);
-  }
+  if (a.c_beg < a.c_end)
+    load_chunk<true, GF32>(buf, a.q, a.k, a.v, a.g, off, offv + kq,
+                           row < len - static_cast<int64_t>(a.c_beg) * BT, kq, vw);
 
   for (int c = a.c_beg; c < a.c_end; ++c) {
-    const int64_t t0 = a.bos + static_cast<int64_t>(c) * BT;
     const int64_t rem = len - static_cast<int64_t>(c) * BT;   // valid rows in this chunk (>0)
+    uint16_t *orow = a.o + offv;                               // o row of this lane (same layout as v)
+
+    // ---- take the current chunk out of the prefetch registers, prefetch c+1 -
+    const ChunkRegs cur = buf;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    off += strk;
+    offv += strv;
+    if (c + 1 < a.c_end) load_chunk<true, GF32>(buf, a.q, a.k, a.v, a.g, off, offv + kq, row < rem - BT, kq, vw);
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- block-local inclusive cumsum over the 16 rows (DPP row scan) ------
     f32x8 gs[2];
-    unpack_gates<DT, GF32>(buf, gs);
+    unpack_gates<DT, GF32>(cur, gs);
     row_scan16(gs);
     if (r == 15) {
       *reinterpret_cast<f32x8 *>(&sm.tot[wv][kq]) = gs[0];
@@ -340,7 +348,7 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
     for (int t = 0; t < NVT; ++t) store_state<DT>(sm.sth, 16 * t + r, krow, S[t]);
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj)
-      if (32 * jj + kq < vw) tile_store8(sm.vs, row, 32 * jj + kq, buf.v[jj]);
+      if (32 * jj + kq < vw) tile_store8(sm.vs, row, 32 * jj + kq, cur.v[jj]);
     wave_sync_lds();
 
     // ---- operands ------------------------------------------------------------
@@ -351,8 +359,8 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
     MV q0b[2];
     auto operand_half = [&](const int jj) {
       const f32x8 half = *reinterpret_cast<const f32x8 *>(&sm.fac[wv][kFacHalf][32 * jj + kq]);
-      const f32x8 qf = M::widen(from_bits<MV>(buf.q[jj]));
-      const f32x8 kf = M::widen(from_bits<MV>(buf.k[jj]));
+      const f32x8 qf = M::widen(from_bits<MV>(cur.q[jj]));
+      const f32x8 kf = M::widen(from_bits<MV>(cur.k[jj]));
       f32x8 eq, ek;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -373,13 +381,6 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
     __builtin_amdgcn_sched_barrier(0);
     operand_half(1);
     lds_barrier();  // --------------------------------------------- barrier 2
-
-    // the registers of chunk c are consumed: prefetch chunk c+1
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    if (c + 1 < a.c_end)
-      load_chunk<true, GF32>(buf, a.q, a.k, a.v, a.g, t0 + BT + row, row < rem - BT, H, V, h, kq, v0, vw);
-    __builtin_amdgcn_sched_barrier(0);
 
     // ---- A^T blocks (rows j of block J, columns i of this block) ------------
     // blocks J > wv are zero, block J == wv is causally masked.
@@ -437,8 +438,7 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
         const f32x8 o8 = {oacc[0] * a.scale, oacc[1] * a.scale, oacc[2] * a.scale, oacc[3] * a.scale,
                           0.f, 0.f, 0.f, 0.f};
         const uint4 ob = to_bits(M::cvt(o8));
-        *reinterpret_cast<uint2 *>(a.o + ((t0 + row) * H + h) * V + v0 + 16 * t + 4 * gq) =
-            make_uint2(ob.x, ob.y);
+        *reinterpret_cast<uint2 *>(orow + 16 * t + 4 * gq) = make_uint2(ob.x, ob.y);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -510,7 +510,7 @@ struct __align__(16) SmemS {
 // for segment 0 and from zero otherwise.  Writes the workspace slot and,
 // for seg >= 1, the segment's total log2 decay.
 template <int DT, bool GF32, int NVT>
-__global__ __launch_bounds__(256, 4) void gla_chunk_state_kernel(
+__global__ __launch_bounds__(256, SSLA_GC_STATE_WAVES) void gla_chunk_state_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int64_t T, int H, int V,
     const float *__restrict__ h0, int P, float *__restrict__ ws_state, float *__restrict__ ws_decay) {
@@ -548,18 +548,24 @@ __global__ __launch_bounds__(256, 4) void gla_chunk_state_kernel(
   segment_range(static_cast<int>((len + BT - 1) / BT), P, seg, c_beg, c_end);
   float dsum = 0.f;   // lane = key
 
+  const int64_t strk = static_cast<int64_t>(BT) * H * KD, strv = static_cast<int64_t>(BT) * H * V;
+  int64_t off = ((bos + static_cast<int64_t>(c_beg) * BT + row) * H + h) * KD + kq;
+  int64_t offv = ((bos + static_cast<int64_t>(c_beg) * BT + row) * H + h) * V + v0 + kq;
   ChunkRegs buf;
-  if (c_beg < c_end) {
-    const int64_t rem0 = len - static_cast<int64_t>(c_beg) * BT;
-    load_chunk<false, GF32>(buf, nullptr, k, v, g, bos + static_cast<int64_t>(c_beg) * BT + row, row < rem0, H, V,
-                            h, kq, v0, vw);
-  }
+  if (c_beg < c_end)
+    load_chunk<false, GF32>(buf, nullptr, k, v, g, off, offv, row < len - static_cast<int64_t>(c_beg) * BT, kq, vw);
   for (int c = c_beg; c < c_end; ++c) {
     const int par = (c - c_beg) & 1;
-    const int64_t t0 = bos + static_cast<int64_t>(c) * BT;
     const int64_t rem = len - static_cast<int64_t>(c) * BT;
+    const ChunkRegs cur = buf;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    off += strk;
+    offv += strv;
+    if (c + 1 < c_end) load_chunk<false, GF32>(buf, nullptr, k, v, g, off, offv, row < rem - BT, kq, vw);
+    __builtin_amdgcn_sched_barrier(0);
     f32x8 gs[2];
-    unpack_gates<DT, GF32>(buf, gs);
+    unpack_gates<DT, GF32>(cur, gs);
     row_scan16(gs);
     if (r == 15) {
       *reinterpret_cast<f32x8 *>(&sm.tot[par][wv][kq]) = gs[0];
@@ -580,7 +586,7 @@ __global__ __launch_bounds__(256, 4) void gla_chunk_state_kernel(
     }
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj)
-      if (32 * jj + kq < vw) tile_store8(sm.vs, row, 32 * jj + kq, buf.v[jj]);
+      if (32 * jj + kq < vw) tile_store8(sm.vs, row, 32 * jj + kq, cur.v[jj]);
     wave_sync_lds();
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
@@ -588,16 +594,11 @@ __global__ __launch_bounds__(256, 4) void gla_chunk_state_kernel(
       f32x8 e2;
 #pragma unroll
       for (int e = 0; e < 8; ++e) e2[e] = fast_exp2(clamp_exp(lg[e] - gs[jj][e]));
-      const f32x8 kf = M::widen(from_bits<MV>(buf.k[jj]));
+      const f32x8 kf = M::widen(from_bits<MV>(cur.k[jj]));
       tile_store8(sm.kh, row, 32 * jj + kq, to_bits(M::cvt(kf * e2)));
     }
     const f32x4 sdec = *reinterpret_cast<const f32x4 *>(&sm.fac[wv][1][krow]);
     lds_barrier();  // ------------------------------ barrier 2 (k^, V ready)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    if (c + 1 < c_end)
-      load_chunk<false, GF32>(buf, nullptr, k, v, g, t0 + BT + row, row < rem - BT, H, V, h, kq, v0, vw);
-    __builtin_amdgcn_sched_barrier(0);
     const MV ka0 = tr_operand<MV>(sm.kh, 8 * gq, 8 * gq + 4, 16 * wv, lane);
     const MV ka1 = tr_operand<MV>(sm.kh, 32 + 8 * gq, 32 + 8 * gq + 4, 16 * wv, lane);
 #pragma unroll
