@@ -173,6 +173,124 @@ int ssla_scatter_mean(const float *src, const int64_t *index, int64_t E,
  * SSLA_OK; *status_out is SSLA_ERR_ARG if any index was out of range. */
 int ssla_scatter_check(const void *workspace, int *status_out, void *stream);
 
+
+/* ------------------------------------------------------------------------
+ * G4 -- event-stream glue (grouping, receptive fields / patches, ordered
+ * index-add, truncation, temporal dropout, pooling keys, dense grids).
+ *
+ * Calls whose output size depends on the data write their counts into the
+ * first int64 words of their workspace; ssla_events_counts() copies them to
+ * the host (synchronising the stream).  Outputs are capacity-sized.  All
+ * orderings are stable (ties keep enumeration order).
+ * ------------------------------------------------------------------------ */
+
+/* Lookup table of 'same'-padded receptive fields: for every field (row-major
+ * over the output grid) the pixel index y*W + x of each kernel coordinate
+ * (row-major), -1 for padding; outcoord (may be NULL) the <x, y> output
+ * coordinate of each field.  Replaces compute_rf2pixels
+ * (utils/farsecnn_utils.py:95-128) and get_patch2pixel_lut
+ * (utils/async_utils.py:96-122).  ssla_rf_lut_shape gives the field count. */
+int ssla_rf_lut_shape(int H, int W, int kh, int kw, int sh, int sw, int64_t *n_rf);
+int ssla_rf_lut(int H, int W, int kh, int kw, int sh, int sw, int64_t *lut, int64_t *outcoord, void *stream);
+
+/* Copies counts[0..n_counts) of the last data-dependent call that used
+ * `workspace` and its input-error flag (1 if an index was out of range). */
+int ssla_events_counts(const void *workspace, int64_t *counts_out, int n_counts, int *bad_out, void *stream);
+
+/* Group padded events [B, N, C] (x, y, t, features...) with lengths[B] by
+ * pixel b*H*W + y*W + x (stable), keeping the latest max_per_px events of
+ * every pixel.  Outputs: features [cap, C-3], time [cap] (int64 of t), per
+ * group batch / h / w / length [cap] with cap = B*N.  counts: [0] groups,
+ * [1] kept events, [2] valid events.  Replaces group_events
+ * (utils/farsecnn_utils.py:130-174; utils/async_utils.py:10-84). */
+size_t ssla_group_events_workspace_size(int B, int64_t N);
+int ssla_group_events(const float *events, const int64_t *lengths, int B, int64_t N, int C, int H, int W,
+                      int max_per_px, float *out_events, int64_t *out_time, int64_t *gr_batch,
+                      int64_t *gr_h, int64_t *gr_w, int64_t *gr_len, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+/* Scatter of pixel groups into receptive fields / patches, the shared core
+ * of gather_receptive_fields (utils/farsecnn_utils.py:177-265) and
+ * scatter_group_events_to_patch (utils/async_utils.py:125-240).  Fields are
+ * (b, rf) for b < B; a field is active when one of its pixels holds a group.
+ * Its events are the runs of its active pixels in kernel-coordinate order,
+ * stably sorted by time.  plan: counts [0] active fields, [1] field events,
+ * [2] max time.  fill (with those counts): per field event its source pixel
+ * event, time (may be NULL) and kernel position; per active field its flat
+ * index b*n_rf + rf and event count.  E_cap bounds the field events. */
+size_t ssla_rf_scatter_workspace_size(int64_t G, int B, int H, int W, int64_t n_rf, int64_t E_cap);
+int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
+                         const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
+                         int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
+                         void *workspace, size_t workspace_bytes, void *stream);
+int ssla_rf_scatter_fill(const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
+                         int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
+                         int64_t n_active, int64_t E_out, int64_t t_max, int64_t *out_src,
+                         int64_t *out_time, int64_t *out_pos, int64_t *f_index, int64_t *f_len,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
+/* out[j, :] = src[idx[j], :] for rows of C floats (0 for idx out of range). */
+int ssla_gather_rows(const float *src, int64_t n_src, const int64_t *idx, int64_t m, int C, float *out,
+                     void *stream);
+
+/* out[r, :] = sum of src rows i with idx[i] == r, added in increasing i from
+ * zero in fp32: the arithmetic of index_add_ into zeros on the CPU.
+ * Replaces gather_patch_events_to_group (utils/async_utils.py:243-264). */
+size_t ssla_index_add_rows_workspace_size(int64_t n);
+int ssla_index_add_rows(const float *src, const int64_t *idx, int64_t n, int C, int64_t n_out, float *out,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+/* Stable sort of (uint64 key, int32 value) pairs on the low end_bit key
+ * bits; vals_in NULL means 0..n-1.  Used for the (batch, time) ordering of
+ * LinearAttention.forward (layers/linear_attention.py:60-65) and the
+ * position bucketing of the patch projections (layers/mos_attention.py:148-167). */
+size_t ssla_sort_pairs_workspace_size(int64_t n);
+int ssla_sort_pairs(const uint64_t *keys_in, const int32_t *vals_in, int64_t n, int end_bit,
+                    uint64_t *keys_out, int32_t *vals_out, void *workspace, size_t workspace_bytes,
+                    void *stream);
+
+/* Workspace of the segment calls below (n_seq = number of segments; for
+ * ssla_pool_segments max(n_f, E)). */
+size_t ssla_segments_workspace_size(int64_t n_seq);
+
+/* truncate_packed_sequence (utils/farsecnn_utils.py:8-33): keep the first
+ * `threshold` rows of every sequence of data [E, C] (and of others [E]).
+ * counts[0] = rows kept. */
+int ssla_truncate_packed(const float *data, const int64_t *seqlens, int64_t n_seq, int64_t E, int C,
+                         int64_t threshold, const int64_t *others, float *out_data, int64_t *out_lengths,
+                         int64_t *out_others, void *workspace, size_t workspace_bytes, void *stream);
+
+/* TemporalDropout.forward keep indices (layers/temporal_dropout.py:30-53):
+ * ceil(len / window) rows per sequence, every window-th, the last kept.
+ * counts[0] = rows kept. */
+int ssla_temporal_dropout_index(const int64_t *lengths, int64_t n_seq, int64_t window, int64_t *out_idx,
+                                int64_t *out_lengths, void *workspace, size_t workspace_bytes, void *stream);
+
+/* repeat_interleave(values, lengths) into out [n]. */
+int ssla_expand_segments(const int64_t *values, const int64_t *lengths, int64_t n_seq, int64_t n,
+                         int64_t *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* SparsePool keys (layers/sparse_pooling.py:149-171): events of a field with
+ * equal time form one pooling segment.  seg[E] (non-decreasing: the sorted
+ * index of ssla_scatter_max / _mean), seg_time / seg_field per segment,
+ * new_lengths[n_f] segments per field, field[E] scratch.  counts[0] =
+ * segments. */
+int ssla_pool_segments(const int64_t *time, const int64_t *lengths, int64_t n_f, int64_t E, int64_t *field,
+                       int64_t *seg, int64_t *seg_time, int64_t *seg_field, int64_t *new_lengths,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* Per-pixel delays in place (MosModel.preprocess_inputs, model_mos.py:
+ * 195-201): column 0 of feat [E, C] (timestamps) becomes
+ * min((t_i - t_(i-1)) / 1e5, 1) within each group, 1 at each group start. */
+int ssla_pixel_delays(float *feat, int64_t E, int C, const int64_t *lengths, int64_t G, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+/* async_event_to_grid (model_mos.py:212-228): the last event of every group
+ * at its (b, h, w) cell of grid [B, C, Hg, Wg]; other cells untouched. */
+int ssla_events_to_grid(const float *events, int64_t E, int C, const int64_t *lengths,
+                        const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w, int64_t G, int B,
+                        int Hg, int Wg, float *grid, void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

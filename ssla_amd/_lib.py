@@ -43,6 +43,30 @@ SIGNATURES = {
     "ssla_scatter_max": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
     "ssla_scatter_mean": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _sz, _vp]),
     "ssla_scatter_check": (_i32, [_vp, C.POINTER(_i32), _vp]),
+    "ssla_rf_lut_shape": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, C.POINTER(_i64)]),
+    "ssla_rf_lut": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "ssla_events_counts": (_i32, [_vp, C.POINTER(_i64), _i32, C.POINTER(_i32), _vp]),
+    "ssla_group_events_workspace_size": (_sz, [_i32, _i64]),
+    "ssla_group_events": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+                                 _vp, _sz, _vp]),
+    "ssla_rf_scatter_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i64, _i64]),
+    "ssla_rf_scatter_plan": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _i32, _i64,
+                                    _vp, _sz, _vp]),
+    "ssla_rf_scatter_fill": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _i32, _i64, _i64, _i64,
+                                    _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ssla_gather_rows": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _vp]),
+    "ssla_index_add_rows_workspace_size": (_sz, [_i64]),
+    "ssla_index_add_rows": (_i32, [_vp, _vp, _i64, _i32, _i64, _vp, _vp, _sz, _vp]),
+    "ssla_sort_pairs_workspace_size": (_sz, [_i64]),
+    "ssla_sort_pairs": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "ssla_segments_workspace_size": (_sz, [_i64]),
+    "ssla_truncate_packed": (_i32, [_vp, _vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ssla_temporal_dropout_index": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "ssla_expand_segments": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "ssla_pool_segments": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ssla_pixel_delays": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _sz, _vp]),
+    "ssla_events_to_grid": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _sz,
+                                   _vp]),
 }
 
 _lock = threading.Lock()

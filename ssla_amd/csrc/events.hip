@@ -1,0 +1,1062 @@
+// Event-stream glue on gfx950: grouping events by pixel, scattering pixel
+// groups into receptive fields / patches, ordered index-add, truncation,
+// temporal dropout, pooling keys and the sparse-to-dense grid.
+//
+// These restate the reference's torch index pipelines
+// (utils/farsecnn_utils.py, utils/async_utils.py, layers/sparse_pooling.py,
+// layers/temporal_dropout.py, layers/linear_attention.py, model_mos.py) as a
+// few fused kernels each.  Device-wide orderings use a stable LSD radix sort
+// and prefix sums from rocPRIM (AMD's header library, compiled in here);
+// every other step is a kernel of this file.  All sorts are stable: ties keep
+// the order in which items were enumerated, which is the order the
+// reference produces whenever its own sort is stable.
+//
+// Calls whose output size depends on the data write their counts into a
+// small device array `counts` (int64) of the workspace; the caller reads it
+// after the call and uses the leading part of the capacity-sized outputs.
+#include <cstring>
+#include <rocprim/rocprim.hpp>
+
+#include "common.h"
+
+namespace ssla {
+namespace {
+
+constexpr int kThreads = 256;
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+inline unsigned grid_for(int64_t n) {
+  return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((n + kThreads - 1) / kThreads, 1 << 20)));
+}
+#define GRID_STRIDE(i, n)                                                                       \
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < (n);      \
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+
+inline int bits_for(uint64_t max_value) {
+  int b = 0;
+  while (b < 64 && (max_value >> b) != 0) ++b;
+  return std::max(b, 1);
+}
+
+// Workspace carve-out helper.
+struct Carve {
+  char *base;
+  size_t off = 0;
+  template <class T>
+  T *take(size_t n) {
+    T *p = reinterpret_cast<T *>(base ? base + off : nullptr);
+    off = align256(off + sizeof(T) * std::max<size_t>(n, 1));
+    return p;
+  }
+};
+
+// rocPRIM temporary storage sizes (queried with a null buffer).
+size_t sort_temp_bytes(size_t n) {
+  size_t tb = 0;
+  rocprim::radix_sort_pairs(nullptr, tb, static_cast<uint64_t *>(nullptr), static_cast<uint64_t *>(nullptr),
+                            static_cast<int32_t *>(nullptr), static_cast<int32_t *>(nullptr), std::max<size_t>(n, 1),
+                            0, 64);
+  return tb;
+}
+size_t scan_temp_bytes(size_t n) {
+  size_t tb = 0;
+  rocprim::exclusive_scan(nullptr, tb, static_cast<int64_t *>(nullptr), static_cast<int64_t *>(nullptr),
+                          static_cast<int64_t>(0), std::max<size_t>(n, 1), rocprim::plus<int64_t>());
+  return tb;
+}
+
+int sort_pairs(void *tmp, size_t tmp_bytes, const uint64_t *kin, uint64_t *kout, const int32_t *vin, int32_t *vout,
+               int64_t n, int end_bit, hipStream_t st) {
+  if (n == 0) return SSLA_OK;
+  size_t tb = tmp_bytes;
+  const hipError_t e = rocprim::radix_sort_pairs(tmp, tb, kin, kout, vin, vout, static_cast<size_t>(n), 0,
+                                                 std::min(std::max(end_bit, 1), 64), st);
+  if (e != hipSuccess) {
+    set_error("radix sort failed: %s", hipGetErrorString(e));
+    return SSLA_ERR_LAUNCH;
+  }
+  return SSLA_OK;
+}
+
+int excl_scan(void *tmp, size_t tmp_bytes, const int64_t *in, int64_t *out, int64_t n, hipStream_t st) {
+  if (n == 0) return SSLA_OK;
+  size_t tb = tmp_bytes;
+  const hipError_t e = rocprim::exclusive_scan(tmp, tb, in, out, static_cast<int64_t>(0), static_cast<size_t>(n),
+                                               rocprim::plus<int64_t>(), st);
+  if (e != hipSuccess) {
+    set_error("prefix sum failed: %s", hipGetErrorString(e));
+    return SSLA_ERR_LAUNCH;
+  }
+  return SSLA_OK;
+}
+
+// ------------------------------------------------------------ utilities --
+__global__ void fill_i64(int64_t *p, int64_t n, int64_t v) { GRID_STRIDE(i, n) p[i] = v; }
+__global__ void fill_i32(int32_t *p, int64_t n, int32_t v) { GRID_STRIDE(i, n) p[i] = v; }
+__global__ void iota_i32(int32_t *p, int64_t n) { GRID_STRIDE(i, n) p[i] = static_cast<int32_t>(i); }
+
+// counts[k] = a[n-1] + b[n-1] (inclusive total from an exclusive scan), or 0.
+__global__ void total_from_scan(const int64_t *excl, const int64_t *val, int64_t n, int64_t *dst) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *dst = n > 0 ? excl[n - 1] + val[n - 1] : 0;
+}
+
+// out[j, :] = src[idx[j], :] (rows of C floats); idx outside [0, n_src) -> 0.
+__global__ void gather_rows_kernel(const float *__restrict__ src, const int64_t *__restrict__ idx, int64_t m,
+                                   int64_t n_src, int C, float *__restrict__ out) {
+  GRID_STRIDE(t, m * C) {
+    const int64_t j = t / C, c = t % C;
+    const int64_t r = idx[j];
+    out[t] = (r >= 0 && r < n_src) ? src[r * C + c] : 0.f;
+  }
+}
+
+// out[i] = val[segment of i] for segments given by exclusive offsets `start`
+// (n_seg segments over n elements); one thread per segment.
+__global__ void expand_segments(const int64_t *__restrict__ val, const int64_t *__restrict__ start,
+                                const int64_t *__restrict__ len, int64_t n_seg, int64_t n, int64_t *__restrict__ out) {
+  GRID_STRIDE(s, n_seg) {
+    const int64_t b = min(max(start[s], (int64_t)0), n), e = min(b + max(len[s], (int64_t)0), n);
+    for (int64_t i = b; i < e; ++i) out[i] = val[s];
+  }
+}
+
+// ------------------------------------------------------------- grouping --
+// Per padded slot (b, j < lengths[b]): the flat event index f = off[b] + j,
+// the pixel id (formed in fp32 as the reference does, exact below 2^24) and
+// the padded row of f.
+__global__ void ge_keys(const float *__restrict__ ev, const int64_t *__restrict__ lengths,
+                        const int64_t *__restrict__ off, int B, int64_t N, int C, int H, int W,
+                        uint64_t *__restrict__ key, int32_t *__restrict__ val, int64_t *__restrict__ row_of,
+                        int32_t *__restrict__ bad) {
+  GRID_STRIDE(s, static_cast<int64_t>(B) * N) {
+    const int64_t b = s / N, j = s % N;
+    if (j >= min(max(lengths[b], (int64_t)0), N)) continue;
+    const int64_t f = off[b] + j;
+    const float x = ev[s * C + 0], y = ev[s * C + 1];
+    const float pid = static_cast<float>(b * static_cast<int64_t>(H) * W) + y * static_cast<float>(W) + x;
+    if (!(x >= 0.f && x < W && y >= 0.f && y < H)) *bad = 1;
+    key[f] = pid >= 0.f ? static_cast<uint64_t>(pid) : 0;
+    val[f] = static_cast<int32_t>(f);
+    row_of[f] = s;
+  }
+}
+
+// E = off[B] (device).  Heads of the sorted events (first of its pixel);
+// entries at or beyond E are the padding slots, which sort last.
+__global__ void ge_heads(const uint64_t *__restrict__ key, int64_t cap, const int64_t *__restrict__ Ep,
+                         int64_t *__restrict__ head) {
+  const int64_t E = *Ep;
+  GRID_STRIDE(i, cap) head[i] = (i < E && (i == 0 || key[i] != key[i - 1])) ? 1 : 0;
+}
+
+// group starts and the group count (counts[0] = G); start[G] = E
+__global__ void ge_starts(const int64_t *__restrict__ head, const int64_t *__restrict__ gpos, int64_t cap,
+                          const int64_t *__restrict__ Ep, int64_t *__restrict__ start, int64_t *__restrict__ counts) {
+  const int64_t E = *Ep;
+  GRID_STRIDE(i, cap) {
+    if (i < E && head[i]) start[gpos[i]] = i;
+    if (i == 0) {
+      const int64_t G = E > 0 ? gpos[E - 1] + head[E - 1] : 0;
+      counts[0] = G;
+      start[G] = E;
+    }
+  }
+}
+
+// per group: kept length and the group's pixel attributes (kept = 0 beyond G)
+__global__ void ge_groups(const int64_t *__restrict__ counts, const int64_t *__restrict__ start, int64_t cap,
+                          const int32_t *__restrict__ order, const int64_t *__restrict__ row_of,
+                          const float *__restrict__ ev, int64_t N, int C, int cap_px, int64_t *__restrict__ kept,
+                          int64_t *__restrict__ gr_batch, int64_t *__restrict__ gr_h, int64_t *__restrict__ gr_w,
+                          int64_t *__restrict__ gr_len) {
+  const int64_t G = counts[0];
+  GRID_STRIDE(g, cap) {
+    if (g >= G) {
+      kept[g] = 0;
+      continue;
+    }
+    const int64_t s = start[g], e = start[g + 1];
+    const int64_t k = min(e - s, static_cast<int64_t>(cap_px));
+    kept[g] = k;
+    gr_len[g] = k;
+    const int64_t r = row_of[order[s]];
+    gr_batch[g] = r / N;
+    gr_w[g] = static_cast<int64_t>(ev[r * C + 0]);
+    gr_h[g] = static_cast<int64_t>(ev[r * C + 1]);
+  }
+}
+
+// emit the kept (latest cap_px) events of every group
+__global__ void ge_emit(const int64_t *__restrict__ head, const int64_t *__restrict__ gpos,
+                        const int64_t *__restrict__ start, const int64_t *__restrict__ kept,
+                        const int64_t *__restrict__ kpre, const int32_t *__restrict__ order,
+                        const int64_t *__restrict__ row_of, const float *__restrict__ ev, int64_t cap,
+                        const int64_t *__restrict__ Ep, int C, float *__restrict__ out_ev,
+                        int64_t *__restrict__ out_t) {
+  const int64_t E = *Ep;
+  GRID_STRIDE(i, cap) {
+    if (i >= E) continue;
+    const int64_t g = gpos[i] + head[i] - 1;
+    const int64_t s = start[g], e = start[g + 1];
+    const int64_t drop = (e - s) - kept[g];
+    const int64_t rank = i - s;
+    if (rank < drop) continue;
+    const int64_t o = kpre[g] + rank - drop;
+    const int64_t r = row_of[order[i]];
+    const float *src = ev + r * C;
+    for (int c = 3; c < C; ++c) out_ev[o * (C - 3) + (c - 3)] = src[c];
+    out_t[o] = static_cast<int64_t>(src[2]);
+  }
+}
+
+__global__ void ge_finish(const int64_t *__restrict__ kpre, const int64_t *__restrict__ kept, int64_t *counts,
+                          const int64_t *__restrict__ Ep) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const int64_t G = counts[0];
+    counts[1] = G > 0 ? kpre[G - 1] + kept[G - 1] : 0;
+    counts[2] = *Ep;
+  }
+}
+
+// ----------------------------------------------------------------- LUTs --
+__global__ void lut_kernel(int H, int W, int kh, int kw, int sh, int sw, int top, int left, int Ho, int Wo,
+                           int64_t *__restrict__ lut, int64_t *__restrict__ outc) {
+  const int64_t n = static_cast<int64_t>(Ho) * Wo * kh * kw;
+  GRID_STRIDE(t, n) {
+    const int64_t rf = t / (kh * kw), a = t % (kh * kw);
+    const int oy = static_cast<int>(rf / Wo), ox = static_cast<int>(rf % Wo);
+    const int y = oy * sh - top + static_cast<int>(a / kw), x = ox * sw - left + static_cast<int>(a % kw);
+    lut[t] = (y >= 0 && y < H && x >= 0 && x < W) ? static_cast<int64_t>(y) * W + x : -1;
+    if (outc && a == 0) {
+      outc[2 * rf] = ox;
+      outc[2 * rf + 1] = oy;
+    }
+  }
+}
+
+// ---------------------------------------------------- field / patch scatter --
+// pixel map: pixmap[b*H*W + h*W + w] = group index
+__global__ void rf_pixmap(const int64_t *__restrict__ gb, const int64_t *__restrict__ gh,
+                          const int64_t *__restrict__ gw, int64_t G, int H, int W, int64_t n_pix,
+                          int32_t *__restrict__ pixmap, int32_t *__restrict__ bad) {
+  GRID_STRIDE(g, G) {
+    const int64_t p = gb[g] * H * W + gh[g] * W + gw[g];
+    if (gh[g] < 0 || gh[g] >= H || gw[g] < 0 || gw[g] >= W || p < 0 || p >= n_pix) {
+      *bad = 1;
+      continue;
+    }
+    pixmap[p] = static_cast<int32_t>(g);
+  }
+}
+
+// per field (b, rf): number of events, active flag
+__global__ void rf_count(const int64_t *__restrict__ lut, int64_t n_rf, int A, int B, int H, int W,
+                         const int32_t *__restrict__ pixmap, const int64_t *__restrict__ glen,
+                         int64_t *__restrict__ nev, int64_t *__restrict__ act) {
+  GRID_STRIDE(f, static_cast<int64_t>(B) * n_rf) {
+    const int64_t b = f / n_rf, r = f % n_rf;
+    int64_t n = 0, a_ = 0;
+    for (int a = 0; a < A; ++a) {
+      const int64_t p = lut[r * A + a];
+      if (p < 0) continue;
+      const int32_t g = pixmap[b * H * W + p];
+      if (g < 0) continue;
+      a_ = 1;
+      n += glen[g];
+    }
+    nev[f] = n;
+    act[f] = a_;
+  }
+}
+
+// enumerate the events of every active field (pixels in kernel-coordinate
+// order, each pixel's run in group order): sort key, source event, position
+__global__ void rf_enumerate(const int64_t *__restrict__ lut, int64_t n_rf, int A, int B, int H, int W,
+                             const int32_t *__restrict__ pixmap, const int64_t *__restrict__ glen,
+                             const int64_t *__restrict__ gstart, const int64_t *__restrict__ act,
+                             const int64_t *__restrict__ act_pre, const int64_t *__restrict__ ev_pre,
+                             const int64_t *__restrict__ time, int64_t E_in, uint64_t t_stride,
+                             uint64_t *__restrict__ key, int32_t *__restrict__ val, int64_t *__restrict__ pre_src,
+                             int64_t *__restrict__ pre_pos) {
+  GRID_STRIDE(t, static_cast<int64_t>(B) * n_rf * A) {
+    const int64_t f = t / A;
+    const int a = static_cast<int>(t % A);
+    if (!act[f]) continue;
+    const int64_t b = f / n_rf, r = f % n_rf;
+    const int64_t p = lut[r * A + a];
+    if (p < 0) continue;
+    const int32_t g = pixmap[b * H * W + p];
+    if (g < 0) continue;
+    int64_t o = ev_pre[f];
+    for (int a2 = 0; a2 < a; ++a2) {
+      const int64_t p2 = lut[r * A + a2];
+      if (p2 < 0) continue;
+      const int32_t g2 = pixmap[b * H * W + p2];
+      if (g2 >= 0) o += glen[g2];
+    }
+    const uint64_t fk = static_cast<uint64_t>(act_pre[f]) * t_stride;
+    const int64_t s = gstart[g];
+    for (int64_t e = 0; e < glen[g]; ++e) {
+      const int64_t src = min(max(s + e, (int64_t)0), E_in - 1);
+      key[o + e] = fk + static_cast<uint64_t>(max(time[src], (int64_t)0));
+      val[o + e] = static_cast<int32_t>(o + e);
+      pre_src[o + e] = src;
+      pre_pos[o + e] = a;
+    }
+  }
+}
+
+// per active field: flat (b, rf) index, event count
+__global__ void rf_fields(const int64_t *__restrict__ act, const int64_t *__restrict__ act_pre,
+                          const int64_t *__restrict__ nev, int64_t n_f, int64_t *__restrict__ f_index,
+                          int64_t *__restrict__ f_len) {
+  GRID_STRIDE(f, n_f) {
+    if (!act[f]) continue;
+    f_index[act_pre[f]] = f;
+    f_len[act_pre[f]] = nev[f];
+  }
+}
+
+__global__ void rf_emit(const int32_t *__restrict__ perm, int64_t E_out, const int64_t *__restrict__ pre_src,
+                        const int64_t *__restrict__ pre_pos, const int64_t *__restrict__ time,
+                        int64_t *__restrict__ o_src, int64_t *__restrict__ o_time, int64_t *__restrict__ o_pos) {
+  GRID_STRIDE(i, E_out) {
+    const int32_t k = perm[i];
+    const int64_t s = pre_src[k];
+    o_src[i] = s;
+    if (o_time) o_time[i] = time[s];
+    o_pos[i] = pre_pos[k];
+  }
+}
+
+__global__ void max_i64(const int64_t *__restrict__ x, int64_t n, unsigned long long *__restrict__ dst) {
+  __shared__ long long s[kThreads];
+  long long m = 0;
+  GRID_STRIDE(i, n) m = max(m, static_cast<long long>(x[i]));
+  s[threadIdx.x] = m;
+  __syncthreads();
+  for (int d = kThreads / 2; d > 0; d >>= 1) {
+    if (threadIdx.x < d) s[threadIdx.x] = max(s[threadIdx.x], s[threadIdx.x + d]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0 && s[0] > 0) atomicMax(dst, static_cast<unsigned long long>(s[0]));
+}
+
+// ------------------------------------------------------- ordered index add --
+// out[r, :] = sum over sorted copies of src rows, in copy order (fp32,
+// starting from zero) -- the arithmetic of a sequential index_add_ into zeros.
+__global__ void index_add_rows(const float *__restrict__ src, const uint64_t *__restrict__ skey,
+                               const int32_t *__restrict__ perm, int64_t n, int64_t n_out, int C,
+                               float *__restrict__ out) {
+  // one wavefront per output row; binary search of its run in the sorted keys
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (r >= n_out) return;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (skey[mid] < static_cast<uint64_t>(r)) lo = mid + 1; else hi = mid;
+  }
+  int64_t e = lo;
+  {
+    int64_t l2 = lo, h2 = n;
+    while (l2 < h2) {
+      const int64_t mid = (l2 + h2) >> 1;
+      if (skey[mid] <= static_cast<uint64_t>(r)) l2 = mid + 1; else h2 = mid;
+    }
+    e = l2;
+  }
+  for (int c0 = 0; c0 < C; c0 += 64) {
+    const int c = c0 + lane;
+    if (c >= C) continue;
+    float acc = 0.f;
+    for (int64_t j = lo; j < e; ++j) acc += src[static_cast<int64_t>(perm[j]) * C + c];
+    out[r * C + c] = acc;
+  }
+}
+
+__global__ void idx_keys(const int64_t *__restrict__ idx, int64_t n, int64_t n_out, uint64_t *__restrict__ key,
+                         int32_t *__restrict__ val, int32_t *__restrict__ bad) {
+  GRID_STRIDE(i, n) {
+    const int64_t r = idx[i];
+    if (r < 0 || r >= n_out) *bad = 1;
+    key[i] = (r >= 0 && r < n_out) ? static_cast<uint64_t>(r) : static_cast<uint64_t>(n_out);
+    val[i] = static_cast<int32_t>(i);
+  }
+}
+
+// ---------------------------------------------------------- truncation --
+// keep the first `thr` elements of every sequence
+__global__ void trunc_len(const int64_t *__restrict__ len, int64_t n, int64_t thr, int64_t *__restrict__ kl) {
+  GRID_STRIDE(s, n) kl[s] = min(max(len[s], (int64_t)0), thr);
+}
+__global__ void trunc_copy(const float *__restrict__ data, const int64_t *__restrict__ others,
+                           const int64_t *__restrict__ start, const int64_t *__restrict__ kl,
+                           const int64_t *__restrict__ kpre, int64_t n_seq, int64_t E, int C,
+                           float *__restrict__ out, int64_t *__restrict__ out_o) {
+  GRID_STRIDE(s, n_seq) {
+    for (int64_t j = 0; j < kl[s]; ++j) {
+      const int64_t src = min(start[s] + j, E - 1), dst = kpre[s] + j;
+      for (int c = 0; c < C; ++c) out[dst * C + c] = data[src * C + c];
+      if (others) out_o[dst] = others[src];
+    }
+  }
+}
+
+// ------------------------------------------------------ temporal dropout --
+__global__ void td_len(const int64_t *__restrict__ len, int64_t n, int64_t w, int64_t *__restrict__ kl) {
+  GRID_STRIDE(s, n) kl[s] = (max(len[s], (int64_t)0) + w - 1) / w;
+}
+__global__ void td_index(const int64_t *__restrict__ len, const int64_t *__restrict__ start,
+                         const int64_t *__restrict__ kl, const int64_t *__restrict__ kpre, int64_t n, int64_t w,
+                         int64_t *__restrict__ idx) {
+  GRID_STRIDE(s, n) {
+    const int64_t L = max(len[s], (int64_t)0);
+    const int64_t off = ((L % w - 1) % w + w) % w;
+    for (int64_t j = 0; j < kl[s]; ++j) idx[kpre[s] + j] = start[s] + off + j * w;
+  }
+}
+
+// --------------------------------------------------------------- pooling --
+// key = time + field * (max_t + 1) over fields in order; segment heads
+__global__ void pool_heads(const int64_t *__restrict__ time, const int64_t *__restrict__ field, int64_t E,
+                           int64_t *__restrict__ head) {
+  GRID_STRIDE(i, E) head[i] = (i == 0 || field[i] != field[i - 1] || time[i] != time[i - 1]) ? 1 : 0;
+}
+__global__ void pool_emit(const int64_t *__restrict__ head, const int64_t *__restrict__ spre,
+                          const int64_t *__restrict__ time, const int64_t *__restrict__ field, int64_t E,
+                          int64_t *__restrict__ seg, int64_t *__restrict__ seg_time, int64_t *__restrict__ seg_field) {
+  GRID_STRIDE(i, E) {
+    const int64_t s = spre[i] + head[i] - 1;
+    seg[i] = s;
+    if (head[i]) {
+      seg_time[s] = time[i];
+      seg_field[s] = field[i];
+    }
+  }
+}
+__global__ void count_by(const int64_t *__restrict__ lab, const int64_t *__restrict__ counts, int which,
+                         int64_t n_lab, int64_t *__restrict__ out) {
+  const int64_t n = counts[which];
+  GRID_STRIDE(i, n) {
+    const int64_t l = lab[i];
+    if (l >= 0 && l < n_lab) atomicAdd(reinterpret_cast<unsigned long long *>(&out[l]), 1ull);
+  }
+}
+
+// field[i] = f for the events of field f (fields laid out in order)
+__global__ void pool_field_of(const int64_t *__restrict__ start, const int64_t *__restrict__ len, int64_t n_f,
+                              int64_t E, int64_t *__restrict__ field) {
+  GRID_STRIDE(f, n_f) {
+    const int64_t b = min(max(start[f], (int64_t)0), E), e = min(b + max(len[f], (int64_t)0), E);
+    for (int64_t i = b; i < e; ++i) field[i] = f;
+  }
+}
+
+__global__ void seg_ends(const int64_t *__restrict__ start, const int64_t *__restrict__ len, int64_t n,
+                         int64_t *__restrict__ end) {
+  GRID_STRIDE(i, n) end[i] = start[i] + len[i];
+}
+
+__global__ void store_u64_as_i64(const unsigned long long *__restrict__ src, int64_t *__restrict__ dst) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *dst = static_cast<int64_t>(*src);
+}
+
+// ---------------------------------------------------------------- delays --
+// column 0 of feat [E, C] holds timestamps; replace them by the per-pixel
+// delay (t_i - t_{i-1}) / 1e5 clamped at 1, with 1 for the first event of
+// every group (model_mos.py:195-201, fp32 arithmetic as there)
+__global__ void pixel_delays(float *__restrict__ feat, const int64_t *__restrict__ start,
+                             const int64_t *__restrict__ len, int64_t G, int64_t E, int C) {
+  GRID_STRIDE(g, G) {
+    const int64_t b = min(max(start[g], (int64_t)0), E), e = min(b + max(len[g], (int64_t)0), E);
+    float prev = b > 0 ? feat[(b - 1) * C] : 0.f;
+    for (int64_t i = b; i < e; ++i) {
+      const float t = feat[i * C];
+      feat[i * C] = (i == b) ? 1.f : fminf((t - prev) / 1e5f, 1.f);
+      prev = t;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- grids --
+// last event of every group at its (b, h, w) cell of a [B, C, Hg, Wg] grid
+__global__ void grid_place(const float *__restrict__ ev, const int64_t *__restrict__ gend, const int64_t *__restrict__ gb,
+                           const int64_t *__restrict__ gh, const int64_t *__restrict__ gw, int64_t G, int64_t E, int C,
+                           int B, int Hg, int Wg, float *__restrict__ grid, int32_t *__restrict__ bad) {
+  GRID_STRIDE(t, G * C) {
+    const int64_t g = t / C;
+    const int c = static_cast<int>(t % C);
+    const int64_t b = gb[g], h = gh[g], w = gw[g];
+    const int64_t last = gend[g] - 1;
+    if (b < 0 || b >= B || h < 0 || h >= Hg || w < 0 || w >= Wg || last < 0 || last >= E) {
+      *bad = 1;
+      continue;
+    }
+    // one group per cell, so the reference's index_add_ into zeros is a store
+    grid[((b * C + c) * Hg + h) * Wg + w] = ev[last * C + c];
+  }
+}
+
+}  // namespace
+}  // namespace ssla
+
+using namespace ssla;
+
+// ======================================================================== C-ABI
+extern "C" int ssla_rf_lut_shape(int H, int W, int kh, int kw, int sh, int sw, int64_t *n_rf) {
+  clear_error();
+  SSLA_CHECK_ARG(H > 0 && W > 0 && kh > 0 && kw > 0 && sh > 0 && sw > 0 && n_rf, "rf_lut_shape: bad sizes");
+  const int ph = ((H + sh - 1) / sh - 1) * sh + kh - H, pw = ((W + sw - 1) / sw - 1) * sw + kw - W;
+  const int Ho = (H + ph - kh) / sh + 1, Wo = (W + pw - kw) / sw + 1;
+  SSLA_CHECK_ARG(Ho > 0 && Wo > 0, "rf_lut_shape: empty output grid");
+  *n_rf = static_cast<int64_t>(Ho) * Wo;
+  return SSLA_OK;
+}
+
+extern "C" int ssla_rf_lut(int H, int W, int kh, int kw, int sh, int sw, int64_t *lut, int64_t *outcoord,
+                           void *stream) {
+  clear_error();
+  int64_t n_rf = 0;
+  const int st0 = ssla_rf_lut_shape(H, W, kh, kw, sh, sw, &n_rf);
+  if (st0 != SSLA_OK) return st0;
+  SSLA_CHECK_ARG(lut != nullptr, "rf_lut: lut is NULL");
+  const int ph = ((H + sh - 1) / sh - 1) * sh + kh - H, pw = ((W + sw - 1) / sw - 1) * sw + kw - W;
+  // floor(p / 2) for the top/left padding (p may be negative: a crop)
+  const int top = ph >= 0 ? ph / 2 : -((-ph + 1) / 2), left = pw >= 0 ? pw / 2 : -((-pw + 1) / 2);
+  const int Ho = (H + ph - kh) / sh + 1, Wo = (W + pw - kw) / sw + 1;
+  hipLaunchKernelGGL(lut_kernel, dim3(grid_for(n_rf * kh * kw)), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     H, W, kh, kw, sh, sw, top, left, Ho, Wo, lut, outcoord);
+  return launch_status("rf_lut");
+}
+
+// ---- group_events ------------------------------------------------------------
+namespace {
+struct GeWs {
+  int64_t *counts, *off, *head, *gpos, *start, *kept, *kpre, *row_of;
+  uint64_t *key, *skey;
+  int32_t *val, *order, *bad;
+  void *tmp;
+  size_t tmp_bytes, total;
+};
+GeWs ge_layout(void *ws, int B, int64_t cap) {
+  Carve c{static_cast<char *>(ws)};
+  GeWs L;
+  L.counts = c.take<int64_t>(8);
+  L.bad = c.take<int32_t>(8);
+  L.off = c.take<int64_t>(B + 1);
+  L.head = c.take<int64_t>(cap);
+  L.gpos = c.take<int64_t>(cap);
+  L.start = c.take<int64_t>(cap + 1);
+  L.kept = c.take<int64_t>(cap);
+  L.kpre = c.take<int64_t>(cap);
+  L.row_of = c.take<int64_t>(cap);
+  L.key = c.take<uint64_t>(cap);
+  L.skey = c.take<uint64_t>(cap);
+  L.val = c.take<int32_t>(cap);
+  L.order = c.take<int32_t>(cap);
+  L.tmp_bytes = std::max(sort_temp_bytes(cap), scan_temp_bytes(std::max<int64_t>(cap, B + 1)));
+  L.tmp = c.take<char>(L.tmp_bytes);
+  L.total = c.off;
+  return L;
+}
+}  // namespace
+
+extern "C" size_t ssla_group_events_workspace_size(int B, int64_t N) {
+  if (B <= 0 || N < 0) return 0;
+  return ge_layout(nullptr, B, static_cast<int64_t>(B) * N).total;
+}
+
+extern "C" int ssla_group_events(const float *events, const int64_t *lengths, int B, int64_t N, int C, int H, int W,
+                                 int max_per_px, float *out_events, int64_t *out_time, int64_t *gr_batch,
+                                 int64_t *gr_h, int64_t *gr_w, int64_t *gr_len, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(B > 0 && N >= 0 && C >= 4 && H > 0 && W > 0 && max_per_px > 0, "group_events: bad sizes");
+  SSLA_CHECK_ARG(static_cast<int64_t>(B) * H * W < (1LL << 24),
+                 "group_events: B*H*W must stay below 2^24 (pixel ids are formed in fp32)");
+  const int64_t cap = static_cast<int64_t>(B) * N;
+  SSLA_CHECK_ARG(cap < 0x7fffffff, "group_events: B*N must stay below 2^31");
+  const GeWs L = ge_layout(workspace, B, cap);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("group_events: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  SSLA_CHECK_ARG(events && lengths && out_events && out_time && gr_batch && gr_h && gr_w && gr_len,
+                 "group_events: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t *Ep = L.off + B;
+  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, L.counts, (int64_t)8, (int64_t)0);
+  hipLaunchKernelGGL(fill_i32, dim3(1), dim3(kThreads), 0, st, L.bad, (int64_t)8, 0);
+  if (cap == 0) return launch_status("group_events");
+  // sample offsets: exclusive scan of the lengths clamped to [0, N]
+  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, L.kept, (int64_t)(B + 1), (int64_t)0);
+  hipLaunchKernelGGL(trunc_len, dim3(grid_for(B)), dim3(kThreads), 0, st, lengths, (int64_t)B, N, L.kept);
+  int s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.off, B + 1, st);
+  if (s) return s;
+  // keys of the valid events; padding slots keep the all-ones key and sort last
+  hipLaunchKernelGGL(fill_i64, dim3(grid_for(cap)), dim3(kThreads), 0, st, reinterpret_cast<int64_t *>(L.key), cap,
+                     (int64_t)-1);
+  hipLaunchKernelGGL(iota_i32, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.val, cap);
+  hipLaunchKernelGGL(fill_i64, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.row_of, cap, (int64_t)0);
+  hipLaunchKernelGGL(ge_keys, dim3(grid_for(cap)), dim3(kThreads), 0, st, events, lengths, L.off, B, N, C, H, W,
+                     L.key, L.val, L.row_of, L.bad);
+  s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.order, cap, 64, st);
+  if (s) return s;
+  hipLaunchKernelGGL(ge_heads, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.skey, cap, Ep, L.head);
+  s = excl_scan(L.tmp, L.tmp_bytes, L.head, L.gpos, cap, st);
+  if (s) return s;
+  hipLaunchKernelGGL(ge_starts, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, cap, Ep, L.start,
+                     L.counts);
+  hipLaunchKernelGGL(ge_groups, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.counts, L.start, cap, L.order,
+                     L.row_of, events, N, C, max_per_px, L.kept, gr_batch, gr_h, gr_w, gr_len);
+  s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.kpre, cap, st);
+  if (s) return s;
+  hipLaunchKernelGGL(ge_emit, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, L.start, L.kept, L.kpre,
+                     L.order, L.row_of, events, cap, Ep, C, out_events, out_time);
+  hipLaunchKernelGGL(ge_finish, dim3(1), dim3(64), 0, st, L.kpre, L.kept, L.counts, Ep);
+  return launch_status("group_events");
+}
+
+// counts of the last data-dependent call that used `workspace` (the first
+// n_counts int64 of the workspace) and its status flag; synchronises stream.
+extern "C" int ssla_events_counts(const void *workspace, int64_t *counts_out, int n_counts, int *bad_out,
+                                  void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(workspace && counts_out && n_counts > 0 && n_counts <= 8, "events_counts: bad arguments");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int64_t buf[8] = {0};
+  int32_t badv[8] = {0};
+  hipError_t e = hipMemcpyAsync(buf, workspace, sizeof(buf), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(badv, static_cast<const char *>(workspace) + 256, sizeof(badv), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) {
+    set_error("events_counts: %s", hipGetErrorString(e));
+    return SSLA_ERR_LAUNCH;
+  }
+  for (int i = 0; i < n_counts; ++i) counts_out[i] = buf[i];
+  if (bad_out) *bad_out = badv[0];
+  return SSLA_OK;
+}
+
+// ---- receptive-field / patch scatter ---------------------------------------------
+namespace {
+struct RfWs {
+  int64_t *counts, *gstart, *nev, *act, *act_pre, *ev_pre, *f_index, *f_len, *pre_src, *pre_pos;
+  int32_t *bad, *pixmap, *val, *perm;
+  uint64_t *key, *skey;
+  unsigned long long *tmax;
+  void *tmp;
+  size_t tmp_bytes, total;
+};
+RfWs rf_layout(void *ws, int64_t G, int64_t n_pix, int64_t n_f, int64_t E_cap) {
+  Carve c{static_cast<char *>(ws)};
+  RfWs L;
+  L.counts = c.take<int64_t>(8);
+  L.bad = c.take<int32_t>(8);
+  L.tmax = c.take<unsigned long long>(1);
+  L.gstart = c.take<int64_t>(G + 1);
+  L.pixmap = c.take<int32_t>(n_pix);
+  L.nev = c.take<int64_t>(n_f);
+  L.act = c.take<int64_t>(n_f);
+  L.act_pre = c.take<int64_t>(n_f);
+  L.ev_pre = c.take<int64_t>(n_f);
+  L.f_index = c.take<int64_t>(n_f);
+  L.f_len = c.take<int64_t>(n_f);
+  L.pre_src = c.take<int64_t>(E_cap);
+  L.pre_pos = c.take<int64_t>(E_cap);
+  L.key = c.take<uint64_t>(E_cap);
+  L.skey = c.take<uint64_t>(E_cap);
+  L.val = c.take<int32_t>(E_cap);
+  L.perm = c.take<int32_t>(E_cap);
+  L.tmp_bytes = std::max(sort_temp_bytes(E_cap), scan_temp_bytes(std::max(n_f, G + 1)));
+  L.tmp = c.take<char>(L.tmp_bytes);
+  L.total = c.off;
+  return L;
+}
+}  // namespace
+
+// E_cap bounds the number of field events (sum over active fields of their
+// pixels' runs; at most A * E_in).
+extern "C" size_t ssla_rf_scatter_workspace_size(int64_t G, int B, int H, int W, int64_t n_rf, int64_t E_cap) {
+  if (G < 0 || B <= 0 || H <= 0 || W <= 0 || n_rf <= 0 || E_cap < 0) return 0;
+  return rf_layout(nullptr, G, static_cast<int64_t>(B) * H * W, static_cast<int64_t>(B) * n_rf, E_cap).total;
+}
+
+// Plan: which (b, rf) fields are active and how many events each holds.
+// counts[0] = active fields, counts[1] = field events, counts[2] = max time.
+extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
+                                    const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
+                                    int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
+                                    void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 && E_cap >= 0,
+                 "rf_scatter_plan: bad sizes");
+  SSLA_CHECK_ARG(E_cap < 0x7fffffff, "rf_scatter_plan: E_cap must stay below 2^31");
+  const int64_t n_pix = static_cast<int64_t>(B) * H * W, n_f = static_cast<int64_t>(B) * n_rf;
+  const RfWs L = rf_layout(workspace, G, n_pix, n_f, E_cap);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("rf_scatter_plan: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  SSLA_CHECK_ARG(lut && (G == 0 || (gr_batch && gr_h && gr_w && gr_len)) && (E_in == 0 || time),
+                 "rf_scatter_plan: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, L.counts, (int64_t)8, (int64_t)0);
+  hipLaunchKernelGGL(fill_i32, dim3(1), dim3(kThreads), 0, st, L.bad, (int64_t)8, 0);
+  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, reinterpret_cast<int64_t *>(L.tmax), (int64_t)1,
+                     (int64_t)0);
+  hipLaunchKernelGGL(fill_i32, dim3(grid_for(n_pix)), dim3(kThreads), 0, st, L.pixmap, n_pix, -1);
+  if (G > 0)
+    hipLaunchKernelGGL(rf_pixmap, dim3(grid_for(G)), dim3(kThreads), 0, st, gr_batch, gr_h, gr_w, G, H, W, n_pix,
+                       L.pixmap, L.bad);
+  int s = excl_scan(L.tmp, L.tmp_bytes, gr_len, L.gstart, G, st);
+  if (s) return s;
+  hipLaunchKernelGGL(rf_count, dim3(grid_for(n_f)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap, gr_len,
+                     L.nev, L.act);
+  s = excl_scan(L.tmp, L.tmp_bytes, L.act, L.act_pre, n_f, st);
+  if (s) return s;
+  s = excl_scan(L.tmp, L.tmp_bytes, L.nev, L.ev_pre, n_f, st);
+  if (s) return s;
+  hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.act_pre, L.act, n_f, L.counts + 0);
+  hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.ev_pre, L.nev, n_f, L.counts + 1);
+  if (E_in > 0)
+    hipLaunchKernelGGL(max_i64, dim3(grid_for(std::min<int64_t>(E_in, 1 << 16))), dim3(kThreads), 0, st, time, E_in,
+                       L.tmax);
+  hipLaunchKernelGGL(rf_fields, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.act, L.act_pre, L.nev, n_f, L.f_index,
+                     L.f_len);
+  hipLaunchKernelGGL(store_u64_as_i64, dim3(1), dim3(64), 0, st, L.tmax, L.counts + 2);
+  return launch_status("rf_scatter_plan");
+}
+
+// Fill (after the plan; n_active / E_out / t_max are the plan's counts):
+// field events in (field, time) order with their source pixel event, time
+// and kernel position; per active field its flat (b, rf) index and length.
+extern "C" int ssla_rf_scatter_fill(const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
+                                    int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
+                                    int64_t n_active, int64_t E_out, int64_t t_max, int64_t *out_src,
+                                    int64_t *out_time, int64_t *out_pos, int64_t *f_index, int64_t *f_len,
+                                    void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  const int64_t n_pix = static_cast<int64_t>(B) * H * W, n_f = static_cast<int64_t>(B) * n_rf;
+  const RfWs L = rf_layout(workspace, G, n_pix, n_f, E_cap);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("rf_scatter_fill: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  SSLA_CHECK_ARG(E_out >= 0 && E_out <= E_cap && n_active >= 0 && n_active <= n_f && t_max >= 0,
+                 "rf_scatter_fill: counts outside the plan's capacity");
+  SSLA_CHECK_ARG(out_src && out_pos && f_index && f_len, "rf_scatter_fill: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint64_t t_stride = static_cast<uint64_t>(t_max) + 1;
+  hipLaunchKernelGGL(rf_enumerate, dim3(grid_for(n_f * A)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap,
+                     gr_len, L.gstart, L.act, L.act_pre, L.ev_pre, time, E_in, t_stride, L.key, L.val, L.pre_src,
+                     L.pre_pos);
+  const int end_bit = bits_for(static_cast<uint64_t>(std::max<int64_t>(n_active, 1)) * t_stride);
+  int s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.perm, E_out, end_bit, st);
+  if (s) return s;
+  if (E_out > 0)
+    hipLaunchKernelGGL(rf_emit, dim3(grid_for(E_out)), dim3(kThreads), 0, st, L.perm, E_out, L.pre_src, L.pre_pos,
+                       time, out_src, out_time, out_pos);
+  if (n_active > 0) {
+    hipError_t e = hipMemcpyAsync(f_index, L.f_index, sizeof(int64_t) * n_active, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(f_len, L.f_len, sizeof(int64_t) * n_active, hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) {
+      set_error("rf_scatter_fill: %s", hipGetErrorString(e));
+      return SSLA_ERR_LAUNCH;
+    }
+  }
+  return launch_status("rf_scatter_fill");
+}
+
+// ---- rows ------------------------------------------------------------------------
+extern "C" int ssla_gather_rows(const float *src, int64_t n_src, const int64_t *idx, int64_t m, int C, float *out,
+                                void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(n_src >= 0 && m >= 0 && C > 0, "gather_rows: bad sizes");
+  if (m == 0) return SSLA_OK;
+  SSLA_CHECK_ARG(src && idx && out, "gather_rows: null pointer");
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(grid_for(m * C)), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     src, idx, m, n_src, C, out);
+  return launch_status("gather_rows");
+}
+
+namespace {
+struct IaWs {
+  uint64_t *key, *skey;
+  int32_t *val, *perm, *bad;
+  void *tmp;
+  size_t tmp_bytes, total;
+};
+IaWs ia_layout(void *ws, int64_t n) {
+  Carve c{static_cast<char *>(ws)};
+  IaWs L;
+  c.take<int64_t>(8);   // counts slot (unused here)
+  L.bad = c.take<int32_t>(8);
+  L.key = c.take<uint64_t>(n);
+  L.skey = c.take<uint64_t>(n);
+  L.val = c.take<int32_t>(n);
+  L.perm = c.take<int32_t>(n);
+  L.tmp_bytes = sort_temp_bytes(n);
+  L.tmp = c.take<char>(L.tmp_bytes);
+  L.total = c.off;
+  return L;
+}
+}  // namespace
+
+extern "C" size_t ssla_index_add_rows_workspace_size(int64_t n) {
+  return n < 0 ? 0 : ia_layout(nullptr, n).total;
+}
+
+extern "C" int ssla_index_add_rows(const float *src, const int64_t *idx, int64_t n, int C, int64_t n_out, float *out,
+                                   void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(n >= 0 && C > 0 && n_out >= 0 && n < 0x7fffffff, "index_add_rows: bad sizes");
+  const IaWs L = ia_layout(workspace, n);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("index_add_rows: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(fill_i32, dim3(1), dim3(kThreads), 0, st, L.bad, (int64_t)8, 0);
+  if (n_out == 0) return launch_status("index_add_rows");
+  SSLA_CHECK_ARG(out && (n == 0 || (src && idx)), "index_add_rows: null pointer");
+  if (n > 0) {
+    hipLaunchKernelGGL(idx_keys, dim3(grid_for(n)), dim3(kThreads), 0, st, idx, n, n_out, L.key, L.val, L.bad);
+    const int s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.perm, n, bits_for(n_out), st);
+    if (s) return s;
+  }
+  hipLaunchKernelGGL(index_add_rows, dim3(static_cast<unsigned>((n_out + 3) / 4)), dim3(256), 0, st, src, L.skey,
+                     L.perm, n, n_out, C, out);
+  return launch_status("index_add_rows");
+}
+
+// ---- stable sort of (uint64 key, int32 value) pairs --------------------------------
+extern "C" size_t ssla_sort_pairs_workspace_size(int64_t n) {
+  return n < 0 ? 0 : align256(sort_temp_bytes(n)) + align256(sizeof(int32_t) * std::max<int64_t>(n, 1));
+}
+
+// vals_in may be NULL (then the values are 0..n-1).  end_bit: number of
+// low key bits that take part (1..64).
+extern "C" int ssla_sort_pairs(const uint64_t *keys_in, const int32_t *vals_in, int64_t n, int end_bit,
+                               uint64_t *keys_out, int32_t *vals_out, void *workspace, size_t workspace_bytes,
+                               void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(n >= 0 && n < 0x7fffffff && end_bit >= 1 && end_bit <= 64, "sort_pairs: bad arguments");
+  const size_t need = ssla_sort_pairs_workspace_size(n);
+  if (!workspace || workspace_bytes < need) {
+    set_error("sort_pairs: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  if (n == 0) return SSLA_OK;
+  SSLA_CHECK_ARG(keys_in && keys_out && vals_out, "sort_pairs: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t tb = sort_temp_bytes(n);
+  const int32_t *vin = vals_in;
+  if (!vin) {
+    int32_t *iota = reinterpret_cast<int32_t *>(static_cast<char *>(workspace) + align256(tb));
+    hipLaunchKernelGGL(iota_i32, dim3(grid_for(n)), dim3(kThreads), 0, st, iota, n);
+    vin = iota;
+  }
+  const int s = sort_pairs(workspace, tb, keys_in, keys_out, vin, vals_out, n, end_bit, st);
+  if (s) return s;
+  return launch_status("sort_pairs");
+}
+
+// ---- segments ---------------------------------------------------------------------
+namespace {
+struct SegWs {
+  int64_t *counts, *start, *kl, *kpre;
+  int32_t *bad;
+  void *tmp;
+  size_t tmp_bytes, total;
+};
+SegWs seg_layout(void *ws, int64_t n_seq) {
+  Carve c{static_cast<char *>(ws)};
+  SegWs L;
+  L.counts = c.take<int64_t>(8);
+  L.bad = c.take<int32_t>(8);
+  L.start = c.take<int64_t>(n_seq + 1);
+  L.kl = c.take<int64_t>(n_seq + 1);
+  L.kpre = c.take<int64_t>(n_seq + 1);
+  L.tmp_bytes = scan_temp_bytes(n_seq + 1);
+  L.tmp = c.take<char>(L.tmp_bytes);
+  L.total = c.off;
+  return L;
+}
+}  // namespace
+
+extern "C" size_t ssla_segments_workspace_size(int64_t n_seq) {
+  return n_seq < 0 ? 0 : seg_layout(nullptr, n_seq).total;
+}
+
+// truncate_packed_sequence: keep the first `threshold` rows of every
+// sequence of data [E, C] (and of others [E], when given).  counts[0] = rows
+// kept.  out_data / out_others hold E rows of capacity.
+extern "C" int ssla_truncate_packed(const float *data, const int64_t *seqlens, int64_t n_seq, int64_t E, int C,
+                                    int64_t threshold, const int64_t *others, float *out_data, int64_t *out_lengths,
+                                    int64_t *out_others, void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(n_seq >= 0 && E >= 0 && C > 0 && threshold >= 0, "truncate_packed: bad sizes");
+  const SegWs L = seg_layout(workspace, n_seq);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("truncate_packed: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, L.counts, (int64_t)8, (int64_t)0);
+  if (n_seq == 0) return launch_status("truncate_packed");
+  SSLA_CHECK_ARG(seqlens && out_lengths && (E == 0 || (data && out_data)) && (!others || out_others),
+                 "truncate_packed: null pointer");
+  int s = excl_scan(L.tmp, L.tmp_bytes, seqlens, L.start, n_seq, st);
+  if (s) return s;
+  hipLaunchKernelGGL(trunc_len, dim3(grid_for(n_seq)), dim3(kThreads), 0, st, seqlens, n_seq, threshold, L.kl);
+  s = excl_scan(L.tmp, L.tmp_bytes, L.kl, L.kpre, n_seq, st);
+  if (s) return s;
+  hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.kpre, L.kl, n_seq, L.counts);
+  if (E > 0)
+    hipLaunchKernelGGL(trunc_copy, dim3(grid_for(n_seq)), dim3(kThreads), 0, st, data, others, L.start, L.kl, L.kpre,
+                       n_seq, E, C, out_data, out_others);
+  if (hipMemcpyAsync(out_lengths, L.kl, sizeof(int64_t) * n_seq, hipMemcpyDeviceToDevice, st) != hipSuccess) {
+    set_error("truncate_packed: copy of the lengths failed");
+    return SSLA_ERR_LAUNCH;
+  }
+  return launch_status("truncate_packed");
+}
+
+// TemporalDropout keep indices: per sequence ceil(len / w) indices, every
+// w-th row, aligned so that the last row is kept.  counts[0] = kept rows.
+extern "C" int ssla_temporal_dropout_index(const int64_t *lengths, int64_t n_seq, int64_t window, int64_t *out_idx,
+                                           int64_t *out_lengths, void *workspace, size_t workspace_bytes,
+                                           void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(n_seq >= 0 && window > 0, "temporal_dropout_index: bad arguments");
+  const SegWs L = seg_layout(workspace, n_seq);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("temporal_dropout_index: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, L.counts, (int64_t)8, (int64_t)0);
+  if (n_seq == 0) return launch_status("temporal_dropout_index");
+  SSLA_CHECK_ARG(lengths && out_idx && out_lengths, "temporal_dropout_index: null pointer");
+  int s = excl_scan(L.tmp, L.tmp_bytes, lengths, L.start, n_seq, st);
+  if (s) return s;
+  hipLaunchKernelGGL(td_len, dim3(grid_for(n_seq)), dim3(kThreads), 0, st, lengths, n_seq, window, L.kl);
+  s = excl_scan(L.tmp, L.tmp_bytes, L.kl, L.kpre, n_seq, st);
+  if (s) return s;
+  hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.kpre, L.kl, n_seq, L.counts);
+  hipLaunchKernelGGL(td_index, dim3(grid_for(n_seq)), dim3(kThreads), 0, st, lengths, L.start, L.kl, L.kpre, n_seq,
+                     window, out_idx);
+  if (hipMemcpyAsync(out_lengths, L.kl, sizeof(int64_t) * n_seq, hipMemcpyDeviceToDevice, st) != hipSuccess) {
+    set_error("temporal_dropout_index: copy of the lengths failed");
+    return SSLA_ERR_LAUNCH;
+  }
+  return launch_status("temporal_dropout_index");
+}
+
+// out[i] = values[s] for every element i of segment s (repeat_interleave);
+// n = sum of lengths (elements beyond the segments are left untouched).
+extern "C" int ssla_expand_segments(const int64_t *values, const int64_t *lengths, int64_t n_seq, int64_t n,
+                                    int64_t *out, void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(n_seq >= 0 && n >= 0, "expand_segments: bad sizes");
+  const SegWs L = seg_layout(workspace, n_seq);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("expand_segments: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  if (n_seq == 0 || n == 0) return SSLA_OK;
+  SSLA_CHECK_ARG(values && lengths && out, "expand_segments: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int s = excl_scan(L.tmp, L.tmp_bytes, lengths, L.start, n_seq, st);
+  if (s) return s;
+  hipLaunchKernelGGL(expand_segments, dim3(grid_for(n_seq)), dim3(kThreads), 0, st, values, L.start, lengths, n_seq, n,
+                     out);
+  return launch_status("expand_segments");
+}
+
+// SparsePool keys: events of field f (fields in order, lengths[f] each)
+// with equal time form one pooling segment.  seg[i] = segment of event i
+// (non-decreasing: the sorted index the pooling kernels take), seg_time /
+// seg_field per segment, new_lengths[f] = segments of field f.
+// counts[0] = segments.  field[i] (the field of event i) is scratch [E].
+extern "C" int ssla_pool_segments(const int64_t *time, const int64_t *lengths, int64_t n_f, int64_t E, int64_t *field,
+                                  int64_t *seg, int64_t *seg_time, int64_t *seg_field, int64_t *new_lengths,
+                                  void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(n_f >= 0 && E >= 0, "pool_segments: bad sizes");
+  const SegWs L = seg_layout(workspace, std::max(n_f, E));
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("pool_segments: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, L.counts, (int64_t)8, (int64_t)0);
+  if (n_f == 0) return launch_status("pool_segments");
+  SSLA_CHECK_ARG(lengths && new_lengths && (E == 0 || (time && field && seg && seg_time && seg_field)),
+                 "pool_segments: null pointer");
+  hipLaunchKernelGGL(fill_i64, dim3(grid_for(n_f)), dim3(kThreads), 0, st, new_lengths, n_f, (int64_t)0);
+  if (E == 0) return launch_status("pool_segments");
+  // field of every event (repeat_interleave of 0..n_f-1)
+  int s = excl_scan(L.tmp, L.tmp_bytes, lengths, L.start, n_f, st);
+  if (s) return s;
+  hipLaunchKernelGGL(pool_field_of, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.start, lengths, n_f, E, field);
+  // segment heads and their prefix
+  int64_t *head = L.kl;   // layout holds max(n_f, E) + 1 entries
+  hipLaunchKernelGGL(pool_heads, dim3(grid_for(E)), dim3(kThreads), 0, st, time, field, E, head);
+  s = excl_scan(L.tmp, L.tmp_bytes, head, L.kpre, E, st);
+  if (s) return s;
+  hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.kpre, head, E, L.counts);
+  hipLaunchKernelGGL(pool_emit, dim3(grid_for(E)), dim3(kThreads), 0, st, head, L.kpre, time, field, E, seg, seg_time,
+                     seg_field);
+  hipLaunchKernelGGL(count_by, dim3(grid_for(E)), dim3(kThreads), 0, st, seg_field, L.counts, 0, n_f, new_lengths);
+  return launch_status("pool_segments");
+}
+
+// Sparse-to-dense grid: the last event of every group at its (b, h, w) cell
+// of grid [B, C, Hg, Wg] (other cells untouched; the caller zeroes the grid).
+extern "C" int ssla_events_to_grid(const float *events, int64_t E, int C, const int64_t *lengths,
+                                   const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w, int64_t G, int B,
+                                   int Hg, int Wg, float *grid, void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(E >= 0 && C > 0 && G >= 0 && B > 0 && Hg > 0 && Wg > 0, "events_to_grid: bad sizes");
+  const SegWs L = seg_layout(workspace, G);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("events_to_grid: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(fill_i32, dim3(1), dim3(kThreads), 0, st, L.bad, (int64_t)8, 0);
+  if (G == 0) return launch_status("events_to_grid");
+  SSLA_CHECK_ARG(events && lengths && gr_batch && gr_h && gr_w && grid, "events_to_grid: null pointer");
+  // end of every group = inclusive prefix of lengths
+  int s = excl_scan(L.tmp, L.tmp_bytes, lengths, L.start, G, st);
+  if (s) return s;
+  hipLaunchKernelGGL(seg_ends, dim3(grid_for(G)), dim3(kThreads), 0, st, L.start, lengths, G, L.kl);
+  hipLaunchKernelGGL(grid_place, dim3(grid_for(G * C)), dim3(kThreads), 0, st, events, L.kl, gr_batch, gr_h, gr_w, G,
+                     E, C, B, Hg, Wg, grid, L.bad);
+  return launch_status("events_to_grid");
+}
+
+// Per-pixel delays in place (MosModel.preprocess_inputs, model_mos.py:195-201):
+// column 0 of feat [E, C] (timestamps) becomes min((t_i - t_{i-1}) / 1e5, 1)
+// within every group and 1 at the first event of a group.
+extern "C" int ssla_pixel_delays(float *feat, int64_t E, int C, const int64_t *lengths, int64_t G, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(E >= 0 && C > 0 && G >= 0, "pixel_delays: bad sizes");
+  const SegWs L = seg_layout(workspace, G);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("pixel_delays: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  if (G == 0 || E == 0) return SSLA_OK;
+  SSLA_CHECK_ARG(feat && lengths, "pixel_delays: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int s = excl_scan(L.tmp, L.tmp_bytes, lengths, L.start, G, st);
+  if (s) return s;
+  hipLaunchKernelGGL(pixel_delays, dim3(grid_for(G)), dim3(kThreads), 0, st, feat, L.start, lengths, G, E, C);
+  return launch_status("pixel_delays");
+}

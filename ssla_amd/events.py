@@ -1,0 +1,329 @@
+"""Event-stream glue of the SSLA path on MI355X.
+
+Drop-ins for the reference's index pipelines (haohq19/ssla), with the same
+names, arguments and dict keys, running the gfx950 kernels of
+``csrc/events.hip`` through libssla_amd.so (no CPU or torch fallback):
+
+* :func:`group_events`                  utils/farsecnn_utils.py:130-174, utils/async_utils.py:10-84
+* :func:`compute_rf2pixels`             utils/farsecnn_utils.py:95-128
+* :func:`get_patch2pixel_lut`           utils/async_utils.py:96-122
+* :func:`gather_receptive_fields`       utils/farsecnn_utils.py:177-265
+* :func:`scatter_group_events_to_patch` utils/async_utils.py:125-240
+* :func:`gather_patch_events_to_group`  utils/async_utils.py:243-264
+* :func:`truncate_packed_sequence`      utils/farsecnn_utils.py:8-33
+* :func:`temporal_dropout_index`        layers/temporal_dropout.py:30-53
+* :func:`pool_segments`                 layers/sparse_pooling.py:149-171
+* :func:`events_to_grid`                model_mos.py:212-228
+* :func:`preprocess_inputs`             model_mos.py:173-209
+
+Every ordering is stable (ties keep enumeration order).  The reference's
+field sorts use ``torch.sort(stable=False)``, whose tie order is
+implementation-defined; where it is stable the results are identical.
+Calls with data-dependent output sizes synchronise once to read the counts
+(the reference's boolean-mask indexing and ``.item()`` calls do the same).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "group_events", "compute_rf2pixels", "get_patch2pixel_lut", "gather_receptive_fields",
+    "scatter_group_events_to_patch", "gather_patch_events_to_group", "truncate_packed_sequence",
+    "temporal_dropout_index", "pool_segments", "events_to_grid", "preprocess_inputs", "gather_rows",
+    "sort_pairs", "expand_segments",
+]
+
+
+def _ws(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _counts(ws: torch.Tensor, n: int, stream: int, what: str, check_bad: bool = True):
+    out = (ctypes.c_int64 * n)()
+    bad = ctypes.c_int(0)
+    _lib.check(_lib.load().ssla_events_counts(_lib.ptr(ws), out, n, ctypes.byref(bad), stream), what)
+    if check_bad and bad.value:
+        raise ValueError(f"{what}: input indices or coordinates out of range")
+    return [int(v) for v in out]
+
+
+def _i64(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.int64).contiguous()
+
+
+# ------------------------------------------------------------------ tables --
+def compute_rf2pixels(frame_size, kernel_size, stride, device=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Receptive-field lookup table and output coordinates ('same' padding,
+    -1 for padded positions); reference utils/farsecnn_utils.py:95-128."""
+    lib = _lib.load()
+    H, W = int(frame_size[0]), int(frame_size[1])
+    kh, kw = int(kernel_size[0]), int(kernel_size[1])
+    sh, sw = int(stride[0]), int(stride[1])
+    n_rf = ctypes.c_int64(0)
+    _lib.check(lib.ssla_rf_lut_shape(H, W, kh, kw, sh, sw, ctypes.byref(n_rf)), "rf_lut_shape")
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    lut = torch.empty(n_rf.value, kh * kw, dtype=torch.int64, device=dev)
+    outc = torch.empty(n_rf.value, 2, dtype=torch.int64, device=dev)
+    _lib.check(lib.ssla_rf_lut(H, W, kh, kw, sh, sw, _lib.ptr(lut), _lib.ptr(outc), _lib.stream_of(lut)), "rf_lut")
+    return lut, outc
+
+
+def get_patch2pixel_lut(frame_size, kernel_size, stride, device=None) -> torch.Tensor:
+    """Patch lookup table; reference utils/async_utils.py:96-122."""
+    return compute_rf2pixels(frame_size, kernel_size, stride, device)[0]
+
+
+# ---------------------------------------------------------------- grouping --
+def group_events(inputs, frame_size, max_events_per_px: int = 512) -> Dict[str, torch.Tensor]:
+    """Group padded events by pixel (reference utils/farsecnn_utils.py:130-174).
+
+    inputs = (events [B, N, C>=4] with x, y, t, features..., lengths [B]).
+    Returns dict(events, time, batch_id, h, w, lengths, batch_size)."""
+    if not (isinstance(inputs, tuple) and len(inputs) == 2):
+        raise ValueError("inputs should be a tuple of (events, lengths)")
+    events, lengths = inputs
+    if events.dim() != 3 or events.size(2) < 4:
+        raise ValueError("events should be a (B, N, C) tensor with C >= 4")
+    if lengths.dim() != 1 or lengths.size(0) != events.size(0):
+        raise ValueError("lengths should be a (B,) tensor")
+    dev = _lib.require_cuda(events, lengths)
+    ev = events.to(torch.float32).contiguous()
+    ln = _i64(lengths)
+    B, N, C = ev.shape
+    H, W = int(frame_size[0]), int(frame_size[1])
+    lib = _lib.load()
+    cap = B * N
+    ws = _ws(lib.ssla_group_events_workspace_size(B, N), dev)
+    out_ev = torch.empty(cap, C - 3, dtype=torch.float32, device=dev)
+    out_t = torch.empty(cap, dtype=torch.int64, device=dev)
+    gb, gh, gw, gl = (torch.empty(cap, dtype=torch.int64, device=dev) for _ in range(4))
+    st = _lib.stream_of(ev)
+    _lib.check(lib.ssla_group_events(_lib.ptr(ev), _lib.ptr(ln), B, N, C, H, W, int(max_events_per_px),
+                                     _lib.ptr(out_ev), _lib.ptr(out_t), _lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw),
+                                     _lib.ptr(gl), _lib.ptr(ws), ws.numel(), st), "group_events")
+    G, E, _ = _counts(ws, 3, st, "group_events")
+    return {"events": out_ev[:E], "time": out_t[:E], "batch_id": gb[:G], "h": gh[:G], "w": gw[:G],
+            "lengths": gl[:G], "batch_size": B}
+
+
+# ------------------------------------------------- fields / patches ----------
+def _rf_scatter(inputs, frame_size, lut):
+    lib = _lib.load()
+    gb, gh, gw, gl = (_i64(inputs[k]) for k in ("batch_id", "h", "w", "lengths"))
+    time = _i64(inputs["time"])
+    dev = _lib.require_cuda(gb, gl, time, lut)
+    B = int(inputs["batch_size"])
+    H, W = int(frame_size[0]), int(frame_size[1])
+    lut = _i64(lut)
+    n_rf, A = lut.shape
+    G, E_in = gl.numel(), time.numel()
+    E_cap = A * E_in
+    ws = _ws(lib.ssla_rf_scatter_workspace_size(G, B, H, W, n_rf, E_cap), dev)
+    st = _lib.stream_of(time)
+    _lib.check(lib.ssla_rf_scatter_plan(_lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), _lib.ptr(gl), G, _lib.ptr(time),
+                                        E_in, B, H, W, _lib.ptr(lut), n_rf, A, E_cap, _lib.ptr(ws), ws.numel(), st),
+               "rf_scatter_plan")
+    n_act, E_out, t_max = _counts(ws, 3, st, "rf_scatter_plan")
+    src = torch.empty(E_out, dtype=torch.int64, device=dev)
+    tim = torch.empty(E_out, dtype=torch.int64, device=dev)
+    pos = torch.empty(E_out, dtype=torch.int64, device=dev)
+    f_index = torch.empty(n_act, dtype=torch.int64, device=dev)
+    f_len = torch.empty(n_act, dtype=torch.int64, device=dev)
+    _lib.check(lib.ssla_rf_scatter_fill(_lib.ptr(gl), G, _lib.ptr(time), E_in, B, H, W, _lib.ptr(lut), n_rf, A, E_cap,
+                                        n_act, E_out, t_max, _lib.ptr(src), _lib.ptr(tim), _lib.ptr(pos),
+                                        _lib.ptr(f_index), _lib.ptr(f_len), _lib.ptr(ws), ws.numel(), st),
+               "rf_scatter_fill")
+    return src, tim, pos, f_index, f_len, n_rf
+
+
+def gather_rows(src: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """out[j] = src[idx[j]] for a 2-D fp32 src (the HIP row gather)."""
+    src = src.to(torch.float32).contiguous()
+    idx = _i64(idx)
+    _lib.require_cuda(src, idx)
+    C = src.shape[1] if src.dim() == 2 else 1
+    out = torch.empty(idx.numel(), C, dtype=torch.float32, device=src.device)
+    if idx.numel():
+        _lib.check(_lib.load().ssla_gather_rows(_lib.ptr(src), src.shape[0], _lib.ptr(idx), idx.numel(), C,
+                                                _lib.ptr(out), _lib.stream_of(src)), "gather_rows")
+    return out
+
+
+def gather_receptive_fields(inputs, frame_size, rf2pixel_lut, rf_outcoord) -> Dict[str, torch.Tensor]:
+    """Pixel groups -> receptive-field sequences (reference
+    utils/farsecnn_utils.py:177-265): dict(events, time, pos_id, lengths, h,
+    w, batch_id, batch_size)."""
+    src, tim, pos, f_index, f_len, n_rf = _rf_scatter(inputs, frame_size, rf2pixel_lut)
+    ev = gather_rows(inputs["events"], src)
+    rf = f_index % n_rf
+    outc = _i64(rf_outcoord)
+    return {"events": ev, "time": tim, "pos_id": pos, "lengths": f_len, "h": outc[rf, 1], "w": outc[rf, 0],
+            "batch_id": f_index // n_rf, "batch_size": inputs["batch_size"]}
+
+
+def scatter_group_events_to_patch(pixel_inputs, frame_size, patch2pixel_lut) -> Dict[str, torch.Tensor]:
+    """Pixel groups -> patch sequences (reference utils/async_utils.py:125-240):
+    dict(events, pos_id, lengths, batch_size, orig_event_idx)."""
+    src, _tim, pos, _f_index, f_len, _ = _rf_scatter(pixel_inputs, frame_size, patch2pixel_lut)
+    ev = gather_rows(pixel_inputs["events"], src)
+    return {"events": ev, "pos_id": pos, "lengths": f_len, "batch_size": pixel_inputs["batch_size"],
+            "orig_event_idx": src}
+
+
+def gather_patch_events_to_group(patch_events: torch.Tensor, patch_event_to_pixel_event_idx: torch.Tensor,
+                                 num_pixel_events: int) -> torch.Tensor:
+    """Sum the patch copies of every pixel event (reference
+    utils/async_utils.py:243-264); copies are added in increasing patch-event
+    order from zero in fp32, as index_add_ does on the CPU."""
+    pe = patch_events.to(torch.float32).contiguous()
+    idx = _i64(patch_event_to_pixel_event_idx)
+    dev = _lib.require_cuda(pe, idx)
+    n, C = pe.shape
+    lib = _lib.load()
+    ws = _ws(lib.ssla_index_add_rows_workspace_size(n), dev)
+    out = torch.empty(int(num_pixel_events), C, dtype=torch.float32, device=dev)
+    st = _lib.stream_of(pe)
+    _lib.check(lib.ssla_index_add_rows(_lib.ptr(pe), _lib.ptr(idx), n, C, int(num_pixel_events), _lib.ptr(out),
+                                       _lib.ptr(ws), ws.numel(), st), "index_add_rows")
+    return out
+
+
+# ---------------------------------------------------------------- sequences --
+def truncate_packed_sequence(data: torch.Tensor, seqlens: torch.Tensor, threshold: int,
+                             others: Optional[torch.Tensor] = None):
+    """Keep the first `threshold` rows of every packed sequence (reference
+    utils/farsecnn_utils.py:8-33); returns (new_data, new_lengths[, new_others])."""
+    d2 = data.to(torch.float32).reshape(data.shape[0], -1).contiguous()
+    sl = _i64(seqlens)
+    dev = _lib.require_cuda(d2, sl)
+    E, C = d2.shape
+    oth = None if others is None else _i64(others)
+    lib = _lib.load()
+    ws = _ws(lib.ssla_segments_workspace_size(sl.numel()), dev)
+    out = torch.empty(E, max(C, 1), dtype=torch.float32, device=dev)
+    out_l = torch.empty(sl.numel(), dtype=torch.int64, device=dev)
+    out_o = None if oth is None else torch.empty(E, dtype=torch.int64, device=dev)
+    st = _lib.stream_of(d2)
+    _lib.check(lib.ssla_truncate_packed(_lib.ptr(d2), _lib.ptr(sl), sl.numel(), E, max(C, 1), int(threshold),
+                                        _lib.ptr(oth), _lib.ptr(out), _lib.ptr(out_l), _lib.ptr(out_o), _lib.ptr(ws),
+                                        ws.numel(), st), "truncate_packed")
+    (n,) = _counts(ws, 1, st, "truncate_packed", check_bad=False)
+    nd = out[:n].reshape((n,) + tuple(data.shape[1:])).to(data.dtype)
+    if others is not None:
+        return nd, out_l, out_o[:n].to(others.dtype)
+    return nd, out_l
+
+
+def temporal_dropout_index(lengths: torch.Tensor, window_size: int):
+    """Keep indices and new lengths of TemporalDropout (reference
+    layers/temporal_dropout.py:30-53)."""
+    ln = _i64(lengths)
+    dev = _lib.require_cuda(ln)
+    lib = _lib.load()
+    ws = _ws(lib.ssla_segments_workspace_size(ln.numel()), dev)
+    # capacity: sum(ceil(len / w)) <= sum(len) + n
+    cap_t = int(ln.sum().item()) + ln.numel()
+    idx = torch.empty(max(cap_t, 1), dtype=torch.int64, device=dev)
+    kl = torch.empty(ln.numel(), dtype=torch.int64, device=dev)
+    st = _lib.stream_of(ln)
+    _lib.check(lib.ssla_temporal_dropout_index(_lib.ptr(ln), ln.numel(), int(window_size), _lib.ptr(idx),
+                                               _lib.ptr(kl), _lib.ptr(ws), ws.numel(), st), "temporal_dropout_index")
+    (n,) = _counts(ws, 1, st, "temporal_dropout_index", check_bad=False)
+    return idx[:n], kl
+
+
+def expand_segments(values: torch.Tensor, lengths: torch.Tensor, total: Optional[int] = None) -> torch.Tensor:
+    """repeat_interleave(values, lengths) on the device."""
+    v, ln = _i64(values), _i64(lengths)
+    dev = _lib.require_cuda(v, ln)
+    n = int(ln.sum().item()) if total is None else int(total)
+    out = torch.empty(n, dtype=torch.int64, device=dev)
+    lib = _lib.load()
+    ws = _ws(lib.ssla_segments_workspace_size(ln.numel()), dev)
+    _lib.check(lib.ssla_expand_segments(_lib.ptr(v), _lib.ptr(ln), ln.numel(), n, _lib.ptr(out), _lib.ptr(ws),
+                                        ws.numel(), _lib.stream_of(v)), "expand_segments")
+    return out
+
+
+def sort_pairs(keys: torch.Tensor, end_bit: int = 64, values: Optional[torch.Tensor] = None):
+    """Stable sort of uint64-valued keys (given as int64, non-negative);
+    returns (sorted keys, permutation as int64)."""
+    k = _i64(keys)
+    dev = _lib.require_cuda(k)
+    n = k.numel()
+    lib = _lib.load()
+    ws = _ws(lib.ssla_sort_pairs_workspace_size(n), dev)
+    ko = torch.empty_like(k)
+    vo = torch.empty(n, dtype=torch.int32, device=dev)
+    vin = None if values is None else values.to(torch.int32).contiguous()
+    _lib.check(lib.ssla_sort_pairs(_lib.ptr(k), _lib.ptr(vin), n, int(end_bit), _lib.ptr(ko), _lib.ptr(vo),
+                                   _lib.ptr(ws), ws.numel(), _lib.stream_of(k)), "sort_pairs")
+    return ko, vo.to(torch.int64)
+
+
+def pool_segments(time: torch.Tensor, lengths: torch.Tensor):
+    """SparsePool keys (reference layers/sparse_pooling.py:149-171): for
+    field sequences laid out in order, the non-decreasing segment index of
+    every event (events of a field with equal time share a segment), the
+    time of every segment and the segment count of every field."""
+    t, ln = _i64(time), _i64(lengths)
+    dev = _lib.require_cuda(t, ln)
+    E, n_f = t.numel(), ln.numel()
+    lib = _lib.load()
+    ws = _ws(lib.ssla_segments_workspace_size(max(n_f, E)), dev)
+    field = torch.empty(max(E, 1), dtype=torch.int64, device=dev)
+    seg = torch.empty(max(E, 1), dtype=torch.int64, device=dev)
+    seg_t = torch.empty(max(E, 1), dtype=torch.int64, device=dev)
+    seg_f = torch.empty(max(E, 1), dtype=torch.int64, device=dev)
+    new_len = torch.empty(n_f, dtype=torch.int64, device=dev)
+    st = _lib.stream_of(t)
+    _lib.check(lib.ssla_pool_segments(_lib.ptr(t), _lib.ptr(ln), n_f, E, _lib.ptr(field), _lib.ptr(seg),
+                                      _lib.ptr(seg_t), _lib.ptr(seg_f), _lib.ptr(new_len), _lib.ptr(ws), ws.numel(),
+                                      st), "pool_segments")
+    (n_seg,) = _counts(ws, 1, st, "pool_segments", check_bad=False)
+    return seg[:E], seg_t[:n_seg], new_len
+
+
+def events_to_grid(x: Dict[str, torch.Tensor], grid_size, channels: int) -> torch.Tensor:
+    """The last event of every group at its cell of a dense [B, C, H, W]
+    grid (reference model_mos.py:212-228)."""
+    ev = x["events"].to(torch.float32).contiguous()
+    ln, gb, gh, gw = (_i64(x[k]) for k in ("lengths", "batch_id", "h", "w"))
+    dev = _lib.require_cuda(ev, ln)
+    B = int(x["batch_size"])
+    Hg, Wg = int(grid_size[0]), int(grid_size[1])
+    if ev.shape[1] != channels:
+        raise ValueError(f"events_to_grid: {ev.shape[1]} channels, expected {channels}")
+    grid = torch.zeros(B, channels, Hg, Wg, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws = _ws(lib.ssla_segments_workspace_size(ln.numel()), dev)
+    st = _lib.stream_of(ev)
+    _lib.check(lib.ssla_events_to_grid(_lib.ptr(ev), ev.shape[0], channels, _lib.ptr(ln), _lib.ptr(gb),
+                                       _lib.ptr(gh), _lib.ptr(gw), ln.numel(), B, Hg, Wg, _lib.ptr(grid),
+                                       _lib.ptr(ws), ws.numel(), st), "events_to_grid")
+    return grid
+
+
+def preprocess_inputs(events: torch.Tensor, lengths: torch.Tensor, frame_size, hot_pixel_thres: int = 50):
+    """MosModel.preprocess_inputs (reference model_mos.py:173-209):
+    <x, y, t, p> -> grouped pixels with features <dt, p>, dt the per-pixel
+    delay clamped at 100 ms and normalised to [0, 1] (1 for the first event
+    of a pixel), hot pixels truncated to their first `hot_pixel_thres`."""
+    ev = events.to(torch.float32)
+    ev = torch.cat([ev[..., :3], ev[..., 2:3], ev[..., 3:]], dim=-1).contiguous()
+    gr = group_events((ev, lengths), frame_size)
+    feats = gr["events"]
+    ln = gr["lengths"]
+    lib = _lib.load()
+    ws = _ws(lib.ssla_segments_workspace_size(ln.numel()), feats.device)
+    _lib.check(lib.ssla_pixel_delays(_lib.ptr(feats), feats.shape[0], feats.shape[1], _lib.ptr(ln), ln.numel(),
+                                     _lib.ptr(ws), ws.numel(), _lib.stream_of(feats)), "pixel_delays")
+    if hot_pixel_thres > 0:
+        gr["events"], gr["lengths"], gr["time"] = truncate_packed_sequence(
+            gr["events"], gr["lengths"], threshold=hot_pixel_thres, others=gr["time"])
+    return gr

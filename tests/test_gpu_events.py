@@ -1,0 +1,166 @@
+"""GPU parity of the event glue (csrc/events.hip via the C-ABI) against the
+golden vectors the reference's own functions wrote
+(tests/golden/event_fixtures.npz) and, at larger seeded sizes, against the
+CPU oracle (oracle/events.py).  Integer outputs and gathered rows are
+compared bit-exactly."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import events as OE
+
+pytestmark = pytest.mark.gpu
+FIX = Path(__file__).resolve().parent / "golden" / "event_fixtures.npz"
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return np.load(FIX, allow_pickle=False)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _grouped(fx, dev, cap=512):
+    from ssla_amd import events as E
+    return E.group_events((_t(fx["ge_events"], dev), _t(fx["ge_lengths"], dev)), tuple(int(v) for v in fx["ge_frame"]),
+                          max_events_per_px=cap)
+
+
+@pytest.mark.parametrize("cap", [4, 512])
+def test_group_events_fixture(dev, fx, cap):
+    gr = _grouped(fx, dev, cap)
+    for key in ("events", "time", "batch_id", "h", "w", "lengths"):
+        np.testing.assert_array_equal(_np(gr[key]), fx[f"ge_farse_{cap}_{key}"], err_msg=key)
+
+
+@pytest.mark.parametrize("name", ["12x15_k3s1", "7x10_k3s2", "9x5_k2s2", "6x8_k5s3"])
+def test_lut_fixture(dev, fx, name):
+    from ssla_amd import events as E
+    fh, fw = (int(v) for v in name.split("_")[0].split("x"))
+    k, s = int(name.split("_")[1][1]), int(name.split("_")[1][3])
+    lut, outc = E.compute_rf2pixels((fh, fw), (k, k), (s, s), device=dev)
+    np.testing.assert_array_equal(_np(lut), fx[f"rf2p_{name}"])
+    np.testing.assert_array_equal(_np(outc), fx[f"rfout_{name}"])
+
+
+@pytest.mark.parametrize("ks", [3, 2])
+def test_patch_scatter_gather_fixture(dev, fx, ks):
+    from ssla_amd import events as E
+    gr = _grouped(fx, dev)
+    gr["events"] = _t(fx["sp_pix_events"], dev)
+    frame = tuple(int(v) for v in fx["ge_frame"])
+    lut = E.get_patch2pixel_lut(frame, (ks, ks), (1, 1), device=dev)
+    res = E.scatter_group_events_to_patch(gr, frame, lut)
+    for key in ("events", "pos_id", "lengths", "orig_event_idx"):
+        np.testing.assert_array_equal(_np(res[key]), fx[f"sps_k{ks}_{key}"], err_msg=key)
+    out = E.gather_patch_events_to_group(_t(fx[f"sp_k{ks}_gather_in"], dev), res["orig_event_idx"],
+                                         fx["sp_pix_events"].shape[0])
+    np.testing.assert_array_equal(_np(out).view(np.uint32), fx[f"sps_k{ks}_gather_out"].view(np.uint32))
+
+
+@pytest.mark.parametrize("k,s", [(2, 2), (3, 2)])
+def test_gather_receptive_fields_fixture(dev, fx, k, s):
+    from ssla_amd import events as E
+    gr = _grouped(fx, dev)
+    gr["events"] = _t(fx["sp_pix_events"], dev)
+    frame = tuple(int(v) for v in fx["ge_frame"])
+    lut, outc = E.compute_rf2pixels(frame, (k, k), (s, s), device=dev)
+    res = E.gather_receptive_fields(gr, frame, lut, outc)
+    for key in ("events", "time", "pos_id", "lengths", "h", "w", "batch_id"):
+        np.testing.assert_array_equal(_np(res[key]), fx[f"grfs_k{k}s{s}_{key}"], err_msg=key)
+
+
+def test_truncate_and_dropout_fixture(dev, fx):
+    from ssla_amd import events as E
+    nd, nl, no = E.truncate_packed_sequence(_t(fx["tr_data"], dev), _t(fx["tr_seqlens"], dev), 4,
+                                            others=_t(fx["tr_other"], dev))
+    np.testing.assert_array_equal(_np(nd), fx["tr_new_data"])
+    np.testing.assert_array_equal(_np(nl), fx["tr_new_lengths"])
+    np.testing.assert_array_equal(_np(no), fx["tr_new_other"])
+    for w in (1, 3, 4):
+        idx, kl = E.temporal_dropout_index(_t(fx["td_in_lengths"], dev), w)
+        np.testing.assert_array_equal(_np(kl), fx[f"td_w{w}_lengths"])
+        np.testing.assert_array_equal(fx["td_in_time"][_np(idx)], fx[f"td_w{w}_time"])
+
+
+def _synthetic(seed, B, N, H, W, dev):
+    gen = np.random.default_rng(seed)
+    ev = np.zeros((B, N, 4), np.float32)
+    lens = gen.integers(N // 2, N + 1, B)
+    for b in range(B):
+        n = int(lens[b])
+        cx, cy = gen.uniform(0, W, 5), gen.uniform(0, H, 5)
+        c = gen.integers(0, 5, n)
+        x = np.clip(np.round(cx[c] + gen.normal(0, 3, n)), 0, W - 1)
+        y = np.clip(np.round(cy[c] + gen.normal(0, 3, n)), 0, H - 1)
+        t = np.sort(gen.integers(0, 20000, n)).astype(np.float32)
+        ev[b, :n] = np.stack([x, y, t, np.where(gen.random(n) < 0.5, -1.0, 1.0)], 1)
+    return ev, lens
+
+
+def test_preprocess_and_fields_synthetic(dev):
+    """Larger seeded window (2 samples, 64x80 frame): preprocess_inputs, a
+    stride-2 pooling field scatter with its segment keys and scatter_max,
+    and the dense grid, all against the oracle."""
+    from ssla_amd import events as E
+    from ssla_amd.scatter import scatter_max
+    H, W = 64, 80
+    ev, lens = _synthetic(7, 2, 3000, H, W, dev)
+    gr = E.preprocess_inputs(_t(ev, dev), _t(lens, dev), (H, W), hot_pixel_thres=20)
+    ro = OE.preprocess_events(ev, lens, (H, W), hot_pixel_thres=20)
+    for key in ("events", "time", "batch_id", "h", "w", "lengths"):
+        np.testing.assert_array_equal(_np(gr[key]), ro[key], err_msg=key)
+
+    lut, outc = E.compute_rf2pixels((H, W), (2, 2), (2, 2), device=dev)
+    rf = E.gather_receptive_fields(gr, (H, W), lut, outc)
+    rro = OE.gather_receptive_fields(ro, (H, W), _np(lut), _np(outc))
+    for key in ("events", "time", "pos_id", "lengths", "h", "w", "batch_id"):
+        np.testing.assert_array_equal(_np(rf[key]), rro[key], err_msg=key)
+
+    seg, seg_t, new_len = E.pool_segments(rf["time"], rf["lengths"])
+    with torch.no_grad():
+        pooled, _ = scatter_max(rf["events"], seg, dim=0, dim_size=int(seg_t.numel()), sorted_index=True)
+    rp = OE.sparse_pool(rro, "max")
+    np.testing.assert_array_equal(_np(pooled), rp["events"])
+    np.testing.assert_array_equal(_np(seg_t), rp["time"])
+    np.testing.assert_array_equal(_np(new_len), rp["lengths"])
+
+    grid = E.events_to_grid(gr, (H, W), gr["events"].shape[1])
+    np.testing.assert_array_equal(_np(grid), OE.event_to_grid(ro, (H, W), ro["events"].shape[1]))
+
+
+def test_patch_scatter_synthetic(dev):
+    from ssla_amd import events as E
+    H, W = 40, 48
+    ev, lens = _synthetic(3, 3, 1500, H, W, dev)
+    evc = np.concatenate([ev, np.random.default_rng(1).normal(size=ev.shape[:2] + (3,)).astype(np.float32)], -1)
+    gr = E.group_events((_t(evc, dev), _t(lens, dev)), (H, W))
+    ro = OE.group_events(evc, lens, (H, W))
+    lut = E.get_patch2pixel_lut((H, W), (3, 3), (1, 1), device=dev)
+    res = E.scatter_group_events_to_patch(gr, (H, W), lut)
+    rres = OE.scatter_group_events_to_patch(ro, (H, W), _np(lut))
+    for key in ("events", "pos_id", "lengths", "orig_event_idx"):
+        np.testing.assert_array_equal(_np(res[key]), rres[key], err_msg=key)
+    pe = np.random.default_rng(2).normal(size=(rres["events"].shape[0], 5)).astype(np.float32)
+    out = E.gather_patch_events_to_group(_t(pe, dev), res["orig_event_idx"], ro["events"].shape[0])
+    ref = OE.gather_patch_events_to_group(pe, rres["orig_event_idx"], ro["events"].shape[0])
+    np.testing.assert_array_equal(_np(out).view(np.uint32), ref.view(np.uint32))
+
+
+def test_empty_and_bad_inputs(dev):
+    from ssla_amd import events as E
+    ev = torch.zeros(2, 5, 4, device=dev)
+    gr = E.group_events((ev, torch.zeros(2, dtype=torch.int64, device=dev)), (4, 4))
+    assert gr["events"].shape[0] == 0 and gr["lengths"].numel() == 0
+    bad = torch.zeros(1, 3, 4, device=dev)
+    bad[0, 1, 0] = 9.0                       # x outside a 4-wide frame
+    with pytest.raises(ValueError):
+        E.group_events((bad, torch.tensor([3], device=dev)), (4, 4))
