@@ -331,11 +331,17 @@ __global__ __launch_bounds__(kScanCells *kScanTpc) void scan_kernel(
         if (incl) break;
         j_end -= 64;
       }
-    } else if (tid == 0) {
-      // error slots of the first kernel -> status word
+    } else {
+      // error slots of the first kernel -> status word (the wavefront reads
+      // them in parallel: block 0 gates every later block's look-back)
       int st = SSLA_OK;
-      for (int i = 0; i < n_err; ++i) if (errs[i] != SSLA_OK) st = errs[i];
-      *status = st;
+      for (int i = tid; i < n_err; i += 64) {
+        const int v = errs[i];
+        if (v != SSLA_OK) st = v;
+      }
+      const uint64_t bad = __builtin_amdgcn_ballot_w64(st != SSLA_OK);
+      if (bad) st = __shfl(st, static_cast<int>(__builtin_ctzll(bad)));
+      if (tid == 0) *status = st;
     }
     if (tid == 0) {
       __hip_atomic_store(&flags[bid], kFlagIncl | pack_pair(ex_c + agg_c, ex_p + agg_p), __ATOMIC_RELAXED,
