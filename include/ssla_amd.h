@@ -242,7 +242,7 @@ int ssla_index_add_rows(const float *src, const int64_t *idx, int64_t n, int C, 
 
 /* Stable sort of (uint64 key, int32 value) pairs on the low end_bit key
  * bits; vals_in NULL means 0..n-1.  Used for the (batch, time) ordering of
- * LinearAttention.forward (layers/linear_attention.py:60-65) and the
+ * LinearAttention.forward (layers/linear_attention.py:62-63) and the
  * position bucketing of the patch projections (layers/mos_attention.py:148-167). */
 size_t ssla_sort_pairs_workspace_size(int64_t n);
 int ssla_sort_pairs(const uint64_t *keys_in, const int32_t *vals_in, int64_t n, int end_bit,
@@ -266,11 +266,12 @@ int ssla_truncate_packed(const float *data, const int64_t *seqlens, int64_t n_se
 int ssla_temporal_dropout_index(const int64_t *lengths, int64_t n_seq, int64_t window, int64_t *out_idx,
                                 int64_t *out_lengths, void *workspace, size_t workspace_bytes, void *stream);
 
-/* repeat_interleave(values, lengths) into out [n]. */
+/* repeat_interleave(values, lengths) into out [n] (layers/linear_attention.py:60,
+ * layers/sparse_pooling.py:27). */
 int ssla_expand_segments(const int64_t *values, const int64_t *lengths, int64_t n_seq, int64_t n,
                          int64_t *out, void *workspace, size_t workspace_bytes, void *stream);
 
-/* SparsePool keys (layers/sparse_pooling.py:149-171): events of a field with
+/* SparsePool keys (layers/sparse_pooling.py:26-48): events of a field with
  * equal time form one pooling segment.  seg[E] (non-decreasing: the sorted
  * index of ssla_scatter_max / _mean), seg_time / seg_field per segment,
  * new_lengths[n_f] segments per field, field[E] scratch.  counts[0] =

@@ -12,7 +12,7 @@ names, arguments and dict keys, running the gfx950 kernels of
 * :func:`gather_patch_events_to_group`  utils/async_utils.py:243-264
 * :func:`truncate_packed_sequence`      utils/farsecnn_utils.py:8-33
 * :func:`temporal_dropout_index`        layers/temporal_dropout.py:30-53
-* :func:`pool_segments`                 layers/sparse_pooling.py:149-171
+* :func:`pool_segments`                 layers/sparse_pooling.py:26-48
 * :func:`events_to_grid`                model_mos.py:212-228
 * :func:`preprocess_inputs`             model_mos.py:173-209
 
@@ -267,7 +267,7 @@ def sort_pairs(keys: torch.Tensor, end_bit: int = 64, values: Optional[torch.Ten
 
 
 def pool_segments(time: torch.Tensor, lengths: torch.Tensor):
-    """SparsePool keys (reference layers/sparse_pooling.py:149-171): for
+    """SparsePool keys (reference layers/sparse_pooling.py:26-48): for
     field sequences laid out in order, the non-decreasing segment index of
     every event (events of a field with equal time share a segment), the
     time of every segment and the segment count of every field."""

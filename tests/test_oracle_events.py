@@ -143,3 +143,43 @@ def test_sparse_pool_brute_force():
     np.testing.assert_array_equal(r["lengths"], [2, 1])
     m = OE.sparse_pool(rf, "mean")
     np.testing.assert_allclose(m["events"], [[2, 1], [2, 5], [3.5, 4]])
+
+
+def test_preprocess_delays_direct_loop(fx):
+    """model_mos.py:173-209 restated event by event: within each pixel group
+    (in time order) feature 0 becomes min((t - t_prev) / 1e5, 1), 1 for the
+    first event of the group; hot pixels keep their first 50 events."""
+    ev = fx["ge_events"][..., [0, 1, 2, 4]]          # <x, y, t, p>
+    lens = fx["ge_lengths"]
+    H, W = (int(v) for v in fx["ge_frame"])
+    gr = OE.preprocess_events(ev, lens, (H, W), hot_pixel_thres=3)
+    # direct loop over the padded input
+    per_pix = {}
+    for b in range(ev.shape[0]):
+        for n in range(int(lens[b])):
+            x, y, t, p = ev[b, n]
+            per_pix.setdefault((b, int(y), int(x)), []).append((t, p))
+    want = []
+    for key in sorted(per_pix):
+        prev = None
+        for i, (t, p) in enumerate(per_pix[key][-512:]):
+            d = 1.0 if prev is None else min((np.float32(t) - np.float32(prev)) / np.float32(1e5), 1.0)
+            prev = t
+            if i < 3:
+                want.append((d, p))
+    want = np.array(want, np.float32)
+    np.testing.assert_allclose(gr["events"][:, 0], want[:, 0], rtol=1e-6)
+    np.testing.assert_array_equal(gr["events"][:, 1], want[:, 1])
+    assert int(np.sum(gr["lengths"])) == want.shape[0]
+
+
+def test_event_to_grid_direct_loop():
+    """model_mos.py:212-228: the last event of each group at its cell."""
+    gr = {"events": np.arange(12, dtype=np.float32).reshape(6, 2), "lengths": np.array([2, 3, 1]),
+          "batch_id": np.array([0, 1, 1]), "h": np.array([1, 0, 2]), "w": np.array([2, 1, 0]), "batch_size": 2}
+    grid = OE.event_to_grid(gr, (3, 3), 2)
+    want = np.zeros((2, 2, 3, 3), np.float32)
+    want[0, :, 1, 2] = gr["events"][1]
+    want[1, :, 0, 1] = gr["events"][4]
+    want[1, :, 2, 0] = gr["events"][5]
+    np.testing.assert_array_equal(grid, want)
