@@ -175,9 +175,7 @@ __device__ __forceinline__ void row_scan16(f32x8 (&x)[2]) {
 
 __device__ __forceinline__ float clamp_exp(float x) { return fminf(fmaxf(x, -kExpClamp), kExpClamp); }
 
-// Raw global loads of one chunk row of this lane: q, k, g at keys
-// {kq..kq+7, 32+kq..32+kq+7} and v at columns {kq.., 32+kq..} (columns
-// beyond the V group are not loaded).
+// Raw loads of one chunk row of this lane (see load_chunk).
 struct ChunkRegs {
   uint4 q[2], k[2];   // 16-bit
   float4 g[4];        // fp32 g ...
@@ -185,36 +183,48 @@ struct ChunkRegs {
   uint4 v[2];
 };
 
-// off: element offset of this lane's row and first key in q, k, g
-// ([T, H, 64] layout); offv: element offset of its row and first column in
-// v ([T, H, V] layout, V group applied).  Both advance by a constant per
-// chunk, so no address is recomputed inside the chunk loops.
+// Per-sequence buffer resources of q, k, g, v and o: the base is the
+// sequence's first row and the size its rows, so the hardware range check
+// returns zeros for loads of rows past the sequence end and drops stores to
+// them.  Rows past the end therefore need no branches: zero g keeps the
+// chunk's total decay at the last valid row, zero k / v remove them from the
+// state update, and their outputs are never written.  Offsets are 32-bit
+// byte offsets (the host checks that a sequence stays below 2 GB).
+struct SeqRsrc {
+  __amdgpu_buffer_rsrc_t q, k, g, v, o;
+};
+
+constexpr int kRsrcWord3 = 0x00020000;   // raw 32-bit data, range checked
+constexpr uint32_t kNoLoad = 0x80000000u; // an offset past every resource: reads zeros, no traffic
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t seq_rsrc(const void *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), kRsrcWord3);
+}
+
+// Raw loads of one chunk row of this lane: q, k, g at keys {kq..kq+7,
+// 32+kq..32+kq+7} and v at columns {kq.., 32+kq..} of its V group.  oq / og /
+// ov are the byte offsets of the lane's first element; `valid` false (no
+// next chunk) turns every load into a zero read without memory traffic, so
+// the instruction stream is the same on every iteration.
 template <bool LOADQ, bool GF32>
-__device__ __forceinline__ void load_chunk(ChunkRegs &R, const uint16_t *__restrict__ q,
-                                           const uint16_t *__restrict__ k,
-                                           const uint16_t *__restrict__ v, const void *__restrict__ g,
-                                           int64_t off, int64_t offv, bool row_ok, int kq, int vw) {
+__device__ __forceinline__ void load_chunk(ChunkRegs &R, const SeqRsrc &rs, bool valid, uint32_t oq,
+                                           uint32_t og, uint32_t ov, int kq, int vw) {
+  const uint32_t q0 = valid ? oq : kNoLoad, g0 = valid ? og : kNoLoad;
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
-    if (row_ok) {
-      if (LOADQ) R.q[jj] = *reinterpret_cast<const uint4 *>(q + off + 32 * jj);
-      R.k[jj] = *reinterpret_cast<const uint4 *>(k + off + 32 * jj);
-      if (GF32) {
-        const float *gp = static_cast<const float *>(g) + off + 32 * jj;
-        R.g[2 * jj] = *reinterpret_cast<const float4 *>(gp);
-        R.g[2 * jj + 1] = *reinterpret_cast<const float4 *>(gp + 4);
-      } else {
-        R.g16[jj] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g) + off + 32 * jj);
-      }
-      R.v[jj] = (32 * jj + kq < vw) ? *reinterpret_cast<const uint4 *>(v + offv + 32 * jj) : make_uint4(0, 0, 0, 0);
+    if (LOADQ) R.q[jj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.q, q0 + 64 * jj, 0, 0));
+    R.k[jj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.k, q0 + 64 * jj, 0, 0));
+    if (GF32) {
+      R.g[2 * jj] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs.g, g0 + 128 * jj, 0, 0));
+      R.g[2 * jj + 1] =
+          __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs.g, g0 + 128 * jj + 16, 0, 0));
     } else {
-      if (LOADQ) R.q[jj] = make_uint4(0, 0, 0, 0);
-      R.k[jj] = make_uint4(0, 0, 0, 0);
-      R.g[2 * jj] = make_float4(0.f, 0.f, 0.f, 0.f);
-      R.g[2 * jj + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
-      R.g16[jj] = make_uint4(0, 0, 0, 0);
-      R.v[jj] = make_uint4(0, 0, 0, 0);
+      R.g16[jj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.g, g0 + 64 * jj, 0, 0));
     }
+    // columns beyond the V group are never used: read zeros instead
+    const uint32_t vo = (valid && 32 * jj + kq < vw) ? ov + 64 * jj : kNoLoad;
+    R.v[jj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.v, vo, 0, 0));
   }
 }
 
@@ -279,6 +289,23 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
   // ---- entering state: keys 16wv + 4gq + i, columns v0 + 16t + r ---------
   const int64_t sbase = (static_cast<int64_t>(a.n) * H + h) * KD;
   const int krow = 16 * wv + 4 * gq;
+  // the first chunk's loads go out before the entering state is read
+  const int row = 16 * wv + r;
+  constexpr int gsz = GF32 ? 4 : 2;   // bytes per g element
+  SeqRsrc rs;
+  rs.q = seq_rsrc(a.q + a.bos * H * KD, len * H * KD * 2);
+  rs.k = seq_rsrc(a.k + a.bos * H * KD, len * H * KD * 2);
+  rs.g = seq_rsrc(static_cast<const char *>(a.g) + a.bos * H * KD * gsz, len * H * KD * gsz);
+  rs.v = seq_rsrc(a.v + a.bos * H * V, len * H * V * 2);
+  rs.o = seq_rsrc(a.o + a.bos * H * V, len * H * V * 2);
+  // byte offsets of this lane's row (chunk c_beg) inside the sequence, and
+  // their per-chunk steps
+  const uint32_t rowi = static_cast<uint32_t>((a.c_beg * BT + row) * H + h);
+  uint32_t oq = (rowi * KD + kq) * 2, og = (rowi * KD + kq) * gsz;
+  uint32_t ov = (rowi * V + v0) * 2;   // row start of the V group (o uses it too)
+  const uint32_t sq = BT * H * KD * 2, sg = BT * H * KD * gsz, sv = BT * H * V * 2;
+  ChunkRegs buf;
+  load_chunk<true, GF32>(buf, rs, a.c_beg < a.c_end, oq, og, ov + 2 * kq, kq, vw);
   f32x4 S[NVT];
   {
     const float *src = nullptr;
@@ -290,27 +317,26 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
       for (int i = 0; i < 4; ++i)
         S[t][i] = src ? src[static_cast<int64_t>(krow + i) * V + v0 + 16 * t + r] : 0.f;
   }
+  // Wait here for the entering state (and the first chunk, needed next
+  // anyway): otherwise the loop's wait bookkeeping carries these loads
+  // around the back edge and drains all loads (vmcnt(0)) in every chunk.
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0) only
 
-  const int row = 16 * wv + r;
-  const int64_t strk = static_cast<int64_t>(BT) * H * KD, strv = static_cast<int64_t>(BT) * H * V;
-  int64_t off = ((a.bos + static_cast<int64_t>(a.c_beg) * BT + row) * H + h) * KD + kq;
-  int64_t offv = ((a.bos + static_cast<int64_t>(a.c_beg) * BT + row) * H + h) * V + v0;   // row start
-  ChunkRegs buf;
-  if (a.c_beg < a.c_end)
-    load_chunk<true, GF32>(buf, a.q, a.k, a.v, a.g, off, offv + kq,
-                           row < len - static_cast<int64_t>(a.c_beg) * BT, kq, vw);
 
-  for (int c = a.c_beg; c < a.c_end; ++c) {
-    const int64_t rem = len - static_cast<int64_t>(c) * BT;   // valid rows in this chunk (>0)
-    uint16_t *orow = a.o + offv;                               // o row of this lane (same layout as v)
+  // Two prefetch register sets used in turn (the loop is unrolled by two),
+  // so no copy is made and the wait at each chunk covers only the loads of
+  // that chunk, not the o stores issued after them.
+  ChunkRegs buf2;
+  auto chunk_step = [&](ChunkRegs &cur, ChunkRegs &nxt, const int c) __attribute__((always_inline)) {
+    const uint32_t orow = ov;   // o row of this lane in this chunk (same layout as v)
 
-    // ---- take the current chunk out of the prefetch registers, prefetch c+1 -
-    const ChunkRegs cur = buf;
+    // ---- prefetch q, k, g, v of c+1 -------------------------------------------
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    off += strk;
-    offv += strv;
-    if (c + 1 < a.c_end) load_chunk<true, GF32>(buf, a.q, a.k, a.v, a.g, off, offv + kq, row < rem - BT, kq, vw);
+    oq += sq;
+    og += sg;
+    ov += sv;
+    load_chunk<true, GF32>(nxt, rs, c + 1 < a.c_end, oq, og, ov + 2 * kq, kq, vw);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- block-local inclusive cumsum over the 16 rows (DPP row scan) ------
@@ -434,11 +460,13 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
           oacc = M::mma(va, ab[pr], oacc);
         }
       }
-      if (row < rem) {
+      {
+        // rows past the sequence end fall outside rs.o and are dropped
         const f32x8 o8 = {oacc[0] * a.scale, oacc[1] * a.scale, oacc[2] * a.scale, oacc[3] * a.scale,
                           0.f, 0.f, 0.f, 0.f};
         const uint4 ob = to_bits(M::cvt(o8));
-        *reinterpret_cast<uint2 *>(orow + 16 * t + 4 * gq) = make_uint2(ob.x, ob.y);
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64((u32x2){ob.x, ob.y}, rs.o, orow + 2 * (16 * t + 4 * gq), 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -455,6 +483,10 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
         S[t] = M::mma(ka1, tr_operand<MV>(sm.vs, 32 + 8 * gq, 32 + 8 * gq + 4, 16 * t, lane), S[t]);
       }
     }
+  };
+  for (int c = a.c_beg; c < a.c_end; c += 2) {
+    chunk_step(buf, buf2, c);
+    if (c + 1 < a.c_end) chunk_step(buf2, buf, c + 1);
   }
 
   // ---- final state of the sequence -----------------------------------------
@@ -548,21 +580,26 @@ __global__ __launch_bounds__(256, SSLA_GC_STATE_WAVES) void gla_chunk_state_kern
   segment_range(static_cast<int>((len + BT - 1) / BT), P, seg, c_beg, c_end);
   float dsum = 0.f;   // lane = key
 
-  const int64_t strk = static_cast<int64_t>(BT) * H * KD, strv = static_cast<int64_t>(BT) * H * V;
-  int64_t off = ((bos + static_cast<int64_t>(c_beg) * BT + row) * H + h) * KD + kq;
-  int64_t offv = ((bos + static_cast<int64_t>(c_beg) * BT + row) * H + h) * V + v0 + kq;
-  ChunkRegs buf;
-  if (c_beg < c_end)
-    load_chunk<false, GF32>(buf, nullptr, k, v, g, off, offv, row < len - static_cast<int64_t>(c_beg) * BT, kq, vw);
-  for (int c = c_beg; c < c_end; ++c) {
+  constexpr int gsz = GF32 ? 4 : 2;
+  SeqRsrc rs;
+  rs.k = seq_rsrc(k + bos * H * KD, len * H * KD * 2);
+  rs.g = seq_rsrc(static_cast<const char *>(g) + bos * H * KD * gsz, len * H * KD * gsz);
+  rs.v = seq_rsrc(v + bos * H * V, len * H * V * 2);
+  const uint32_t rowi = static_cast<uint32_t>((c_beg * BT + row) * H + h);
+  uint32_t oq = (rowi * KD + kq) * 2, og = (rowi * KD + kq) * gsz;
+  uint32_t ov = (rowi * V + v0 + kq) * 2;
+  const uint32_t sq = BT * H * KD * 2, sg = BT * H * KD * gsz, sv = BT * H * V * 2;
+  ChunkRegs buf, buf2;
+  load_chunk<false, GF32>(buf, rs, c_beg < c_end, oq, og, ov, kq, vw);
+  // the loop is unrolled by two over the two register sets (no copies)
+  auto chunk_step = [&](ChunkRegs &cur, ChunkRegs &nxt, const int c) __attribute__((always_inline)) {
     const int par = (c - c_beg) & 1;
-    const int64_t rem = len - static_cast<int64_t>(c) * BT;
-    const ChunkRegs cur = buf;
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    off += strk;
-    offv += strv;
-    if (c + 1 < c_end) load_chunk<false, GF32>(buf, nullptr, k, v, g, off, offv, row < rem - BT, kq, vw);
+    oq += sq;
+    og += sg;
+    ov += sv;
+    load_chunk<false, GF32>(nxt, rs, c + 1 < c_end, oq, og, ov, kq, vw);
     __builtin_amdgcn_sched_barrier(0);
     f32x8 gs[2];
     unpack_gates<DT, GF32>(cur, gs);
@@ -609,6 +646,10 @@ __global__ __launch_bounds__(256, SSLA_GC_STATE_WAVES) void gla_chunk_state_kern
     }
     // kh / vs / fac are rewritten after the next chunk's barrier 1, which
     // every wavefront reaches only after these reads
+  };
+  for (int c = c_beg; c < c_end; c += 2) {
+    chunk_step(buf, buf2, c);
+    if (c + 1 < c_end) chunk_step(buf2, buf, c + 1);
   }
 
   const int64_t slot = (static_cast<int64_t>(n) * H + h) * P + seg;
@@ -751,6 +792,11 @@ extern "C" int ssla_gla_chunk_fwd(const void *q, const void *k, const void *v, c
   }
   if (n_seq == 0) return SSLA_OK;
   SSLA_CHECK_ARG(cu_seqlens != nullptr, "gla_chunk_fwd: cu_seqlens is NULL");
+  // kernels address a sequence with 32-bit byte offsets
+  if (T * H * static_cast<int64_t>(std::max(K, V)) * 4 >= (int64_t{1} << 31)) {
+    set_error("gla_chunk_fwd: T * H * max(K, V) * 4 must stay below 2^31 bytes (T=%lld H=%d)", (long long)T, H);
+    return SSLA_ERR_UNSUPPORTED;
+  }
   SSLA_CHECK_ARG(T == 0 || (q && k && v && g && o), "gla_chunk_fwd: null tensor pointer");
   SSLA_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(g, 16) && aligned(v, 16) && aligned(o, 8),
                  "gla_chunk_fwd: q/k/g/v must be 16-byte and o 8-byte aligned");
