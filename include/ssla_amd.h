@@ -140,7 +140,7 @@ int ssla_sparse_gla_step(const int32_t *site_idx, int n_active,
  *
  * src: fp32 [E, C]; index: int64 [E], every value in [0, n_out) (checked on
  * the device: an out-of-range index makes the call's status word report
- * SSLA_ERR_ARG via ssla_scatter_check, the offending row is skipped).
+ * SSLA_ERR_ARG via ssla_scatter_check; the unsorted path skips the event).
  *
  * scatter_max: out[n, c] = max over {e : index[e] = n} of src[e, c];
  *   argmax[n, c] = the SMALLEST such e attaining the maximum (floating-point
@@ -153,6 +153,8 @@ int ssla_sparse_gla_step(const int32_t *site_idx, int n_active,
  *
  * `index_sorted` = 1 promises index is non-decreasing (the segment ids that
  * unique_consecutive produces); the kernels then skip the bucketing pass.
+ * A broken promise or an out-of-range value is reported through the status
+ * word (SSLA_ERR_ARG), and the sorted path's output is then unspecified.
  * Workspace: ssla_scatter_workspace_size(E, C, n_out) bytes (16-byte aligned,
  * no initialisation needed).  Any C >= 1; E below 2^31, n_out below 2^30.
  * Concurrent calls must use distinct workspaces.

@@ -169,8 +169,8 @@ void oracle_sparse_gla_step(const int32_t *site, int n_active, const float *q, c
  * semantics; called at reference layers/sparse_pooling.py:33): events are
  * visited in index order, a strictly greater value replaces the running
  * maximum, so among equal maxima (floating-point ==) the smallest event
- * index wins.  Empty rows: out = 0, argmax = E.  out gets src[argmax]'s
- * bits. */
+ * index wins; NaN never wins (a row whose values are all NaN counts as
+ * empty).  Empty rows: out = 0, argmax = E.  out gets src[argmax]'s bits. */
 void oracle_scatter_max(const float *src, const int64_t *index, int64_t E, int C, int64_t n_out,
                         float *out, int64_t *argmax) {
   for (int64_t i = 0; i < n_out * C; ++i) {
@@ -182,7 +182,8 @@ void oracle_scatter_max(const float *src, const int64_t *index, int64_t E, int C
     for (int c = 0; c < C; ++c) {
       const float x = src[e * C + c];
       int64_t *a = &argmax[r * C + c];
-      if (*a < 0 || x > src[*a * C + c]) *a = e;
+      /* NaN never wins; ties keep the smallest e (events come in order) */
+      if (x == x && (*a < 0 || x > src[*a * C + c])) *a = e;
     }
   }
   for (int64_t i = 0; i < n_out * C; ++i) {

@@ -57,6 +57,45 @@ def test_sorted_segments(dev):
     _check(dev, src, index, 1000, sorted_index=False)
 
 
+@pytest.mark.parametrize("C", [1, 3, 64, 65, 100, 300])
+def test_random_sorted(dev, C):
+    """Sorted (segment) path across channel blocks, with empty leading,
+    inner and trailing rows."""
+    gen = torch.Generator().manual_seed(100 + C)
+    E, n_out = 5000, 400
+    index = torch.sort(torch.randint(3, n_out - 20, (E,), generator=gen)).values
+    index = index[(index % 7) != 0]          # inner empty rows
+    src = torch.randn(index.numel(), C, generator=gen)
+    _check(dev, src, index, n_out, sorted_index=True)
+
+
+def test_sorted_rows_spanning_many_tiles(dev):
+    """Rows longer than 64 tiles (the fix-up reads 64 tile flags at a time),
+    rows ending exactly on tile boundaries, ties."""
+    gen = torch.Generator().manual_seed(7)
+    lens = [1, 63, 64, 128, 5000, 1, 64 * 70 + 3, 2, 129]
+    index = torch.cat([torch.full((n,), r * 3, dtype=torch.int64) for r, n in enumerate(lens)])
+    src = torch.randint(-2, 3, (index.numel(), 8), generator=gen).float()
+    _check(dev, src, index, 3 * len(lens) + 5, sorted_index=True)
+
+
+def test_sorted_special_values(dev):
+    """-inf ties (first index wins), NaN never wins (a row of only NaN is
+    treated as having no winner), signed zeros."""
+    index = torch.tensor([0, 0, 0, 1, 1, 2, 2, 2, 4])
+    src = torch.tensor([[-np.inf, 1.0], [-np.inf, 1.0], [-5.0, np.nan],
+                        [np.nan, -0.0], [np.nan, 0.0],
+                        [2.0, -np.inf], [np.nan, -np.inf], [2.0, 3.0],
+                        [0.0, -0.0]], dtype=torch.float32)
+    from ssla_amd.scatter import scatter_max
+    o_s, a_s = scatter_max(src.to(dev), index.to(dev), dim=0, dim_size=6, sorted_index=True)
+    o_u, a_u = scatter_max(src.to(dev), index.to(dev), dim=0, dim_size=6, sorted_index=False)
+    assert np.array_equal(o_s.cpu().numpy().view(np.uint32), o_u.cpu().numpy().view(np.uint32))
+    assert np.array_equal(a_s.cpu().numpy(), a_u.cpu().numpy())
+    ro, ra = oracle.scatter_max(src.numpy(), index.numpy(), 6)
+    assert np.array_equal(a_s.cpu().numpy(), ra)
+
+
 def test_many_rows_global_counting(dev):
     """More output rows than the LDS histogram holds (global-counter path),
     plus a row with several pieces."""

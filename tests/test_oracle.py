@@ -246,6 +246,18 @@ def test_scatter_max_vs_torch_and_brute_force(ties):
                 assert out[r, c] == m
 
 
+def test_scatter_max_nan_never_wins_and_neg_inf_ties():
+    """NaN never wins (all-NaN rows count as empty, as with an initial value
+    below every number); -inf is an ordinary value whose ties keep the
+    first event."""
+    nan, inf = np.nan, np.inf
+    src = np.array([[nan], [5.0], [nan], [nan], [-inf], [-inf], [2.0], [nan]], np.float32)
+    index = np.array([0, 0, 1, 1, 2, 2, 3, 3])
+    out, arg = oracle.scatter_max(src, index, 5)
+    assert arg[:, 0].tolist() == [1, 8, 4, 6, 8]
+    assert out[:, 0].tolist() == [5.0, 0.0, -inf, 2.0, 0.0]
+
+
 def test_scatter_max_signed_zero_takes_first_bits():
     src = np.array([[0.0], [-0.0], [-1.0]], np.float32)
     out, arg = oracle.scatter_max(src[[1, 0, 2]], np.array([0, 0, 0]), 1)
