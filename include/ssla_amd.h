@@ -294,6 +294,24 @@ int ssla_events_to_grid(const float *events, int64_t E, int C, const int64_t *le
                         const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w, int64_t G, int B,
                         int Hg, int Wg, float *grid, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Event ingestion: Prophesee .dat Event2D records -> the padded batch
+ * tensor (reference utils/io/dat_events_tools.py:15,40-47 record decode;
+ * model_base.py:82-117 pad_batches).
+ *
+ * records: device copy of n_records raw 8-byte records (uint32 t, int32 w:
+ * x = w & 16383, y = (w >> 14) & 16383, p = (w >> 28) & 1), 8-byte aligned.
+ * sample_start: device int64 [B + 1], non-decreasing, sample b's records are
+ * [sample_start[b], sample_start[b+1]) (rows outside [0, n_records) are
+ * treated as padding).  events: device float32 [B, max_len, 4], 16-byte
+ * aligned.  layout SSLA_EVENTS_XYTP (Gen1 / NCaltech101): rows (x, y, t,
+ * 2p - 1), padding rows (0, 0, 0, -1); SSLA_EVENTS_TXYP: rows (t, x, y, p),
+ * padding rows 0.  t is converted to float32 with round-to-nearest-even.
+ * ------------------------------------------------------------------------ */
+enum { SSLA_EVENTS_XYTP = 0, SSLA_EVENTS_TXYP = 1 };
+int ssla_dat_decode_batch(const void *records, int64_t n_records, const int64_t *sample_start, int B,
+                          int64_t max_len, int layout, float *events, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -243,3 +243,32 @@ def sparse_pool(rf, reduce="max"):
     new_len = np.bincount(field[head], minlength=lens.size) if lens.size else np.zeros(0, np.int64)
     new_len = new_len[new_len > 0]
     return {"events": out, "time": new_t, "lengths": new_len}
+
+
+# ------------------------------------------------------------- ingestion --
+def dat_decode(rec):
+    """utils/io/dat_events_tools.py:40-47: raw Event2D records (t u4, w i4)
+    -> dict of t, x, y, p arrays (x = w & 16383, y = (w & 268419072) >> 14,
+    p = (w & 268435456) >> 28)."""
+    rec = np.asarray(rec)
+    w = rec["_"].astype(np.int64)
+    return {"t": rec["t"].copy(), "x": w & 16383, "y": (w & 268419072) >> 14,
+            "p": (w & 268435456) >> 28}
+
+
+def pad_batches(samples, dataset="Gen1"):
+    """model_base.py:82-117 on decoded samples (dicts or structured arrays
+    with t, x, y, p): each sample stacked as float32 [t, x, y, p] rows
+    (numpy astype rounding), zero-padded to the longest, then for Gen1 /
+    NCaltech101 reordered to <x, y, t, p> with p -> 2p - 1 (padding rows
+    included).  Returns (events [B, L, 4] float32, lengths [B])."""
+    rows = [np.stack([np.asarray(s[f]).astype(np.float32) for f in ("t", "x", "y", "p")], axis=-1)
+            for s in samples]
+    lens = [len(r) for r in rows]
+    L = max(lens)
+    ev = np.stack([np.pad(r, ((0, L - n), (0, 0)), mode="constant", constant_values=0)
+                   for n, r in zip(lens, rows)], axis=0)
+    if dataset in ("Gen1", "NCaltech101"):
+        ev = ev[:, :, [1, 2, 0, 3]]
+        ev[:, :, -1] = ev[:, :, -1] * 2 - 1
+    return ev, np.asarray(lens, np.int64)

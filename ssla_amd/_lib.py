@@ -67,6 +67,7 @@ SIGNATURES = {
     "ssla_pixel_delays": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _sz, _vp]),
     "ssla_events_to_grid": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _sz,
                                    _vp]),
+    "ssla_dat_decode_batch": (_i32, [_vp, _i64, _vp, _i32, _i64, _i32, _vp, _vp]),
 }
 
 _lock = threading.Lock()
