@@ -119,6 +119,16 @@ int ssla_diag_scan_fwd(const float *u, const float *g,
                        const int64_t *cu_seqlens, int n_seq, int64_t T,
                        int C, float *h, void *stream);
 
+/* Its backward, given the forward's h and the output gradient dout:
+ *   dh_t = dout_t + g_{t+1} dh_{t+1} (0 past the sequence end),
+ *   du_t = dh_t,  dg_t = dh_t h_{t-1} (h_{bos-1} = 0);
+ * du, dg: fp32 [T, C], rows outside every sequence written with zeros.
+ * Replaces SequentialScan.backward / sequential_scan_bwd (reference
+ * ops/common/scan.py:116-137, :55-86). */
+int ssla_diag_scan_bwd(const float *dout, const float *g, const float *h,
+                       const int64_t *cu_seqlens, int n_seq, int64_t T,
+                       int C, float *du, float *dg, void *stream);
+
 /* One time bin of the per-site matrix-state GLA update.  For active site
  * i (site = site_idx[i], sorted ascending, unique, < n_sites):
  *   S[site] <- diag(exp(g_i)) S[site] + k_i v_i^T ;  o_i = (scale q_i)^T S[site]

@@ -57,11 +57,12 @@ def load():
         lib.oracle_gla_chunk.argtypes = [_f32, _f32, _f32, _f32, _i64, ci, ci, ci, ci, cd,
                                          _Opt(_f32), ci, _f64, _Opt(_f64)]
         lib.oracle_diag_scan.argtypes = [_f32, _f32, _i64, ci, c64, ci, _f64]
+        lib.oracle_diag_scan_bwd.argtypes = [_f32, _f32, _f32, _i64, ci, c64, ci, _f64, _f64]
         lib.oracle_sparse_gla_step.argtypes = [_i32, ci, _f32, _f32, _f32, _f32, _f32, ci, ci, ci,
                                                cd, _f64]
         lib.oracle_scatter_max.argtypes = [_f32, _i64, c64, ci, c64, _f32, _i64]
         lib.oracle_scatter_mean.argtypes = [_f32, _i64, c64, ci, c64, _f64]
-        for fn in (lib.oracle_gla_recurrent, lib.oracle_gla_chunk, lib.oracle_diag_scan,
+        for fn in (lib.oracle_gla_recurrent, lib.oracle_gla_chunk, lib.oracle_diag_scan, lib.oracle_diag_scan_bwd,
                    lib.oracle_sparse_gla_step, lib.oracle_scatter_max, lib.oracle_scatter_mean):
             fn.restype = None
         _lib = lib
@@ -139,6 +140,18 @@ def diag_scan(u, g, cu_seqlens):
     h = np.zeros((T, C_), np.float64)
     load().oracle_diag_scan(u, g, cu, cu.size - 1, T, C_, h)
     return h
+
+
+def diag_scan_bwd(u, g, dout, cu_seqlens):
+    """sequential_scan_bwd (reference ops/common/scan.py:55-86) in fp64:
+    (du, dg) for the output gradient dout."""
+    u, g, dout = _f(u), _f(g), _f(dout)
+    T, C_ = u.shape
+    cu = np.ascontiguousarray(cu_seqlens, dtype=np.int64)
+    du = np.zeros((T, C_), np.float64)
+    dg = np.zeros((T, C_), np.float64)
+    load().oracle_diag_scan_bwd(u, g, dout, cu, cu.size - 1, T, C_, du, dg)
+    return du, dg
 
 
 def sparse_gla_step(site_idx, q, k, v, g, state, scale=None):

@@ -137,6 +137,36 @@ void oracle_diag_scan(const float *u, const float *g, const int64_t *cu, int n_s
   }
 }
 
+/* sequential_scan_bwd (reference ops/common/scan.py:55-86): per sequence
+ * and channel, t from eos-1 down to bos: dh += do_t; du_t = dh;
+ * dg_t = dh * h_{t-1} (0 at bos); dh *= g_t.  h is the forward output
+ * (recomputed here in fp64 from u, g).  Rows outside all sequences stay 0. */
+void oracle_diag_scan_bwd(const float *u, const float *g, const float *dout, const int64_t *cu, int n_seq,
+                          int64_t T, int C, double *du, double *dg) {
+  memset(du, 0, sizeof(double) * (size_t)T * C);
+  memset(dg, 0, sizeof(double) * (size_t)T * C);
+#pragma omp parallel for schedule(dynamic)
+  for (int n = 0; n < n_seq; ++n) {
+    const int64_t bos = cu[n], eos = cu[n + 1];
+    double *h = (double *)malloc(sizeof(double) * (size_t)(eos > bos ? eos - bos : 1));
+    for (int c = 0; c < C; ++c) {
+      double s = 0.0;
+      for (int64_t t = bos; t < eos; ++t) {
+        s = s * (double)g[t * C + c] + (double)u[t * C + c];
+        h[t - bos] = s;
+      }
+      double dh = 0.0;
+      for (int64_t t = eos - 1; t >= bos; --t) {
+        dh += (double)dout[t * C + c];
+        du[t * C + c] = dh;
+        dg[t * C + c] = dh * (t > bos ? h[t - 1 - bos] : 0.0);
+        dh *= (double)g[t * C + c];
+      }
+    }
+    free(h);
+  }
+}
+
 /* One bin of the per-site state update (naive_gla_recurrent on a length-1
  * sequence per active site, initial state = stored fp32 state, final state
  * stored back as fp32).  Inactive rows of `state` are not touched. */

@@ -37,6 +37,7 @@ SIGNATURES = {
     "ssla_gla_recurrent_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32,
                                       _f32, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "ssla_diag_scan_fwd": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _vp, _vp]),
+    "ssla_diag_scan_bwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _vp, _vp, _vp]),
     "ssla_sparse_gla_step": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                     _f32, _vp, _vp]),
     "ssla_scatter_workspace_size": (_sz, [_i64, _i32, _i64]),

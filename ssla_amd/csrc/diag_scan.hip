@@ -4,7 +4,7 @@
 // (reference ops/common/scan.py:20-43, :90-114): the state is fp32, restarts
 // at every sequence start, and rows that belong to no sequence are zero.
 //
-// Layout: u, g, h are fp32 [T, C].  A wavefront handles `slots` sequences at
+// Layout: u, g, h (and do, du, dg of the backward) are fp32 [T, C].  A wavefront handles `slots` sequences at
 // once when C is small (lanes = slot x channel), or one 64-channel slice of
 // one sequence when C > 64.  Each step's loads do not depend on the state,
 // so the loop prefetches kUnroll steps ahead; only the fma chain is serial.
@@ -55,6 +55,56 @@ __global__ __launch_bounds__(256) void diag_scan_kernel(
   }
 }
 
+// Backward (sequential_scan_bwd, reference ops/common/scan.py:55-86): per
+// sequence and channel, walking t down from eos - 1 to bos with dh = 0:
+//   dh += do_t;  du_t = dh;  dg_t = dh * h_{t-1} (h_{bos-1} = 0);  dh *= g_t.
+// The next step's "dh * g_t + do_{t-1}" is one fma.  Same wavefront layout
+// and prefetch as the forward, in reverse.
+__global__ __launch_bounds__(256) void diag_scan_bwd_kernel(
+    const float *__restrict__ dout, const float *__restrict__ g, const float *__restrict__ h,
+    const int64_t *__restrict__ cu_seqlens, int n_seq, int64_t T, int C, int cw, int n_cblk,
+    int64_t n_items, float *__restrict__ du, float *__restrict__ dg) {
+  const int lane = threadIdx.x & 63;
+  const int slots = 64 / cw;
+  const int slot = lane / cw;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t item = wave * slots + slot;
+  if (item >= n_items) return;
+  const int n = static_cast<int>(item / n_cblk);
+  const int c = static_cast<int>(item % n_cblk) * cw + (lane % cw);
+  if (c >= C) return;
+  const int64_t bos = min(max(cu_seqlens[n], (int64_t)0), T);
+  const int64_t eos = min(max(cu_seqlens[n + 1], bos), T);
+
+  float dh = 0.f, gn = 0.f;   // gn: g of the step after the current one
+  int64_t t = eos;
+  for (; t - kUnroll >= bos; t -= kUnroll) {
+    float dd[kUnroll], gg[kUnroll], hp[kUnroll];
+#pragma unroll
+    for (int i = 0; i < kUnroll; ++i) {
+      const int64_t s = t - 1 - i;
+      dd[i] = dout[s * C + c];
+      gg[i] = g[s * C + c];
+      hp[i] = s > bos ? h[(s - 1) * C + c] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kUnroll; ++i) {
+      const int64_t s = t - 1 - i;
+      dh = fmaf(dh, gn, dd[i]);
+      du[s * C + c] = dh;
+      dg[s * C + c] = dh * hp[i];
+      gn = gg[i];
+    }
+  }
+  for (; t > bos; --t) {
+    const int64_t s = t - 1;
+    dh = fmaf(dh, gn, dout[s * C + c]);
+    du[s * C + c] = dh;
+    dg[s * C + c] = dh * (s > bos ? h[(s - 1) * C + c] : 0.f);
+    gn = g[s * C + c];
+  }
+}
+
 // Zero the rows before cu_seqlens[0] and from cu_seqlens[n_seq] on (all rows
 // when n_seq == 0).  A kernel rather than hipMemsetAsync so that the call can
 // be captured into a HIP graph.
@@ -75,6 +125,38 @@ __global__ __launch_bounds__(256) void diag_scan_zero_tail(
 
 }  // namespace
 }  // namespace ssla
+
+extern "C" int ssla_diag_scan_bwd(const float *dout, const float *g, const float *h, const int64_t *cu_seqlens,
+                                  int n_seq, int64_t T, int C, float *du, float *dg, void *stream) {
+  using namespace ssla;
+  clear_error();
+  SSLA_CHECK_ARG(n_seq >= 0 && T >= 0 && C > 0, "diag_scan_bwd: bad sizes n_seq=%d T=%lld C=%d",
+                 n_seq, (long long)T, C);
+  if (T == 0) return SSLA_OK;
+  SSLA_CHECK_ARG(dout && g && h && du && dg, "diag_scan_bwd: null tensor pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n_seq > 0) {
+    SSLA_CHECK_ARG(cu_seqlens != nullptr, "diag_scan_bwd: cu_seqlens is NULL");
+    int cw = 64;
+    if (C <= 32) {
+      cw = 1;
+      while (cw < C) cw <<= 1;
+    }
+    const int n_cblk = (C + cw - 1) / cw;
+    const int64_t n_items = static_cast<int64_t>(n_seq) * n_cblk;
+    const int64_t blocks = ((n_items + 64 / cw - 1) / (64 / cw) + 3) / 4;
+    if (blocks > 0x7fffffff) {
+      set_error("diag_scan_bwd: too many sequences");
+      return SSLA_ERR_UNSUPPORTED;
+    }
+    hipLaunchKernelGGL(diag_scan_bwd_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, dout, g, h,
+                       cu_seqlens, n_seq, T, C, cw, n_cblk, n_items, du, dg);
+  }
+  // rows in no sequence: zero gradients (the reference's zeros_like)
+  hipLaunchKernelGGL(diag_scan_zero_tail, dim3(64), dim3(256), 0, st, cu_seqlens, n_seq, T, C, du);
+  hipLaunchKernelGGL(diag_scan_zero_tail, dim3(64), dim3(256), 0, st, cu_seqlens, n_seq, T, C, dg);
+  return launch_status("diag_scan_bwd");
+}
 
 extern "C" int ssla_diag_scan_fwd(const float *u, const float *g, const int64_t *cu_seqlens,
                                   int n_seq, int64_t T, int C, float *h, void *stream) {

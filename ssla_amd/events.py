@@ -35,7 +35,7 @@ __all__ = [
     "group_events", "compute_rf2pixels", "get_patch2pixel_lut", "gather_receptive_fields",
     "scatter_group_events_to_patch", "gather_patch_events_to_group", "truncate_packed_sequence",
     "temporal_dropout_index", "pool_segments", "events_to_grid", "preprocess_inputs", "gather_rows",
-    "sort_pairs", "expand_segments",
+    "sort_pairs", "expand_segments", "GatherRows", "IndexAddRows",
 ]
 
 
@@ -141,17 +141,65 @@ def _rf_scatter(inputs, frame_size, lut):
     return src, tim, pos, f_index, f_len, n_rf
 
 
-def gather_rows(src: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
-    """out[j] = src[idx[j]] for a 2-D fp32 src (the HIP row gather)."""
-    src = src.to(torch.float32).contiguous()
-    idx = _i64(idx)
-    _lib.require_cuda(src, idx)
+def _gather_rows(src: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
     C = src.shape[1] if src.dim() == 2 else 1
     out = torch.empty(idx.numel(), C, dtype=torch.float32, device=src.device)
     if idx.numel():
         _lib.check(_lib.load().ssla_gather_rows(_lib.ptr(src), src.shape[0], _lib.ptr(idx), idx.numel(), C,
                                                 _lib.ptr(out), _lib.stream_of(src)), "gather_rows")
     return out
+
+
+def _index_add_rows(src: torch.Tensor, idx: torch.Tensor, n_out: int) -> torch.Tensor:
+    n, C = src.shape
+    lib = _lib.load()
+    ws = _ws(lib.ssla_index_add_rows_workspace_size(n), src.device)
+    out = torch.empty(int(n_out), C, dtype=torch.float32, device=src.device)
+    _lib.check(lib.ssla_index_add_rows(_lib.ptr(src), _lib.ptr(idx), n, C, int(n_out), _lib.ptr(out),
+                                       _lib.ptr(ws), ws.numel(), _lib.stream_of(src)), "index_add_rows")
+    return out
+
+
+class GatherRows(torch.autograd.Function):
+    """out = src[idx]; its backward sums the output gradient rows back into
+    the source rows (the index_add kernel: ordered, deterministic)."""
+
+    @staticmethod
+    def forward(ctx, src, idx):
+        ctx.save_for_backward(idx)
+        ctx.n_src = src.shape[0]
+        return _gather_rows(src, idx)
+
+    @staticmethod
+    def backward(ctx, dout):
+        (idx,) = ctx.saved_tensors
+        return _index_add_rows(dout.to(torch.float32).contiguous(), idx, ctx.n_src), None
+
+
+class IndexAddRows(torch.autograd.Function):
+    """out[r] = sum of src rows i with idx[i] == r; its backward gathers the
+    output gradient rows (d src[i] = d out[idx[i]])."""
+
+    @staticmethod
+    def forward(ctx, src, idx, n_out):
+        ctx.save_for_backward(idx)
+        return _index_add_rows(src, idx, n_out)
+
+    @staticmethod
+    def backward(ctx, dout):
+        (idx,) = ctx.saved_tensors
+        return _gather_rows(dout.to(torch.float32).contiguous(), idx), None, None
+
+
+def gather_rows(src: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """out[j] = src[idx[j]] for a 2-D fp32 src (the HIP row gather);
+    differentiable in src."""
+    src = src.to(torch.float32).contiguous()
+    idx = _i64(idx)
+    _lib.require_cuda(src, idx)
+    if torch.is_grad_enabled() and src.requires_grad:
+        return GatherRows.apply(src, idx)
+    return _gather_rows(src, idx)
 
 
 def gather_receptive_fields(inputs, frame_size, rf2pixel_lut, rf_outcoord) -> Dict[str, torch.Tensor]:
@@ -182,15 +230,10 @@ def gather_patch_events_to_group(patch_events: torch.Tensor, patch_event_to_pixe
     order from zero in fp32, as index_add_ does on the CPU."""
     pe = patch_events.to(torch.float32).contiguous()
     idx = _i64(patch_event_to_pixel_event_idx)
-    dev = _lib.require_cuda(pe, idx)
-    n, C = pe.shape
-    lib = _lib.load()
-    ws = _ws(lib.ssla_index_add_rows_workspace_size(n), dev)
-    out = torch.empty(int(num_pixel_events), C, dtype=torch.float32, device=dev)
-    st = _lib.stream_of(pe)
-    _lib.check(lib.ssla_index_add_rows(_lib.ptr(pe), _lib.ptr(idx), n, C, int(num_pixel_events), _lib.ptr(out),
-                                       _lib.ptr(ws), ws.numel(), st), "index_add_rows")
-    return out
+    _lib.require_cuda(pe, idx)
+    if torch.is_grad_enabled() and pe.requires_grad:
+        return IndexAddRows.apply(pe, idx, int(num_pixel_events))
+    return _index_add_rows(pe, idx, int(num_pixel_events))
 
 
 # ---------------------------------------------------------------- sequences --

@@ -2,7 +2,8 @@
 
 * :func:`scan` -- drop-in for ``ops.common.scan.scan(u, g, cu_seqlens)``
   (reference ops/common/scan.py:140-163): varlen diagonal gated scan
-  ``h_t = g_t * h_{t-1} + u_t`` with a zero state at each sequence start.
+  ``h_t = g_t * h_{t-1} + u_t`` with a zero state at each sequence start,
+  with its backward (:class:`SequentialScan`).
 * :func:`sparse_gla_step` -- one time bin of the per-site matrix-state GLA
   update at active sites only (no reference function; its math is
   ``naive_gla_recurrent``, reference ops/gla/naive.py:50-111, on a length-1
@@ -20,26 +21,54 @@ import torch
 from . import _lib
 from .gla import _recurrent
 
-__all__ = ["scan", "sparse_gla_step", "sparse_gla_scan"]
+__all__ = ["scan", "SequentialScan", "sparse_gla_step", "sparse_gla_scan"]
+
+
+def _scan_fwd(u: torch.Tensor, g: torch.Tensor, cu: torch.Tensor) -> torch.Tensor:
+    T, C = u.shape
+    h = torch.empty_like(u)
+    st = _lib.load().ssla_diag_scan_fwd(_lib.ptr(u), _lib.ptr(g), _lib.ptr(cu), cu.numel() - 1, T, C,
+                                        _lib.ptr(h), _lib.stream_of(u))
+    _lib.check(st, "ssla_diag_scan_fwd")
+    return h
+
+
+class SequentialScan(torch.autograd.Function):
+    """Forward and backward of the varlen diagonal scan (reference
+    ops/common/scan.py:89-137): saves g and h, and the backward kernel
+    returns (du, dg) with zeros on rows in no sequence."""
+
+    @staticmethod
+    def forward(ctx, u, g, cu_seqlens):
+        h = _scan_fwd(u, g, cu_seqlens)
+        ctx.save_for_backward(g, h, cu_seqlens)
+        return h
+
+    @staticmethod
+    def backward(ctx, dout):
+        g, h, cu = ctx.saved_tensors
+        dout = dout.to(torch.float32).contiguous()
+        T, C = h.shape
+        du, dg = torch.empty_like(h), torch.empty_like(h)
+        st = _lib.load().ssla_diag_scan_bwd(_lib.ptr(dout), _lib.ptr(g), _lib.ptr(h), _lib.ptr(cu), cu.numel() - 1,
+                                            T, C, _lib.ptr(du), _lib.ptr(dg), _lib.stream_of(h))
+        _lib.check(st, "ssla_diag_scan_bwd")
+        return du, dg, None
 
 
 def scan(u: torch.Tensor, g: torch.Tensor, cu_seqlens: torch.Tensor) -> torch.Tensor:
     """Varlen diagonal scan; u, g fp32 ``[T, C]`` -> h ``[T, C]`` (rows in no
-    sequence are zero, as with the reference's ``zeros_like``)."""
+    sequence are zero, as with the reference's ``zeros_like``).  Differentiable
+    in u and g (``ssla_diag_scan_bwd``)."""
     if u.dim() != 2 or u.shape != g.shape:
         raise ValueError(f"scan: u and g must both be [T, C], got {tuple(u.shape)}, {tuple(g.shape)}")
     dev = _lib.require_cuda(u, g)
-    _lib.require_no_grad("scan", u, g)
     u = u.to(torch.float32).contiguous()
     g = g.to(torch.float32).contiguous()
     cu = cu_seqlens.to(device=dev, dtype=torch.int64).contiguous()
-    T, C = u.shape
-    h = torch.empty_like(u)
-    lib = _lib.load()
-    st = lib.ssla_diag_scan_fwd(_lib.ptr(u), _lib.ptr(g), _lib.ptr(cu), cu.numel() - 1, T, C,
-                                _lib.ptr(h), _lib.stream_of(u))
-    _lib.check(st, "ssla_diag_scan_fwd")
-    return h
+    if torch.is_grad_enabled() and (u.requires_grad or g.requires_grad):
+        return SequentialScan.apply(u, g, cu)
+    return _scan_fwd(u, g, cu)
 
 
 def sparse_gla_step(site_idx: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

@@ -14,6 +14,8 @@ o from the previous state) fails:
   test_planted_mistakes_are_caught shows mutated recurrences fail these.
 * diag_scan: geometric closed form for constant gates, brute-force
   products, and equality with gla_recurrent at K = V = 1.
+* diag_scan_bwd: torch autograd (fp64) through a loop of the forward,
+  suffix-sum closed form for unit gates, central differences.
 * sparse_gla_step: equality with gla_recurrent on length-1 sequences with
   initial_state = the stored state; inactive rows untouched byte for byte.
 * scatter_max / scatter_mean: torch.scatter_reduce('amax'/'mean',
@@ -200,6 +202,69 @@ def test_scan_is_gla_with_unit_keys():
     ones = np.ones((T, C, 1), np.float32)
     o, _ = oracle.gla_recurrent(ones, ones, u[:, :, None], np.log(g)[:, :, None], cu, 1.0)
     assert np.allclose(h, o[:, :, 0], rtol=1e-6, atol=1e-7)
+
+
+def _scan_autograd(u, g, cu, dout):
+    """(du, dg) by torch autograd (float64, CPU) through a plain loop of the
+    forward recurrence: an independent derivation of the backward."""
+    U = torch.tensor(u, dtype=torch.float64, requires_grad=True)
+    G = torch.tensor(g, dtype=torch.float64, requires_grad=True)
+    rows = [torch.zeros(u.shape[1], dtype=torch.float64) for _ in range(u.shape[0])]
+    for s, e in zip(cu[:-1], cu[1:]):
+        hprev = torch.zeros(u.shape[1], dtype=torch.float64)
+        for t in range(int(s), int(e)):
+            hprev = hprev * G[t] + U[t]
+            rows[t] = hprev
+    (torch.stack(rows) * torch.tensor(dout, dtype=torch.float64)).sum().backward()
+    return U.grad.numpy(), G.grad.numpy()
+
+
+def test_scan_bwd_matches_autograd():
+    rng = np.random.default_rng(21)
+    T, C = 37, 6
+    u, dout = _rand(rng, T, C), _rand(rng, T, C)
+    g = (1 / (1 + np.exp(-_rand(rng, T, C)))).astype(np.float32)
+    cu = np.array([3, 10, 10, 31])   # leading / trailing rows in no sequence, an empty sequence
+    du, dg = oracle.diag_scan_bwd(u, g, dout, cu)
+    rdu, rdg = _scan_autograd(u, g, cu, dout)
+    assert np.allclose(du, rdu, rtol=1e-12, atol=1e-12) and np.allclose(dg, rdg, rtol=1e-12, atol=1e-12)
+    assert (du[:3] == 0).all() and (dg[31:] == 0).all()
+
+
+def test_scan_bwd_unit_gate_closed_form_and_finite_differences():
+    rng = np.random.default_rng(22)
+    T, C = 20, 3
+    u, dout = _rand(rng, T, C), _rand(rng, T, C)
+    ones = np.ones((T, C), np.float32)
+    du, dg = oracle.diag_scan_bwd(u, ones, dout, [0, T])
+    suffix = np.cumsum(dout[::-1].astype(np.float64), axis=0)[::-1]   # g = 1: du_t = sum_{s>=t} do_s
+    assert np.allclose(du, suffix, rtol=1e-12)
+    h = np.cumsum(u.astype(np.float64), axis=0)
+    assert np.allclose(dg[1:], suffix[1:] * h[:-1], rtol=1e-12) and (dg[0] == 0).all()
+    # central differences of the fp64 forward along a random direction
+    g = (0.5 + 0.4 * np.tanh(_rand(rng, T, C))).astype(np.float32)
+    du, dg = oracle.diag_scan_bwd(u, g, dout, [0, T])
+    dirg = _rand(rng, T, C).astype(np.float64)
+    eps = 1e-3
+    def loss(gg):
+        return float((oracle.diag_scan(u, gg.astype(np.float32), [0, T]) * dout).sum())
+    # the forward rounds g to fp32: use a direction exactly representable after scaling
+    gp, gm = g.astype(np.float64) + eps * dirg, g.astype(np.float64) - eps * dirg
+    fd = (loss(gp) - loss(gm)) / (2 * eps)
+    assert abs(fd - float((dg * dirg).sum())) < 1e-3 * (1 + abs(fd))
+
+
+def test_scan_bwd_planted_mistake_is_caught():
+    """dg from h_t instead of h_{t-1} (an off-by-one) fails the autograd check."""
+    rng = np.random.default_rng(23)
+    T, C = 15, 2
+    u, dout = _rand(rng, T, C), _rand(rng, T, C)
+    g = (1 / (1 + np.exp(-_rand(rng, T, C)))).astype(np.float32)
+    h = oracle.diag_scan(u, g, [0, T])
+    du, _ = oracle.diag_scan_bwd(u, g, dout, [0, T])
+    wrong_dg = du * h
+    _, rdg = _scan_autograd(u, g, np.array([0, T]), dout)
+    assert not np.allclose(wrong_dg, rdg, rtol=1e-3, atol=1e-3)
 
 
 # --------------------------------------------------------- sparse step ----
