@@ -84,6 +84,26 @@ int ssla_gla_chunk_fwd(const void *q, const void *k, const void *v,
                        const float *h0, void *o, float *ht, int dtype,
                        void *workspace, size_t workspace_bytes, void *stream);
 
+/* Backward of ssla_gla_chunk_fwd: ChunkGLAFunction.backward /
+ * chunk_gla_bwd (reference ops/gla/chunk.py:1096-1116, 963-1053, with
+ * chunk_bwd_dh, ops/common/chunk_h.py:145-239).  dout [T, H, V] (dtype of
+ * v), dht [N, H, K, V] fp32 or NULL (no final-state gradient), h0 as in the
+ * forward (NULL = zero).  Writes dq, dk [T, H, K] and dv [T, H, V] in the
+ * input dtype, dg [T, H, K] in g's dtype, dh0 [N, H, K, V] fp32 (skipped when
+ * NULL).  Rows outside [cu_seqlens[0], cu_seqlens[n_seq]) are not written.
+ * Supported: dtype BF16 or F16, K == 64, V a multiple of 16 up to 64.
+ * Workspace: ssla_gla_chunk_bwd_workspace_size bytes (16-byte aligned, no
+ * initialisation needed): chunk offsets and two fp32 states per chunk
+ * (every chunk's entering state and leaving-state gradient). */
+size_t ssla_gla_chunk_bwd_workspace_size(int n_seq, int64_t T, int H, int K, int V);
+int ssla_gla_chunk_bwd(const void *q, const void *k, const void *v,
+                       const void *g, int g_dtype,
+                       const int64_t *cu_seqlens, int n_seq, int64_t T,
+                       int H, int K, int V, float scale, const float *h0,
+                       const void *dout, const float *dht, void *dq, void *dk,
+                       void *dv, void *dg, float *dh0, int dtype,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
 /* Fused recurrent forward (state in registers, serial over t).  Same math
  * and signature as naive_gla_recurrent (reference ops/gla/naive.py:50-111).
  * Supported: dtype F32/BF16/F16, K <= 256, V <= 256.

@@ -54,6 +54,9 @@ def load():
         ci, cd, c64 = C.c_int, C.c_double, C.c_int64
         lib.oracle_gla_recurrent.argtypes = [_f32, _f32, _f32, _f32, _i64, ci, ci, ci, ci, cd,
                                              _Opt(_f32), _f64, _Opt(_f64)]
+        lib.oracle_gla_recurrent_bwd.argtypes = [_f32, _f32, _f32, _f32, _i64, ci, ci, ci, ci, cd,
+                                                 _Opt(_f32), _f32, _Opt(_f32), _f64, _f64, _f64, _f64,
+                                                 _Opt(_f64)]
         lib.oracle_gla_chunk.argtypes = [_f32, _f32, _f32, _f32, _i64, ci, ci, ci, ci, cd,
                                          _Opt(_f32), ci, _f64, _Opt(_f64)]
         lib.oracle_diag_scan.argtypes = [_f32, _f32, _i64, ci, c64, ci, _f64]
@@ -62,7 +65,7 @@ def load():
                                                cd, _f64]
         lib.oracle_scatter_max.argtypes = [_f32, _i64, c64, ci, c64, _f32, _i64]
         lib.oracle_scatter_mean.argtypes = [_f32, _i64, c64, ci, c64, _f64]
-        for fn in (lib.oracle_gla_recurrent, lib.oracle_gla_chunk, lib.oracle_diag_scan, lib.oracle_diag_scan_bwd,
+        for fn in (lib.oracle_gla_recurrent, lib.oracle_gla_recurrent_bwd, lib.oracle_gla_chunk, lib.oracle_diag_scan, lib.oracle_diag_scan_bwd,
                    lib.oracle_sparse_gla_step, lib.oracle_scatter_max, lib.oracle_scatter_mean):
             fn.restype = None
         _lib = lib
@@ -89,6 +92,25 @@ def gla_recurrent(q, k, v, g, cu_seqlens, scale=None, initial_state=None, output
     ht = np.zeros((N, H, K, V), np.float64) if output_final_state else None
     load().oracle_gla_recurrent(q, k, v, g, cu, N, H, K, V, float(scale), h0, o, ht)
     return o, ht
+
+
+def gla_recurrent_bwd(q, k, v, g, cu_seqlens, do, scale=None, initial_state=None, dht=None):
+    """Gradients (dq, dk, dv, dg, dh0) of naive_gla_recurrent (o and the
+    final state) for output gradients do [T, H, V] and dht [N, H, K, V] (or
+    None), fp64; dh0 is None without an initial state."""
+    q, k, v, g, do = _f(q), _f(k), _f(v), _f(g), _f(do)
+    T, H, K = q.shape
+    V = v.shape[-1]
+    cu = np.ascontiguousarray(cu_seqlens, dtype=np.int64)
+    N = cu.size - 1
+    scale = K ** -0.5 if scale is None else float(scale)
+    h0 = None if initial_state is None else _f(initial_state)
+    dht = None if dht is None else _f(dht)
+    dq, dk, dg = (np.zeros((T, H, K)) for _ in range(3))
+    dv = np.zeros((T, H, V))
+    dh0 = np.zeros((N, H, K, V)) if h0 is not None else None
+    load().oracle_gla_recurrent_bwd(q, k, v, g, cu, N, H, K, V, scale, h0, do, dht, dq, dk, dv, dg, dh0)
+    return dq, dk, dv, dg, dh0
 
 
 def gla_chunk(q, k, v, g, cu_seqlens, scale=None, initial_state=None, output_final_state=True,

@@ -50,6 +50,88 @@ void oracle_gla_recurrent(const float *q, const float *k, const float *v, const 
   }
 }
 
+/* Backward of naive_gla_recurrent (the gradients that ChunkGLAFunction.
+ * backward returns, reference ops/gla/chunk.py:1096-1116), fp64: with dS the
+ * gradient of the state, walking t down from eos-1 (dS = dht, or 0):
+ *   dS += scale q_t do_t^T;  dq_t = scale S_t do_t;  dk_t = dS v_t;
+ *   dv_t = dS^T k_t;  dg_t[k] = e^{g_t[k]} sum_v dS[k,v] S_{t-1}[k,v];
+ *   dS = diag(e^{g_t}) dS;   and dh0 = dS at the end.
+ * States come from a forward pass with a checkpoint every 64 steps; each
+ * block of 64 is recomputed forward before its reverse walk.  dh0 / dht may
+ * be NULL.  Rows outside all sequences are left untouched. */
+void oracle_gla_recurrent_bwd(const float *q, const float *k, const float *v, const float *g,
+                              const int64_t *cu, int n_seq, int H, int K, int V, double scale,
+                              const float *h0, const float *dout, const float *dht, double *dq,
+                              double *dk, double *dv, double *dg, double *dh0) {
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int n = 0; n < n_seq; ++n) {
+    for (int h = 0; h < H; ++h) {
+      const int64_t bos = cu[n], eos = cu[n + 1], L = eos - bos;
+      const int64_t nb = (L + 63) / 64;
+      const size_t KV = (size_t)K * V;
+      double *ck = (double *)malloc(sizeof(double) * KV * (size_t)(nb + 1));   /* state before each block */
+      double *blk = (double *)malloc(sizeof(double) * KV * 65);                /* states of one block */
+      double *dS = (double *)malloc(sizeof(double) * KV);
+      double *S = (double *)malloc(sizeof(double) * KV);
+      for (size_t i = 0; i < KV; ++i) S[i] = h0 ? (double)h0[((int64_t)n * H + h) * KV + i] : 0.0;
+      for (int64_t b = 0; b < nb; ++b) {
+        memcpy(ck + KV * b, S, sizeof(double) * KV);
+        for (int64_t t = bos + 64 * b; t < bos + 64 * b + 64 && t < eos; ++t)
+          for (int kk = 0; kk < K; ++kk) {
+            const double d = exp((double)g[IDX3(t, h, kk, H, K)]), kv = (double)k[IDX3(t, h, kk, H, K)];
+            for (int vv = 0; vv < V; ++vv)
+              S[kk * V + vv] = d * S[kk * V + vv] + kv * (double)v[IDX3(t, h, vv, H, V)];
+          }
+      }
+      for (size_t i = 0; i < KV; ++i) dS[i] = dht ? (double)dht[((int64_t)n * H + h) * KV + i] : 0.0;
+      for (int64_t b = nb - 1; b >= 0; --b) {
+        const int64_t t0 = bos + 64 * b, t1 = (t0 + 64 < eos) ? t0 + 64 : eos;
+        memcpy(blk, ck + KV * b, sizeof(double) * KV);   /* blk[j] = state after row t0 + j - 1 */
+        for (int64_t t = t0; t < t1; ++t) {
+          double *P = blk + KV * (t - t0), *Q = P + KV;
+          for (int kk = 0; kk < K; ++kk) {
+            const double d = exp((double)g[IDX3(t, h, kk, H, K)]), kv = (double)k[IDX3(t, h, kk, H, K)];
+            for (int vv = 0; vv < V; ++vv) Q[kk * V + vv] = d * P[kk * V + vv] + kv * (double)v[IDX3(t, h, vv, H, V)];
+          }
+        }
+        for (int64_t t = t1 - 1; t >= t0; --t) {
+          const double *St = blk + KV * (t - t0 + 1), *Sp = blk + KV * (t - t0);
+          for (int kk = 0; kk < K; ++kk) {
+            const double qs = (double)q[IDX3(t, h, kk, H, K)] * scale;
+            for (int vv = 0; vv < V; ++vv) dS[kk * V + vv] += qs * (double)dout[IDX3(t, h, vv, H, V)];
+          }
+          for (int kk = 0; kk < K; ++kk) {
+            double aq = 0.0, ak = 0.0, ag = 0.0;
+            for (int vv = 0; vv < V; ++vv) {
+              aq += St[kk * V + vv] * (double)dout[IDX3(t, h, vv, H, V)];
+              ak += dS[kk * V + vv] * (double)v[IDX3(t, h, vv, H, V)];
+              ag += dS[kk * V + vv] * Sp[kk * V + vv];
+            }
+            dq[IDX3(t, h, kk, H, K)] = scale * aq;
+            dk[IDX3(t, h, kk, H, K)] = ak;
+            dg[IDX3(t, h, kk, H, K)] = exp((double)g[IDX3(t, h, kk, H, K)]) * ag;
+          }
+          for (int vv = 0; vv < V; ++vv) {
+            double a = 0.0;
+            for (int kk = 0; kk < K; ++kk) a += dS[kk * V + vv] * (double)k[IDX3(t, h, kk, H, K)];
+            dv[IDX3(t, h, vv, H, V)] = a;
+          }
+          for (int kk = 0; kk < K; ++kk) {
+            const double d = exp((double)g[IDX3(t, h, kk, H, K)]);
+            for (int vv = 0; vv < V; ++vv) dS[kk * V + vv] *= d;
+          }
+        }
+      }
+      if (dh0)
+        for (size_t i = 0; i < KV; ++i) dh0[((int64_t)n * H + h) * KV + i] = dS[i];
+      free(ck);
+      free(blk);
+      free(dS);
+      free(S);
+    }
+  }
+}
+
 /* Chunked form of the same map, restating the reference forward pipeline
  * chunk_gla_fwd (reference ops/gla/chunk.py:906-960) with fp64 everywhere:
  *   1. G = chunk-local inclusive cumsum of g, restarting every BT rows of each

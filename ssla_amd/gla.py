@@ -9,8 +9,11 @@ Drop-in for the reference's GLA API (haohq19/ssla ``ops/gla``):
   recurrent form with the signature of ``naive_gla_recurrent``
   (reference ops/gla/naive.py:50-111).
 
-Both are forward-only and run hand-written gfx950 kernels through
-libssla_amd.so; there is no CPU or Triton fallback.  Layouts are the
+They run hand-written gfx950 kernels through libssla_amd.so; there is no
+CPU or Triton fallback.  ``chunk_gla`` is differentiable
+(:class:`ChunkGLAFunction`, backward ``ssla_gla_chunk_bwd``) for the shapes
+the backward kernels take (bf16/fp16, K == 64, V a multiple of 16 up to
+64); the recurrent form is forward-only.  Layouts are the
 reference's packed varlen layouts: q, k, g ``[T, H, K]``, v ``[T, H, V]``,
 ``cu_seqlens`` int64 ``[N + 1]``, states ``[N, H, K, V]`` fp32.
 """
@@ -22,7 +25,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["chunk_gla", "fused_recurrent_gla", "naive_gla_recurrent", "chunk_kernel_supports"]
+__all__ = ["chunk_gla", "ChunkGLAFunction", "fused_recurrent_gla", "naive_gla_recurrent", "chunk_kernel_supports",
+           "chunk_backward_supports"]
 
 
 def chunk_kernel_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
@@ -32,7 +36,13 @@ def chunk_kernel_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
             and v.shape[-1] % 16 == 0 and v.shape[-1] <= 256)
 
 
-def _prep(name, q, k, v, g, cu_seqlens, initial_state):
+def chunk_backward_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
+    """True when ``ssla_gla_chunk_bwd`` handles this dtype/shape (bf16/fp16,
+    K == 64, V a multiple of 16 up to 64)."""
+    return chunk_kernel_supports(q, v) and v.shape[-1] <= 64
+
+
+def _prep(name, q, k, v, g, cu_seqlens, initial_state, allow_grad=False):
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (g, "g")):
         if t.dim() != 3:
             raise ValueError(f"{name}: {nm} must be [T, H, D], got shape {tuple(t.shape)}")
@@ -46,7 +56,8 @@ def _prep(name, q, k, v, g, cu_seqlens, initial_state):
     if q.dtype not in _lib.DTYPE_CODE:
         raise TypeError(f"{name}: unsupported dtype {q.dtype}")
     dev = _lib.require_cuda(q, k, v, g, initial_state)
-    _lib.require_no_grad(name, q, k, v, g, initial_state)
+    if not allow_grad:
+        _lib.require_no_grad(name, q, k, v, g, initial_state)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     if g.dtype != torch.float32 and g.dtype != q.dtype:
         g = g.float()
@@ -86,7 +97,19 @@ def chunk_gla(
         )
     if scale is None:
         scale = q.shape[-1] ** -0.5
-    q, k, v, g, cu, h0 = _prep("chunk_gla", q, k, v, g, cu_seqlens, initial_state)
+    grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (q, k, v, g, initial_state))
+    q, k, v, g, cu, h0 = _prep("chunk_gla", q, k, v, g, cu_seqlens, initial_state, allow_grad=grad)
+    if grad:
+        if not chunk_backward_supports(q, v):
+            raise NotImplementedError(
+                "chunk_gla backward needs bf16/fp16 inputs with K == 64 and V a multiple of 16 up to 64 "
+                f"(got {q.dtype}, K={q.shape[-1]}, V={v.shape[-1]})")
+        return ChunkGLAFunction.apply(q, k, v, g, float(scale), h0, output_final_state, cu)
+    return _chunk_fwd(q, k, v, g, cu, float(scale), h0, output_final_state)
+
+
+def _chunk_fwd(q, k, v, g, cu, scale, h0, output_final_state):
     T, H, K = q.shape
     V = v.shape[-1]
     N = cu.numel() - 1
@@ -105,6 +128,42 @@ def chunk_gla(
         _lib.DTYPE_CODE[q.dtype], _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
     _lib.check(st, "ssla_gla_chunk_fwd")
     return o, ht
+
+
+class ChunkGLAFunction(torch.autograd.Function):
+    """Forward ``ssla_gla_chunk_fwd``, backward ``ssla_gla_chunk_bwd``
+    (reference ChunkGLAFunction, ops/gla/chunk.py:1056-1116): the backward
+    recomputes every chunk's state from q, k, v, g and h0 instead of saving
+    them.  Returns dq, dk, dv in the input dtype, dg in g's dtype and dh0
+    (fp32) when an initial state was given."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, scale, initial_state, output_final_state, cu_seqlens):
+        o, ht = _chunk_fwd(q, k, v, g, cu_seqlens, scale, initial_state, output_final_state)
+        ctx.save_for_backward(q, k, v, g, initial_state, cu_seqlens)
+        ctx.scale = scale
+        return o, ht
+
+    @staticmethod
+    def backward(ctx, do, dht):
+        q, k, v, g, h0, cu = ctx.saved_tensors
+        T, H, K = q.shape
+        V = v.shape[-1]
+        N = cu.numel() - 1
+        do = do.to(v.dtype).contiguous()
+        dht = None if dht is None else dht.to(torch.float32).contiguous()
+        dq, dk = torch.empty_like(q), torch.empty_like(k)
+        dv, dg = torch.empty_like(v), torch.empty_like(g)
+        dh0 = torch.empty_like(h0) if h0 is not None else None
+        lib = _lib.load()
+        ws_bytes = lib.ssla_gla_chunk_bwd_workspace_size(N, T, H, K, V)
+        ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+        st = lib.ssla_gla_chunk_bwd(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.DTYPE_CODE[g.dtype], _lib.ptr(cu), N, T, H, K, V,
+            float(ctx.scale), _lib.ptr(h0), _lib.ptr(do), _lib.ptr(dht), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+            _lib.ptr(dg), _lib.ptr(dh0), _lib.DTYPE_CODE[q.dtype], _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
+        _lib.check(st, "ssla_gla_chunk_bwd")
+        return dq, dk, dv, dg, None, dh0, None, None
 
 
 def _recurrent(q, k, v, g, cu, scale, h0, o, ht, state_idx, n_rows):

@@ -341,3 +341,71 @@ def test_scatter_mean_vs_torch():
                     for c in range(C)], 1) / np.maximum(cnt, 1)[:, None]
     assert np.allclose(out, ref, rtol=1e-12, atol=1e-12)
     assert (out[cnt == 0] == 0).all()
+
+
+# ------------------------------------------------------- GLA backward ----
+def _gla_autograd(q, k, v, g, cu, scale, h0, dout, dht):
+    """Gradients by torch autograd (float64, CPU) through a plain loop of the
+    recurrence S_t = e^{g_t} S_{t-1} + k_t v_t^T, o_t = scale q_t S_t."""
+    tq, tk, tv, tg = (torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in (q, k, v, g))
+    th0 = None if h0 is None else torch.tensor(h0, dtype=torch.float64, requires_grad=True)
+    T, H, K = q.shape
+    V = v.shape[-1]
+    outs = [None] * T
+    finals = []
+    for n in range(len(cu) - 1):
+        S = th0[n] if th0 is not None else torch.zeros(H, K, V, dtype=torch.float64)
+        for t in range(int(cu[n]), int(cu[n + 1])):
+            S = torch.exp(tg[t])[:, :, None] * S + tk[t][:, :, None] * tv[t][:, None, :]
+            outs[t] = torch.einsum("hk,hkv->hv", tq[t] * scale, S)
+        finals.append(S)
+    o = torch.stack([x if x is not None else torch.zeros(H, V, dtype=torch.float64) for x in outs])
+    loss = (o * torch.tensor(dout, dtype=torch.float64)).sum()
+    if dht is not None:
+        loss = loss + (torch.stack(finals) * torch.tensor(dht, dtype=torch.float64)).sum()
+    loss.backward()
+    return tq.grad.numpy(), tk.grad.numpy(), tv.grad.numpy(), tg.grad.numpy(), (
+        None if th0 is None else th0.grad.numpy())
+
+
+@pytest.mark.parametrize("with_state", [False, True])
+def test_gla_bwd_matches_autograd(with_state):
+    rng = np.random.default_rng(31)
+    lens, H, K, V = [70, 0, 5, 140], 2, 6, 5   # crosses the oracle's 64-step checkpoints
+    q, k, v, g, cu = _gla_inputs(rng, lens, H, K, V, gate=-0.5)
+    g = np.minimum(g, 0).astype(np.float32)
+    dout = _rand(rng, q.shape[0], H, V)
+    h0 = _rand(rng, len(lens), H, K, V) * 0.3 if with_state else None
+    dht = _rand(rng, len(lens), H, K, V) if with_state else None
+    got = oracle.gla_recurrent_bwd(q, k, v, g, cu, dout, 0.7, h0, dht)
+    ref = _gla_autograd(q, k, v, g, cu, 0.7, h0, dout, dht)
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dh0"), got, ref):
+        if b is None:
+            assert a is None
+            continue
+        assert np.allclose(a, b, rtol=1e-10, atol=1e-10), name
+
+
+def test_gla_bwd_dg_identity_and_finite_differences():
+    """dg = reverse cumsum of (q dq - k dk) plus dht . ht (per sequence), and
+    a central difference of the fp64 forward along a random direction."""
+    rng = np.random.default_rng(32)
+    lens, H, K, V = [90], 1, 4, 3
+    q, k, v, g, cu = _gla_inputs(rng, lens, H, K, V, gate=-0.5)
+    g = np.minimum(g, 0).astype(np.float32)
+    dout = _rand(rng, 90, H, V)
+    h0 = _rand(rng, 1, H, K, V) * 0.3
+    dht = _rand(rng, 1, H, K, V)
+    dq, dk, dv, dg, dh0 = oracle.gla_recurrent_bwd(q, k, v, g, cu, dout, 1.0, h0, dht)
+    _, ht = oracle.gla_recurrent(q, k, v, g, cu, 1.0, h0, True)
+    r = q.astype(np.float64) * dq - k.astype(np.float64) * dk
+    want = np.cumsum(r[::-1], axis=0)[::-1] + (dht[0] * ht[0]).sum(-1)[None]
+    assert np.allclose(dg, want, rtol=1e-9, atol=1e-9)
+    d = _rand(rng, 90, H, K).astype(np.float64)
+    eps = 1e-4
+
+    def loss(gg):
+        o, s = oracle.gla_recurrent(q, k, v, gg.astype(np.float32), cu, 1.0, h0, True)
+        return float((o * dout).sum() + (s * dht).sum())
+    fd = (loss(g + eps * d) - loss(g - eps * d)) / (2 * eps)
+    assert abs(fd - float((dg * d).sum())) < 2e-3 * (1 + abs(fd))
