@@ -241,6 +241,54 @@ def calibrate_copy(torch, dev, mib=256, reps=3):
     print(json.dumps({"calibrate_copy_bytes": n * 4, "reps": reps}), flush=True)
 
 
+def bench_chunk_bwd(torch, lib, reps, dev):
+    """Backward of config 2 (ssla_gla_chunk_bwd): gradients of o and ht for
+    the C2 batch, two input sets alternating."""
+    from ssla_amd import _lib, synthetic
+    Tt, H, D = C2["B"] * C2["T"], C2["H"], C2["D"]
+    sets = []
+    for seed in (0, 1):
+        x = synthetic.chunk_gla_inputs(seed=seed, device=dev)
+        gen = torch.Generator(device=dev).manual_seed(100 + seed)
+        x["do"] = torch.randn(x["v"].shape, generator=gen, device=dev).to(torch.bfloat16)
+        x["dht"] = torch.randn(x["initial_state"].shape, generator=gen, device=dev) * 0.1
+        for name, like in (("dq", "q"), ("dk", "k"), ("dv", "v"), ("dg", "g"), ("dh0", "initial_state")):
+            x[name] = torch.empty_like(x[like])
+        sets.append(x)
+    ws_bytes = lib.ssla_gla_chunk_bwd_workspace_size(C2["B"], Tt, H, D, D)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def launch(x):
+        st = lib.ssla_gla_chunk_bwd(
+            x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(), _lib.SSLA_F32,
+            x["cu_seqlens"].data_ptr(), C2["B"], Tt, H, D, D, float(x["scale"]), x["initial_state"].data_ptr(),
+            x["do"].data_ptr(), x["dht"].data_ptr(), x["dq"].data_ptr(), x["dk"].data_ptr(), x["dv"].data_ptr(),
+            x["dg"].data_ptr(), x["dh0"].data_ptr(), _lib.SSLA_BF16, ws.data_ptr(), ws_bytes, sh)
+        _lib.check(st, "ssla_gla_chunk_bwd")
+
+    for i in range(3):
+        launch(sets[i % 2])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        launch(sets[i % 2])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    n16, n32, st_b = Tt * H * D * 2, Tt * H * D * 4, C2["B"] * H * D * D * 4
+    alg = 4 * n16 + n32 + 2 * st_b + 3 * n16 + n32 + st_b   # q k v do g h0 dht in; dq dk dv dg dh0 out
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": "chunk_gla backward (config 2): dq, dk, dv, dg, dh0 of o and ht; bf16, fp32 g",
+            "metric": "GLA chunk bwd Mtok/s", "value": Tt / (ms * 1e-3) / 1e6, "unit": "Mtok/s",
+            "ms_per_call": ms,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes": alg,
+                         "note": "whole call (state passes + chunk kernel)"}}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -248,7 +296,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", choices=["chunk", "sparse", "pool", "pool_sorted"], default=None,
+    ap.add_argument("--only", choices=["chunk", "sparse", "pool", "pool_sorted", "chunk_bwd"], default=None,
                     help="run one workload and print its line (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 256 MiB device copies (counter calibration) and exit")
@@ -269,6 +317,9 @@ def main(argv=None):
     lib = _lib.load()
     if args.only == "sparse":
         print(json.dumps(bench_sparse(torch, lib, args.steps, dev)), flush=True)
+        return 0
+    if args.only == "chunk_bwd":
+        print(json.dumps(bench_chunk_bwd(torch, lib, args.steps, dev)), flush=True)
         return 0
     if args.only in ("pool", "pool_sorted"):
         print(json.dumps(bench_pool(torch, lib, args.steps, dev, args.only == "pool_sorted")), flush=True)
@@ -300,7 +351,7 @@ def main(argv=None):
     }
     if not args.no_secondary and args.only is None:
         line["secondary"] = [bench_sparse(torch, lib, 10, dev), bench_pool(torch, lib, 20, dev),
-                             bench_pool(torch, lib, 20, dev, sorted_index=True)]
+                             bench_pool(torch, lib, 20, dev, sorted_index=True), bench_chunk_bwd(torch, lib, 10, dev)]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(r["sample"])
     print(json.dumps(line), flush=True)

@@ -84,12 +84,14 @@ __device__ __forceinline__ void seq_bounds(const int64_t *cu, int n, int64_t T, 
   eos = min(max(cu[n + 1], bos), T);
 }
 
-// coff[n] = chunks of sequences 0..n-1 (coff[n_seq] = all chunks).  One
-// workgroup; sequence n's state slots are coff[n] + n .. coff[n+1] + n.
+constexpr int kSegC = 8;   // chunks per segment of the state passes
+
+// coff[n] = chunks of sequences 0..n-1 and sgoff[n] = their segments of
+// kSegC chunks (coff[n_seq], sgoff[n_seq]: the totals).  One workgroup.
 __global__ __launch_bounds__(256) void bwd_offsets_kernel(const int64_t *__restrict__ cu, int n_seq, int64_t T,
-                                                          int64_t *__restrict__ coff) {
-  __shared__ int64_t part[256];
-  int64_t carry = 0;
+                                                          int64_t *__restrict__ coff, int64_t *__restrict__ sgoff) {
+  __shared__ int64_t pc[256], ps[256];
+  int64_t carry_c = 0, carry_s = 0;
   for (int base = 0; base < n_seq; base += 256) {
     const int n = base + static_cast<int>(threadIdx.x);
     int64_t c = 0;
@@ -98,122 +100,268 @@ __global__ __launch_bounds__(256) void bwd_offsets_kernel(const int64_t *__restr
       seq_bounds(cu, n, T, bos, eos);
       c = (eos - bos + BT - 1) / BT;
     }
-    part[threadIdx.x] = c;
+    const int64_t sgc = (c + kSegC - 1) / kSegC;
+    pc[threadIdx.x] = c;
+    ps[threadIdx.x] = sgc;
     __syncthreads();
-    for (int d = 1; d < 256; d <<= 1) {   // inclusive scan (Hillis-Steele)
-      const int64_t x = threadIdx.x >= static_cast<unsigned>(d) ? part[threadIdx.x - d] : 0;
+    for (int d = 1; d < 256; d <<= 1) {   // inclusive scans (Hillis-Steele)
+      const bool up = threadIdx.x >= static_cast<unsigned>(d);
+      const int64_t xc = up ? pc[threadIdx.x - d] : 0, xs = up ? ps[threadIdx.x - d] : 0;
       __syncthreads();
-      part[threadIdx.x] += x;
+      pc[threadIdx.x] += xc;
+      ps[threadIdx.x] += xs;
       __syncthreads();
     }
-    if (n < n_seq) coff[n] = carry + part[threadIdx.x] - c;
-    carry += part[255];
+    if (n < n_seq) {
+      coff[n] = carry_c + pc[threadIdx.x] - c;
+      sgoff[n] = carry_s + ps[threadIdx.x] - sgc;
+    }
+    carry_c += pc[255];
+    carry_s += ps[255];
     __syncthreads();
   }
-  if (threadIdx.x == 0) coff[n_seq] = carry;
+  if (threadIdx.x == 0) {
+    coff[n_seq] = carry_c;
+    sgoff[n_seq] = carry_s;
+  }
 }
 
 // --------------------------------------------------------- state passes --
-// One wavefront per (sequence, head, 16 value columns v0..v0+15).  Lane l
-// holds state rows (keys) 16 Kb + 4 (l / 16) + i of tile Kb, column l % 16.
-// REV = false: X = k, Y = v, factor e^(G_last - G_t), chunks in order, the
-//              state is stored before each chunk and after the last one.
-// REV = true : X = scale q, Y = do, factor e^(G_t), chunks in reverse, the
-//              gradient is stored after the end (dht) and after each chunk.
+// Each sequence's chunks are cut into segments of kSegC chunks.  A local
+// pass runs every segment from a zero state (one workgroup per (segment,
+// head); wavefront w owns value columns 16 w .. 16 w + 15, lane l holds
+// keys 16 Kb + 4 (l / 16) + i of tile Kb, column l % 16):
+// * forward (REV = false): X = k, Y = v, factor e^(G_last - G_t); stores the
+//   local state entering each chunk, the log2 decay from the segment start
+//   to it, and the segment's local end state and total decay;
+// * reverse (REV = true): X = scale q, Y = do, factor e^(G_t), chunks in
+//   reverse; stores the local gradient of the state entering each chunk and
+//   the log2 decay from there to the segment end.
+// The fold then carries states across segments, and the chunk kernel adds
+// the carried part: state = local + 2^decay * carried (per key).
+// All loads of a chunk are issued at once (16-byte pieces, every thread),
+// and the next chunk's pieces are in flight while the current one runs.
+
+struct __align__(16) SmemP {
+  uint16_t x[BT][KD];
+  float g[BT][KD];     // raw gates, then the log2 cumsum
+  uint16_t y[BT][64];
+  float glast[KD];
+  float psum[4][KD];
+};
+
+// Finds n with off[n] <= i < off[n + 1] (the last n with off[n] <= i).
+__device__ __forceinline__ int find_seq(const int64_t *off, int n_seq, int64_t i) {
+  int lo = 0, hi = n_seq - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (off[mid] <= i) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Log2 cumsum of the staged gates of one chunk (in place), 4 threads per key.
+__device__ __forceinline__ void gate_cumsum(float (&gt)[BT][KD], float (&psum)[4][KD], float *glast) {
+  const int key = threadIdx.x & 63, qd = threadIdx.x >> 6;
+  float run[16];
+  float s = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    s += gt[16 * qd + r][key];
+    run[r] = s;
+  }
+  psum[qd][key] = s;
+  __syncthreads();
+  float off = 0.f;
+  for (int b = 0; b < qd; ++b) off += psum[b][key];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) gt[16 * qd + r][key] = (run[r] + off) * kLog2e;
+  if (qd == 3) glast[key] = (s + off) * kLog2e;
+  __syncthreads();
+}
+
 template <bool REV, int DT, bool GF32>
-__global__ __launch_bounds__(64) void bwd_state_pass(const uint16_t *__restrict__ X, const uint16_t *__restrict__ Y,
-                                                     const void *__restrict__ g, const int64_t *__restrict__ cu,
-                                                     const int64_t *__restrict__ coff, int n_seq, int64_t T, int H,
-                                                     int V, float xscale, const float *__restrict__ s_init,
-                                                     float *__restrict__ slots, float *__restrict__ s_out) {
-  __shared__ uint16_t xs[BT][KD];
-  __shared__ float gs[BT][KD];
-  __shared__ uint16_t ys[BT][16];
-  __shared__ float glast[KD];
-  const int lane = threadIdx.x;
-  const int nvb = V / 16;
-  const int64_t item = blockIdx.x;
-  const int vb = static_cast<int>(item % nvb);
-  const int h = static_cast<int>((item / nvb) % H);
-  const int n = static_cast<int>(item / (static_cast<int64_t>(nvb) * H));
-  if (n >= n_seq) return;
-  const int v0 = vb * 16;
+__global__ __launch_bounds__(256) void bwd_seg_pass(const uint16_t *__restrict__ X, const uint16_t *__restrict__ Y,
+                                                    const void *__restrict__ g, const int64_t *__restrict__ cu,
+                                                    const int64_t *__restrict__ coff,
+                                                    const int64_t *__restrict__ sgoff, int n_seq, int64_t T, int H,
+                                                    int V, float xscale, float *__restrict__ loc,
+                                                    float *__restrict__ dec, float *__restrict__ eloc,
+                                                    float *__restrict__ dtot) {
+  __shared__ SmemP sm;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int h = static_cast<int>(blockIdx.x % H);
+  const int64_t sg = blockIdx.x / H;
+  if (sg >= sgoff[n_seq]) return;   // workgroup-uniform
+  const int n = find_seq(sgoff, n_seq, sg);
   int64_t bos, eos;
   seq_bounds(cu, n, T, bos, eos);
   const int64_t nc = (eos - bos + BT - 1) / BT;
-  const int64_t slot0 = coff[n] + n;
-  const int col = lane & 15, grp = lane >> 4;
+  const int64_t j0 = (sg - sgoff[n]) * kSegC;   // first chunk of the segment in the sequence
+  const int m = static_cast<int>(min(static_cast<int64_t>(kSegC), nc - j0));
+  const int64_t c0 = coff[n] + j0;              // its global chunk index
+  const int v0 = 16 * w;
+  const bool active = v0 < V;
   const int64_t KV = static_cast<int64_t>(KD) * V;
-  auto sidx = [&](int64_t slot, int key) { return (slot * H + h) * KV + static_cast<int64_t>(key) * V + v0 + col; };
+  const int nyp = BT * V / 8;                   // 16-byte pieces of a chunk's Y rows
+
+  // prefetch registers: X 2 pieces, g 4 (fp32) or 2 (16-bit), Y up to 2
+  uint4 px[2], pg[4], py[2];
+  auto fetch = [&](int64_t j) {
+    const int64_t t0 = bos + j * BT;
+    const int nrows = static_cast<int>(min(static_cast<int64_t>(BT), eos - t0));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid * 2 + i, r = e >> 3, pc = e & 7;
+      px[i] = r < nrows ? *reinterpret_cast<const uint4 *>(X + ((t0 + r) * H + h) * KD + pc * 8) : uint4{0, 0, 0, 0};
+    }
+    if constexpr (GF32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid * 4 + i, r = e >> 4, pc = e & 15;
+        pg[i] = r < nrows ? *reinterpret_cast<const uint4 *>(static_cast<const float *>(g) + ((t0 + r) * H + h) * KD + pc * 4)
+                          : uint4{0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid * 2 + i, r = e >> 3, pc = e & 7;
+        pg[i] = r < nrows ? *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g) + ((t0 + r) * H + h) * KD + pc * 8)
+                          : uint4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e / (V / 8), pc = e % (V / 8);
+      py[i] = (e < nyp && r < nrows) ? *reinterpret_cast<const uint4 *>(Y + ((t0 + r) * H + h) * V + pc * 8)
+                                     : uint4{0, 0, 0, 0};
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid * 2 + i;
+      *reinterpret_cast<uint4 *>(&sm.x[e >> 3][(e & 7) * 8]) = px[i];
+    }
+    if constexpr (GF32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid * 4 + i;
+        *reinterpret_cast<uint4 *>(&sm.g[e >> 4][(e & 15) * 4]) = pg[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid * 2 + i, r = e >> 3, pc = e & 7;
+        const uint16_t *u = reinterpret_cast<const uint16_t *>(&pg[i]);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) sm.g[r][pc * 8 + q] = Elt<DT>::f(u[q]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i;
+      if (e < nyp) *reinterpret_cast<uint4 *>(&sm.y[e / (V / 8)][(e % (V / 8)) * 8]) = py[i];
+    }
+  };
 
   f32x4 acc[4];
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
+  for (int kb = 0; kb < 4; ++kb) acc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float D = 0.f;   // lane = key (wavefront 0): log2 decay accumulated so far
+  auto store_loc = [&](int64_t c) {
+    if (active) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = kb * 16 + grp * 4 + i;
-      acc[kb][i] = s_init ? s_init[((static_cast<int64_t>(n) * H + h) * KD + key) * V + v0 + col] : 0.f;
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          loc[(c * H + h) * KV + static_cast<int64_t>(kb * 16 + grp * 4 + i) * V + v0 + col] = acc[kb][i];
     }
-  auto store = [&](int64_t slot) {
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) slots[sidx(slot, kb * 16 + grp * 4 + i)] = acc[kb][i];
+    if (w == 0) dec[(c * H + h) * KD + lane] = D;
   };
-  if (REV) store(slot0 + nc);
 
-  for (int64_t jj = 0; jj < nc; ++jj) {
-    const int64_t j = REV ? nc - 1 - jj : jj;
-    if (!REV) store(slot0 + j);
-    const int64_t t0 = bos + j * BT;
-    const int nrows = static_cast<int>(min(static_cast<int64_t>(BT), eos - t0));
-    // stage: lane = key for X and the gate cumsum; Y 16 columns
-    float run = 0.f;
-#pragma unroll 8
-    for (int r = 0; r < BT; ++r) {
-      const bool ok = r < nrows;
-      const int64_t row = (t0 + r) * H + h;
-      xs[r][lane] = ok ? X[row * KD + lane] : static_cast<uint16_t>(0);
-      run += ok ? load_g<GF32, DT>(g, row * KD + lane) * kLog2e : 0.f;
-      gs[r][lane] = run;
-    }
-    glast[lane] = run;
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const int r = rr * 4 + grp;
-      ys[r][col] = r < nrows ? Y[((t0 + r) * H + h) * V + v0 + col] : static_cast<uint16_t>(0);
-    }
+  fetch(REV ? j0 + m - 1 : j0);
+  for (int it = 0; it < m; ++it) {
+    const int64_t j = REV ? j0 + m - 1 - it : j0 + it;
+    stage();
+    if (it + 1 < m) fetch(REV ? j - 1 : j + 1);   // next chunk in flight
     __syncthreads();
-    // decay, then add X~^T Y (keys x time) x (time x 16 columns)
+    gate_cumsum(sm.g, sm.psum, sm.glast);
+    if (!REV) store_loc(c0 + (j - j0));
+    if (active) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+      for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[kb][i] *= cexp2(glast[kb * 16 + grp * 4 + i]);
+        for (int i = 0; i < 4; ++i) acc[kb][i] *= cexp2(sm.glast[kb * 16 + grp * 4 + i]);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        float a[8], b[8];
-        const int key = kb * 16 + col;
+        for (int ks = 0; ks < 2; ++ks) {
+          float a[8], b[8];
+          const int key = kb * 16 + col;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int t = ks * 32 + grp * 8 + e;
-          const float x = Elt<DT>::f(xs[t][key]) * xscale;
-          a[e] = x * cexp2(REV ? gs[t][key] : glast[key] - gs[t][key]);
-          b[e] = Elt<DT>::f(ys[t][col]);
+          for (int e = 0; e < 8; ++e) {
+            const int t = ks * 32 + grp * 8 + e;
+            const float x = Elt<DT>::f(sm.x[t][key]) * xscale;
+            a[e] = x * cexp2(REV ? sm.g[t][key] : sm.glast[key] - sm.g[t][key]);
+            b[e] = Elt<DT>::f(sm.y[t][v0 + col]);
+          }
+          acc[kb] = mma3(a, b, acc[kb]);
         }
-        acc[kb] = mma3(a, b, acc[kb]);
       }
     }
-    __syncthreads();
-    if (REV) store(slot0 + j);
+    D += sm.glast[lane];
+    if (REV) store_loc(c0 + (j - j0));
+    __syncthreads();   // the LDS tiles are rewritten by the next chunk
   }
-  if (!REV) store(slot0 + nc);
-  if (REV && s_out) {
+  if (!REV) {
+    if (active) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        s_out[((static_cast<int64_t>(n) * H + h) * KD + kb * 16 + grp * 4 + i) * V + v0 + col] = acc[kb][i];
+        for (int i = 0; i < 4; ++i)
+          eloc[(sg * H + h) * KV + static_cast<int64_t>(kb * 16 + grp * 4 + i) * V + v0 + col] = acc[kb][i];
+    }
+    if (w == 0) dtot[(sg * H + h) * KD + lane] = D;
   }
+}
+
+// Carries states across the segments of one (sequence, head):
+//   Sin[0] = h0 (or 0), Sin[s+1] = 2^Dtot[s] Sin[s] + Eloc[s] (Sin[nseg] = ht)
+//   dSend[nseg-1] = dht (or 0), dSend[s-1] = 2^Dtot[s] dSend[s] + dloc[first chunk of s]
+// and dh0 = 2^Dtot[0] dSend[0] + dloc[first chunk].  Sin has nseg + 1
+// entries per sequence (index sgoff[n] + n + s).
+__global__ __launch_bounds__(256) void bwd_fold_kernel(const int64_t *__restrict__ coff,
+                                                       const int64_t *__restrict__ sgoff, int n_seq, int H, int V,
+                                                       const float *__restrict__ h0, const float *__restrict__ dht,
+                                                       const float *__restrict__ eloc, const float *__restrict__ dtot,
+                                                       const float *__restrict__ dloc, float *__restrict__ sin_,
+                                                       float *__restrict__ dsend, float *__restrict__ dh0) {
+  // one thread per (sequence, head, state element)
+  const int64_t KV = static_cast<int64_t>(KD) * V;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t idx = gid % KV;
+  const int h = static_cast<int>((gid / KV) % H);
+  const int n = static_cast<int>(gid / (KV * H));
+  if (n >= n_seq) return;
+  const int key = static_cast<int>(idx / V);
+  const int64_t sg0 = sgoff[n], nseg = sgoff[n + 1] - sg0;
+  const int64_t o = (static_cast<int64_t>(n) * H + h) * KV + idx;
+  float S = h0 ? h0[o] : 0.f;
+  for (int64_t s = 0; s < nseg; ++s) {
+    sin_[((sg0 + n + s) * H + h) * KV + idx] = S;
+    S = cexp2(dtot[((sg0 + s) * H + h) * KD + key]) * S + eloc[((sg0 + s) * H + h) * KV + idx];
+  }
+  sin_[((sg0 + n + nseg) * H + h) * KV + idx] = S;
+  float dS = dht ? dht[o] : 0.f;
+  for (int64_t s = nseg - 1; s >= 0; --s) {
+    dsend[((sg0 + s) * H + h) * KV + idx] = dS;
+    const int64_t cf = coff[n] + s * kSegC;
+    dS = cexp2(dtot[((sg0 + s) * H + h) * KD + key]) * dS + dloc[(cf * H + h) * KV + idx];
+  }
+  if (dh0) dh0[o] = dS;
 }
 
 // ------------------------------------------------------------ chunk pass --
@@ -224,6 +372,7 @@ __global__ __launch_bounds__(64) void bwd_state_pass(const uint16_t *__restrict_
 // columns padded with zeros to VP = V rounded up to 32).
 struct __align__(16) SmemC {
   uint16_t q[BT][KD], k[BT][KD], v[BT][64], dout[BT][64];
+  float h[KD][64];     // h[c] as [key][value]
   float dh[KD][64];    // dh[c] as [key][value]
   union {
     struct {
@@ -242,9 +391,10 @@ template <int DT, bool GF32>
 __global__ __launch_bounds__(256) void bwd_chunk_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const void *__restrict__ g, const uint16_t *__restrict__ dout, const int64_t *__restrict__ cu,
-    const int64_t *__restrict__ coff, int n_seq, int64_t T, int H, int V, float scale,
-    const float *__restrict__ hs, const float *__restrict__ dhs, uint16_t *__restrict__ dq,
-    uint16_t *__restrict__ dk, uint16_t *__restrict__ dv, void *__restrict__ dg) {
+    const int64_t *__restrict__ coff, const int64_t *__restrict__ sgoff, int n_seq, int64_t T, int H, int V,
+    float scale, const float *__restrict__ hloc, const float *__restrict__ dfw, const float *__restrict__ dloc,
+    const float *__restrict__ drv, const float *__restrict__ sin_, const float *__restrict__ dsend,
+    uint16_t *__restrict__ dq, uint16_t *__restrict__ dk, uint16_t *__restrict__ dv, void *__restrict__ dg) {
   __shared__ SmemC sm;
   auto X = [](uint16_t b) { return Elt<DT>::f(b); };   // a staged input value
   const int tid = threadIdx.x;
@@ -253,49 +403,99 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
   const int h = static_cast<int>(blockIdx.x % H);
   const int64_t c = blockIdx.x / H;
   if (c >= coff[n_seq]) return;   // workgroup-uniform
-  // sequence of chunk c: the last n with coff[n] <= c
-  int lo = 0, hi = n_seq - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (coff[mid] <= c) lo = mid;
-    else hi = mid - 1;
-  }
-  const int n = lo;
+  const int n = find_seq(coff, n_seq, c);
   int64_t bos, eos;
   seq_bounds(cu, n, T, bos, eos);
   const int64_t j = c - coff[n];
   const int64_t t0 = bos + j * BT;
   const int nrows = static_cast<int>(min(static_cast<int64_t>(BT), eos - t0));
-  const int64_t slot = coff[n] + n + j;   // h[c] entering, slot + 1: leaving state / dh[c]
   const int64_t KV = static_cast<int64_t>(KD) * V;
-  const float *hc = hs + (slot * H + h) * KV;
-  const float *hn = hs + ((slot + 1) * H + h) * KV;
-  const float *dhc = dhs + ((slot + 1) * H + h) * KV;
   const int VP = (V + 31) & ~31;
+  // states of this chunk: local part + 2^decay * carried part (per key)
+  const int64_t nc = (eos - bos + BT - 1) / BT;
+  const int64_t sgi = sgoff[n] + j / kSegC;
+  const bool last_in_seg = (j % kSegC) == kSegC - 1 || j == nc - 1;
+  const float *sin_c = sin_ + ((sgi + n) * H + h) * KV;        // carried into this segment
+  const float *sin_n = sin_ + ((sgi + n + 1) * H + h) * KV;    // carried into the next (or ht)
+  const float *dsend_c = dsend + (sgi * H + h) * KV;           // gradient at this segment's end
 
-  // ---- staging: q, k, v, do rows (4 threads per row, 16 columns each)
+  // ---- staging: q, k, v, do and the gates, 16-byte pieces from every thread
   {
-    const int r = tid >> 2, c0 = (tid & 3) * 16;
-    const bool ok = r < nrows;
-    const int64_t row = (t0 + r) * H + h;
+    const uint4 z = {0, 0, 0, 0};
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      sm.q[r][c0 + e] = ok ? q[row * KD + c0 + e] : static_cast<uint16_t>(0);
-      sm.k[r][c0 + e] = ok ? k[row * KD + c0 + e] : static_cast<uint16_t>(0);
-      const bool okv = ok && c0 + e < V;
-      sm.v[r][c0 + e] = okv ? v[row * V + c0 + e] : static_cast<uint16_t>(0);
-      sm.dout[r][c0 + e] = okv ? dout[row * V + c0 + e] : static_cast<uint16_t>(0);
-      sm.dh[r][c0 + e] = c0 + e < V ? dhc[static_cast<int64_t>(r) * V + c0 + e] : 0.f;   // row r = key
+    for (int i = 0; i < 2; ++i) {   // q, k: 512 pieces each
+      const int e = tid * 2 + i, r = e >> 3, pc = e & 7;
+      const int64_t o = ((t0 + r) * H + h) * KD + pc * 8;
+      *reinterpret_cast<uint4 *>(&sm.q[r][pc * 8]) = r < nrows ? *reinterpret_cast<const uint4 *>(q + o) : z;
+      *reinterpret_cast<uint4 *>(&sm.k[r][pc * 8]) = r < nrows ? *reinterpret_cast<const uint4 *>(k + o) : z;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {   // v, do: 64 rows x 8 pieces (zero beyond V)
+      const int e = tid * 2 + i, r = e >> 3, pc = e & 7;
+      const bool ok = r < nrows && pc * 8 < V;
+      const int64_t o = ((t0 + r) * H + h) * V + pc * 8;
+      *reinterpret_cast<uint4 *>(&sm.v[r][pc * 8]) = ok ? *reinterpret_cast<const uint4 *>(v + o) : z;
+      *reinterpret_cast<uint4 *>(&sm.dout[r][pc * 8]) = ok ? *reinterpret_cast<const uint4 *>(dout + o) : z;
+    }
+    if constexpr (GF32) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid * 4 + i, r = e >> 4, pc = e & 15;
+        *reinterpret_cast<uint4 *>(&sm.G[r][pc * 4]) =
+            r < nrows ? *reinterpret_cast<const uint4 *>(static_cast<const float *>(g) + ((t0 + r) * H + h) * KD + pc * 4)
+                      : z;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid * 2 + i, r = e >> 3, pc = e & 7;
+        const uint4 u4 = r < nrows
+            ? *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g) + ((t0 + r) * H + h) * KD + pc * 8)
+            : z;
+        const uint16_t *u = reinterpret_cast<const uint16_t *>(&u4);
+#pragma unroll
+        for (int qq = 0; qq < 8; ++qq) sm.G[r][pc * 8 + qq] = Elt<DT>::f(u[qq]);
+      }
     }
   }
-  if (w == 0) {   // gate cumsum per key (lane = key), block reference points
-    float run = 0.f;
-#pragma unroll 8
-    for (int r = 0; r < BT; ++r) {
-      run += r < nrows ? load_g<GF32, DT>(g, ((t0 + r) * H + h) * KD + lane) * kLog2e : 0.f;
-      sm.G[r][lane] = run;
+  {   // h[c], dh[c] (leaving-state gradient) and sum_v dh[c] h[c+1]; row = key,
+      // 4 threads per key, 16 value columns each (float4 pieces)
+    const int key = tid >> 2, c0 = (tid & 3) * 16;
+    const float fe = cexp2(dfw[(c * H + h) * KD + key]);
+    const float fn = last_in_seg ? 0.f : cexp2(dfw[((c + 1) * H + h) * KD + key]);
+    const float fr = last_in_seg ? 0.f : cexp2(drv[((c + 1) * H + h) * KD + key]);
+    float part = 0.f;
+#pragma unroll
+    for (int e4 = 0; e4 < 16; e4 += 4) {
+      const int vc = c0 + e4;
+      float4 hv = {0.f, 0.f, 0.f, 0.f}, dv4 = {0.f, 0.f, 0.f, 0.f};
+      if (vc < V) {
+        const int64_t o = static_cast<int64_t>(key) * V + vc;
+        const float4 sc = *reinterpret_cast<const float4 *>(sin_c + o);
+        const float4 hl = *reinterpret_cast<const float4 *>(hloc + (c * H + h) * KV + o);
+        hv = make_float4(hl.x + fe * sc.x, hl.y + fe * sc.y, hl.z + fe * sc.z, hl.w + fe * sc.w);
+        float4 hn, ds = *reinterpret_cast<const float4 *>(dsend_c + o);
+        if (last_in_seg) {
+          hn = *reinterpret_cast<const float4 *>(sin_n + o);
+          dv4 = ds;
+        } else {
+          const float4 hl1 = *reinterpret_cast<const float4 *>(hloc + ((c + 1) * H + h) * KV + o);
+          const float4 dl1 = *reinterpret_cast<const float4 *>(dloc + ((c + 1) * H + h) * KV + o);
+          hn = make_float4(hl1.x + fn * sc.x, hl1.y + fn * sc.y, hl1.z + fn * sc.z, hl1.w + fn * sc.w);
+          dv4 = make_float4(dl1.x + fr * ds.x, dl1.y + fr * ds.y, dl1.z + fr * ds.z, dl1.w + fr * ds.w);
+        }
+        part += dv4.x * hn.x + dv4.y * hn.y + dv4.z * hn.z + dv4.w * hn.w;
+      }
+      *reinterpret_cast<float4 *>(&sm.h[key][vc]) = hv;
+      *reinterpret_cast<float4 *>(&sm.dh[key][vc]) = dv4;
     }
-    sm.glast[lane] = run;
+    part += __shfl_xor(part, 1);
+    part += __shfl_xor(part, 2);
+    if ((tid & 3) == 0) sm.term[key] = part;
+  }
+  __syncthreads();
+  gate_cumsum(sm.G, sm.bsum, sm.glast);   // (bsum doubles as its scratch)
+  if (w == 0) {   // block reference points
     float ep = 0.f;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -303,30 +503,33 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
       sm.M[b][lane] = 0.5f * (ep + eb);
       ep = eb;
     }
-  } else if (w == 1) {   // sum_v dh[c] * (state leaving the chunk)
-    float s = 0.f;
-    for (int vv = 0; vv < V; ++vv) s += dhc[static_cast<int64_t>(lane) * V + vv] * hn[static_cast<int64_t>(lane) * V + vv];
-    sm.term[lane] = s;
   }
   __syncthreads();
 
   const int I = w;   // this wavefront's row block
-  // ---- A and dA, rows of block I (zero above the diagonal)
+  // ---- A and dA, rows of block I (zero above the diagonal); the q side
+  // (q e^(G - M_I)) of the A products is the same for every column block
+  float qa[2][8];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int kk = ks * 32 + grp * 8 + e, t = 16 * I + col;
+      qa[ks][e] = X(sm.q[t][kk]) * cexp2(sm.G[t][kk] - sm.M[I][kk]);
+    }
   for (int J = 0; J < 4; ++J) {
     f32x4 a4 = {0.f, 0.f, 0.f, 0.f}, d4 = {0.f, 0.f, 0.f, 0.f};
     if (J <= I) {
       const int t = 16 * I + col, s = 16 * J + col;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        float a[8], b[8];
+        float b[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int kk = ks * 32 + grp * 8 + e;
-          const float m = sm.M[I][kk];
-          a[e] = X(sm.q[t][kk]) * cexp2(sm.G[t][kk] - m);
-          b[e] = X(sm.k[s][kk]) * cexp2(m - sm.G[s][kk]);
+          b[e] = X(sm.k[s][kk]) * cexp2(sm.M[I][kk] - sm.G[s][kk]);
         }
-        a4 = mma3(a, b, a4);
+        a4 = mma3(qa[ks], b, a4);
       }
       for (int vs = 0; vs < VP; vs += 32) {
         float a[8], b[8];
@@ -388,7 +591,7 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int vc = vs + grp * 8 + e;
-          b[e] = vc < V ? hc[static_cast<int64_t>(key) * V + vc] : 0.f;
+          b[e] = sm.h[key][vc];
         }
         ae[N] = mma3(a, b, ae[N]);
       }
@@ -523,37 +726,71 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
   }
 }
 
+// Workspace: offsets, per-chunk local states / decays of both passes, and
+// per-segment end states, decays, carried states and gradients.
+struct BwdWs {
+  int64_t *coff, *sgoff;
+  float *hloc, *dloc, *dfw, *drv, *eloc, *dtot, *sin_, *dsend;
+  size_t total;
+};
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+inline BwdWs bwd_ws(char *base, int n_seq, int64_t T, int H, int V) {
+  const int64_t cmax = (T + BT - 1) / BT + n_seq;                  // chunks
+  const int64_t smax = (cmax + kSegC - 1) / kSegC + n_seq;         // segments
+  const size_t kv = static_cast<size_t>(H) * KD * V * sizeof(float), kk = static_cast<size_t>(H) * KD * sizeof(float);
+  BwdWs w;
+  size_t p = 0;
+  auto take = [&](size_t bytes) {
+    char *q = base ? base + p : nullptr;
+    p = align256(p + bytes);
+    return q;
+  };
+  w.coff = reinterpret_cast<int64_t *>(take(sizeof(int64_t) * (n_seq + 1)));
+  w.sgoff = reinterpret_cast<int64_t *>(take(sizeof(int64_t) * (n_seq + 1)));
+  w.hloc = reinterpret_cast<float *>(take(kv * cmax));
+  w.dloc = reinterpret_cast<float *>(take(kv * cmax));
+  w.dfw = reinterpret_cast<float *>(take(kk * cmax));
+  w.drv = reinterpret_cast<float *>(take(kk * cmax));
+  w.eloc = reinterpret_cast<float *>(take(kv * smax));
+  w.dtot = reinterpret_cast<float *>(take(kk * smax));
+  w.sin_ = reinterpret_cast<float *>(take(kv * (smax + n_seq)));
+  w.dsend = reinterpret_cast<float *>(take(kv * smax));
+  w.total = p;
+  return w;
+}
+
 template <int DT, bool GF32>
 int launch_bwd(const void *q, const void *k, const void *v, const void *g, const int64_t *cu, int n_seq, int64_t T,
                int H, int V, float scale, const float *h0, const void *dout, const float *dht, void *dq, void *dk,
-               void *dv, void *dg, float *dh0, int64_t *coff, float *hs, float *dhs, hipStream_t st) {
+               void *dv, void *dg, float *dh0, const BwdWs &w, hipStream_t st) {
   const auto *Q = static_cast<const uint16_t *>(q);
   const auto *Kp = static_cast<const uint16_t *>(k);
   const auto *Vp = static_cast<const uint16_t *>(v);
   const auto *DO = static_cast<const uint16_t *>(dout);
-  hipLaunchKernelGGL(bwd_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T, coff);
-  const int64_t passes = static_cast<int64_t>(n_seq) * H * (V / 16);
-  hipLaunchKernelGGL((bwd_state_pass<false, DT, GF32>), dim3(static_cast<unsigned>(passes)), dim3(64), 0, st, Kp, Vp, g,
-                     cu, coff, n_seq, T, H, V, 1.f, h0, hs, static_cast<float *>(nullptr));
-  hipLaunchKernelGGL((bwd_state_pass<true, DT, GF32>), dim3(static_cast<unsigned>(passes)), dim3(64), 0, st, Q, DO, g,
-                     cu, coff, n_seq, T, H, V, scale, dht, dhs, dh0);
-  const int64_t chunks = (T + BT - 1) / BT + n_seq;
-  hipLaunchKernelGGL((bwd_chunk_kernel<DT, GF32>), dim3(static_cast<unsigned>(chunks * H)), dim3(256), 0, st, Q, Kp, Vp,
-                     g, DO, cu, coff, n_seq, T, H, V, scale, hs, dhs, static_cast<uint16_t *>(dq),
-                     static_cast<uint16_t *>(dk), static_cast<uint16_t *>(dv), dg);
+  hipLaunchKernelGGL(bwd_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T, w.coff, w.sgoff);
+  const int64_t cmax = (T + BT - 1) / BT + n_seq;
+  const int64_t smax = (cmax + kSegC - 1) / kSegC + n_seq;
+  hipLaunchKernelGGL((bwd_seg_pass<false, DT, GF32>), dim3(static_cast<unsigned>(smax * H)), dim3(256), 0, st, Kp, Vp,
+                     g, cu, w.coff, w.sgoff, n_seq, T, H, V, 1.f, w.hloc, w.dfw, w.eloc, w.dtot);
+  hipLaunchKernelGGL((bwd_seg_pass<true, DT, GF32>), dim3(static_cast<unsigned>(smax * H)), dim3(256), 0, st, Q, DO, g,
+                     cu, w.coff, w.sgoff, n_seq, T, H, V, scale, w.dloc, w.drv, static_cast<float *>(nullptr),
+                     static_cast<float *>(nullptr));
+  const int64_t fold_threads = static_cast<int64_t>(n_seq) * H * KD * V;
+  hipLaunchKernelGGL(bwd_fold_kernel, dim3(static_cast<unsigned>((fold_threads + 255) / 256)), dim3(256), 0, st,
+                     w.coff, w.sgoff, n_seq, H, V, h0, dht, w.eloc, w.dtot, w.dloc, w.sin_, w.dsend, dh0);
+  hipLaunchKernelGGL((bwd_chunk_kernel<DT, GF32>), dim3(static_cast<unsigned>(cmax * H)), dim3(256), 0, st, Q, Kp, Vp,
+                     g, DO, cu, w.coff, w.sgoff, n_seq, T, H, V, scale, w.hloc, w.dfw, w.dloc, w.drv, w.sin_,
+                     w.dsend, static_cast<uint16_t *>(dq), static_cast<uint16_t *>(dk), static_cast<uint16_t *>(dv),
+                     dg);
   return launch_status("gla_chunk_bwd");
 }
-
-inline int64_t bwd_slots(int n_seq, int64_t T) { return (T + BT - 1) / BT + 2 * static_cast<int64_t>(n_seq); }
-inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 }  // namespace
 }  // namespace ssla
 
 extern "C" size_t ssla_gla_chunk_bwd_workspace_size(int n_seq, int64_t T, int H, int K, int V) {
   if (n_seq < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0) return 0;
-  const size_t st = static_cast<size_t>(ssla::bwd_slots(n_seq, T)) * H * K * V * sizeof(float);
-  return ssla::align256(sizeof(int64_t) * (n_seq + 1)) + 2 * ssla::align256(st);
+  return ssla::bwd_ws(nullptr, n_seq, T, H, V).total;
 }
 
 extern "C" int ssla_gla_chunk_bwd(const void *q, const void *k, const void *v, const void *g, int g_dtype,
@@ -586,24 +823,20 @@ extern "C" int ssla_gla_chunk_bwd(const void *q, const void *k, const void *v, c
   }
   SSLA_CHECK_ARG(aligned(workspace, 16), "gla_chunk_bwd: workspace must be 16-byte aligned");
   const int64_t chunks = (T + BT - 1) / BT + n_seq;
-  if (chunks * H > 0x7fffffff || static_cast<int64_t>(n_seq) * H * (V / 16) > 0x7fffffff) {
+  if (chunks * H > 0x7fffffff) {
     set_error("gla_chunk_bwd: too many chunks");
     return SSLA_ERR_UNSUPPORTED;
   }
-  char *base = static_cast<char *>(workspace);
-  int64_t *coff = reinterpret_cast<int64_t *>(base);
-  const size_t st_bytes = align256(static_cast<size_t>(bwd_slots(n_seq, T)) * H * K * V * sizeof(float));
-  float *hs = reinterpret_cast<float *>(base + align256(sizeof(int64_t) * (n_seq + 1)));
-  float *dhs = reinterpret_cast<float *>(reinterpret_cast<char *>(hs) + st_bytes);
+  const BwdWs w = bwd_ws(static_cast<char *>(workspace), n_seq, T, H, V);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool gf32 = g_dtype == SSLA_F32;
   if (dtype == SSLA_BF16)
     return gf32 ? launch_bwd<SSLA_BF16, true>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, dout, dht, dq, dk,
-                                              dv, dg, dh0, coff, hs, dhs, st)
+                                              dv, dg, dh0, w, st)
                 : launch_bwd<SSLA_BF16, false>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, dout, dht, dq,
-                                               dk, dv, dg, dh0, coff, hs, dhs, st);
+                                               dk, dv, dg, dh0, w, st);
   return gf32 ? launch_bwd<SSLA_F16, true>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, dout, dht, dq, dk, dv,
-                                           dg, dh0, coff, hs, dhs, st)
+                                           dg, dh0, w, st)
               : launch_bwd<SSLA_F16, false>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, dout, dht, dq, dk,
-                                            dv, dg, dh0, coff, hs, dhs, st);
+                                            dv, dg, dh0, w, st);
 }
