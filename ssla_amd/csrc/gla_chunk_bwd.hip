@@ -32,8 +32,8 @@
 // use e^(G_t - M_I) on the output side and e^(M_I - G_s) on the operand side,
 // so for non-positive gates no factor exceeds the decay over half a block.
 // Exponents are clamped to +-126.  Products run on v_mfma_f32_16x16x32_bf16
-// as split bf16 triples (see mma3) with fp32 accumulation; states, A, dA and
-// dg are fp32.
+// as split bf16 products (see mmax) with fp32 accumulation; states, A, dA
+// and dg are fp32.
 #include "common.h"
 
 namespace ssla {
@@ -50,16 +50,24 @@ __device__ __forceinline__ float cexp2(float x) { return fast_exp2(fminf(fmaxf(x
 // mantissa bits per operand.  dg is a reverse cumsum of q dq - k dk, whose
 // terms cancel (strongly so for fast-decaying gates); single bf16 operands
 // leave it with errors of several percent.
+// AX / BX: the operand is an exact bf16 value (a bf16 input), so its
+// remainder is zero and its lo product is skipped.
 typedef float f32x8 __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ f32x4 mma3(const float (&a)[8], const float (&b)[8], f32x4 c) {
+template <bool AX, bool BX>
+__device__ __forceinline__ f32x4 mmax(const float (&a)[8], const float (&b)[8], f32x4 c) {
   const f32x8 va = {a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7]};
   const f32x8 vb = {b[0], b[1], b[2], b[3], b[4], b[5], b[6], b[7]};
   const bf16x8 ah = __builtin_convertvector(va, bf16x8), bh = __builtin_convertvector(vb, bf16x8);
-  const bf16x8 al = __builtin_convertvector(va - __builtin_convertvector(ah, f32x8), bf16x8);
-  const bf16x8 bl = __builtin_convertvector(vb - __builtin_convertvector(bh, f32x8), bf16x8);
   c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+  if constexpr (!BX) {
+    const bf16x8 bl = __builtin_convertvector(vb - __builtin_convertvector(bh, f32x8), bf16x8);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+  }
+  if constexpr (!AX) {
+    const bf16x8 al = __builtin_convertvector(va - __builtin_convertvector(ah, f32x8), bf16x8);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+  }
+  return c;
 }
 
 // 16-bit input element <-> fp32
@@ -161,14 +169,17 @@ __device__ __forceinline__ int find_seq(const int64_t *off, int n_seq, int64_t i
   return lo;
 }
 
-// Log2 cumsum of the staged gates of one chunk (in place), 4 threads per key.
-__device__ __forceinline__ void gate_cumsum(float (&gt)[BT][KD], float (&psum)[4][KD], float *glast) {
+// Log2 cumsum of the staged gates of one chunk (in place) by NT threads:
+// NT / 64 threads per key, each over 64 / (NT / 64) consecutive rows.
+template <int NT, int LD>
+__device__ __forceinline__ void gate_cumsum(float (&gt)[BT][LD], float (&psum)[NT / 64][KD], float *glast) {
+  constexpr int NQ = NT / 64, RQ = BT / NQ;
   const int key = threadIdx.x & 63, qd = threadIdx.x >> 6;
-  float run[16];
+  float run[RQ];
   float s = 0.f;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    s += gt[16 * qd + r][key];
+  for (int r = 0; r < RQ; ++r) {
+    s += gt[RQ * qd + r][key];
     run[r] = s;
   }
   psum[qd][key] = s;
@@ -176,8 +187,8 @@ __device__ __forceinline__ void gate_cumsum(float (&gt)[BT][KD], float (&psum)[4
   float off = 0.f;
   for (int b = 0; b < qd; ++b) off += psum[b][key];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) gt[16 * qd + r][key] = (run[r] + off) * kLog2e;
-  if (qd == 3) glast[key] = (s + off) * kLog2e;
+  for (int r = 0; r < RQ; ++r) gt[RQ * qd + r][key] = (run[r] + off) * kLog2e;
+  if (qd == NQ - 1) glast[key] = (s + off) * kLog2e;
   __syncthreads();
 }
 
@@ -290,7 +301,7 @@ __global__ __launch_bounds__(256) void bwd_seg_pass(const uint16_t *__restrict__
     stage();
     if (it + 1 < m) fetch(REV ? j - 1 : j + 1);   // next chunk in flight
     __syncthreads();
-    gate_cumsum(sm.g, sm.psum, sm.glast);
+    gate_cumsum<256>(sm.g, sm.psum, sm.glast);
     if (!REV) store_loc(c0 + (j - j0));
     if (active) {
 #pragma unroll
@@ -308,7 +319,7 @@ __global__ __launch_bounds__(256) void bwd_seg_pass(const uint16_t *__restrict__
             a[e] = x * cexp2(REV ? sm.g[t][key] : sm.glast[key] - sm.g[t][key]);
             b[e] = Elt<DT>::f(sm.y[t][v0 + col]);
           }
-          acc[kb] = mma3(a, b, acc[kb]);
+          acc[kb] = mmax<false, DT == SSLA_BF16>(a, b, acc[kb]);
         }
       }
     }
@@ -365,41 +376,48 @@ __global__ __launch_bounds__(256) void bwd_fold_kernel(const int64_t *__restrict
 }
 
 // ------------------------------------------------------------ chunk pass --
-// One workgroup (4 wavefronts) per (chunk, head).  Wavefront I owns rows
-// 16 I .. 16 I + 15: it computes those rows of A and dA, then dq, dk, dv and
-// the q dq - k dk terms of those rows; dg is a reverse cumsum over the
-// chunk.  q, k, v, do are staged as rows of 64 input-dtype values (value
-// columns padded with zeros to VP = V rounded up to 32).
+// One workgroup (8 wavefronts) per (chunk, head).  Wavefronts w and w + 4
+// own rows 16 I .. 16 I + 15 (I = w % 4) and split the output tiles between
+// them (half P = w / 4): column blocks J of A and dA with J % 2 == P, key
+// tiles 2 P and 2 P + 1 of dq and dk, value tiles N % 2 == P of dv; two
+// wavefronts per SIMD hide each other's LDS latency.  dg is a reverse cumsum
+// over the chunk.  q, k, v, do are staged as rows of 64 input-dtype values
+// (value columns padded with zeros to VP = V rounded up to 32).
+constexpr int kCW = 8;   // wavefronts per chunk workgroup
+constexpr int kL16 = 64, kL32 = 64;   // LDS row lengths (16-bit and fp32 tiles)
+
 struct __align__(16) SmemC {
-  uint16_t q[BT][KD], k[BT][KD], v[BT][64], dout[BT][64];
-  float h[KD][64];     // h[c] as [key][value]
-  float dh[KD][64];    // dh[c] as [key][value]
+  uint16_t q[BT][kL16], k[BT][kL16], v[BT][kL16], dout[BT][kL16];
+  float h[KD][kL32];   // h[c] as [key][value]
+  float dh[KD][kL32];  // dh[c] as [key][value]
   union {
     struct {
-      float A[BT][BT], dA[BT][BT];
+      float A[BT][kL32], dA[BT][kL32];
     } p;
-    float r[BT][KD];   // q dq - k dk (after the products)
+    float r[BT][kL32];   // q dq - k dk (after the products)
   } u;
-  float G[BT][KD];     // log2 cumsum
+  float G[BT][kL32];   // log2 cumsum
   float M[4][KD];      // block reference points
   float glast[KD];
   float term[KD];      // sum_v dh[c] h[c+1]
-  float bsum[4][KD];
+  float bsum[kCW][KD];
 };
 
 template <int DT, bool GF32>
-__global__ __launch_bounds__(256) void bwd_chunk_kernel(
+__global__ __launch_bounds__(64 * kCW) void bwd_chunk_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
     const void *__restrict__ g, const uint16_t *__restrict__ dout, const int64_t *__restrict__ cu,
     const int64_t *__restrict__ coff, const int64_t *__restrict__ sgoff, int n_seq, int64_t T, int H, int V,
     float scale, const float *__restrict__ hloc, const float *__restrict__ dfw, const float *__restrict__ dloc,
     const float *__restrict__ drv, const float *__restrict__ sin_, const float *__restrict__ dsend,
     uint16_t *__restrict__ dq, uint16_t *__restrict__ dk, uint16_t *__restrict__ dv, void *__restrict__ dg) {
+  constexpr bool EX = DT == SSLA_BF16;   // input values are exact bf16 operands
   __shared__ SmemC sm;
   auto X = [](uint16_t b) { return Elt<DT>::f(b); };   // a staged input value
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
+  const int I = w & 3, P = w >> 2;
   const int h = static_cast<int>(blockIdx.x % H);
   const int64_t c = blockIdx.x / H;
   if (c >= coff[n_seq]) return;   // workgroup-uniform
@@ -422,51 +440,44 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
   // ---- staging: q, k, v, do and the gates, 16-byte pieces from every thread
   {
     const uint4 z = {0, 0, 0, 0};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {   // q, k: 512 pieces each
-      const int e = tid * 2 + i, r = e >> 3, pc = e & 7;
-      const int64_t o = ((t0 + r) * H + h) * KD + pc * 8;
-      *reinterpret_cast<uint4 *>(&sm.q[r][pc * 8]) = r < nrows ? *reinterpret_cast<const uint4 *>(q + o) : z;
-      *reinterpret_cast<uint4 *>(&sm.k[r][pc * 8]) = r < nrows ? *reinterpret_cast<const uint4 *>(k + o) : z;
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {   // v, do: 64 rows x 8 pieces (zero beyond V)
-      const int e = tid * 2 + i, r = e >> 3, pc = e & 7;
-      const bool ok = r < nrows && pc * 8 < V;
-      const int64_t o = ((t0 + r) * H + h) * V + pc * 8;
-      *reinterpret_cast<uint4 *>(&sm.v[r][pc * 8]) = ok ? *reinterpret_cast<const uint4 *>(v + o) : z;
-      *reinterpret_cast<uint4 *>(&sm.dout[r][pc * 8]) = ok ? *reinterpret_cast<const uint4 *>(dout + o) : z;
-    }
+    auto put = [](void *dst, const uint4 &x) {   // 16 bytes into an 8-byte-aligned row
+      uint2 *d = static_cast<uint2 *>(dst);
+      d[0] = make_uint2(x.x, x.y);
+      d[1] = make_uint2(x.z, x.w);
+    };
+    const int r = tid >> 3, pc = tid & 7;   // 64 rows x 8 pieces
+    const int64_t oq = ((t0 + r) * H + h) * KD + pc * 8;
+    put(&sm.q[r][pc * 8], r < nrows ? *reinterpret_cast<const uint4 *>(q + oq) : z);
+    put(&sm.k[r][pc * 8], r < nrows ? *reinterpret_cast<const uint4 *>(k + oq) : z);
+    const bool okv = r < nrows && pc * 8 < V;
+    const int64_t ov = ((t0 + r) * H + h) * V + pc * 8;
+    put(&sm.v[r][pc * 8], okv ? *reinterpret_cast<const uint4 *>(v + ov) : z);
+    put(&sm.dout[r][pc * 8], okv ? *reinterpret_cast<const uint4 *>(dout + ov) : z);
     if constexpr (GF32) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = tid * 4 + i, r = e >> 4, pc = e & 15;
-        *reinterpret_cast<uint4 *>(&sm.G[r][pc * 4]) =
-            r < nrows ? *reinterpret_cast<const uint4 *>(static_cast<const float *>(g) + ((t0 + r) * H + h) * KD + pc * 4)
-                      : z;
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid * 2 + i, rr = e >> 4, p4 = e & 15;
+        put(&sm.G[rr][p4 * 4],
+            rr < nrows
+                ? *reinterpret_cast<const uint4 *>(static_cast<const float *>(g) + ((t0 + rr) * H + h) * KD + p4 * 4)
+                : z);
       }
     } else {
+      const uint4 u4 = r < nrows ? *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g) + oq) : z;
+      const uint16_t *u = reinterpret_cast<const uint16_t *>(&u4);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int e = tid * 2 + i, r = e >> 3, pc = e & 7;
-        const uint4 u4 = r < nrows
-            ? *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(g) + ((t0 + r) * H + h) * KD + pc * 8)
-            : z;
-        const uint16_t *u = reinterpret_cast<const uint16_t *>(&u4);
-#pragma unroll
-        for (int qq = 0; qq < 8; ++qq) sm.G[r][pc * 8 + qq] = Elt<DT>::f(u[qq]);
-      }
+      for (int qq = 0; qq < 8; ++qq) sm.G[r][pc * 8 + qq] = Elt<DT>::f(u[qq]);
     }
   }
   {   // h[c], dh[c] (leaving-state gradient) and sum_v dh[c] h[c+1]; row = key,
-      // 4 threads per key, 16 value columns each (float4 pieces)
-    const int key = tid >> 2, c0 = (tid & 3) * 16;
+      // 8 threads per key, 8 value columns each (float4 pieces)
+    const int key = tid >> 3, c0 = (tid & 7) * 8;
     const float fe = cexp2(dfw[(c * H + h) * KD + key]);
     const float fn = last_in_seg ? 0.f : cexp2(dfw[((c + 1) * H + h) * KD + key]);
     const float fr = last_in_seg ? 0.f : cexp2(drv[((c + 1) * H + h) * KD + key]);
     float part = 0.f;
 #pragma unroll
-    for (int e4 = 0; e4 < 16; e4 += 4) {
+    for (int e4 = 0; e4 < 8; e4 += 4) {
       const int vc = c0 + e4;
       float4 hv = {0.f, 0.f, 0.f, 0.f}, dv4 = {0.f, 0.f, 0.f, 0.f};
       if (vc < V) {
@@ -486,15 +497,18 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
         }
         part += dv4.x * hn.x + dv4.y * hn.y + dv4.z * hn.z + dv4.w * hn.w;
       }
-      *reinterpret_cast<float4 *>(&sm.h[key][vc]) = hv;
-      *reinterpret_cast<float4 *>(&sm.dh[key][vc]) = dv4;
+      *reinterpret_cast<float2 *>(&sm.h[key][vc]) = make_float2(hv.x, hv.y);
+      *reinterpret_cast<float2 *>(&sm.h[key][vc + 2]) = make_float2(hv.z, hv.w);
+      *reinterpret_cast<float2 *>(&sm.dh[key][vc]) = make_float2(dv4.x, dv4.y);
+      *reinterpret_cast<float2 *>(&sm.dh[key][vc + 2]) = make_float2(dv4.z, dv4.w);
     }
     part += __shfl_xor(part, 1);
     part += __shfl_xor(part, 2);
-    if ((tid & 3) == 0) sm.term[key] = part;
+    part += __shfl_xor(part, 4);
+    if ((tid & 7) == 0) sm.term[key] = part;
   }
   __syncthreads();
-  gate_cumsum(sm.G, sm.bsum, sm.glast);   // (bsum doubles as its scratch)
+  gate_cumsum<64 * kCW>(sm.G, sm.bsum, sm.glast);   // (bsum doubles as its scratch)
   if (w == 0) {   // block reference points
     float ep = 0.f;
 #pragma unroll
@@ -506,70 +520,71 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
   }
   __syncthreads();
 
-  const int I = w;   // this wavefront's row block
-  // ---- A and dA, rows of block I (zero above the diagonal); the q side
-  // (q e^(G - M_I)) of the A products is the same for every column block
-  float qa[2][8];
+  // ---- A and dA, rows of block I, column blocks J of this half (zero above
+  // the diagonal); the q side (q e^(G - M_I)) is the same for every J
+  {
+    float qa[2][8];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int kk = ks * 32 + grp * 8 + e, t = 16 * I + col;
-      qa[ks][e] = X(sm.q[t][kk]) * cexp2(sm.G[t][kk] - sm.M[I][kk]);
-    }
-  for (int J = 0; J < 4; ++J) {
-    f32x4 a4 = {0.f, 0.f, 0.f, 0.f}, d4 = {0.f, 0.f, 0.f, 0.f};
-    if (J <= I) {
-      const int t = 16 * I + col, s = 16 * J + col;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        float b[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int kk = ks * 32 + grp * 8 + e;
-          b[e] = X(sm.k[s][kk]) * cexp2(sm.M[I][kk] - sm.G[s][kk]);
-        }
-        a4 = mma3(qa[ks], b, a4);
+      for (int e = 0; e < 8; ++e) {
+        const int kk = ks * 32 + grp * 8 + e, t = 16 * I + col;
+        qa[ks][e] = X(sm.q[t][kk]) * cexp2(sm.G[t][kk] - sm.M[I][kk]);
       }
-      for (int vs = 0; vs < VP; vs += 32) {
-        float a[8], b[8];
+    for (int J = P; J < 4; J += 2) {
+      f32x4 a4 = {0.f, 0.f, 0.f, 0.f}, d4 = {0.f, 0.f, 0.f, 0.f};
+      if (J <= I) {
+        const int t = 16 * I + col, s = 16 * J + col;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int vc = vs + grp * 8 + e;
-          a[e] = X(sm.dout[t][vc]);
-          b[e] = X(sm.v[s][vc]);
+        for (int ks = 0; ks < 2; ++ks) {
+          float b[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int kk = ks * 32 + grp * 8 + e;
+            b[e] = X(sm.k[s][kk]) * cexp2(sm.M[I][kk] - sm.G[s][kk]);
+          }
+          a4 = mmax<false, false>(qa[ks], b, a4);
         }
-        d4 = mma3(a, b, d4);
-      }
-    }
+        for (int vs = 0; vs < VP; vs += 32) {
+          float a[8], b[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * I + grp * 4 + i, s = 16 * J + col;
-      const bool keep = J <= I && s <= t;
-      sm.u.p.A[t][s] = keep ? scale * a4[i] : 0.f;
-      sm.u.p.dA[t][s] = keep ? scale * d4[i] : 0.f;
+          for (int e = 0; e < 8; ++e) {
+            const int vc = vs + grp * 8 + e;
+            a[e] = X(sm.dout[t][vc]);
+            b[e] = X(sm.v[s][vc]);
+          }
+          d4 = mmax<EX, EX>(a, b, d4);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * I + grp * 4 + i, s = 16 * J + col;
+        const bool keep = J <= I && s <= t;
+        sm.u.p.A[t][s] = keep ? scale * a4[i] : 0.f;
+        sm.u.p.dA[t][s] = keep ? scale * d4[i] : 0.f;
+      }
     }
   }
   __syncthreads();
 
-  // ---- dq (rows t of block I), keys in 4 tiles
-  float dqv[4][4], dkv[4][4];
+  // ---- dq (rows t of block I), key tiles 2P, 2P + 1
+  float dqv[2][4], dkv[2][4];
   {
-    f32x4 ai[4], ae[4];
+    f32x4 ai[2], ae[2];
 #pragma unroll
-    for (int N = 0; N < 4; ++N) {
-      ai[N] = f32x4{0.f, 0.f, 0.f, 0.f};
-      ae[N] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nn = 0; nn < 2; ++nn) {
+      ai[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
+      ae[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     const int t = 16 * I + col;
     const int s_end = 16 * (I + 1);
     for (int ss = 0; ss < s_end; ss += 32) {   // intra: dA[t, s] (k e^(M_I - G))[s, key]
       float a[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) a[e] = (sm.u.p.dA[t][ss + grp * 8 + e]);
+      for (int e = 0; e < 8; ++e) a[e] = sm.u.p.dA[t][ss + grp * 8 + e];
 #pragma unroll
-      for (int N = 0; N < 4; ++N) {
-        const int key = N * 16 + col;
+      for (int nn = 0; nn < 2; ++nn) {
+        const int key = (2 * P + nn) * 16 + col;
         const float m = sm.M[I][key];
         float b[8];
 #pragma unroll
@@ -577,7 +592,7 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
           const int s = ss + grp * 8 + e;
           b[e] = s < s_end ? X(sm.k[s][key]) * cexp2(m - sm.G[s][key]) : 0.f;
         }
-        ai[N] = mma3(a, b, ai[N]);
+        ai[nn] = mmax<false, false>(a, b, ai[nn]);
       }
     }
     for (int vs = 0; vs < VP; vs += 32) {   // inter: do[t, v] h[c][key, v]
@@ -585,43 +600,40 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) a[e] = X(sm.dout[t][vs + grp * 8 + e]);
 #pragma unroll
-      for (int N = 0; N < 4; ++N) {
-        const int key = N * 16 + col;
+      for (int nn = 0; nn < 2; ++nn) {
+        const int key = (2 * P + nn) * 16 + col;
         float b[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int vc = vs + grp * 8 + e;
-          b[e] = sm.h[key][vc];
-        }
-        ae[N] = mma3(a, b, ae[N]);
+        for (int e = 0; e < 8; ++e) b[e] = sm.h[key][vs + grp * 8 + e];
+        ae[nn] = mmax<EX, false>(a, b, ae[nn]);
       }
     }
 #pragma unroll
-    for (int N = 0; N < 4; ++N)
+    for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int tt = 16 * I + grp * 4 + i, key = N * 16 + col;
+        const int tt = 16 * I + grp * 4 + i, key = (2 * P + nn) * 16 + col;
         const float gt = sm.G[tt][key];
-        dqv[N][i] = ai[N][i] * cexp2(gt - sm.M[I][key]) + scale * ae[N][i] * cexp2(gt);
+        dqv[nn][i] = ai[nn][i] * cexp2(gt - sm.M[I][key]) + scale * ae[nn][i] * cexp2(gt);
       }
   }
-  // ---- dk (rows s of block I)
+  // ---- dk (rows s of block I), key tiles 2P, 2P + 1
   {
-    f32x4 ai[4], ae[4];
+    f32x4 ai[2], ae[2];
 #pragma unroll
-    for (int N = 0; N < 4; ++N) {
-      ai[N] = f32x4{0.f, 0.f, 0.f, 0.f};
-      ae[N] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nn = 0; nn < 2; ++nn) {
+      ai[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
+      ae[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     const int s = 16 * I + col;
     const int t_beg = 16 * I;
     for (int ts = t_beg & ~31; ts < BT; ts += 32) {   // intra: dA[t, s] (q e^(G - M_I))[t, key]
       float a[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) a[e] = (sm.u.p.dA[ts + grp * 8 + e][s]);
+      for (int e = 0; e < 8; ++e) a[e] = sm.u.p.dA[ts + grp * 8 + e][s];
 #pragma unroll
-      for (int N = 0; N < 4; ++N) {
-        const int key = N * 16 + col;
+      for (int nn = 0; nn < 2; ++nn) {
+        const int key = (2 * P + nn) * 16 + col;
         const float m = sm.M[I][key];
         float b[8];
 #pragma unroll
@@ -629,7 +641,7 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
           const int t = ts + grp * 8 + e;
           b[e] = t >= t_beg ? X(sm.q[t][key]) * cexp2(sm.G[t][key] - m) : 0.f;
         }
-        ai[N] = mma3(a, b, ai[N]);
+        ai[nn] = mmax<false, false>(a, b, ai[nn]);
       }
     }
     for (int vs = 0; vs < VP; vs += 32) {   // inter: v[s, v] dh[c][key, v]
@@ -637,25 +649,25 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) a[e] = X(sm.v[s][vs + grp * 8 + e]);
 #pragma unroll
-      for (int N = 0; N < 4; ++N) {
-        const int key = N * 16 + col;
+      for (int nn = 0; nn < 2; ++nn) {
+        const int key = (2 * P + nn) * 16 + col;
         float b[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) b[e] = (sm.dh[key][vs + grp * 8 + e]);
-        ae[N] = mma3(a, b, ae[N]);
+        for (int e = 0; e < 8; ++e) b[e] = sm.dh[key][vs + grp * 8 + e];
+        ae[nn] = mmax<EX, false>(a, b, ae[nn]);
       }
     }
 #pragma unroll
-    for (int N = 0; N < 4; ++N)
+    for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int ss = 16 * I + grp * 4 + i, key = N * 16 + col;
+        const int ss = 16 * I + grp * 4 + i, key = (2 * P + nn) * 16 + col;
         const float gs = sm.G[ss][key];
-        dkv[N][i] = ai[N][i] * cexp2(sm.M[I][key] - gs) + ae[N][i] * cexp2(sm.glast[key] - gs);
+        dkv[nn][i] = ai[nn][i] * cexp2(sm.M[I][key] - gs) + ae[nn][i] * cexp2(sm.glast[key] - gs);
       }
   }
-  // ---- dv (rows s of block I), value columns in tiles of 16
-  for (int N = 0; N < VP / 16; ++N) {
+  // ---- dv (rows s of block I), value tiles N with N % 2 == P
+  for (int N = P; N < VP / 16; N += 2) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     const int s = 16 * I + col;
     const int vc = N * 16 + col;
@@ -665,10 +677,10 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int t = ts + grp * 8 + e;
-        a[e] = (sm.u.p.A[t][s]);
+        a[e] = sm.u.p.A[t][s];
         b[e] = X(sm.dout[t][vc]);
       }
-      acc = mma3(a, b, acc);
+      acc = mmax<false, EX>(a, b, acc);
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {   // inter: (k e^(G_last - G))[s, key] dh[c][key, v]
@@ -677,9 +689,9 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
       for (int e = 0; e < 8; ++e) {
         const int kk = ks * 32 + grp * 8 + e;
         a[e] = X(sm.k[s][kk]) * cexp2(sm.glast[kk] - sm.G[s][kk]);
-        b[e] = (sm.dh[kk][vc]);
+        b[e] = sm.dh[kk][vc];
       }
-      acc = mma3(a, b, acc);
+      acc = mmax<false, false>(a, b, acc);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -690,32 +702,32 @@ __global__ __launch_bounds__(256) void bwd_chunk_kernel(
   // ---- dq, dk out; r = q dq - k dk for dg
   __syncthreads();   // every wavefront is done with A and dA (r reuses them)
 #pragma unroll
-  for (int N = 0; N < 4; ++N)
+  for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int tt = 16 * I + grp * 4 + i, key = N * 16 + col;
-      sm.u.r[tt][key] = X(sm.q[tt][key]) * dqv[N][i] - X(sm.k[tt][key]) * dkv[N][i];
+      const int tt = 16 * I + grp * 4 + i, key = (2 * P + nn) * 16 + col;
+      sm.u.r[tt][key] = X(sm.q[tt][key]) * dqv[nn][i] - X(sm.k[tt][key]) * dkv[nn][i];
       if (tt < nrows) {
         const int64_t o = ((t0 + tt) * H + h) * KD + key;
-        dq[o] = Elt<DT>::b(dqv[N][i]);
-        dk[o] = Elt<DT>::b(dkv[N][i]);
+        dq[o] = Elt<DT>::b(dqv[nn][i]);
+        dk[o] = Elt<DT>::b(dkv[nn][i]);
       }
     }
   __syncthreads();
   // ---- dg: reverse cumsum over the chunk + the leaving-state term;
-  // thread (w, lane): key = lane, rows 16 w .. 16 w + 15
+  // thread (w, lane): key = lane, rows 8 w .. 8 w + 7
   {
     const int key = lane;
-    float s = 0.f;
+    float sacc = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s += sm.u.r[16 * w + r][key];
-    sm.bsum[w][key] = s;
+    for (int r = 0; r < 8; ++r) sacc += sm.u.r[8 * w + r][key];
+    sm.bsum[w][key] = sacc;
     __syncthreads();
     float run = sm.term[key];
-    for (int b = 3; b > w; --b) run += sm.bsum[b][key];
+    for (int b = kCW - 1; b > w; --b) run += sm.bsum[b][key];
 #pragma unroll
-    for (int r = 15; r >= 0; --r) {
-      const int tt = 16 * w + r;
+    for (int r = 7; r >= 0; --r) {
+      const int tt = 8 * w + r;
       run += sm.u.r[tt][key];
       if (tt < nrows) {
         const int64_t o = ((t0 + tt) * H + h) * KD + key;
@@ -778,7 +790,7 @@ int launch_bwd(const void *q, const void *k, const void *v, const void *g, const
   const int64_t fold_threads = static_cast<int64_t>(n_seq) * H * KD * V;
   hipLaunchKernelGGL(bwd_fold_kernel, dim3(static_cast<unsigned>((fold_threads + 255) / 256)), dim3(256), 0, st,
                      w.coff, w.sgoff, n_seq, H, V, h0, dht, w.eloc, w.dtot, w.dloc, w.sin_, w.dsend, dh0);
-  hipLaunchKernelGGL((bwd_chunk_kernel<DT, GF32>), dim3(static_cast<unsigned>(cmax * H)), dim3(256), 0, st, Q, Kp, Vp,
+  hipLaunchKernelGGL((bwd_chunk_kernel<DT, GF32>), dim3(static_cast<unsigned>(cmax * H)), dim3(64 * kCW), 0, st, Q, Kp, Vp,
                      g, DO, cu, w.coff, w.sgoff, n_seq, T, H, V, scale, w.hloc, w.dfw, w.dloc, w.drv, w.sin_,
                      w.dsend, static_cast<uint16_t *>(dq), static_cast<uint16_t *>(dk), static_cast<uint16_t *>(dv),
                      dg);

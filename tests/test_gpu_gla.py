@@ -162,5 +162,8 @@ def test_chunk_errors(dev):
     with pytest.raises(ValueError, match="number of initial states"):
         chunk_gla(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev), initial_state=s0[:1].to(dev))
     qg = q.to(dev).requires_grad_(True)
-    with pytest.raises(NotImplementedError):
-        chunk_gla(qg, k.to(dev), v.to(dev), g.to(dev), cu.to(dev))
+    o, _ = chunk_gla(qg, k.to(dev), v.to(dev), g.to(dev), cu.to(dev))
+    assert o.requires_grad   # V = 64 has a backward
+    v128 = torch.randn(30, 2, 128, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(NotImplementedError):   # V > 64 has none
+        chunk_gla(qg, k.to(dev), v128, g.to(dev), cu.to(dev))
