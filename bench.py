@@ -10,8 +10,10 @@ already resident in HBM.  Two input sets (2 x 203 MB, more than the 256 MB
 Infinity Cache) alternate so that the timed loop streams from HBM.
 
 Secondary lines (same JSON object): the per-site sparse GLA scan (config 3,
-64 bins per step) and the scatter-max pooling (config 4, 1e6 events, in
-shuffled order and sorted by cell).
+64 bins per step), the scatter-max pooling (config 4, 1e6 events, in
+shuffled order and sorted by cell), the chunk GLA backward at config 2, and
+the first stage of the MOS_S backbone (ingest, preprocess, two MosAttention
+layers, SparseMaxPool, TemporalDropout) on 8 synthetic Gen1 windows.
 
 Prints ONE JSON line.  Kernel durations come from HIP events recorded on
 the stream the kernels are launched on (torch's current stream, which is
@@ -191,6 +193,67 @@ def bench_pool(torch, lib, reps, dev, sorted_index=False):
                          "note": "whole call (bucketing + reduce), not one kernel"}}
 
 
+def bench_event_stage(torch, lib, reps, dev):
+    """First stage of the reference's MOS_S backbone (configs/model/MOS_S.yaml
+    layers 1-4, built as model_mos.py:32-122 builds them, run as
+    model_mos.py:157-209) over a C5-like batch of 8 Gen1 windows (~50k events
+    each): the .dat records are decoded and padded on the device (ingest,
+    PCIe copy of the records included), then preprocess ->
+    MosAttention(2 -> 12, k1) -> MosAttention(12, k3) -> SparseMaxPool(k2) ->
+    TemporalDropout(4), forward only.  Each step is timed with HIP events on
+    the current stream (host syncs inside a layer count)."""
+    import numpy as np
+    from ssla_amd import events as E, io, layers, synthetic
+    frame = (240, 304)
+    ev, ln = synthetic.event_windows()
+    recs = []
+    for b in range(ev.shape[0]):
+        x = ev[b, :int(ln[b])].numpy()
+        r = np.empty(x.shape[0], dtype=io.EV_TYPE)
+        r["t"] = x[:, 2].astype(np.uint32)
+        r["_"] = (x[:, 0].astype(np.int32) + (x[:, 1].astype(np.int32) << 14)
+                  + (((x[:, 3] + 1) // 2).astype(np.int32) << 28))
+        recs.append(r)
+    torch.manual_seed(0)
+    m1 = layers.MosAttention(2, 12, frame, (1, 1)).to(dev)
+    m2 = layers.MosAttention(12, 12, frame, (3, 3)).to(dev)
+    pool = layers.SparseMaxPool(frame, kernel_size=(2, 2)).to(dev)
+    drop = layers.TemporalDropout(4, pool.frame_output_size).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    names = ["ingest", "preprocess", "mos_k1_h12", "mos_k3_h12", "maxpool_k2", "tdrop_w4"]
+
+    def run(ev_marks):
+        x = io.pad_events(recs, dev)
+        ev_marks[1].record(stream)
+        x = E.preprocess_inputs(x[0], x[1].to(dev), frame, 50)
+        ev_marks[2].record(stream)
+        for i, m in enumerate((m1, m2, pool, drop)):
+            x = m(x)
+            ev_marks[3 + i].record(stream)
+        return x
+
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+    with torch.no_grad():
+        for _ in range(2):
+            marks[0].record(stream)
+            out = run(marks)
+        torch.cuda.synchronize()
+        tot = [0.0] * len(names)
+        for _ in range(reps):
+            marks[0].record(stream)
+            out = run(marks)
+            torch.cuda.synchronize()
+            for i in range(len(names)):
+                tot[i] += marks[i].elapsed_time(marks[i + 1])
+    per = {n: t / reps for n, t in zip(names, tot)}
+    ms = sum(per.values())
+    n_ev = int(ln.sum())
+    return {"workload": "MOS_S stage 1 forward on 8 Gen1 windows (C5-like, synthetic): ingest + preprocess + "
+                        "MosAttention k1/k3 (hidden 12) + SparseMaxPool k2 + TemporalDropout 4",
+            "metric": "stage-1 events/s", "value": n_ev / (ms * 1e-3), "unit": "events/s", "ms_per_call": ms,
+            "events_in": n_ev, "events_out": int(out["lengths"].sum()), "ms_per_step": per}
+
+
 def cpu_baseline(x, min_s=10.0):
     """The fp64 C restatement of naive_gla_recurrent (oracle/) on this host,
     run over the sequences of the same C2 batch, cycling through the batch
@@ -296,7 +359,7 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", choices=["chunk", "sparse", "pool", "pool_sorted", "chunk_bwd"], default=None,
+    ap.add_argument("--only", choices=["chunk", "sparse", "pool", "pool_sorted", "chunk_bwd", "event_stage"], default=None,
                     help="run one workload and print its line (profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 256 MiB device copies (counter calibration) and exit")
@@ -320,6 +383,9 @@ def main(argv=None):
         return 0
     if args.only == "chunk_bwd":
         print(json.dumps(bench_chunk_bwd(torch, lib, args.steps, dev)), flush=True)
+        return 0
+    if args.only == "event_stage":
+        print(json.dumps(bench_event_stage(torch, lib, args.steps, dev)), flush=True)
         return 0
     if args.only in ("pool", "pool_sorted"):
         print(json.dumps(bench_pool(torch, lib, args.steps, dev, args.only == "pool_sorted")), flush=True)
@@ -351,7 +417,8 @@ def main(argv=None):
     }
     if not args.no_secondary and args.only is None:
         line["secondary"] = [bench_sparse(torch, lib, 10, dev), bench_pool(torch, lib, 20, dev),
-                             bench_pool(torch, lib, 20, dev, sorted_index=True), bench_chunk_bwd(torch, lib, 10, dev)]
+                             bench_pool(torch, lib, 20, dev, sorted_index=True), bench_chunk_bwd(torch, lib, 10, dev),
+                             bench_event_stage(torch, lib, 5, dev)]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(r["sample"])
     print(json.dumps(line), flush=True)

@@ -272,6 +272,30 @@ size_t ssla_index_add_rows_workspace_size(int64_t n);
 int ssla_index_add_rows(const float *src, const int64_t *idx, int64_t n, int C, int64_t n_out, float *out,
                         void *workspace, size_t workspace_bytes, void *stream);
 
+/* Fused MosAttention forward (inference): everything of MosAttention.forward
+ * (layers/mos_attention.py:75-140) after scatter_group_events_to_patch --
+ * _apply_scatter_proj and _apply_gather_proj (:148-167), q/v/g projections,
+ * sigmoid, scan (ops/common/scan.py:20-43), o_proj,
+ * gather_patch_events_to_group (utils/async_utils.py:243-264), input_proj,
+ * the residual and LayerNorm -- in three kernels with no intermediate sort.
+ * Rows come from ssla_rf_scatter_fill (row_src, row_pos, patch_len of the
+ * n_patches active patches; rows of a patch consecutive and in time order).
+ * Weights fp32 as the reference module holds them: w_scatter
+ * [A or 1, hidden, c_in] (scatter_per_pos = 0: one matrix), w_q/w_v/w_g/w_o
+ * [hidden, hidden], w_gather [A or 1, hidden, hidden], w_in [hidden, c_in]
+ * or NULL (then c_in == hidden), ln_w/ln_b [hidden], eps.  out [n_events,
+ * hidden].  Supports c_in, hidden <= 32, A <= 49 and weights that fit 64 KB
+ * of LDS (ssla_mos_attention_lds_bytes); SSLA_ERR_UNSUPPORTED otherwise. */
+size_t ssla_mos_attention_workspace_size(int64_t n_events, int c_in, int hidden, int A, int64_t n_rows,
+                                         int64_t n_patches);
+size_t ssla_mos_attention_lds_bytes(int c_in, int hidden, int A, int scatter_per_pos, int gather_per_pos);
+int ssla_mos_attention_fwd(const float *events, int64_t n_events, int c_in, const int64_t *row_src,
+                           const int64_t *row_pos, int64_t n_rows, const int64_t *patch_len, int64_t n_patches,
+                           int A, const float *w_scatter, int scatter_per_pos, const float *w_q, const float *w_v,
+                           const float *w_g, const float *w_o, const float *w_gather, int gather_per_pos,
+                           const float *w_in, const float *ln_w, const float *ln_b, float eps, int hidden,
+                           float *out, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Stable sort of (uint64 key, int32 value) pairs on the low end_bit key
  * bits; vals_in NULL means 0..n-1.  Used for the (batch, time) ordering of
  * LinearAttention.forward (layers/linear_attention.py:62-63) and the

@@ -61,6 +61,10 @@ SIGNATURES = {
     "ssla_gather_rows": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _vp]),
     "ssla_index_add_rows_workspace_size": (_sz, [_i64]),
     "ssla_index_add_rows": (_i32, [_vp, _vp, _i64, _i32, _i64, _vp, _vp, _sz, _vp]),
+    "ssla_mos_attention_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i64, _i64]),
+    "ssla_mos_attention_lds_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "ssla_mos_attention_fwd": (_i32, [_vp, _i64, _i32, _vp, _vp, _i64, _vp, _i64, _i32, _vp, _i32, _vp, _vp, _vp,
+                                      _vp, _vp, _i32, _vp, _vp, _vp, _f32, _i32, _vp, _vp, _sz, _vp]),
     "ssla_sort_pairs_workspace_size": (_sz, [_i64]),
     "ssla_sort_pairs": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
     "ssla_segments_workspace_size": (_sz, [_i64]),

@@ -1,0 +1,467 @@
+// Fused MosAttention forward on gfx950 (inference path).
+//
+// Reference: layers/mos_attention.py:75-140 after scatter_group_events_to_patch
+// (utils/async_utils.py:125-240), with _apply_scatter_proj / _apply_gather_proj
+// (mos_attention.py:148-167), scan (ops/common/scan.py:20-43) and
+// gather_patch_events_to_group (utils/async_utils.py:243-264).  Per patch row
+// r (rows of one patch consecutive, in time order; src[r] the pixel event,
+// pos[r] its kernel position):
+//   x   = Ws[pos] e[src]                  (scatter projection)
+//   q   = Wq x,  v = Wv x,  a = sigmoid(Wg x)
+//   h_r = a_r h_(r-1) + v_r               (h = 0 before each patch)
+//   o_r = Wgp[pos] (Wo (q h))             (o_proj, then gather projection)
+// and per pixel event e:
+//   y_e = LayerNorm(sum over the copies r of e of o_r + (Win e or e)).
+//
+// Kernels:
+// * mos_mark_starts / mos_dst_fill -- patch-start flags from the patch
+//   lengths, and the inverse of the row -> (event, position) map:
+//   dst[e * A + pos] = r (each pair occurs at most once), so the sum over an
+//   event's copies needs no sort.
+// * mos_patch_kernel -- one lane per patch row: the projections run in
+//   registers with the weights in LDS (position-dependent matrices padded so
+//   that lanes reading different positions hit different banks), the
+//   recurrence is a segmented scan of the pairs (a, v) across the wavefront
+//   (combine (A1, B1) then (A2, B2) = (A1 A2, A2 B1 + B2), restarted at patch
+//   starts), carried from one 64-row window to the next.  Each wavefront
+//   owns a window of rows [k L, (k + 1) L) shifted to patch boundaries: it
+//   starts at the first patch start at or after k L and finishes the patch
+//   that crosses (k + 1) L, so no patch is split between wavefronts.
+// * mos_event_kernel -- one lane per pixel event: the copies summed in
+//   increasing patch order (decreasing kernel position), the residual (or its
+//   input projection) added, then LayerNorm over the hidden channels.
+// All arithmetic is fp32.
+#include <cstring>
+#include <rocprim/rocprim.hpp>
+
+#include "common.h"
+
+namespace ssla {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWin = 256;       // rows per wavefront window (before the shift to patch boundaries)
+constexpr int kMaxPos = 49;     // kernel positions (up to 7 x 7)
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+inline unsigned grid_for(int64_t n) {
+  return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((n + kThreads - 1) / kThreads, 1 << 20)));
+}
+#define MOS_GRID_STRIDE(i, n)                                                                   \
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < (n);      \
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+
+struct MosWs {
+  int64_t *cu;       // [n_patch + 1] exclusive scan of the patch lengths
+  uint8_t *start;    // [R] 1 at the first row of every patch
+  int32_t *dst;      // [E * A] row of (event, position), or -1
+  float *orow;       // [R, HP] projected rows
+  void *tmp;
+  size_t tmp_bytes, total;
+};
+
+size_t scan_bytes(int64_t n) {
+  size_t tb = 0;
+  (void)rocprim::exclusive_scan(nullptr, tb, static_cast<int64_t *>(nullptr), static_cast<int64_t *>(nullptr),
+                          static_cast<int64_t>(0), static_cast<size_t>(std::max<int64_t>(n, 1)),
+                          rocprim::plus<int64_t>());
+  return tb;
+}
+
+MosWs mos_layout(void *base, int64_t E, int A, int64_t R, int64_t n_patch, int HP) {
+  char *b = static_cast<char *>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char *p = b ? b + off : nullptr;
+    off = align256(off + std::max<size_t>(bytes, 1));
+    return p;
+  };
+  MosWs w;
+  w.cu = reinterpret_cast<int64_t *>(take(sizeof(int64_t) * (n_patch + 1)));
+  w.start = reinterpret_cast<uint8_t *>(take(static_cast<size_t>(R)));
+  w.dst = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * static_cast<size_t>(E) * A));
+  w.orow = reinterpret_cast<float *>(take(sizeof(float) * static_cast<size_t>(R) * HP));
+  w.tmp_bytes = scan_bytes(n_patch);
+  w.tmp = take(w.tmp_bytes);
+  w.total = off;
+  return w;
+}
+
+__global__ void mos_fill_u8(uint8_t *p, int64_t n) { MOS_GRID_STRIDE(i, n) p[i] = 0; }
+__global__ void mos_fill_i32(int32_t *p, int64_t n, int32_t v) { MOS_GRID_STRIDE(i, n) p[i] = v; }
+
+// start[cu[p]] = 1 for every patch (empty patches mark the next patch's
+// first row, which is a start anyway).
+__global__ void mos_mark_starts(const int64_t *__restrict__ cu, int64_t n_patch, int64_t R,
+                                uint8_t *__restrict__ start) {
+  if (blockIdx.x == 0 && threadIdx.x == 0 && R > 0) start[0] = 1;   // rows before the first patch: none
+  MOS_GRID_STRIDE(p, n_patch) {
+    const int64_t r = cu[p];
+    if (r >= 0 && r < R) start[r] = 1;
+  }
+}
+
+__global__ void mos_dst_fill(const int64_t *__restrict__ src, const int64_t *__restrict__ pos, int64_t R,
+                             int64_t E, int A, int32_t *__restrict__ dst) {
+  MOS_GRID_STRIDE(r, R) {
+    const int64_t s = src[r], a = pos[r];
+    if (s >= 0 && s < E && a >= 0 && a < A) dst[s * A + a] = static_cast<int32_t>(r);
+  }
+}
+
+// LDS weight layout (floats): position-dependent matrices are padded by 4
+// floats each so that lanes on different positions read different banks.
+template <int CP, int HP>
+struct MosW {
+  static constexpr int kS = HP * CP + 4;   // scatter matrix stride
+  static constexpr int kG = HP * HP + 4;   // gather matrix stride
+  static constexpr int kU = HP * HP;       // uniform matrices
+  static size_t bytes(int As, int Ag) { return sizeof(float) * (static_cast<size_t>(As) * kS + Ag * kG + 4 * kU); }
+};
+
+// Fill the padded LDS copy of the weights (zeros outside cin x hid).
+template <int CP, int HP>
+__device__ void load_weights(float *sw, const float *ws, int As, const float *wq, const float *wv, const float *wg,
+                             const float *wo, const float *wgp, int Ag, int cin, int hid) {
+  typedef MosW<CP, HP> L;
+  float *s_s = sw, *s_g = sw + As * L::kS, *s_u = s_g + Ag * L::kG;
+  const int n_s = As * L::kS, n_g = Ag * L::kG;
+  for (int i = threadIdx.x; i < n_s; i += blockDim.x) {
+    const int a = i / L::kS, o = i % L::kS, j = o / CP, c = o % CP;
+    s_s[i] = (o < HP * CP && j < hid && c < cin) ? ws[(static_cast<int64_t>(a) * hid + j) * cin + c] : 0.f;
+  }
+  for (int i = threadIdx.x; i < n_g; i += blockDim.x) {
+    const int a = i / L::kG, o = i % L::kG, j = o / HP, c = o % HP;
+    s_g[i] = (o < HP * HP && j < hid && c < hid) ? wgp[(static_cast<int64_t>(a) * hid + j) * hid + c] : 0.f;
+  }
+  for (int i = threadIdx.x; i < 4 * L::kU; i += blockDim.x) {
+    const int m = i / L::kU, o = i % L::kU, j = o / HP, c = o % HP;
+    const float *src = m == 0 ? wq : m == 1 ? wv : m == 2 ? wg : wo;
+    s_u[i] = (j < hid && c < hid) ? src[j * hid + c] : 0.f;
+  }
+}
+
+// First row >= x that starts a patch (R if none): 64 flags per step.
+__device__ __forceinline__ int64_t next_start(const uint8_t *__restrict__ start, int64_t x, int64_t R, int lane) {
+  for (int64_t y = x; y < R; y += 64) {
+    const int64_t r = y + lane;
+    const bool f = r < R && start[r] != 0;
+    const unsigned long long m = __ballot(f);
+    if (m) return y + __builtin_ctzll(m);
+  }
+  return R;
+}
+
+template <int CP, int HP>
+__global__ __launch_bounds__(kThreads) void mos_patch_kernel(
+    const float *__restrict__ ev, int64_t E, int cin, int hid, const int64_t *__restrict__ src,
+    const int64_t *__restrict__ pos, int64_t R, const uint8_t *__restrict__ start, int A,
+    const float *__restrict__ ws, int As, const float *__restrict__ wq, const float *__restrict__ wv,
+    const float *__restrict__ wg, const float *__restrict__ wo, const float *__restrict__ wgp, int Ag,
+    float *__restrict__ orow) {
+  typedef MosW<CP, HP> L;
+  extern __shared__ float sw[];
+  load_weights<CP, HP>(sw, ws, As, wq, wv, wg, wo, wgp, Ag, cin, hid);
+  __syncthreads();
+  const float *s_s = sw, *s_g = sw + As * L::kS, *s_u = s_g + Ag * L::kG;
+  const float *s_q = s_u, *s_v = s_u + L::kU, *s_a = s_u + 2 * L::kU, *s_o = s_u + 3 * L::kU;
+
+  const int lane = threadIdx.x & 63;
+  const int64_t n_win = (R + kWin - 1) / kWin;
+  const int64_t wave0 = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * (kThreads / 64);
+  for (int64_t k = wave0; k < n_win; k += n_waves) {
+    const int64_t rs = next_start(start, k * kWin, R, lane);
+    const int64_t re = next_start(start, std::min<int64_t>((k + 1) * kWin, R), R, lane);
+    float carry[HP];
+#pragma unroll
+    for (int j = 0; j < HP; ++j) carry[j] = 0.f;
+    for (int64_t b = rs; b < re; b += 64) {
+      // weights are re-read from LDS each window (broadcast reads) rather
+      // than hoisted into registers, which would cost all the occupancy
+      asm volatile("" ::: "memory");
+      const int64_t r = b + lane;
+      const bool valid = r < re;
+      int flag = 1;
+      float e[CP];
+      int ps = 0, pg = 0;
+      if (valid) {
+        flag = start[r] != 0;
+        const int64_t s = min(max(src[r], (int64_t)0), E - 1);
+        const int p = static_cast<int>(min(max(pos[r], (int64_t)0), static_cast<int64_t>(A - 1)));
+        ps = As > 1 ? p : 0;
+        pg = Ag > 1 ? p : 0;
+#pragma unroll
+        for (int c = 0; c < CP; ++c) e[c] = c < cin ? ev[s * cin + c] : 0.f;
+      } else {
+#pragma unroll
+        for (int c = 0; c < CP; ++c) e[c] = 0.f;
+      }
+      // scatter projection
+      float x[HP];
+      {
+        const float *m = s_s + ps * L::kS;
+#pragma unroll
+        for (int j = 0; j < HP; ++j) {
+          float acc = 0.f;
+#pragma unroll
+          for (int c = 0; c < CP; ++c) acc = fmaf(m[j * CP + c], e[c], acc);
+          x[j] = acc;
+        }
+      }
+      // q, v, gate
+      float q[HP], A_[HP], B_[HP];
+#pragma unroll
+      for (int j = 0; j < HP; ++j) {
+        float aq = 0.f, av = 0.f, ag = 0.f;
+#pragma unroll
+        for (int c = 0; c < HP; ++c) {
+          aq = fmaf(s_q[j * HP + c], x[c], aq);
+          av = fmaf(s_v[j * HP + c], x[c], av);
+          ag = fmaf(s_a[j * HP + c], x[c], ag);
+        }
+        q[j] = aq;
+        B_[j] = av;
+        A_[j] = 1.f / (1.f + expf(-ag));
+      }
+      // segmented inclusive scan of (A, B) across the wavefront
+      int F = flag;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int Fp = __shfl_up(F, d);
+        const bool take = lane >= d && !F;
+#pragma unroll
+        for (int j = 0; j < HP; ++j) {
+          const float Ap = __shfl_up(A_[j], d), Bp = __shfl_up(B_[j], d);
+          if (take) {
+            B_[j] = fmaf(A_[j], Bp, B_[j]);
+            A_[j] = A_[j] * Ap;
+          }
+        }
+        if (lane >= d) F |= Fp;
+      }
+      // rows whose patch started before this window continue the carry
+      float hq[HP];
+#pragma unroll
+      for (int j = 0; j < HP; ++j) {
+        const float h = F ? B_[j] : fmaf(A_[j], carry[j], B_[j]);
+        carry[j] = __shfl(h, 63);
+        hq[j] = q[j] * h;
+      }
+      // o_proj, then the gather projection
+      float o[HP];
+#pragma unroll
+      for (int j = 0; j < HP; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < HP; ++c) acc = fmaf(s_o[j * HP + c], hq[c], acc);
+        o[j] = acc;
+      }
+      if (valid) {
+        const float *m = s_g + pg * L::kG;
+        float *dst = orow + r * HP;
+#pragma unroll
+        for (int j = 0; j < HP; j += 4) {
+          float4 y;
+          float *yy = reinterpret_cast<float *>(&y);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            float acc = 0.f;
+            if (j + u < HP) {
+#pragma unroll
+              for (int c = 0; c < HP; ++c) acc = fmaf(m[(j + u) * HP + c], o[c], acc);
+            }
+            yy[u] = acc;
+          }
+          *reinterpret_cast<float4 *>(dst + j) = y;
+        }
+      }
+    }
+  }
+}
+
+// One lane per pixel event: sum of its copies, residual, LayerNorm.
+template <int CP, int HP>
+__global__ __launch_bounds__(kThreads) void mos_event_kernel(
+    const float *__restrict__ ev, int64_t E, int cin, int hid, int A, const int32_t *__restrict__ dst,
+    const float *__restrict__ orow, int64_t R, const float *__restrict__ win, const float *__restrict__ ln_w,
+    const float *__restrict__ ln_b, float eps, float *__restrict__ out) {
+  __shared__ float s_in[HP * CP], s_w[HP], s_b[HP];
+  for (int i = threadIdx.x; i < HP * CP; i += blockDim.x) {
+    const int j = i / CP, c = i % CP;
+    s_in[i] = (win && j < hid && c < cin) ? win[j * cin + c] : 0.f;
+  }
+  for (int i = threadIdx.x; i < HP; i += blockDim.x) {
+    s_w[i] = i < hid ? ln_w[i] : 0.f;
+    s_b[i] = i < hid ? ln_b[i] : 0.f;
+  }
+  __syncthreads();
+  MOS_GRID_STRIDE(e, E) {
+    asm volatile("" ::: "memory");   // keep the weights in LDS, not in registers
+    float y[HP];
+#pragma unroll
+    for (int j = 0; j < HP; ++j) y[j] = 0.f;
+    for (int a = A - 1; a >= 0; --a) {
+      const int32_t r = dst[e * A + a];
+      if (r < 0 || r >= R) continue;
+      const float *o = orow + static_cast<int64_t>(r) * HP;
+#pragma unroll
+      for (int j = 0; j < HP; j += 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(o + j);
+        y[j] += t.x;
+        if (j + 1 < HP) y[j + 1] += t.y;
+        if (j + 2 < HP) y[j + 2] += t.z;
+        if (j + 3 < HP) y[j + 3] += t.w;
+      }
+    }
+    float x[CP];
+#pragma unroll
+    for (int c = 0; c < CP; ++c) x[c] = c < cin ? ev[e * cin + c] : 0.f;
+    if (win) {
+#pragma unroll
+      for (int j = 0; j < HP; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < CP; ++c) acc = fmaf(s_in[j * CP + c], x[c], acc);
+        y[j] += acc;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < HP; ++j) y[j] += (j < CP && j < cin) ? x[j < CP ? j : 0] : 0.f;
+    }
+    float mean = 0.f;
+#pragma unroll
+    for (int j = 0; j < HP; ++j) mean += j < hid ? y[j] : 0.f;
+    mean /= static_cast<float>(hid);
+    float var = 0.f;
+#pragma unroll
+    for (int j = 0; j < HP; ++j) {
+      const float d = y[j] - mean;
+      var += j < hid ? d * d : 0.f;
+    }
+    var /= static_cast<float>(hid);
+    const float rstd = 1.f / sqrtf(var + eps);
+#pragma unroll
+    for (int j = 0; j < HP; ++j)
+      if (j < hid) out[e * hid + j] = (y[j] - mean) * rstd * s_w[j] + s_b[j];
+  }
+}
+
+template <int CP, int HP>
+int launch_mos(const float *ev, int64_t E, int cin, int hid, const int64_t *src, const int64_t *pos, int64_t R,
+               int A, const float *ws, int As, const float *wq, const float *wv, const float *wg, const float *wo,
+               const float *wgp, int Ag, const float *win, const float *ln_w, const float *ln_b, float eps,
+               float *out, const MosWs &w, hipStream_t st) {
+  const size_t lds = MosW<CP, HP>::bytes(As, Ag);
+  if (R > 0) {
+    const int64_t n_win = (R + kWin - 1) / kWin;
+    const int64_t wgs = std::min<int64_t>((n_win + 3) / 4, 4096);
+    hipLaunchKernelGGL((mos_patch_kernel<CP, HP>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads), lds, st, ev, E,
+                       cin, hid, src, pos, R, w.start, A, ws, As, wq, wv, wg, wo, wgp, Ag, w.orow);
+  }
+  if (E > 0)
+    hipLaunchKernelGGL((mos_event_kernel<CP, HP>), dim3(grid_for(E)), dim3(kThreads), 0, st, ev, E, cin, hid, A,
+                       w.dst, w.orow, R, win, ln_w, ln_b, eps, out);
+  return launch_status("mos_attention_fwd");
+}
+
+// (cin, hid) -> the instantiated (CP, HP) that runs it ({0, 0}: not
+// supported): the first template, in order of cost, that covers both sizes
+// (the reference model's layers have exact ones).
+struct Tpl {
+  int cp, hp;
+};
+constexpr Tpl kTpls[] = {{2, 12}, {12, 12}, {16, 16}, {12, 24}, {24, 24}, {24, 32}, {32, 32}};
+inline Tpl pick_tpl(int cin, int hid) {
+  if (cin <= 0 || hid <= 0) return {0, 0};
+  for (const Tpl &t : kTpls)
+    if (cin <= t.cp && hid <= t.hp) return t;
+  return {0, 0};
+}
+
+}  // namespace
+}  // namespace ssla
+
+extern "C" size_t ssla_mos_attention_workspace_size(int64_t n_events, int c_in, int hidden, int A, int64_t n_rows,
+                                                    int64_t n_patches) {
+  using namespace ssla;
+  const Tpl t = pick_tpl(c_in, hidden);
+  if (n_events < 0 || A <= 0 || n_rows < 0 || n_patches < 0 || t.hp == 0) return 0;
+  return mos_layout(nullptr, n_events, A, n_rows, n_patches, t.hp).total;
+}
+
+extern "C" size_t ssla_mos_attention_lds_bytes(int c_in, int hidden, int A, int scatter_per_pos, int gather_per_pos) {
+  using namespace ssla;
+  const Tpl t = pick_tpl(c_in, hidden);
+  if (t.hp == 0 || A <= 0) return 0;
+  const int As = scatter_per_pos ? A : 1, Ag = gather_per_pos ? A : 1;
+  return sizeof(float) * (static_cast<size_t>(As) * (t.hp * t.cp + 4) + static_cast<size_t>(Ag) * (t.hp * t.hp + 4) +
+                          4 * static_cast<size_t>(t.hp) * t.hp);
+}
+
+extern "C" int ssla_mos_attention_fwd(const float *events, int64_t n_events, int c_in, const int64_t *row_src,
+                                      const int64_t *row_pos, int64_t n_rows, const int64_t *patch_len,
+                                      int64_t n_patches, int A, const float *w_scatter, int scatter_per_pos,
+                                      const float *w_q, const float *w_v, const float *w_g, const float *w_o,
+                                      const float *w_gather, int gather_per_pos, const float *w_in,
+                                      const float *ln_w, const float *ln_b, float eps, int hidden, float *out,
+                                      void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace ssla;
+  clear_error();
+  SSLA_CHECK_ARG(n_events >= 0 && n_rows >= 0 && n_patches >= 0 && c_in > 0 && hidden > 0 && A > 0,
+                 "mos_attention_fwd: bad sizes E=%lld R=%lld P=%lld cin=%d hidden=%d A=%d", (long long)n_events,
+                 (long long)n_rows, (long long)n_patches, c_in, hidden, A);
+  const Tpl tpl = pick_tpl(c_in, hidden);
+  if (tpl.hp == 0 || A > kMaxPos) {
+    set_error("mos_attention_fwd: needs input and hidden sizes up to 32 and at most %d kernel positions "
+              "(cin=%d hidden=%d A=%d)", kMaxPos, c_in, hidden, A);
+    return SSLA_ERR_UNSUPPORTED;
+  }
+  if (!w_in && c_in != hidden) {
+    set_error("mos_attention_fwd: input size %d differs from hidden %d but no input projection given", c_in, hidden);
+    return SSLA_ERR_ARG;
+  }
+  const size_t lds = ssla_mos_attention_lds_bytes(c_in, hidden, A, scatter_per_pos, gather_per_pos);
+  if (lds > 64 * 1024) {
+    set_error("mos_attention_fwd: weights need %zu bytes of LDS (at most 65536)", lds);
+    return SSLA_ERR_UNSUPPORTED;
+  }
+  SSLA_CHECK_ARG(n_rows < 0x7fffffff && n_events * A < (int64_t{1} << 40), "mos_attention_fwd: too many rows");
+  if (n_events == 0) return SSLA_OK;
+  SSLA_CHECK_ARG(events && out && w_scatter && w_q && w_v && w_g && w_o && w_gather && ln_w && ln_b,
+                 "mos_attention_fwd: null pointer");
+  SSLA_CHECK_ARG(n_rows == 0 || (row_src && row_pos && patch_len), "mos_attention_fwd: null row arrays");
+  const MosWs w = mos_layout(workspace, n_events, A, n_rows, n_patches, tpl.hp);
+  if (!workspace || workspace_bytes < w.total) {
+    set_error("mos_attention_fwd: workspace of %zu bytes needed, %zu given", w.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(mos_fill_i32, dim3(grid_for(n_events * A)), dim3(kThreads), 0, st, w.dst, n_events * A, -1);
+  if (n_rows > 0) {
+    hipLaunchKernelGGL(mos_fill_u8, dim3(grid_for(n_rows)), dim3(kThreads), 0, st, w.start, n_rows);
+    if (n_patches > 0) {
+      size_t tb = w.tmp_bytes;
+      const hipError_t e = rocprim::exclusive_scan(w.tmp, tb, patch_len, w.cu, static_cast<int64_t>(0),
+                                                   static_cast<size_t>(n_patches), rocprim::plus<int64_t>(), st);
+      if (e != hipSuccess) {
+        set_error("mos_attention_fwd: prefix sum failed: %s", hipGetErrorString(e));
+        return SSLA_ERR_LAUNCH;
+      }
+      hipLaunchKernelGGL(mos_mark_starts, dim3(grid_for(n_patches)), dim3(kThreads), 0, st, w.cu, n_patches, n_rows,
+                         w.start);
+    }
+    hipLaunchKernelGGL(mos_dst_fill, dim3(grid_for(n_rows)), dim3(kThreads), 0, st, row_src, row_pos, n_rows,
+                       n_events, A, w.dst);
+  }
+  const int As = scatter_per_pos ? A : 1, Ag = gather_per_pos ? A : 1;
+#define MOS_CASE(C, H)                                                                                          \
+  if (tpl.cp == C && tpl.hp == H)                                                                               \
+    return launch_mos<C, H>(events, n_events, c_in, hidden, row_src, row_pos, n_rows, A, w_scatter, As, w_q, w_v, \
+                            w_g, w_o, w_gather, Ag, w_in, ln_w, ln_b, eps, out, w, st);
+  MOS_CASE(2, 12) MOS_CASE(12, 12) MOS_CASE(16, 16) MOS_CASE(12, 24) MOS_CASE(24, 24) MOS_CASE(24, 32)
+  MOS_CASE(32, 32)
+#undef MOS_CASE
+  set_error("mos_attention_fwd: no kernel for cin=%d hidden=%d", c_in, hidden);
+  return SSLA_ERR_UNSUPPORTED;
+}

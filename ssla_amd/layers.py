@@ -130,11 +130,51 @@ class MosAttention(nn.Module):
             return F.linear(x, w[0])
         return _grouped_linear(x, pos, w)
 
-    def forward(self, inputs):
+    def _fused_ok(self, events):
+        """The fused forward (ssla_mos_attention_fwd) runs when no gradient is
+        recorded and the weights fit its kernels (input, hidden <= 32)."""
+        if torch.is_grad_enabled() and (events.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        A = self.kernel_size[0] * self.kernel_size[1]
+        lds = _lib.load().ssla_mos_attention_lds_bytes(self.input_size, self.hidden_size, A, int(self.scatter_proj),
+                                                       int(self.gather_proj))
+        return 0 < lds <= 64 * 1024
+
+    def _forward_fused(self, inputs, dev):
+        events = inputs["events"].to(torch.float32).contiguous()
+        src, _tim, pos, _f_index, f_len, _n_rf = E._rf_scatter(inputs, self.frame_size, self.patch2pixel_lut)
+        A = self.kernel_size[0] * self.kernel_size[1]
+        n, R, P = events.shape[0], src.numel(), f_len.numel()
+        lib = _lib.load()
+        ws = E._ws(lib.ssla_mos_attention_workspace_size(n, self.input_size, self.hidden_size, A, R, P), dev)
+        out = torch.empty(n, self.hidden_size, dtype=torch.float32, device=dev)
+        f32 = lambda t: t.detach().to(torch.float32).contiguous()   # noqa: E731
+        w = [f32(x) for x in (self.scatter_conv_weights, self.q_proj.weight, self.v_proj.weight, self.g_proj.weight,
+                              self.o_proj.weight, self.gather_conv_weights, self.norm.weight, self.norm.bias)]
+        w_in = f32(self.input_proj.weight) if self.input_proj is not None else None
+        _lib.check(lib.ssla_mos_attention_fwd(
+            _lib.ptr(events), n, self.input_size, _lib.ptr(src), _lib.ptr(pos), R, _lib.ptr(f_len), P, A,
+            _lib.ptr(w[0]), int(self.scatter_proj), _lib.ptr(w[1]), _lib.ptr(w[2]), _lib.ptr(w[3]), _lib.ptr(w[4]),
+            _lib.ptr(w[5]), int(self.gather_proj), _lib.ptr(w_in) if w_in is not None else None, _lib.ptr(w[6]),
+            _lib.ptr(w[7]), float(self.norm.eps), self.hidden_size, _lib.ptr(out), _lib.ptr(ws), ws.numel(),
+            _lib.stream_of(events)), "mos_attention_fwd")
+        return out
+
+    def forward(self, inputs, fused=None):
+        """fused: None picks the fused forward whenever it applies; False
+        forces the composed (differentiable) path; True requires the fused
+        one (SslaError if it does not apply)."""
         events = inputs["events"]
         lengths = inputs["lengths"]
         dev = _lib.require_cuda(events, lengths)
         _ensure_lut(self, "patch2pixel_lut", None, self.frame_size, self.kernel_size, self.stride, dev)
+        use_fused = self._fused_ok(events) if fused is None else bool(fused)
+        if use_fused:
+            if fused and not self._fused_ok(events):
+                raise _lib.SslaError("fused MosAttention forward needs no grad, input and hidden sizes <= 32")
+            out = self._forward_fused(inputs, dev)
+            return {"events": out, "time": inputs["time"], "w": inputs["w"], "h": inputs["h"],
+                    "batch_id": inputs["batch_id"], "lengths": lengths, "batch_size": inputs["batch_size"]}
         patch = E.scatter_group_events_to_patch(inputs, self.frame_size, self.patch2pixel_lut)
         p_len, p_ev, p_pos = patch["lengths"], patch["events"], patch["pos_id"]
         x = self._project(p_ev, p_pos, self.scatter_conv_weights, self.scatter_proj, self.input_size)

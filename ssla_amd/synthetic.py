@@ -13,6 +13,10 @@ the device by the caller):
 * :func:`pooling_events` -- 1e6 events on 304x240 (70 % in 20 Gaussian
   clusters of sigma 8 px, 30 % uniform) with C=64 fp32 features, pooled
   2x2 into the 152x120 cell grid.
+* :func:`event_windows` -- a batch of Gen1 windows (304x240 sensor, 100 ms
+  each, about 50k events per window from the same cluster mixture, t
+  sorted and uniform in the window, polarity +-1 equiprobable) as the padded
+  <x, y, t, p> batch the model's preprocessing takes.
 """
 from __future__ import annotations
 
@@ -115,3 +119,34 @@ def pooling_events(E=1_000_000, C=64, W=304, Hp=240, n_clusters=20, sigma=8.0, s
     gen = torch.Generator().manual_seed(seed)
     src = torch.randn(E, C, generator=gen)
     return src, torch.from_numpy(index), Wc * (Hp // 2)
+
+
+def event_windows(B=8, n_mean=50_000, W=304, Hp=240, window_us=100_000, n_clusters=20, sigma=8.0, seed=0):
+    """Returns (events fp32 [B, N, 4] as <x, y, t, p>, lengths int64 [B]):
+    window b holds n_mean * (0.8 + 0.4 * b / (B - 1)) events (ragged
+    batch), 70 % in Gaussian clusters (sigma px) around centres that drift
+    across the window, 30 % uniform; t (microseconds) sorted uniform in
+    [0, window_us); p = +-1; rows past a window's length are (0, 0, 0, -1),
+    the padding of the reference's collate."""
+    rng = np.random.default_rng(seed)
+    lens = [int(n_mean * (0.8 + 0.4 * b / max(B - 1, 1))) for b in range(B)]
+    N = max(lens)
+    ev = np.zeros((B, N, 4), np.float32)
+    for b, n in enumerate(lens):
+        t = np.sort(rng.integers(0, window_us, n))
+        c0 = rng.uniform([0, 0], [W, Hp], size=(n_clusters, 2))
+        vel = rng.uniform(-30, 30, size=(n_clusters, 2))          # px per window
+        n_cl = int(round(0.7 * n))
+        pick = rng.permutation(n)
+        cl, un = pick[:n_cl], pick[n_cl:]
+        xy = np.empty((n, 2))
+        which = rng.integers(0, n_clusters, size=n_cl)
+        xy[cl] = c0[which] + vel[which] * (t[cl, None] / window_us) + rng.normal(0.0, sigma, size=(n_cl, 2))
+        xy[un] = rng.uniform([0, 0], [W, Hp], size=(len(un), 2))
+        xy = np.rint(xy)
+        ev[b, :n, 0] = np.clip(xy[:, 0], 0, W - 1)
+        ev[b, :n, 1] = np.clip(xy[:, 1], 0, Hp - 1)
+        ev[b, :n, 2] = t
+        ev[b, :n, 3] = 2 * rng.integers(0, 2, n) - 1
+        ev[b, n:, 3] = -1
+    return torch.from_numpy(ev), torch.tensor(lens, dtype=torch.int64)

@@ -45,17 +45,18 @@ def state(fx, tag):
     return {k[len(pre):]: torch.from_numpy(fx[k]) for k in fx.files if k.startswith(pre)}
 
 
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "composed"])
 @pytest.mark.parametrize("tag", sorted(MOS_CASES))
-def test_mos_attention_matches_reference(lfx, tag):
+def test_mos_attention_matches_reference(lfx, tag, fused):
     from ssla_amd.layers import MosAttention
     C, k, s, sp, gp = MOS_CASES[tag]
     frame = tuple(int(v) for v in lfx["in_frame"])
     layer = MosAttention(C, 8, frame, k, s, scatter_proj=sp, gather_proj=gp)
     layer.load_state_dict(state(lfx, tag), strict=True)
     layer = layer.cuda()
-    print(f"mos {tag}: E={lfx['in_time'].shape[0]} C={C} k={k} s={s}", flush=True)
+    print(f"mos {tag}: E={lfx['in_time'].shape[0]} C={C} k={k} s={s} fused={fused}", flush=True)
     with torch.no_grad():
-        r = layer(dev_inputs(lfx, C))
+        r = layer(dev_inputs(lfx, C), fused=fused)
     np.testing.assert_allclose(r["events"].cpu().numpy(), lfx[f"{tag}_out"], **TOL)
     # the device-built table equals the reference's registered buffer
     np.testing.assert_array_equal(layer.patch2pixel_lut.cpu().numpy(), lfx[f"{tag}_sd_patch2pixel_lut"])
@@ -77,7 +78,8 @@ def test_linear_attention_matches_reference(lfx, tag):
     np.testing.assert_allclose(r["events"].cpu().numpy(), lfx[f"{tag}_out"], **TOL)
 
 
-def test_mos_attention_larger_vs_oracle():
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "composed"])
+def test_mos_attention_larger_vs_oracle(fused):
     """A bigger random case (hot pixels, many patches) against the fp64 oracle."""
     from ssla_amd.layers import MosAttention
     from ssla_amd import events as E
@@ -87,10 +89,10 @@ def test_mos_attention_larger_vs_oracle():
     gr = E.group_events((ev.cuda(), lengths.cuda()), (H, W))
     C = 16
     gr["events"] = torch.randn(gr["time"].shape[0], C, device="cuda")
-    layer = MosAttention(C, 32, (H, W), (3, 3), (1, 1)).cuda()
-    print(f"mos oracle: E={gr['time'].shape[0]}", flush=True)
+    layer = MosAttention(C, 24, (H, W), (3, 3), (1, 1)).cuda()
+    print(f"mos oracle: E={gr['time'].shape[0]} fused={fused}", flush=True)
     with torch.no_grad():
-        r = layer(gr)
+        r = layer(gr, fused=fused)
     p = {k: v.detach().cpu().numpy() for k, v in layer.state_dict().items()}
     grn = {k: (v.cpu().numpy() if torch.is_tensor(v) else v) for k, v in gr.items()}
     want = OL.mos_attention(p, grn, (H, W), (3, 3), (1, 1))
