@@ -640,6 +640,104 @@ extern "C" int ssla_events_counts(const void *workspace, int64_t *counts_out, in
   return SSLA_OK;
 }
 
+// ---- receptive-field / patch scatter without a sort --------------------------------
+// When every pixel run is non-decreasing in time (clamped at 0, the sort
+// key), the stable (field, time) order is fixed by counting: event i of the
+// run at kernel position a of field f lands on row
+//   ev_pre[f] + i + sum_{a' < a} #(run a' <= t) + sum_{a' > a} #(run a' < t),
+// exactly where the stable sort of rf_enumerate's keys puts it (ties keep
+// the enumeration order: position, then run order).
+namespace {
+// counts[3] += number of groups whose run is not non-decreasing in time
+__global__ void rf_unsorted_runs(const int64_t *__restrict__ gstart, const int64_t *__restrict__ glen, int64_t G,
+                                 const int64_t *__restrict__ time, int64_t E_in,
+                                 unsigned long long *__restrict__ n_bad) {
+  GRID_STRIDE(g, G) {
+    const int64_t s = gstart[g], n = glen[g];
+    int64_t prev = 0;
+    bool bad = false;
+    for (int64_t i = 0; i < n; ++i) {
+      const int64_t e = s + i;
+      if (e < 0 || e >= E_in) { bad = true; break; }
+      const int64_t t = max(time[e], (int64_t)0);
+      if (i > 0 && t < prev) { bad = true; break; }
+      prev = t;
+    }
+    if (bad) atomicAdd(n_bad, 1ull);
+  }
+}
+
+// inv[p * A + a] = rf with lut[rf * A + a] == p (each (pixel, position)
+// pair belongs to at most one field)
+__global__ void rf_inv_lut(const int64_t *__restrict__ lut, int64_t n_rf, int A, int64_t HW,
+                           int32_t *__restrict__ inv) {
+  GRID_STRIDE(t, n_rf * A) {
+    const int64_t p = lut[t];
+    if (p >= 0 && p < HW) inv[p * A + t % A] = static_cast<int32_t>(t / A);
+  }
+}
+
+__global__ void rf_event_groups(const int64_t *__restrict__ gstart, const int64_t *__restrict__ glen, int64_t G,
+                                int64_t E_in, int32_t *__restrict__ ev2g) {
+  GRID_STRIDE(g, G) {
+    const int64_t s = gstart[g];
+    for (int64_t i = 0; i < glen[g]; ++i)
+      if (s + i >= 0 && s + i < E_in) ev2g[s + i] = static_cast<int32_t>(g);
+  }
+}
+
+// number of run elements < t (lower) or <= t (upper), times clamped at 0
+__device__ __forceinline__ int64_t run_count(const int64_t *__restrict__ time, int64_t s, int64_t n, int64_t t,
+                                             bool upper) {
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    const int64_t v = max(time[s + mid], (int64_t)0);
+    if (upper ? v <= t : v < t) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// one thread per (event, kernel position)
+__global__ void rf_merge(const int32_t *__restrict__ ev2g, const int64_t *__restrict__ gb,
+                         const int64_t *__restrict__ gh, const int64_t *__restrict__ gw,
+                         const int64_t *__restrict__ gstart, const int64_t *__restrict__ glen,
+                         const int32_t *__restrict__ pixmap, const int32_t *__restrict__ inv,
+                         const int64_t *__restrict__ lut, int64_t n_rf, int A, int H, int W,
+                         const int64_t *__restrict__ ev_pre, const int64_t *__restrict__ time, int64_t E_in,
+                         int64_t E_out, int64_t *__restrict__ o_src, int64_t *__restrict__ o_time,
+                         int64_t *__restrict__ o_pos, int32_t *__restrict__ dst_map) {
+  const int64_t HW = static_cast<int64_t>(H) * W;
+  GRID_STRIDE(t, E_in * A) {
+    const int64_t e = t / A;
+    const int a = static_cast<int>(t % A);
+    const int32_t g = ev2g[e];
+    if (g < 0) continue;
+    const int64_t b = gb[g], p = gh[g] * W + gw[g];
+    if (p < 0 || p >= HW) continue;
+    const int32_t rf = inv[p * A + a];
+    if (rf < 0) continue;
+    const int64_t tt = max(time[e], (int64_t)0);
+    int64_t rank = e - gstart[g];
+    for (int a2 = 0; a2 < A; ++a2) {
+      if (a2 == a) continue;
+      const int64_t p2 = lut[static_cast<int64_t>(rf) * A + a2];
+      if (p2 < 0) continue;
+      const int32_t g2 = pixmap[b * HW + p2];
+      if (g2 < 0) continue;
+      rank += run_count(time, gstart[g2], glen[g2], tt, a2 < a);
+    }
+    const int64_t row = ev_pre[b * n_rf + rf] + rank;
+    if (row < 0 || row >= E_out) continue;   // inconsistent inputs: drop, never write out of range
+    o_src[row] = e;
+    if (o_time) o_time[row] = time[e];
+    o_pos[row] = a;
+    if (dst_map) dst_map[e * A + a] = static_cast<int32_t>(row);
+  }
+}
+}  // namespace
+
 // ---- receptive-field / patch scatter ---------------------------------------------
 namespace {
 struct RfWs {
@@ -685,7 +783,9 @@ extern "C" size_t ssla_rf_scatter_workspace_size(int64_t G, int B, int H, int W,
 }
 
 // Plan: which (b, rf) fields are active and how many events each holds.
-// counts[0] = active fields, counts[1] = field events, counts[2] = max time.
+// counts[0] = active fields, counts[1] = field events, counts[2] = max time,
+// counts[3] = pixel runs that are not non-decreasing in time (0: the
+// sort-free fill applies).
 extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
                                     const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
                                     int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
@@ -727,6 +827,9 @@ extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h
   hipLaunchKernelGGL(rf_fields, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.act, L.act_pre, L.nev, n_f, L.f_index,
                      L.f_len);
   hipLaunchKernelGGL(store_u64_as_i64, dim3(1), dim3(64), 0, st, L.tmax, L.counts + 2);
+  if (G > 0)
+    hipLaunchKernelGGL(rf_unsorted_runs, dim3(grid_for(G)), dim3(kThreads), 0, st, L.gstart, gr_len, G, time, E_in,
+                       reinterpret_cast<unsigned long long *>(L.counts + 3));
   return launch_status("rf_scatter_plan");
 }
 
@@ -768,6 +871,59 @@ extern "C" int ssla_rf_scatter_fill(const int64_t *gr_len, int64_t G, const int6
     }
   }
   return launch_status("rf_scatter_fill");
+}
+
+
+// Fill without a sort, for plans with counts[3] == 0 (every pixel run sorted
+// by time): the same outputs as ssla_rf_scatter_fill.  inv (H * W * A int32)
+// and ev_group (E_in int32) are scratch the caller provides; dst_map
+// (E_in * A int32, optional) receives the row of every (event, position)
+// pair, -1 where the pair is in no field.
+extern "C" int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
+                                           const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in,
+                                           int B, int H, int W, const int64_t *lut, int64_t n_rf, int A,
+                                           int64_t E_cap, int64_t n_active, int64_t E_out, int64_t *out_src,
+                                           int64_t *out_time, int64_t *out_pos, int64_t *f_index, int64_t *f_len,
+                                           int32_t *inv, int32_t *ev_group, int32_t *dst_map, void *workspace,
+                                           size_t workspace_bytes, void *stream) {
+  clear_error();
+  const int64_t n_pix = static_cast<int64_t>(B) * H * W, n_f = static_cast<int64_t>(B) * n_rf;
+  const RfWs L = rf_layout(workspace, G, n_pix, n_f, E_cap);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("rf_scatter_fill_sorted: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  SSLA_CHECK_ARG(E_out >= 0 && E_out <= E_cap && n_active >= 0 && n_active <= n_f && A > 0,
+                 "rf_scatter_fill_sorted: counts outside the plan's capacity");
+  SSLA_CHECK_ARG(out_src && out_pos && f_index && f_len && inv && (E_in == 0 || ev_group),
+                 "rf_scatter_fill_sorted: null pointer");
+  SSLA_CHECK_ARG(G == 0 || (gr_batch && gr_h && gr_w && gr_len), "rf_scatter_fill_sorted: null group arrays");
+  SSLA_CHECK_ARG(E_out < 0x7fffffff, "rf_scatter_fill_sorted: E_out must stay below 2^31");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t HW = static_cast<int64_t>(H) * W;
+  hipLaunchKernelGGL(fill_i32, dim3(grid_for(HW * A)), dim3(kThreads), 0, st, inv, HW * A, -1);
+  hipLaunchKernelGGL(rf_inv_lut, dim3(grid_for(n_rf * A)), dim3(kThreads), 0, st, lut, n_rf, A, HW, inv);
+  if (E_in > 0) {
+    hipLaunchKernelGGL(fill_i32, dim3(grid_for(E_in)), dim3(kThreads), 0, st, ev_group, E_in, -1);
+    if (dst_map)
+      hipLaunchKernelGGL(fill_i32, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, dst_map, E_in * A, -1);
+    if (G > 0)
+      hipLaunchKernelGGL(rf_event_groups, dim3(grid_for(G)), dim3(kThreads), 0, st, L.gstart, gr_len, G, E_in,
+                         ev_group);
+    if (E_out > 0)
+      hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, ev_group, gr_batch, gr_h, gr_w,
+                         L.gstart, gr_len, L.pixmap, inv, lut, n_rf, A, H, W, L.ev_pre, time, E_in, E_out, out_src,
+                         out_time, out_pos, dst_map);
+  }
+  if (n_active > 0) {
+    hipError_t e = hipMemcpyAsync(f_index, L.f_index, sizeof(int64_t) * n_active, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(f_len, L.f_len, sizeof(int64_t) * n_active, hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) {
+      set_error("rf_scatter_fill_sorted: %s", hipGetErrorString(e));
+      return SSLA_ERR_LAUNCH;
+    }
+  }
+  return launch_status("rf_scatter_fill_sorted");
 }
 
 // ---- rows ------------------------------------------------------------------------

@@ -152,6 +152,77 @@ __device__ __forceinline__ int64_t next_start(const uint8_t *__restrict__ start,
   return R;
 }
 
+// Dot product of an LDS weight row (16-byte aligned when N % 4 == 0, 8-byte
+// when N % 2 == 0) with x, in column order: one 16-byte LDS read per four
+// FMAs.
+template <int N>
+__device__ __forceinline__ float dot_lds(const float *row, const float (&x)[N]) {
+  float acc = 0.f;
+  if constexpr (N % 4 == 0) {
+    const float4 *r4 = reinterpret_cast<const float4 *>(row);
+#pragma unroll
+    for (int c = 0; c < N; c += 4) {
+      const float4 w = r4[c / 4];
+      acc = fmaf(w.x, x[c], acc);
+      acc = fmaf(w.y, x[c + 1], acc);
+      acc = fmaf(w.z, x[c + 2], acc);
+      acc = fmaf(w.w, x[c + 3], acc);
+    }
+  } else if constexpr (N % 2 == 0) {
+    const float2 *r2 = reinterpret_cast<const float2 *>(row);
+#pragma unroll
+    for (int c = 0; c < N; c += 2) {
+      const float2 w = r2[c / 2];
+      acc = fmaf(w.x, x[c], acc);
+      acc = fmaf(w.y, x[c + 1], acc);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < N; ++c) acc = fmaf(row[c], x[c], acc);
+  }
+  return acc;
+}
+
+// Index, position and start flag of patch row r (r >= re: a start with
+// index 0, which keeps every later load in bounds).
+struct RowIdx {
+  int64_t s;
+  int p, flag;
+};
+__device__ __forceinline__ void fetch_idx(RowIdx &ix, const int64_t *__restrict__ src,
+                                          const int64_t *__restrict__ pos, const uint8_t *__restrict__ start,
+                                          int64_t r, int64_t re, int64_t E, int A) {
+  ix.s = 0;
+  ix.p = 0;
+  ix.flag = 1;
+  if (r < re) {
+    ix.s = min(max(src[r], (int64_t)0), E - 1);
+    ix.p = static_cast<int>(min(max(pos[r], (int64_t)0), static_cast<int64_t>(A - 1)));
+    ix.flag = start[r] != 0;
+  }
+}
+
+// Event row s (cin values, zero-padded to CP): 16-byte loads when the row
+// is exactly CP wide and CP is a multiple of 4 (rows then stay 16-byte
+// aligned), else element loads.
+template <int CP>
+__device__ __forceinline__ void fetch_row(float (&e)[CP], const float *__restrict__ ev, int64_t s, int cin) {
+  if (CP % 4 == 0 && cin == CP) {
+    const float4 *p = reinterpret_cast<const float4 *>(ev + s * CP);
+#pragma unroll
+    for (int c = 0; c < CP; c += 4) {
+      const float4 t = p[c / 4];
+      e[c] = t.x;
+      e[c + 1] = t.y;
+      e[c + 2] = t.z;
+      e[c + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CP; ++c) e[c] = c < cin ? ev[s * cin + c] : 0.f;
+  }
+}
+
 template <int CP, int HP>
 __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
     const float *__restrict__ ev, int64_t E, int cin, int hid, const int64_t *__restrict__ src,
@@ -160,7 +231,8 @@ __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
     const float *__restrict__ wg, const float *__restrict__ wo, const float *__restrict__ wgp, int Ag,
     float *__restrict__ orow) {
   typedef MosW<CP, HP> L;
-  extern __shared__ float sw[];
+  extern __shared__ float4 sw4[];   // 16-byte aligned: every matrix stride is a multiple of 4 floats
+  float *sw = reinterpret_cast<float *>(sw4);
   load_weights<CP, HP>(sw, ws, As, wq, wv, wg, wo, wgp, Ag, cin, hid);
   __syncthreads();
   const float *s_s = sw, *s_g = sw + As * L::kS, *s_u = s_g + Ag * L::kG;
@@ -176,53 +248,50 @@ __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
     float carry[HP];
 #pragma unroll
     for (int j = 0; j < HP; ++j) carry[j] = 0.f;
+    // two-stage prefetch: row indices two windows ahead, event rows one
+    // window ahead (their address needs the index), compute on the current
+    RowIdx i0, i1;
+    float e0[CP];
+    fetch_idx(i0, src, pos, start, rs + lane, re, E, A);
+    fetch_row<CP>(e0, ev, i0.s, cin);
+    fetch_idx(i1, src, pos, start, rs + 64 + lane, re, E, A);
     for (int64_t b = rs; b < re; b += 64) {
       // weights are re-read from LDS each window (broadcast reads) rather
       // than hoisted into registers, which would cost all the occupancy
       asm volatile("" ::: "memory");
       const int64_t r = b + lane;
       const bool valid = r < re;
-      int flag = 1;
-      float e[CP];
-      int ps = 0, pg = 0;
-      if (valid) {
-        flag = start[r] != 0;
-        const int64_t s = min(max(src[r], (int64_t)0), E - 1);
-        const int p = static_cast<int>(min(max(pos[r], (int64_t)0), static_cast<int64_t>(A - 1)));
-        ps = As > 1 ? p : 0;
-        pg = Ag > 1 ? p : 0;
-#pragma unroll
-        for (int c = 0; c < CP; ++c) e[c] = c < cin ? ev[s * cin + c] : 0.f;
+      float en[CP];
+      RowIdx i2;
+      if (b + 64 < re) {
+        fetch_row<CP>(en, ev, i1.s, cin);
       } else {
 #pragma unroll
-        for (int c = 0; c < CP; ++c) e[c] = 0.f;
+        for (int c = 0; c < CP; ++c) en[c] = 0.f;
       }
+      fetch_idx(i2, src, pos, start, b + 128 + lane, re, E, A);
+      const int flag = i0.flag;
+      const int ps = As > 1 ? i0.p : 0, pg = Ag > 1 ? i0.p : 0;
+      float e[CP];
+#pragma unroll
+      for (int c = 0; c < CP; ++c) e[c] = e0[c];
       // scatter projection
       float x[HP];
       {
         const float *m = s_s + ps * L::kS;
 #pragma unroll
-        for (int j = 0; j < HP; ++j) {
-          float acc = 0.f;
-#pragma unroll
-          for (int c = 0; c < CP; ++c) acc = fmaf(m[j * CP + c], e[c], acc);
-          x[j] = acc;
-        }
+        for (int j = 0; j < HP; ++j) x[j] = dot_lds<CP>(m + j * CP, e);
       }
       // q, v, gate
       float q[HP], A_[HP], B_[HP];
 #pragma unroll
       for (int j = 0; j < HP; ++j) {
-        float aq = 0.f, av = 0.f, ag = 0.f;
-#pragma unroll
-        for (int c = 0; c < HP; ++c) {
-          aq = fmaf(s_q[j * HP + c], x[c], aq);
-          av = fmaf(s_v[j * HP + c], x[c], av);
-          ag = fmaf(s_a[j * HP + c], x[c], ag);
-        }
+        const float aq = dot_lds<HP>(s_q + j * HP, x), av = dot_lds<HP>(s_v + j * HP, x),
+                    ag = dot_lds<HP>(s_a + j * HP, x);
         q[j] = aq;
         B_[j] = av;
-        A_[j] = 1.f / (1.f + expf(-ag));
+        // sigmoid on the transcendental unit (exp2 and reciprocal, ~1 ulp each)
+        A_[j] = __builtin_amdgcn_rcpf(1.f + fast_exp2(-ag * kLog2e));
       }
       // segmented inclusive scan of (A, B) across the wavefront
       int F = flag;
@@ -251,12 +320,7 @@ __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
       // o_proj, then the gather projection
       float o[HP];
 #pragma unroll
-      for (int j = 0; j < HP; ++j) {
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < HP; ++c) acc = fmaf(s_o[j * HP + c], hq[c], acc);
-        o[j] = acc;
-      }
+      for (int j = 0; j < HP; ++j) o[j] = dot_lds<HP>(s_o + j * HP, hq);
       if (valid) {
         const float *m = s_g + pg * L::kG;
         float *dst = orow + r * HP;
@@ -266,16 +330,15 @@ __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
           float *yy = reinterpret_cast<float *>(&y);
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            float acc = 0.f;
-            if (j + u < HP) {
-#pragma unroll
-              for (int c = 0; c < HP; ++c) acc = fmaf(m[(j + u) * HP + c], o[c], acc);
-            }
-            yy[u] = acc;
+            yy[u] = j + u < HP ? dot_lds<HP>(m + (j + u) * HP, o) : 0.f;
           }
           *reinterpret_cast<float4 *>(dst + j) = y;
         }
       }
+      i0 = i1;
+      i1 = i2;
+#pragma unroll
+      for (int c = 0; c < CP; ++c) e0[c] = en[c];
     }
   }
 }
@@ -315,8 +378,7 @@ __global__ __launch_bounds__(kThreads) void mos_event_kernel(
       }
     }
     float x[CP];
-#pragma unroll
-    for (int c = 0; c < CP; ++c) x[c] = c < cin ? ev[e * cin + c] : 0.f;
+    fetch_row<CP>(x, ev, e, cin);
     if (win) {
 #pragma unroll
       for (int j = 0; j < HP; ++j) {
@@ -341,9 +403,18 @@ __global__ __launch_bounds__(kThreads) void mos_event_kernel(
     }
     var /= static_cast<float>(hid);
     const float rstd = 1.f / sqrtf(var + eps);
+    if (HP % 4 == 0 && hid == HP) {
+      float4 *po = reinterpret_cast<float4 *>(out + e * HP);
 #pragma unroll
-    for (int j = 0; j < HP; ++j)
-      if (j < hid) out[e * hid + j] = (y[j] - mean) * rstd * s_w[j] + s_b[j];
+      for (int j = 0; j < HP; j += 4)
+        po[j / 4] = make_float4((y[j] - mean) * rstd * s_w[j] + s_b[j], (y[j + 1] - mean) * rstd * s_w[j + 1] + s_b[j + 1],
+                                (y[j + 2] - mean) * rstd * s_w[j + 2] + s_b[j + 2],
+                                (y[j + 3] - mean) * rstd * s_w[j + 3] + s_b[j + 3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < HP; ++j)
+        if (j < hid) out[e * hid + j] = (y[j] - mean) * rstd * s_w[j] + s_b[j];
+    }
   }
 }
 

@@ -112,7 +112,13 @@ def group_events(inputs, frame_size, max_events_per_px: int = 512) -> Dict[str, 
 
 
 # ------------------------------------------------- fields / patches ----------
-def _rf_scatter(inputs, frame_size, lut):
+def _rf_scatter(inputs, frame_size, lut, force_sort=False, dst_map=False):
+    """Field / patch rows of the pixel groups: (src, time, pos, f_index, f_len,
+    n_rf[, dst]).  Pixel runs sorted by time (the plan counts the others)
+    take the sort-free fill; force_sort=True always takes the radix-sort
+    fill (the general path).  dst_map=True also returns the row of every
+    (event, kernel position) pair ([E_in * A] int32, -1 if none; sort-free
+    fill only, else None)."""
     lib = _lib.load()
     gb, gh, gw, gl = (_i64(inputs[k]) for k in ("batch_id", "h", "w", "lengths"))
     time = _i64(inputs["time"])
@@ -128,16 +134,29 @@ def _rf_scatter(inputs, frame_size, lut):
     _lib.check(lib.ssla_rf_scatter_plan(_lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), _lib.ptr(gl), G, _lib.ptr(time),
                                         E_in, B, H, W, _lib.ptr(lut), n_rf, A, E_cap, _lib.ptr(ws), ws.numel(), st),
                "rf_scatter_plan")
-    n_act, E_out, t_max = _counts(ws, 3, st, "rf_scatter_plan")
+    n_act, E_out, t_max, n_unsorted = _counts(ws, 4, st, "rf_scatter_plan")
     src = torch.empty(E_out, dtype=torch.int64, device=dev)
     tim = torch.empty(E_out, dtype=torch.int64, device=dev)
     pos = torch.empty(E_out, dtype=torch.int64, device=dev)
     f_index = torch.empty(n_act, dtype=torch.int64, device=dev)
     f_len = torch.empty(n_act, dtype=torch.int64, device=dev)
-    _lib.check(lib.ssla_rf_scatter_fill(_lib.ptr(gl), G, _lib.ptr(time), E_in, B, H, W, _lib.ptr(lut), n_rf, A, E_cap,
-                                        n_act, E_out, t_max, _lib.ptr(src), _lib.ptr(tim), _lib.ptr(pos),
-                                        _lib.ptr(f_index), _lib.ptr(f_len), _lib.ptr(ws), ws.numel(), st),
-               "rf_scatter_fill")
+    dst = None
+    if n_unsorted == 0 and not force_sort:
+        inv = torch.empty(H * W * A, dtype=torch.int32, device=dev)
+        ev_group = torch.empty(max(E_in, 1), dtype=torch.int32, device=dev)
+        dst = torch.empty(E_in * A, dtype=torch.int32, device=dev) if dst_map else None
+        _lib.check(lib.ssla_rf_scatter_fill_sorted(
+            _lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), _lib.ptr(gl), G, _lib.ptr(time), E_in, B, H, W, _lib.ptr(lut),
+            n_rf, A, E_cap, n_act, E_out, _lib.ptr(src), _lib.ptr(tim), _lib.ptr(pos), _lib.ptr(f_index),
+            _lib.ptr(f_len), _lib.ptr(inv), _lib.ptr(ev_group), _lib.ptr(dst), _lib.ptr(ws), ws.numel(), st),
+            "rf_scatter_fill_sorted")
+    else:
+        _lib.check(lib.ssla_rf_scatter_fill(_lib.ptr(gl), G, _lib.ptr(time), E_in, B, H, W, _lib.ptr(lut), n_rf, A,
+                                            E_cap, n_act, E_out, t_max, _lib.ptr(src), _lib.ptr(tim), _lib.ptr(pos),
+                                            _lib.ptr(f_index), _lib.ptr(f_len), _lib.ptr(ws), ws.numel(), st),
+                   "rf_scatter_fill")
+    if dst_map:
+        return src, tim, pos, f_index, f_len, n_rf, dst
     return src, tim, pos, f_index, f_len, n_rf
 
 

@@ -164,3 +164,46 @@ def test_empty_and_bad_inputs(dev):
     bad[0, 1, 0] = 9.0                       # x outside a 4-wide frame
     with pytest.raises(ValueError):
         E.group_events((bad, torch.tensor([3], device=dev)), (4, 4))
+
+
+@pytest.mark.parametrize("k,s", [(3, 1), (1, 1), (2, 2), (3, 2), (5, 1)])
+def test_sort_free_field_fill_equals_sort(dev, k, s):
+    """The sort-free fill (pixel runs sorted by time, rows placed by counting)
+    equals the radix-sort fill bit for bit on a clustered batch with many
+    timestamp ties, and its (event, position) -> row map inverts the rows."""
+    from ssla_amd import events as E
+    H, W = 48, 56
+    ev, lens = _synthetic(11 + k, 3, 4000, H, W, dev)
+    ev[..., 2] = np.floor(ev[..., 2] / 50.0)   # coarse times: many ties across a field's runs
+    gr = E.group_events((_t(ev, dev), _t(lens, dev)), (H, W))
+    lut, _ = E.compute_rf2pixels((H, W), (k, k), (s, s), device=dev)
+    print(f"sort-free fill k={k} s={s}: E={gr['time'].numel()}", flush=True)
+    a = E._rf_scatter(gr, (H, W), lut, dst_map=True)
+    b = E._rf_scatter(gr, (H, W), lut, force_sort=True)
+    for name, x, y in zip(("src", "time", "pos", "f_index", "f_len"), a[:5], b[:5]):
+        np.testing.assert_array_equal(_np(x), _np(y), err_msg=name)
+    src, pos, dst = _np(a[0]), _np(a[2]), _np(a[6])
+    A = k * k
+    assert np.array_equal(dst[src * A + pos], np.arange(src.size))
+    assert int((dst >= 0).sum()) == src.size
+
+
+def test_unsorted_runs_take_the_sort_path(dev):
+    """A pixel run out of time order (possible in a hand-built dict) is
+    counted by the plan; the sort fill then gives the oracle's rows."""
+    from ssla_amd import events as E
+    H, W = 6, 7
+    ev, lens = _synthetic(5, 1, 300, H, W, dev)
+    evc = np.concatenate([ev, np.random.default_rng(4).normal(size=ev.shape[:2] + (2,)).astype(np.float32)], -1)
+    gr = E.group_events((_t(evc, dev), _t(lens, dev)), (H, W))
+    ro = OE.group_events(evc, lens, (H, W))
+    g = int(np.argmax(ro["lengths"]))                 # reverse the longest run's times
+    s0 = int(np.sum(ro["lengths"][:g]))
+    n = int(ro["lengths"][g])
+    ro["time"][s0:s0 + n] = ro["time"][s0:s0 + n][::-1].copy()
+    gr["time"] = _t(ro["time"], dev)
+    lut = E.get_patch2pixel_lut((H, W), (3, 3), (1, 1), device=dev)
+    res = E.scatter_group_events_to_patch(gr, (H, W), lut)
+    rres = OE.scatter_group_events_to_patch(ro, (H, W), _np(lut))
+    for key in ("events", "pos_id", "lengths", "orig_event_idx"):
+        np.testing.assert_array_equal(_np(res[key]), rres[key], err_msg=key)
