@@ -263,17 +263,17 @@ int ssla_rf_scatter_fill(const int64_t *gr_len, int64_t G, const int64_t *time, 
                          void *workspace, size_t workspace_bytes, void *stream);
 
 /* Sort-free fill for plans whose counts[3] is 0 (every pixel run
- * non-decreasing in time, as group_events and the field outputs leave them):
- * the same outputs as ssla_rf_scatter_fill, each row placed by counting the
- * earlier events of the field's other runs.  inv (H * W * A int32) and
- * ev_group (E_in int32) are caller scratch; dst_map (E_in * A int32, may be
- * NULL) receives the row of every (event, kernel position) pair or -1. */
+ * non-decreasing in time, as group_events and the field outputs leave them,
+ * and E_in <= E_cap): the same outputs as ssla_rf_scatter_fill, each row
+ * placed by counting the earlier events of the field's other runs.  inv
+ * (H * W * A int32) is caller scratch; dst_map (E_in * A int32, may be NULL)
+ * receives the row of every (event, kernel position) pair or -1. */
 int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
                                 const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B, int H,
                                 int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap, int64_t n_active,
                                 int64_t E_out, int64_t *out_src, int64_t *out_time, int64_t *out_pos,
-                                int64_t *f_index, int64_t *f_len, int32_t *inv, int32_t *ev_group, int32_t *dst_map,
-                                void *workspace, size_t workspace_bytes, void *stream);
+                                int64_t *f_index, int64_t *f_len, int32_t *inv, int32_t *dst_map, void *workspace,
+                                size_t workspace_bytes, void *stream);
 
 /* out[j, :] = src[idx[j], :] for rows of C floats (0 for idx out of range). */
 int ssla_gather_rows(const float *src, int64_t n_src, const int64_t *idx, int64_t m, int C, float *out,

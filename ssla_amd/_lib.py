@@ -59,7 +59,7 @@ SIGNATURES = {
     "ssla_rf_scatter_fill": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _i32, _i64, _i64, _i64,
                                     _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ssla_rf_scatter_fill_sorted": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _i32,
-                                           _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+                                           _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ssla_gather_rows": (_i32, [_vp, _i64, _vp, _i64, _i32, _vp, _vp]),
     "ssla_index_add_rows_workspace_size": (_sz, [_i64]),
     "ssla_index_add_rows": (_i32, [_vp, _vp, _i64, _i32, _i64, _vp, _vp, _sz, _vp]),

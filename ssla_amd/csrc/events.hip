@@ -135,7 +135,9 @@ __global__ void ge_keys(const float *__restrict__ ev, const int64_t *__restrict_
     const float x = ev[s * C + 0], y = ev[s * C + 1];
     const float pid = static_cast<float>(b * static_cast<int64_t>(H) * W) + y * static_cast<float>(W) + x;
     if (!(x >= 0.f && x < W && y >= 0.f && y < H)) *bad = 1;
-    key[f] = pid >= 0.f ? static_cast<uint64_t>(pid) : 0;
+    // out-of-frame events (reported through bad) stay inside the sorted bits
+    const uint64_t n_pix = static_cast<uint64_t>(B) * H * W;
+    key[f] = pid >= 0.f ? min(static_cast<uint64_t>(pid), n_pix) : 0;
     val[f] = static_cast<int32_t>(f);
     row_of[f] = s;
   }
@@ -594,14 +596,16 @@ extern "C" int ssla_group_events(const float *events, const int64_t *lengths, in
   hipLaunchKernelGGL(trunc_len, dim3(grid_for(B)), dim3(kThreads), 0, st, lengths, (int64_t)B, N, L.kept);
   int s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.off, B + 1, st);
   if (s) return s;
-  // keys of the valid events; padding slots keep the all-ones key and sort last
+  // keys of the valid events (pixel ids < B*H*W); padding slots take the key
+  // B*H*W and sort last, so only the bits of B*H*W need sorting
+  const int64_t n_pix = static_cast<int64_t>(B) * H * W;
   hipLaunchKernelGGL(fill_i64, dim3(grid_for(cap)), dim3(kThreads), 0, st, reinterpret_cast<int64_t *>(L.key), cap,
-                     (int64_t)-1);
+                     n_pix);
   hipLaunchKernelGGL(iota_i32, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.val, cap);
   hipLaunchKernelGGL(fill_i64, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.row_of, cap, (int64_t)0);
   hipLaunchKernelGGL(ge_keys, dim3(grid_for(cap)), dim3(kThreads), 0, st, events, lengths, L.off, B, N, C, H, W,
                      L.key, L.val, L.row_of, L.bad);
-  s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.order, cap, 64, st);
+  s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.order, cap, bits_for(static_cast<uint64_t>(n_pix)), st);
   if (s) return s;
   hipLaunchKernelGGL(ge_heads, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.skey, cap, Ep, L.head);
   s = excl_scan(L.tmp, L.tmp_bytes, L.head, L.gpos, cap, st);
@@ -648,20 +652,31 @@ extern "C" int ssla_events_counts(const void *workspace, int64_t *counts_out, in
 // exactly where the stable sort of rf_enumerate's keys puts it (ties keep
 // the enumeration order: position, then run order).
 namespace {
-// counts[3] += number of groups whose run is not non-decreasing in time
-__global__ void rf_unsorted_runs(const int64_t *__restrict__ gstart, const int64_t *__restrict__ glen, int64_t G,
-                                 const int64_t *__restrict__ time, int64_t E_in,
-                                 unsigned long long *__restrict__ n_bad) {
+// Per group: ev2g[e] = g for the events of its run (when store), and
+// n_bad += 1 if the run is not non-decreasing in time (clamped at 0) or
+// leaves [0, E_in).  Without store (ev2g too small) one thread adds 1, which
+// sends the caller to the sort fill.
+__global__ void rf_groups_scan(const int64_t *__restrict__ gstart, const int64_t *__restrict__ glen, int64_t G,
+                               const int64_t *__restrict__ time, int64_t E_in, int32_t *__restrict__ ev2g, int store,
+                               unsigned long long *__restrict__ n_bad) {
+  if (!store) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(n_bad, 1ull);
+    return;
+  }
   GRID_STRIDE(g, G) {
     const int64_t s = gstart[g], n = glen[g];
     int64_t prev = 0;
     bool bad = false;
     for (int64_t i = 0; i < n; ++i) {
       const int64_t e = s + i;
-      if (e < 0 || e >= E_in) { bad = true; break; }
+      if (e < 0 || e >= E_in) {
+        bad = true;
+        break;
+      }
       const int64_t t = max(time[e], (int64_t)0);
-      if (i > 0 && t < prev) { bad = true; break; }
+      bad |= i > 0 && t < prev;
       prev = t;
+      ev2g[e] = static_cast<int32_t>(g);
     }
     if (bad) atomicAdd(n_bad, 1ull);
   }
@@ -674,15 +689,6 @@ __global__ void rf_inv_lut(const int64_t *__restrict__ lut, int64_t n_rf, int A,
   GRID_STRIDE(t, n_rf * A) {
     const int64_t p = lut[t];
     if (p >= 0 && p < HW) inv[p * A + t % A] = static_cast<int32_t>(t / A);
-  }
-}
-
-__global__ void rf_event_groups(const int64_t *__restrict__ gstart, const int64_t *__restrict__ glen, int64_t G,
-                                int64_t E_in, int32_t *__restrict__ ev2g) {
-  GRID_STRIDE(g, G) {
-    const int64_t s = gstart[g];
-    for (int64_t i = 0; i < glen[g]; ++i)
-      if (s + i >= 0 && s + i < E_in) ev2g[s + i] = static_cast<int32_t>(g);
   }
 }
 
@@ -827,9 +833,15 @@ extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h
   hipLaunchKernelGGL(rf_fields, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.act, L.act_pre, L.nev, n_f, L.f_index,
                      L.f_len);
   hipLaunchKernelGGL(store_u64_as_i64, dim3(1), dim3(64), 0, st, L.tmax, L.counts + 2);
-  if (G > 0)
-    hipLaunchKernelGGL(rf_unsorted_runs, dim3(grid_for(G)), dim3(kThreads), 0, st, L.gstart, gr_len, G, time, E_in,
-                       reinterpret_cast<unsigned long long *>(L.counts + 3));
+  // event -> group table (the sort-free fill's input; kept in the value
+  // buffer of the sort path, which needs E_in <= E_cap) and the count of
+  // unsorted runs
+  const int store = E_in <= E_cap;
+  if (store && E_in > 0)
+    hipLaunchKernelGGL(fill_i32, dim3(grid_for(E_in)), dim3(kThreads), 0, st, L.val, E_in, -1);
+  if (G > 0 || !store)
+    hipLaunchKernelGGL(rf_groups_scan, dim3(grid_for(std::max<int64_t>(G, 1))), dim3(kThreads), 0, st, L.gstart,
+                       gr_len, G, time, E_in, L.val, store, reinterpret_cast<unsigned long long *>(L.counts + 3));
   return launch_status("rf_scatter_plan");
 }
 
@@ -875,8 +887,8 @@ extern "C" int ssla_rf_scatter_fill(const int64_t *gr_len, int64_t G, const int6
 
 
 // Fill without a sort, for plans with counts[3] == 0 (every pixel run sorted
-// by time): the same outputs as ssla_rf_scatter_fill.  inv (H * W * A int32)
-// and ev_group (E_in int32) are scratch the caller provides; dst_map
+// by time): the same outputs as ssla_rf_scatter_fill, from the plan's event
+// -> group table.  inv (H * W * A int32) is scratch the caller provides; dst_map
 // (E_in * A int32, optional) receives the row of every (event, position)
 // pair, -1 where the pair is in no field.
 extern "C" int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
@@ -884,8 +896,8 @@ extern "C" int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_
                                            int B, int H, int W, const int64_t *lut, int64_t n_rf, int A,
                                            int64_t E_cap, int64_t n_active, int64_t E_out, int64_t *out_src,
                                            int64_t *out_time, int64_t *out_pos, int64_t *f_index, int64_t *f_len,
-                                           int32_t *inv, int32_t *ev_group, int32_t *dst_map, void *workspace,
-                                           size_t workspace_bytes, void *stream) {
+                                           int32_t *inv, int32_t *dst_map, void *workspace, size_t workspace_bytes,
+                                           void *stream) {
   clear_error();
   const int64_t n_pix = static_cast<int64_t>(B) * H * W, n_f = static_cast<int64_t>(B) * n_rf;
   const RfWs L = rf_layout(workspace, G, n_pix, n_f, E_cap);
@@ -895,8 +907,8 @@ extern "C" int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_
   }
   SSLA_CHECK_ARG(E_out >= 0 && E_out <= E_cap && n_active >= 0 && n_active <= n_f && A > 0,
                  "rf_scatter_fill_sorted: counts outside the plan's capacity");
-  SSLA_CHECK_ARG(out_src && out_pos && f_index && f_len && inv && (E_in == 0 || ev_group),
-                 "rf_scatter_fill_sorted: null pointer");
+  SSLA_CHECK_ARG(out_src && out_pos && f_index && f_len && inv, "rf_scatter_fill_sorted: null pointer");
+  SSLA_CHECK_ARG(E_in <= E_cap, "rf_scatter_fill_sorted: needs E_in <= E_cap (the plan's event table)");
   SSLA_CHECK_ARG(G == 0 || (gr_batch && gr_h && gr_w && gr_len), "rf_scatter_fill_sorted: null group arrays");
   SSLA_CHECK_ARG(E_out < 0x7fffffff, "rf_scatter_fill_sorted: E_out must stay below 2^31");
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -904,14 +916,10 @@ extern "C" int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_
   hipLaunchKernelGGL(fill_i32, dim3(grid_for(HW * A)), dim3(kThreads), 0, st, inv, HW * A, -1);
   hipLaunchKernelGGL(rf_inv_lut, dim3(grid_for(n_rf * A)), dim3(kThreads), 0, st, lut, n_rf, A, HW, inv);
   if (E_in > 0) {
-    hipLaunchKernelGGL(fill_i32, dim3(grid_for(E_in)), dim3(kThreads), 0, st, ev_group, E_in, -1);
     if (dst_map)
       hipLaunchKernelGGL(fill_i32, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, dst_map, E_in * A, -1);
-    if (G > 0)
-      hipLaunchKernelGGL(rf_event_groups, dim3(grid_for(G)), dim3(kThreads), 0, st, L.gstart, gr_len, G, E_in,
-                         ev_group);
     if (E_out > 0)
-      hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, ev_group, gr_batch, gr_h, gr_w,
+      hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.val, gr_batch, gr_h, gr_w,
                          L.gstart, gr_len, L.pixmap, inv, lut, n_rf, A, H, W, L.ev_pre, time, E_in, E_out, out_src,
                          out_time, out_pos, dst_map);
   }

@@ -143,12 +143,11 @@ def _rf_scatter(inputs, frame_size, lut, force_sort=False, dst_map=False):
     dst = None
     if n_unsorted == 0 and not force_sort:
         inv = torch.empty(H * W * A, dtype=torch.int32, device=dev)
-        ev_group = torch.empty(max(E_in, 1), dtype=torch.int32, device=dev)
         dst = torch.empty(E_in * A, dtype=torch.int32, device=dev) if dst_map else None
         _lib.check(lib.ssla_rf_scatter_fill_sorted(
             _lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), _lib.ptr(gl), G, _lib.ptr(time), E_in, B, H, W, _lib.ptr(lut),
             n_rf, A, E_cap, n_act, E_out, _lib.ptr(src), _lib.ptr(tim), _lib.ptr(pos), _lib.ptr(f_index),
-            _lib.ptr(f_len), _lib.ptr(inv), _lib.ptr(ev_group), _lib.ptr(dst), _lib.ptr(ws), ws.numel(), st),
+            _lib.ptr(f_len), _lib.ptr(inv), _lib.ptr(dst), _lib.ptr(ws), ws.numel(), st),
             "rf_scatter_fill_sorted")
     else:
         _lib.check(lib.ssla_rf_scatter_fill(_lib.ptr(gl), G, _lib.ptr(time), E_in, B, H, W, _lib.ptr(lut), n_rf, A,
