@@ -248,10 +248,19 @@ def bench_event_stage(torch, lib, reps, dev):
     per = {n: t / reps for n, t in zip(names, tot)}
     ms = sum(per.values())
     n_ev = int(ln.sum())
+    # work of the k3 layer (outside the timing): pixel events and patch rows
+    with torch.no_grad():
+        x = E.preprocess_inputs(*[t.to(dev) for t in io.pad_events(recs, dev)], frame, 50)
+        x = m1(x)
+        rows = int(E._rf_scatter(x, frame, m2.patch2pixel_lut)[0].numel())
+        px = int(x["time"].numel())
     return {"workload": "MOS_S stage 1 forward on 8 Gen1 windows (C5-like, synthetic): ingest + preprocess + "
                         "MosAttention k1/k3 (hidden 12) + SparseMaxPool k2 + TemporalDropout 4",
             "metric": "stage-1 events/s", "value": n_ev / (ms * 1e-3), "unit": "events/s", "ms_per_call": ms,
-            "events_in": n_ev, "events_out": int(out["lengths"].sum()), "ms_per_step": per}
+            "events_in": n_ev, "events_out": int(out["lengths"].sum()), "ms_per_step": per,
+            "mos_k3": {"pixel_events": px, "patch_rows": rows,
+                       "fp32_flop": 2 * rows * (12 * 12 + 3 * 12 * 12 + 12 * 12 + 12 * 12),
+                       "note": "scatter proj, q/v/g, o_proj, gather proj per patch row"}}
 
 
 def cpu_baseline(x, min_s=10.0):

@@ -42,6 +42,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWin = 256;       // rows per wavefront window (before the shift to patch boundaries)
 constexpr int kMaxPos = 49;     // kernel positions (up to 7 x 7)
+constexpr size_t kMaxLds = 64 * 1024;   // weights held in LDS per workgroup
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 inline unsigned grid_for(int64_t n) {
@@ -56,6 +57,7 @@ struct MosWs {
   uint8_t *start;    // [R] 1 at the first row of every patch
   int32_t *dst;      // [E * A] row of (event, position), or -1
   float *orow;       // [R, HP] projected rows
+  float *wfold;      // folded weights (3 A scatter-side + A gather-side matrices)
   void *tmp;
   size_t tmp_bytes, total;
 };
@@ -68,7 +70,7 @@ size_t scan_bytes(int64_t n) {
   return tb;
 }
 
-MosWs mos_layout(void *base, int64_t E, int A, int64_t R, int64_t n_patch, int HP) {
+MosWs mos_layout(void *base, int64_t E, int A, int64_t R, int64_t n_patch, int CP, int HP) {
   char *b = static_cast<char *>(base);
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -81,6 +83,8 @@ MosWs mos_layout(void *base, int64_t E, int A, int64_t R, int64_t n_patch, int H
   w.start = reinterpret_cast<uint8_t *>(take(static_cast<size_t>(R)));
   w.dst = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * static_cast<size_t>(E) * A));
   w.orow = reinterpret_cast<float *>(take(sizeof(float) * static_cast<size_t>(R) * HP));
+  w.wfold = reinterpret_cast<float *>(
+      take(sizeof(float) * (3 * static_cast<size_t>(A) * (HP * CP + 4) + static_cast<size_t>(A) * (HP * HP + 4))));
   w.tmp_bytes = scan_bytes(n_patch);
   w.tmp = take(w.tmp_bytes);
   w.total = off;
@@ -117,7 +121,40 @@ struct MosW {
   static constexpr int kG = HP * HP + 4;   // gather matrix stride
   static constexpr int kU = HP * HP;       // uniform matrices
   static size_t bytes(int As, int Ag) { return sizeof(float) * (static_cast<size_t>(As) * kS + Ag * kG + 4 * kU); }
+  // folded: Wq Ws[a], Wv Ws[a], Wg Ws[a] (stride kS) and Wgp[a] Wo (stride kG)
+  __host__ __device__ static size_t fold_floats(int As, int Ag) { return 3 * static_cast<size_t>(As) * kS + static_cast<size_t>(Ag) * kG; }
+  static size_t fold_bytes(int As, int Ag) { return sizeof(float) * fold_floats(As, Ag); }
 };
+
+// The folded matrices in their LDS layout (zero-padded), once per call:
+// q = (Wq Ws[a]) e, v = (Wv Ws[a]) e, g = (Wg Ws[a]) e and o = (Wgp[a] Wo)(q h)
+// take 3 cin hid + hid^2 FMAs per row instead of 4 hid^2 + cin hid + hid^2.
+template <int CP, int HP>
+__global__ void mos_fold_weights(const float *__restrict__ ws, int As, const float *__restrict__ wq,
+                                 const float *__restrict__ wv, const float *__restrict__ wg,
+                                 const float *__restrict__ wo, const float *__restrict__ wgp, int Ag, int cin, int hid,
+                                 float *__restrict__ out) {
+  typedef MosW<CP, HP> L;
+  const int64_t n_s = 3 * static_cast<int64_t>(As) * L::kS, n = static_cast<int64_t>(L::fold_floats(As, Ag));
+  MOS_GRID_STRIDE(i, n) {
+    float acc = 0.f;
+    if (i < n_s) {
+      const int m = static_cast<int>(i / (As * L::kS));
+      const int rem = static_cast<int>(i % (As * L::kS)), a = rem / L::kS, o = rem % L::kS;
+      const int j = o / CP, c = o % CP;
+      if (o < HP * CP && j < hid && c < cin) {
+        const float *w = m == 0 ? wq : m == 1 ? wv : wg;
+        for (int k = 0; k < hid; ++k) acc = fmaf(w[j * hid + k], ws[(static_cast<int64_t>(a) * hid + k) * cin + c], acc);
+      }
+    } else {
+      const int i2 = static_cast<int>(i - n_s), a = i2 / L::kG, o = i2 % L::kG;
+      const int j = o / HP, c = o % HP;
+      if (o < HP * HP && j < hid && c < hid)
+        for (int k = 0; k < hid; ++k) acc = fmaf(wgp[(static_cast<int64_t>(a) * hid + j) * hid + k], wo[k * hid + c], acc);
+    }
+    out[i] = acc;
+  }
+}
 
 // Fill the padded LDS copy of the weights (zeros outside cin x hid).
 template <int CP, int HP>
@@ -223,20 +260,29 @@ __device__ __forceinline__ void fetch_row(float (&e)[CP], const float *__restric
   }
 }
 
-template <int CP, int HP>
+template <int CP, int HP, bool FOLD>
 __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
     const float *__restrict__ ev, int64_t E, int cin, int hid, const int64_t *__restrict__ src,
     const int64_t *__restrict__ pos, int64_t R, const uint8_t *__restrict__ start, int A,
     const float *__restrict__ ws, int As, const float *__restrict__ wq, const float *__restrict__ wv,
     const float *__restrict__ wg, const float *__restrict__ wo, const float *__restrict__ wgp, int Ag,
-    float *__restrict__ orow) {
+    const float *__restrict__ wfold, float *__restrict__ orow) {
   typedef MosW<CP, HP> L;
   extern __shared__ float4 sw4[];   // 16-byte aligned: every matrix stride is a multiple of 4 floats
   float *sw = reinterpret_cast<float *>(sw4);
-  load_weights<CP, HP>(sw, ws, As, wq, wv, wg, wo, wgp, Ag, cin, hid);
+  if constexpr (FOLD) {
+    const int n4 = static_cast<int>(L::fold_floats(As, Ag) / 4);
+    const float4 *src4 = reinterpret_cast<const float4 *>(wfold);
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) sw4[i] = src4[i];
+  } else {
+    load_weights<CP, HP>(sw, ws, As, wq, wv, wg, wo, wgp, Ag, cin, hid);
+  }
   __syncthreads();
+  // unfolded layout
   const float *s_s = sw, *s_g = sw + As * L::kS, *s_u = s_g + Ag * L::kG;
   const float *s_q = s_u, *s_v = s_u + L::kU, *s_a = s_u + 2 * L::kU, *s_o = s_u + 3 * L::kU;
+  // folded layout
+  const float *f_q = sw, *f_v = sw + As * L::kS, *f_g = sw + 2 * As * L::kS, *f_o = sw + 3 * As * L::kS;
 
   const int lane = threadIdx.x & 63;
   const int64_t n_win = (R + kWin - 1) / kWin;
@@ -275,23 +321,30 @@ __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
       float e[CP];
 #pragma unroll
       for (int c = 0; c < CP; ++c) e[c] = e0[c];
-      // scatter projection
-      float x[HP];
-      {
+      // scatter projection, q, v, gate
+      float q[HP], A_[HP], B_[HP];
+      if constexpr (FOLD) {
+        const int off = ps * L::kS;
+#pragma unroll
+        for (int j = 0; j < HP; ++j) {
+          q[j] = dot_lds<CP>(f_q + off + j * CP, e);
+          B_[j] = dot_lds<CP>(f_v + off + j * CP, e);
+          const float ag = dot_lds<CP>(f_g + off + j * CP, e);
+          // sigmoid on the transcendental unit (exp2 and reciprocal, ~1 ulp each)
+          A_[j] = __builtin_amdgcn_rcpf(1.f + fast_exp2(-ag * kLog2e));
+        }
+      } else {
+        float x[HP];
         const float *m = s_s + ps * L::kS;
 #pragma unroll
         for (int j = 0; j < HP; ++j) x[j] = dot_lds<CP>(m + j * CP, e);
-      }
-      // q, v, gate
-      float q[HP], A_[HP], B_[HP];
 #pragma unroll
-      for (int j = 0; j < HP; ++j) {
-        const float aq = dot_lds<HP>(s_q + j * HP, x), av = dot_lds<HP>(s_v + j * HP, x),
-                    ag = dot_lds<HP>(s_a + j * HP, x);
-        q[j] = aq;
-        B_[j] = av;
-        // sigmoid on the transcendental unit (exp2 and reciprocal, ~1 ulp each)
-        A_[j] = __builtin_amdgcn_rcpf(1.f + fast_exp2(-ag * kLog2e));
+        for (int j = 0; j < HP; ++j) {
+          q[j] = dot_lds<HP>(s_q + j * HP, x);
+          B_[j] = dot_lds<HP>(s_v + j * HP, x);
+          const float ag = dot_lds<HP>(s_a + j * HP, x);
+          A_[j] = __builtin_amdgcn_rcpf(1.f + fast_exp2(-ag * kLog2e));
+        }
       }
       // segmented inclusive scan of (A, B) across the wavefront
       int F = flag;
@@ -317,12 +370,17 @@ __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
         carry[j] = __shfl(h, 63);
         hq[j] = q[j] * h;
       }
-      // o_proj, then the gather projection
+      // o_proj, then the gather projection (folded: one product)
       float o[HP];
+      if constexpr (FOLD) {
 #pragma unroll
-      for (int j = 0; j < HP; ++j) o[j] = dot_lds<HP>(s_o + j * HP, hq);
+        for (int j = 0; j < HP; ++j) o[j] = hq[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < HP; ++j) o[j] = dot_lds<HP>(s_o + j * HP, hq);
+      }
       if (valid) {
-        const float *m = s_g + pg * L::kG;
+        const float *m = (FOLD ? f_o : s_g) + pg * L::kG;
         float *dst = orow + r * HP;
 #pragma unroll
         for (int j = 0; j < HP; j += 4) {
@@ -423,12 +481,23 @@ int launch_mos(const float *ev, int64_t E, int cin, int hid, const int64_t *src,
                int A, const float *ws, int As, const float *wq, const float *wv, const float *wg, const float *wo,
                const float *wgp, int Ag, const float *win, const float *ln_w, const float *ln_b, float eps,
                float *out, const MosWs &w, hipStream_t st) {
-  const size_t lds = MosW<CP, HP>::bytes(As, Ag);
+  typedef MosW<CP, HP> L;
+  const bool fold = L::fold_bytes(As, Ag) <= kMaxLds;
   if (R > 0) {
     const int64_t n_win = (R + kWin - 1) / kWin;
-    const int64_t wgs = std::min<int64_t>((n_win + 3) / 4, 4096);
-    hipLaunchKernelGGL((mos_patch_kernel<CP, HP>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads), lds, st, ev, E,
-                       cin, hid, src, pos, R, w.start, A, ws, As, wq, wv, wg, wo, wgp, Ag, w.orow);
+    const int64_t wgs = std::min<int64_t>((n_win + 3) / 4, 2048);
+    if (fold) {
+      const int64_t nf = static_cast<int64_t>(L::fold_floats(As, Ag));
+      hipLaunchKernelGGL((mos_fold_weights<CP, HP>), dim3(grid_for(nf)), dim3(kThreads), 0, st, ws, As, wq, wv, wg, wo,
+                         wgp, Ag, cin, hid, w.wfold);
+      hipLaunchKernelGGL((mos_patch_kernel<CP, HP, true>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads),
+                         L::fold_bytes(As, Ag), st, ev, E, cin, hid, src, pos, R, w.start, A, ws, As, wq, wv, wg, wo,
+                         wgp, Ag, w.wfold, w.orow);
+    } else {
+      hipLaunchKernelGGL((mos_patch_kernel<CP, HP, false>), dim3(static_cast<unsigned>(wgs)), dim3(kThreads),
+                         L::bytes(As, Ag), st, ev, E, cin, hid, src, pos, R, w.start, A, ws, As, wq, wv, wg, wo, wgp,
+                         Ag, w.wfold, w.orow);
+    }
   }
   if (E > 0)
     hipLaunchKernelGGL((mos_event_kernel<CP, HP>), dim3(grid_for(E)), dim3(kThreads), 0, st, ev, E, cin, hid, A,
@@ -458,7 +527,7 @@ extern "C" size_t ssla_mos_attention_workspace_size(int64_t n_events, int c_in, 
   using namespace ssla;
   const Tpl t = pick_tpl(c_in, hidden);
   if (n_events < 0 || A <= 0 || n_rows < 0 || n_patches < 0 || t.hp == 0) return 0;
-  return mos_layout(nullptr, n_events, A, n_rows, n_patches, t.hp).total;
+  return mos_layout(nullptr, n_events, A, n_rows, n_patches, t.cp, t.hp).total;
 }
 
 extern "C" size_t ssla_mos_attention_lds_bytes(int c_in, int hidden, int A, int scatter_per_pos, int gather_per_pos) {
@@ -466,8 +535,10 @@ extern "C" size_t ssla_mos_attention_lds_bytes(int c_in, int hidden, int A, int 
   const Tpl t = pick_tpl(c_in, hidden);
   if (t.hp == 0 || A <= 0) return 0;
   const int As = scatter_per_pos ? A : 1, Ag = gather_per_pos ? A : 1;
-  return sizeof(float) * (static_cast<size_t>(As) * (t.hp * t.cp + 4) + static_cast<size_t>(Ag) * (t.hp * t.hp + 4) +
-                          4 * static_cast<size_t>(t.hp) * t.hp);
+  const size_t kS = t.hp * t.cp + 4, kG = t.hp * t.hp + 4;
+  const size_t fold = sizeof(float) * (3 * As * kS + Ag * kG);
+  const size_t plain = sizeof(float) * (As * kS + Ag * kG + 4 * static_cast<size_t>(t.hp) * t.hp);
+  return fold <= kMaxLds ? fold : plain;   // the folded weights when they fit
 }
 
 extern "C" int ssla_mos_attention_fwd(const float *events, int64_t n_events, int c_in, const int64_t *row_src,
@@ -493,8 +564,8 @@ extern "C" int ssla_mos_attention_fwd(const float *events, int64_t n_events, int
     return SSLA_ERR_ARG;
   }
   const size_t lds = ssla_mos_attention_lds_bytes(c_in, hidden, A, scatter_per_pos, gather_per_pos);
-  if (lds > 64 * 1024) {
-    set_error("mos_attention_fwd: weights need %zu bytes of LDS (at most 65536)", lds);
+  if (lds > kMaxLds) {
+    set_error("mos_attention_fwd: weights need %zu bytes of LDS (at most %zu)", lds, kMaxLds);
     return SSLA_ERR_UNSUPPORTED;
   }
   SSLA_CHECK_ARG(n_rows < 0x7fffffff && n_events * A < (int64_t{1} << 40), "mos_attention_fwd: too many rows");
@@ -502,7 +573,7 @@ extern "C" int ssla_mos_attention_fwd(const float *events, int64_t n_events, int
   SSLA_CHECK_ARG(events && out && w_scatter && w_q && w_v && w_g && w_o && w_gather && ln_w && ln_b,
                  "mos_attention_fwd: null pointer");
   SSLA_CHECK_ARG(n_rows == 0 || (row_src && row_pos && patch_len), "mos_attention_fwd: null row arrays");
-  const MosWs w = mos_layout(workspace, n_events, A, n_rows, n_patches, tpl.hp);
+  const MosWs w = mos_layout(workspace, n_events, A, n_rows, n_patches, tpl.cp, tpl.hp);
   if (!workspace || workspace_bytes < w.total) {
     set_error("mos_attention_fwd: workspace of %zu bytes needed, %zu given", w.total, workspace_bytes);
     return SSLA_ERR_WORKSPACE;
