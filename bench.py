@@ -417,7 +417,7 @@ def main(argv=None):
                    "global_batch": C2["B"], "seq_len": C2["T"], "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "ssla_gla_chunk_fwd (state + fold + segment kernels, one call)",
+                     "kernel": "ssla_gla_chunk_fwd (state + segment kernels, one call)",
                      "kernel_avg_us": r["kernel_avg_ms"] * 1e3,
                      "algorithmic_bytes": alg_bytes},
         "mfma": {"achieved": tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -10,16 +10,16 @@
 //   S_c+1 = diag(exp(G_last)) S_c + (k_c * exp(G_last - G))^T v_c
 // with S_0 = h0 (or 0) and ht = S after the last chunk.
 //
-// Schedule (three launches; the only intermediates are per-segment states):
+// Schedule (two launches; the only intermediates are per-segment states):
 // * Each (sequence, head, V group) chain is cut into P segments of whole
 //   chunks (P chosen so that about two workgroups run per CU).
 // * state pass  : segments 0..P-2 run the state recurrence only (reads k, g,
 //   v) from h0 (segment 0) or zero, leaving the segment's final state and
 //   total log2-decay D in a workspace slot.
-// * prefix fold : E(1) = slot 0, E(s+1) = 2^D(s) E(s) + slot s, written back
-//   in place, so slot s-1 holds the state entering segment s.
-// * segment pass: every segment runs the full chunk loop from its entering
-//   state and writes o (and ht for the last segment).
+// * segment pass: every segment first folds the slots of the segments before
+//   it into its entering state (E = slot 0, E = 2^D(j) E + slot j for
+//   0 < j < s), then runs the full chunk loop from it and writes o (and ht
+//   for the last segment).
 //
 // Inside a workgroup (256 threads, 4 wavefronts): wavefront I owns chunk
 // rows 16I..16I+15 ("block" I) and state rows (keys) 16I..16I+15 as MFMA
@@ -396,7 +396,8 @@ struct ChunkArgs {
   const float *h0;
   uint16_t *o;
   float *ht;
-  const float *ws_state;   // [n_seq, H, P, K, V] fp32: slot s-1 = state entering segment s
+  const float *ws_state;   // [n_seq, H, P, K, V] fp32: slot s = local end state of segment s
+  const float *ws_decay;   // [n_seq, H, P, K] fp32: total log2 decay of segment s
   int64_t bos;             // first row of the sequence
   int64_t len;             // rows of the sequence
   int c_beg, c_end;        // chunk range of the segment
@@ -445,14 +446,54 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
   load_chunk<true, GF32>(buf, rs, a.c_beg < a.c_end, oq, og, ov + 2 * kq, kq, vw);
   f32x4 S[NVT];
   {
-    const float *src = nullptr;
-    if (a.seg == 0) src = a.h0 ? a.h0 + sbase * V : nullptr;
-    else src = a.ws_state + ((static_cast<int64_t>(a.n) * H + h) * a.P + (a.seg - 1)) * KD * V;
+    // entering state: h0 for segment 0, else the fold of the earlier
+    // segments' slots, E = slot 0, E = 2^D(j) E + slot j for 0 < j < seg (in
+    // this order, so every segment gets the same bits); slots and decays are
+    // loaded eight at a time, so up to 8 segments take one round trip
+    const int64_t chain = static_cast<int64_t>(a.n) * H + h;
+    const int64_t eo = static_cast<int64_t>(krow) * V + v0 + r;   // this lane's element (i = 0, t = 0)
+    if (a.seg == 0) {
+      const float *src = a.h0 ? a.h0 + sbase * V : nullptr;
 #pragma unroll
-    for (int t = 0; t < NVT; ++t)
+      for (int t = 0; t < NVT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        S[t][i] = src ? src[static_cast<int64_t>(krow + i) * V + v0 + 16 * t + r] : 0.f;
+        for (int i = 0; i < 4; ++i) S[t][i] = src ? src[eo + static_cast<int64_t>(i) * V + 16 * t] : 0.f;
+    } else {
+      const float *slots = a.ws_state + chain * a.P * KD * V + eo;
+      const float *dk = a.ws_decay + chain * a.P * KD + krow;
+      for (int j0 = 0; j0 < a.seg; j0 += 8) {
+        float x[8][NVT][4];
+        f32x4 d[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (j0 + u < a.seg) {
+            const float *sl = slots + static_cast<int64_t>(j0 + u) * KD * V;
+            d[u] = *reinterpret_cast<const f32x4 *>(dk + static_cast<int64_t>(j0 + u) * KD);
+#pragma unroll
+            for (int t = 0; t < NVT; ++t)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) x[u][t][i] = sl[static_cast<int64_t>(i) * V + 16 * t];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int j = j0 + u;
+          if (j == 0) {
+#pragma unroll
+            for (int t = 0; t < NVT; ++t)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) S[t][i] = x[u][t][i];
+          } else if (j < a.seg) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float f = fast_exp2(clamp_exp(d[u][i]));
+#pragma unroll
+              for (int t = 0; t < NVT; ++t) S[t][i] = fmaf(f, S[t][i], x[u][t][i]);
+            }
+          }
+        }
+      }
+    }
   }
   // Wait here for the entering state (and the first chunk, needed next
   // anyway): otherwise the loop's wait bookkeeping carries these loads
@@ -643,7 +684,7 @@ __global__ __launch_bounds__(256, SSLA_GC_SEG_WAVES) void gla_chunk_segment_kern
     const uint16_t *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int64_t T, int H, int V, float scale,
     const float *__restrict__ h0, uint16_t *__restrict__ o, float *__restrict__ ht, int P,
-    const float *__restrict__ ws_state) {
+    const float *__restrict__ ws_state, const float *__restrict__ ws_decay) {
   __shared__ SmemA sm;
   const int nvg = V / (16 * NVT);
   // block -> (sequence, head, V group, segment); the segments of one
@@ -659,6 +700,7 @@ __global__ __launch_bounds__(256, SSLA_GC_SEG_WAVES) void gla_chunk_segment_kern
   a.n = static_cast<int>(b / H);
   a.q = q; a.k = k; a.v = v; a.g = g; a.h0 = h0; a.o = o; a.ht = ht;
   a.ws_state = ws_state;
+  a.ws_decay = ws_decay;
   a.H = H; a.V = V; a.scale = scale;
   a.v0 = vg * 16 * NVT;
   a.bos = min(max(cu_seqlens[a.n], (int64_t)0), T);
@@ -805,40 +847,6 @@ __global__ __launch_bounds__(256, SSLA_GC_STATE_WAVES) void gla_chunk_state_kern
   if (wv == 0 && v0 == 0) ws_decay[slot * KD + lane] = dsum;
 }
 
-// ----------------------------------------------------------- prefix fold --
-// One thread per (sequence, head, key, column): E(1) = slot 0 and
-// E(s+1) = 2^D(s) E(s) + slot s for s = 1..P-2, written back in place.
-// Slots are read eight at a time ahead of the serial fold.
-__global__ __launch_bounds__(256) void gla_chunk_fold_kernel(float *__restrict__ ws_state,
-                                                             const float *__restrict__ ws_decay, int64_t n_elems,
-                                                             int V, int P) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n_elems) return;
-  const int64_t kv = static_cast<int64_t>(KD) * V;
-  const int64_t chain = i / kv, e = i % kv;
-  const int key = static_cast<int>(e / V);
-  float *base = ws_state + chain * P * kv + e;
-  const float *dec = ws_decay + chain * P * KD + key;
-  float acc = base[0];
-  for (int s0 = 1; s0 < P - 1; s0 += 8) {
-    float x[8], d[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int s = s0 + u;
-      x[u] = s < P - 1 ? base[s * kv] : 0.f;
-      d[u] = s < P - 1 ? dec[static_cast<int64_t>(s) * KD] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int s = s0 + u;
-      if (s < P - 1) {
-        acc = fmaf(fast_exp2(clamp_exp(d[u])), acc, x[u]);
-        base[s * kv] = acc;
-      }
-    }
-  }
-}
-
 inline int pick_nvt(int V) {
   const int tiles = V / 16;
   for (int nvt = 4; nvt >= 1; --nvt)
@@ -888,16 +896,11 @@ int launch_nvt(const void *q, const void *k, const void *v, const void *g, const
     hipLaunchKernelGGL((gla_chunk_state_kernel<DT, GF32, NVT>), dim3(static_cast<unsigned>(blocks_s)),
                        dim3(256), 0, st, static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
                        g, cu, n_seq, T, H, V, h0, P, ws_state, ws_decay);
-    if (P > 2) {
-      const int64_t n_elems = static_cast<int64_t>(n_seq) * H * KD * V;
-      hipLaunchKernelGGL(gla_chunk_fold_kernel, dim3(static_cast<unsigned>((n_elems + 255) / 256)), dim3(256), 0,
-                         st, ws_state, ws_decay, n_elems, V, P);
-    }
   }
   hipLaunchKernelGGL((gla_chunk_segment_kernel<DT, GF32, NVT>), dim3(static_cast<unsigned>(blocks_a)),
                      dim3(256), 0, st, q16, static_cast<const uint16_t *>(k),
                      static_cast<const uint16_t *>(v), g, cu, n_seq, T, H, V, scale, h0, o16, ht, P,
-                     ws_state);
+                     ws_state, ws_decay);
   return launch_status("gla_chunk_fwd");
 }
 
