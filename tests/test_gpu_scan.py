@@ -132,3 +132,48 @@ def test_sparse_scan_matches_steps(dev):
     o_a = torch.cat(outs)[torch.from_numpy(order).to(dev)]
     assert_close(o_b.cpu().numpy(), o_a.cpu().numpy(), 1e-4, "o")
     assert_close(st_b.cpu().numpy(), st_a.cpu().numpy(), 1e-4, "state")
+
+
+def test_sparse_step_graph_replay(dev):
+    """The per-bin pass (one ssla_sparse_gla_step launch per bin) captured as
+    one HIP graph: every replay, with eager work and synchronisations between
+    replays, reproduces the eager pass bit for bit (states and outputs)."""
+    from ssla_amd import _lib, synthetic
+    lib = _lib.load()
+    sb = synthetic.sparse_scan_bins(n_bins=12, seed=4)
+    bins = [dict(s=torch.from_numpy(sb.sites[b]).to(dev), q=sb.q[b].to(dev), k=sb.k[b].to(dev),
+                 v=sb.v[b].to(dev), g=sb.g[b].to(dev), o=torch.empty(sb.sites[b].size, 4, 32, device=dev))
+            for b in range(12)]
+    state0 = sb.state0.to(dev).contiguous()
+    state = state0.clone()
+
+    def one_pass(sh):
+        for x in bins:
+            _lib.check(lib.ssla_sparse_gla_step(x["s"].data_ptr(), x["s"].numel(), x["q"].data_ptr(),
+                                                x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
+                                                state.data_ptr(), sb.n_sites, 4, 32, 32, float(sb.scale),
+                                                x["o"].data_ptr(), sh), "sparse_gla_step")
+
+    one_pass(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    st_e, o_e = state.clone(), [x["o"].clone() for x in bins]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        state.copy_(state0)
+        one_pass(side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        one_pass(torch.cuda.current_stream().cuda_stream)
+    for rep in range(3):
+        state.copy_(state0)
+        for x in bins:
+            x["o"].fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"graph replay {rep}", flush=True)
+        assert torch.equal(state, st_e), f"state differs on replay {rep}"
+        for b, x in enumerate(bins):
+            assert torch.equal(x["o"], o_e[b]), f"o of bin {b} differs on replay {rep}"
