@@ -56,7 +56,7 @@ struct MosWs {
   int64_t *cu;       // [n_patch + 1] exclusive scan of the patch lengths
   uint8_t *start;    // [R] 1 at the first row of every patch
   int32_t *dst;      // [E * A] row of (event, position), or -1
-  float *orow;       // [R, HP] projected rows
+  float *orow;       // [R + 1, HP] projected rows, row R zero
   float *wfold;      // folded weights (3 A scatter-side + A gather-side matrices)
   void *tmp;
   size_t tmp_bytes, total;
@@ -82,7 +82,7 @@ MosWs mos_layout(void *base, int64_t E, int A, int64_t R, int64_t n_patch, int C
   w.cu = reinterpret_cast<int64_t *>(take(sizeof(int64_t) * (n_patch + 1)));
   w.start = reinterpret_cast<uint8_t *>(take(static_cast<size_t>(R)));
   w.dst = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * static_cast<size_t>(E) * A));
-  w.orow = reinterpret_cast<float *>(take(sizeof(float) * static_cast<size_t>(R) * HP));
+  w.orow = reinterpret_cast<float *>(take(sizeof(float) * static_cast<size_t>(R + 1) * HP));   // + zero row
   w.wfold = reinterpret_cast<float *>(
       take(sizeof(float) * (3 * static_cast<size_t>(A) * (HP * CP + 4) + static_cast<size_t>(A) * (HP * HP + 4))));
   w.tmp_bytes = scan_bytes(n_patch);
@@ -422,18 +422,30 @@ __global__ __launch_bounds__(kThreads) void mos_event_kernel(
     float y[HP];
 #pragma unroll
     for (int j = 0; j < HP; ++j) y[j] = 0.f;
-    for (int a = A - 1; a >= 0; --a) {
-      const int32_t r = dst[e * A + a];
-      if (r < 0 || r >= R) continue;
-      const float *o = orow + static_cast<int64_t>(r) * HP;
+    // copies in decreasing kernel position, three at a time with every row
+    // load issued before the adds (a missing copy reads the zero row R)
+    for (int a0 = A - 1; a0 >= 0; a0 -= 3) {
+      const float *p[3];
 #pragma unroll
-      for (int j = 0; j < HP; j += 4) {
-        const float4 t = *reinterpret_cast<const float4 *>(o + j);
-        y[j] += t.x;
-        if (j + 1 < HP) y[j + 1] += t.y;
-        if (j + 2 < HP) y[j + 2] += t.z;
-        if (j + 3 < HP) y[j + 3] += t.w;
+      for (int u = 0; u < 3; ++u) {
+        const int a = a0 - u;
+        const int32_t r = a >= 0 ? dst[e * A + a] : -1;
+        p[u] = orow + (r >= 0 && r < R ? static_cast<int64_t>(r) : R) * HP;
       }
+      float4 t[3][HP / 4];
+#pragma unroll
+      for (int u = 0; u < 3; ++u)
+#pragma unroll
+        for (int j = 0; j < HP / 4; ++j) t[u][j] = reinterpret_cast<const float4 *>(p[u])[j];
+#pragma unroll
+      for (int u = 0; u < 3; ++u)
+#pragma unroll
+        for (int j = 0; j < HP / 4; ++j) {
+          y[4 * j] += t[u][j].x;
+          y[4 * j + 1] += t[u][j].y;
+          y[4 * j + 2] += t[u][j].z;
+          y[4 * j + 3] += t[u][j].w;
+        }
     }
     float x[CP];
     fetch_row<CP>(x, ev, e, cin);
@@ -580,6 +592,8 @@ extern "C" int ssla_mos_attention_fwd(const float *events, int64_t n_events, int
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(mos_fill_i32, dim3(grid_for(n_events * A)), dim3(kThreads), 0, st, w.dst, n_events * A, -1);
+  hipLaunchKernelGGL(mos_fill_i32, dim3(1), dim3(kThreads), 0, st, reinterpret_cast<int32_t *>(w.orow + n_rows * tpl.hp),
+                     static_cast<int64_t>(tpl.hp), 0);   // the zero row
   if (n_rows > 0) {
     hipLaunchKernelGGL(mos_fill_u8, dim3(grid_for(n_rows)), dim3(kThreads), 0, st, w.start, n_rows);
     if (n_patches > 0) {
