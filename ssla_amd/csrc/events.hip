@@ -251,10 +251,12 @@ __global__ void rf_pixmap(const int64_t *__restrict__ gb, const int64_t *__restr
   }
 }
 
-// per field (b, rf): number of events, active flag
+// per field (b, rf): number of events, active flag, and (pk non-null) both
+// packed as nev * 2^21 + act, so that one prefix sum yields both
+constexpr int kPackBits = 21;
 __global__ void rf_count(const int64_t *__restrict__ lut, int64_t n_rf, int A, int B, int H, int W,
                          const int32_t *__restrict__ pixmap, const int64_t *__restrict__ glen,
-                         int64_t *__restrict__ nev, int64_t *__restrict__ act) {
+                         int64_t *__restrict__ nev, int64_t *__restrict__ act, int64_t *__restrict__ pk) {
   GRID_STRIDE(f, static_cast<int64_t>(B) * n_rf) {
     const int64_t b = f / n_rf, r = f % n_rf;
     int64_t n = 0, a_ = 0;
@@ -268,6 +270,23 @@ __global__ void rf_count(const int64_t *__restrict__ lut, int64_t n_rf, int A, i
     }
     nev[f] = n;
     act[f] = a_;
+    if (pk) pk[f] = (n << kPackBits) | a_;
+  }
+}
+
+// act_pre / ev_pre and their totals (counts[0], counts[1]) from the prefix
+// sum of the packed pairs
+__global__ void rf_unpack(const int64_t *__restrict__ pk_pre, const int64_t *__restrict__ pk, int64_t n,
+                          int64_t *__restrict__ act_pre, int64_t *__restrict__ ev_pre, int64_t *__restrict__ counts) {
+  constexpr int64_t mask = (int64_t{1} << kPackBits) - 1;
+  GRID_STRIDE(f, n) {
+    act_pre[f] = pk_pre[f] & mask;
+    ev_pre[f] = pk_pre[f] >> kPackBits;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const int64_t t = n > 0 ? pk_pre[n - 1] + pk[n - 1] : 0;
+    counts[0] = t & mask;
+    counts[1] = t >> kPackBits;
   }
 }
 
@@ -819,14 +838,24 @@ extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h
                        L.pixmap, L.bad);
   int s = excl_scan(L.tmp, L.tmp_bytes, gr_len, L.gstart, G, st);
   if (s) return s;
+  // one prefix sum of the packed (events, active) pairs while the active
+  // count fits 21 bits (f_index / f_len hold the pairs until rf_fields)
+  const bool packed = n_f < (int64_t{1} << kPackBits);
   hipLaunchKernelGGL(rf_count, dim3(grid_for(n_f)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap, gr_len,
-                     L.nev, L.act);
-  s = excl_scan(L.tmp, L.tmp_bytes, L.act, L.act_pre, n_f, st);
-  if (s) return s;
-  s = excl_scan(L.tmp, L.tmp_bytes, L.nev, L.ev_pre, n_f, st);
-  if (s) return s;
-  hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.act_pre, L.act, n_f, L.counts + 0);
-  hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.ev_pre, L.nev, n_f, L.counts + 1);
+                     L.nev, L.act, packed ? L.f_index : nullptr);
+  if (packed) {
+    s = excl_scan(L.tmp, L.tmp_bytes, L.f_index, L.f_len, n_f, st);
+    if (s) return s;
+    hipLaunchKernelGGL(rf_unpack, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.f_len, L.f_index, n_f, L.act_pre,
+                       L.ev_pre, L.counts);
+  } else {
+    s = excl_scan(L.tmp, L.tmp_bytes, L.act, L.act_pre, n_f, st);
+    if (s) return s;
+    s = excl_scan(L.tmp, L.tmp_bytes, L.nev, L.ev_pre, n_f, st);
+    if (s) return s;
+    hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.act_pre, L.act, n_f, L.counts + 0);
+    hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.ev_pre, L.nev, n_f, L.counts + 1);
+  }
   if (E_in > 0)
     hipLaunchKernelGGL(max_i64, dim3(grid_for(std::min<int64_t>(E_in, 1 << 16))), dim3(kThreads), 0, st, time, E_in,
                        L.tmax);
