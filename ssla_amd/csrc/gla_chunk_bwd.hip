@@ -193,19 +193,17 @@ __device__ __forceinline__ void gate_cumsum(float (&gt)[BT][LD], float (&psum)[N
 }
 
 template <bool REV, int DT, bool GF32>
-__global__ __launch_bounds__(256) void bwd_seg_pass(const uint16_t *__restrict__ X, const uint16_t *__restrict__ Y,
-                                                    const void *__restrict__ g, const int64_t *__restrict__ cu,
-                                                    const int64_t *__restrict__ coff,
-                                                    const int64_t *__restrict__ sgoff, int n_seq, int64_t T, int H,
-                                                    int V, float xscale, float *__restrict__ loc,
-                                                    float *__restrict__ dec, float *__restrict__ eloc,
-                                                    float *__restrict__ dtot) {
-  __shared__ SmemP sm;
+__device__ __forceinline__ void seg_pass(SmemP &sm, const int64_t bid, const uint16_t *__restrict__ X,
+                                         const uint16_t *__restrict__ Y, const void *__restrict__ g,
+                                         const int64_t *__restrict__ cu, const int64_t *__restrict__ coff,
+                                         const int64_t *__restrict__ sgoff, int n_seq, int64_t T, int H, int V,
+                                         float xscale, float *__restrict__ loc, float *__restrict__ dec,
+                                         float *__restrict__ eloc, float *__restrict__ dtot) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
-  const int h = static_cast<int>(blockIdx.x % H);
-  const int64_t sg = blockIdx.x / H;
+  const int h = static_cast<int>(bid % H);
+  const int64_t sg = bid / H;
   if (sg >= sgoff[n_seq]) return;   // workgroup-uniform
   const int n = find_seq(sgoff, n_seq, sg);
   int64_t bos, eos;
@@ -337,6 +335,28 @@ __global__ __launch_bounds__(256) void bwd_seg_pass(const uint16_t *__restrict__
     }
     if (w == 0) dtot[(sg * H + h) * KD + lane] = D;
   }
+}
+
+// Both passes in one launch: blocks [0, nb) run the forward pass (X = k,
+// Y = v), blocks [nb, 2 nb) the reverse pass (X = scale q, Y = do); they are
+// independent, so the two halves fill the GPU together.
+template <int DT, bool GF32>
+__global__ __launch_bounds__(256) void bwd_seg_passes(const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+                                                      const uint16_t *__restrict__ q, const uint16_t *__restrict__ dout,
+                                                      const void *__restrict__ g, const int64_t *__restrict__ cu,
+                                                      const int64_t *__restrict__ coff,
+                                                      const int64_t *__restrict__ sgoff, int n_seq, int64_t T, int H,
+                                                      int V, float scale, int64_t nb, float *__restrict__ hloc,
+                                                      float *__restrict__ dfw, float *__restrict__ eloc,
+                                                      float *__restrict__ dtot, float *__restrict__ dloc,
+                                                      float *__restrict__ drv) {
+  __shared__ SmemP sm;
+  const int64_t b = blockIdx.x;
+  if (b < nb)
+    seg_pass<false, DT, GF32>(sm, b, k, v, g, cu, coff, sgoff, n_seq, T, H, V, 1.f, hloc, dfw, eloc, dtot);
+  else
+    seg_pass<true, DT, GF32>(sm, b - nb, q, dout, g, cu, coff, sgoff, n_seq, T, H, V, scale, dloc, drv, nullptr,
+                             nullptr);
 }
 
 // Carries states across the segments of one (sequence, head):
@@ -782,11 +802,9 @@ int launch_bwd(const void *q, const void *k, const void *v, const void *g, const
   hipLaunchKernelGGL(bwd_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T, w.coff, w.sgoff);
   const int64_t cmax = (T + BT - 1) / BT + n_seq;
   const int64_t smax = (cmax + kSegC - 1) / kSegC + n_seq;
-  hipLaunchKernelGGL((bwd_seg_pass<false, DT, GF32>), dim3(static_cast<unsigned>(smax * H)), dim3(256), 0, st, Kp, Vp,
-                     g, cu, w.coff, w.sgoff, n_seq, T, H, V, 1.f, w.hloc, w.dfw, w.eloc, w.dtot);
-  hipLaunchKernelGGL((bwd_seg_pass<true, DT, GF32>), dim3(static_cast<unsigned>(smax * H)), dim3(256), 0, st, Q, DO, g,
-                     cu, w.coff, w.sgoff, n_seq, T, H, V, scale, w.dloc, w.drv, static_cast<float *>(nullptr),
-                     static_cast<float *>(nullptr));
+  const int64_t nb = smax * H;
+  hipLaunchKernelGGL((bwd_seg_passes<DT, GF32>), dim3(static_cast<unsigned>(2 * nb)), dim3(256), 0, st, Kp, Vp, Q, DO,
+                     g, cu, w.coff, w.sgoff, n_seq, T, H, V, scale, nb, w.hloc, w.dfw, w.eloc, w.dtot, w.dloc, w.drv);
   const int64_t fold_threads = static_cast<int64_t>(n_seq) * H * KD * V;
   hipLaunchKernelGGL(bwd_fold_kernel, dim3(static_cast<unsigned>((fold_threads + 255) / 256)), dim3(256), 0, st,
                      w.coff, w.sgoff, n_seq, H, V, h0, dht, w.eloc, w.dtot, w.dloc, w.sin_, w.dsend, dh0);
