@@ -91,3 +91,17 @@ def test_chunk_bwd_unsupported_raises(dev):
     v = torch.randn(10, 1, 128, device=dev, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
         chunk_gla(q, q.detach(), v, torch.zeros(10, 1, 64, device=dev), torch.tensor([0, 10], device=dev))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_chunk_bwd_16bit_gates(dev, dtype):
+    """g in the input dtype (the kernels' 16-bit gate path; dg comes back in
+    that dtype): the oracle sees the same rounded gates."""
+    q, k, v, g, cu, s0, do, dht = _inputs([150, 64, 37, 1], 2, 64, dtype, seed=11, gate="randn-1")
+    g16 = g.to(dtype)
+    print(f"gla bwd 16-bit gates: {dtype}", flush=True)
+    got = _gpu_grads(dev, q, k, v, g16, cu, s0, do, dht, 64 ** -0.5)
+    ref = oracle.gla_recurrent_bwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), g16.float().numpy(),
+                                   cu.numpy(), do.float().numpy(), 64 ** -0.5, s0.numpy(), dht.numpy())
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dh0"), got, ref):
+        assert_close(a, b, RTOL, f"{name}[16-bit g {dtype}]", ratio_mode=True)
