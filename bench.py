@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
-Headline workload: chunked GLA forward, B=8 sequences x
+Headline workload (config 2, C2): chunked GLA forward, B=8 sequences x
 T=4096 tokens, H=8, K=V=64, chunk 64, bf16 q/k/v/o, fp32 g/h0/ht.  One
 "step" = one call of ssla_gla_chunk_fwd over the whole batch with inputs
 already resident in HBM.  Two input sets (2 x 203 MB, more than the 256 MB
@@ -527,7 +527,7 @@ def main(argv=None):
         "value": value, "unit": "Mtok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "chunk_gla_fwd (BASELINE config 2): B=8, H=8, T=4096, K=V=64, chunk 64; "
+        "config": {"workload": "chunk_gla_fwd (config 2, C2): B=8, H=8, T=4096, K=V=64, chunk 64; "
                                "bf16 q/k/v/o, fp32 g/h0/ht; 2 input sets alternating (> MALL)",
                    "global_batch": C2["B"], "seq_len": C2["T"], "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",

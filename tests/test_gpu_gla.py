@@ -58,7 +58,7 @@ def _run(fn, q, k, v, g, cu, s0, scale, dev):
 
 
 def test_recurrent_c1_fp32(dev):
-    """N=1, H=4, T=256, K=V=32, fp32, q pre-scaled by
+    """Config 1 (C1): N=1, H=4, T=256, K=V=32, fp32, q pre-scaled by
     1/sqrt(32) and scale=1.0, zero initial state."""
     from ssla_amd.gla import fused_recurrent_gla
     torch.manual_seed(0)
@@ -130,7 +130,7 @@ def test_chunk_matches_recurrent_kernel(dev):
 
 
 def test_chunk_c2_full(dev):
-    """BASELINE config 2 at full size: B=8, H=8, T=4096, D=64, bf16,
+    """Config 2 (C2) at full size: B=8, H=8, T=4096, D=64, bf16,
     h0 ~ N(0, 0.1), vs the fp64 naive recurrence."""
     from ssla_amd import synthetic
     from ssla_amd.gla import chunk_gla

@@ -84,7 +84,7 @@ def test_scan_layer_shapes(dev):
 
 
 def test_sparse_step_c3_bins(dev):
-    """BASELINE config 3 (76x60 sites, H=4, D=32), first 16 bins: o and all
+    """Config 3 (C3: 76x60 sites, H=4, D=32), first 16 bins: o and all
     states checked after every bin; inactive states bit-identical."""
     from ssla_amd import synthetic
     from ssla_amd.scan import sparse_gla_step

@@ -140,7 +140,7 @@ def test_out_of_range_index_raises(dev):
 
 
 def test_c4_full(dev):
-    """BASELINE config 4 at full size: 1e6 clustered events, C=64, 152x120
+    """Config 4 (C4) at full size: 1e6 clustered events, C=64, 152x120
     cells; shuffled (bucketing path) and sorted (segment path)."""
     from ssla_amd import synthetic
     src, index, n_out = synthetic.pooling_events()
