@@ -73,7 +73,9 @@ const char *ssla_last_error(void);
  * BF16 or F16, K == 64, V a multiple of 16 (<= 256).
  * Each sequence is split into segments processed in parallel; the
  * workspace (ssla_gla_chunk_workspace_size bytes, 16-byte aligned, no
- * initialisation needed) holds one fp32 state per segment.  A size of 0
+ * initialisation needed) holds one bf16 state (as the reference stores its
+ * per-chunk states, ops/gla/chunk.py:933) and one fp32 decay row per
+ * segment.  A size of 0
  * means no workspace is needed for this shape (pass NULL, 0). */
 size_t ssla_gla_chunk_workspace_size(int n_seq, int64_t T, int H, int K, int V);
 

@@ -14,8 +14,9 @@
 // * Each (sequence, head, V group) chain is cut into P segments of whole
 //   chunks (P chosen so that about two workgroups run per CU).
 // * state pass  : segments 0..P-2 run the state recurrence only (reads k, g,
-//   v) from h0 (segment 0) or zero, leaving the segment's final state and
-//   total log2-decay D in a workspace slot.
+//   v) from h0 (segment 0) or zero, leaving the segment's final state (in
+//   bf16, as the reference keeps its per-chunk states) and total log2-decay
+//   D in a workspace slot.
 // * segment pass: every segment first folds the slots of the segments before
 //   it into its entering state (E = slot 0, E = 2^D(j) E + slot j for
 //   0 < j < s), then runs the full chunk loop from it and writes o (and ht
@@ -390,13 +391,29 @@ __device__ __forceinline__ void store_state(uint16_t *sth, int vcol, int krow, c
   *reinterpret_cast<uint2 *>(sth + swz(vcol, krow)) = make_uint2(b.x, b.y);
 }
 
+// Position of a lane's accumulator tiles inside a workspace slot: the
+// state pass writes, and the segment pass reads, the 4*NVT values of each
+// lane (tile t, rows i) as one contiguous run, so both use 8-byte accesses.
+template <int NVT>
+__device__ __forceinline__ int64_t slot_index(int v0, int wv, int lane) {
+  return static_cast<int64_t>((v0 / (16 * NVT) * 4 + wv) * 64 + lane) * (4 * NVT);
+}
+
+// Four bf16 values (packed low half first) -> fp32.
+__device__ __forceinline__ void unpack_bf16x4(const uint2 &b, float (&x)[4]) {
+  x[0] = __uint_as_float(b.x << 16);
+  x[1] = __uint_as_float(b.x & 0xffff0000u);
+  x[2] = __uint_as_float(b.y << 16);
+  x[3] = __uint_as_float(b.y & 0xffff0000u);
+}
+
 struct ChunkArgs {
   const uint16_t *q, *k, *v;
   const void *g;
   const float *h0;
   uint16_t *o;
   float *ht;
-  const float *ws_state;   // [n_seq, H, P, K, V] fp32: slot s = local end state of segment s
+  const uint16_t *ws_state;  // [n_seq, H, P] slots of K*V bf16 in slot_index order: local end state of segment s
   const float *ws_decay;   // [n_seq, H, P, K] fp32: total log2 decay of segment s
   int64_t bos;             // first row of the sequence
   int64_t len;             // rows of the sequence
@@ -459,22 +476,25 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
 #pragma unroll
         for (int i = 0; i < 4; ++i) S[t][i] = src ? src[eo + static_cast<int64_t>(i) * V + 16 * t] : 0.f;
     } else {
-      const float *slots = a.ws_state + chain * a.P * KD * V + eo;
+      const uint16_t *slots = a.ws_state + chain * a.P * KD * V + slot_index<NVT>(a.v0, wv, lane);
       const float *dk = a.ws_decay + chain * a.P * KD + krow;
       for (int j0 = 0; j0 < a.seg; j0 += 8) {
-        float x[8][NVT][4];
+        uint2 xb[8][NVT];
         f32x4 d[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           if (j0 + u < a.seg) {
-            const float *sl = slots + static_cast<int64_t>(j0 + u) * KD * V;
+            const uint16_t *sl = slots + static_cast<int64_t>(j0 + u) * KD * V;
             d[u] = *reinterpret_cast<const f32x4 *>(dk + static_cast<int64_t>(j0 + u) * KD);
 #pragma unroll
-            for (int t = 0; t < NVT; ++t)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) x[u][t][i] = sl[static_cast<int64_t>(i) * V + 16 * t];
+            for (int t = 0; t < NVT; ++t) xb[u][t] = *reinterpret_cast<const uint2 *>(sl + 4 * t);
           }
         }
+        float x[8][NVT][4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int t = 0; t < NVT; ++t) unpack_bf16x4(xb[u][t], x[u][t]);
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int j = j0 + u;
@@ -684,7 +704,7 @@ __global__ __launch_bounds__(256, SSLA_GC_SEG_WAVES) void gla_chunk_segment_kern
     const uint16_t *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int64_t T, int H, int V, float scale,
     const float *__restrict__ h0, uint16_t *__restrict__ o, float *__restrict__ ht, int P,
-    const float *__restrict__ ws_state, const float *__restrict__ ws_decay) {
+    const uint16_t *__restrict__ ws_state, const float *__restrict__ ws_decay) {
   __shared__ SmemA sm;
   const int nvg = V / (16 * NVT);
   // block -> (sequence, head, V group, segment); the segments of one
@@ -727,7 +747,7 @@ template <int DT, bool GF32, int NVT>
 __global__ __launch_bounds__(256, SSLA_GC_STATE_WAVES) void gla_chunk_state_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int64_t T, int H, int V,
-    const float *__restrict__ h0, int P, float *__restrict__ ws_state, float *__restrict__ ws_decay) {
+    const float *__restrict__ h0, int P, uint16_t *__restrict__ ws_state, float *__restrict__ ws_decay) {
   typedef Mfma<DT> M;
   typedef typename M::Vec MV;
   __shared__ SmemS sm;
@@ -839,11 +859,13 @@ __global__ __launch_bounds__(256, SSLA_GC_STATE_WAVES) void gla_chunk_state_kern
   if (c < c_end) chunk_step(buf, buf2, c);
 
   const int64_t slot = (static_cast<int64_t>(n) * H + h) * P + seg;
-  float *dst = ws_state + slot * KD * V;
+  uint16_t *dst = ws_state + slot * KD * V + slot_index<NVT>(v0, wv, lane);
 #pragma unroll
-  for (int t = 0; t < NVT; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[static_cast<int64_t>(krow + i) * V + v0 + 16 * t + r] = S[t][i];
+  for (int t = 0; t < NVT; ++t) {
+    const f32x8 s8 = {S[t][0], S[t][1], S[t][2], S[t][3], 0.f, 0.f, 0.f, 0.f};
+    const uint4 bits = to_bits(QK::cvt(s8));
+    *reinterpret_cast<uint2 *>(dst + 4 * t) = make_uint2(bits.x, bits.y);
+  }
   if (wv == 0 && v0 == 0) ws_decay[slot * KD + lane] = dsum;
 }
 
@@ -876,13 +898,13 @@ inline int pick_segments(int n_seq, int64_t T, int H, int V) {
 inline size_t workspace_bytes_for(int n_seq, int H, int V, int P) {
   if (P <= 1) return 0;
   const size_t slots = static_cast<size_t>(n_seq) * H * P;
-  return slots * KD * V * sizeof(float) + slots * KD * sizeof(float);
+  return slots * KD * V * sizeof(uint16_t) + slots * KD * sizeof(float);
 }
 
 template <int DT, bool GF32, int NVT>
 int launch_nvt(const void *q, const void *k, const void *v, const void *g, const int64_t *cu, int n_seq,
                int64_t T, int H, int V, float scale, const float *h0, void *o, float *ht, int P,
-               float *ws_state, float *ws_decay, hipStream_t st) {
+               uint16_t *ws_state, float *ws_decay, hipStream_t st) {
   const int nvg = V / (16 * NVT);
   const int64_t blocks_a = static_cast<int64_t>(n_seq) * H * nvg * P;
   if (blocks_a > 0x7fffffff) {
@@ -907,7 +929,7 @@ int launch_nvt(const void *q, const void *k, const void *v, const void *g, const
 template <int DT, bool GF32>
 int launch_chunk(const void *q, const void *k, const void *v, const void *g, const int64_t *cu, int n_seq,
                  int64_t T, int H, int V, float scale, const float *h0, void *o, float *ht, int P,
-                 float *ws_state, float *ws_decay, hipStream_t st) {
+                 uint16_t *ws_state, float *ws_decay, hipStream_t st) {
   switch (pick_nvt(V)) {
     case 4: return launch_nvt<DT, GF32, 4>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
     case 3: return launch_nvt<DT, GF32, 3>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
@@ -963,8 +985,9 @@ extern "C" int ssla_gla_chunk_fwd(const void *q, const void *k, const void *v, c
     return SSLA_ERR_WORKSPACE;
   }
   SSLA_CHECK_ARG(need == 0 || aligned(workspace, 16), "gla_chunk_fwd: workspace must be 16-byte aligned");
-  float *ws_state = static_cast<float *>(workspace);
-  float *ws_decay = need ? ws_state + static_cast<size_t>(n_seq) * H * P * KD * V : nullptr;
+  uint16_t *ws_state = static_cast<uint16_t *>(workspace);
+  // slots are K*V*2 bytes (a multiple of 2048), so the decays stay 16-byte aligned
+  float *ws_decay = need ? reinterpret_cast<float *>(ws_state + static_cast<size_t>(n_seq) * H * P * KD * V) : nullptr;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool gf32 = g_dtype == SSLA_F32;
   if (dtype == SSLA_BF16)
