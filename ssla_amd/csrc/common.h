@@ -25,6 +25,12 @@ void clear_error();
     }                                        \
   } while (0)
 
+// Copy `bytes` (at most 4096) of device memory to host memory and wait for
+// the stream: one copy into a per-thread pinned staging buffer (a pageable
+// destination makes the runtime stage and synchronise each copy itself).
+// Returns the HIP error.
+hipError_t read_to_host(void *dst, const void *src, size_t bytes, hipStream_t st);
+
 inline int launch_status(const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -655,16 +655,17 @@ extern "C" int ssla_events_counts(const void *workspace, int64_t *counts_out, in
   clear_error();
   SSLA_CHECK_ARG(workspace && counts_out && n_counts > 0 && n_counts <= 8, "events_counts: bad arguments");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int64_t buf[8] = {0};
-  int32_t badv[8] = {0};
-  hipError_t e = hipMemcpyAsync(buf, workspace, sizeof(buf), hipMemcpyDeviceToHost, st);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(badv, static_cast<const char *>(workspace) + 256, sizeof(badv), hipMemcpyDeviceToHost, st);
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  // counts at byte 0, the bad-input flag at byte 256: one read covers both
+  unsigned char raw[256 + sizeof(int32_t)];
+  const hipError_t e = read_to_host(raw, workspace, sizeof(raw), st);
   if (e != hipSuccess) {
     set_error("events_counts: %s", hipGetErrorString(e));
     return SSLA_ERR_LAUNCH;
   }
+  int64_t buf[8];
+  int32_t badv[1];
+  memcpy(buf, raw, sizeof(buf));
+  memcpy(badv, raw + 256, sizeof(badv));
   for (int i = 0; i < n_counts; ++i) counts_out[i] = buf[i];
   if (bad_out) *bad_out = badv[0];
   return SSLA_OK;

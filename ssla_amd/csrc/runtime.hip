@@ -16,6 +16,23 @@ void set_error(const char *fmt, ...) {
 
 void clear_error() { g_last_error[0] = '\0'; }
 
+hipError_t read_to_host(void *dst, const void *src, size_t bytes, hipStream_t st) {
+  constexpr size_t kStage = 4096;
+  // one pinned buffer per host thread, kept until the process ends
+  static thread_local void *stage = nullptr;
+  if (bytes > kStage) return hipErrorInvalidValue;
+  if (stage == nullptr) {
+    void *p = nullptr;
+    const hipError_t e = hipHostMalloc(&p, kStage, hipHostMallocDefault);
+    if (e != hipSuccess) return e;
+    stage = p;
+  }
+  hipError_t e = hipMemcpyAsync(stage, src, bytes, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e == hipSuccess) memcpy(dst, stage, bytes);
+  return e;
+}
+
 }  // namespace ssla
 
 extern "C" int ssla_version(void) { return 100; }

@@ -813,8 +813,7 @@ extern "C" int ssla_scatter_check(const void *workspace, int *status_out, void *
   SSLA_CHECK_ARG(workspace && status_out, "scatter_check: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   int32_t v = 0;
-  hipError_t e = hipMemcpyAsync(&v, workspace, sizeof(int32_t), hipMemcpyDeviceToHost, st);
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  const hipError_t e = ssla::read_to_host(&v, workspace, sizeof(int32_t), st);
   if (e != hipSuccess) {
     ssla::set_error("scatter_check: %s", hipGetErrorString(e));
     return SSLA_ERR_LAUNCH;
