@@ -102,6 +102,40 @@ __global__ void fill_i64(int64_t *p, int64_t n, int64_t v) { GRID_STRIDE(i, n) p
 __global__ void fill_i32(int32_t *p, int64_t n, int32_t v) { GRID_STRIDE(i, n) p[i] = v; }
 __global__ void iota_i32(int32_t *p, int64_t n) { GRID_STRIDE(i, n) p[i] = static_cast<int32_t>(i); }
 
+// One launch for a call's set-up fills: the 8 count words and 8 status
+// flags to zero, a[0..na) = va and b[0..nb) = vb (either range may be
+// empty).  Grid: grid_for(max(8, na, nb)).
+__global__ void clear_and_fill(int64_t *counts, int32_t *bad, int64_t *a, int64_t na, int64_t va, int32_t *b,
+                               int64_t nb, int32_t vb) {
+  GRID_STRIDE(i, 8) {
+    counts[i] = 0;
+    bad[i] = 0;
+  }
+  GRID_STRIDE(i, na) a[i] = va;
+  GRID_STRIDE(i, nb) b[i] = vb;
+}
+
+// Sorted-fill set-up in one launch: inv and dst to -1, and the field
+// index / length rows of the plan copied to the outputs.
+__global__ void rf_sorted_setup(int32_t *inv, int64_t n_inv, int32_t *dst, int64_t n_dst, int64_t *f_index,
+                                const int64_t *plan_index, int64_t *f_len, const int64_t *plan_len, int64_t n_act) {
+  GRID_STRIDE(i, n_inv) inv[i] = -1;
+  GRID_STRIDE(i, n_dst) dst[i] = -1;
+  GRID_STRIDE(i, n_act) {
+    f_index[i] = plan_index[i];
+    f_len[i] = plan_len[i];
+  }
+}
+
+// Group-events set-up: key[i] = pad (sorts last), val[i] = i, row[i] = 0.
+__global__ void ge_init(int64_t *key, int32_t *val, int64_t *row, int64_t n, int64_t pad) {
+  GRID_STRIDE(i, n) {
+    key[i] = pad;
+    val[i] = static_cast<int32_t>(i);
+    row[i] = 0;
+  }
+}
+
 // counts[k] = a[n-1] + b[n-1] (inclusive total from an exclusive scan), or 0.
 __global__ void total_from_scan(const int64_t *excl, const int64_t *val, int64_t n, int64_t *dst) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *dst = n > 0 ? excl[n - 1] + val[n - 1] : 0;
@@ -614,21 +648,22 @@ extern "C" int ssla_group_events(const float *events, const int64_t *lengths, in
                  "group_events: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t *Ep = L.off + B;
-  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, L.counts, (int64_t)8, (int64_t)0);
-  hipLaunchKernelGGL(fill_i32, dim3(1), dim3(kThreads), 0, st, L.bad, (int64_t)8, 0);
-  if (cap == 0) return launch_status("group_events");
+  if (cap == 0) {
+    hipLaunchKernelGGL(clear_and_fill, dim3(1), dim3(kThreads), 0, st, L.counts, L.bad, nullptr, (int64_t)0,
+                       (int64_t)0, nullptr, (int64_t)0, 0);
+    return launch_status("group_events");
+  }
   // sample offsets: exclusive scan of the lengths clamped to [0, N]
-  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, L.kept, (int64_t)(B + 1), (int64_t)0);
+  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max<int64_t>(8, B + 1))), dim3(kThreads), 0, st, L.counts,
+                     L.bad, L.kept, (int64_t)(B + 1), (int64_t)0, nullptr, (int64_t)0, 0);
   hipLaunchKernelGGL(trunc_len, dim3(grid_for(B)), dim3(kThreads), 0, st, lengths, (int64_t)B, N, L.kept);
   int s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.off, B + 1, st);
   if (s) return s;
   // keys of the valid events (pixel ids < B*H*W); padding slots take the key
   // B*H*W and sort last, so only the bits of B*H*W need sorting
   const int64_t n_pix = static_cast<int64_t>(B) * H * W;
-  hipLaunchKernelGGL(fill_i64, dim3(grid_for(cap)), dim3(kThreads), 0, st, reinterpret_cast<int64_t *>(L.key), cap,
-                     n_pix);
-  hipLaunchKernelGGL(iota_i32, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.val, cap);
-  hipLaunchKernelGGL(fill_i64, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.row_of, cap, (int64_t)0);
+  hipLaunchKernelGGL(ge_init, dim3(grid_for(cap)), dim3(kThreads), 0, st, reinterpret_cast<int64_t *>(L.key), L.val,
+                     L.row_of, cap, n_pix);
   hipLaunchKernelGGL(ge_keys, dim3(grid_for(cap)), dim3(kThreads), 0, st, events, lengths, L.off, B, N, C, H, W,
                      L.key, L.val, L.row_of, L.bad);
   s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.order, cap, bits_for(static_cast<uint64_t>(n_pix)), st);
@@ -836,11 +871,8 @@ extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h
   SSLA_CHECK_ARG(lut && (G == 0 || (gr_batch && gr_h && gr_w && gr_len)) && (E_in == 0 || time),
                  "rf_scatter_plan: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, L.counts, (int64_t)8, (int64_t)0);
-  hipLaunchKernelGGL(fill_i32, dim3(1), dim3(kThreads), 0, st, L.bad, (int64_t)8, 0);
-  hipLaunchKernelGGL(fill_i64, dim3(1), dim3(kThreads), 0, st, reinterpret_cast<int64_t *>(L.tmax), (int64_t)1,
-                     (int64_t)0);
-  hipLaunchKernelGGL(fill_i32, dim3(grid_for(n_pix)), dim3(kThreads), 0, st, L.pixmap, n_pix, -1);
+  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max<int64_t>(8, n_pix))), dim3(kThreads), 0, st, L.counts,
+                     L.bad, reinterpret_cast<int64_t *>(L.tmax), (int64_t)1, (int64_t)0, L.pixmap, n_pix, -1);
   if (G > 0)
     hipLaunchKernelGGL(rf_pixmap, dim3(grid_for(G)), dim3(kThreads), 0, st, gr_batch, gr_h, gr_w, G, H, W, n_pix,
                        L.pixmap, L.bad);
@@ -950,23 +982,16 @@ extern "C" int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_
   SSLA_CHECK_ARG(E_out < 0x7fffffff, "rf_scatter_fill_sorted: E_out must stay below 2^31");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t HW = static_cast<int64_t>(H) * W;
-  hipLaunchKernelGGL(fill_i32, dim3(grid_for(HW * A)), dim3(kThreads), 0, st, inv, HW * A, -1);
+  const int64_t n_dst = dst_map ? E_in * A : 0;
+  const int64_t n_act = std::max<int64_t>(n_active, 0);
+  hipLaunchKernelGGL(rf_sorted_setup, dim3(grid_for(std::max(std::max(HW * A, n_dst), n_act))), dim3(kThreads), 0, st,
+                     inv, HW * A, dst_map, n_dst, f_index, L.f_index, f_len, L.f_len, n_act);
   hipLaunchKernelGGL(rf_inv_lut, dim3(grid_for(n_rf * A)), dim3(kThreads), 0, st, lut, n_rf, A, HW, inv);
   if (E_in > 0) {
-    if (dst_map)
-      hipLaunchKernelGGL(fill_i32, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, dst_map, E_in * A, -1);
     if (E_out > 0)
       hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.val, gr_batch, gr_h, gr_w,
                          L.gstart, gr_len, L.pixmap, inv, lut, n_rf, A, H, W, L.ev_pre, time, E_in, E_out, out_src,
                          out_time, out_pos, dst_map);
-  }
-  if (n_active > 0) {
-    hipError_t e = hipMemcpyAsync(f_index, L.f_index, sizeof(int64_t) * n_active, hipMemcpyDeviceToDevice, st);
-    if (e == hipSuccess) e = hipMemcpyAsync(f_len, L.f_len, sizeof(int64_t) * n_active, hipMemcpyDeviceToDevice, st);
-    if (e != hipSuccess) {
-      set_error("rf_scatter_fill_sorted: %s", hipGetErrorString(e));
-      return SSLA_ERR_LAUNCH;
-    }
   }
   return launch_status("rf_scatter_fill_sorted");
 }
