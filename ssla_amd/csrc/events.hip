@@ -85,8 +85,49 @@ int sort_pairs(void *tmp, size_t tmp_bytes, const uint64_t *kin, uint64_t *kout,
   return SSLA_OK;
 }
 
+// Exclusive prefix sum of up to kSmallScan values in one workgroup (one
+// launch; rocPRIM's scan takes two).  Thread t owns values 8t .. 8t+7; the
+// thread totals are scanned across each wavefront with shuffles and across
+// the 16 wavefronts through LDS.  Every value is read before any is
+// written, so in == out is allowed.
+constexpr int kScanThreads = 1024, kScanPer = 8;
+constexpr int64_t kSmallScan = static_cast<int64_t>(kScanThreads) * kScanPer;
+
+__global__ __launch_bounds__(kScanThreads) void small_excl_scan(const int64_t *in, int64_t *out, int64_t n) {
+  __shared__ int64_t wsum[kScanThreads / 64];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int64_t v[kScanPer];
+  int64_t s = 0;
+#pragma unroll
+  for (int e = 0; e < kScanPer; ++e) {
+    const int64_t i = static_cast<int64_t>(t) * kScanPer + e;
+    v[e] = i < n ? in[i] : 0;
+    s += v[e];
+  }
+  int64_t x = s;   // inclusive scan of the thread totals across the wavefront
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  int64_t run = x - s;
+  for (int j = 0; j < w; ++j) run += wsum[j];
+#pragma unroll
+  for (int e = 0; e < kScanPer; ++e) {
+    const int64_t i = static_cast<int64_t>(t) * kScanPer + e;
+    if (i < n) out[i] = run;
+    run += v[e];
+  }
+}
+
 int excl_scan(void *tmp, size_t tmp_bytes, const int64_t *in, int64_t *out, int64_t n, hipStream_t st) {
   if (n == 0) return SSLA_OK;
+  if (n <= kSmallScan) {
+    hipLaunchKernelGGL(small_excl_scan, dim3(1), dim3(kScanThreads), 0, st, in, out, n);
+    return SSLA_OK;
+  }
   size_t tb = tmp_bytes;
   const hipError_t e = rocprim::exclusive_scan(tmp, tb, in, out, static_cast<int64_t>(0), static_cast<size_t>(n),
                                                rocprim::plus<int64_t>(), st);

@@ -207,3 +207,21 @@ def test_unsorted_runs_take_the_sort_path(dev):
     rres = OE.scatter_group_events_to_patch(ro, (H, W), _np(lut))
     for key in ("events", "pos_id", "lengths", "orig_event_idx"):
         np.testing.assert_array_equal(_np(res[key]), rres[key], err_msg=key)
+
+
+@pytest.mark.parametrize("n", [1, 1000, 8191, 8192, 8193, 30000])
+def test_prefix_sums_across_the_one_workgroup_limit(dev, n):
+    """Prefix sums of up to 8192 values run in one workgroup, longer ones
+    through rocPRIM: expand_segments (an exclusive scan of the lengths) and
+    temporal_dropout_index (two scans) on both sides of the limit, against
+    numpy's repeat and the CPU oracle."""
+    from ssla_amd import events as E
+    rng = np.random.default_rng(n)
+    ln = rng.integers(0, 4, size=n)
+    vals = rng.integers(-5, 5, size=n)
+    got = E.expand_segments(torch.from_numpy(vals).to(dev), torch.from_numpy(ln).to(dev)).cpu().numpy()
+    assert np.array_equal(got, np.repeat(vals, ln))
+    idx, kl = E.temporal_dropout_index(torch.from_numpy(ln).to(dev), 3)
+    want_idx, want_kl = OE.temporal_dropout_index(ln, 3)
+    assert np.array_equal(kl.cpu().numpy(), want_kl)
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
