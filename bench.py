@@ -125,7 +125,7 @@ def bench_sparse(torch, lib, reps, dev):
             st = lib.ssla_sparse_gla_step(x["s"].data_ptr(), x["s"].numel(), x["q"].data_ptr(),
                                           x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
                                           state.data_ptr(), sb.n_sites, 4, 32, 32, float(sb.scale),
-                                          x["o"].data_ptr(), sh)
+                                          x["o"].data_ptr(), None, sh)
             _lib.check(st, "ssla_sparse_gla_step")
 
     one_pass()
@@ -200,7 +200,7 @@ def bench_sparse_batched(torch, lib, reps, dev):
         st = lib.ssla_gla_recurrent_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), _lib.SSLA_F32,
                                         cu.data_ptr(), int(uniq.size), T, H, K, V, float(sb.scale), state.data_ptr(),
                                         o.data_ptr(), state.data_ptr(), sidx.data_ptr(), int(state.shape[0]),
-                                        _lib.SSLA_F32, sh)
+                                        None, _lib.SSLA_F32, sh)
         _lib.check(st, "ssla_gla_recurrent_fwd")
 
     call()

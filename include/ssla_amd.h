@@ -49,6 +49,13 @@ int ssla_version(void);
 /* Message of the last failing call on this host thread ("" if none). */
 const char *ssla_last_error(void);
 
+/* Status words.  Entry points that validate data only the device sees
+ * (index lists) take an optional `int32_t *status` in device memory: the
+ * kernels store SSLA_ERR_ARG there when they find a bad entry and never
+ * write it otherwise, so the caller sets it to SSLA_OK before the call.
+ * ssla_status_read copies it to *value_out, synchronising `stream`. */
+int ssla_status_read(const int32_t *status, int *value_out, void *stream);
+
 /* ------------------------------------------------------------------------
  * G1 -- gated linear attention (GLA) forward, varlen, vector (per-key) gates.
  *
@@ -114,9 +121,12 @@ int ssla_gla_chunk_bwd(const void *q, const void *k, const void *v,
  * initial and final state to row state_idx[n] of h0 / ht, which may then be
  * the SAME buffer (in-place per-site state update; rows not named by
  * state_idx are never read or written).  n_state_rows is the row count of
- * h0/ht when state_idx is given (a sequence whose state_idx is outside
- * [0, n_state_rows) is skipped).  This is the batched form of the per-site
- * sparse GLA step over many time bins.
+ * h0/ht when state_idx is given.  state_idx must be strictly increasing and
+ * inside [0, n_state_rows) (so no two sequences share a state row): a
+ * sequence whose entry is not is skipped -- its o rows are written as zeros,
+ * no state is touched -- and SSLA_ERR_ARG is stored in *status (device
+ * int32, may be NULL; see ssla_status_read).  This is the batched form of
+ * the per-site sparse GLA step over many time bins.
  * Sequences are clamped to [0, T) on the device, so a malformed cu_seqlens
  * cannot address memory outside the tensors. */
 int ssla_gla_recurrent_fwd(const void *q, const void *k, const void *v,
@@ -125,7 +135,7 @@ int ssla_gla_recurrent_fwd(const void *q, const void *k, const void *v,
                            int H, int K, int V, float scale,
                            const float *h0, void *o, float *ht,
                            const int32_t *state_idx, int n_state_rows,
-                           int dtype, void *stream);
+                           int32_t *status, int dtype, void *stream);
 
 /* ------------------------------------------------------------------------
  * G2 -- sparse sequential scans.
@@ -152,18 +162,23 @@ int ssla_diag_scan_bwd(const float *dout, const float *g, const float *h,
                        int C, float *du, float *dg, void *stream);
 
 /* One time bin of the per-site matrix-state GLA update.  For active site
- * i (site = site_idx[i], sorted ascending, unique, < n_sites):
+ * i (site = site_idx[i], strictly increasing, inside [0, n_sites)):
  *   S[site] <- diag(exp(g_i)) S[site] + k_i v_i^T ;  o_i = (scale q_i)^T S[site]
  * q, k, g: fp32 [n_active, H, K]; v, o: fp32 [n_active, H, V];
  * state: fp32 [n_sites, H, K, V], updated in place; rows of inactive sites
  * are neither read nor written.  No reference function exists for this
  * step; it is naive_gla_recurrent (ops/gla/naive.py:50-111) applied to a
  * length-1 sequence per active site with initial_state = S[site].
+ * An entry that is out of range or not above the entry before it (a
+ * duplicate, an unsorted list) is skipped: its o rows are written as zeros,
+ * no state is touched, and SSLA_ERR_ARG is stored in *status (device int32,
+ * may be NULL; see ssla_status_read).
  * Supported: K, V in {16, 32, 64}. */
 int ssla_sparse_gla_step(const int32_t *site_idx, int n_active,
                          const float *q, const float *k, const float *v,
                          const float *g, float *state, int n_sites, int H,
-                         int K, int V, float scale, float *o, void *stream);
+                         int K, int V, float scale, float *o, int32_t *status,
+                         void *stream);
 
 /* ------------------------------------------------------------------------
  * G3 -- scatter-reduce pooling (torch_scatter.scatter_max / scatter_mean

@@ -38,11 +38,12 @@ SIGNATURES = {
     "ssla_gla_chunk_bwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32, _f32, _vp,
                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
     "ssla_gla_recurrent_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32,
-                                      _f32, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
+                                      _f32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
     "ssla_diag_scan_fwd": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _vp, _vp]),
     "ssla_diag_scan_bwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _vp, _vp, _vp]),
     "ssla_sparse_gla_step": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
-                                    _f32, _vp, _vp]),
+                                    _f32, _vp, _vp, _vp]),
+    "ssla_status_read": (_i32, [_vp, C.POINTER(_i32), _vp]),
     "ssla_scatter_workspace_size": (_sz, [_i64, _i32, _i64]),
     "ssla_scatter_max": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
     "ssla_scatter_mean": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _sz, _vp]),
@@ -120,6 +121,18 @@ def check(status: int, what: str) -> None:
     if status == SSLA_ERR_UNSUPPORTED:
         raise NotImplementedError(msg)
     raise SslaError(f"{msg} (status {status})")
+
+
+def new_status(device) -> torch.Tensor:
+    """A device status word set to SSLA_OK (see ssla_status_read)."""
+    return torch.zeros(1, dtype=torch.int32, device=device)
+
+
+def read_status(status: torch.Tensor) -> int:
+    """Value of a device status word (synchronises its stream)."""
+    v = C.c_int(0)
+    check(load().ssla_status_read(status.data_ptr(), C.byref(v), stream_of(status)), "ssla_status_read")
+    return v.value
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

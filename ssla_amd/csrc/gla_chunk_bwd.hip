@@ -818,6 +818,14 @@ int launch_bwd(const void *q, const void *k, const void *v, const void *g, const
   return launch_status("gla_chunk_bwd");
 }
 
+// With no rows at all (T == 0) every sequence is empty: its initial-state
+// gradient is the final-state gradient (ht == h0), or zero without one.
+__global__ __launch_bounds__(256) void bwd_empty_dh0_kernel(const float *__restrict__ dht, float *__restrict__ dh0,
+                                                            int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) dh0[i] = dht ? dht[i] : 0.f;
+}
+
 }  // namespace
 }  // namespace ssla
 
@@ -847,7 +855,14 @@ extern "C" int ssla_gla_chunk_bwd(const void *q, const void *k, const void *v, c
     set_error("gla_chunk_bwd: needs K == 64 and V a multiple of 16 up to 64 (K=%d V=%d)", K, V);
     return SSLA_ERR_UNSUPPORTED;
   }
-  if (n_seq == 0 || T == 0) return SSLA_OK;
+  if (n_seq == 0) return SSLA_OK;
+  if (T == 0) {
+    if (!dh0) return SSLA_OK;
+    const int64_t n = static_cast<int64_t>(n_seq) * H * K * V;
+    hipLaunchKernelGGL(bwd_empty_dh0_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), dht, dh0, n);
+    return launch_status("gla_chunk_bwd");
+  }
   SSLA_CHECK_ARG(q && k && v && g && cu_seqlens && dout && dq && dk && dv && dg, "gla_chunk_bwd: null pointer");
   const size_t need = ssla_gla_chunk_bwd_workspace_size(n_seq, T, H, K, V);
   if (workspace == nullptr || workspace_bytes < need) {

@@ -14,6 +14,22 @@ namespace {
 constexpr int kBV = 16;   // value columns per wavefront
 constexpr int kKG = 4;    // key groups per wavefront (64 / kBV)
 
+// A sequence whose state row is outside [0, n_rows) or not above the row of
+// the sequence before it (state_idx must be strictly increasing, so no two
+// sequences share a state row) is skipped: its o rows are written as zeros,
+// no state is read or written, and the status word is set to SSLA_ERR_ARG.
+__device__ __forceinline__ bool bad_state_row(const int32_t *state_idx, int n, int64_t srow, int n_rows) {
+  return state_idx && (srow < 0 || srow >= n_rows || (n > 0 && static_cast<int64_t>(state_idx[n - 1]) >= srow));
+}
+
+template <int DT>
+__device__ __forceinline__ void skip_sequence(void *o, int64_t bos, int64_t eos, int H, int h, int V, int col,
+                                              bool writer, int lane, int32_t *status) {
+  if (writer)
+    for (int64_t t = bos; t < eos; ++t) Elem<DT>::store(o, (t * H + h) * V + col, 0.f);
+  if (status && lane == 0) __hip_atomic_store(status, SSLA_ERR_ARG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // KPL consecutive elements of a row from index i into fp32: 16-byte loads
 // for fp32, 8-byte loads for 16-bit types (i a multiple of KPL >= 4, base
 // 16-byte aligned: checked by the host before this path is chosen).
@@ -54,7 +70,7 @@ __global__ __launch_bounds__(256) void gla_recurrent_vec_kernel(
     const int64_t *__restrict__ cu_seqlens, int n_seq, int H, int K, int V,
     float scale, const float *__restrict__ h0, void *__restrict__ o,
     float *__restrict__ ht, const int32_t *__restrict__ state_idx, int n_state_rows,
-    int64_t T) {
+    int64_t T, int32_t *__restrict__ status) {
   const int lane = threadIdx.x & 63;
   const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int n_vt = (V + kBV - 1) / kBV;
@@ -68,7 +84,10 @@ __global__ __launch_bounds__(256) void gla_recurrent_vec_kernel(
   const int64_t bos = min(max(cu_seqlens[n], (int64_t)0), T);
   const int64_t eos = min(max(cu_seqlens[n + 1], bos), T);
   const int64_t srow = state_idx ? static_cast<int64_t>(state_idx[n]) : n;
-  if (state_idx && (srow < 0 || srow >= n_state_rows)) return;
+  if (bad_state_row(state_idx, n, srow, n_state_rows)) {
+    skip_sequence<DT>(o, bos, eos, H, h, V, col, (lane >> 4) == 0 && col_ok, lane, status);
+    return;
+  }
 
   float S[KPL];
 #pragma unroll
@@ -117,7 +136,7 @@ __global__ __launch_bounds__(256) void gla_recurrent_kernel(
     const int64_t *__restrict__ cu_seqlens, int n_seq, int H, int K, int V,
     float scale, const float *__restrict__ h0, void *__restrict__ o,
     float *__restrict__ ht, const int32_t *__restrict__ state_idx, int n_state_rows,
-    int64_t T) {
+    int64_t T, int32_t *__restrict__ status) {
   const int lane = threadIdx.x & 63;
   const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int n_vt = (V + kBV - 1) / kBV;
@@ -136,7 +155,10 @@ __global__ __launch_bounds__(256) void gla_recurrent_kernel(
   const int64_t bos = min(max(cu_seqlens[n], (int64_t)0), T);
   const int64_t eos = min(max(cu_seqlens[n + 1], bos), T);
   const int64_t srow = state_idx ? static_cast<int64_t>(state_idx[n]) : n;
-  if (state_idx && (srow < 0 || srow >= n_state_rows)) return;  // never touch foreign rows
+  if (bad_state_row(state_idx, n, srow, n_state_rows)) {   // never touch foreign rows
+    skip_sequence<DT>(o, bos, eos, H, h, V, col, kg == 0 && col_ok, lane, status);
+    return;
+  }
 
   float S[KPL];
 #pragma unroll
@@ -180,7 +202,7 @@ template <int DT, int GDT>
 int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
                      const int64_t *cu, int n_seq, int H, int K, int V, float scale,
                      const float *h0, void *o, float *ht, const int32_t *sidx,
-                     int n_rows, int64_t T, hipStream_t st) {
+                     int n_rows, int64_t T, int32_t *status, hipStream_t st) {
   const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   const int n_vt = (V + kBV - 1) / kBV;
   const int64_t items = static_cast<int64_t>(n_seq) * H * n_vt;
@@ -199,7 +221,7 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
   if (vec) {
 #define SSLA_RECV(KPL_)                                                                        \
   hipLaunchKernelGGL((gla_recurrent_vec_kernel<DT, GDT, KPL_>), grid, block, 0, st, q, k, v, g, \
-                     cu, n_seq, H, K, V, scale, h0, o, ht, sidx, n_rows, T)
+                     cu, n_seq, H, K, V, scale, h0, o, ht, sidx, n_rows, T, status)
     switch (K / kKG) {
       case 4: SSLA_RECV(4); return launch_status("gla_recurrent_fwd");
       case 8: SSLA_RECV(8); return launch_status("gla_recurrent_fwd");
@@ -210,7 +232,7 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
   }
 #define SSLA_REC(KPL_)                                                                     \
   hipLaunchKernelGGL((gla_recurrent_kernel<DT, GDT, KPL_>), grid, block, 0, st, q, k, v, g, \
-                     cu, n_seq, H, K, V, scale, h0, o, ht, sidx, n_rows, T)
+                     cu, n_seq, H, K, V, scale, h0, o, ht, sidx, n_rows, T, status)
   if (kpl_needed <= 4) SSLA_REC(4);
   else if (kpl_needed <= 8) SSLA_REC(8);
   else if (kpl_needed <= 16) SSLA_REC(16);
@@ -229,7 +251,7 @@ extern "C" int ssla_gla_recurrent_fwd(const void *q, const void *k, const void *
                                       int H, int K, int V, float scale,
                                       const float *h0, void *o, float *ht,
                                       const int32_t *state_idx, int n_state_rows,
-                                      int dtype, void *stream) {
+                                      int32_t *status, int dtype, void *stream) {
   using namespace ssla;
   clear_error();
   SSLA_CHECK_ARG(n_seq >= 0 && T >= 0 && H > 0 && K > 0 && V > 0,
@@ -247,19 +269,19 @@ extern "C" int ssla_gla_recurrent_fwd(const void *q, const void *k, const void *
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == SSLA_F32) {
     if (g_dtype != SSLA_F32) { set_error("gla_recurrent_fwd: fp32 inputs need fp32 g"); return SSLA_ERR_DTYPE; }
-    return launch_recurrent<SSLA_F32, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, st);
+    return launch_recurrent<SSLA_F32, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
   }
   if (dtype == SSLA_BF16) {
     if (g_dtype == SSLA_F32)
-      return launch_recurrent<SSLA_BF16, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, st);
+      return launch_recurrent<SSLA_BF16, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
     if (g_dtype == SSLA_BF16)
-      return launch_recurrent<SSLA_BF16, SSLA_BF16>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, st);
+      return launch_recurrent<SSLA_BF16, SSLA_BF16>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
   }
   if (dtype == SSLA_F16) {
     if (g_dtype == SSLA_F32)
-      return launch_recurrent<SSLA_F16, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, st);
+      return launch_recurrent<SSLA_F16, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
     if (g_dtype == SSLA_F16)
-      return launch_recurrent<SSLA_F16, SSLA_F16>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, st);
+      return launch_recurrent<SSLA_F16, SSLA_F16>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
   }
   set_error("gla_recurrent_fwd: unsupported dtype %d / g_dtype %d", dtype, g_dtype);
   return SSLA_ERR_DTYPE;

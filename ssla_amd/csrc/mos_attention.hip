@@ -545,7 +545,7 @@ extern "C" size_t ssla_mos_attention_workspace_size(int64_t n_events, int c_in, 
 extern "C" size_t ssla_mos_attention_lds_bytes(int c_in, int hidden, int A, int scatter_per_pos, int gather_per_pos) {
   using namespace ssla;
   const Tpl t = pick_tpl(c_in, hidden);
-  if (t.hp == 0 || A <= 0) return 0;
+  if (t.hp == 0 || A <= 0 || A > kMaxPos) return 0;   // 0: the fused kernels do not take this layer
   const int As = scatter_per_pos ? A : 1, Ag = gather_per_pos ? A : 1;
   const size_t kS = t.hp * t.cp + 4, kG = t.hp * t.hp + 4;
   const size_t fold = sizeof(float) * (3 * As * kS + Ag * kG);

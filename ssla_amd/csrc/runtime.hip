@@ -38,3 +38,17 @@ hipError_t read_to_host(void *dst, const void *src, size_t bytes, hipStream_t st
 extern "C" int ssla_version(void) { return 100; }
 
 extern "C" const char *ssla_last_error(void) { return ssla::g_last_error; }
+
+extern "C" int ssla_status_read(const int32_t *status, int *value_out, void *stream) {
+  using namespace ssla;
+  clear_error();
+  SSLA_CHECK_ARG(status && value_out, "status_read: null pointer");
+  int32_t v = 0;
+  const hipError_t e = read_to_host(&v, status, sizeof(v), static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) {
+    set_error("status_read: %s", hipGetErrorString(e));
+    return SSLA_ERR_LAUNCH;
+  }
+  *value_out = v;
+  return SSLA_OK;
+}

@@ -12,6 +12,13 @@
 // states of inactive sites stay bit-identical.  The kernel is a pure HBM
 // stream: 2*K*V*4 bytes of state plus (3K + 2V)*4 bytes of q/k/g/v/o per
 // (site, head).
+//
+// The site list must be strictly increasing and inside [0, n_sites): an
+// entry that is not (out of range, or not above the entry before it -- a
+// duplicate or an unsorted list) is skipped: its o rows are written as
+// zeros, no state is touched, and the status word (if given) is set to
+// SSLA_ERR_ARG.  A strictly increasing list also rules out two wavefronts
+// updating one state tile.
 #include "common.h"
 
 namespace ssla {
@@ -21,7 +28,8 @@ template <int K, int V>
 __global__ __launch_bounds__(256) void sparse_gla_step_kernel(
     const int32_t *__restrict__ site_idx, int n_active, const float *__restrict__ q,
     const float *__restrict__ k, const float *__restrict__ v, const float *__restrict__ g,
-    float *__restrict__ state, int n_sites, int H, float scale, float *__restrict__ o) {
+    float *__restrict__ state, int n_sites, int H, float scale, float *__restrict__ o,
+    int32_t *__restrict__ status) {
   constexpr int VL = V / 4;          // lanes per state row (float4 each)
   constexpr int RG = 64 / VL;        // row groups per wavefront
   constexpr int RPL = K / RG;        // rows per lane
@@ -32,10 +40,14 @@ __global__ __launch_bounds__(256) void sparse_gla_step_kernel(
   const int i = static_cast<int>(item / H);
   const int h = static_cast<int>(item % H);
   const int site = site_idx[i];
-  if (site < 0 || site >= n_sites) return;
   const int vc = lane % VL;          // float4 column
   const int rg = lane / VL;          // row group: rows rg*RPL .. rg*RPL+RPL-1
   const int64_t io = static_cast<int64_t>(i) * H + h;
+  if (site < 0 || site >= n_sites || (i > 0 && site_idx[i - 1] >= site)) {
+    if (rg == 0) reinterpret_cast<float4 *>(o + io * V)[vc] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (status && lane == 0) __hip_atomic_store(status, SSLA_ERR_ARG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   const float4 vv = reinterpret_cast<const float4 *>(v + io * V)[vc];
   float4 *S = reinterpret_cast<float4 *>(state + (static_cast<int64_t>(site) * H + h) * K * V);
 
@@ -79,7 +91,7 @@ __global__ __launch_bounds__(256) void sparse_gla_step_kernel(
 extern "C" int ssla_sparse_gla_step(const int32_t *site_idx, int n_active, const float *q,
                                     const float *k, const float *v, const float *g,
                                     float *state, int n_sites, int H, int K, int V, float scale,
-                                    float *o, void *stream) {
+                                    float *o, int32_t *status, void *stream) {
   using namespace ssla;
   clear_error();
   SSLA_CHECK_ARG(n_active >= 0 && n_sites >= 0 && H > 0,
@@ -97,7 +109,7 @@ extern "C" int ssla_sparse_gla_step(const int32_t *site_idx, int n_active, const
 #define SSLA_STEP(KK, VV)                                                                       \
   if (K == KK && V == VV) {                                                                     \
     hipLaunchKernelGGL((sparse_gla_step_kernel<KK, VV>), grid, block, 0, st, site_idx, n_active, \
-                       q, k, v, g, state, n_sites, H, scale, o);                                \
+                       q, k, v, g, state, n_sites, H, scale, o, status);                        \
     return launch_status("sparse_gla_step");                                                    \
   }
   SSLA_STEP(16, 16) SSLA_STEP(16, 32) SSLA_STEP(16, 64)

@@ -166,7 +166,7 @@ class ChunkGLAFunction(torch.autograd.Function):
         return dq, dk, dv, dg, None, dh0, None, None
 
 
-def _recurrent(q, k, v, g, cu, scale, h0, o, ht, state_idx, n_rows):
+def _recurrent(q, k, v, g, cu, scale, h0, o, ht, state_idx, n_rows, status=None):
     T, H, K = q.shape
     V = v.shape[-1]
     N = cu.numel() - 1
@@ -174,7 +174,7 @@ def _recurrent(q, k, v, g, cu, scale, h0, o, ht, state_idx, n_rows):
     st = lib.ssla_gla_recurrent_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.DTYPE_CODE[g.dtype],
         _lib.ptr(cu), N, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(o), _lib.ptr(ht),
-        _lib.ptr(state_idx), int(n_rows), _lib.DTYPE_CODE[q.dtype], _lib.stream_of(q))
+        _lib.ptr(state_idx), int(n_rows), _lib.ptr(status), _lib.DTYPE_CODE[q.dtype], _lib.stream_of(q))
     _lib.check(st, "ssla_gla_recurrent_fwd")
     return o, ht
 
@@ -192,7 +192,11 @@ def fused_recurrent_gla(
     """Recurrent GLA forward with the signature and semantics of
     ``naive_gla_recurrent`` (reference ops/gla/naive.py:50-111):
     ``S_t = exp(g_t) * S_{t-1} + k_t v_t^T``, ``o_t = (scale q_t) . S_t``;
-    o has q's dtype, the final state is fp32."""
+    o has q's dtype, the final state is fp32.  As the reference concatenates
+    the outputs of its sequences (naive.py:106), o holds the rows
+    ``cu_seqlens[0]:cu_seqlens[-1]`` (all T rows when the sequences cover
+    the batch, the usual case; reading the two bounds is one host sync
+    otherwise, as the reference's ``.item()`` calls are)."""
     if scale is None:
         scale = q.shape[-1] ** -0.5
     q, k, v, g, cu, h0 = _prep("fused_recurrent_gla", q, k, v, g, cu_seqlens, initial_state)
@@ -204,7 +208,11 @@ def fused_recurrent_gla(
                          f"got {tuple(h0.shape)}")
     o = torch.empty(T, H, V, device=q.device, dtype=q.dtype)
     ht = torch.empty(N, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
-    return _recurrent(q, k, v, g, cu, float(scale), h0, o, ht, None, 0)
+    o, ht = _recurrent(q, k, v, g, cu, float(scale), h0, o, ht, None, 0)
+    lo, hi = (int(x) for x in cu_seqlens[[0, -1]].tolist()) if N > 0 else (0, 0)
+    if (lo, hi) != (0, T):
+        o = o[lo:hi]
+    return o, ht
 
 
 naive_gla_recurrent = fused_recurrent_gla

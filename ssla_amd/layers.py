@@ -11,8 +11,11 @@ arguments, parameter / buffer names and dict interface (haohq19/ssla):
 
 The event glue, the diagonal scan and the pooling run the gfx950 kernels of
 libssla_amd.so; the dense projections are plain library GEMMs and the
-normalisation a library LayerNorm.  Forward only (the layers raise when a
-gradient is requested through the custom kernels).
+normalisation a library LayerNorm.  The layers train: the scan, the row
+gathers / ordered index-adds and the scatter reductions have backward
+passes, so autograd runs through the composed MosAttention forward,
+LinearAttention and the SparsePool family (the fused MosAttention forward is
+inference only and is skipped whenever a gradient is recorded).
 
 Deviations, all deliberate: every ordering is stable (the reference's
 unstable field sorts have implementation-defined tie order); SparsePool does
@@ -132,10 +135,13 @@ class MosAttention(nn.Module):
 
     def _fused_ok(self, events):
         """The fused forward (ssla_mos_attention_fwd) runs when no gradient is
-        recorded and the weights fit its kernels (input, hidden <= 32)."""
+        recorded and the weights fit its kernels (input, hidden <= 32, at most
+        49 kernel positions, weights within 64 KB of LDS)."""
         if torch.is_grad_enabled() and (events.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
         A = self.kernel_size[0] * self.kernel_size[1]
+        if A > 49:
+            return False
         lds = _lib.load().ssla_mos_attention_lds_bytes(self.input_size, self.hidden_size, A, int(self.scatter_proj),
                                                        int(self.gather_proj))
         return 0 < lds <= 64 * 1024

@@ -72,12 +72,16 @@ def scan(u: torch.Tensor, g: torch.Tensor, cu_seqlens: torch.Tensor) -> torch.Te
 
 
 def sparse_gla_step(site_idx: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                    g: torch.Tensor, state: torch.Tensor, scale: Optional[float] = None) -> torch.Tensor:
+                    g: torch.Tensor, state: torch.Tensor, scale: Optional[float] = None,
+                    check: bool = True) -> torch.Tensor:
     """Update ``state[site_idx]`` in place for one time bin and return o.
 
-    site_idx: int32 ``[n]`` (sorted, unique); q, k, g: fp32 ``[n, H, K]``;
-    v: fp32 ``[n, H, V]``; state: fp32 ``[n_sites, H, K, V]``.
-    Rows of inactive sites are neither read nor written.
+    site_idx: int32 ``[n]`` (strictly increasing, inside ``[0, n_sites)``);
+    q, k, g: fp32 ``[n, H, K]``; v: fp32 ``[n, H, V]``; state: fp32
+    ``[n_sites, H, K, V]``.  Rows of inactive sites are neither read nor
+    written.  An entry out of range or not above the one before it is
+    skipped (its o rows are zero, no state changes); with ``check`` (one host
+    sync) that raises ValueError after the call.
     """
     n, H, K = q.shape
     V = v.shape[-1]
@@ -97,20 +101,26 @@ def sparse_gla_step(site_idx: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v:
     q, k, v, g = (t.to(torch.float32).contiguous() for t in (q, k, v, g))
     o = torch.empty(n, H, V, device=q.device, dtype=torch.float32)
     lib = _lib.load()
+    status = _lib.new_status(q.device) if check and n else None
     st = lib.ssla_sparse_gla_step(_lib.ptr(sidx), n, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v),
                                   _lib.ptr(g), _lib.ptr(state), state.shape[0], H, K, V,
-                                  float(scale), _lib.ptr(o), _lib.stream_of(q))
+                                  float(scale), _lib.ptr(o), _lib.ptr(status), _lib.stream_of(q))
     _lib.check(st, "ssla_sparse_gla_step")
+    if status is not None and _lib.read_status(status) != _lib.SSLA_OK:
+        raise ValueError(f"sparse_gla_step: site_idx must be strictly increasing and inside [0, {state.shape[0]})")
     return o
 
 
 def sparse_gla_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
                     cu_seqlens: torch.Tensor, seq_site: torch.Tensor, state: torch.Tensor,
-                    scale: Optional[float] = None) -> torch.Tensor:
+                    scale: Optional[float] = None, check: bool = True) -> torch.Tensor:
     """Many bins at once: sequence n (rows ``cu_seqlens[n]:cu_seqlens[n+1]``,
     ordered in time) is the history of site ``seq_site[n]``; its state row
     is read from and written back to ``state`` in place.  Returns o with
-    q's dtype.  Sites must be unique across sequences."""
+    q's dtype.  ``seq_site`` must be strictly increasing and inside
+    ``[0, n_sites)``; a sequence whose entry is not is skipped (zero o rows,
+    state untouched) and, with ``check`` (one host sync), ValueError is
+    raised after the call."""
     T, H, K = q.shape
     V = v.shape[-1]
     if state.dim() != 4 or state.shape[1:] != (H, K, V) or state.dtype != torch.float32 \
@@ -127,5 +137,8 @@ def sparse_gla_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     g = g.to(torch.float32).contiguous() if g.dtype != q.dtype else g.contiguous()
     o = torch.empty(T, H, V, device=q.device, dtype=q.dtype)
-    _recurrent(q, k, v, g, cu, float(scale), state, o, state, sidx, state.shape[0])
+    status = _lib.new_status(dev) if check and sidx.numel() else None
+    _recurrent(q, k, v, g, cu, float(scale), state, o, state, sidx, state.shape[0], status)
+    if status is not None and _lib.read_status(status) != _lib.SSLA_OK:
+        raise ValueError(f"sparse_gla_scan: seq_site must be strictly increasing and inside [0, {state.shape[0]})")
     return o

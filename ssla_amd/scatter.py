@@ -11,6 +11,12 @@ Semantics (torch_scatter's documented behaviour): empty output rows are 0
 (argmax = E); ``argmax`` picks the smallest event index among equal maxima
 (deterministic, unlike atomic implementations); mean divides the sum by
 ``max(count, 1)``.
+
+Both are differentiable in ``src`` as torch_scatter's are: the gradient of
+``scatter_max`` goes to the winning event of every (row, channel) (none for
+empty rows), that of ``scatter_mean`` is the row's gradient over its count.
+``out=`` is not supported (torch_scatter reduces into the existing contents
+of ``out``; the reference never passes it): it raises NotImplementedError.
 """
 from __future__ import annotations
 
@@ -44,7 +50,6 @@ def _prep(name, src, index, dim, dim_size):
     elif index.dim() != 1 or index.shape[0] != E:
         raise ValueError(f"{name}: index must be [E] or [E, C], got {tuple(index.shape)}")
     _lib.require_cuda(src, index)
-    _lib.require_no_grad(name, src)
     if src.dtype != torch.float32:
         raise TypeError(f"{name}: src must be fp32, got {src.dtype}")
     index = index.to(torch.int64).contiguous()
@@ -73,6 +78,50 @@ def _run(name, fn, src, index, n_out, sorted_index, out, argmax, check):
                              + (" or not sorted" if sorted_index else ""))
 
 
+def _no_out(name, out):
+    if out is not None:
+        raise NotImplementedError(
+            f"{name}: out= is not supported (torch_scatter would reduce into the existing contents of out); "
+            "pass out=None and copy the result")
+
+
+class _ScatterMax(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, src, idx, n_out, sorted_index, check):
+        E, Cc = src.shape
+        res = torch.empty(n_out, Cc, device=src.device, dtype=torch.float32)
+        arg = torch.empty(n_out, Cc, device=src.device, dtype=torch.int64)
+        _run("scatter_max", _lib.load().ssla_scatter_max, src, idx, n_out, sorted_index, res, arg, check)
+        ctx.save_for_backward(arg)
+        ctx.n_src = E
+        ctx.mark_non_differentiable(arg)
+        return res, arg
+
+    @staticmethod
+    def backward(ctx, d_out, _d_arg):
+        (arg,) = ctx.saved_tensors
+        grad = torch.zeros(ctx.n_src + 1, arg.shape[1], device=arg.device, dtype=d_out.dtype)
+        grad.scatter_(0, arg, d_out.contiguous())   # argmax = E (empty row) lands in the dropped extra row
+        return grad[:ctx.n_src], None, None, None, None
+
+
+class _ScatterMean(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, src, idx, n_out, sorted_index, check):
+        Cc = src.shape[1]
+        res = torch.empty(n_out, Cc, device=src.device, dtype=torch.float32)
+        _run("scatter_mean", _lib.load().ssla_scatter_mean, src, idx, n_out, sorted_index, res, None, check)
+        ctx.save_for_backward(idx)
+        ctx.n_out = n_out
+        return res
+
+    @staticmethod
+    def backward(ctx, d_out):
+        (idx,) = ctx.saved_tensors
+        cnt = torch.bincount(idx, minlength=ctx.n_out).clamp_(min=1).to(d_out.dtype)
+        return (d_out / cnt[:, None]).index_select(0, idx), None, None, None, None
+
+
 def scatter_max(src: torch.Tensor, index: torch.Tensor, dim: int = -1,
                 out: Optional[torch.Tensor] = None, dim_size: Optional[int] = None,
                 sorted_index: bool = False, check: bool = True
@@ -80,15 +129,11 @@ def scatter_max(src: torch.Tensor, index: torch.Tensor, dim: int = -1,
     """Row-wise maximum and first-index argmax.  ``sorted_index=True``
     promises a non-decreasing index (e.g. a ``unique_consecutive`` inverse);
     ``check`` reports out-of-range (or unsorted) indices as ValueError."""
-    src_c, idx, n_out, Cc, squeeze = _prep("scatter_max", src, index, dim, dim_size)
-    res = torch.empty(n_out, Cc, device=src.device, dtype=torch.float32)
-    arg = torch.empty(n_out, Cc, device=src.device, dtype=torch.int64)
-    _run("scatter_max", _lib.load().ssla_scatter_max, src_c, idx, n_out, sorted_index, res, arg, check)
+    _no_out("scatter_max", out)
+    src_c, idx, n_out, _Cc, squeeze = _prep("scatter_max", src, index, dim, dim_size)
+    res, arg = _ScatterMax.apply(src_c, idx, n_out, sorted_index, check)
     if squeeze:
         res, arg = res[:, 0], arg[:, 0]
-    if out is not None:
-        out.copy_(res)
-        res = out
     return res, arg
 
 
@@ -96,12 +141,9 @@ def scatter_mean(src: torch.Tensor, index: torch.Tensor, dim: int = -1,
                  out: Optional[torch.Tensor] = None, dim_size: Optional[int] = None,
                  sorted_index: bool = False, check: bool = True) -> torch.Tensor:
     """Row-wise mean (sum / max(count, 1))."""
-    src_c, idx, n_out, Cc, squeeze = _prep("scatter_mean", src, index, dim, dim_size)
-    res = torch.empty(n_out, Cc, device=src.device, dtype=torch.float32)
-    _run("scatter_mean", _lib.load().ssla_scatter_mean, src_c, idx, n_out, sorted_index, res, None, check)
+    _no_out("scatter_mean", out)
+    src_c, idx, n_out, _Cc, squeeze = _prep("scatter_mean", src, index, dim, dim_size)
+    res = _ScatterMean.apply(src_c, idx, n_out, sorted_index, check)
     if squeeze:
         res = res[:, 0]
-    if out is not None:
-        out.copy_(res)
-        res = out
     return res

@@ -45,10 +45,10 @@ def test_argument_errors_without_device_work():
     assert st == _lib.SSLA_ERR_UNSUPPORTED
     # K > 256 on the recurrent kernel
     st = lib.ssla_gla_recurrent_fwd(None, None, None, None, 0, None, 1, 0, 1, 300, 64, 1.0, None, None,
-                                    None, None, 0, _lib.SSLA_F32, None)
+                                    None, None, 0, None, _lib.SSLA_F32, None)
     assert st == _lib.SSLA_ERR_UNSUPPORTED
     # unsupported sparse-step shape
-    st = lib.ssla_sparse_gla_step(None, 1, None, None, None, None, None, 1, 1, 48, 48, 1.0, None, None)
+    st = lib.ssla_sparse_gla_step(None, 1, None, None, None, None, None, 1, 1, 48, 48, 1.0, None, None, None)
     assert st == _lib.SSLA_ERR_ARG  # null pointers are rejected first
     # scatter: non-positive C, n_out beyond 2^30, and a missing workspace
     st = lib.ssla_scatter_max(None, None, 10, 0, 4, 0, None, None, None, 0, None)
@@ -93,3 +93,21 @@ def test_python_wrappers_reject_cpu_tensors():
         chunk_gla(x, x, x, x, torch.tensor([0, 4]))
     with pytest.raises(ValueError, match="device tensors"):
         scan(torch.zeros(4, 3), torch.zeros(4, 3), torch.tensor([0, 4]))
+
+
+def test_fused_mos_attention_limits():
+    """The fused MosAttention kernels take at most 49 kernel positions: the
+    LDS query reports 0 (not applicable) beyond that even when the weights
+    would fit, so the layer picks the composed forward."""
+    from ssla_amd import _lib
+    lib = _lib.load()
+    assert 0 < lib.ssla_mos_attention_lds_bytes(2, 12, 49, 1, 1) <= 64 * 1024
+    assert lib.ssla_mos_attention_lds_bytes(2, 12, 64, 1, 1) == 0
+    assert lib.ssla_mos_attention_lds_bytes(48, 48, 9, 1, 1) == 0
+
+
+def test_status_read_rejects_null():
+    from ssla_amd import _lib
+    import ctypes
+    v = ctypes.c_int(0)
+    assert _lib.load().ssla_status_read(None, ctypes.byref(v), None) == _lib.SSLA_ERR_ARG

@@ -167,3 +167,19 @@ def test_chunk_errors(dev):
     v128 = torch.randn(30, 2, 128, dtype=torch.bfloat16, device=dev)
     with pytest.raises(NotImplementedError):   # V > 64 has none
         chunk_gla(qg, k.to(dev), v128, g.to(dev), cu.to(dev))
+
+
+def test_recurrent_returns_sequence_rows(dev):
+    """naive_gla_recurrent concatenates the outputs of its sequences
+    (reference ops/gla/naive.py:104-106): with cu_seqlens = [2, 5, 9] over 12
+    rows, o is the 7 rows 2..8, each equal to the oracle's row."""
+    from ssla_amd.gla import naive_gla_recurrent
+    q, k, v, g, _, s0 = _inputs([12], 2, 32, 32, torch.float32, seed=77, h0=False)
+    cu = torch.tensor([2, 5, 9], dtype=torch.int64)
+    s0 = torch.randn(2, 2, 32, 32, generator=torch.Generator().manual_seed(78)) * 0.1
+    print("recurrent: sequence rows only", flush=True)
+    o, ht = _run(naive_gla_recurrent, q, k, v, g, cu, s0, 32 ** -0.5, dev)
+    assert o.shape == (7, 2, 32)
+    ro, rht = _oracle(q, k, v, g, cu, s0, 32 ** -0.5)
+    assert_close(o, ro[2:9], RTOL_F32, "o rows")
+    assert_close(ht, rht, RTOL_F32, "ht")

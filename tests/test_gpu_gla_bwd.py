@@ -105,3 +105,25 @@ def test_chunk_bwd_16bit_gates(dev, dtype):
                                    cu.numpy(), do.float().numpy(), 64 ** -0.5, s0.numpy(), dht.numpy())
     for name, a, b in zip(("dq", "dk", "dv", "dg", "dh0"), got, ref):
         assert_close(a, b, RTOL, f"{name}[16-bit g {dtype}]", ratio_mode=True)
+
+
+def test_chunk_bwd_all_sequences_empty(dev):
+    """T == 0 with sequences present: ht equals h0, so the initial-state
+    gradient is exactly the final-state gradient (zero without one)."""
+    from ssla_amd.gla import chunk_gla
+    H, N = 2, 3
+    gen = torch.Generator().manual_seed(21)
+    z = [torch.zeros(0, H, 64, device=dev, dtype=torch.bfloat16).requires_grad_() for _ in range(3)]
+    g = torch.zeros(0, H, 64, device=dev).requires_grad_()
+    cu = torch.zeros(N + 1, dtype=torch.int64, device=dev)
+    dht = (torch.randn(N, H, 64, 64, generator=gen) * 0.1).to(dev)
+    print("gla bwd: every sequence empty", flush=True)
+    h0 = (torch.randn(N, H, 64, 64, generator=gen) * 0.1).to(dev).requires_grad_()
+    o, ht = chunk_gla(z[0], z[1], z[2], g, cu, initial_state=h0, output_final_state=True)
+    assert o.shape == (0, H, 64) and torch.equal(ht, h0.detach())
+    (ht * dht).sum().backward()
+    assert torch.equal(h0.grad, dht)
+    h0b = h0.detach().clone().requires_grad_()
+    o, _ = chunk_gla(z[0], z[1], z[2], g, cu, initial_state=h0b, output_final_state=False)
+    torch.autograd.backward([o], [torch.zeros_like(o)])
+    assert h0b.grad is not None and not h0b.grad.any()

@@ -84,10 +84,11 @@ def test_fused_single_event_and_disabled_projections():
         assert_close(a, b, TOL, f"single event sp={sp} gp={gp}")
 
 
-@pytest.mark.parametrize("cin,hid,k", [(48, 48, 3), (16, 32, 3)])
+@pytest.mark.parametrize("cin,hid,k", [(48, 48, 3), (16, 32, 3), (2, 12, 8)])
 def test_fused_unsupported_sizes(cin, hid, k):
-    """Hidden > 32, or weights beyond 64 KB of LDS (hidden 32 with 9
-    positions): fused=True raises, the default runs the composed path."""
+    """Hidden > 32, weights beyond 64 KB of LDS (hidden 32 with 9
+    positions), or more than 49 kernel positions (8 x 8, whose small weights
+    would fit LDS): fused=True raises, the default runs the composed path."""
     from ssla_amd import _lib
     from ssla_amd.layers import MosAttention
     gr = _grouped(B=1, n_mean=2000, C=cin)

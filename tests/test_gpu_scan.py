@@ -152,7 +152,7 @@ def test_sparse_step_graph_replay(dev):
             _lib.check(lib.ssla_sparse_gla_step(x["s"].data_ptr(), x["s"].numel(), x["q"].data_ptr(),
                                                 x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
                                                 state.data_ptr(), sb.n_sites, 4, 32, 32, float(sb.scale),
-                                                x["o"].data_ptr(), sh), "sparse_gla_step")
+                                                x["o"].data_ptr(), None, sh), "sparse_gla_step")
 
     one_pass(torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
@@ -177,3 +177,72 @@ def test_sparse_step_graph_replay(dev):
         assert torch.equal(state, st_e), f"state differs on replay {rep}"
         for b, x in enumerate(bins):
             assert torch.equal(x["o"], o_e[b]), f"o of bin {b} differs on replay {rep}"
+
+
+def test_sparse_step_rejects_bad_site_lists(dev):
+    """An out-of-range site and a duplicate are reported (ValueError from
+    the wrapper, SSLA_ERR_ARG in the status word through the C-ABI); their o
+    rows are zero, no state they name changes, and the valid entries are
+    updated as usual."""
+    from ssla_amd import _lib
+    from ssla_amd.scan import sparse_gla_step
+    gen = torch.Generator().manual_seed(31)
+    n_sites, H, K, V = 50, 2, 32, 32
+    state0 = torch.randn(n_sites, H, K, V, generator=gen) * 0.1
+    sites = np.array([3, 7, 7, 12, 60], dtype=np.int32)   # duplicate 7, out-of-range 60
+    n = sites.size
+    q, k, v = (torch.randn(n, H, D, generator=gen) for D in (K, K, V))
+    g = F.logsigmoid(torch.randn(n, H, K, generator=gen))
+    st = state0.clone().to(dev)
+    print("sparse step: bad site list through the wrapper", flush=True)
+    with torch.no_grad(), pytest.raises(ValueError, match="strictly increasing"):
+        sparse_gla_step(torch.from_numpy(sites).to(dev), q.to(dev), k.to(dev), v.to(dev), g.to(dev), st)
+    # the same call through the C-ABI: status word, zero rows, state effects
+    lib = _lib.load()
+    st = state0.clone().to(dev)
+    o = torch.full((n, H, V), float("nan"), device=dev)
+    status = _lib.new_status(dev)
+    qd, kd, vd, gd = (t.to(dev).contiguous() for t in (q, k, v, g))
+    sd = torch.from_numpy(sites).to(dev)
+    _lib.check(lib.ssla_sparse_gla_step(sd.data_ptr(), n, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                        gd.data_ptr(), st.data_ptr(), n_sites, H, K, V, K ** -0.5,
+                                        o.data_ptr(), status.data_ptr(), _lib.stream_of(qd)), "step")
+    assert _lib.read_status(status) == _lib.SSLA_ERR_ARG
+    o = o.cpu()
+    assert torch.equal(o[2], torch.zeros(H, V)) and torch.equal(o[4], torch.zeros(H, V))
+    ref_state = state0.numpy().copy()
+    good = [0, 1, 3]
+    ro = oracle.sparse_gla_step(sites[good], q.numpy()[good], k.numpy()[good], v.numpy()[good],
+                                g.numpy()[good], ref_state, K ** -0.5)
+    assert_close(o.numpy()[good], ro, 1e-4, "o of the valid entries")
+    assert_close(st.cpu().numpy(), ref_state, 1e-4, "states (site 7 updated once)")
+
+
+def test_sparse_scan_rejects_bad_site_lists(dev):
+    """sparse_gla_scan (ssla_gla_recurrent_fwd with state_idx): a repeated
+    site is reported and its sequence skipped (zero o rows)."""
+    from ssla_amd import _lib
+    from ssla_amd.gla import _recurrent
+    from ssla_amd.scan import sparse_gla_scan
+    gen = torch.Generator().manual_seed(32)
+    H, K, V, n_sites = 2, 32, 32, 20
+    lens = [3, 2, 4]
+    T = sum(lens)
+    q, k, v = (torch.randn(T, H, D, generator=gen).to(dev) for D in (K, K, V))
+    g = F.logsigmoid(torch.randn(T, H, K, generator=gen)).to(dev)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=dev)
+    state0 = (torch.randn(n_sites, H, K, V, generator=gen) * 0.1).to(dev)
+    print("sparse scan: repeated site", flush=True)
+    with torch.no_grad(), pytest.raises(ValueError, match="strictly increasing"):
+        sparse_gla_scan(q, k, v, g, cu, torch.tensor([4, 9, 9], device=dev), state0.clone())
+    st = state0.clone()
+    o = torch.full((T, H, V), float("nan"), device=dev)
+    status = _lib.new_status(dev)
+    with torch.no_grad():
+        _recurrent(q, k, v, g, cu, K ** -0.5, st, o, st, torch.tensor([4, 9, 9], device=dev, dtype=torch.int32),
+                   n_sites, status)
+    assert _lib.read_status(status) == _lib.SSLA_ERR_ARG
+    assert torch.equal(o[5:].cpu(), torch.zeros(4, H, V))
+    assert torch.isfinite(o[:5]).all()
+    untouched = [i for i in range(n_sites) if i not in (4, 9)]
+    assert torch.equal(st[untouched], state0[untouched])
