@@ -93,6 +93,24 @@ int ssla_gla_chunk_fwd(const void *q, const void *k, const void *v,
                        const float *h0, void *o, float *ht, int dtype,
                        void *workspace, size_t workspace_bytes, void *stream);
 
+/* Allocation-free variant of ssla_gla_chunk_fwd (same arguments without
+ * the workspace, same kernels, same results bit for bit).  It has no
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The workspace is a static device array
+ * of 64 MiB inside the library, one copy per GPU, held until the process
+ * ends; a shape whose ssla_gla_chunk_workspace_size exceeds it returns
+ * SSLA_ERR_WORKSPACE.  Every call on one GPU uses that GPU's array, so calls
+ * that overlap on one GPU (concurrent streams or host threads) race: run
+ * them in one stream order.  The first call on a device looks the array's
+ * address up (hipGetSymbolAddress); it allocates nothing. */
+int ssla_gla_chunk_fwd_noalloc(const void *q, const void *k, const void *v,
+                               const void *g, int g_dtype,
+                               const int64_t *cu_seqlens, int n_seq, int64_t T,
+                               int H, int K, int V, float scale,
+                               const float *h0, void *o, float *ht, int dtype,
+                               void *stream);
+
 /* Backward of ssla_gla_chunk_fwd: ChunkGLAFunction.backward /
  * chunk_gla_bwd (reference ops/gla/chunk.py:1096-1116, 963-1053, with
  * chunk_bwd_dh, ops/common/chunk_h.py:145-239).  dout [T, H, V] (dtype of

@@ -46,6 +46,17 @@
 // the end.
 #include "common.h"
 
+#include <atomic>
+#include <mutex>
+
+// Scratch of ssla_gla_chunk_fwd_noalloc: a fixed device array (one copy per
+// GPU, zero-filled when the code object loads, held until the process
+// ends) that stands in for the caller's workspace.  Host code never passes
+// its name to a kernel: the name is a host-side stand-in; the device address
+// comes from hipGetSymbolAddress (noalloc_scratch below).
+static constexpr size_t kNoallocScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
 namespace ssla {
 namespace {
 
@@ -995,4 +1006,76 @@ extern "C" int ssla_gla_chunk_fwd(const void *q, const void *k, const void *v, c
                 : launch_chunk<SSLA_BF16, false>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
   return gf32 ? launch_chunk<SSLA_F16, true>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st)
               : launch_chunk<SSLA_F16, false>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
+}
+
+namespace ssla {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the device that runs `stream` (the current
+// device for the null stream), looked up once per device with that device
+// current and cached.
+int noalloc_scratch(hipStream_t stream, void **out) {
+  int cur = 0, dev = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e == hipSuccess) {
+    dev = cur;
+    if (stream) e = hipStreamGetDevice(stream, &dev);
+  }
+  if (e != hipSuccess) {
+    set_error("gla_chunk_fwd_noalloc: device query failed: %s", hipGetErrorString(e));
+    return SSLA_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    set_error("gla_chunk_fwd_noalloc: device %d beyond the %d the scratch table holds", dev, kMaxScratchDevices);
+    return SSLA_ERR_UNSUPPORTED;
+  }
+  void *p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      if (dev != cur) e = hipSetDevice(dev);
+      if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (dev != cur) {
+        const hipError_t e2 = hipSetDevice(cur);
+        if (e == hipSuccess) e = e2;
+      }
+      if (e != hipSuccess || p == nullptr) {
+        set_error("gla_chunk_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+        return SSLA_ERR_LAUNCH;
+      }
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return SSLA_OK;
+}
+
+}  // namespace
+}  // namespace ssla
+
+extern "C" int ssla_gla_chunk_fwd_noalloc(const void *q, const void *k, const void *v, const void *g,
+                                          int g_dtype, const int64_t *cu_seqlens, int n_seq, int64_t T,
+                                          int H, int K, int V, float scale, const float *h0, void *o,
+                                          float *ht, int dtype, void *stream) {
+  using namespace ssla;
+  clear_error();
+  const size_t need = ssla_gla_chunk_workspace_size(n_seq, T, H, K, V);
+  if (need > kNoallocScratchBytes) {
+    set_error("gla_chunk_fwd_noalloc: this shape needs %zu bytes of workspace, the static scratch holds %zu "
+              "(call ssla_gla_chunk_fwd with a workspace)", need, kNoallocScratchBytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  void *ws = nullptr;
+  if (need > 0) {
+    const int st = noalloc_scratch(static_cast<hipStream_t>(stream), &ws);
+    if (st != SSLA_OK) return st;
+  }
+  return ssla_gla_chunk_fwd(q, k, v, g, g_dtype, cu_seqlens, n_seq, T, H, K, V, scale, h0, o, ht, dtype, ws,
+                            need > 0 ? kNoallocScratchBytes : 0, stream);
 }
