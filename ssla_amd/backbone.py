@@ -1,0 +1,217 @@
+"""The asynchronous forward step of a sparse GLA backbone on MI355X: the
+fifth configuration of the benchmark this package is measured on.
+
+The reference's MosModel step (model_mos.py:157-170) preprocesses a window
+of events into pixel groups (:173-209), runs its backbone of sparse layers,
+turns the stride-8/16/32 outputs into dense grids (async_event_to_grid,
+:212-228) and ends with a YOLOX head (layers/yolox_head.py:183-230).  Its
+layers keep no state from one window to the next.  The configuration
+measured here keeps one: every stage holds a per-site GLA state
+``S[site] in R^{H x D x D}`` (fp32, resident in HBM) that is carried across
+consecutive windows, and a window updates the states of the sites it
+touches only.  For a site with events ``x_1..x_n`` (in time order) in this
+window, with ``q, k, v = W x`` (bf16) and per-key log-gates
+``g = logsigmoid(W_g x) / 16``:
+
+    S <- diag(exp(g_t)) S + k_t v_t^T,   o_t = (D^-1/2 q_t)^T S      (t = 1..n)
+
+which is the reference's ``naive_gla_recurrent`` (ops/gla/naive.py:50-111)
+over the site's events with ``initial_state = S[site]`` and the final state
+written back -- one ``ssla_gla_recurrent_fwd`` launch with ``state_idx``
+per stage (``sparse_gla_scan``).  Sites without events keep their states
+bit for bit.
+
+Step (one window, B samples):
+  preprocess (group_events, pixel delays, hot-pixel truncation)
+  stem: per-event embedding 2 -> C1, SparseMaxPool k=4 (stride 4)
+  stage s = 1..4 (C = 32/64/128/256 at stride 4/8/16/32, H = 4, D = 32):
+      SiteGLABlock (projections in bf16, the per-site recurrence with fp32
+      states, output projection, residual, LayerNorm in fp32), then
+      SparseMaxPool k=2 for stages 1-3
+  dense grids of the stage 2-4 outputs (last event of every site)
+  DetectionHead (the YOLOX head's inference path, bf16)
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List, Sequence, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import events as E
+from .layers import SparseMaxPool
+from .scan import sparse_gla_scan
+
+__all__ = ["SiteGLABlock", "DetectionHead", "AsyncSparseGLA", "STAGES"]
+
+# (channels, stride) of the four stages
+STAGES: Tuple[Tuple[int, int], ...] = ((32, 4), (64, 8), (128, 16), (256, 32))
+
+
+def grid_of(frame_size: Sequence[int], stride: int) -> Tuple[int, int]:
+    """Output grid of 'same'-padded pooling by `stride` (ceil division)."""
+    return (-(-int(frame_size[0]) // stride), -(-int(frame_size[1]) // stride))
+
+
+class SiteGLABlock(nn.Module):
+    """Per-site matrix-state GLA over the sites active in one window.
+
+    ``forward(inputs, state, grid_size)`` takes a grouped-events dict whose
+    groups are sites of a ``grid_size`` grid (one group per active site, its
+    events in time order, groups in increasing (batch, row, column) order --
+    the layout SparsePool produces) and ``state`` fp32
+    ``[B * Hg * Wg, heads, head_dim, head_dim]``, updated in place.
+    """
+
+    def __init__(self, in_channels: int, out_channels: int, heads: int = 4, head_dim: int = 32,
+                 gate_normalizer: float = 16.0):
+        super().__init__()
+        self.in_channels, self.out_channels = in_channels, out_channels
+        self.heads, self.head_dim = heads, head_dim
+        self.gate_normalizer = gate_normalizer
+        hd = heads * head_dim
+        self.q_proj = nn.Linear(in_channels, hd, bias=False)
+        self.k_proj = nn.Linear(in_channels, hd, bias=False)
+        self.v_proj = nn.Linear(in_channels, hd, bias=False)
+        self.g_proj = nn.Linear(in_channels, hd, bias=False)
+        self.o_proj = nn.Linear(hd, out_channels, bias=False)
+        self.res_proj = nn.Linear(in_channels, out_channels, bias=False) if in_channels != out_channels else None
+        self.norm = nn.LayerNorm(out_channels)
+
+    def project(self, x: torch.Tensor):
+        """q, k, v (bf16 ``[n, H, D]``) and log-gates g (fp32 ``[n, H, D]``)."""
+        n = x.shape[0]
+        xb = x.to(torch.bfloat16)
+        shp = (n, self.heads, self.head_dim)
+        q, k, v = (F.linear(xb, p.weight.to(torch.bfloat16)).view(shp)
+                   for p in (self.q_proj, self.k_proj, self.v_proj))
+        g = F.logsigmoid(F.linear(xb, self.g_proj.weight.to(torch.bfloat16)).float()) / self.gate_normalizer
+        return q, k, v, g.view(shp)
+
+    def finish(self, o: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """LayerNorm(o_proj(o) + residual) in fp32 (projections in bf16)."""
+        n = x.shape[0]
+        y = F.linear(o.reshape(n, -1), self.o_proj.weight.to(torch.bfloat16)).float()
+        if self.res_proj is not None:
+            y = y + F.linear(x.to(torch.bfloat16), self.res_proj.weight.to(torch.bfloat16)).float()
+        else:
+            y = y + x
+        return self.norm(y)
+
+    @staticmethod
+    def sites(inputs: Dict[str, torch.Tensor], grid_size: Sequence[int]) -> torch.Tensor:
+        Hg, Wg = int(grid_size[0]), int(grid_size[1])
+        return ((inputs["batch_id"] * Hg + inputs["h"]) * Wg + inputs["w"]).to(torch.int32)
+
+    def forward(self, inputs: Dict[str, torch.Tensor], state: torch.Tensor, grid_size: Sequence[int],
+                check: bool = False) -> Dict[str, torch.Tensor]:
+        x = inputs["events"].to(torch.float32)
+        lengths = inputs["lengths"]
+        cu = F.pad(torch.cumsum(lengths, 0), (1, 0))
+        q, k, v, g = self.project(x)
+        o = sparse_gla_scan(q, k, v, g, cu, self.sites(inputs, grid_size), state,
+                            scale=self.head_dim ** -0.5, check=check)
+        out = dict(inputs)
+        out["events"] = self.finish(o, x)
+        return out
+
+
+class DetectionHead(nn.Module):
+    """The YOLOX head's inference path (reference layers/yolox_head.py:
+    100-182 structure, 183-230 forward, 234-256 decode): per level a 1x1
+    conv + BatchNorm + SiLU branch for classes and one for boxes, 1x1
+    predictions of boxes (4), objectness (1) and classes; outputs ``[B,
+    anchors, 5 + classes]`` with box centres ``(t + cell) * stride`` and
+    sizes ``exp(t) * stride``.  No losses (the step has no labels)."""
+
+    def __init__(self, num_classes: int, strides: Sequence[int], in_channels: Sequence[int], width: int):
+        super().__init__()
+        self.num_classes, self.strides = num_classes, tuple(strides)
+
+        def branch(c):
+            return nn.Sequential(nn.Conv2d(c, width, 1), nn.BatchNorm2d(width), nn.SiLU())
+
+        self.cls_convs = nn.ModuleList(branch(c) for c in in_channels)
+        self.reg_convs = nn.ModuleList(branch(c) for c in in_channels)
+        self.cls_preds = nn.ModuleList(nn.Conv2d(width, num_classes, 1) for _ in in_channels)
+        self.reg_preds = nn.ModuleList(nn.Conv2d(width, 4, 1) for _ in in_channels)
+        self.obj_preds = nn.ModuleList(nn.Conv2d(width, 1, 1) for _ in in_channels)
+        prior = -math.log((1 - 0.01) / 0.01)
+        for m in list(self.cls_preds) + list(self.obj_preds):
+            nn.init.constant_(m.bias, prior)
+
+    def forward(self, xin: List[torch.Tensor]) -> torch.Tensor:
+        outs = []
+        for lvl, x in enumerate(xin):
+            cls_feat = self.cls_convs[lvl](x)
+            reg_feat = self.reg_convs[lvl](x)
+            out = torch.cat([self.reg_preds[lvl](reg_feat), self.obj_preds[lvl](reg_feat),
+                             self.cls_preds[lvl](cls_feat)], 1)
+            B, C, Hh, Ww = out.shape
+            out = out.permute(0, 2, 3, 1).reshape(B, Hh * Ww, C)
+            yv, xv = torch.meshgrid(torch.arange(Hh, device=x.device), torch.arange(Ww, device=x.device),
+                                    indexing="ij")
+            cell = torch.stack((xv, yv), 2).reshape(1, Hh * Ww, 2).to(out.dtype)
+            s = self.strides[lvl]
+            out = torch.cat([(out[..., :2] + cell) * s, torch.exp(out[..., 2:4]) * s, out[..., 4:]], -1)
+            outs.append(out)
+        return torch.cat(outs, 1)
+
+
+class AsyncSparseGLA(nn.Module):
+    """Stem, four per-site GLA stages with pooling, dense grids and the
+    detection head.  ``forward(events, lengths, states)`` runs one window
+    (``events`` fp32 ``[B, N, 4]`` as <x, y, t, p> with ``lengths [B]``, the
+    reference's collated batch) and updates ``states`` (``init_states``) in
+    place; it returns the head output and the per-stage outputs."""
+
+    def __init__(self, frame_size=(240, 304), num_classes: int = 2, stages=STAGES, heads: int = 4,
+                 head_dim: int = 32, hot_pixel_thres: int = 50):
+        super().__init__()
+        self.frame_size = tuple(frame_size)
+        self.stages = tuple(stages)
+        self.heads, self.head_dim = heads, head_dim
+        self.hot_pixel_thres = hot_pixel_thres
+        self.grid_sizes = [grid_of(frame_size, s) for _, s in self.stages]
+        c1 = self.stages[0][0]
+        self.embed = nn.Linear(2, c1, bias=False)
+        self.stem_pool = SparseMaxPool(self.frame_size, kernel_size=(self.stages[0][1],) * 2)
+        blocks, pools = [], []
+        c_prev = c1
+        for i, (c, _) in enumerate(self.stages):
+            blocks.append(SiteGLABlock(c_prev, c, heads, head_dim))
+            if i + 1 < len(self.stages):
+                k = self.stages[i + 1][1] // self.stages[i][1]
+                pools.append(SparseMaxPool(self.grid_sizes[i], kernel_size=(k, k)))
+            c_prev = c
+        self.blocks = nn.ModuleList(blocks)
+        self.pools = nn.ModuleList(pools)
+        self.head_levels = list(range(1, len(self.stages)))          # strides 8, 16, 32
+        chans = [self.stages[i][0] for i in self.head_levels]
+        self.head = DetectionHead(num_classes, [self.stages[i][1] for i in self.head_levels], chans, chans[-1])
+        self.head.to(torch.bfloat16)
+        self.head.eval()
+
+    def init_states(self, batch_size: int, device) -> List[torch.Tensor]:
+        D = self.head_dim
+        return [torch.zeros(batch_size * Hg * Wg, self.heads, D, D, dtype=torch.float32, device=device)
+                for Hg, Wg in self.grid_sizes]
+
+    def stem(self, events: torch.Tensor, lengths: torch.Tensor) -> Dict[str, torch.Tensor]:
+        gr = E.preprocess_inputs(events, lengths, self.frame_size, self.hot_pixel_thres)
+        gr["events"] = F.linear(gr["events"].to(torch.bfloat16), self.embed.weight.to(torch.bfloat16)).float()
+        return self.stem_pool(gr)
+
+    def forward(self, events: torch.Tensor, lengths: torch.Tensor, states: List[torch.Tensor]):
+        x = self.stem(events, lengths)
+        feats = []
+        for i, blk in enumerate(self.blocks):
+            x = blk(x, states[i], self.grid_sizes[i])
+            feats.append(x)
+            if i < len(self.pools):
+                x = self.pools[i](x)
+        grids = [E.events_to_grid(feats[i], self.grid_sizes[i], self.stages[i][0]).to(torch.bfloat16)
+                 for i in self.head_levels]
+        return self.head(grids), feats

@@ -17,6 +17,10 @@ the device by the caller):
   each, about 50k events per window from the same cluster mixture, t
   sorted and uniform in the window, polarity +-1 equiprobable) as the padded
   <x, y, t, p> batch the model's preprocessing takes.
+* :func:`async_windows` -- consecutive 100 ms windows of one stream (the
+  same cluster mixture, centres drifting across windows, absolute
+  timestamps) for the asynchronous forward step that carries its per-site
+  states from window to window.
 """
 from __future__ import annotations
 
@@ -150,3 +154,38 @@ def event_windows(B=8, n_mean=50_000, W=304, Hp=240, window_us=100_000, n_cluste
         ev[b, :n, 3] = 2 * rng.integers(0, 2, n) - 1
         ev[b, n:, 3] = -1
     return torch.from_numpy(ev), torch.tensor(lens, dtype=torch.int64)
+
+
+def async_windows(n_windows=20, n_events=50_000, W=304, Hp=240, window_us=100_000, n_clusters=20, sigma=8.0,
+                  seed=0) -> List[torch.Tensor]:
+    """``n_windows`` consecutive windows of one event stream, each an fp32
+    ``[1, n_events, 4]`` batch of <x, y, t, p> (t in microseconds from the
+    stream start, sorted; window w covers [w, w + 1) * window_us).  70 % of
+    the events fall in Gaussian clusters (sigma px) whose centres move at a
+    constant velocity across the whole stream, 30 % are uniform; p = +-1
+    equiprobable.  Clusters persisting from window to window make the same
+    sites active again, so the carried per-site states matter."""
+    rng = np.random.default_rng(seed)
+    c0 = rng.uniform([0, 0], [W, Hp], size=(n_clusters, 2))
+    vel = rng.uniform(-30, 30, size=(n_clusters, 2))            # px per window
+    out = []
+    for w in range(n_windows):
+        t = np.sort(rng.integers(0, window_us, n_events)) + w * window_us
+        n_cl = int(round(0.7 * n_events))
+        pick = rng.permutation(n_events)
+        cl, un = pick[:n_cl], pick[n_cl:]
+        xy = np.empty((n_events, 2))
+        which = rng.integers(0, n_clusters, size=n_cl)
+        pos = c0[which] + vel[which] * (t[cl, None] / window_us)
+        pos = np.abs(np.mod(pos, [2 * W, 2 * Hp]))                 # reflect at the borders
+        pos = np.where(pos >= [W, Hp], [2 * W, 2 * Hp] - pos, pos)
+        xy[cl] = pos + rng.normal(0.0, sigma, size=(n_cl, 2))
+        xy[un] = rng.uniform([0, 0], [W, Hp], size=(len(un), 2))
+        xy = np.rint(xy)
+        ev = np.empty((1, n_events, 4), np.float32)
+        ev[0, :, 0] = np.clip(xy[:, 0], 0, W - 1)
+        ev[0, :, 1] = np.clip(xy[:, 1], 0, Hp - 1)
+        ev[0, :, 2] = t
+        ev[0, :, 3] = 2 * rng.integers(0, 2, n_events) - 1
+        out.append(torch.from_numpy(ev))
+    return out

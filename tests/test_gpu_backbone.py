@@ -1,0 +1,179 @@
+"""GPU parity of the asynchronous forward step (ssla_amd.backbone, the fifth
+benchmark configuration) against its CPU restatement (oracle.backbone).
+
+Every piece is checked on the GPU's own input to that piece, so a
+difference is pinned to the piece that made it:
+* preprocessing and pooling keys (times, lengths, sites) bit for bit; pooled
+  features bit for bit when the pooled rows are the GPU's own (the max
+  selects, it does not round);
+* bf16 projections within bf16 rounding: RMS error ratio <= 2e-3 and every
+  element within 2 bf16 ulps (2^-7 relative) plus 2e-3 of the RMS;
+* the per-site recurrence on the GPU's q, k, v, g: o (rounded to bf16) at
+  the north star's bf16 bar (RMS ratio <= 2e-2), the fp32 states of the
+  active sites at 1e-4, the states of every inactive site unchanged bit
+  for bit;
+* LayerNorm outputs and the bf16 detection head within bf16 rounding of
+  their inputs (ratio <= 2e-2).
+The whole ``forward`` equals the piecewise run bit for bit (the kernels are
+deterministic)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import backbone as ob
+from tests.conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(module):
+    return {k: v.detach().float().cpu().numpy() for k, v in module.state_dict().items()}
+
+
+def _np(x):
+    return x.detach().float().cpu().numpy()
+
+
+def _np_dict(d):
+    """A grouped-events dict on the host: fp32 features, int64 keys."""
+    out = {}
+    for key, val in d.items():
+        if torch.is_tensor(val):
+            out[key] = _np(val) if key == "events" else val.cpu().numpy().astype(np.int64)
+        else:
+            out[key] = val
+    return out
+
+
+def _int_keys_equal(gpu, ref, what):
+    for key in ("lengths", "time", "h", "w", "batch_id"):
+        a, b = _np(gpu[key]).astype(np.int64), np.asarray(ref[key], np.int64)
+        assert a.shape == b.shape and np.array_equal(a, b), f"{what}: {key} differs"
+
+
+def _close_bf16(a, b, name):
+    """bf16 GEMM results: 2 ulps elementwise plus 2e-3 of the RMS."""
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    rms = float(np.sqrt(np.mean(b * b))) if b.size else 0.0
+    err = np.abs(a - b)
+    bad = err > 2.0 ** -7 * np.abs(b) + 2e-3 * rms
+    assert not bad.any(), f"{name}: {int(bad.sum())}/{bad.size} beyond 2 bf16 ulps; max err {err.max():.3g}"
+    ratio = float(np.sqrt(np.mean(err * err)) / (rms + 1e-30)) if b.size else 0.0
+    assert ratio <= 2e-3, f"{name}: RMS ratio {ratio:.3g}"
+
+
+def _window_piecewise(model, ev, ln, states, params, dev, check_oracle=True, tag=""):
+    from ssla_amd.scan import sparse_gla_scan
+    frame = model.frame_size
+    with torch.no_grad():
+        x = model.stem(ev.to(dev), ln.to(dev))
+    if check_oracle:
+        rx = ob.stem(params, ev.numpy(), ln.numpy(), frame, model.stages[0][1])
+        _int_keys_equal(x, rx, f"stem{tag}")
+        _close_bf16(_np(x["events"]), rx["events"], f"stem events{tag}")
+    feats = []
+    for i, blk in enumerate(model.blocks):
+        p = {k[len(f"blocks.{i}."):]: v for k, v in params.items() if k.startswith(f"blocks.{i}.")}
+        grid = model.grid_sizes[i]
+        before = states[i].clone()
+        xe = x["events"].to(torch.float32)
+        with torch.no_grad():
+            q, k, v, g = blk.project(xe)
+            cu = torch.nn.functional.pad(torch.cumsum(x["lengths"], 0), (1, 0))
+            sites = blk.sites(x, grid)
+            o = sparse_gla_scan(q, k, v, g, cu, sites, states[i], scale=blk.head_dim ** -0.5)
+            y = blk.finish(o, xe)
+        out = dict(x)
+        out["events"] = y
+        if check_oracle:
+            xn = _np(xe)
+            rq, rk, rv, rg = ob.block_project(p, xn, blk.heads, blk.head_dim)
+            for nm, a, b in (("q", q, rq), ("k", k, rk), ("v", v, rv), ("g", g, rg)):
+                _close_bf16(_np(a), b, f"stage {i} {nm}{tag}")
+            ref_state = before.cpu().numpy()
+            ro = ob.block_scan(_np(q), _np(k), _np(v), _np(g), _np(x["lengths"]).astype(np.int64),
+                               _np(sites).astype(np.int64), ref_state, blk.head_dim ** -0.5)
+            assert_close(_np(o), ro, 2e-2, f"stage {i} o{tag}", ratio_mode=True)
+            act = np.unique(_np(sites).astype(np.int64))
+            inact = torch.from_numpy(np.setdiff1d(np.arange(states[i].shape[0]), act)).to(dev)
+            assert torch.equal(states[i][inact], before[inact]), f"stage {i}: inactive states changed{tag}"
+            assert_close(states[i].cpu().numpy()[act], ref_state[act], 1e-4, f"stage {i} states{tag}")
+            ry = ob.block_finish(p, _np(o).astype(np.float64), xn)
+            assert_close(_np(y), ry, 2e-2, f"stage {i} out{tag}", ratio_mode=True)
+        feats.append(out)
+        if i < len(model.pools):
+            with torch.no_grad():
+                x = model.pools[i](out)
+            if check_oracle:
+                rp = ob.max_pool(_np_dict(out), grid, model.stages[i + 1][1] // model.stages[i][1])
+                _int_keys_equal(x, rp, f"pool {i}{tag}")
+                assert np.array_equal(_np(x["events"]), rp["events"]), f"pool {i} events{tag}"
+    from ssla_amd import events as E
+    with torch.no_grad():
+        grids = [E.events_to_grid(feats[i], model.grid_sizes[i], model.stages[i][0]) for i in model.head_levels]
+        out = model.head([gg.to(torch.bfloat16) for gg in grids])
+    if check_oracle:
+        for lvl, i in enumerate(model.head_levels):
+            rg = oracle.events.event_to_grid(_np_dict(feats[i]), model.grid_sizes[i], model.stages[i][0])
+            assert np.array_equal(_np(grids[lvl]), rg), f"grid {lvl}{tag}"
+        hp = {k[5:]: v for k, v in params.items() if k.startswith("head.")}
+        rh = ob.head(hp, [_np(gg) for gg in grids], [model.stages[i][1] for i in model.head_levels])
+        assert_close(_np(out), rh, 2e-2, f"head{tag}", ratio_mode=True)
+    return out, feats
+
+
+def test_async_step_windows_vs_oracle(dev):
+    """Three consecutive windows of 5k events: every piece against the
+    oracle, states carried from window to window (so later windows start
+    from non-zero states), and forward() == the piecewise run."""
+    import oracle.events  # noqa: F401
+    from ssla_amd import synthetic
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(0)
+    model = AsyncSparseGLA().to(dev)
+    params = _params(model)
+    states = model.init_states(1, dev)
+    for w, ev in enumerate(synthetic.async_windows(3, 5000, seed=1)):
+        ln = torch.tensor([ev.shape[1]])
+        print(f"async step window {w}: {ev.shape[1]} events", flush=True)
+        states_fwd = [s.clone() for s in states]
+        out, _ = _window_piecewise(model, ev, ln, states, params, dev, tag=f" w{w}")
+        with torch.no_grad():
+            out_f, _ = model(ev.to(dev), ln.to(dev), states_fwd)
+        assert torch.equal(out_f, out), f"forward() differs from the piecewise run in window {w}"
+        for i in range(4):
+            assert torch.equal(states_fwd[i], states[i]), f"forward() states differ (stage {i}, window {w})"
+
+
+def test_async_step_full_size_properties(dev):
+    """Four windows of 50k events at full size: head output [1, 1505, 7]
+    and finite, every state row either unchanged (inactive site) or
+    changed, stage outputs unit-scale (LayerNorm), and a rerun from the same
+    states is bit-identical."""
+    from ssla_amd import synthetic
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(1)
+    model = AsyncSparseGLA().to(dev)
+    states = model.init_states(1, dev)
+    for w, ev in enumerate(synthetic.async_windows(4, 50_000, seed=2)):
+        ln = torch.tensor([ev.shape[1]], device=dev)
+        print(f"async step full size window {w}", flush=True)
+        prev = [s.clone() for s in states]
+        with torch.no_grad():
+            out, feats = model(ev.to(dev), ln, states)
+            again = [p.clone() for p in prev]
+            out2, _ = model(ev.to(dev), ln, again)
+        assert out.shape == (1, 30 * 38 + 15 * 19 + 8 * 10, 7) and torch.isfinite(out.float()).all()
+        assert torch.equal(out, out2) and all(torch.equal(a, b) for a, b in zip(again, states))
+        for i, f in enumerate(feats):
+            sites = ((f["batch_id"] * model.grid_sizes[i][0] + f["h"]) * model.grid_sizes[i][1] + f["w"]).long()
+            assert bool((sites[1:] > sites[:-1]).all()), f"stage {i}: site list not strictly increasing"
+            changed = (states[i] != prev[i]).flatten(1).any(1)
+            mask = torch.zeros_like(changed)
+            mask[sites] = True
+            assert not bool((changed & ~mask).any()), f"stage {i}: an inactive state changed"
+            assert bool(changed[sites].all()), f"stage {i}: an active state did not change"
+            y = f["events"]
+            assert torch.isfinite(y).all()
+            assert abs(float(y.mean())) < 0.1 and 0.8 < float(y.std()) < 1.2
