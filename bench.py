@@ -9,11 +9,19 @@ T=4096 tokens, H=8, K=V=64, chunk 64, bf16 q/k/v/o, fp32 g/h0/ht.  One
 already resident in HBM.  Two input sets (2 x 203 MB, more than the 256 MB
 Infinity Cache) alternate so that the timed loop streams from HBM.
 
-Secondary lines (same JSON object): the per-site sparse GLA scan (config 3,
-64 bins per step), the scatter-max pooling (config 4, 1e6 events, in
-shuffled order and sorted by cell), the chunk GLA backward at config 2, and
-the first stage of the MOS_S backbone (ingest, preprocess, two MosAttention
-layers, SparseMaxPool, TemporalDropout) on 8 synthetic Gen1 windows.
+Secondary lines (same JSON object): config 1 (the recurrent GLA call the
+reference runs on the CPU), the per-site sparse GLA scan (config 3, 64 bins
+per pass, bin by bin and in one call), the scatter-max pooling (config 4,
+1e6 events, in shuffled order and sorted by cell), the asynchronous forward
+step (config 5, 20 windows x 50k events with carried per-site states), the
+chunk GLA backward at config 2, and the first stage of the MOS_S backbone
+(ingest, preprocess, two MosAttention layers, SparseMaxPool,
+TemporalDropout) on 8 synthetic Gen1 windows.
+
+CPU baselines (``cpu_baseline`` of the main line and of the config 1, 3, 4
+and 5 lines) time this build's PyTorch / fp64 restatements of the
+reference's CPU-capable paths (oracle/) on the host's cores after the GPU
+measurements, with the thread count, host CPU count and CPU model recorded.
 
 Prints ONE JSON line.  Kernel durations come from HIP events recorded on
 the stream the kernels are launched on (torch's current stream, which is
@@ -51,20 +59,74 @@ def c2_flops():
     return Tt * H * ((BT + 1) * (D + D) + 4 * D * D)
 
 
-def _traffic_from_profile(name):
+def _source_sha(rel):
+    import hashlib
+    return hashlib.sha256((ROOT / rel).read_bytes()).hexdigest()[:16]
+
+
+def _traffic_from_profile(name, source):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, scaled by the copy-kernel calibration), read from the
-    committed summary profiles/<name>; None if absent."""
+    committed summary profiles/<name>, with the note that says where it came
+    from.  The summary records the sha256 (first 16 hex digits) of the
+    kernel source it was measured on; when that is not the current source
+    the figure is stale and None is returned."""
     p = ROOT / "profiles" / name
     if not p.exists():
-        return None
+        return None, f"profiles/{name} missing"
+    val, sha = None, None
     for line in p.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
             try:
-                return float(line.split(":", 1)[1].strip().split()[0])
+                val = float(line.split(":", 1)[1].strip().split()[0])
             except ValueError:
-                return None
-    return None
+                val = None
+        elif line.startswith("source_sha256_16:"):
+            sha = line.split(":", 1)[1].strip().split()[0]
+    cur = _source_sha(source)
+    if sha != cur:
+        return None, (f"profiles/{name} was measured on {source} sha {sha}, the current source is {cur}: "
+                      "stale, not reported")
+    return val, f"rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE from profiles/{name} ({source} sha {cur})"
+
+
+def _cpu_info():
+    """Host-core facts recorded with every CPU baseline."""
+    import torch
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"host_cpus": os.cpu_count(), "torch_threads": torch.get_num_threads(), "cpu_model": model}
+
+
+def _cpu_threads():
+    """Threads for the CPU legs: the box's CPU share (OMP_NUM_THREADS is set
+    to it there), never more than the host reports."""
+    n = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    return max(1, min(n, os.cpu_count() or 1))
+
+
+def _median_time(fn, runs=3):
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], ts
+
+
+def _flush_mall(torch, dev, buf=[]):
+    """Write 512 MiB so that nothing of the previous pass stays in the
+    256 MB Infinity Cache (used between timed passes, outside the timing)."""
+    if not buf:
+        buf.append(torch.empty(512 * 2**20 // 4, dtype=torch.float32, device=dev))
+    buf[0].zero_()
 
 
 def bench_chunk(torch, lib, steps, warmup, dev):
@@ -107,136 +169,202 @@ def bench_chunk(torch, lib, steps, warmup, dev):
                 tokens=Tt, sample=sets[0])
 
 
-def bench_sparse(torch, lib, reps, dev):
-    """Config 3: 64 bins of per-site GLA updates, bin by bin."""
-    from ssla_amd import _lib, synthetic
-    sb = synthetic.sparse_scan_bins()
-    state = sb.state0.to(dev).contiguous()
-    bins = []
-    for b in range(len(sb.sites)):
-        bins.append(dict(s=torch.from_numpy(sb.sites[b]).to(dev), q=sb.q[b].to(dev), k=sb.k[b].to(dev),
-                         v=sb.v[b].to(dev), g=sb.g[b].to(dev),
-                         o=torch.empty(sb.sites[b].size, 4, 32, device=dev)))
-    stream = torch.cuda.current_stream(dev)
-    sh = stream.cuda_stream
+C3_STEP_BYTES = 4 * (2 * 4 * 32 * 32 + 3 * 4 * 32 + 2 * 4 * 32) + 4   # state in + out, q k g v o, index
 
-    def one_pass():
-        for x in bins:
-            st = lib.ssla_sparse_gla_step(x["s"].data_ptr(), x["s"].numel(), x["q"].data_ptr(),
-                                          x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
-                                          state.data_ptr(), sb.n_sites, 4, 32, 32, float(sb.scale),
-                                          x["o"].data_ptr(), None, sh)
+
+def _c3_sets(torch, dev, n_sets=2):
+    """Config-3 inputs on the device, n_sets independent draws (state table
+    74.7 MB + the bins' q, k, v, g, o about 146 MB per set)."""
+    from ssla_amd import synthetic
+    sets = []
+    for seed in range(n_sets):
+        sb = synthetic.sparse_scan_bins(seed=seed)
+        bins = [dict(s=torch.from_numpy(sb.sites[b]).to(dev), q=sb.q[b].to(dev), k=sb.k[b].to(dev),
+                     v=sb.v[b].to(dev), g=sb.g[b].to(dev), o=torch.empty(sb.sites[b].size, 4, 32, device=dev))
+                for b in range(len(sb.sites))]
+        sets.append(dict(sb=sb, bins=bins, state=sb.state0.to(dev).contiguous()))
+    return sets
+
+
+def cpu_sparse(sb, n_bins=64, runs=5):
+    """CPU leg of config 3: the per-bin torch loop (gather the active states,
+    decay-and-add update, o, scatter back) over the pass's n_bins bins."""
+    import torch
+    from oracle import torch_ref
+    torch.set_num_threads(_cpu_threads())
+    sites = [torch.from_numpy(s).long() for s in sb.sites[:n_bins]]
+    steps = sum(int(s.numel()) for s in sites)
+    torch_ref.sparse_scan_bins(sb.state0.clone(), sites[:2], sb.q, sb.k, sb.v, sb.g, sb.scale)   # warm-up
+    med, ts = _median_time(lambda: torch_ref.sparse_scan_bins(sb.state0.clone(), sites, sb.q, sb.k, sb.v, sb.g,
+                                                              sb.scale), runs)
+    return {"value": steps / med, "unit": "site-steps/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{n_bins} bins ({steps} site-steps), torch fp32 per-bin index_select / "
+                      f"update / einsum / index_copy_; median of {len(ts)} runs {[round(t, 3) for t in ts]} s",
+            **_cpu_info()}
+
+
+def bench_sparse(torch, lib, reps, dev, sets=None):
+    """Config 3: 64 bins of per-site GLA updates, bin by bin (one
+    ssla_sparse_gla_step launch per bin).  Two independent input sets
+    alternate and 512 MiB are written between passes (outside the timing),
+    so every pass starts with nothing in the Infinity Cache; within a pass
+    a state row read by several bins may stay cached, as it would in use."""
+    from ssla_amd import _lib
+    sets = sets or _c3_sets(torch, dev)
+    stream = torch.cuda.current_stream(dev)
+    n_sites = sets[0]["sb"].n_sites
+    scale = float(sets[0]["sb"].scale)
+
+    def one_pass(x, sh):
+        for b in x["bins"]:
+            st = lib.ssla_sparse_gla_step(b["s"].data_ptr(), b["s"].numel(), b["q"].data_ptr(), b["k"].data_ptr(),
+                                          b["v"].data_ptr(), b["g"].data_ptr(), x["state"].data_ptr(), n_sites, 4, 32,
+                                          32, scale, b["o"].data_ptr(), None, sh)
             _lib.check(st, "ssla_sparse_gla_step")
 
-    one_pass()
+    def timed(run, n):
+        tot = 0.0
+        for i in range(n):
+            _flush_mall(torch, dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            run(sets[i % len(sets)])
+            e1.record(stream)
+            torch.cuda.synchronize()
+            tot += e0.elapsed_time(e1)
+        return tot / n
+
+    for x in sets:
+        one_pass(x, stream.cuda_stream)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        one_pass()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    # the same pass captured once as a HIP graph and replayed (no launch gaps)
+    ms = timed(lambda x: one_pass(x, stream.cuda_stream), reps)
+    # the same pass captured once per set as a HIP graph and replayed (no launch gaps)
     side = torch.cuda.Stream(dev)
     side.wait_stream(stream)
     with torch.cuda.stream(side):
-        sh = side.cuda_stream
-        one_pass()
+        for x in sets:
+            one_pass(x, side.cuda_stream)
     stream.wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        sh = torch.cuda.current_stream(dev).cuda_stream
-        one_pass()
-    sh = stream.cuda_stream
-    graph.replay()
+    graphs = []
+    for x in sets:
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            one_pass(x, torch.cuda.current_stream(dev).cuda_stream)
+        graphs.append(gr)
+    for gr in graphs:
+        gr.replay()
     torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(reps):
-        graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_graph = e0.elapsed_time(e1) / reps
-    steps = sb.site_steps
-    per_step_bytes = 4 * (2 * 4 * 32 * 32 + 3 * 4 * 32 + 2 * 4 * 32) + 4
-    gbs = steps * per_step_bytes / (ms * 1e-3) / 1e9
-    gbs_graph = steps * per_step_bytes / (ms_graph * 1e-3) / 1e9
+    gidx = {id(x): i for i, x in enumerate(sets)}
+    ms_graph = timed(lambda x: graphs[gidx[id(x)]].replay(), reps)
+    steps = sets[0]["sb"].site_steps
+    gbs = steps * C3_STEP_BYTES / (ms * 1e-3) / 1e9
+    gbs_graph = steps * C3_STEP_BYTES / (ms_graph * 1e-3) / 1e9
     return {"workload": "sparse_gla_step config 3: 76x60 sites, 64 bins, H=4, K=V=32, fp32",
             "metric": "sparse scan site-steps/s", "value": steps / (ms * 1e-3), "unit": "site-steps/s",
-            "ms_per_pass": ms, "site_steps_per_pass": steps, "launches_per_pass": len(bins),
+            "ms_per_pass": ms, "site_steps_per_pass": steps, "launches_per_pass": len(sets[0]["bins"]),
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gbs / HBM_PEAK_GBS, "bytes_per_site_step": per_step_bytes,
-                         "note": "per-pass average over 64 launches, launch gaps included"},
+                         "frac": gbs / HBM_PEAK_GBS, "bytes_per_site_step": C3_STEP_BYTES,
+                         "note": "per-pass average over 64 launches (launch gaps included); 2 input sets "
+                                 "(2 x 221 MB) alternate and the Infinity Cache is flushed before every pass"},
             "graph": {"value": steps / (ms_graph * 1e-3), "ms_per_pass": ms_graph, "achieved": gbs_graph,
                       "frac": gbs_graph / HBM_PEAK_GBS,
-                      "note": "the 64 launches captured once as a HIP graph and replayed"}}
+                      "note": "the 64 launches captured once as a HIP graph and replayed"},
+            "cpu_baseline": cpu_sparse(sets[0]["sb"])}
 
 
 def bench_sparse_batched(torch, lib, reps, dev):
     """Config 3 with all 64 bins in one call (sparse_gla_scan ->
     ssla_gla_recurrent_fwd with state_idx): the same site-steps regrouped
     site-major, stable in time (outside the timing), so each active site's
-    state is read and written once per pass instead of once per step.  The
-    state is restored between passes by a device copy outside the events."""
+    state is read and written once per pass instead of once per step.  Two
+    input sets alternate; the state is restored and 512 MiB are written
+    before every call, outside the events."""
     import numpy as np
     from ssla_amd import _lib, synthetic
-    sb = synthetic.sparse_scan_bins()
-    site_all = np.concatenate(sb.sites)
-    order = np.argsort(site_all, kind="stable")
-    uniq, counts = np.unique(site_all[order], return_counts=True)
-    cu = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int64, device=dev)
-    sidx = torch.from_numpy(uniq.astype(np.int32)).to(dev)
-    perm = torch.from_numpy(order)
-    q, k, v, g = (torch.cat(xs)[perm].to(dev).contiguous() for xs in (sb.q, sb.k, sb.v, sb.g))
-    T, H, K = q.shape
-    V = v.shape[-1]
-    state0 = sb.state0.to(dev).contiguous()
-    state = state0.clone()
-    o = torch.empty(T, H, V, device=dev)
+    sets = []
+    for seed in (0, 1):
+        sb = synthetic.sparse_scan_bins(seed=seed)
+        site_all = np.concatenate(sb.sites)
+        order = np.argsort(site_all, kind="stable")
+        uniq, counts = np.unique(site_all[order], return_counts=True)
+        perm = torch.from_numpy(order)
+        x = dict(cu=torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int64, device=dev),
+                 sidx=torch.from_numpy(uniq.astype(np.int32)).to(dev), n=int(uniq.size), scale=float(sb.scale),
+                 state0=sb.state0.to(dev).contiguous())
+        for nm, xs in (("q", sb.q), ("k", sb.k), ("v", sb.v), ("g", sb.g)):
+            x[nm] = torch.cat(xs)[perm].to(dev).contiguous()
+        x["state"] = x["state0"].clone()
+        x["o"] = torch.empty_like(x["v"])
+        sets.append(x)
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
 
-    def call():
-        st = lib.ssla_gla_recurrent_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), _lib.SSLA_F32,
-                                        cu.data_ptr(), int(uniq.size), T, H, K, V, float(sb.scale), state.data_ptr(),
-                                        o.data_ptr(), state.data_ptr(), sidx.data_ptr(), int(state.shape[0]),
-                                        None, _lib.SSLA_F32, sh)
+    def call(x):
+        T, H, K = x["q"].shape
+        V = x["v"].shape[-1]
+        st = lib.ssla_gla_recurrent_fwd(x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
+                                        _lib.SSLA_F32, x["cu"].data_ptr(), x["n"], T, H, K, V, x["scale"],
+                                        x["state"].data_ptr(), x["o"].data_ptr(), x["state"].data_ptr(),
+                                        x["sidx"].data_ptr(), int(x["state"].shape[0]), None, _lib.SSLA_F32, sh)
         _lib.check(st, "ssla_gla_recurrent_fwd")
 
-    call()
+    for x in sets:
+        call(x)
     torch.cuda.synchronize()
     ms_tot = 0.0
-    for _ in range(reps):
-        state.copy_(state0)
+    for i in range(reps):
+        x = sets[i % 2]
+        x["state"].copy_(x["state0"])
+        _flush_mall(torch, dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        call()
+        call(x)
         e1.record(stream)
         torch.cuda.synchronize()
         ms_tot += e0.elapsed_time(e1)
     ms = ms_tot / reps
-    steps = T
-    alg = steps * 4 * (3 * H * K + 2 * H * V) + int(uniq.size) * 2 * H * K * V * 4
+    T, H, K = sets[0]["q"].shape
+    V = sets[0]["v"].shape[-1]
+    alg = T * 4 * (3 * H * K + 2 * H * V) + sets[0]["n"] * 2 * H * K * V * 4
     gbs = alg / (ms * 1e-3) / 1e9
     return {"workload": "sparse scan config 3, 64 bins in one call (per-site histories, state once per site)",
-            "metric": "sparse scan site-steps/s", "value": steps / (ms * 1e-3), "unit": "site-steps/s",
-            "ms_per_pass": ms, "site_steps_per_pass": steps, "active_sites": int(uniq.size),
+            "metric": "sparse scan site-steps/s", "value": T / (ms * 1e-3), "unit": "site-steps/s",
+            "ms_per_pass": ms, "site_steps_per_pass": T, "active_sites": sets[0]["n"],
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes": alg,
-                         "note": "q, k, g, v in and o out per step; the state of each active site in and out once"}}
+                         "note": "q, k, g, v in and o out per step; the state of each active site in and out "
+                                 "once; Infinity Cache flushed before every call"}}
+
+
+def cpu_pool(src, index, n_out):
+    """CPU leg of config 4: Tensor.scatter_reduce_('amax', include_self=False)
+    plus the first-index argmax pass (torch_scatter is not installed)."""
+    import torch
+    from oracle import torch_ref
+    torch.set_num_threads(_cpu_threads())
+    torch_ref.scatter_max(src[:10000], index[:10000], n_out)   # warm-up
+    med, ts = _median_time(lambda: torch_ref.scatter_max(src, index, n_out), 5)
+    return {"value": src.shape[0] / med, "unit": "events/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the whole config-4 call ({src.shape[0]} events x {src.shape[1]} channels, same index "
+                      f"order), torch fp32 scatter_reduce_ amax + first-index argmax; median of {len(ts)} runs "
+                      f"{[round(t, 3) for t in ts]} s", **_cpu_info()}
 
 
 def bench_pool(torch, lib, reps, dev, sorted_index=False):
     """Config 4: scatter_max of 1e6 clustered events (C=64) into 152x120
     cells; with sorted_index the events are first ordered by cell (the
-    non-decreasing segment ids SparsePool hands over), outside the timing."""
+    non-decreasing segment ids SparsePool hands over), outside the timing.
+    Two input sets (2 x 264 MB) alternate."""
     from ssla_amd import _lib, synthetic
     sets = []
+    cpu_in = None
     for seed in (0, 1):
         src, index, n_out = synthetic.pooling_events(seed=seed)
         if sorted_index:
             index, order = torch.sort(index, stable=True)
             src = src[order]
+        if cpu_in is None:
+            cpu_in = (src, index, n_out)
         sets.append(dict(src=src.to(dev), idx=index.to(dev)))
     E, C = sets[0]["src"].shape
     ws_bytes = lib.ssla_scatter_workspace_size(E, C, n_out)
@@ -269,7 +397,8 @@ def bench_pool(torch, lib, reps, dev, sorted_index=False):
             "ms_per_call": ms,
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes": alg,
-                         "note": "whole call (bucketing + reduce), not one kernel"}}
+                         "note": "whole call (bucketing + reduce), not one kernel"},
+            "cpu_baseline": cpu_pool(*cpu_in)}
 
 
 def bench_event_stage(torch, lib, reps, dev):
@@ -375,40 +504,166 @@ def bench_event_stage(torch, lib, reps, dev):
                          "note": "fp32 FMAs of the patch rows; the per-row weight choice keeps it off MFMA"}}
 
 
-def cpu_baseline(x, min_s=10.0):
-    """The fp64 C restatement of naive_gla_recurrent (oracle/) on this host,
-    run over the sequences of the same C2 batch, cycling through the batch
-    until at least min_s seconds of CPU work are done (one pass over the 8
-    sequences takes well under a second)."""
-    import numpy as np
-    import oracle
-    q = x["q"].float().cpu().numpy()
-    k = x["k"].float().cpu().numpy()
-    v = x["v"].float().cpu().numpy()
-    g = x["g"].cpu().numpy()
-    h0 = x["initial_state"].cpu().numpy()
-    cu = x["cu_seqlens"].cpu().numpy()
-    n_seq = len(cu) - 1
+def cpu_baseline(x):
+    """CPU leg of config 2: the fp32 PyTorch restatement of
+    naive_gla_recurrent (ops/gla/naive.py:50-111, per time step [H, K, V]
+    tensor ops) on this host's cores, over the 8 whole 4096-token sequences
+    of the same C2 batch, timed one sequence per run (the sequences are
+    independent, so the batch rate is the per-sequence rate): the median of
+    the 8 runs, after a warm-up on 64 tokens."""
+    import torch
+    from oracle import torch_ref
+    torch.set_num_threads(_cpu_threads())
+    q, k, v, g = (x[nm].float().cpu() for nm in ("q", "k", "v", "g"))
+    h0 = x["initial_state"].cpu()
+    cu = x["cu_seqlens"].cpu()
+    scale = float(x["scale"])
     H = q.shape[1]
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    oracle.load()
-    done_tok, t_used, runs = 0, 0.0, 0
-    while t_used < min_s:
-        n = runs % n_seq
+    torch_ref.naive_gla_recurrent(q[:64], k[:64], v[:64], g[:64], torch.tensor([0, 64]), scale, h0[:1], True)
+    runs = []
+    for n in range(len(cu) - 1):
         s, e = int(cu[n]), int(cu[n + 1])
         t0 = time.perf_counter()
-        oracle.gla_recurrent(q[s:e], k[s:e], v[s:e], g[s:e], np.array([0, e - s]), float(x["scale"]),
-                             h0[n:n + 1], True)
-        t_used += time.perf_counter() - t0
-        done_tok += e - s
-        runs += 1
-    rate = done_tok / t_used / 1e6
-    return {"value": rate, "unit": "Mtok/s", "cores": min(threads, H, os.cpu_count() or 1),
-            "kind": "port",
-            "sample": f"{runs} sequence runs ({runs / n_seq:.1f} passes over the 8 x 4096-token batch, "
-                      f"{done_tok} tokens x {H} heads) of naive_gla_recurrent's fp64 C restatement, "
-                      f"OpenMP over heads, {t_used:.1f} s",
-            "host_cpus": os.cpu_count()}
+        torch_ref.naive_gla_recurrent(q[s:e], k[s:e], v[s:e], g[s:e], torch.tensor([0, e - s]), scale,
+                                      h0[n:n + 1], True)
+        runs.append((time.perf_counter() - t0, e - s))
+    runs.sort()
+    t_med, tok = runs[len(runs) // 2]
+    return {"value": tok / t_med / 1e6, "unit": "Mtok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the {len(runs)} sequences of the C2 batch ({tok} tokens x {H} heads each), one run per "
+                      f"sequence, torch fp32 naive_gla_recurrent restatement; median {t_med:.2f} s of "
+                      f"{[round(r[0], 2) for r in runs]} s", **_cpu_info()}
+
+
+def bench_c1(torch, lib, reps, dev):
+    """Config 1 (plumbing): naive recurrent GLA forward, N=1, H=4, T=256,
+    K=V=32, fp32, q pre-scaled by 32^-1/2 and scale 1.0, zero initial state
+    (seed 0).  The reference runs this on the CPU: its wall time with the
+    host's threads is the baseline; the value is the same call through
+    naive_gla_recurrent on the GPU (HIP events, launch included)."""
+    import torch.nn.functional as F
+    from oracle import torch_ref
+    from ssla_amd.gla import naive_gla_recurrent
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(256, 4, 32, generator=gen) * 32 ** -0.5
+    k, v = torch.randn(256, 4, 32, generator=gen), torch.randn(256, 4, 32, generator=gen)
+    g = F.logsigmoid(torch.randn(256, 4, 32, generator=gen) / 16)
+    cu = torch.tensor([0, 256])
+    dq, dk, dv, dg, dcu = (t.to(dev) for t in (q, k, v, g, cu))
+    stream = torch.cuda.current_stream(dev)
+    with torch.no_grad():
+        for _ in range(3):
+            naive_gla_recurrent(dq, dk, dv, dg, dcu, 1.0, None, True)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            naive_gla_recurrent(dq, dk, dv, dg, dcu, 1.0, None, True)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    gpu_ms = e0.elapsed_time(e1) / reps
+    torch.set_num_threads(_cpu_threads())
+    torch_ref.naive_gla_recurrent(q[:16], k[:16], v[:16], g[:16], torch.tensor([0, 16]), 1.0, None, True)
+    med, ts = _median_time(lambda: torch_ref.naive_gla_recurrent(q, k, v, g, cu, 1.0, None, True), 5)
+    return {"workload": "naive_gla_recurrent config 1 (C1): N=1, H=4, T=256, K=V=32, fp32, scale 1.0",
+            "metric": "C1 recurrent GLA forward wall time", "value": gpu_ms, "unit": "ms",
+            "higher_is_better": False, "roofline": None,
+            "note": "plumbing configuration: 256 serial steps of a 4x32x32 state, no roofline binds; the GPU "
+                    "time is the wrapper call (device-to-device, one launch)",
+            "cpu_baseline": {"value": med * 1e3, "unit": "ms", "cores": torch.get_num_threads(), "kind": "port",
+                             "sample": f"the whole C1 call, torch fp32 naive_gla_recurrent restatement; median of "
+                                       f"{len(ts)} runs {[round(t * 1e3, 2) for t in ts]} ms", **_cpu_info()}}
+
+
+def cpu_async_step(model, window, n_events):
+    """CPU leg of config 5: the fp64 restatement of one window of the step
+    (oracle.backbone: numpy event glue, C recurrence, numpy projections and
+    head) on this host's cores, one window, one run (it takes seconds)."""
+    import numpy as np
+    import torch
+    from oracle import backbone as ob
+    torch.set_num_threads(_cpu_threads())
+    params = {k: v.detach().float().cpu().numpy() for k, v in model.state_dict().items()}
+    states = [np.zeros((Hg * Wg, model.heads, model.head_dim, model.head_dim), np.float32)
+              for Hg, Wg in model.grid_sizes]
+    ev = window.cpu().numpy()
+    t0 = time.perf_counter()
+    ob.async_step(params, ev, np.array([n_events]), states)
+    dt = time.perf_counter() - t0
+    return {"value": 1.0 / dt, "unit": "windows/s", "events_per_s": n_events / dt, "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"one {n_events}-event window of the step in the CPU restatement "
+                                      f"(oracle.backbone.async_step, fp64), {dt:.1f} s", **_cpu_info()}
+
+
+def bench_async_step(torch, lib, dev, n_windows=20, n_events=50_000, cpu=True):
+    """Config 5: the asynchronous forward step (ssla_amd.backbone) over
+    n_windows consecutive windows of n_events events, per-stage states
+    carried from window to window; raw <x, y, t, p> windows resident on the
+    device before the timing.  value = windows/s over the whole timed run
+    (host wall clock, synchronised); a second, instrumented pass over the
+    same windows (fresh states) times each piece with HIP events, and the
+    per-site scan of every stage is priced against HBM."""
+    from ssla_amd import synthetic
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(0)
+    model = AsyncSparseGLA().to(dev).eval()
+    wins = [w.to(dev) for w in synthetic.async_windows(n_windows, n_events, seed=0)]
+    ln = torch.tensor([n_events], device=dev)
+    stream = torch.cuda.current_stream(dev)
+    with torch.no_grad():
+        warm = model.init_states(1, dev)
+        for w in wins[:2]:
+            model(w, ln, warm)
+        states = model.init_states(1, dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for w in wins:
+            model(w, ln, states)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        # instrumented pass: per-piece HIP events
+        states = model.init_states(1, dev)
+        piece_ms, scan_bytes, scan_ms = {}, [0] * 4, [0.0] * 4
+        for w in wins:
+            marks = [("start", torch.cuda.Event(enable_timing=True))]
+            marks[0][1].record(stream)
+
+            def mark(name):
+                e = torch.cuda.Event(enable_timing=True)
+                e.record(stream)
+                marks.append((name, e))
+
+            _, feats = model(w, ln, states, mark=mark)
+            torch.cuda.synchronize()
+            interval = {nm: a.elapsed_time(b) for (_, a), (nm, b) in zip(marks[:-1], marks[1:])}
+            for nm, ms in interval.items():
+                piece_ms[nm] = piece_ms.get(nm, 0.0) + ms / n_windows
+            hd = model.heads * model.head_dim
+            for i, f in enumerate(feats):
+                n_ev, n_site = int(f["events"].shape[0]), int(f["lengths"].numel())
+                scan_bytes[i] += n_ev * (3 * hd * 2 + hd * 4 + hd * 2) + n_site * 2 * hd * model.head_dim * 4
+                scan_ms[i] += interval[f"s{i}.scan"]
+    per_window_ms = wall * 1e3 / n_windows
+    scans = []
+    for i in range(4):
+        gbs = scan_bytes[i] / (scan_ms[i] * 1e-3) / 1e9
+        scans.append({"stage": i + 1, "ms_per_window": scan_ms[i] / n_windows,
+                      "algorithmic_bytes_per_window": scan_bytes[i] // n_windows, "achieved": gbs,
+                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS})
+    line = {"workload": f"async forward step (config 5): {n_windows} windows x {n_events} events, 4 stages "
+                        "32/64/128/256 ch at stride 4/8/16/32, H=4, D=32, per-site fp32 states carried, "
+                        "bf16 projections and head",
+            "metric": "async step windows/s", "value": n_windows / wall, "unit": "windows/s",
+            "events_per_s": n_windows * n_events / wall, "ms_per_window": per_window_ms,
+            "ms_per_piece": piece_ms, "scan_kernels": scans,
+            "roofline": {"bound": "hbm", "kernel": "ssla_gla_recurrent_fwd with state_idx (per-site scan), "
+                                                   "stage 1", **{k: scans[0][k] for k in
+                                                                 ("achieved", "peak", "unit", "frac")},
+                         "note": "per stage: bf16 q/k/v, fp32 g, bf16 o per event plus each active site's "
+                                 "fp32 state in and out; the step as a whole is launch/glue-bound"}}
+    if cpu:
+        line["cpu_baseline"] = cpu_async_step(model, wins[0], n_events)
+    return line
 
 
 def calibrate_copy(torch, dev, mib=256, reps=3):
@@ -480,8 +735,10 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", choices=["chunk", "sparse", "sparse_batched", "pool", "pool_sorted", "chunk_bwd", "event_stage"], default=None,
-                    help="run one workload and print its line (profiling runs)")
+    ap.add_argument("--only", choices=["chunk", "c1", "sparse", "sparse_batched", "pool", "pool_sorted", "chunk_bwd",
+                                       "event_stage", "async_step"], default=None,
+                    help="run one workload and print its line (profiling runs; --no-cpu-baseline skips "
+                         "the CPU legs where a line has one)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 256 MiB device copies (counter calibration) and exit")
     args = ap.parse_args(argv)
@@ -499,6 +756,12 @@ def main(argv=None):
         calibrate_copy(torch, dev)
         return 0
     lib = _lib.load()
+    if args.only == "c1":
+        print(json.dumps(bench_c1(torch, lib, args.steps, dev)), flush=True)
+        return 0
+    if args.only == "async_step":
+        print(json.dumps(bench_async_step(torch, lib, dev, cpu=not args.no_cpu_baseline)), flush=True)
+        return 0
     if args.only == "sparse":
         print(json.dumps(bench_sparse(torch, lib, args.steps, dev)), flush=True)
         return 0
@@ -520,7 +783,7 @@ def main(argv=None):
     kern_s = r["kernel_avg_ms"] * 1e-3
     alg_bytes = c2_bytes()
     achieved = alg_bytes / kern_s / 1e9
-    traffic = _traffic_from_profile("gla_chunk_fwd_c2_pmc.txt")
+    traffic, traffic_note = _traffic_from_profile("gla_chunk_fwd_c2_pmc.txt", "ssla_amd/csrc/gla_chunk.hip")
     tflops = c2_flops() / kern_s / 1e12
     line = {
         "metric": "GLA chunk fwd Mtok/s (%bf16 MFMA peak); sparse scan site-steps/s (%HBM BW)",
@@ -531,7 +794,7 @@ def main(argv=None):
                                "bf16 q/k/v/o, fp32 g/h0/ht; 2 input sets alternating (> MALL)",
                    "global_batch": C2["B"], "seq_len": C2["T"], "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_note,
                      "kernel": "ssla_gla_chunk_fwd (state + segment kernels, one call)",
                      "kernel_avg_us": r["kernel_avg_ms"] * 1e3,
                      "algorithmic_bytes": alg_bytes},
@@ -540,10 +803,11 @@ def main(argv=None):
                  "note": "causal-useful flops; the shape is HBM-bound (31.8 flop/B < 312 ridge)"},
     }
     if not args.no_secondary and args.only is None:
-        line["secondary"] = [bench_sparse(torch, lib, 10, dev), bench_sparse_batched(torch, lib, 10, dev),
-                             bench_pool(torch, lib, 20, dev),
-                             bench_pool(torch, lib, 20, dev, sorted_index=True), bench_chunk_bwd(torch, lib, 10, dev),
-                             bench_event_stage(torch, lib, 5, dev)]
+        line["secondary"] = [bench_c1(torch, lib, 20, dev), bench_sparse(torch, lib, 10, dev),
+                             bench_sparse_batched(torch, lib, 10, dev), bench_pool(torch, lib, 20, dev),
+                             bench_pool(torch, lib, 20, dev, sorted_index=True),
+                             bench_async_step(torch, lib, dev, cpu=not args.no_cpu_baseline),
+                             bench_chunk_bwd(torch, lib, 10, dev), bench_event_stage(torch, lib, 5, dev)]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(r["sample"])
     print(json.dumps(line), flush=True)

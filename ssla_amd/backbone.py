@@ -106,15 +106,23 @@ class SiteGLABlock(nn.Module):
         return ((inputs["batch_id"] * Hg + inputs["h"]) * Wg + inputs["w"]).to(torch.int32)
 
     def forward(self, inputs: Dict[str, torch.Tensor], state: torch.Tensor, grid_size: Sequence[int],
-                check: bool = False) -> Dict[str, torch.Tensor]:
+                check: bool = False, mark=None) -> Dict[str, torch.Tensor]:
+        """``mark(name)`` (optional) is called after each piece: "project",
+        "scan", "finish" (a timing hook; it must not touch the tensors)."""
         x = inputs["events"].to(torch.float32)
         lengths = inputs["lengths"]
         cu = F.pad(torch.cumsum(lengths, 0), (1, 0))
         q, k, v, g = self.project(x)
+        if mark:
+            mark("project")
         o = sparse_gla_scan(q, k, v, g, cu, self.sites(inputs, grid_size), state,
                             scale=self.head_dim ** -0.5, check=check)
+        if mark:
+            mark("scan")
         out = dict(inputs)
         out["events"] = self.finish(o, x)
+        if mark:
+            mark("finish")
         return out
 
 
@@ -204,14 +212,26 @@ class AsyncSparseGLA(nn.Module):
         gr["events"] = F.linear(gr["events"].to(torch.bfloat16), self.embed.weight.to(torch.bfloat16)).float()
         return self.stem_pool(gr)
 
-    def forward(self, events: torch.Tensor, lengths: torch.Tensor, states: List[torch.Tensor]):
+    def forward(self, events: torch.Tensor, lengths: torch.Tensor, states: List[torch.Tensor], mark=None):
+        """``mark(name)`` (optional) is called after each piece ("stem",
+        "s<i>.project" / ".scan" / ".finish" / ".pool", "grids", "head"): a
+        timing hook that must not touch the tensors."""
         x = self.stem(events, lengths)
+        if mark:
+            mark("stem")
         feats = []
         for i, blk in enumerate(self.blocks):
-            x = blk(x, states[i], self.grid_sizes[i])
+            x = blk(x, states[i], self.grid_sizes[i], mark=(lambda nm, i=i: mark(f"s{i}.{nm}")) if mark else None)
             feats.append(x)
             if i < len(self.pools):
                 x = self.pools[i](x)
+                if mark:
+                    mark(f"s{i}.pool")
         grids = [E.events_to_grid(feats[i], self.grid_sizes[i], self.stages[i][0]).to(torch.bfloat16)
                  for i in self.head_levels]
-        return self.head(grids), feats
+        if mark:
+            mark("grids")
+        out = self.head(grids)
+        if mark:
+            mark("head")
+        return out, feats
