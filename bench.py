@@ -203,7 +203,7 @@ def cpu_sparse(sb, n_bins=64, runs=5):
             **_cpu_info()}
 
 
-def bench_sparse(torch, lib, reps, dev, sets=None):
+def bench_sparse(torch, lib, reps, dev, sets=None, cpu=True):
     """Config 3: 64 bins of per-site GLA updates, bin by bin (one
     ssla_sparse_gla_step launch per bin).  Two independent input sets
     alternate and 512 MiB are written between passes (outside the timing),
@@ -269,7 +269,7 @@ def bench_sparse(torch, lib, reps, dev, sets=None):
             "graph": {"value": steps / (ms_graph * 1e-3), "ms_per_pass": ms_graph, "achieved": gbs_graph,
                       "frac": gbs_graph / HBM_PEAK_GBS,
                       "note": "the 64 launches captured once as a HIP graph and replayed"},
-            "cpu_baseline": cpu_sparse(sets[0]["sb"])}
+            **({"cpu_baseline": cpu_sparse(sets[0]["sb"])} if cpu else {})}
 
 
 def bench_sparse_batched(torch, lib, reps, dev):
@@ -350,7 +350,7 @@ def cpu_pool(src, index, n_out):
                       f"{[round(t, 3) for t in ts]} s", **_cpu_info()}
 
 
-def bench_pool(torch, lib, reps, dev, sorted_index=False):
+def bench_pool(torch, lib, reps, dev, sorted_index=False, cpu=True):
     """Config 4: scatter_max of 1e6 clustered events (C=64) into 152x120
     cells; with sorted_index the events are first ordered by cell (the
     non-decreasing segment ids SparsePool hands over), outside the timing.
@@ -398,7 +398,7 @@ def bench_pool(torch, lib, reps, dev, sorted_index=False):
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "algorithmic_bytes": alg,
                          "note": "whole call (bucketing + reduce), not one kernel"},
-            "cpu_baseline": cpu_pool(*cpu_in)}
+            **({"cpu_baseline": cpu_pool(*cpu_in)} if cpu else {})}
 
 
 def bench_event_stage(torch, lib, reps, dev):
@@ -763,7 +763,7 @@ def main(argv=None):
         print(json.dumps(bench_async_step(torch, lib, dev, cpu=not args.no_cpu_baseline)), flush=True)
         return 0
     if args.only == "sparse":
-        print(json.dumps(bench_sparse(torch, lib, args.steps, dev)), flush=True)
+        print(json.dumps(bench_sparse(torch, lib, args.steps, dev, cpu=not args.no_cpu_baseline)), flush=True)
         return 0
     if args.only == "chunk_bwd":
         print(json.dumps(bench_chunk_bwd(torch, lib, args.steps, dev)), flush=True)
@@ -775,7 +775,8 @@ def main(argv=None):
         print(json.dumps(bench_event_stage(torch, lib, args.steps, dev)), flush=True)
         return 0
     if args.only in ("pool", "pool_sorted"):
-        print(json.dumps(bench_pool(torch, lib, args.steps, dev, args.only == "pool_sorted")), flush=True)
+        print(json.dumps(bench_pool(torch, lib, args.steps, dev, args.only == "pool_sorted",
+                                    cpu=not args.no_cpu_baseline)), flush=True)
         return 0
     r = bench_chunk(torch, lib, args.steps, args.warmup, dev)
     ms_step = r["wall_s"] * 1e3 / args.steps
