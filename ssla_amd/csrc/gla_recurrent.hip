@@ -30,62 +30,111 @@ __device__ __forceinline__ void skip_sequence(void *o, int64_t bos, int64_t eos,
   if (status && lane == 0) __hip_atomic_store(status, SSLA_ERR_ARG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// KPL consecutive elements of a row from index i into fp32: 16-byte loads
-// for fp32, 8-byte loads for 16-bit types (i a multiple of KPL >= 4, base
-// 16-byte aligned: checked by the host before this path is chosen).
+// ------------------------------------------------------- staged kernel --
+// Each wavefront owns one (sequence, head, 16-column V tile); its lanes are
+// 4 key groups x 16 value columns, each lane holding KPL = K/4 fp32 state
+// rows.  The wavefront walks its sequence in blocks of kSB steps: a
+// block's q, k, g rows (this head) and v tile are fetched with 16-byte
+// buffer loads into registers while the previous block is being computed,
+// then parked in a wave-private LDS buffer, from which every step reads its
+// KPL keys (the 16 lanes of a key group read the same address: one
+// broadcast).  A sequence of n steps therefore waits on about n / kSB
+// memory round trips instead of n.  The decays exp(g) of a block are
+// computed once per (step, key) while the block is parked (fp32 in LDS),
+// not once per value column, and the output scale is applied once to the
+// reduced dot product.  Rows past the sequence end fall outside the block's
+// buffer resources and read as zeros (decay 1 and k = 0 leave the state
+// unchanged), and their outputs are not stored.
+constexpr int kSB = 16;   // steps per staged block
+
+template <int DT, int GDT, int KPL>
+struct Staged {
+  static constexpr int K = 4 * KPL;
+  static constexpr int ES = DT == SSLA_F32 ? 4 : 2;    // bytes per q/k/v element
+  static constexpr int GS = GDT == SSLA_F32 ? 4 : 2;   // bytes per g element
+  static constexpr int QB = K * ES, GB = K * GS, VB = kBV * ES;   // row bytes (v: one tile)
+  static constexpr int PQ = kSB * QB / 16, PG = kSB * GB / 16, PV = kSB * VB / 16;   // 16-byte pieces
+  static constexpr int NQ = (PQ + 63) / 64, NG = (PG + 63) / 64, NV = (PV + 63) / 64;
+  static constexpr int DB = K * 4;            // bytes of a row of fp32 decays
+  static constexpr int OQ = 0, OK = kSB * QB, OD = 2 * kSB * QB, OV = 2 * kSB * QB + kSB * DB;
+  static constexpr int BYTES = OV + kSB * VB;   // LDS per wavefront
+};
+
+constexpr uint32_t kNoRow = 0x80000000u;   // an offset past every resource: reads zeros
+constexpr int kRawRsrc = 0x00020000;        // raw 32-bit data, range checked
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void *base, int64_t bytes) {
+  bytes = min(bytes, static_cast<int64_t>(0x7ffffff0));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), kRawRsrc);
+}
+
+// N (4, 8 or 16) consecutive elements of type DT at byte address p of LDS.
 template <int DT, int N>
-__device__ __forceinline__ void load_run(const void *p, int64_t i, float (&x)[N]) {
-  static_assert(N % 4 == 0, "runs of whole 4-element pieces");
+__device__ __forceinline__ void lds_run(const unsigned char *p, float (&x)[N]) {
   if constexpr (DT == SSLA_F32) {
-    const float4 *s = reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
 #pragma unroll
     for (int j = 0; j < N / 4; ++j) {
-      const float4 t = s[j];
-      x[4 * j] = t.x;
-      x[4 * j + 1] = t.y;
-      x[4 * j + 2] = t.z;
-      x[4 * j + 3] = t.w;
+      const float4 t = *reinterpret_cast<const float4 *>(p + 16 * j);
+      x[4 * j] = t.x; x[4 * j + 1] = t.y; x[4 * j + 2] = t.z; x[4 * j + 3] = t.w;
     }
   } else {
-    const uint2 *s = reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(p) + i);
 #pragma unroll
     for (int j = 0; j < N / 4; ++j) {
-      const uint2 u = s[j];
+      const uint2 u = *reinterpret_cast<const uint2 *>(p + 8 * j);
       const uint16_t e[4] = {static_cast<uint16_t>(u.x), static_cast<uint16_t>(u.x >> 16),
                              static_cast<uint16_t>(u.y), static_cast<uint16_t>(u.y >> 16)};
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        x[4 * j + c] = DT == SSLA_BF16 ? bf16_bits_to_f32(e[c]) : f16_bits_to_f32(e[c]);
+      for (int c = 0; c < 4; ++c) x[4 * j + c] = DT == SSLA_BF16 ? bf16_bits_to_f32(e[c]) : f16_bits_to_f32(e[c]);
     }
   }
 }
 
-// Same recurrence for K == 4 * KPL with aligned rows: each lane's KPL keys
-// are one contiguous run, loaded with vector loads, and the next step's
-// q, k, g, v are in flight while the current step is computed.
+template <int DT>
+__device__ __forceinline__ float lds_elem(const unsigned char *p) {
+  if constexpr (DT == SSLA_F32) return *reinterpret_cast<const float *>(p);
+  else {
+    const uint16_t b = *reinterpret_cast<const uint16_t *>(p);
+    return DT == SSLA_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+  }
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <int DT, int GDT, int KPL>
-__global__ __launch_bounds__(256) void gla_recurrent_vec_kernel(
+__global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
     const void *__restrict__ q, const void *__restrict__ k,
     const void *__restrict__ v, const void *__restrict__ g,
-    const int64_t *__restrict__ cu_seqlens, int n_seq, int H, int K, int V,
+    const int64_t *__restrict__ cu_seqlens, int n_seq, int H, int V,
     float scale, const float *__restrict__ h0, void *__restrict__ o,
     float *__restrict__ ht, const int32_t *__restrict__ state_idx, int n_state_rows,
     int64_t T, int32_t *__restrict__ status) {
+  typedef Staged<DT, GDT, KPL> G;
+  constexpr int K = G::K;
+  constexpr int U = 2;   // steps per group (kSB is a multiple)
+  __shared__ __align__(16) unsigned char smem[4][G::BYTES];
   const int lane = threadIdx.x & 63;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int wv = threadIdx.x >> 6;
+  unsigned char *lds = smem[wv];
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wv;
   const int n_vt = (V + kBV - 1) / kBV;
-  if (item >= static_cast<int64_t>(n_seq) * H * n_vt) return;  // whole wavefront exits
+  if (item >= static_cast<int64_t>(n_seq) * H * n_vt) return;  // whole wavefront exits (no workgroup barrier)
   const int vt = static_cast<int>(item % n_vt);
   const int h = static_cast<int>((item / n_vt) % H);
   const int n = static_cast<int>(item / (static_cast<int64_t>(n_vt) * H));
   const int col = vt * kBV + (lane & 15);
-  const int k0 = (lane >> 4) * KPL;
+  const int kg = lane >> 4;
+  const int k0 = kg * KPL;
   const bool col_ok = col < V;
   const int64_t bos = min(max(cu_seqlens[n], (int64_t)0), T);
   const int64_t eos = min(max(cu_seqlens[n + 1], bos), T);
   const int64_t srow = state_idx ? static_cast<int64_t>(state_idx[n]) : n;
   if (bad_state_row(state_idx, n, srow, n_state_rows)) {
-    skip_sequence<DT>(o, bos, eos, H, h, V, col, (lane >> 4) == 0 && col_ok, lane, status);
+    skip_sequence<DT>(o, bos, eos, H, h, V, col, kg == 0 && col_ok, lane, status);
     return;
   }
 
@@ -93,35 +142,127 @@ __global__ __launch_bounds__(256) void gla_recurrent_vec_kernel(
 #pragma unroll
   for (int i = 0; i < KPL; ++i) S[i] = (h0 && col_ok) ? h0[((srow * H + h) * K + k0 + i) * V + col] : 0.f;
 
-  typedef Elem<DT> E;
-  float qc[KPL], kc[KPL], gc[KPL], vc = 0.f;
-  auto fetch = [&](int64_t t, float (&qx)[KPL], float (&kx)[KPL], float (&gx)[KPL], float &vx) {
-    const int64_t base = (t * H + h) * K + k0;
-    load_run<DT, KPL>(q, base, qx);
-    load_run<DT, KPL>(k, base, kx);
-    load_run<GDT, KPL>(g, base, gx);
-    vx = col_ok ? E::load(v, (t * H + h) * V + col) : 0.f;
+  // this lane's pieces of a block: piece p = lane + 64 j of each array
+  uint4 rq[G::NQ], rk[G::NQ], rg[G::NG], rv[G::NV];
+  auto issue = [&](int64_t t0) __attribute__((always_inline)) {
+    const int64_t rows = eos - t0;
+    const char *qb = static_cast<const char *>(q) + t0 * H * G::QB;
+    const char *kb = static_cast<const char *>(k) + t0 * H * G::QB;
+    const char *gb = static_cast<const char *>(g) + t0 * H * G::GB;
+    const char *vb = static_cast<const char *>(v) + t0 * H * static_cast<int64_t>(V) * G::ES;
+    const auto rsq = rows_rsrc(qb, rows * H * G::QB), rsk = rows_rsrc(kb, rows * H * G::QB);
+    const auto rsg = rows_rsrc(gb, rows * H * G::GB);
+    const auto rsv = rows_rsrc(vb, rows * H * static_cast<int64_t>(V) * G::ES);
+#pragma unroll
+    for (int j = 0; j < G::NQ; ++j) {
+      const int p = lane + 64 * j;
+      const int st = p / (G::QB / 16), c = p % (G::QB / 16);
+      const uint32_t off = p < G::PQ ? static_cast<uint32_t>((st * H + h) * G::QB + 16 * c) : kNoRow;
+      rq[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsq, off, 0, 0));
+      rk[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, off, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < G::NG; ++j) {
+      const int p = lane + 64 * j;
+      const int st = p / (G::GB / 16), c = p % (G::GB / 16);
+      const uint32_t off = p < G::PG ? static_cast<uint32_t>((st * H + h) * G::GB + 16 * c) : kNoRow;
+      rg[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsg, off, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < G::NV; ++j) {
+      const int p = lane + 64 * j;
+      const int st = p / (G::VB / 16), c = p % (G::VB / 16);
+      const uint32_t off = p < G::PV ? static_cast<uint32_t>((static_cast<int64_t>(st) * H + h) * V * G::ES +
+                                                             vt * G::VB + 16 * c)
+                                     : kNoRow;
+      rv[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0));
+    }
   };
-  if (bos < eos) fetch(bos, qc, kc, gc, vc);
-  for (int64_t t = bos; t < eos; ++t) {
-    float qn[KPL], kn[KPL], gn[KPL], vn = 0.f;
-    if (t + 1 < eos) fetch(t + 1, qn, kn, gn, vn);
-    float acc = 0.f;
+  auto park = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      S[i] = fmaf(fast_exp2(gc[i] * kLog2e), S[i], kc[i] * vc);
-      acc = fmaf(qc[i] * scale, S[i], acc);
+    for (int j = 0; j < G::NQ; ++j) {
+      const int p = lane + 64 * j;
+      if (p < G::PQ) {
+        *reinterpret_cast<uint4 *>(lds + G::OQ + 16 * p) = rq[j];
+        *reinterpret_cast<uint4 *>(lds + G::OK + 16 * p) = rk[j];
+      }
     }
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
-    if ((lane >> 4) == 0 && col_ok) E::store(o, (t * H + h) * V + col, acc);
+    // decays of the block's gates: piece p holds 16 / GS gates, i.e.
+    // 64 / GS bytes of fp32 decays at the same position of the decay rows
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      qc[i] = qn[i];
-      kc[i] = kn[i];
-      gc[i] = gn[i];
+    for (int j = 0; j < G::NG; ++j) {
+      const int p = lane + 64 * j;
+      if (p < G::PG) {
+        if constexpr (GDT == SSLA_F32) {
+          const float4 x = __builtin_bit_cast(float4, rg[j]);
+          *reinterpret_cast<float4 *>(lds + G::OD + 16 * p) =
+              make_float4(fast_exp2(x.x * kLog2e), fast_exp2(x.y * kLog2e), fast_exp2(x.z * kLog2e),
+                          fast_exp2(x.w * kLog2e));
+        } else {
+          const uint32_t w[4] = {rg[j].x, rg[j].y, rg[j].z, rg[j].w};
+          float dd[8];
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const uint16_t b = static_cast<uint16_t>(w[c >> 1] >> (16 * (c & 1)));
+            dd[c] = fast_exp2((GDT == SSLA_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b)) * kLog2e);
+          }
+          *reinterpret_cast<float4 *>(lds + G::OD + 32 * p) = make_float4(dd[0], dd[1], dd[2], dd[3]);
+          *reinterpret_cast<float4 *>(lds + G::OD + 32 * p + 16) = make_float4(dd[4], dd[5], dd[6], dd[7]);
+        }
+      }
     }
-    vc = vn;
+#pragma unroll
+    for (int j = 0; j < G::NV; ++j) {
+      const int p = lane + 64 * j;
+      if (p < G::PV) *reinterpret_cast<uint4 *>(lds + G::OV + 16 * p) = rv[j];
+    }
+  };
+
+  typedef Elem<DT> E;
+  const int64_t nblk = (eos - bos + kSB - 1) / kSB;
+  if (nblk > 0) issue(bos);
+  for (int64_t b = 0; b < nblk; ++b) {
+    const int64_t t0 = bos + b * kSB;
+    wave_lds_sync();   // the previous block's reads are done
+    park();
+    wave_lds_sync();
+    if (b + 1 < nblk) issue(t0 + kSB);
+    const int ns = static_cast<int>(min(static_cast<int64_t>(kSB), eos - t0));
+    // Steps in groups of U: the k v products of the group first
+    // (independent of the state), then the U state updates (the only
+    // dependency carried from step to step is one fma per state element),
+    // then the U cross-lane reductions together.  Steps of the group past
+    // the sequence end read the zero rows (no change) and store nothing.
+    for (int s0 = 0; s0 < ns; s0 += U) {
+      float d[U][KPL], kv[U][KPL], qs[U][KPL];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int st = s0 + u;
+        lds_run<DT, KPL>(lds + G::OQ + st * G::QB + k0 * G::ES, qs[u]);
+        lds_run<DT, KPL>(lds + G::OK + st * G::QB + k0 * G::ES, kv[u]);
+        lds_run<SSLA_F32, KPL>(lds + G::OD + st * G::DB + k0 * 4, d[u]);
+        const float vc = lds_elem<DT>(lds + G::OV + st * G::VB + (lane & 15) * G::ES);
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) kv[u][i] *= vc;
+      }
+      float acc[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        acc[u] = 0.f;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) {
+          S[i] = fmaf(d[u][i], S[i], kv[u][i]);
+          acc[u] = fmaf(qs[u][i], S[i], acc[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[u] += __shfl_xor(acc[u], 16);
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[u] += __shfl_xor(acc[u], 32);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (kg == 0 && col_ok && s0 + u < ns) E::store(o, ((t0 + s0 + u) * H + h) * V + col, acc[u] * scale);
+    }
   }
   if (ht && col_ok) {
 #pragma unroll
@@ -215,20 +356,22 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
   }
   dim3 grid(static_cast<unsigned>(blocks)), block(64 * waves_per_block);
   const int kpl_needed = (K + kKG - 1) / kKG;
-  // vector path: every lane's run of keys is whole (K = 4 KPL), aligned, and
-  // short enough to double-buffer in registers (K <= 64)
-  const bool vec = (K % 16 == 0) && al16(q) && al16(k) && al16(g) && K <= 64;
-  if (vec) {
-#define SSLA_RECV(KPL_)                                                                        \
-  hipLaunchKernelGGL((gla_recurrent_vec_kernel<DT, GDT, KPL_>), grid, block, 0, st, q, k, v, g, \
-                     cu, n_seq, H, K, V, scale, h0, o, ht, sidx, n_rows, T, status)
+  // staged path: every lane's run of keys is whole (K = 4 KPL <= 64), and
+  // q/k/g rows and the v rows are whole 16-byte pieces at 16-byte aligned
+  // addresses
+  const int es = DT == SSLA_F32 ? 4 : 2;
+  const bool staged = (K % 16 == 0) && K <= 64 && (V * es) % 16 == 0 && al16(q) && al16(k) && al16(g) && al16(v);
+  if (staged) {
+#define SSLA_RECS(KPL_)                                                                          \
+  hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_>), grid, block, 0, st, q, k, v, g, \
+                     cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status)
     switch (K / kKG) {
-      case 4: SSLA_RECV(4); return launch_status("gla_recurrent_fwd");
-      case 8: SSLA_RECV(8); return launch_status("gla_recurrent_fwd");
-      case 16: SSLA_RECV(16); return launch_status("gla_recurrent_fwd");
+      case 4: SSLA_RECS(4); return launch_status("gla_recurrent_fwd");
+      case 8: SSLA_RECS(8); return launch_status("gla_recurrent_fwd");
+      case 16: SSLA_RECS(16); return launch_status("gla_recurrent_fwd");
       default: break;   // other K: the general kernel
     }
-#undef SSLA_RECV
+#undef SSLA_RECS
   }
 #define SSLA_REC(KPL_)                                                                     \
   hipLaunchKernelGGL((gla_recurrent_kernel<DT, GDT, KPL_>), grid, block, 0, st, q, k, v, g, \
