@@ -14,13 +14,20 @@
 // * Each (sequence, head, V group) chain is cut into P segments of whole
 //   chunks (P chosen so that about two workgroups run per CU).
 // * state pass  : segments 0..P-2 run the state recurrence only (reads k, g,
-//   v) from h0 (segment 0) or zero, leaving the segment's final state (in
-//   bf16, as the reference keeps its per-chunk states) and total log2-decay
-//   D in a workspace slot.
+//   v) from h0 (segment 0) or zero, leaving the segment's final state and
+//   total log2-decay D in a workspace slot.  The state is stored as a bf16
+//   pair: hi = bf16(S) and lo = bf16(S - hi), so hi + lo holds S to about
+//   2^-17.
 // * segment pass: every segment first folds the slots of the segments before
 //   it into its entering state (E = slot 0, E = 2^D(j) E + slot j for
 //   0 < j < s), then runs the full chunk loop from it and writes o (and ht
-//   for the last segment).
+//   for the last segment).  The fold uses the hi halves: the entering state
+//   reaches o through a product in the input dtype, as the reference's
+//   per-chunk states do (bf16 at states_in_fp32=False).  The last segment,
+//   whose final state becomes ht, adds the fold of the lo halves at the end,
+//   decayed through its own chunks (the fold is linear, so
+//   ht = S(fold(hi)) + decay * fold(lo)): ht carries fp32-level accuracy
+//   across segments without delaying the segment's first chunk.
 //
 // Inside a workgroup (256 threads, 4 wavefronts): wavefront I owns chunk
 // rows 16I..16I+15 ("block" I) and state rows (keys) 16I..16I+15 as MFMA
@@ -48,6 +55,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 // Scratch of ssla_gla_chunk_fwd_noalloc: a fixed device array (one copy per
 // GPU, zero-filled when the code object loads, held until the process
@@ -424,7 +432,8 @@ struct ChunkArgs {
   const float *h0;
   uint16_t *o;
   float *ht;
-  const uint16_t *ws_state;  // [n_seq, H, P] slots of K*V bf16 in slot_index order: local end state of segment s
+  const uint16_t *ws_state;  // [n_seq, H, P] slots of K*V bf16 in slot_index order: local end state of segment s (hi)
+  const uint16_t *ws_lo;     // the same slots: bf16(S - hi)
   const float *ws_decay;   // [n_seq, H, P, K] fp32: total log2 decay of segment s
   int64_t bos;             // first row of the sequence
   int64_t len;             // rows of the sequence
@@ -438,6 +447,50 @@ __device__ __forceinline__ void segment_range(int nch, int P, int seg, int &c0, 
   const int per = (nch + P - 1) / P;
   c0 = min(seg * per, nch);
   c1 = min(c0 + per, nch);
+}
+
+// E = slot 0, E = 2^D(j) E + slot j for 0 < j < a.seg (in this order, so
+// every segment gets the same bits), over this lane's values of the hi
+// halves (LO = false) or the lo halves (LO = true).  Slots and decays are
+// loaded eight at a time, so up to 8 segments take one round trip.
+template <int NVT, bool LO>
+__device__ __forceinline__ void fold_slots(const struct ChunkArgs &a, int64_t sl0, const float *dk, f32x4 (&S)[NVT]) {
+  const uint16_t *base = LO ? a.ws_lo : a.ws_state;
+  for (int j0 = 0; j0 < a.seg; j0 += 8) {
+    uint2 xb[8][NVT];
+    f32x4 d[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (j0 + u < a.seg) {
+        const int64_t so = sl0 + static_cast<int64_t>(j0 + u) * KD * a.V;
+        d[u] = *reinterpret_cast<const f32x4 *>(dk + static_cast<int64_t>(j0 + u) * KD);
+#pragma unroll
+        for (int t = 0; t < NVT; ++t) xb[u][t] = *reinterpret_cast<const uint2 *>(base + so + 4 * t);
+      }
+    }
+    float x[8][NVT][4];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int t = 0; t < NVT; ++t) unpack_bf16x4(xb[u][t], x[u][t]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + u;
+      if (j == 0) {
+#pragma unroll
+        for (int t = 0; t < NVT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) S[t][i] = x[u][t][i];
+      } else if (j < a.seg) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float f = fast_exp2(clamp_exp(d[u][i]));
+#pragma unroll
+          for (int t = 0; t < NVT; ++t) S[t][i] = fmaf(f, S[t][i], x[u][t][i]);
+        }
+      }
+    }
+  }
 }
 
 // --------------------------------------------------------- segment pass --
@@ -477,7 +530,8 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
     // entering state: h0 for segment 0, else the fold of the earlier
     // segments' slots, E = slot 0, E = 2^D(j) E + slot j for 0 < j < seg (in
     // this order, so every segment gets the same bits); slots and decays are
-    // loaded eight at a time, so up to 8 segments take one round trip
+    // loaded in batches (8, or 4 with the lo halves), so up to 8 segments
+    // take one or two round trips
     const int64_t chain = static_cast<int64_t>(a.n) * H + h;
     const int64_t eo = static_cast<int64_t>(krow) * V + v0 + r;   // this lane's element (i = 0, t = 0)
     if (a.seg == 0) {
@@ -487,43 +541,9 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
 #pragma unroll
         for (int i = 0; i < 4; ++i) S[t][i] = src ? src[eo + static_cast<int64_t>(i) * V + 16 * t] : 0.f;
     } else {
-      const uint16_t *slots = a.ws_state + chain * a.P * KD * V + slot_index<NVT>(a.v0, wv, lane);
+      const int64_t sl0 = chain * a.P * KD * V + slot_index<NVT>(a.v0, wv, lane);
       const float *dk = a.ws_decay + chain * a.P * KD + krow;
-      for (int j0 = 0; j0 < a.seg; j0 += 8) {
-        uint2 xb[8][NVT];
-        f32x4 d[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (j0 + u < a.seg) {
-            const uint16_t *sl = slots + static_cast<int64_t>(j0 + u) * KD * V;
-            d[u] = *reinterpret_cast<const f32x4 *>(dk + static_cast<int64_t>(j0 + u) * KD);
-#pragma unroll
-            for (int t = 0; t < NVT; ++t) xb[u][t] = *reinterpret_cast<const uint2 *>(sl + 4 * t);
-          }
-        }
-        float x[8][NVT][4];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-#pragma unroll
-          for (int t = 0; t < NVT; ++t) unpack_bf16x4(xb[u][t], x[u][t]);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int j = j0 + u;
-          if (j == 0) {
-#pragma unroll
-            for (int t = 0; t < NVT; ++t)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) S[t][i] = x[u][t][i];
-          } else if (j < a.seg) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float f = fast_exp2(clamp_exp(d[u][i]));
-#pragma unroll
-              for (int t = 0; t < NVT; ++t) S[t][i] = fmaf(f, S[t][i], x[u][t][i]);
-            }
-          }
-        }
-      }
+      fold_slots<NVT, false>(a, sl0, dk, S);
     }
   }
   // Wait here for the entering state (and the first chunk, needed next
@@ -536,6 +556,7 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
   // so no copy is made and the wait at each chunk covers only the loads of
   // that chunk, not the o stores issued after them.
   SegRegs buf2;
+  f32x4 dec_prod = {1.f, 1.f, 1.f, 1.f};   // decay of this lane's state rows over the segment
   auto chunk_step = [&](SegRegs &cur, SegRegs &nxt, const int c) __attribute__((always_inline)) {
     const uint32_t orow = ov;   // o row of this lane in this chunk (same layout as v)
 
@@ -685,6 +706,7 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
       const f32x4 sdec = *reinterpret_cast<const f32x4 *>(&sm.fac[wv][kFacDec][krow]);
       const MV ka0 = tr_operand<MV>(sm.kh, 8 * gq, 8 * gq + 4, 16 * wv, lane);
       const MV ka1 = tr_operand<MV>(sm.kh, 32 + 8 * gq, 32 + 8 * gq + 4, 16 * wv, lane);
+      dec_prod *= sdec;
 #pragma unroll
       for (int t = 0; t < NVT; ++t) {
         S[t] *= sdec;
@@ -702,6 +724,18 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
 
   // ---- final state of the sequence -----------------------------------------
   if (a.seg == a.P - 1 && a.ht) {
+    if (a.seg > 0) {
+      // the lo halves of the earlier segments' states, folded as the hi
+      // halves were and carried through this segment's decay
+      const int64_t chain = static_cast<int64_t>(a.n) * H + h;
+      f32x4 lo[NVT];
+      fold_slots<NVT, true>(a, chain * a.P * KD * V + slot_index<NVT>(a.v0, wv, lane),
+                            a.ws_decay + chain * a.P * KD + krow, lo);
+#pragma unroll
+      for (int t = 0; t < NVT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S[t][i] = fmaf(dec_prod[i], lo[t][i], S[t][i]);
+    }
 #pragma unroll
     for (int t = 0; t < NVT; ++t)
 #pragma unroll
@@ -715,7 +749,7 @@ __global__ __launch_bounds__(256, SSLA_GC_SEG_WAVES) void gla_chunk_segment_kern
     const uint16_t *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int64_t T, int H, int V, float scale,
     const float *__restrict__ h0, uint16_t *__restrict__ o, float *__restrict__ ht, int P,
-    const uint16_t *__restrict__ ws_state, const float *__restrict__ ws_decay) {
+    const uint16_t *__restrict__ ws_state, const uint16_t *__restrict__ ws_lo, const float *__restrict__ ws_decay) {
   __shared__ SmemA sm;
   const int nvg = V / (16 * NVT);
   // block -> (sequence, head, V group, segment); the segments of one
@@ -731,6 +765,7 @@ __global__ __launch_bounds__(256, SSLA_GC_SEG_WAVES) void gla_chunk_segment_kern
   a.n = static_cast<int>(b / H);
   a.q = q; a.k = k; a.v = v; a.g = g; a.h0 = h0; a.o = o; a.ht = ht;
   a.ws_state = ws_state;
+  a.ws_lo = ws_lo;
   a.ws_decay = ws_decay;
   a.H = H; a.V = V; a.scale = scale;
   a.v0 = vg * 16 * NVT;
@@ -758,7 +793,8 @@ template <int DT, bool GF32, int NVT>
 __global__ __launch_bounds__(256, SSLA_GC_STATE_WAVES) void gla_chunk_state_kernel(
     const uint16_t *__restrict__ k, const uint16_t *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int64_t T, int H, int V,
-    const float *__restrict__ h0, int P, uint16_t *__restrict__ ws_state, float *__restrict__ ws_decay) {
+    const float *__restrict__ h0, int P, uint16_t *__restrict__ ws_state, uint16_t *__restrict__ ws_lo,
+    float *__restrict__ ws_decay) {
   typedef Mfma<DT> M;
   typedef typename M::Vec MV;
   __shared__ SmemS sm;
@@ -870,12 +906,15 @@ __global__ __launch_bounds__(256, SSLA_GC_STATE_WAVES) void gla_chunk_state_kern
   if (c < c_end) chunk_step(buf, buf2, c);
 
   const int64_t slot = (static_cast<int64_t>(n) * H + h) * P + seg;
-  uint16_t *dst = ws_state + slot * KD * V + slot_index<NVT>(v0, wv, lane);
+  const int64_t so = slot * KD * V + slot_index<NVT>(v0, wv, lane);
 #pragma unroll
   for (int t = 0; t < NVT; ++t) {
     const f32x8 s8 = {S[t][0], S[t][1], S[t][2], S[t][3], 0.f, 0.f, 0.f, 0.f};
-    const uint4 bits = to_bits(QK::cvt(s8));
-    *reinterpret_cast<uint2 *>(dst + 4 * t) = make_uint2(bits.x, bits.y);
+    const bf16x8 hi = QK::cvt(s8);
+    const uint4 bits = to_bits(hi);
+    const uint4 lbits = to_bits(QK::cvt(s8 - QK::widen(hi)));   // S - hi is exact in fp32
+    *reinterpret_cast<uint2 *>(ws_state + so + 4 * t) = make_uint2(bits.x, bits.y);
+    *reinterpret_cast<uint2 *>(ws_lo + so + 4 * t) = make_uint2(lbits.x, lbits.y);
   }
   if (wv == 0 && v0 == 0) ws_decay[slot * KD + lane] = dsum;
 }
@@ -909,13 +948,13 @@ inline int pick_segments(int n_seq, int64_t T, int H, int V) {
 inline size_t workspace_bytes_for(int n_seq, int H, int V, int P) {
   if (P <= 1) return 0;
   const size_t slots = static_cast<size_t>(n_seq) * H * P;
-  return slots * KD * V * sizeof(uint16_t) + slots * KD * sizeof(float);
+  return 2 * slots * KD * V * sizeof(uint16_t) + slots * KD * sizeof(float);   // hi, lo, decays
 }
 
 template <int DT, bool GF32, int NVT>
 int launch_nvt(const void *q, const void *k, const void *v, const void *g, const int64_t *cu, int n_seq,
                int64_t T, int H, int V, float scale, const float *h0, void *o, float *ht, int P,
-               uint16_t *ws_state, float *ws_decay, hipStream_t st) {
+               uint16_t *ws_state, uint16_t *ws_lo, float *ws_decay, hipStream_t st) {
   const int nvg = V / (16 * NVT);
   const int64_t blocks_a = static_cast<int64_t>(n_seq) * H * nvg * P;
   if (blocks_a > 0x7fffffff) {
@@ -928,24 +967,24 @@ int launch_nvt(const void *q, const void *k, const void *v, const void *g, const
     const int64_t blocks_s = static_cast<int64_t>(n_seq) * H * nvg * (P - 1);
     hipLaunchKernelGGL((gla_chunk_state_kernel<DT, GF32, NVT>), dim3(static_cast<unsigned>(blocks_s)),
                        dim3(256), 0, st, static_cast<const uint16_t *>(k), static_cast<const uint16_t *>(v),
-                       g, cu, n_seq, T, H, V, h0, P, ws_state, ws_decay);
+                       g, cu, n_seq, T, H, V, h0, P, ws_state, ws_lo, ws_decay);
   }
   hipLaunchKernelGGL((gla_chunk_segment_kernel<DT, GF32, NVT>), dim3(static_cast<unsigned>(blocks_a)),
                      dim3(256), 0, st, q16, static_cast<const uint16_t *>(k),
                      static_cast<const uint16_t *>(v), g, cu, n_seq, T, H, V, scale, h0, o16, ht, P,
-                     ws_state, ws_decay);
+                     ws_state, ws_lo, ws_decay);
   return launch_status("gla_chunk_fwd");
 }
 
 template <int DT, bool GF32>
 int launch_chunk(const void *q, const void *k, const void *v, const void *g, const int64_t *cu, int n_seq,
                  int64_t T, int H, int V, float scale, const float *h0, void *o, float *ht, int P,
-                 uint16_t *ws_state, float *ws_decay, hipStream_t st) {
+                 uint16_t *ws_state, uint16_t *ws_lo, float *ws_decay, hipStream_t st) {
   switch (pick_nvt(V)) {
-    case 4: return launch_nvt<DT, GF32, 4>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
-    case 3: return launch_nvt<DT, GF32, 3>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
-    case 2: return launch_nvt<DT, GF32, 2>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
-    default: return launch_nvt<DT, GF32, 1>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
+    case 4: return launch_nvt<DT, GF32, 4>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_lo, ws_decay, st);
+    case 3: return launch_nvt<DT, GF32, 3>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_lo, ws_decay, st);
+    case 2: return launch_nvt<DT, GF32, 2>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_lo, ws_decay, st);
+    default: return launch_nvt<DT, GF32, 1>(q, k, v, g, cu, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_lo, ws_decay, st);
   }
 }
 
@@ -997,15 +1036,17 @@ extern "C" int ssla_gla_chunk_fwd(const void *q, const void *k, const void *v, c
   }
   SSLA_CHECK_ARG(need == 0 || aligned(workspace, 16), "gla_chunk_fwd: workspace must be 16-byte aligned");
   uint16_t *ws_state = static_cast<uint16_t *>(workspace);
-  // slots are K*V*2 bytes (a multiple of 2048), so the decays stay 16-byte aligned
-  float *ws_decay = need ? reinterpret_cast<float *>(ws_state + static_cast<size_t>(n_seq) * H * P * KD * V) : nullptr;
+  // slots are K*V*2 bytes (a multiple of 2048), so lo and the decays stay 16-byte aligned
+  const size_t slot_elems = static_cast<size_t>(n_seq) * H * P * KD * V;
+  uint16_t *ws_lo = need ? ws_state + slot_elems : nullptr;
+  float *ws_decay = need ? reinterpret_cast<float *>(ws_state + 2 * slot_elems) : nullptr;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool gf32 = g_dtype == SSLA_F32;
   if (dtype == SSLA_BF16)
-    return gf32 ? launch_chunk<SSLA_BF16, true>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st)
-                : launch_chunk<SSLA_BF16, false>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
-  return gf32 ? launch_chunk<SSLA_F16, true>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st)
-              : launch_chunk<SSLA_F16, false>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_decay, st);
+    return gf32 ? launch_chunk<SSLA_BF16, true>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_lo, ws_decay, st)
+                : launch_chunk<SSLA_BF16, false>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_lo, ws_decay, st);
+  return gf32 ? launch_chunk<SSLA_F16, true>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_lo, ws_decay, st)
+              : launch_chunk<SSLA_F16, false>(q, k, v, g, cu_seqlens, n_seq, T, H, V, scale, h0, o, ht, P, ws_state, ws_lo, ws_decay, st);
 }
 
 namespace ssla {

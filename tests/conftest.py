@@ -22,28 +22,40 @@ def dev():
     return torch.device("cuda:0")
 
 
-def assert_close(actual, ref, rtol, name="", atol_scale=None, ratio_mode=False):
-    """Elementwise |a - b| <= rtol * |b| + atol with atol = rtol * rms(ref)
-    (a bare rtol is ill-posed near zero), plus RMSE/RMS(ref) <= rtol.
+def assert_close(actual, ref, rtol, name="", atol_scale=None, band=None, ratio_max=None):
+    """Elementwise |a - b| <= rtol * |b| + atol, and RMSE / RMS(ref) <= ratio_max.
 
-    ratio_mode (bf16/fp16 GLA outputs): the bar is the reference's own
-    error ratio RMSE/RMS(ref) <= rtol (get_err_ratio, reference
-    utils/ela_utils.py:67-70), with every element still inside
-    rtol * |b| + 10 * rtol * rms(ref) -- bf16 operand rounding puts a few
-    elements of a 16M-element output several sigma out, as it does for the
-    reference's own bf16 path."""
+    atol = band * rms(ref) when `band` is given, else `atol_scale`, else
+    rtol * rms(ref) (a bare rtol is ill-posed near zero); ratio_max defaults
+    to rtol.  The bf16/fp16 GLA checks pass `band` and `ratio_max`: both are
+    at most twice the error measured for that check on the MI355X (the
+    measured values, and how they arise, are listed in DESIGN.md), well
+    inside the north star's bf16 bar (rtol 2e-2 on the reference's error
+    ratio, get_err_ratio, utils/ela_utils.py:67-70).  With SSLA_PARITY_LOG
+    set, every check appends its measured RMS ratio and worst error to that
+    file."""
     a = np.asarray(actual, dtype=np.float64)
     b = np.asarray(ref, dtype=np.float64)
     assert a.shape == b.shape, f"{name}: shape {a.shape} != {b.shape}"
     assert np.isfinite(a).all(), f"{name}: non-finite values"
     rms = float(np.sqrt(np.mean(b * b))) if b.size else 0.0
-    atol = rtol * rms if atol_scale is None else atol_scale
-    if ratio_mode:
-        atol = 10 * rtol * rms
+    if band is not None:
+        atol = band * rms
+    else:
+        atol = rtol * rms if atol_scale is None else atol_scale
+    if ratio_max is None:
+        ratio_max = rtol
     err = np.abs(a - b)
     bad = err > rtol * np.abs(b) + atol
     ratio = float(np.sqrt(np.mean(err * err)) / (rms + 1e-30)) if b.size else 0.0
+    log = os.environ.get("SSLA_PARITY_LOG")
+    if log:
+        import json
+        with open(log, "a") as f:
+            f.write(json.dumps({"name": name, "n": int(b.size), "rms_ratio": ratio,
+                                "worst_over_rms": float(err.max() / (rms + 1e-30)) if b.size else 0.0,
+                                "rtol": rtol, "band": band, "ratio_max": ratio_max}) + "\n")
     assert not bad.any(), (f"{name}: {int(bad.sum())}/{bad.size} elements outside rtol={rtol} "
                            f"atol={atol:.3g}; max err {err.max():.3g}, rms ratio {ratio:.3g}")
-    assert ratio <= rtol, f"{name}: RMSE/RMS {ratio:.3g} > {rtol}"
+    assert ratio <= ratio_max, f"{name}: RMSE/RMS {ratio:.3g} > {ratio_max}"
     return ratio

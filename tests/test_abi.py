@@ -71,14 +71,14 @@ def test_workspace_size_monotone():
 
 def test_chunk_forward_workspace_layout():
     """The chunk forward's workspace holds, per (sequence, head, segment), a
-    K x V bf16 state and K fp32 decays; C2 (8 sequences of 4096 tokens,
+    K x V state as a bf16 (hi, lo) pair and K fp32 decays; C2 (8 sequences of 4096 tokens,
     8 heads) runs 8 segments per sequence, and with V = 128 (two 64-column
     groups, twice the chains) 4.  One sequence of one chunk needs no
     workspace, and unsupported shapes report 0."""
     from ssla_amd import _lib
     lib = _lib.load()
-    assert lib.ssla_gla_chunk_workspace_size(8, 8 * 4096, 8, 64, 64) == 8 * 8 * 8 * (64 * 64 * 2 + 64 * 4)
-    assert lib.ssla_gla_chunk_workspace_size(8, 8 * 4096, 8, 64, 128) == 8 * 8 * 4 * (64 * 128 * 2 + 64 * 4)
+    assert lib.ssla_gla_chunk_workspace_size(8, 8 * 4096, 8, 64, 64) == 8 * 8 * 8 * (2 * 64 * 64 * 2 + 64 * 4)
+    assert lib.ssla_gla_chunk_workspace_size(8, 8 * 4096, 8, 64, 128) == 8 * 8 * 4 * (2 * 64 * 128 * 2 + 64 * 4)
     assert lib.ssla_gla_chunk_workspace_size(1, 64, 8, 64, 64) == 0
     assert lib.ssla_gla_chunk_workspace_size(1, 4096, 8, 32, 64) == 0
     assert lib.ssla_gla_chunk_workspace_size(1, 4096, 8, 64, 40) == 0

@@ -8,12 +8,13 @@ difference is pinned to the piece that made it:
   selects, it does not round);
 * bf16 projections within bf16 rounding: RMS error ratio <= 2e-3 and every
   element within 2 bf16 ulps (2^-7 relative) plus 2e-3 of the RMS;
-* the per-site recurrence on the GPU's q, k, v, g: o (rounded to bf16) at
-  the north star's bf16 bar (RMS ratio <= 2e-2), the fp32 states of the
+* the per-site recurrence on the GPU's q, k, v, g: o (rounded to bf16)
+  within twice its measured error (RMS ratio 3.3e-3 against the north
+  star's 2e-2, every element within 0.12 of the RMS), the fp32 states of the
   active sites at 1e-4, the states of every inactive site unchanged bit
   for bit;
-* LayerNorm outputs and the bf16 detection head within bf16 rounding of
-  their inputs (ratio <= 2e-2).
+* LayerNorm outputs and the bf16 detection head within twice their
+  measured errors (RMS ratios 5e-5 and 3.5e-3).
 The whole ``forward`` equals the piecewise run bit for bit (the kernels are
 deterministic)."""
 import numpy as np
@@ -94,13 +95,13 @@ def _window_piecewise(model, ev, ln, states, params, dev, check_oracle=True, tag
             ref_state = before.cpu().numpy()
             ro = ob.block_scan(_np(q), _np(k), _np(v), _np(g), _np(x["lengths"]).astype(np.int64),
                                _np(sites).astype(np.int64), ref_state, blk.head_dim ** -0.5)
-            assert_close(_np(o), ro, 2e-2, f"stage {i} o{tag}", ratio_mode=True)
+            assert_close(_np(o), ro, 0.0, f"stage {i} o{tag}", band=0.12, ratio_max=3.3e-3)
             act = np.unique(_np(sites).astype(np.int64))
             inact = torch.from_numpy(np.setdiff1d(np.arange(states[i].shape[0]), act)).to(dev)
             assert torch.equal(states[i][inact], before[inact]), f"stage {i}: inactive states changed{tag}"
             assert_close(states[i].cpu().numpy()[act], ref_state[act], 1e-4, f"stage {i} states{tag}")
             ry = ob.block_finish(p, _np(o).astype(np.float64), xn)
-            assert_close(_np(y), ry, 2e-2, f"stage {i} out{tag}", ratio_mode=True)
+            assert_close(_np(y), ry, 0.0, f"stage {i} out{tag}", band=0.033, ratio_max=5e-5)
         feats.append(out)
         if i < len(model.pools):
             with torch.no_grad():
@@ -119,7 +120,7 @@ def _window_piecewise(model, ev, ln, states, params, dev, check_oracle=True, tag
             assert np.array_equal(_np(grids[lvl]), rg), f"grid {lvl}{tag}"
         hp = {k[5:]: v for k, v in params.items() if k.startswith("head.")}
         rh = ob.head(hp, [_np(gg) for gg in grids], [model.stages[i][1] for i in model.head_levels])
-        assert_close(_np(out), rh, 2e-2, f"head{tag}", ratio_mode=True)
+        assert_close(_np(out), rh, 0.0, f"head{tag}", band=0.024, ratio_max=3.5e-3)
     return out, feats
 
 

@@ -1,9 +1,13 @@
 """GPU parity: chunked and recurrent GLA forward (HIP, via the C-ABI) vs the
 fp64 CPU oracle (restating reference ops/gla/naive.py:50-111).
 
-Tolerances (north star): bf16 inputs with fp32 accumulation rtol 2e-2,
-fp32 inputs rtol 1e-4, both with atol = rtol * rms(reference) -- see
-tests/conftest.assert_close.
+Tolerances: fp32 paths rtol 1e-4 with atol = rtol * rms(reference) (north
+star).  The bf16 / fp16 chunk outputs are held to bands measured on the
+MI355X: every element within `band * rms`, and RMSE / RMS within
+`ratio_max`, each at most twice the measured value of that check (the
+north star's bf16 bar is an RMS ratio of 2e-2; the measured ratios are
+2-4e-3 for o).  ht is fp32: its error is the bf16 rounding of the decayed
+k operand of the state product, as in the reference's chunk_fwd_h.
 """
 import numpy as np
 import pytest
@@ -18,6 +22,10 @@ pytestmark = pytest.mark.gpu
 RTOL_BF16 = 2e-2
 RTOL_F16 = 1e-2
 RTOL_F32 = 1e-4
+
+# (band, ratio_max) of the chunk forward per gate regime, <= 2x measured
+O_BANDS = {"logsig": (0.085, 6.5e-3), "randn-1": (0.23, 6.5e-3), "strong": (0.14, 6.5e-3), "zero": (0.044, 4.5e-3)}
+HT_BANDS = {"logsig": (0.023, 1.4e-3), "randn-1": (0.27, 3e-3), "strong": (2.7e-4, 1.3e-5), "zero": (3.2e-6, 1.2e-7)}
 
 
 def _inputs(lens, H, K, V, dtype, seed=0, gate="logsig", h0=True, qscale=None):
@@ -93,20 +101,23 @@ def test_chunk_varlen(dev, V, gate):
     q, k, v, g, cu, s0 = _inputs(lens, 3, 64, V, torch.bfloat16, seed=V, gate=gate)
     o, ht = _run(chunk_gla, q, k, v, g, cu, s0, 64 ** -0.5, dev)
     ro, rht = _oracle(q, k, v, g, cu, s0, 64 ** -0.5)
-    assert_close(o, ro, RTOL_BF16, f"o[{gate}]", ratio_mode=True)
-    assert_close(ht, rht, RTOL_BF16, f"ht[{gate}]", ratio_mode=True)
+    assert_close(o, ro, 0.0, f"o[{gate}]", band=O_BANDS[gate][0], ratio_max=O_BANDS[gate][1])
+    assert_close(ht, rht, 0.0, f"ht[{gate}]", band=HT_BANDS[gate][0], ratio_max=HT_BANDS[gate][1])
 
 
 def test_chunk_fp16_and_bf16_gates(dev):
     from ssla_amd.gla import chunk_gla
     lens = [100, 300]
-    for dtype, rtol in ((torch.float16, RTOL_F16), (torch.bfloat16, RTOL_BF16)):
+    # (o band, o ratio, ht band, ht ratio), <= 2x measured
+    bands = {torch.float16: (0.045, 4.5e-3, 2.3e-3, 2.1e-4), torch.bfloat16: (0.074, 6.5e-3, 0.021, 1.7e-3)}
+    for dtype in (torch.float16, torch.bfloat16):
         q, k, v, g, cu, s0 = _inputs(lens, 2, 64, 64, dtype, seed=3)
         g_lp = g.to(dtype)           # g in the input dtype
         o, ht = _run(chunk_gla, q, k, v, g_lp, cu, s0, 0.125, dev)
         ro, rht = _oracle(q, k, v, g_lp.float(), cu, s0, 0.125)
-        assert_close(o, ro, rtol, f"o[{dtype}]", ratio_mode=True)
-        assert_close(ht, rht, rtol, f"ht[{dtype}]", ratio_mode=True)
+        ob, orat, hb, hrat = bands[dtype]
+        assert_close(o, ro, 0.0, f"o[{dtype}]", band=ob, ratio_max=orat)
+        assert_close(ht, rht, 0.0, f"ht[{dtype}]", band=hb, ratio_max=hrat)
 
 
 def test_chunk_no_initial_state_no_final(dev):
@@ -116,7 +127,7 @@ def test_chunk_no_initial_state_no_final(dev):
         o, ht = chunk_gla(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev))
     assert ht is None
     ro, _ = _oracle(q, k, v, g, cu, None, 64 ** -0.5)
-    assert_close(o.float().cpu().numpy(), ro, RTOL_BF16, "o", ratio_mode=True)
+    assert_close(o.float().cpu().numpy(), ro, 0.0, "o", band=0.056, ratio_max=6.5e-3)
 
 
 def test_chunk_matches_recurrent_kernel(dev):
@@ -125,8 +136,8 @@ def test_chunk_matches_recurrent_kernel(dev):
     q, k, v, g, cu, s0 = _inputs([500, 12, 333], 4, 64, 64, torch.bfloat16, seed=9)
     o1, h1 = _run(chunk_gla, q, k, v, g, cu, s0, 0.125, dev)
     o2, h2 = _run(fused_recurrent_gla, q, k, v, g, cu, s0, 0.125, dev)
-    assert_close(o1, o2, RTOL_BF16, "o", ratio_mode=True)
-    assert_close(h1, h2, RTOL_BF16, "ht", ratio_mode=True)
+    assert_close(o1, o2, 0.0, "o", band=0.1, ratio_max=7e-3)
+    assert_close(h1, h2, 0.0, "ht", band=0.022, ratio_max=1.7e-3)
 
 
 def test_chunk_c2_full(dev):
@@ -143,8 +154,8 @@ def test_chunk_c2_full(dev):
     ro, rht = oracle.gla_recurrent(x["q"].float().numpy(), x["k"].float().numpy(),
                                    x["v"].float().numpy(), x["g"].numpy(), x["cu_seqlens"].numpy(),
                                    x["scale"], x["initial_state"].numpy(), True)
-    assert_close(o.float().cpu().numpy(), ro, RTOL_BF16, "o", ratio_mode=True)
-    assert_close(ht.cpu().numpy(), rht, RTOL_BF16, "ht")
+    assert_close(o.float().cpu().numpy(), ro, 0.0, "o", band=0.12, ratio_max=6.5e-3)
+    assert_close(ht.cpu().numpy(), rht, 0.0, "ht", band=0.025, ratio_max=1.6e-3)
 
 
 def test_chunk_repeatable(dev):

@@ -2,10 +2,11 @@
 ssla_gla_chunk_bwd) vs the fp64 CPU oracle of the recurrent backward
 (oracle.gla_recurrent_bwd, pinned against torch autograd in
 tests/test_oracle.py).  The products run as split bf16 triples with fp32
-accumulation and the gradients are rounded to the input dtype at the end;
-the bar is the error ratio RMSE / RMS(reference) <= 1e-2, half the
-reference's own 2e-2 bar for bf16 outputs (measured: dq, dk, dv 0.17 %,
-which is bf16 output rounding; dg <= 0.7 % with gates below -5)."""
+accumulation and the gradients are rounded to the input dtype at the end.
+Each gradient of each case is held to twice its measured error on the
+MI355X: every element within `band * rms` and RMSE / RMS within
+`ratio_max` (measured: dq, dk, dv 0.17 %, which is bf16 output rounding;
+dg <= 0.7 % with gates below -5; the north star's bar for bf16 is 2e-2)."""
 import numpy as np
 import pytest
 import torch
@@ -15,7 +16,28 @@ import oracle
 from tests.conftest import assert_close
 
 pytestmark = pytest.mark.gpu
-RTOL = 1e-2
+
+# (band, ratio_max) per case and gradient, <= 2x measured (dg of the
+# strong-gate case keeps the earlier 1e-2 ratio bound, 1.5x measured)
+_B16 = {"dq": (0.053, 3.3e-3), "dk": (0.051, 3.3e-3), "dv": (0.05, 3.3e-3), "dg": (1.1e-3, 1e-4), "dh0": (1.1e-4, 4e-6)}
+BANDS = {
+    "logsig": _B16,
+    "randn-1": {"dq": (0.31, 3.4e-3), "dk": (0.45, 3.4e-3), "dv": (0.24, 3.3e-3), "dg": (3.4e-3, 7e-5),
+                "dh0": (3.3e-4, 4.9e-6)},
+    "strong": {"dq": (0.059, 3.3e-3), "dk": (0.059, 3.3e-3), "dv": (0.059, 3.3e-3), "dg": (0.127, 1e-2),
+               "dh0": (2.1e-6, 6.8e-8)},
+    "zero": {"dq": (0.041, 3.3e-3), "dk": (0.041, 3.3e-3), "dv": (0.03, 3.3e-3), "dg": (3.4e-5, 4.4e-6),
+             "dh0": (2.5e-6, 1.3e-7)},
+    "no h0": {"dq": (0.027, 3.3e-3), "dk": (0.046, 3.3e-3), "dv": (0.027, 3.3e-3), "dg": (4.4e-4, 8.7e-5)},
+    "fp16": {"dq": (6.9e-3, 4.2e-4), "dk": (6.7e-3, 4.2e-4), "dv": (3.3e-3, 4e-4), "dg": (6.4e-4, 9.3e-5),
+             "dh0": (9.3e-5, 6.3e-6)},
+    "long": {"dq": (0.053, 3.3e-3), "dk": (0.054, 3.3e-3), "dv": (0.053, 3.3e-3), "dg": (9.4e-4, 1e-4),
+             "dh0": (6e-5, 5e-6)},
+    "16-bit g bf16": {"dq": (0.11, 3.2e-3), "dk": (0.22, 3.4e-3), "dv": (0.099, 3.4e-3), "dg": (0.14, 3.1e-3),
+                      "dh0": (2.4e-4, 4.8e-6)},
+    "16-bit g fp16": {"dq": (0.02, 4.3e-4), "dk": (0.016, 4.1e-4), "dv": (8.4e-3, 4.2e-4), "dg": (0.016, 3.8e-4),
+                      "dh0": (3.6e-4, 6.8e-6)},
+}
 
 
 def _inputs(lens, H, V, dtype, seed, gate="logsig", h0=True):
@@ -52,18 +74,20 @@ def _gpu_grads(dev, q, k, v, g, cu, s0, do, dht, scale):
     return out
 
 
-def _check(dev, lens, H, V, dtype, seed, gate="logsig", h0=True, scale=64 ** -0.5, tag=""):
+def _check(dev, lens, H, V, dtype, seed, gate="logsig", h0=True, scale=64 ** -0.5, tag="", case=None):
     q, k, v, g, cu, s0, do, dht = _inputs(lens, H, V, dtype, seed, gate, h0)
     print(f"gla bwd {tag}: lens={lens} H={H} V={V} {dtype} gate={gate} h0={h0}", flush=True)
     got = _gpu_grads(dev, q, k, v, g, cu, s0, do, dht, scale)
     ref = oracle.gla_recurrent_bwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), g.numpy(), cu.numpy(),
                                    do.float().numpy(), scale, None if s0 is None else s0.numpy(),
                                    None if dht is None else dht.numpy())
+    bands = BANDS[case or gate]
     for name, a, b in zip(("dq", "dk", "dv", "dg", "dh0"), got, ref):
         if b is None:
             assert a is None
             continue
-        assert_close(a, b, RTOL, f"{name}[{tag}]", ratio_mode=True)
+        band, ratio_max = bands[name]
+        assert_close(a, b, 0.0, f"{name}[{tag}]", band=band, ratio_max=ratio_max)
 
 
 @pytest.mark.parametrize("V", [16, 32, 48, 64])
@@ -75,14 +99,14 @@ def test_chunk_bwd_varlen(dev, V, gate):
 
 
 def test_chunk_bwd_no_state_and_fp16(dev):
-    _check(dev, [150, 90], 2, 64, torch.bfloat16, seed=3, h0=False, tag="no h0")
-    _check(dev, [150, 90], 2, 64, torch.float16, seed=4, tag="fp16")
+    _check(dev, [150, 90], 2, 64, torch.bfloat16, seed=3, h0=False, tag="no h0", case="no h0")
+    _check(dev, [150, 90], 2, 64, torch.float16, seed=4, tag="fp16", case="fp16")
 
 
 def test_chunk_bwd_long_sequences(dev):
     """Two 4096-token sequences (64 chunks each), H = 4: the state passes
     carry 64 chunks."""
-    _check(dev, [4096, 4096], 4, 64, torch.bfloat16, seed=5, tag="long")
+    _check(dev, [4096, 4096], 4, 64, torch.bfloat16, seed=5, tag="long", case="long")
 
 
 def test_chunk_bwd_unsupported_raises(dev):
@@ -103,8 +127,10 @@ def test_chunk_bwd_16bit_gates(dev, dtype):
     got = _gpu_grads(dev, q, k, v, g16, cu, s0, do, dht, 64 ** -0.5)
     ref = oracle.gla_recurrent_bwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), g16.float().numpy(),
                                    cu.numpy(), do.float().numpy(), 64 ** -0.5, s0.numpy(), dht.numpy())
+    bands = BANDS["16-bit g bf16" if dtype == torch.bfloat16 else "16-bit g fp16"]
     for name, a, b in zip(("dq", "dk", "dv", "dg", "dh0"), got, ref):
-        assert_close(a, b, RTOL, f"{name}[16-bit g {dtype}]", ratio_mode=True)
+        band, ratio_max = bands[name]
+        assert_close(a, b, 0.0, f"{name}[16-bit g {dtype}]", band=band, ratio_max=ratio_max)
 
 
 def test_chunk_bwd_all_sequences_empty(dev):
