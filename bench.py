@@ -305,7 +305,8 @@ def bench_sparse_batched(torch, lib, reps, dev):
         st = lib.ssla_gla_recurrent_fwd(x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
                                         _lib.SSLA_F32, x["cu"].data_ptr(), x["n"], T, H, K, V, x["scale"],
                                         x["state"].data_ptr(), x["o"].data_ptr(), x["state"].data_ptr(),
-                                        x["sidx"].data_ptr(), int(x["state"].shape[0]), None, _lib.SSLA_F32, sh)
+                                        x["sidx"].data_ptr(), int(x["state"].shape[0]), None, _lib.SSLA_F32, None,
+                                        0, sh)
         _lib.check(st, "ssla_gla_recurrent_fwd")
 
     for x in sets:

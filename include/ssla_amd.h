@@ -146,14 +146,25 @@ int ssla_gla_chunk_bwd(const void *q, const void *k, const void *v,
  * int32, may be NULL; see ssla_status_read).  This is the batched form of
  * the per-site sparse GLA step over many time bins.
  * Sequences are clamped to [0, T) on the device, so a malformed cu_seqlens
- * cannot address memory outside the tensors. */
+ * cannot address memory outside the tensors.
+ *
+ * workspace (optional; NULL, 0 for none): with ssla_gla_recurrent_workspace_size
+ * bytes (16-byte aligned, no initialisation needed) long sequences are cut
+ * into 128-step segments that run in parallel -- a pass that leaves each
+ * segment's local end state and decay, then one that folds them into every
+ * segment's entering state (fp32 throughout) -- instead of one wavefront
+ * walking the whole sequence.  The size query returns 0 for shapes where
+ * the single pass is as fast (sequences shorter than 32 steps on average)
+ * or not available (K not a multiple of 16 up to 64); then pass NULL, 0. */
+size_t ssla_gla_recurrent_workspace_size(int n_seq, int64_t T, int H, int K, int V);
 int ssla_gla_recurrent_fwd(const void *q, const void *k, const void *v,
                            const void *g, int g_dtype,
                            const int64_t *cu_seqlens, int n_seq, int64_t T,
                            int H, int K, int V, float scale,
                            const float *h0, void *o, float *ht,
                            const int32_t *state_idx, int n_state_rows,
-                           int32_t *status, int dtype, void *stream);
+                           int32_t *status, int dtype, void *workspace,
+                           size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------------
  * G2 -- sparse sequential scans.

@@ -39,8 +39,9 @@ SIGNATURES = {
     "ssla_gla_chunk_bwd_workspace_size": (_sz, [_i32, _i64, _i32, _i32, _i32]),
     "ssla_gla_chunk_bwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32, _f32, _vp,
                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
+    "ssla_gla_recurrent_workspace_size": (_sz, [_i32, _i64, _i32, _i32, _i32]),
     "ssla_gla_recurrent_fwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32,
-                                      _f32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp]),
+                                      _f32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _sz, _vp]),
     "ssla_diag_scan_fwd": (_i32, [_vp, _vp, _vp, _i32, _i64, _i32, _vp, _vp]),
     "ssla_diag_scan_bwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _vp, _vp, _vp]),
     "ssla_sparse_gla_step": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,

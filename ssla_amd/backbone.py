@@ -150,15 +150,30 @@ class DetectionHead(nn.Module):
         for m in list(self.cls_preds) + list(self.obj_preds):
             nn.init.constant_(m.bias, prior)
 
+    @staticmethod
+    def _conv1x1(x, conv):
+        return F.linear(x, conv.weight.view(conv.out_channels, conv.in_channels), conv.bias)
+
+    def _branch(self, x, seq):
+        conv, bn, _ = seq
+        y = F.batch_norm(self._conv1x1(x, conv), bn.running_mean, bn.running_var, bn.weight, bn.bias, False, 0.0,
+                         bn.eps)
+        return F.silu(y)
+
     def forward(self, xin: List[torch.Tensor]) -> torch.Tensor:
+        # A 1x1 convolution is a linear map of every cell's channels: the
+        # maps are taken channel-last ([B * H * W, C], the order the outputs
+        # are laid out in) and run as GEMMs; BatchNorm in eval mode and SiLU
+        # are elementwise.
         outs = []
         for lvl, x in enumerate(xin):
-            cls_feat = self.cls_convs[lvl](x)
-            reg_feat = self.reg_convs[lvl](x)
-            out = torch.cat([self.reg_preds[lvl](reg_feat), self.obj_preds[lvl](reg_feat),
-                             self.cls_preds[lvl](cls_feat)], 1)
-            B, C, Hh, Ww = out.shape
-            out = out.permute(0, 2, 3, 1).reshape(B, Hh * Ww, C)
+            B, Cin, Hh, Ww = x.shape
+            xc = x.permute(0, 2, 3, 1).reshape(B * Hh * Ww, Cin)
+            cls_feat = self._branch(xc, self.cls_convs[lvl])
+            reg_feat = self._branch(xc, self.reg_convs[lvl])
+            out = torch.cat([self._conv1x1(reg_feat, self.reg_preds[lvl]), self._conv1x1(reg_feat, self.obj_preds[lvl]),
+                             self._conv1x1(cls_feat, self.cls_preds[lvl])], 1)
+            out = out.view(B, Hh * Ww, -1)
             yv, xv = torch.meshgrid(torch.arange(Hh, device=x.device), torch.arange(Ww, device=x.device),
                                     indexing="ij")
             cell = torch.stack((xv, yv), 2).reshape(1, Hh * Ww, 2).to(out.dtype)

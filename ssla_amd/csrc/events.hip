@@ -538,21 +538,45 @@ __global__ void pool_emit(const int64_t *__restrict__ head, const int64_t *__res
     }
   }
 }
-__global__ void count_by(const int64_t *__restrict__ lab, const int64_t *__restrict__ counts, int which,
-                         int64_t n_lab, int64_t *__restrict__ out) {
-  const int64_t n = counts[which];
-  GRID_STRIDE(i, n) {
-    const int64_t l = lab[i];
-    if (l >= 0 && l < n_lab) atomicAdd(reinterpret_cast<unsigned long long *>(&out[l]), 1ull);
+// The last index j in [0, n) with a[j] <= x, for a non-decreasing a
+// (0 when a[0] > x).
+__device__ __forceinline__ int64_t last_le(const int64_t *__restrict__ a, int64_t n, int64_t x) {
+  int64_t lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (a[mid] <= x) lo = mid;
+    else hi = mid - 1;
   }
+  return lo;
 }
 
-// field[i] = f for the events of field f (fields laid out in order)
+// The first index j in [0, n) with a[j] >= x (n if none), a non-decreasing.
+__device__ __forceinline__ int64_t first_ge(const int64_t *__restrict__ a, int64_t n, int64_t x) {
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (a[mid] < x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// out[f] = the number of the counts[which] labels equal to f, for labels
+// that are non-decreasing (the segments' fields): two binary searches per
+// label value, no atomics.
+__global__ void count_sorted_by(const int64_t *__restrict__ lab, const int64_t *__restrict__ counts, int which,
+                                int64_t n_lab, int64_t *__restrict__ out) {
+  const int64_t n = counts[which];
+  GRID_STRIDE(f, n_lab) out[f] = first_ge(lab, n, f + 1) - first_ge(lab, n, f);
+}
+
+// field[i] = f for the events of field f (fields laid out in order: start
+// is the exclusive prefix of the lengths), one thread per event.
 __global__ void pool_field_of(const int64_t *__restrict__ start, const int64_t *__restrict__ len, int64_t n_f,
                               int64_t E, int64_t *__restrict__ field) {
-  GRID_STRIDE(f, n_f) {
-    const int64_t b = min(max(start[f], (int64_t)0), E), e = min(b + max(len[f], (int64_t)0), E);
-    for (int64_t i = b; i < e; ++i) field[i] = f;
+  GRID_STRIDE(i, E) {
+    const int64_t f = last_le(start, n_f, i);
+    if (i >= start[f] && i < start[f] + len[f]) field[i] = f;
   }
 }
 
@@ -755,10 +779,12 @@ extern "C" int ssla_events_counts(const void *workspace, int64_t *counts_out, in
 // exactly where the stable sort of rf_enumerate's keys puts it (ties keep
 // the enumeration order: position, then run order).
 namespace {
-// Per group: ev2g[e] = g for the events of its run (when store), and
-// n_bad += 1 if the run is not non-decreasing in time (clamped at 0) or
-// leaves [0, E_in).  Without store (ev2g too small) one thread adds 1, which
-// sends the caller to the sort fill.
+// ev2g[e] = g for the events e of group g's run (when store; one thread
+// per event, its group found by binary search over the run starts gstart,
+// the exclusive prefix of the run lengths), and n_bad > 0 if a run is not
+// non-decreasing in time (clamped at 0: one count per decreasing pair) or
+// leaves [0, E_in) (one count per such run).  Without store (ev2g too small)
+// one thread adds 1, which sends the caller to the sort fill.
 __global__ void rf_groups_scan(const int64_t *__restrict__ gstart, const int64_t *__restrict__ glen, int64_t G,
                                const int64_t *__restrict__ time, int64_t E_in, int32_t *__restrict__ ev2g, int store,
                                unsigned long long *__restrict__ n_bad) {
@@ -766,22 +792,17 @@ __global__ void rf_groups_scan(const int64_t *__restrict__ gstart, const int64_t
     if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(n_bad, 1ull);
     return;
   }
+  GRID_STRIDE(e, E_in) {
+    const int64_t g = last_le(gstart, G, e);
+    const int64_t s = gstart[g];
+    if (e >= s && e < s + glen[g]) {
+      ev2g[e] = static_cast<int32_t>(g);
+      if (e > s && max(time[e], (int64_t)0) < max(time[e - 1], (int64_t)0)) atomicAdd(n_bad, 1ull);
+    }
+  }
   GRID_STRIDE(g, G) {
     const int64_t s = gstart[g], n = glen[g];
-    int64_t prev = 0;
-    bool bad = false;
-    for (int64_t i = 0; i < n; ++i) {
-      const int64_t e = s + i;
-      if (e < 0 || e >= E_in) {
-        bad = true;
-        break;
-      }
-      const int64_t t = max(time[e], (int64_t)0);
-      bad |= i > 0 && t < prev;
-      prev = t;
-      ev2g[e] = static_cast<int32_t>(g);
-    }
-    if (bad) atomicAdd(n_bad, 1ull);
+    if (n > 0 && (s < 0 || s + n > E_in)) atomicAdd(n_bad, 1ull);
   }
 }
 
@@ -950,8 +971,9 @@ extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h
   if (store && E_in > 0)
     hipLaunchKernelGGL(fill_i32, dim3(grid_for(E_in)), dim3(kThreads), 0, st, L.val, E_in, -1);
   if (G > 0 || !store)
-    hipLaunchKernelGGL(rf_groups_scan, dim3(grid_for(std::max<int64_t>(G, 1))), dim3(kThreads), 0, st, L.gstart,
-                       gr_len, G, time, E_in, L.val, store, reinterpret_cast<unsigned long long *>(L.counts + 3));
+    hipLaunchKernelGGL(rf_groups_scan, dim3(grid_for(std::max<int64_t>(std::max(G, E_in), 1))), dim3(kThreads), 0,
+                       st, L.gstart, gr_len, G, time, E_in, L.val, store,
+                       reinterpret_cast<unsigned long long *>(L.counts + 3));
   return launch_status("rf_scatter_plan");
 }
 
@@ -1269,7 +1291,7 @@ extern "C" int ssla_pool_segments(const int64_t *time, const int64_t *lengths, i
   // field of every event (repeat_interleave of 0..n_f-1)
   int s = excl_scan(L.tmp, L.tmp_bytes, lengths, L.start, n_f, st);
   if (s) return s;
-  hipLaunchKernelGGL(pool_field_of, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.start, lengths, n_f, E, field);
+  hipLaunchKernelGGL(pool_field_of, dim3(grid_for(E)), dim3(kThreads), 0, st, L.start, lengths, n_f, E, field);
   // segment heads and their prefix
   int64_t *head = L.kl;   // layout holds max(n_f, E) + 1 entries
   hipLaunchKernelGGL(pool_heads, dim3(grid_for(E)), dim3(kThreads), 0, st, time, field, E, head);
@@ -1278,7 +1300,8 @@ extern "C" int ssla_pool_segments(const int64_t *time, const int64_t *lengths, i
   hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.kpre, head, E, L.counts);
   hipLaunchKernelGGL(pool_emit, dim3(grid_for(E)), dim3(kThreads), 0, st, head, L.kpre, time, field, E, seg, seg_time,
                      seg_field);
-  hipLaunchKernelGGL(count_by, dim3(grid_for(E)), dim3(kThreads), 0, st, seg_field, L.counts, 0, n_f, new_lengths);
+  hipLaunchKernelGGL(count_sorted_by, dim3(grid_for(n_f)), dim3(kThreads), 0, st, seg_field, L.counts, 0, n_f,
+                     new_lengths);
   return launch_status("pool_segments");
 }
 

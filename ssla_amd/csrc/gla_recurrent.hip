@@ -105,14 +105,78 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int DT, int GDT, int KPL>
+// ---------------------------------------------------- segmented schedule --
+// Long sequences are cut into segments of kSegSteps steps (at least one per
+// sequence, so empty sequences still pass h0 to ht), numbered globally
+// (segoff[n] = first segment of sequence n, computed on the device).
+// * state pass (kSegState): every segment but the last of its sequence runs
+//   from a zero state and leaves its local end state L_j and the product
+//   P_j of its decays (per key); the first segment also copies h0 (read
+//   once, here) into the workspace.
+// * output pass (kSegOut): segment s of a sequence enters with
+//   E = h0, E = P_j E + L_j for j < s (the recurrence is linear in the
+//   state, so this is the state after segment s - 1 up to rounding), runs its
+//   steps writing o, and the last segment writes ht.  Multi-segment
+//   sequences read h0 from the copy, so an in-place update (ht == h0) never
+//   races with a segment that has not read it yet.
+constexpr int kSegSteps = 128;
+enum { kPlain = 0, kSegState = 1, kSegOut = 2 };
+
+struct SegWs {
+  const int64_t *segoff;   // [n_seq + 1]
+  float *slot;             // [n_segs_max, H, K, V]: L_j
+  float *prod;             // [n_segs_max, H, K]: P_j
+  float *h0c;              // [n_seq, H, K, V]: copy of the initial states
+  int64_t n_segs_max;      // upper bound of the segment count (grid size)
+};
+
+__device__ __forceinline__ int find_seg_seq(const int64_t *off, int n_seq, int64_t i) {
+  int lo = 0, hi = n_seq - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (off[mid] <= i) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// segoff[n] = segments of sequences 0..n-1 (segoff[n_seq]: the total).  One
+// workgroup of 256 threads.
+__global__ __launch_bounds__(256) void seg_offsets_kernel(const int64_t *__restrict__ cu, int n_seq, int64_t T,
+                                                          int64_t *__restrict__ segoff) {
+  __shared__ int64_t ps[256];
+  int64_t carry = 0;
+  for (int base = 0; base < n_seq; base += 256) {
+    const int n = base + static_cast<int>(threadIdx.x);
+    int64_t c = 0;
+    if (n < n_seq) {
+      const int64_t bos = min(max(cu[n], (int64_t)0), T);
+      const int64_t eos = min(max(cu[n + 1], bos), T);
+      c = max((eos - bos + kSegSteps - 1) / kSegSteps, (int64_t)1);
+    }
+    ps[threadIdx.x] = c;
+    __syncthreads();
+    for (int d = 1; d < 256; d <<= 1) {   // inclusive scan (Hillis-Steele)
+      const int64_t x = threadIdx.x >= static_cast<unsigned>(d) ? ps[threadIdx.x - d] : 0;
+      __syncthreads();
+      ps[threadIdx.x] += x;
+      __syncthreads();
+    }
+    if (n < n_seq) segoff[n] = carry + ps[threadIdx.x] - c;
+    carry += ps[255];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) segoff[n_seq] = carry;
+}
+
+template <int DT, int GDT, int KPL, int MODE>
 __global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
     const void *__restrict__ q, const void *__restrict__ k,
     const void *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int H, int V,
     float scale, const float *__restrict__ h0, void *__restrict__ o,
     float *__restrict__ ht, const int32_t *__restrict__ state_idx, int n_state_rows,
-    int64_t T, int32_t *__restrict__ status) {
+    int64_t T, int32_t *__restrict__ status, SegWs sw) {
   typedef Staged<DT, GDT, KPL> G;
   constexpr int K = G::K;
   constexpr int U = 2;   // steps per group (kSB is a multiple)
@@ -122,25 +186,74 @@ __global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
   unsigned char *lds = smem[wv];
   const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wv;
   const int n_vt = (V + kBV - 1) / kBV;
-  if (item >= static_cast<int64_t>(n_seq) * H * n_vt) return;  // whole wavefront exits (no workgroup barrier)
+  const int64_t n_units = MODE == kPlain ? static_cast<int64_t>(n_seq) : sw.n_segs_max;
+  if (item >= n_units * H * n_vt) return;  // whole wavefront exits (no workgroup barrier)
   const int vt = static_cast<int>(item % n_vt);
   const int h = static_cast<int>((item / n_vt) % H);
-  const int n = static_cast<int>(item / (static_cast<int64_t>(n_vt) * H));
+  const int64_t unit = item / (static_cast<int64_t>(n_vt) * H);   // sequence, or global segment
+  int n = static_cast<int>(unit);
+  int64_t seg = 0, nseg = 1;
+  if (MODE != kPlain) {
+    if (unit >= sw.segoff[n_seq]) return;   // past the actual segment count
+    n = find_seg_seq(sw.segoff, n_seq, unit);
+    seg = unit - sw.segoff[n];
+    nseg = sw.segoff[n + 1] - sw.segoff[n];
+    if (MODE == kSegState && seg == nseg - 1) return;   // the last segment needs no local state
+  }
   const int col = vt * kBV + (lane & 15);
   const int kg = lane >> 4;
   const int k0 = kg * KPL;
   const bool col_ok = col < V;
-  const int64_t bos = min(max(cu_seqlens[n], (int64_t)0), T);
-  const int64_t eos = min(max(cu_seqlens[n + 1], bos), T);
+  const int64_t sbos = min(max(cu_seqlens[n], (int64_t)0), T);
+  const int64_t seos = min(max(cu_seqlens[n + 1], sbos), T);
+  const int64_t bos = MODE == kPlain ? sbos : min(sbos + seg * kSegSteps, seos);      // this unit's steps
+  const int64_t eos = MODE == kPlain ? seos : min(bos + kSegSteps, seos);
   const int64_t srow = state_idx ? static_cast<int64_t>(state_idx[n]) : n;
   if (bad_state_row(state_idx, n, srow, n_state_rows)) {
-    skip_sequence<DT>(o, bos, eos, H, h, V, col, kg == 0 && col_ok, lane, status);
+    if (MODE != kSegState) skip_sequence<DT>(o, bos, eos, H, h, V, col, kg == 0 && col_ok, lane, status);
     return;
   }
 
   float S[KPL];
+  float dprod[KPL];   // product of the decays of this unit (state pass)
 #pragma unroll
-  for (int i = 0; i < KPL; ++i) S[i] = (h0 && col_ok) ? h0[((srow * H + h) * K + k0 + i) * V + col] : 0.f;
+  for (int i = 0; i < KPL; ++i) dprod[i] = 1.f;
+  const int64_t e0 = (static_cast<int64_t>(h) * K + k0) * V + col;   // this lane's element (i = 0) of a state
+  if (MODE == kSegState) {
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) S[i] = 0.f;
+    if (seg == 0 && col_ok) {
+      float *dst = sw.h0c + static_cast<int64_t>(n) * H * K * V + e0;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) dst[i * V] = h0 ? h0[srow * H * K * V + e0 + i * V] : 0.f;
+    }
+  } else {
+    const float *src = nullptr;
+    if (MODE == kSegOut && nseg > 1) src = sw.h0c + static_cast<int64_t>(n) * H * K * V;
+    else if (h0) src = h0 + srow * H * K * V;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) S[i] = (src && col_ok) ? src[e0 + i * V] : 0.f;
+    if (MODE == kSegOut) {
+      // fold the earlier segments' local states, eight per round trip
+      for (int64_t j0 = 0; j0 < seg; j0 += 8) {
+        float L[8][KPL], P[8][KPL];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int64_t gj = sw.segoff[n] + j0 + u;
+#pragma unroll
+          for (int i = 0; i < KPL; ++i) {
+            const bool ok = j0 + u < seg;
+            L[u][i] = (ok && col_ok) ? sw.slot[gj * H * K * V + e0 + i * V] : 0.f;
+            P[u][i] = ok ? sw.prod[(gj * H + h) * K + k0 + i] : 1.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int i = 0; i < KPL; ++i) S[i] = fmaf(P[u][i], S[i], L[u][i]);
+      }
+    }
+  }
 
   // this lane's pieces of a block: piece p = lane + 64 j of each array
   uint4 rq[G::NQ], rk[G::NQ], rg[G::NG], rv[G::NV];
@@ -245,6 +358,17 @@ __global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
 #pragma unroll
         for (int i = 0; i < KPL; ++i) kv[u][i] *= vc;
       }
+      if (MODE == kSegState) {
+        // state only: steps past the unit's end have decay 1 and k = 0
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int i = 0; i < KPL; ++i) {
+            S[i] = fmaf(d[u][i], S[i], kv[u][i]);
+            dprod[i] *= d[u][i];
+          }
+        continue;
+      }
       float acc[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -264,7 +388,19 @@ __global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
         if (kg == 0 && col_ok && s0 + u < ns) E::store(o, ((t0 + s0 + u) * H + h) * V + col, acc[u] * scale);
     }
   }
-  if (ht && col_ok) {
+  if (MODE == kSegState) {
+    const int64_t gs = unit;
+    if (col_ok) {
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) sw.slot[gs * H * K * V + e0 + i * V] = S[i];
+    }
+    if (vt == 0 && (lane & 15) == 0) {
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) sw.prod[(gs * H + h) * K + k0 + i] = dprod[i];
+    }
+    return;
+  }
+  if (ht && col_ok && seg == nseg - 1) {
 #pragma unroll
     for (int i = 0; i < KPL; ++i) ht[((srow * H + h) * K + k0 + i) * V + col] = S[i];
   }
@@ -339,11 +475,37 @@ __global__ __launch_bounds__(256) void gla_recurrent_kernel(
   }
 }
 
+// Workspace of the segmented schedule (0: not used for this shape -- K
+// outside the staged kernels, or sequences of fewer than kSegSteps / 4
+// steps on average, where one pass is as fast).
+struct SegLayout {
+  size_t segoff, slot, prod, h0c, total;
+  int64_t n_segs_max;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+inline SegLayout seg_layout(int n_seq, int64_t T, int H, int K, int V) {
+  SegLayout L{};
+  if (n_seq <= 0 || T <= 0 || K % 16 != 0 || K > 64 || V <= 0) return L;
+  if (T < static_cast<int64_t>(n_seq) * (kSegSteps / 4)) return L;
+  L.n_segs_max = T / kSegSteps + n_seq + 1;
+  const size_t hkv = static_cast<size_t>(H) * K * V;
+  size_t p = 0;
+  L.segoff = p; p = align256(p + sizeof(int64_t) * (n_seq + 1));
+  L.slot = p;   p = align256(p + sizeof(float) * L.n_segs_max * hkv);
+  L.prod = p;   p = align256(p + sizeof(float) * L.n_segs_max * H * K);
+  L.h0c = p;    p = align256(p + sizeof(float) * n_seq * hkv);
+  L.total = p;
+  return L;
+}
+
 template <int DT, int GDT>
 int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
                      const int64_t *cu, int n_seq, int H, int K, int V, float scale,
                      const float *h0, void *o, float *ht, const int32_t *sidx,
-                     int n_rows, int64_t T, int32_t *status, hipStream_t st) {
+                     int n_rows, int64_t T, int32_t *status, void *workspace, size_t ws_bytes,
+                     hipStream_t st) {
   const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
   const int n_vt = (V + kBV - 1) / kBV;
   const int64_t items = static_cast<int64_t>(n_seq) * H * n_vt;
@@ -362,9 +524,36 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
   const int es = DT == SSLA_F32 ? 4 : 2;
   const bool staged = (K % 16 == 0) && K <= 64 && (V * es) % 16 == 0 && al16(q) && al16(k) && al16(g) && al16(v);
   if (staged) {
-#define SSLA_RECS(KPL_)                                                                          \
-  hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_>), grid, block, 0, st, q, k, v, g, \
-                     cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status)
+    const SegLayout L = seg_layout(n_seq, T, H, K, V);
+    const bool segmented = L.total > 0 && workspace != nullptr && ws_bytes >= L.total;
+    SegWs sw{};
+    dim3 sgrid = grid;
+    if (segmented) {
+      char *w = static_cast<char *>(workspace);
+      sw.segoff = reinterpret_cast<const int64_t *>(w + L.segoff);
+      sw.slot = reinterpret_cast<float *>(w + L.slot);
+      sw.prod = reinterpret_cast<float *>(w + L.prod);
+      sw.h0c = reinterpret_cast<float *>(w + L.h0c);
+      sw.n_segs_max = L.n_segs_max;
+      const int64_t sblocks = (L.n_segs_max * H * n_vt + waves_per_block - 1) / waves_per_block;
+      if (sblocks > 0x7fffffff) {
+        set_error("gla_recurrent_fwd: too many (segment, head, tile) items");
+        return SSLA_ERR_UNSUPPORTED;
+      }
+      sgrid = dim3(static_cast<unsigned>(sblocks));
+      hipLaunchKernelGGL(seg_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T,
+                         reinterpret_cast<int64_t *>(w + L.segoff));
+    }
+#define SSLA_RECS(KPL_)                                                                                     \
+  if (segmented) {                                                                                          \
+    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegState>), sgrid, block, 0, st, q, k, v, \
+                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                  \
+    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegOut>), sgrid, block, 0, st, q, k, v,   \
+                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                  \
+  } else {                                                                                                  \
+    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kPlain>), grid, block, 0, st, q, k, v, g,  \
+                       cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                     \
+  }
     switch (K / kKG) {
       case 4: SSLA_RECS(4); return launch_status("gla_recurrent_fwd");
       case 8: SSLA_RECS(8); return launch_status("gla_recurrent_fwd");
@@ -394,7 +583,8 @@ extern "C" int ssla_gla_recurrent_fwd(const void *q, const void *k, const void *
                                       int H, int K, int V, float scale,
                                       const float *h0, void *o, float *ht,
                                       const int32_t *state_idx, int n_state_rows,
-                                      int32_t *status, int dtype, void *stream) {
+                                      int32_t *status, int dtype, void *workspace,
+                                      size_t workspace_bytes, void *stream) {
   using namespace ssla;
   clear_error();
   SSLA_CHECK_ARG(n_seq >= 0 && T >= 0 && H > 0 && K > 0 && V > 0,
@@ -412,20 +602,25 @@ extern "C" int ssla_gla_recurrent_fwd(const void *q, const void *k, const void *
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == SSLA_F32) {
     if (g_dtype != SSLA_F32) { set_error("gla_recurrent_fwd: fp32 inputs need fp32 g"); return SSLA_ERR_DTYPE; }
-    return launch_recurrent<SSLA_F32, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
+    return launch_recurrent<SSLA_F32, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, workspace, workspace_bytes, st);
   }
   if (dtype == SSLA_BF16) {
     if (g_dtype == SSLA_F32)
-      return launch_recurrent<SSLA_BF16, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
+      return launch_recurrent<SSLA_BF16, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, workspace, workspace_bytes, st);
     if (g_dtype == SSLA_BF16)
-      return launch_recurrent<SSLA_BF16, SSLA_BF16>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
+      return launch_recurrent<SSLA_BF16, SSLA_BF16>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, workspace, workspace_bytes, st);
   }
   if (dtype == SSLA_F16) {
     if (g_dtype == SSLA_F32)
-      return launch_recurrent<SSLA_F16, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
+      return launch_recurrent<SSLA_F16, SSLA_F32>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, workspace, workspace_bytes, st);
     if (g_dtype == SSLA_F16)
-      return launch_recurrent<SSLA_F16, SSLA_F16>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, st);
+      return launch_recurrent<SSLA_F16, SSLA_F16>(q, k, v, g, cu_seqlens, n_seq, H, K, V, scale, h0, o, ht, state_idx, n_state_rows, T, status, workspace, workspace_bytes, st);
   }
   set_error("gla_recurrent_fwd: unsupported dtype %d / g_dtype %d", dtype, g_dtype);
   return SSLA_ERR_DTYPE;
+}
+
+extern "C" size_t ssla_gla_recurrent_workspace_size(int n_seq, int64_t T, int H, int K, int V) {
+  if (H <= 0) return 0;
+  return ssla::seg_layout(n_seq, T, H, K, V).total;
 }

@@ -171,10 +171,13 @@ def _recurrent(q, k, v, g, cu, scale, h0, o, ht, state_idx, n_rows, status=None)
     V = v.shape[-1]
     N = cu.numel() - 1
     lib = _lib.load()
+    ws_bytes = lib.ssla_gla_recurrent_workspace_size(N, T, H, K, V)
+    ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
     st = lib.ssla_gla_recurrent_fwd(
         _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.DTYPE_CODE[g.dtype],
         _lib.ptr(cu), N, T, H, K, V, float(scale), _lib.ptr(h0), _lib.ptr(o), _lib.ptr(ht),
-        _lib.ptr(state_idx), int(n_rows), _lib.ptr(status), _lib.DTYPE_CODE[q.dtype], _lib.stream_of(q))
+        _lib.ptr(state_idx), int(n_rows), _lib.ptr(status), _lib.DTYPE_CODE[q.dtype], _lib.ptr(ws), ws_bytes,
+        _lib.stream_of(q))
     _lib.check(st, "ssla_gla_recurrent_fwd")
     return o, ht
 

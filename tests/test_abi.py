@@ -45,7 +45,7 @@ def test_argument_errors_without_device_work():
     assert st == _lib.SSLA_ERR_UNSUPPORTED
     # K > 256 on the recurrent kernel
     st = lib.ssla_gla_recurrent_fwd(None, None, None, None, 0, None, 1, 0, 1, 300, 64, 1.0, None, None,
-                                    None, None, 0, None, _lib.SSLA_F32, None)
+                                    None, None, 0, None, _lib.SSLA_F32, None, 0, None)
     assert st == _lib.SSLA_ERR_UNSUPPORTED
     # unsupported sparse-step shape
     st = lib.ssla_sparse_gla_step(None, 1, None, None, None, None, None, 1, 1, 48, 48, 1.0, None, None, None)

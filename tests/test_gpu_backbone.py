@@ -164,9 +164,12 @@ def test_async_step_full_size_properties(dev):
         with torch.no_grad():
             out, feats = model(ev.to(dev), ln, states)
             again = [p.clone() for p in prev]
-            out2, _ = model(ev.to(dev), ln, again)
+            out2, feats2 = model(ev.to(dev), ln, again)
         assert out.shape == (1, 30 * 38 + 15 * 19 + 8 * 10, 7) and torch.isfinite(out.float()).all()
-        assert torch.equal(out, out2) and all(torch.equal(a, b) for a, b in zip(again, states))
+        for i in range(4):
+            assert torch.equal(feats[i]["events"], feats2[i]["events"]), f"stage {i} output differs on a rerun"
+            assert torch.equal(again[i], states[i]), f"stage {i} states differ on a rerun"
+        assert torch.equal(out, out2), "head output differs on a rerun"
         for i, f in enumerate(feats):
             sites = ((f["batch_id"] * model.grid_sizes[i][0] + f["h"]) * model.grid_sizes[i][1] + f["w"]).long()
             assert bool((sites[1:] > sites[:-1]).all()), f"stage {i}: site list not strictly increasing"

@@ -246,3 +246,44 @@ def test_sparse_scan_rejects_bad_site_lists(dev):
     assert torch.isfinite(o[:5]).all()
     untouched = [i for i in range(n_sites) if i not in (4, 9)]
     assert torch.equal(st[untouched], state0[untouched])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sparse_scan_long_sequences_in_place(dev, dtype):
+    """Long and ragged per-site histories (the segmented schedule: 128-step
+    segments folded into each other, and an in-place state table that the
+    last segment overwrites while the first reads it from the copy): o and
+    the updated states against the oracle, other rows untouched bit for
+    bit."""
+    from ssla_amd import _lib
+    from ssla_amd.scan import sparse_gla_scan
+    gen = torch.Generator().manual_seed(40)
+    lens = [700, 5, 300, 129, 0, 1000, 128]
+    sites = [2, 3, 7, 8, 11, 15, 19]
+    H, K, V, n_sites = 4, 32, 32, 24
+    T = sum(lens)
+    assert _lib.load().ssla_gla_recurrent_workspace_size(len(lens), T, H, K, V) > 0
+    q, k, v = (torch.randn(T, H, D, generator=gen).to(dtype) for D in (K, K, V))
+    g = F.logsigmoid(torch.randn(T, H, K, generator=gen) / 4)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64)
+    state0 = torch.randn(n_sites, H, K, V, generator=gen) * 0.1
+    st = state0.clone().to(dev)
+    print(f"sparse scan long sequences {dtype}", flush=True)
+    with torch.no_grad():
+        o = sparse_gla_scan(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev),
+                            torch.tensor(sites, dtype=torch.int32, device=dev), st, scale=K ** -0.5)
+    ro, rht = oracle.gla_recurrent(q.float().numpy(), k.float().numpy(), v.float().numpy(), g.numpy(), cu.numpy(),
+                                   K ** -0.5, state0.numpy()[sites], True)
+    if dtype == torch.float32:
+        assert_close(o.cpu().numpy(), ro, 1e-4, "o")
+    else:   # o rounded to bf16: within a bf16 rounding (2^-8 relative, fp32 sums on both sides) of each element
+        assert_close(o.float().cpu().numpy(), ro, 2 ** -8, "o", band=1e-4, ratio_max=3e-3)
+    assert_close(st.cpu().numpy()[sites], rht, 1e-4, "states")
+    others = [i for i in range(n_sites) if i not in sites]
+    assert torch.equal(st[others].cpu(), state0[others])
+    # the same call again from the same states: the same bits
+    st2 = state0.clone().to(dev)
+    with torch.no_grad():
+        o2 = sparse_gla_scan(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev),
+                             torch.tensor(sites, dtype=torch.int32, device=dev), st2, scale=K ** -0.5)
+    assert torch.equal(o2, o) and torch.equal(st2, st), "segmented scan not repeatable"
