@@ -531,26 +531,66 @@ inline Tpl pick_tpl(int cin, int hid) {
   return {0, 0};
 }
 
+// LDS of the small kernels' weights: the folded weights when they fit,
+// else the plain ones.
+inline size_t small_lds(const Tpl &t, int A, int As, int Ag) {
+  const size_t kS = t.hp * t.cp + 4, kG = t.hp * t.hp + 4;
+  const size_t fold = sizeof(float) * (3 * As * kS + Ag * kG);
+  const size_t plain = sizeof(float) * (As * kS + Ag * kG + 4 * static_cast<size_t>(t.hp) * t.hp);
+  (void)A;
+  return fold <= kMaxLds ? fold : plain;
+}
+
+}  // namespace
+
+// The matrix-core path for sizes the small kernels do not take
+// (mos_attention_mfma.hip).
+namespace mosm {
+bool supported(int cin, int H, int A);
+size_t workspace_bytes(int64_t E, int cin, int H, int A, int64_t R, int64_t P);
+size_t lds_bytes(int cin, int H);
+int forward(const float *events, int64_t E, int cin, const int64_t *row_src, const int64_t *row_pos, int64_t R,
+            const int64_t *patch_len, int64_t P, int A, const float *w_scatter, int As, const float *w_q,
+            const float *w_v, const float *w_g, const float *w_o, const float *w_gather, int Ag, const float *w_in,
+            const float *ln_w, const float *ln_b, float eps, int H, float *out, void *workspace,
+            size_t workspace_bytes_given, hipStream_t st);
+}  // namespace mosm
+
+namespace {
+// Which kernels take a layer: 1 the small kernels (input and hidden <= 32,
+// weights within 64 KB of LDS), 2 the matrix-core path (input and hidden
+// multiples of 4 up to 128), 0 none.
+inline int pick_path(int cin, int hid, int A, int As, int Ag) {
+  if (A <= 0 || A > kMaxPos) return 0;
+  const Tpl t = pick_tpl(cin, hid);
+  if (t.hp != 0 && small_lds(t, A, As, Ag) <= kMaxLds) return 1;
+  return mosm::supported(cin, hid, A) ? 2 : 0;
+}
 }  // namespace
 }  // namespace ssla
 
 extern "C" size_t ssla_mos_attention_workspace_size(int64_t n_events, int c_in, int hidden, int A, int64_t n_rows,
                                                     int64_t n_patches) {
   using namespace ssla;
+  if (n_events < 0 || A <= 0 || A > kMaxPos || n_rows < 0 || n_patches < 0) return 0;
+  // the larger of the two paths' needs (which one runs depends on the
+  // projections' sharing, not known here)
+  size_t bytes = 0;
   const Tpl t = pick_tpl(c_in, hidden);
-  if (n_events < 0 || A <= 0 || n_rows < 0 || n_patches < 0 || t.hp == 0) return 0;
-  return mos_layout(nullptr, n_events, A, n_rows, n_patches, t.cp, t.hp).total;
+  if (t.hp != 0) bytes = mos_layout(nullptr, n_events, A, n_rows, n_patches, t.cp, t.hp).total;
+  if (mosm::supported(c_in, hidden, A))
+    bytes = std::max(bytes, mosm::workspace_bytes(n_events, c_in, hidden, A, n_rows, n_patches));
+  return bytes;
 }
 
 extern "C" size_t ssla_mos_attention_lds_bytes(int c_in, int hidden, int A, int scatter_per_pos, int gather_per_pos) {
   using namespace ssla;
-  const Tpl t = pick_tpl(c_in, hidden);
-  if (t.hp == 0 || A <= 0 || A > kMaxPos) return 0;   // 0: the fused kernels do not take this layer
   const int As = scatter_per_pos ? A : 1, Ag = gather_per_pos ? A : 1;
-  const size_t kS = t.hp * t.cp + 4, kG = t.hp * t.hp + 4;
-  const size_t fold = sizeof(float) * (3 * As * kS + Ag * kG);
-  const size_t plain = sizeof(float) * (As * kS + Ag * kG + 4 * static_cast<size_t>(t.hp) * t.hp);
-  return fold <= kMaxLds ? fold : plain;   // the folded weights when they fit
+  switch (pick_path(c_in, hidden, A, As, Ag)) {
+    case 1: return small_lds(pick_tpl(c_in, hidden), A, As, Ag);
+    case 2: return mosm::lds_bytes(c_in, hidden);
+    default: return 0;   // 0: the fused kernels do not take this layer
+  }
 }
 
 extern "C" int ssla_mos_attention_fwd(const float *events, int64_t n_events, int c_in, const int64_t *row_src,
@@ -565,32 +605,36 @@ extern "C" int ssla_mos_attention_fwd(const float *events, int64_t n_events, int
   SSLA_CHECK_ARG(n_events >= 0 && n_rows >= 0 && n_patches >= 0 && c_in > 0 && hidden > 0 && A > 0,
                  "mos_attention_fwd: bad sizes E=%lld R=%lld P=%lld cin=%d hidden=%d A=%d", (long long)n_events,
                  (long long)n_rows, (long long)n_patches, c_in, hidden, A);
-  const Tpl tpl = pick_tpl(c_in, hidden);
-  if (tpl.hp == 0 || A > kMaxPos) {
-    set_error("mos_attention_fwd: needs input and hidden sizes up to 32 and at most %d kernel positions "
-              "(cin=%d hidden=%d A=%d)", kMaxPos, c_in, hidden, A);
+  const int As = scatter_per_pos ? A : 1, Ag = gather_per_pos ? A : 1;
+  const int path = pick_path(c_in, hidden, A, As, Ag);
+  if (path == 0) {
+    set_error("mos_attention_fwd: needs at most %d kernel positions and either input and hidden sizes up to 32 "
+              "with weights within %zu bytes of LDS, or sizes that are multiples of 4 up to 128 "
+              "(cin=%d hidden=%d A=%d)", kMaxPos, kMaxLds, c_in, hidden, A);
     return SSLA_ERR_UNSUPPORTED;
   }
   if (!w_in && c_in != hidden) {
     set_error("mos_attention_fwd: input size %d differs from hidden %d but no input projection given", c_in, hidden);
     return SSLA_ERR_ARG;
   }
-  const size_t lds = ssla_mos_attention_lds_bytes(c_in, hidden, A, scatter_per_pos, gather_per_pos);
-  if (lds > kMaxLds) {
-    set_error("mos_attention_fwd: weights need %zu bytes of LDS (at most %zu)", lds, kMaxLds);
-    return SSLA_ERR_UNSUPPORTED;
-  }
   SSLA_CHECK_ARG(n_rows < 0x7fffffff && n_events * A < (int64_t{1} << 40), "mos_attention_fwd: too many rows");
   if (n_events == 0) return SSLA_OK;
   SSLA_CHECK_ARG(events && out && w_scatter && w_q && w_v && w_g && w_o && w_gather && ln_w && ln_b,
                  "mos_attention_fwd: null pointer");
   SSLA_CHECK_ARG(n_rows == 0 || (row_src && row_pos && patch_len), "mos_attention_fwd: null row arrays");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (path == 2) {
+    SSLA_CHECK_ARG(aligned(events, 16), "mos_attention_fwd: events must be 16-byte aligned");
+    return mosm::forward(events, n_events, c_in, row_src, row_pos, n_rows, patch_len, n_patches, A, w_scatter, As,
+                         w_q, w_v, w_g, w_o, w_gather, Ag, w_in, ln_w, ln_b, eps, hidden, out, workspace,
+                         workspace_bytes, st);
+  }
+  const Tpl tpl = pick_tpl(c_in, hidden);
   const MosWs w = mos_layout(workspace, n_events, A, n_rows, n_patches, tpl.cp, tpl.hp);
   if (!workspace || workspace_bytes < w.total) {
     set_error("mos_attention_fwd: workspace of %zu bytes needed, %zu given", w.total, workspace_bytes);
     return SSLA_ERR_WORKSPACE;
   }
-  hipStream_t st = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(mos_fill_i32, dim3(grid_for(n_events * A)), dim3(kThreads), 0, st, w.dst, n_events * A, -1);
   hipLaunchKernelGGL(mos_fill_i32, dim3(1), dim3(kThreads), 0, st, reinterpret_cast<int32_t *>(w.orow + n_rows * tpl.hp),
                      static_cast<int64_t>(tpl.hp), 0);   // the zero row
@@ -610,7 +654,6 @@ extern "C" int ssla_mos_attention_fwd(const float *events, int64_t n_events, int
     hipLaunchKernelGGL(mos_dst_fill, dim3(grid_for(n_rows)), dim3(kThreads), 0, st, row_src, row_pos, n_rows,
                        n_events, A, w.dst);
   }
-  const int As = scatter_per_pos ? A : 1, Ag = gather_per_pos ? A : 1;
 #define MOS_CASE(C, H)                                                                                          \
   if (tpl.cp == C && tpl.hp == H)                                                                               \
     return launch_mos<C, H>(events, n_events, c_in, hidden, row_src, row_pos, n_rows, A, w_scatter, As, w_q, w_v, \

@@ -96,14 +96,20 @@ def test_python_wrappers_reject_cpu_tensors():
 
 
 def test_fused_mos_attention_limits():
-    """The fused MosAttention kernels take at most 49 kernel positions: the
-    LDS query reports 0 (not applicable) beyond that even when the weights
-    would fit, so the layer picks the composed forward."""
+    """The fused MosAttention kernels take at most 49 kernel positions (the
+    LDS query reports 0, not applicable, beyond that even when the weights
+    would fit, so the layer picks the composed forward); sizes past the
+    small kernels' (hidden > 32, or weights beyond 64 KB of LDS) go to the
+    matrix-core path when input and hidden are multiples of 4 up to 128."""
     from ssla_amd import _lib
     lib = _lib.load()
     assert 0 < lib.ssla_mos_attention_lds_bytes(2, 12, 49, 1, 1) <= 64 * 1024
     assert lib.ssla_mos_attention_lds_bytes(2, 12, 64, 1, 1) == 0
-    assert lib.ssla_mos_attention_lds_bytes(48, 48, 9, 1, 1) == 0
+    for cin, hid in ((48, 48), (24, 48), (48, 96), (96, 96), (16, 32), (128, 128)):
+        assert 0 < lib.ssla_mos_attention_lds_bytes(cin, hid, 9, 1, 1) <= 64 * 1024, (cin, hid)
+        assert lib.ssla_mos_attention_workspace_size(1000, cin, hid, 9, 5000, 800) > 5000 * hid * 4 * 5
+    for cin, hid in ((6, 48), (48, 132), (48, 50)):
+        assert lib.ssla_mos_attention_lds_bytes(cin, hid, 9, 1, 1) == 0, (cin, hid)
 
 
 def test_status_read_rejects_null():

@@ -78,19 +78,21 @@ def test_linear_attention_matches_reference(lfx, tag):
     np.testing.assert_allclose(r["events"].cpu().numpy(), lfx[f"{tag}_out"], **TOL)
 
 
+@pytest.mark.parametrize("cin,hid", [(16, 24), (24, 48), (48, 96)])
 @pytest.mark.parametrize("fused", [True, False], ids=["fused", "composed"])
-def test_mos_attention_larger_vs_oracle(fused):
-    """A bigger random case (hot pixels, many patches) against the fp64 oracle."""
+def test_mos_attention_larger_vs_oracle(fused, cin, hid):
+    """A bigger random case (hot pixels, many patches) against the fp64
+    oracle; hidden 24 runs the small fused kernels, 48 and 96 the
+    matrix-core path."""
     from ssla_amd.layers import MosAttention
     from ssla_amd import events as E
     torch.manual_seed(7)
     B, N, H, W = 2, 3000, 24, 32
     ev, lengths = _random_events(B, N, H, W, seed=7)
     gr = E.group_events((ev.cuda(), lengths.cuda()), (H, W))
-    C = 16
-    gr["events"] = torch.randn(gr["time"].shape[0], C, device="cuda")
-    layer = MosAttention(C, 24, (H, W), (3, 3), (1, 1)).cuda()
-    print(f"mos oracle: E={gr['time'].shape[0]} fused={fused}", flush=True)
+    gr["events"] = torch.randn(gr["time"].shape[0], cin, device="cuda")
+    layer = MosAttention(cin, hid, (H, W), (3, 3), (1, 1)).cuda()
+    print(f"mos oracle: E={gr['time'].shape[0]} cin={cin} hid={hid} fused={fused}", flush=True)
     with torch.no_grad():
         r = layer(gr, fused=fused)
     p = {k: v.detach().cpu().numpy() for k, v in layer.state_dict().items()}
