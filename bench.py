@@ -729,6 +729,88 @@ def bench_chunk_bwd(torch, lib, reps, dev):
                          "note": "whole call (state passes + chunk kernel)"}}
 
 
+def bench_mos_backbone(torch, lib, reps, dev):
+    """The reference's MOS_S backbone forward (configs/model/MOS_S.yaml
+    layers, built as model_mos.py:32-122 builds them, run as
+    model_mos.py:157-209), random-init weights, over a C5-like batch of 8
+    Gen1 windows (~50k events each): preprocess, then four stages of two
+    MosAttention layers (hidden 12 / 24 / 48 / 96; the first of stages 2-4
+    with an input projection) with SparseMaxPool k2 + TemporalDropout 4
+    between them.  Every layer is timed with HIP events on the current stream
+    (host syncs inside a layer count).  For the hidden 48 / 96 layers (the
+    matrix-core path) the same layer through the composed forward is timed
+    too, on the same input."""
+    from ssla_amd import events as E, layers, synthetic
+    frame = (240, 304)
+    ev, ln = synthetic.event_windows()
+    ev, ln = ev.to(dev), ln.to(dev)
+    torch.manual_seed(0)
+    mods, names = [], []
+    size, cin = frame, 2
+    for st, hid in enumerate((12, 24, 48, 96)):
+        for j in range(2):
+            k = 1 if (st == 0 and j == 0) else 3
+            mods.append(layers.MosAttention(cin, hid, size, (k, k)).to(dev))
+            names.append(f"s{st + 1}_mos{j + 1}_k{k}_{cin}to{hid}")
+            cin = hid
+        if st < 3:
+            pool = layers.SparseMaxPool(size, kernel_size=(2, 2)).to(dev)
+            mods += [pool, layers.TemporalDropout(4, pool.frame_output_size).to(dev)]
+            names += [f"s{st + 1}_maxpool", f"s{st + 1}_tdrop"]
+            size = pool.frame_output_size
+    stream = torch.cuda.current_stream(dev)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(len(mods) + 2)]
+
+    def run(fused=None):
+        marks[0].record(stream)
+        x = E.preprocess_inputs(ev, ln, frame, 50)
+        marks[1].record(stream)
+        ins = []
+        for i, m in enumerate(mods):
+            ins.append(x)
+            x = m(x, fused=fused) if isinstance(m, layers.MosAttention) else m(x)
+            marks[2 + i].record(stream)
+        return x, ins
+
+    with torch.no_grad():
+        for _ in range(2):
+            out, ins = run()
+        torch.cuda.synchronize()
+        tot = [0.0] * (len(mods) + 1)
+        for _ in range(reps):
+            out, ins = run()
+            torch.cuda.synchronize()
+            for i in range(len(mods) + 1):
+                tot[i] += marks[i].elapsed_time(marks[i + 1])
+        per = {n: t / reps for n, t in zip(["preprocess"] + names, tot)}
+        ms = sum(per.values())
+        # hidden 48 / 96: fused (matrix-core) vs composed on each layer's own input
+        big = {}
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for i, (m, n) in enumerate(zip(mods, names)):
+            if not isinstance(m, layers.MosAttention) or m.hidden_size < 48:
+                continue
+            rows = {}
+            for mode in (True, False):
+                m(ins[i], fused=mode)
+                torch.cuda.synchronize()
+                a.record(stream)
+                for _ in range(reps):
+                    m(ins[i], fused=mode)
+                b.record(stream)
+                torch.cuda.synchronize()
+                rows["fused_ms" if mode else "composed_ms"] = a.elapsed_time(b) / reps
+            rows["pixel_events"] = int(ins[i]["time"].numel())
+            rows["speedup"] = rows["composed_ms"] / rows["fused_ms"]
+            big[n] = rows
+    n_ev = int(ln.sum())
+    return {"workload": "MOS_S backbone forward on 8 Gen1 windows (C5-like, synthetic): preprocess + 8 MosAttention "
+                        "(hidden 12/24/48/96) + 3 x (SparseMaxPool k2 + TemporalDropout 4)",
+            "metric": "MOS_S backbone events/s", "value": n_ev / (ms * 1e-3), "unit": "events/s", "ms_per_call": ms,
+            "events_in": n_ev, "events_out": int(out["lengths"].sum()), "ms_per_step": per,
+            "hidden_48_96_fused_vs_composed": big}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -737,7 +819,7 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--only", choices=["chunk", "c1", "sparse", "sparse_batched", "pool", "pool_sorted", "chunk_bwd",
-                                       "event_stage", "async_step"], default=None,
+                                       "event_stage", "async_step", "mos_s"], default=None,
                     help="run one workload and print its line (profiling runs; --no-cpu-baseline skips "
                          "the CPU legs where a line has one)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -771,6 +853,9 @@ def main(argv=None):
         return 0
     if args.only == "sparse_batched":
         print(json.dumps(bench_sparse_batched(torch, lib, args.steps, dev)), flush=True)
+        return 0
+    if args.only == "mos_s":
+        print(json.dumps(bench_mos_backbone(torch, lib, args.steps, dev)), flush=True)
         return 0
     if args.only == "event_stage":
         print(json.dumps(bench_event_stage(torch, lib, args.steps, dev)), flush=True)
@@ -809,7 +894,8 @@ def main(argv=None):
                              bench_sparse_batched(torch, lib, 10, dev), bench_pool(torch, lib, 20, dev),
                              bench_pool(torch, lib, 20, dev, sorted_index=True),
                              bench_async_step(torch, lib, dev, cpu=not args.no_cpu_baseline),
-                             bench_chunk_bwd(torch, lib, 10, dev), bench_event_stage(torch, lib, 5, dev)]
+                             bench_chunk_bwd(torch, lib, 10, dev), bench_event_stage(torch, lib, 5, dev),
+                             bench_mos_backbone(torch, lib, 5, dev)]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(r["sample"])
     print(json.dumps(line), flush=True)

@@ -624,7 +624,8 @@ extern "C" int ssla_mos_attention_fwd(const float *events, int64_t n_events, int
   SSLA_CHECK_ARG(n_rows == 0 || (row_src && row_pos && patch_len), "mos_attention_fwd: null row arrays");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (path == 2) {
-    SSLA_CHECK_ARG(aligned(events, 16), "mos_attention_fwd: events must be 16-byte aligned");
+    SSLA_CHECK_ARG(aligned(events, 16) && (!w_in || aligned(w_in, 16)),
+                   "mos_attention_fwd: events and w_in must be 16-byte aligned");
     return mosm::forward(events, n_events, c_in, row_src, row_pos, n_rows, patch_len, n_patches, A, w_scatter, As,
                          w_q, w_v, w_g, w_o, w_gather, Ag, w_in, ln_w, ln_b, eps, hidden, out, workspace,
                          workspace_bytes, st);

@@ -4,22 +4,26 @@
 // Same computation as the fused kernels of mos_attention.hip (reference
 // layers/mos_attention.py:75-167: scatter projection, q/v/g, sigmoid, the
 // scan over every patch, o_proj, gather projection, the sum over an event's
-// copies, residual, LayerNorm), but the projections run as GEMMs over the
-// patch rows bucketed by kernel position instead of one lane per row:
-// * the per-position matrices are folded once per call:
-//   Wa[a] = [Wq; Wv; Wg] Ws[a]  ([3H, Cin]) and Wb[a] = Wgp[a] Wo ([H, H]);
-// * the rows are bucketed by position with a stable device radix sort (no
-//   host synchronisation) and cut into tiles of 64 rows of one position;
-// * mos_gemm_kernel runs each tile against its position's matrix with
-//   v_mfma_f32_16x16x4_f32 (fp32 operands: exact products, fp32 sums), the
-//   first time gathering the rows' events and splitting the result into q,
-//   v and sigmoid(g), the second time taking q * h as its input;
-// * the varlen diagonal scan h = a h + v runs per patch (diag_scan.hip);
-// * mos_rows_event_kernel sums every event's copies in increasing patch
-//   order (decreasing kernel position, the order index_add_ visits them),
-//   adds the residual (or its input projection) and applies LayerNorm, one
-//   wavefront per event.
-// All values are fp32; the row buffers (q, v, a, h, z) live in the workspace.
+// copies, residual, LayerNorm), with the projections as GEMMs over the pixel
+// events instead of one lane per patch row.  Row r of the patch layout is
+// the copy of pixel event src[r] at kernel position pos[r]; dst[e A + a] is
+// the inverse map (or -1).
+// * fold_kernel: the per-position matrices, once per call,
+//     Wa[a] = [Wq; Wv; Wg] Ws[a]  ([3H, Cin]),  Wb[a] = Wgp[a] Wo  ([H, H]).
+// * mos_in_kernel: [E, Cin] x [Cin, A 3H] (one shared Wa when the scatter
+//   projection is shared), each output element (e, a, n) written to row
+//   dst[e A + a] as q, v or sigmoid(g).  The events are read in order; no
+//   row sort or gather.
+// * mos_scan_kernel: h = a h + v along each patch's rows (zero start), and
+//   q h written over q.
+// * mos_out_kernel: per event, y = sum over a of Wb[a] (q h)[dst[e A + a]]
+//   (+ Win e, or + e), i.e. [E, A H (+ Cin)] x [A H (+ Cin), H] with the
+//   rows gathered, then LayerNorm over the event's H outputs in the same
+//   workgroup.
+// Products are v_mfma_f32_16x16x4_f32 (fp32 operands, exact products, fp32
+// sums); the summation order differs from the reference's row by row
+// GEMMs and index_add_ by rounding only.  q / v / a (then q h) live in the
+// workspace as [R, H] fp32.
 #include <cstring>
 #include <rocprim/rocprim.hpp>
 
@@ -30,11 +34,11 @@ namespace mosm {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kTile = 64;     // rows per GEMM tile
-constexpr int kCols = 64;     // columns per GEMM tile
+constexpr int kTile = 64;     // events per GEMM tile
+constexpr int kCols = 64;     // output columns per tile of the input GEMM
 constexpr int kKc = 16;       // reduction elements staged per step
 constexpr int kPad = 4;       // LDS row padding (floats)
-constexpr int kMaxEventWgs = 2048;
+constexpr int kMaxPosM = 49;  // kernel positions
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 inline unsigned grid_for(int64_t n) {
@@ -47,14 +51,8 @@ inline unsigned grid_for(int64_t n) {
 struct Ws {
   int64_t *cu;         // [P + 1] patch row offsets
   int32_t *dst;        // [E * A] row of (event, position), or -1
-  uint64_t *keys;      // [R] sorted positions
-  int32_t *perm;       // [R] original row of each sorted position
-  int64_t *boff;       // [A + 1] first sorted row of each position
-  int64_t *toff;       // [A + 1] first tile of each position
   float *wa, *wb;      // folded matrices
-  float *q, *v, *a, *h, *z;   // [R, H] each
-  void *sort_tmp;
-  size_t sort_bytes;
+  float *q, *v, *a;    // [R, H] each; q h replaces q after the scan
   void *scan_tmp;
   size_t scan_bytes;
   size_t total;
@@ -68,7 +66,7 @@ size_t excl_scan_bytes(int64_t n) {
   return tb;
 }
 
-Ws layout(void *base, int64_t E, int cin, int H, int A, int As, int Ag, int64_t R, int64_t P) {
+Ws layout(void *base, int64_t E, int cin, int H, int A, int64_t R, int64_t P) {
   char *b = static_cast<char *>(base);
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -79,16 +77,10 @@ Ws layout(void *base, int64_t E, int cin, int H, int A, int As, int Ag, int64_t 
   Ws w;
   w.cu = reinterpret_cast<int64_t *>(take(sizeof(int64_t) * (P + 1)));
   w.dst = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * static_cast<size_t>(E) * A));
-  w.keys = reinterpret_cast<uint64_t *>(take(sizeof(uint64_t) * R));
-  w.perm = reinterpret_cast<int32_t *>(take(sizeof(int32_t) * R));
-  w.boff = reinterpret_cast<int64_t *>(take(sizeof(int64_t) * (A + 1)));
-  w.toff = reinterpret_cast<int64_t *>(take(sizeof(int64_t) * (A + 1)));
-  w.wa = reinterpret_cast<float *>(take(sizeof(float) * static_cast<size_t>(As) * 3 * H * cin));
-  w.wb = reinterpret_cast<float *>(take(sizeof(float) * static_cast<size_t>(Ag) * H * H));
-  float **rows[5] = {&w.q, &w.v, &w.a, &w.h, &w.z};
+  w.wa = reinterpret_cast<float *>(take(sizeof(float) * static_cast<size_t>(A) * 3 * H * cin));
+  w.wb = reinterpret_cast<float *>(take(sizeof(float) * static_cast<size_t>(A) * H * H));
+  float **rows[3] = {&w.q, &w.v, &w.a};
   for (float **r : rows) *r = reinterpret_cast<float *>(take(sizeof(float) * static_cast<size_t>(R) * H));
-  w.sort_bytes = ssla_sort_pairs_workspace_size(R);
-  w.sort_tmp = take(w.sort_bytes);
   w.scan_bytes = excl_scan_bytes(P);
   w.scan_tmp = take(w.scan_bytes);
   w.total = off;
@@ -110,110 +102,65 @@ __global__ void dst_fill(const int64_t *__restrict__ src, const int64_t *__restr
 
 // Wa[a][n][c] = sum_j Wqvg[n][j] Ws[a][j][c]  (Wqvg = [Wq; Wv; Wg], [3H, H])
 // Wb[a][n][c] = sum_j Wgp[a][n][j] Wo[j][c]
+// Four independent partial sums, so a thread's loads are not one chain.
 __global__ void fold_kernel(const float *__restrict__ ws, int As, const float *__restrict__ wq,
                             const float *__restrict__ wv, const float *__restrict__ wg, const float *__restrict__ wo,
                             const float *__restrict__ wgp, int Ag, int cin, int H, float *__restrict__ wa,
                             float *__restrict__ wb) {
   const int64_t na = static_cast<int64_t>(As) * 3 * H * cin, nb = static_cast<int64_t>(Ag) * H * H;
   MOSM_GRID_STRIDE(i, na + nb) {
-    float acc = 0.f;
+    const float *w1, *w2;
+    int64_t stride;
     if (i < na) {
       const int c = static_cast<int>(i % cin);
       const int n = static_cast<int>((i / cin) % (3 * H));
       const int64_t a = i / (static_cast<int64_t>(cin) * 3 * H);
-      const float *w1 = (n < H ? wq : n < 2 * H ? wv : wg) + static_cast<int64_t>(n % H) * H;
-      const float *w2 = ws + a * H * cin + c;
-      for (int j = 0; j < H; ++j) acc = fmaf(w1[j], w2[static_cast<int64_t>(j) * cin], acc);
-      wa[i] = acc;
+      w1 = (n < H ? wq : n < 2 * H ? wv : wg) + static_cast<int64_t>(n % H) * H;
+      w2 = ws + a * H * cin + c;
+      stride = cin;
     } else {
       const int64_t k = i - na;
       const int c = static_cast<int>(k % H);
       const int n = static_cast<int>((k / H) % H);
       const int64_t a = k / (static_cast<int64_t>(H) * H);
-      const float *w1 = wgp + (a * H + n) * H;
-      for (int j = 0; j < H; ++j) acc = fmaf(w1[j], wo[static_cast<int64_t>(j) * H + c], acc);
-      wb[k] = acc;
+      w1 = wgp + (a * H + n) * H;
+      w2 = wo + c;
+      stride = H;
     }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int j = 0;
+    for (; j + 4 <= H; j += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] = fmaf(w1[j + u], w2[(j + u) * stride], acc[u]);
+    }
+    for (; j < H; ++j) acc[0] = fmaf(w1[j], w2[j * stride], acc[0]);
+    const float s = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    if (i < na) wa[i] = s;
+    else wb[i - na] = s;
   }
 }
 
-// boff[a] = first sorted row with position >= a (a = 0..A), toff[a] = tiles
-// of the positions before a (kTile rows each); one workgroup.
-__global__ void bucket_kernel(const uint64_t *__restrict__ keys, int64_t R, int A, int64_t *__restrict__ boff,
-                              int64_t *__restrict__ toff) {
-  __shared__ int64_t s_b[64];
-  const int a = threadIdx.x;
-  if (a <= A) {
-    int64_t lo = 0, hi = R;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
-      if (keys[mid] < static_cast<uint64_t>(a)) lo = mid + 1;
-      else hi = mid;
-    }
-    s_b[a] = lo;
-    boff[a] = lo;
-  }
-  __syncthreads();
-  if (a == 0) {
-    int64_t t = 0;
-    for (int p = 0; p < A; ++p) {
-      toff[p] = t;
-      t += (s_b[p + 1] - s_b[p] + kTile - 1) / kTile;
-    }
-    toff[A] = t;
-  }
-}
-
-// The last index j in [0, n) with off[j] <= x (off non-decreasing).
-__device__ __forceinline__ int last_le(const int64_t *off, int n, int64_t x) {
-  int lo = 0, hi = n - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (off[mid] <= x) lo = mid;
-    else hi = mid - 1;
-  }
-  return lo;
-}
-
-enum { kLoadGather = 0, kLoadQH = 1 };
-enum { kEpiQVA = 0, kEpiOut = 1 };
-
-// One workgroup per (tile of kTile sorted rows of one position, kCols
-// output columns); the four wavefronts own 32 x 32 quarters (2 x 2 MFMA
-// tiles of 16 x 16).  Each step stages kKc reduction elements of the rows
-// and of the weight rows in LDS (one 16-byte piece per thread each).
 // v_mfma_f32_16x16x4_f32 operand layout: lane l holds A[l % 16][l / 16] and
 // B[l / 16][l % 16]; the accumulator holds D[4 (l / 16) + i][l % 16].
-template <int LOAD, int EPI>
-__global__ __launch_bounds__(kThreads) void mos_gemm_kernel(
-    const float *__restrict__ X, const float *__restrict__ X2, const int64_t *__restrict__ src, int64_t n_x,
-    const int32_t *__restrict__ perm, const int64_t *__restrict__ boff, const int64_t *__restrict__ toff, int A,
-    const float *__restrict__ W, int per_pos, int N, int Kd, int H, float *__restrict__ o0,
-    float *__restrict__ o1, float *__restrict__ o2) {
+
+// The input GEMM.  Workgroup: (tile of kTile events, kCols columns of the
+// As x 3H outputs); the four wavefronts own 32 x 32 quarters (2 x 2 MFMA
+// tiles).  Each step stages kKc input channels of the events and of the
+// weight rows in LDS, one 16-byte piece per thread each.  Column n' of the
+// outputs is position a = n' / 3H (0 when the projection is shared: then
+// every copy of the event takes the same value) and channel n = n' % 3H:
+// q (n < H), v, or sigmoid(g) (n >= 2H), written to row dst[e A + a].
+__global__ __launch_bounds__(kThreads) void mos_in_kernel(
+    const float *__restrict__ X, int64_t E, int cin, const float *__restrict__ W, int As, int H, int A,
+    const int32_t *__restrict__ dst, float *__restrict__ oq, float *__restrict__ ov, float *__restrict__ oa) {
   __shared__ __align__(16) float xs[kTile][kKc + kPad];
   __shared__ __align__(16) float wsm[kCols][kKc + kPad];
-  __shared__ int32_t s_orig[kTile];
-  __shared__ int64_t s_row[kTile];
-  const int64_t t = blockIdx.x;
-  if (t >= toff[A]) return;   // past the actual tile count (uniform over the workgroup)
-  const int a = last_le(toff, A + 1, t);
-  const int64_t r0 = boff[a] + (t - toff[a]) * kTile;
-  const int nr = static_cast<int>(min(static_cast<int64_t>(kTile), boff[a + 1] - r0));
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  const int N1 = 3 * H, N = As * N1;
   const int c0 = blockIdx.y * kCols;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  if (tid < kTile) {
-    const int32_t o = tid < nr ? perm[r0 + tid] : -1;
-    s_orig[tid] = o;
-    int64_t row = -1;
-    if (o >= 0) row = LOAD == kLoadGather ? src[o] : o;
-    if (LOAD == kLoadGather && (row < 0 || row >= n_x)) row = -1;
-    s_row[tid] = row;
-  }
-  __syncthreads();
-  const float *Wa = W + (per_pos ? static_cast<int64_t>(a) * N * Kd : 0);
-  // staging: thread tid loads piece (row tid / 4, elements 4 (tid % 4) .. +3)
   const int sr = tid >> 2, sk = 4 * (tid & 3);
-  const int64_t xrow = s_row[sr];
+  const int64_t xe = e0 + sr;
   const int wcol = c0 + sr;
   f32x4 acc[2][2];
 #pragma unroll
@@ -221,15 +168,12 @@ __global__ __launch_bounds__(kThreads) void mos_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
   const int rb = 32 * (wv & 1), cb = 32 * (wv >> 1);
-  for (int k0 = 0; k0 < Kd; k0 += kKc) {
+  for (int k0 = 0; k0 < cin; k0 += kKc) {
     const int k = k0 + sk;
     f32x4 xv = {0.f, 0.f, 0.f, 0.f}, wvv = {0.f, 0.f, 0.f, 0.f};
-    if (k < Kd) {   // Kd is a multiple of 4: a piece is all in or all out
-      if (xrow >= 0) {
-        xv = *reinterpret_cast<const f32x4 *>(X + xrow * Kd + k);
-        if (LOAD == kLoadQH) xv *= *reinterpret_cast<const f32x4 *>(X2 + xrow * Kd + k);
-      }
-      if (wcol < N) wvv = *reinterpret_cast<const f32x4 *>(Wa + static_cast<int64_t>(wcol) * Kd + k);
+    if (k < cin) {   // cin is a multiple of 4: a piece is all in or all out
+      if (xe < E) xv = *reinterpret_cast<const f32x4 *>(X + xe * cin + k);
+      if (wcol < N) wvv = *reinterpret_cast<const f32x4 *>(W + static_cast<int64_t>(wcol) * cin + k);
     }
     __syncthreads();   // the previous step's operand reads are done
     *reinterpret_cast<f32x4 *>(&xs[sr][sk]) = xv;
@@ -249,106 +193,241 @@ __global__ __launch_bounds__(kThreads) void mos_gemm_kernel(
         for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
   }
-  // epilogue: element (row rb + 16 i + 4 (lane / 16) + e, column cb + 16 j + lane % 16)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = c0 + cb + 16 * j + (lane & 15);
+    if (col >= N) continue;
+    const int a = col / N1, n = col - a * N1;
+    float *o = n < H ? oq : n < 2 * H ? ov : oa;
+    const int ch = n < H ? n : n < 2 * H ? n - H : n - 2 * H;
+    const bool sig = n >= 2 * H;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t ev = e0 + rb + 16 * i + 4 * (lane >> 4) + e;
+        if (ev >= E) continue;
+        float val = acc[i][j][e];
+        if (sig) val = __builtin_amdgcn_rcpf(1.f + fast_exp2(-val * kLog2e));
+        if (As > 1) {
+          const int32_t r = dst[ev * A + a];
+          if (r >= 0) o[static_cast<int64_t>(r) * H + ch] = val;
+        } else {
+          for (int p = 0; p < A; ++p) {
+            const int32_t r = dst[ev * A + p];
+            if (r >= 0) o[static_cast<int64_t>(r) * H + ch] = val;
+          }
+        }
+      }
+  }
+}
+
+// h = a h + v along the rows of each patch (zero start), then q <- q h.
+// One wavefront per patch; lane l holds channels l and l + 64.  The loads of
+// kU rows go out before their serial fma chain.
+constexpr int kU = 4;
+__global__ __launch_bounds__(kThreads) void mos_scan_kernel(const int64_t *__restrict__ cu, int64_t P, int64_t R,
+                                                            int H, float *__restrict__ q, const float *__restrict__ v,
+                                                            const float *__restrict__ a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  if (p >= P) return;
+  const int64_t bos = min(max(cu[p], int64_t{0}), R), eos = min(max(cu[p + 1], bos), R);
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int c = lane + 64 * half;
+    if (c >= H) break;
+    float h = 0.f;
+    int64_t t = bos;
+    for (; t + kU <= eos; t += kU) {
+      float vv[kU], aa[kU], qq[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t o = (t + u) * H + c;
+        vv[u] = v[o];
+        aa[u] = a[o];
+        qq[u] = q[o];
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        h = fmaf(aa[u], h, vv[u]);
+        q[(t + u) * H + c] = qq[u] * h;
+      }
+    }
+    for (; t < eos; ++t) {
+      const int64_t o = t * H + c;
+      h = fmaf(a[o], h, v[o]);
+      q[o] = q[o] * h;
+    }
+  }
+}
+
+// The output GEMM with the copy sum, residual and LayerNorm.  Workgroup:
+// kTile events x all HP (H padded to a multiple of 32) outputs; wavefront w
+// owns rows 32 (w & 1) .. +31 and columns (HP / 2) (w >> 1) .. + HP / 2 - 1
+// (2 x HP / 32 MFMA tiles).  The reduction runs over the positions a (the H
+// channels of row dst[e A + a] of q h, zero for a missing copy, against
+// Wb[a]) and then, with an input projection, over the event's Cin inputs
+// against Win.  Each step stages kKc reduction elements.
+template <int HP>
+__global__ __launch_bounds__(kThreads) void mos_out_kernel(
+    const float *__restrict__ qh, int64_t R, const float *__restrict__ X, int64_t E, int cin, int H, int A,
+    const int32_t *__restrict__ dst, const float *__restrict__ Wb, int Ag, const float *__restrict__ win,
+    const float *__restrict__ ln_w, const float *__restrict__ ln_b, float eps, float *__restrict__ out) {
+  constexpr int NT = HP / 32;            // column tiles per wavefront
+  constexpr int NW = (HP + 63) / 64;     // weight pieces staged per thread
+  __shared__ __align__(16) float xs[kTile][kKc + kPad];
+  __shared__ __align__(16) float wsm[HP][kKc + kPad];
+  __shared__ int32_t s_dst[kTile * kMaxPosM];
+  __shared__ float s_part[2][kTile];
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  for (int i = tid; i < kTile * A; i += kThreads) {
+    const int64_t e = e0 + i / A;
+    const int32_t r = e < E ? dst[e0 * A + i] : -1;
+    s_dst[i] = (r >= 0 && r < R) ? r : -1;
+  }
+  const int sr = tid >> 2, sk = 4 * (tid & 3);
+  f32x4 acc[2][NT];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = rb + 16 * i + 4 * (lane >> 4) + e;
-      if (row >= nr) continue;
-      const int64_t o = s_orig[row];
+    for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const int rb = 32 * (wv & 1), cb = (HP / 2) * (wv >> 1);
+  const int steps_h = (H + kKc - 1) / kKc;
+  const int steps_in = win ? (cin + kKc - 1) / kKc : 0;
+  const int n_steps = A * steps_h + steps_in;
+  __syncthreads();   // s_dst
+  for (int s = 0; s < n_steps; ++s) {
+    const bool res = s >= A * steps_h;
+    const int a = res ? 0 : s / steps_h;
+    const int k = (res ? (s - A * steps_h) : (s - a * steps_h)) * kKc + sk;
+    const int kd = res ? cin : H;
+    f32x4 xv = {0.f, 0.f, 0.f, 0.f};
+    if (k < kd) {   // H and cin are multiples of 4: a piece is all in or all out
+      if (res) {
+        const int64_t e = e0 + sr;
+        if (e < E) xv = *reinterpret_cast<const f32x4 *>(X + e * cin + k);
+      } else {
+        const int32_t r = s_dst[sr * A + a];
+        if (r >= 0) xv = *reinterpret_cast<const f32x4 *>(qh + static_cast<int64_t>(r) * H + k);
+      }
+    }
+    const float *Wk = res ? win : Wb + (Ag > 1 ? static_cast<int64_t>(a) * H * H : 0);
+    f32x4 wr[NW];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = c0 + cb + 16 * j + (lane & 15);
-        if (col >= N) continue;
-        const float val = acc[i][j][e];
-        if (EPI == kEpiQVA) {
-          if (col < H) o0[o * H + col] = val;
-          else if (col < 2 * H) o1[o * H + col - H] = val;
-          else o2[o * H + col - 2 * H] = __builtin_amdgcn_rcpf(1.f + fast_exp2(-val * kLog2e));   // sigmoid
-        } else {
-          o0[o * N + col] = val;
+    for (int p = 0; p < NW; ++p) {
+      const int n = sr + 64 * p;
+      wr[p] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      if (n < H && k < kd) wr[p] = *reinterpret_cast<const f32x4 *>(Wk + static_cast<int64_t>(n) * kd + k);
+    }
+    __syncthreads();   // the previous step's operand reads are done
+    *reinterpret_cast<f32x4 *>(&xs[sr][sk]) = xv;
+#pragma unroll
+    for (int p = 0; p < NW; ++p)
+      if (sr + 64 * p < HP) *reinterpret_cast<f32x4 *>(&wsm[sr + 64 * p][sk]) = wr[p];
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kKc / 4; ++kk) {
+      const int kl = 4 * kk + (lane >> 4);
+      float av[2], bv[NT];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) av[i] = xs[rb + 16 * i + (lane & 15)][kl];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) bv[j] = wsm[cb + 16 * j + (lane & 15)][kl];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  // identity residual (cin == H)
+  if (!win) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t ev = e0 + rb + 16 * i + 4 * (lane >> 4) + e;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int col = cb + 16 * j + (lane & 15);
+          if (ev < E && col < H) acc[i][j][e] += X[ev * cin + col];
         }
       }
-    }
-}
-
-// Pixel events, one wavefront each (grid-stride): y = the sum of the
-// event's copies' rows z (decreasing kernel position), plus the residual
-// (Win e, or e), then LayerNorm; lane l holds channels l and l + 64.  With an
-// input projection its transpose is staged in LDS (WinT[c][j], H * cin
-// floats), so the lanes of a wavefront read consecutive words.
-__global__ __launch_bounds__(kThreads) void mos_rows_event_kernel(
-    const float *__restrict__ ev, int64_t E, int cin, int H, int A, const int32_t *__restrict__ dst,
-    const float *__restrict__ z, int64_t R, const float *__restrict__ win, const float *__restrict__ ln_w,
-    const float *__restrict__ ln_b, float eps, float *__restrict__ out) {
-  extern __shared__ float win_t[];
-  if (win) {
-    for (int i = threadIdx.x; i < H * cin; i += kThreads) {
-      const int j = i / cin, c = i - j * cin;
-      win_t[c * H + j] = win[i];
+  }
+  // LayerNorm over the columns < H: row sums over the 16 lanes of a lane
+  // group, then over the two column halves through LDS; the mean first,
+  // then the mean square deviation from it.
+  float mean[2][4] = {}, rstd[2][4] = {};
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    float part[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int col = cb + 16 * j + (lane & 15);
+          const float y = acc[i][j][e];
+          const float d = pass == 0 ? y : (y - mean[i][e]) * (y - mean[i][e]);
+          s += col < H ? d : 0.f;
+        }
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m);
+        part[i][e] = s;
+      }
+    __syncthreads();   // the previous pass's reads of s_part are done
+    if ((lane & 15) == 0) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s_part[wv >> 1][rb + 16 * i + 4 * (lane >> 4) + e] = part[i][e];
     }
     __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = rb + 16 * i + 4 * (lane >> 4) + e;
+        const float tot = s_part[0][row] + s_part[1][row];
+        if (pass == 0) mean[i][e] = tot / static_cast<float>(H);
+        else rstd[i][e] = 1.f / sqrtf(tot / static_cast<float>(H) + eps);
+      }
   }
-  const int lane = threadIdx.x & 63;
-  const int j0 = lane, j1 = lane + 64;
-  const bool ok0 = j0 < H, ok1 = j1 < H;
-  const float lw0 = ok0 ? ln_w[j0] : 0.f, lb0 = ok0 ? ln_b[j0] : 0.f;
-  const float lw1 = ok1 ? ln_w[j1] : 0.f, lb1 = ok1 ? ln_b[j1] : 0.f;
-  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * (kThreads / 64);
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6); e < E; e += n_waves) {
-    float y0 = 0.f, y1 = 0.f;
-    for (int pa = A - 1; pa >= 0; --pa) {
-      const int32_t r = dst[e * A + pa];
-      if (r >= 0 && r < R) {
-        if (ok0) y0 += z[static_cast<int64_t>(r) * H + j0];
-        if (ok1) y1 += z[static_cast<int64_t>(r) * H + j1];
-      }
-    }
-    const float *x = ev + e * cin;
-    if (win) {
-      float r0 = 0.f, r1 = 0.f;
-      for (int c = 0; c < cin; ++c) {
-        const float xc = x[c];
-        if (ok0) r0 = fmaf(win_t[c * H + j0], xc, r0);
-        if (ok1) r1 = fmaf(win_t[c * H + j1], xc, r1);
-      }
-      y0 += r0;
-      y1 += r1;
-    } else {
-      if (ok0) y0 += x[j0];
-      if (ok1) y1 += x[j1];
-    }
-    float s = (ok0 ? y0 : 0.f) + (ok1 ? y1 : 0.f);
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
-    const float mean = s / static_cast<float>(H);
-    const float d0 = ok0 ? y0 - mean : 0.f, d1 = ok1 ? y1 - mean : 0.f;
-    float v = d0 * d0 + d1 * d1;
+  for (int j = 0; j < NT; ++j) {
+    const int col = cb + 16 * j + (lane & 15);
+    if (col >= H) continue;
+    const float lw = ln_w[col], lb = ln_b[col];
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    const float rstd = 1.f / sqrtf(v / static_cast<float>(H) + eps);
-    if (ok0) out[e * H + j0] = d0 * rstd * lw0 + lb0;
-    if (ok1) out[e * H + j1] = d1 * rstd * lw1 + lb1;
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t ev = e0 + rb + 16 * i + 4 * (lane >> 4) + e;
+        if (ev < E) out[ev * H + col] = (acc[i][j][e] - mean[i][e]) * rstd[i][e] * lw + lb;
+      }
   }
 }
 
 }  // namespace
 
 bool supported(int cin, int H, int A) {
-  return cin > 0 && H > 0 && cin <= 128 && H <= 128 && cin % 4 == 0 && H % 4 == 0 && A > 0 && A <= 63;
+  return cin > 0 && H > 0 && cin <= 128 && H <= 128 && cin % 4 == 0 && H % 4 == 0 && A > 0 && A <= kMaxPosM;
 }
 
-// LDS of the largest kernel: the GEMM tiles, or the event kernel's
-// transposed input projection (present when cin != H).
+// LDS of the largest kernel (the output GEMM at the padded hidden size).
 size_t lds_bytes(int cin, int H) {
-  const size_t gemm = sizeof(float) * (kTile + kCols) * (kKc + kPad) + (sizeof(int32_t) + sizeof(int64_t)) * kTile;
-  const size_t ev = cin != H ? sizeof(float) * cin * H : 0;
-  return std::max(gemm, ev);
+  (void)cin;
+  const size_t hp = (H + 31) / 32 * 32;
+  return sizeof(float) * (kTile + hp) * (kKc + kPad) + sizeof(int32_t) * kTile * kMaxPosM +
+         sizeof(float) * 2 * kTile;
 }
 
 size_t workspace_bytes(int64_t E, int cin, int H, int A, int64_t R, int64_t P) {
-  return layout(nullptr, E, cin, H, A, A, A, R, P).total;
+  return layout(nullptr, E, cin, H, A, R, P).total;
 }
 
 int forward(const float *events, int64_t E, int cin, const int64_t *row_src, const int64_t *row_pos, int64_t R,
@@ -356,12 +435,17 @@ int forward(const float *events, int64_t E, int cin, const int64_t *row_src, con
             const float *w_v, const float *w_g, const float *w_o, const float *w_gather, int Ag, const float *w_in,
             const float *ln_w, const float *ln_b, float eps, int H, float *out, void *workspace,
             size_t workspace_bytes_given, hipStream_t st) {
-  const Ws w = layout(workspace, E, cin, H, A, A, A, R, P);
+  const Ws w = layout(workspace, E, cin, H, A, R, P);
   if (!workspace || workspace_bytes_given < w.total) {
     set_error("mos_attention_fwd: workspace of %zu bytes needed, %zu given", w.total, workspace_bytes_given);
     return SSLA_ERR_WORKSPACE;
   }
   if (E == 0) return SSLA_OK;
+  const int64_t tiles = (E + kTile - 1) / kTile;
+  if (tiles > 0x7fffffff) {
+    set_error("mos_attention_fwd: too many events");
+    return SSLA_ERR_UNSUPPORTED;
+  }
   hipLaunchKernelGGL(fill_i32, dim3(grid_for(E * A)), dim3(kThreads), 0, st, w.dst, E * A, -1);
   if (R > 0) {
     if (P > 0) {
@@ -374,40 +458,31 @@ int forward(const float *events, int64_t E, int cin, const int64_t *row_src, con
       }
     }
     hipLaunchKernelGGL(dst_fill, dim3(grid_for(R)), dim3(kThreads), 0, st, row_src, row_pos, R, E, A, w.dst, w.cu, P);
-    const int64_t nf = static_cast<int64_t>(As) * 3 * H * cin + static_cast<int64_t>(Ag) * H * H;
-    hipLaunchKernelGGL(fold_kernel, dim3(grid_for(nf)), dim3(kThreads), 0, st, w_scatter, As, w_q, w_v, w_g, w_o,
-                       w_gather, Ag, cin, H, w.wa, w.wb);
-    // rows bucketed by position (stable), tiles of kTile rows per position
-    int end_bit = 1;
-    while ((1 << end_bit) < A) ++end_bit;
-    int s = ssla_sort_pairs(reinterpret_cast<const uint64_t *>(row_pos), nullptr, R, end_bit, w.keys, w.perm,
-                            w.sort_tmp, w.sort_bytes, st);
-    if (s) return s;
-    hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(64), 0, st, w.keys, R, A, w.boff, w.toff);
-    const int64_t tiles_max = R / kTile + A + 1;
-    if (tiles_max > 0x7fffffff) {
-      set_error("mos_attention_fwd: too many rows");
-      return SSLA_ERR_UNSUPPORTED;
-    }
-    // scatter projection folded with q / v / g: one bucket matrix per
-    // position (or one matrix for all when the projection is shared)
-    const int N1 = 3 * H;
-    hipLaunchKernelGGL((mos_gemm_kernel<kLoadGather, kEpiQVA>),
-                       dim3(static_cast<unsigned>(tiles_max), (N1 + kCols - 1) / kCols), dim3(kThreads), 0, st,
-                       events, nullptr, row_src, E, w.perm, w.boff, w.toff, A, w.wa, As > 1 ? 1 : 0, N1, cin, H, w.q,
-                       w.v, w.a);
-    s = ssla_diag_scan_fwd(w.v, w.a, w.cu, static_cast<int>(P), R, H, w.h, st);
-    if (s) return s;
-    // o_proj folded with the gather projection, on q * h
-    hipLaunchKernelGGL((mos_gemm_kernel<kLoadQH, kEpiOut>),
-                       dim3(static_cast<unsigned>(tiles_max), (H + kCols - 1) / kCols), dim3(kThreads), 0, st, w.q,
-                       w.h, nullptr, R, w.perm, w.boff, w.toff, A, w.wb, Ag > 1 ? 1 : 0, H, H, H, w.z, nullptr,
-                       nullptr);
   }
-  const int64_t blocks = std::min<int64_t>((E + kThreads / 64 - 1) / (kThreads / 64), kMaxEventWgs);
-  const size_t lds = w_in ? sizeof(float) * H * cin : 0;
-  hipLaunchKernelGGL(mos_rows_event_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, st, events, E,
-                     cin, H, A, w.dst, w.z, R, w_in, ln_w, ln_b, eps, out);
+  const int64_t nf = static_cast<int64_t>(As) * 3 * H * cin + static_cast<int64_t>(Ag) * H * H;
+  hipLaunchKernelGGL(fold_kernel, dim3(grid_for(nf)), dim3(kThreads), 0, st, w_scatter, As, w_q, w_v, w_g, w_o,
+                     w_gather, Ag, cin, H, w.wa, w.wb);
+  if (R > 0) {
+    const int N = As * 3 * H;
+    hipLaunchKernelGGL(mos_in_kernel, dim3(static_cast<unsigned>(tiles), (N + kCols - 1) / kCols), dim3(kThreads), 0,
+                       st, events, E, cin, w.wa, As, H, A, w.dst, w.q, w.v, w.a);
+    if (P > 0) {
+      const int64_t blocks = (P + kThreads / 64 - 1) / (kThreads / 64);
+      if (blocks > 0x7fffffff) {
+        set_error("mos_attention_fwd: too many patches");
+        return SSLA_ERR_UNSUPPORTED;
+      }
+      hipLaunchKernelGGL(mos_scan_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st, w.cu, P, R, H,
+                         w.q, w.v, w.a);
+    }
+  }
+  const int hp = (H + 31) / 32 * 32;
+#define MOSM_OUT(HPV)                                                                                              \
+  if (hp == HPV)                                                                                                   \
+    hipLaunchKernelGGL((mos_out_kernel<HPV>), dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, st, w.q, R,   \
+                       events, E, cin, H, A, w.dst, w.wb, Ag, w_in, ln_w, ln_b, eps, out);
+  MOSM_OUT(32) MOSM_OUT(64) MOSM_OUT(96) MOSM_OUT(128)
+#undef MOSM_OUT
   return launch_status("mos_attention_fwd");
 }
 

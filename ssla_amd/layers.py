@@ -135,8 +135,9 @@ class MosAttention(nn.Module):
 
     def _fused_ok(self, events):
         """The fused forward (ssla_mos_attention_fwd) runs when no gradient is
-        recorded and the weights fit its kernels (input, hidden <= 32, at most
-        49 kernel positions, weights within 64 KB of LDS)."""
+        recorded, the kernel has at most 49 positions and the sizes fit one of
+        its paths: input and hidden <= 32 with the weights within 64 KB of LDS,
+        or input and hidden multiples of 4 up to 128 (matrix cores)."""
         if torch.is_grad_enabled() and (events.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
         A = self.kernel_size[0] * self.kernel_size[1]
@@ -177,7 +178,8 @@ class MosAttention(nn.Module):
         use_fused = self._fused_ok(events) if fused is None else bool(fused)
         if use_fused:
             if fused and not self._fused_ok(events):
-                raise _lib.SslaError("fused MosAttention forward needs no grad, input and hidden sizes <= 32")
+                raise _lib.SslaError("fused MosAttention forward needs no grad, at most 49 kernel positions and input / "
+                                     "hidden sizes <= 32 or multiples of 4 up to 128")
             out = self._forward_fused(inputs, dev)
             return {"events": out, "time": inputs["time"], "w": inputs["w"], "h": inputs["h"],
                     "batch_id": inputs["batch_id"], "lengths": lengths, "batch_size": inputs["batch_size"]}

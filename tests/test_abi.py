@@ -107,7 +107,7 @@ def test_fused_mos_attention_limits():
     assert lib.ssla_mos_attention_lds_bytes(2, 12, 64, 1, 1) == 0
     for cin, hid in ((48, 48), (24, 48), (48, 96), (96, 96), (16, 32), (128, 128)):
         assert 0 < lib.ssla_mos_attention_lds_bytes(cin, hid, 9, 1, 1) <= 64 * 1024, (cin, hid)
-        assert lib.ssla_mos_attention_workspace_size(1000, cin, hid, 9, 5000, 800) > 5000 * hid * 4 * 5
+        assert lib.ssla_mos_attention_workspace_size(1000, cin, hid, 9, 5000, 800) >= 5000 * hid * 4 * 3
     for cin, hid in ((6, 48), (48, 132), (48, 50)):
         assert lib.ssla_mos_attention_lds_bytes(cin, hid, 9, 1, 1) == 0, (cin, hid)
 
