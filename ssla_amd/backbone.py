@@ -80,22 +80,40 @@ class SiteGLABlock(nn.Module):
         self.res_proj = nn.Linear(in_channels, out_channels, bias=False) if in_channels != out_channels else None
         self.norm = nn.LayerNorm(out_channels)
 
+    def _bf16(self) -> Dict[str, torch.Tensor]:
+        """bf16 copies of the projection weights, converted once and again
+        only when a weight changes (in-place updates bump its version, a
+        move or reassignment changes its storage)."""
+        mods = {"q": self.q_proj, "k": self.k_proj, "v": self.v_proj, "g": self.g_proj, "o": self.o_proj}
+        if self.res_proj is not None:
+            mods["r"] = self.res_proj
+        if torch.is_grad_enabled() and any(m.weight.requires_grad for m in mods.values()):
+            return {nm: m.weight.to(torch.bfloat16) for nm, m in mods.items()}   # differentiable, not cached
+        key = tuple((m.weight.data_ptr(), m.weight._version, m.weight.device) for m in mods.values())
+        cache = getattr(self, "_bf16_cache", None)
+        if cache is None or cache[0] != key:
+            with torch.no_grad():
+                cache = (key, {nm: m.weight.detach().to(torch.bfloat16) for nm, m in mods.items()})
+            self._bf16_cache = cache
+        return cache[1]
+
     def project(self, x: torch.Tensor):
         """q, k, v (bf16 ``[n, H, D]``) and log-gates g (fp32 ``[n, H, D]``)."""
         n = x.shape[0]
+        w = self._bf16()
         xb = x.to(torch.bfloat16)
         shp = (n, self.heads, self.head_dim)
-        q, k, v = (F.linear(xb, p.weight.to(torch.bfloat16)).view(shp)
-                   for p in (self.q_proj, self.k_proj, self.v_proj))
-        g = F.logsigmoid(F.linear(xb, self.g_proj.weight.to(torch.bfloat16)).float()) / self.gate_normalizer
+        q, k, v = (F.linear(xb, w[nm]).view(shp) for nm in ("q", "k", "v"))
+        g = F.logsigmoid(F.linear(xb, w["g"]).float()) / self.gate_normalizer
         return q, k, v, g.view(shp)
 
     def finish(self, o: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
         """LayerNorm(o_proj(o) + residual) in fp32 (projections in bf16)."""
         n = x.shape[0]
-        y = F.linear(o.reshape(n, -1), self.o_proj.weight.to(torch.bfloat16)).float()
+        w = self._bf16()
+        y = F.linear(o.reshape(n, -1), w["o"]).float()
         if self.res_proj is not None:
-            y = y + F.linear(x.to(torch.bfloat16), self.res_proj.weight.to(torch.bfloat16)).float()
+            y = y + F.linear(x.to(torch.bfloat16), w["r"]).float()
         else:
             y = y + x
         return self.norm(y)
@@ -160,7 +178,40 @@ class DetectionHead(nn.Module):
                          bn.eps)
         return F.silu(y)
 
-    def forward(self, xin: List[torch.Tensor]) -> torch.Tensor:
+    def forward(self, xin: List[torch.Tensor], graph: bool = True) -> torch.Tensor:
+        """The head on dense maps ``xin`` (``[B, C_l, H_l, W_l]`` per level).
+        Its ~60 small launches depend on nothing but the shapes, so on a GPU
+        without autograd (and with ``graph``) the first call for a shape
+        captures them once as a HIP graph that later calls replay: the
+        inputs are copied into the graph's buffers and its output is copied
+        out, so the result is the eager result bit for bit."""
+        if not (graph and xin and xin[0].is_cuda and not torch.is_grad_enabled()):
+            return self._forward_eager(xin)
+        key = (tuple((tuple(x.shape), x.dtype, x.device) for x in xin),
+               tuple((t.data_ptr(), t._version) for t in list(self.parameters()) + list(self.buffers())))
+        cache = getattr(self, "_graph_cache", None)
+        if cache is None or cache[0] != key:
+            cache = (key,) + self._capture(xin)
+            self._graph_cache = cache
+        _, gr, static_in, static_out = cache
+        for dst, src in zip(static_in, xin):
+            dst.copy_(src)
+        gr.replay()
+        return static_out.clone()
+
+    def _capture(self, xin: List[torch.Tensor]):
+        static_in = [x.detach().clone() for x in xin]
+        side = torch.cuda.Stream(device=static_in[0].device)
+        side.wait_stream(torch.cuda.current_stream(static_in[0].device))
+        with torch.cuda.stream(side):
+            self._forward_eager(static_in)   # warm-up: library handles and kernels loaded outside the capture
+        torch.cuda.current_stream(static_in[0].device).wait_stream(side)
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            static_out = self._forward_eager(static_in)
+        return gr, static_in, static_out
+
+    def _forward_eager(self, xin: List[torch.Tensor]) -> torch.Tensor:
         # A 1x1 convolution is a linear map of every cell's channels: the
         # maps are taken channel-last ([B * H * W, C], the order the outputs
         # are laid out in) and run as GEMMs; BatchNorm in eval mode and SiLU
@@ -224,7 +275,16 @@ class AsyncSparseGLA(nn.Module):
 
     def stem(self, events: torch.Tensor, lengths: torch.Tensor) -> Dict[str, torch.Tensor]:
         gr = E.preprocess_inputs(events, lengths, self.frame_size, self.hot_pixel_thres)
-        gr["events"] = F.linear(gr["events"].to(torch.bfloat16), self.embed.weight.to(torch.bfloat16)).float()
+        w = self.embed.weight
+        key = (w.data_ptr(), w._version, w.device)
+        cache = getattr(self, "_embed_bf16", None)
+        if torch.is_grad_enabled() and w.requires_grad:
+            cache = (None, w.to(torch.bfloat16))   # differentiable, not cached
+        elif cache is None or cache[0] != key:
+            with torch.no_grad():
+                cache = (key, w.detach().to(torch.bfloat16))
+            self._embed_bf16 = cache
+        gr["events"] = F.linear(gr["events"].to(torch.bfloat16), cache[1]).float()
         return self.stem_pool(gr)
 
     def forward(self, events: torch.Tensor, lengths: torch.Tensor, states: List[torch.Tensor], mark=None):

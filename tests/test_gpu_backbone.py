@@ -181,3 +181,28 @@ def test_async_step_full_size_properties(dev):
             y = f["events"]
             assert torch.isfinite(y).all()
             assert abs(float(y.mean())) < 0.1 and 0.8 < float(y.std()) < 1.2
+
+
+def test_head_graph_replays_match_eager(dev):
+    """The detection head's HIP-graph replay equals its eager run bit for
+    bit on every replay: new inputs each time, eager work and host syncs
+    between replays, and a re-capture after an in-place weight update."""
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(4)
+    model = AsyncSparseGLA().to(dev)
+    head = model.head
+    shapes = [(1, model.stages[i][0], *model.grid_sizes[i]) for i in model.head_levels]
+    gen = torch.Generator(device=dev).manual_seed(9)
+    with torch.no_grad():
+        for rep in range(5):
+            xin = [torch.randn(s, device=dev, generator=gen).to(torch.bfloat16) for s in shapes]
+            print(f"head graph replay {rep}", flush=True)
+            got = head(xin)
+            _ = torch.randn(1000, 1000, device=dev).sum()   # eager work between replays
+            torch.cuda.synchronize()
+            want = head(xin, graph=False)
+            assert torch.equal(got, want), f"replay {rep} differs from eager"
+        head.cls_preds[0].bias.add_(0.5)   # in place: the next call captures again
+        xin = [torch.randn(s, device=dev, generator=gen).to(torch.bfloat16) for s in shapes]
+        got = head(xin)
+        assert torch.equal(got, head(xin, graph=False)), "stale graph after a weight update"
