@@ -6,6 +6,8 @@
 // to ht.  One wavefront owns one (sequence, head, 16-column V tile); its 64
 // lanes are 4 key-groups x 16 value columns, each lane holding KPL rows of
 // the fp32 state.  The o reduction over the 4 key-groups is two xor-shuffles.
+#include <utility>
+
 #include "common.h"
 
 namespace ssla {
@@ -46,6 +48,7 @@ __device__ __forceinline__ void skip_sequence(void *o, int64_t bos, int64_t eos,
 // buffer resources and read as zeros (decay 1 and k = 0 leave the state
 // unchanged), and their outputs are not stored.
 constexpr int kSB = 16;   // steps per staged block
+constexpr int kFoldB = 2; // segment states folded per round trip
 
 template <int DT, int GDT, int KPL>
 struct Staged {
@@ -169,8 +172,39 @@ __global__ __launch_bounds__(256) void seg_offsets_kernel(const int64_t *__restr
   if (threadIdx.x == 0) segoff[n_seq] = carry;
 }
 
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile
+// time (the index is a constant expression inside f).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// x summed over the four 16-lane rows of the wavefront (lane l gets the
+// sum over lanes l mod 16 + 16 r), with v_permlane16_swap (rows 0 <-> 1,
+// 2 <-> 3) and v_permlane32_swap (halves): VALU lane swaps, no LDS.
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float sum_key_groups(float x) {
+  const u32x2 a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(a.x) + __uint_as_float(a.y);
+  const u32x2 b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(b.x) + __uint_as_float(b.y);
+}
+
+// One output element, rounded to nearest even by the conversion
+// instructions (no branches).
+template <int DT>
+__device__ __forceinline__ void store_out(void *o, int64_t i, float x) {
+  if constexpr (DT == SSLA_BF16) static_cast<__bf16 *>(o)[i] = static_cast<__bf16>(x);
+  else if constexpr (DT == SSLA_F16) static_cast<_Float16 *>(o)[i] = static_cast<_Float16>(x);
+  else static_cast<float *>(o)[i] = x;
+}
+
 template <int DT, int GDT, int KPL, int MODE>
-__global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
+__global__ __launch_bounds__(256, KPL <= 8 ? 4 : 2) void gla_recurrent_staged_kernel(
     const void *__restrict__ q, const void *__restrict__ k,
     const void *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int H, int V,
@@ -179,7 +213,7 @@ __global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
     int64_t T, int32_t *__restrict__ status, SegWs sw) {
   typedef Staged<DT, GDT, KPL> G;
   constexpr int K = G::K;
-  constexpr int U = 2;   // steps per group (kSB is a multiple)
+  constexpr int U = 1;   // steps per group (kSB / 2 is a multiple); more costs registers, not time
   __shared__ __align__(16) unsigned char smem[4][G::BYTES];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -234,11 +268,13 @@ __global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
 #pragma unroll
     for (int i = 0; i < KPL; ++i) S[i] = (src && col_ok) ? src[e0 + i * V] : 0.f;
     if (MODE == kSegOut) {
-      // fold the earlier segments' local states, eight per round trip
-      for (int64_t j0 = 0; j0 < seg; j0 += 8) {
-        float L[8][KPL], P[8][KPL];
+      // fold the earlier segments' local states, kFoldB per round trip (a
+      // small batch: these registers count against the whole kernel's
+      // allocation, and most sequences have few segments)
+      for (int64_t j0 = 0; j0 < seg; j0 += kFoldB) {
+        float L[kFoldB][KPL], P[kFoldB][KPL];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kFoldB; ++u) {
           const int64_t gj = sw.segoff[n] + j0 + u;
 #pragma unroll
           for (int i = 0; i < KPL; ++i) {
@@ -248,7 +284,7 @@ __global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
           }
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < kFoldB; ++u)
 #pragma unroll
           for (int i = 0; i < KPL; ++i) S[i] = fmaf(P[u][i], S[i], L[u][i]);
       }
@@ -343,50 +379,72 @@ __global__ __launch_bounds__(256) void gla_recurrent_staged_kernel(
     const int ns = static_cast<int>(min(static_cast<int64_t>(kSB), eos - t0));
     // Steps in groups of U: the k v products of the group first
     // (independent of the state), then the U state updates (the only
-    // dependency carried from step to step is one fma per state element),
-    // then the U cross-lane reductions together.  Steps of the group past
-    // the sequence end read the zero rows (no change) and store nothing.
-    for (int s0 = 0; s0 < ns; s0 += U) {
-      float d[U][KPL], kv[U][KPL], qs[U][KPL];
+    // dependency carried from step to step is one fma per state element).
+    // Groups past the block's last step are skipped (a wavefront-uniform
+    // branch); steps of a group past the sequence end read the zero rows
+    // (decay 1, k = 0: no change) and store nothing.  Each step's partial
+    // dot product q . S over this lane's keys stays in a register until its
+    // half block (kHB steps) is done; the sums over the 4 key groups then
+    // run as lane swaps on the VALU, and key group kg stores the steps
+    // s = kg mod 4 of the half.
+    constexpr int kHB = kSB / 2;
+    static_for<2>([&](auto hi) __attribute__((always_inline)) {
+      constexpr int h0s = decltype(hi)::value * kHB;   // first step of this half
+      float acc[kHB];
+      static_for<kHB / U>([&](auto gi) __attribute__((always_inline)) {
+        constexpr int sl = decltype(gi)::value * U;     // step within the half: acc index
+        constexpr int s0 = h0s + sl;
+        if (s0 >= ns) return;
+        float d[U][KPL], kv[U][KPL], qs[U][KPL];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int st = s0 + u;
-        lds_run<DT, KPL>(lds + G::OQ + st * G::QB + k0 * G::ES, qs[u]);
-        lds_run<DT, KPL>(lds + G::OK + st * G::QB + k0 * G::ES, kv[u]);
-        lds_run<SSLA_F32, KPL>(lds + G::OD + st * G::DB + k0 * 4, d[u]);
-        const float vc = lds_elem<DT>(lds + G::OV + st * G::VB + (lane & 15) * G::ES);
+        for (int u = 0; u < U; ++u) {
+          const int st = s0 + u;
+          if (MODE != kSegState) lds_run<DT, KPL>(lds + G::OQ + st * G::QB + k0 * G::ES, qs[u]);
+          lds_run<DT, KPL>(lds + G::OK + st * G::QB + k0 * G::ES, kv[u]);
+          lds_run<SSLA_F32, KPL>(lds + G::OD + st * G::DB + k0 * 4, d[u]);
+          const float vc = lds_elem<DT>(lds + G::OV + st * G::VB + (lane & 15) * G::ES);
 #pragma unroll
-        for (int i = 0; i < KPL; ++i) kv[u][i] *= vc;
-      }
-      if (MODE == kSegState) {
-        // state only: steps past the unit's end have decay 1 and k = 0
+          for (int i = 0; i < KPL; ++i) kv[u][i] *= vc;
+        }
+        if (MODE == kSegState) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int i = 0; i < KPL; ++i) {
+              S[i] = fmaf(d[u][i], S[i], kv[u][i]);
+              dprod[i] *= d[u][i];
+            }
+          return;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float a = 0.f;
 #pragma unroll
           for (int i = 0; i < KPL; ++i) {
             S[i] = fmaf(d[u][i], S[i], kv[u][i]);
-            dprod[i] *= d[u][i];
+            a = fmaf(qs[u][i], S[i], a);
           }
-        continue;
-      }
-      float acc[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        acc[u] = 0.f;
-#pragma unroll
-        for (int i = 0; i < KPL; ++i) {
-          S[i] = fmaf(d[u][i], S[i], kv[u][i]);
-          acc[u] = fmaf(qs[u][i], S[i], acc[u]);
+          acc[sl + u] = a;
         }
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) acc[u] += __shfl_xor(acc[u], 16);
-#pragma unroll
-      for (int u = 0; u < U; ++u) acc[u] += __shfl_xor(acc[u], 32);
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (kg == 0 && col_ok && s0 + u < ns) E::store(o, ((t0 + s0 + u) * H + h) * V + col, acc[u] * scale);
-    }
+      });
+      if (MODE == kSegState || h0s >= ns) return;
+      static_for<kHB>([&](auto si) __attribute__((always_inline)) {
+        constexpr int sl = decltype(si)::value;
+        if (h0s + sl < ns) acc[sl] = sum_key_groups(acc[sl]);
+      });
+      static_for<kHB / 4>([&](auto ji) __attribute__((always_inline)) {
+        constexpr int j = decltype(ji)::value;
+        // acc[4 j + kg] by masks (a select chain would be turned into a
+        // run-time index into acc, which moves acc to scratch memory)
+        const uint32_t m = static_cast<uint32_t>(kg);
+        const uint32_t bits = (__float_as_uint(acc[4 * j]) & (0u - static_cast<uint32_t>(m == 0))) |
+                              (__float_as_uint(acc[4 * j + 1]) & (0u - static_cast<uint32_t>(m == 1))) |
+                              (__float_as_uint(acc[4 * j + 2]) & (0u - static_cast<uint32_t>(m == 2))) |
+                              (__float_as_uint(acc[4 * j + 3]) & (0u - static_cast<uint32_t>(m == 3)));
+        const int st = h0s + 4 * j + kg;
+        if (col_ok && st < ns) store_out<DT>(o, ((t0 + st) * H + h) * V + col, __uint_as_float(bits) * scale);
+      });
+    });
   }
   if (MODE == kSegState) {
     const int64_t gs = unit;
