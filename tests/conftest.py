@@ -29,7 +29,7 @@ def assert_close(actual, ref, rtol, name="", atol_scale=None, band=None, ratio_m
     rtol * rms(ref) (a bare rtol is ill-posed near zero); ratio_max defaults
     to rtol.  The bf16/fp16 GLA checks pass `band` and `ratio_max`: both are
     at most twice the error measured for that check on the MI355X (the
-    measured values, and how they arise, are listed in DESIGN.md), well
+    measured values are what SSLA_PARITY_LOG records), well
     inside the north star's bf16 bar (rtol 2e-2 on the reference's error
     ratio, get_err_ratio, utils/ela_utils.py:67-70).  With SSLA_PARITY_LOG
     set, every check appends its measured RMS ratio and worst error to that
