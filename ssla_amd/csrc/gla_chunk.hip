@@ -919,6 +919,35 @@ __global__ __launch_bounds__(256, SSLA_GC_STATE_WAVES) void gla_chunk_state_kern
   if (wv == 0 && v0 == 0) ws_decay[slot * KD + lane] = dsum;
 }
 
+// Longest sequence of cu_seqlens (clamped to [0, T] as the kernels clamp
+// them) against max_rows; reads cu_seqlens back in pieces of 512 entries.
+int check_seq_lengths(const int64_t *cu, int n_seq, int64_t T, int64_t max_rows, hipStream_t st) {
+  constexpr int kPiece = 512;
+  int64_t buf[kPiece + 1];
+  int64_t prev = 0;
+  for (int i0 = 0; i0 <= n_seq; i0 += kPiece) {
+    const int cnt = std::min(kPiece, n_seq + 1 - i0);
+    const hipError_t e = read_to_host(buf, cu + i0, sizeof(int64_t) * cnt, st);
+    if (e != hipSuccess) {
+      set_error("gla_chunk_fwd: reading cu_seqlens failed: %s", hipGetErrorString(e));
+      return SSLA_ERR_LAUNCH;
+    }
+    for (int j = 0; j < cnt; ++j) {
+      const int64_t b = std::min(std::max(buf[j], int64_t{0}), T);
+      if (i0 + j > 0) {
+        const int64_t len = b - std::min(std::max(prev, int64_t{0}), T);
+        if (len > max_rows) {
+          set_error("gla_chunk_fwd: sequence %d has %lld rows; one sequence must stay below 2^31 bytes per "
+                    "tensor (at most %lld rows at this H, K, V)", i0 + j - 1, (long long)len, (long long)max_rows);
+          return SSLA_ERR_UNSUPPORTED;
+        }
+      }
+      prev = buf[j];
+    }
+  }
+  return SSLA_OK;
+}
+
 inline int pick_nvt(int V) {
   const int tiles = V / 16;
   for (int nvt = 4; nvt >= 1; --nvt)
@@ -1012,9 +1041,17 @@ extern "C" int ssla_gla_chunk_fwd(const void *q, const void *k, const void *v, c
   if (n_seq == 0) return SSLA_OK;
   SSLA_CHECK_ARG(cu_seqlens != nullptr, "gla_chunk_fwd: cu_seqlens is NULL");
   // kernels address a sequence with 32-bit byte offsets
-  if (T * H * static_cast<int64_t>(std::max(K, V)) * 4 >= (int64_t{1} << 31)) {
-    set_error("gla_chunk_fwd: T * H * max(K, V) * 4 must stay below 2^31 bytes (T=%lld H=%d)", (long long)T, H);
-    return SSLA_ERR_UNSUPPORTED;
+  {
+    // Each sequence's rows are addressed through buffer resources with
+    // 32-bit byte offsets: a sequence must stay below 2^31 bytes per tensor.
+    // Only a batch whose whole tensor reaches that size can hold such a
+    // sequence; then the lengths are read back (one host synchronisation).
+    const int64_t row_bytes = static_cast<int64_t>(H) * std::max(K, V) * 4;
+    const int64_t max_rows = ((int64_t{1} << 31) - 1) / row_bytes;
+    if (T > max_rows) {
+      const int st = check_seq_lengths(cu_seqlens, n_seq, T, max_rows, static_cast<hipStream_t>(stream));
+      if (st != SSLA_OK) return st;
+    }
   }
   SSLA_CHECK_ARG(T == 0 || (q && k && v && g && o), "gla_chunk_fwd: null tensor pointer");
   SSLA_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(g, 16) && aligned(v, 16) && aligned(o, 8),

@@ -194,3 +194,62 @@ def test_recurrent_returns_sequence_rows(dev):
     ro, rht = _oracle(q, k, v, g, cu, s0, 32 ** -0.5)
     assert_close(o, ro[2:9], RTOL_F32, "o rows")
     assert_close(ht, rht, RTOL_F32, "ht")
+
+
+def test_chunk_batch_128(dev):
+    """B=128 sequences of T=4096, H=8, K=V=64 in bf16 (a 1 GiB fp32 g
+    tensor): sequences 0, 64 and 127 against the fp64 oracle, and the last
+    8 sequences run as a batch of their own (a different segment schedule)
+    against the same rows of the big batch."""
+    from ssla_amd.gla import chunk_gla
+    B, T, H, D = 128, 4096, 8, 64
+    gen = torch.Generator(device=dev).manual_seed(21)
+    q = (torch.randn(B * T, H, D, device=dev, generator=gen) / 8).to(torch.bfloat16)
+    k = torch.randn(B * T, H, D, device=dev, generator=gen).to(torch.bfloat16)
+    v = torch.randn(B * T, H, D, device=dev, generator=gen).to(torch.bfloat16)
+    g = F.logsigmoid(torch.randn(B * T, H, D, device=dev, generator=gen) / 16)
+    h0 = torch.randn(B, H, D, D, device=dev, generator=gen) * 0.1
+    cu = torch.arange(0, B * T + 1, T, device=dev, dtype=torch.int64)
+    print("chunk batch 128: full call", flush=True)
+    with torch.no_grad():
+        o, ht = chunk_gla(q, k, v, g, cu, scale=1.0, initial_state=h0, output_final_state=True)
+    torch.cuda.synchronize()
+    for n in (0, 64, 127):
+        r = slice(n * T, (n + 1) * T)
+        ro, rht = oracle.gla_recurrent(q[r].float().cpu().numpy(), k[r].float().cpu().numpy(),
+                                       v[r].float().cpu().numpy(), g[r].cpu().numpy(),
+                                       np.array([0, T], np.int64), 1.0, h0[n:n + 1].cpu().numpy(), True)
+        assert_close(o[r].float().cpu().numpy(), ro, 0.0, f"o seq {n}", band=0.12, ratio_max=6.5e-3)
+        assert_close(ht[n:n + 1].cpu().numpy(), rht, 0.0, f"ht seq {n}", band=0.025, ratio_max=1.6e-3)
+    print("chunk batch 128: last 8 alone", flush=True)
+    r = slice(120 * T, 128 * T)
+    with torch.no_grad():
+        o8, ht8 = chunk_gla(q[r], k[r], v[r], g[r], cu[:9].clone(), scale=1.0, initial_state=h0[120:],
+                            output_final_state=True)
+    assert_close(o8.float().cpu().numpy(), o[r].float().cpu().numpy(), 0.0, "o batch 8 vs 128",
+                 band=0.24, ratio_max=1.3e-2)
+    assert_close(ht8.cpu().numpy(), ht[120:].cpu().numpy(), 0.0, "ht batch 8 vs 128", band=0.05, ratio_max=3.2e-3)
+
+
+def test_chunk_sequence_size_limit(dev):
+    """A sequence's rows must stay below 2^31 bytes per tensor (32-bit buffer
+    offsets), the batch may not: with H=64 (131,071 rows at most), two
+    sequences of 65,536 rows run (zero inputs: o = 0, ht = h0 up to the
+    segment states' rounding), one of
+    131,072 rows is refused."""
+    from ssla_amd.gla import chunk_gla
+    H, D, n = 64, 64, 65536
+    q = torch.zeros(2 * n, H, D, device=dev, dtype=torch.bfloat16)
+    g = torch.zeros(2 * n, H, D, device=dev)
+    h0 = torch.randn(2, H, D, D, device=dev)
+    print("chunk size limit: two sequences of 65536 rows", flush=True)
+    with torch.no_grad():
+        o, ht = chunk_gla(q, q, q, g, torch.tensor([0, n, 2 * n], device=dev), scale=1.0, initial_state=h0,
+                          output_final_state=True)
+    torch.cuda.synchronize()
+    assert not o.any()
+    # ht = h0 through the segment states (bf16 hi / lo pairs: about 2^-17)
+    assert torch.allclose(ht, h0, rtol=2e-5, atol=1e-6)
+    print("chunk size limit: one sequence of 131072 rows", flush=True)
+    with pytest.raises(NotImplementedError, match="2\\^31"):
+        chunk_gla(q, q, q, g, torch.tensor([0, 2 * n], device=dev), scale=1.0, initial_state=h0[:1])
