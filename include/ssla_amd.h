@@ -77,12 +77,16 @@ int ssla_status_read(const int32_t *status, int *value_out, void *stream);
  * together with chunk_local_cumsum (ops/utils/cumsum.py:346-364),
  * chunk_fwd_h (ops/common/chunk_h.py:242-294) and the intra-chunk /
  * output kernels (ops/gla/chunk.py:33-249, :644-743).  Supported: dtype
- * BF16 or F16, K == 64, V a multiple of 16 (<= 256).
+ * BF16 or F16, K == 64, V a multiple of 16 (<= 256); one sequence below
+ * 2^31 bytes per tensor (rows * H * max(K, V) * 4), SSLA_ERR_UNSUPPORTED
+ * otherwise.  Only a batch with T * H * max(K, V) * 4 >= 2^31 can hold such
+ * a sequence: then cu_seqlens is read back to check (one host
+ * synchronisation).
  * Each sequence is split into segments processed in parallel; the
  * workspace (ssla_gla_chunk_workspace_size bytes, 16-byte aligned, no
- * initialisation needed) holds one bf16 state (as the reference stores its
- * per-chunk states, ops/gla/chunk.py:933) and one fp32 decay row per
- * segment.  A size of 0
+ * initialisation needed) holds one bf16 hi / lo state pair (as the
+ * reference stores its per-chunk states, ops/gla/chunk.py:933) and one
+ * fp32 decay row per segment.  A size of 0
  * means no workspace is needed for this shape (pass NULL, 0). */
 size_t ssla_gla_chunk_workspace_size(int n_seq, int64_t T, int H, int K, int V);
 
