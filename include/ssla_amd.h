@@ -213,6 +213,28 @@ int ssla_sparse_gla_step(const int32_t *site_idx, int n_active,
                          int K, int V, float scale, float *o, int32_t *status,
                          void *stream);
 
+/* Projections of the per-site GLA block of the asynchronous step (config
+ * C5: ssla_amd.backbone.SiteGLABlock), each one launch on bf16 matrix
+ * cores.  No reference function: the block is the C5 configuration's; the
+ * rounding points are torch's bf16 F.linear (bf16 operands, fp32 sums, the
+ * result rounded once to bf16).
+ * ssla_site_project: x fp32 [n, cin]; w bf16 [4 hd, cin] (the rows of Wq,
+ *   Wk, Wv, Wg in turn); q, k, v = bf16(bf16(x) W^T) as bf16 [n, hd];
+ *   g = logsigmoid(bf16(bf16(x) Wg^T)) / gate_normalizer as fp32 [n, hd].
+ *   cin a multiple of 32, hd of 16.
+ * ssla_site_finish: o bf16 [n, hd]; wo bf16 [cout, hd]; x fp32 [n, cin];
+ *   wr bf16 [cout, cin] or NULL (then cin == cout);
+ *   y = LayerNorm(bf16(o Wo^T) + (bf16(bf16(x) Wr^T) or x)) * ln_w + ln_b
+ *   (biased variance, eps inside the root), fp32 [n, cout].  hd, cin
+ *   multiples of 32; cout in {16, 32, 64, 96, 128, 192, 256}.
+ * x, o and the weights 16-byte aligned; SSLA_ERR_UNSUPPORTED for other
+ * sizes. */
+int ssla_site_project(const float *x, int64_t n, int cin, const uint16_t *w, int hd, float gate_normalizer,
+                      uint16_t *q, uint16_t *k, uint16_t *v, float *g, void *stream);
+int ssla_site_finish(const uint16_t *o, int64_t n, int hd, const uint16_t *wo, const float *x, int cin,
+                     const uint16_t *wr, const float *ln_w, const float *ln_b, float eps, int cout, float *y,
+                     void *stream);
+
 /* ------------------------------------------------------------------------
  * G3 -- scatter-reduce pooling (torch_scatter.scatter_max / scatter_mean
  * semantics along dim 0 with an index broadcast over channels, as called

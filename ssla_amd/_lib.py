@@ -47,6 +47,8 @@ SIGNATURES = {
     "ssla_sparse_gla_step": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32,
                                     _f32, _vp, _vp, _vp]),
     "ssla_status_read": (_i32, [_vp, C.POINTER(_i32), _vp]),
+    "ssla_site_project": (_i32, [_vp, _i64, _i32, _vp, _i32, _f32, _vp, _vp, _vp, _vp, _vp]),
+    "ssla_site_finish": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _f32, _i32, _vp, _vp]),
     "ssla_scatter_workspace_size": (_sz, [_i64, _i32, _i64]),
     "ssla_scatter_max": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
     "ssla_scatter_mean": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _sz, _vp]),

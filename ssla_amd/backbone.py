@@ -93,16 +93,37 @@ class SiteGLABlock(nn.Module):
         cache = getattr(self, "_bf16_cache", None)
         if cache is None or cache[0] != key:
             with torch.no_grad():
-                cache = (key, {nm: m.weight.detach().to(torch.bfloat16) for nm, m in mods.items()})
+                ws = {nm: m.weight.detach().to(torch.bfloat16).contiguous() for nm, m in mods.items()}
+                ws["qkvg"] = torch.cat([ws[nm] for nm in ("q", "k", "v", "g")], 0).contiguous()
+                cache = (key, ws)
             self._bf16_cache = cache
         return cache[1]
+
+    def _fused(self, *tensors) -> bool:
+        """The one-launch kernels (ssla_site_project / ssla_site_finish) take
+        the block: device tensors, no gradient recorded, sizes they cover."""
+        hd = self.heads * self.head_dim
+        return (all(t.is_cuda for t in tensors) and not (torch.is_grad_enabled() and (
+                    any(t.requires_grad for t in tensors) or any(p.requires_grad for p in self.parameters())))
+                and self.in_channels % 32 == 0 and hd % 32 == 0
+                and self.out_channels in (16, 32, 64, 96, 128, 192, 256))
 
     def project(self, x: torch.Tensor):
         """q, k, v (bf16 ``[n, H, D]``) and log-gates g (fp32 ``[n, H, D]``)."""
         n = x.shape[0]
         w = self._bf16()
-        xb = x.to(torch.bfloat16)
         shp = (n, self.heads, self.head_dim)
+        if self._fused(x):
+            from . import _lib
+            hd = self.heads * self.head_dim
+            x = x.to(torch.float32).contiguous()
+            q, k, v = (torch.empty(n, hd, dtype=torch.bfloat16, device=x.device) for _ in range(3))
+            g = torch.empty(n, hd, dtype=torch.float32, device=x.device)
+            _lib.check(_lib.load().ssla_site_project(
+                _lib.ptr(x), n, self.in_channels, _lib.ptr(w["qkvg"]), hd, float(self.gate_normalizer),
+                _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.stream_of(x)), "ssla_site_project")
+            return q.view(shp), k.view(shp), v.view(shp), g.view(shp)
+        xb = x.to(torch.bfloat16)
         q, k, v = (F.linear(xb, w[nm]).view(shp) for nm in ("q", "k", "v"))
         g = F.logsigmoid(F.linear(xb, w["g"]).float()) / self.gate_normalizer
         return q, k, v, g.view(shp)
@@ -111,6 +132,18 @@ class SiteGLABlock(nn.Module):
         """LayerNorm(o_proj(o) + residual) in fp32 (projections in bf16)."""
         n = x.shape[0]
         w = self._bf16()
+        if self._fused(o, x) and o.dtype == torch.bfloat16:
+            from . import _lib
+            hd = self.heads * self.head_dim
+            o = o.reshape(n, hd).contiguous()
+            x = x.to(torch.float32).contiguous()
+            y = torch.empty(n, self.out_channels, dtype=torch.float32, device=x.device)
+            _lib.check(_lib.load().ssla_site_finish(
+                _lib.ptr(o), n, hd, _lib.ptr(w["o"]), _lib.ptr(x), self.in_channels,
+                _lib.ptr(w["r"]) if self.res_proj is not None else None, _lib.ptr(self.norm.weight),
+                _lib.ptr(self.norm.bias), float(self.norm.eps), self.out_channels, _lib.ptr(y), _lib.stream_of(x)),
+                "ssla_site_finish")
+            return y
         y = F.linear(o.reshape(n, -1), w["o"]).float()
         if self.res_proj is not None:
             y = y + F.linear(x.to(torch.bfloat16), w["r"]).float()

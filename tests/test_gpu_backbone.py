@@ -20,6 +20,7 @@ deterministic)."""
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 import oracle
 from oracle import backbone as ob
@@ -206,3 +207,35 @@ def test_head_graph_replays_match_eager(dev):
         xin = [torch.randn(s, device=dev, generator=gen).to(torch.bfloat16) for s in shapes]
         got = head(xin)
         assert torch.equal(got, head(xin, graph=False)), "stale graph after a weight update"
+
+
+def test_site_block_kernels_match_torch(dev):
+    """ssla_site_project / ssla_site_finish against the same block run as
+    torch's bf16 F.linear calls (the rounding points the kernels follow) for
+    every stage shape of the step: the bf16 outputs within one bf16 unit of
+    rounding (fp32 sums in another order can move a rounding), the gates and
+    the LayerNorm outputs within 1e-3 of their RMS."""
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(5)
+    model = AsyncSparseGLA().to(dev)
+    gen = torch.Generator(device=dev).manual_seed(6)
+    for i, blk in enumerate(model.blocks):
+        n = 3001 + 17 * i
+        x = torch.randn(n, blk.in_channels, device=dev, generator=gen)
+        print(f"site block kernels stage {i}: {blk.in_channels} -> {blk.out_channels}", flush=True)
+        with torch.no_grad():
+            q, k, v, g = blk.project(x)
+            o = (torch.randn(n, blk.heads * blk.head_dim, device=dev, generator=gen) * 0.3).to(torch.bfloat16)
+            y = blk.finish(o.view(n, blk.heads, blk.head_dim), x)
+            xb = x.to(torch.bfloat16)
+            w = {nm: getattr(blk, f"{nm}_proj").weight.to(torch.bfloat16) for nm in ("q", "k", "v", "g", "o")}
+            ref = [F.linear(xb, w[nm]).view(q.shape) for nm in ("q", "k", "v")]
+            rg = (F.logsigmoid(F.linear(xb, w["g"]).float()) / blk.gate_normalizer).view(g.shape)
+            ry = F.linear(o, w["o"]).float()
+            ry = ry + (F.linear(xb, blk.res_proj.weight.to(torch.bfloat16)).float() if blk.res_proj is not None else x)
+            ry = blk.norm(ry)
+        for nm, a, b in zip("qkv", (q, k, v), ref):
+            a, b = _np(a), _np(b)
+            assert np.all(np.abs(a - b) <= 2.0 ** -8 * np.abs(b) + 1e-30), f"stage {i} {nm}: beyond one bf16 unit"
+        assert_close(_np(g), _np(rg), 0.0, f"stage {i} g", band=1e-3, ratio_max=1e-3)
+        assert_close(_np(y), _np(ry), 0.0, f"stage {i} y", band=1e-3, ratio_max=1e-3)
