@@ -235,6 +235,32 @@ int ssla_site_finish(const uint16_t *o, int64_t n, int hd, const uint16_t *wo, c
                      const uint16_t *wr, const float *ln_w, const float *ln_b, float eps, int cout, float *y,
                      void *stream);
 
+/* The detection head of the asynchronous step (ssla_amd.backbone.
+ * DetectionHead, the YOLOX head's inference path: reference
+ * layers/yolox_head.py:183-230 forward, :234-256 decode) over all levels in
+ * one launch.  Per level: grid fp32 [batch, c, h, w] (rounded to bf16 as
+ * the module's input); w_br bf16 [2 width, c] (the cls branch's 1x1
+ * convolution rows, then the reg branch's); br_scale / br_shift fp32
+ * [2 width] (eval-mode batch norm and the convolution bias folded: f =
+ * SiLU(acc * scale + shift)); w_pred bf16 [16, 2 width] (rows: 4 box, 1
+ * objectness, then the classes; zero where a prediction does not read a
+ * branch) and b_pred fp32 [16]; stride.  out bf16 [batch, sum h w, n_out]:
+ * ((p0 + x) s, (p1 + y) s, exp(p2) s, exp(p3) s, p4, p5 ...) per cell in
+ * row-major cell order, levels in turn.  width a multiple of 8 up to 256,
+ * c a multiple of 32, 5 <= n_out <= 16.  No reference C function. */
+#define SSLA_HEAD_MAX_LEVELS 4
+typedef struct {
+  const float *grid;
+  const uint16_t *w_br;
+  const float *br_scale;
+  const float *br_shift;
+  const uint16_t *w_pred;
+  const float *b_pred;
+  int c, h, w, stride;
+} ssla_head_level;
+int ssla_detect_head(const ssla_head_level *levels, int n_levels, int batch, int n_out, int width, uint16_t *out,
+                     void *stream);
+
 /* ------------------------------------------------------------------------
  * G3 -- scatter-reduce pooling (torch_scatter.scatter_max / scatter_mean
  * semantics along dim 0 with an index broadcast over channels, as called

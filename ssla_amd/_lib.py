@@ -27,6 +27,13 @@ DTYPE_CODE = {torch.float32: SSLA_F32, torch.bfloat16: SSLA_BF16, torch.float16:
 
 _vp, _i32, _i64, _f32, _sz = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
 
+
+class HeadLevel(C.Structure):
+    """ssla_head_level of include/ssla_amd.h."""
+    _fields_ = [("grid", C.c_void_p), ("w_br", C.c_void_p), ("br_scale", C.c_void_p), ("br_shift", C.c_void_p),
+                ("w_pred", C.c_void_p), ("b_pred", C.c_void_p), ("c", C.c_int), ("h", C.c_int), ("w", C.c_int),
+                ("stride", C.c_int)]
+
 # name -> (restype, argtypes); must match include/ssla_amd.h
 SIGNATURES = {
     "ssla_version": (_i32, []),
@@ -49,6 +56,7 @@ SIGNATURES = {
     "ssla_status_read": (_i32, [_vp, C.POINTER(_i32), _vp]),
     "ssla_site_project": (_i32, [_vp, _i64, _i32, _vp, _i32, _f32, _vp, _vp, _vp, _vp, _vp]),
     "ssla_site_finish": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _f32, _i32, _vp, _vp]),
+    "ssla_detect_head": (_i32, [C.POINTER(HeadLevel), _i32, _i32, _i32, _i32, _vp, _vp]),
     "ssla_scatter_workspace_size": (_sz, [_i64, _i32, _i64]),
     "ssla_scatter_max": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
     "ssla_scatter_mean": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _sz, _vp]),

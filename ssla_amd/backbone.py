@@ -211,38 +211,67 @@ class DetectionHead(nn.Module):
                          bn.eps)
         return F.silu(y)
 
-    def forward(self, xin: List[torch.Tensor], graph: bool = True) -> torch.Tensor:
-        """The head on dense maps ``xin`` (``[B, C_l, H_l, W_l]`` per level).
-        Its ~60 small launches depend on nothing but the shapes, so on a GPU
-        without autograd (and with ``graph``) the first call for a shape
-        captures them once as a HIP graph that later calls replay: the
-        inputs are copied into the graph's buffers and its output is copied
-        out, so the result is the eager result bit for bit."""
-        if not (graph and xin and xin[0].is_cuda and not torch.is_grad_enabled()):
-            return self._forward_eager(xin)
-        key = (tuple((tuple(x.shape), x.dtype, x.device) for x in xin),
-               tuple((t.data_ptr(), t._version) for t in list(self.parameters()) + list(self.buffers())))
-        cache = getattr(self, "_graph_cache", None)
-        if cache is None or cache[0] != key:
-            cache = (key,) + self._capture(xin)
-            self._graph_cache = cache
-        _, gr, static_in, static_out = cache
-        for dst, src in zip(static_in, xin):
-            dst.copy_(src)
-        gr.replay()
-        return static_out.clone()
+    def forward(self, xin: List[torch.Tensor], fused: bool = True) -> torch.Tensor:
+        """The head on dense maps ``xin`` (``[B, C_l, H_l, W_l]`` per level,
+        fp32 or bf16).  On a GPU without autograd (and with ``fused``) all
+        levels run as one kernel (ssla_detect_head: the two branches' 1x1
+        convolutions as one bf16 GEMM, batch norm and SiLU in fp32, the
+        predictions as a second GEMM, the decode); otherwise the module's
+        bf16 ops run one by one."""
+        if not (fused and xin and xin[0].is_cuda and not torch.is_grad_enabled()):
+            dt = self.cls_convs[0][0].weight.dtype
+            return self._forward_eager([x.to(dt) for x in xin])
+        from . import _lib
+        prm = self._fused_params()
+        B = int(xin[0].shape[0])
+        grids = [x.to(torch.float32).contiguous() for x in xin]
+        lv = (_lib.HeadLevel * len(grids))()
+        for i, x in enumerate(grids):
+            w_br, sc, sh, w_p, b_p = prm[i]
+            lv[i] = _lib.HeadLevel(_lib.ptr(x), _lib.ptr(w_br), _lib.ptr(sc), _lib.ptr(sh), _lib.ptr(w_p),
+                                   _lib.ptr(b_p), int(x.shape[1]), int(x.shape[2]), int(x.shape[3]),
+                                   int(self.strides[i]))
+        n_out = 5 + self.num_classes
+        n_anchor = sum(int(x.shape[2]) * int(x.shape[3]) for x in grids)
+        out = torch.empty(B, n_anchor, n_out, dtype=torch.bfloat16, device=grids[0].device)
+        width = self.cls_convs[0][0].out_channels
+        _lib.check(_lib.load().ssla_detect_head(lv, len(grids), B, n_out, width, _lib.ptr(out),
+                                                _lib.stream_of(grids[0])), "ssla_detect_head")
+        return out
 
-    def _capture(self, xin: List[torch.Tensor]):
-        static_in = [x.detach().clone() for x in xin]
-        side = torch.cuda.Stream(device=static_in[0].device)
-        side.wait_stream(torch.cuda.current_stream(static_in[0].device))
-        with torch.cuda.stream(side):
-            self._forward_eager(static_in)   # warm-up: library handles and kernels loaded outside the capture
-        torch.cuda.current_stream(static_in[0].device).wait_stream(side)
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
-            static_out = self._forward_eager(static_in)
-        return gr, static_in, static_out
+    def _fused_params(self):
+        """Per level: the two branch convolutions' weights stacked (bf16
+        [2 width, C]), batch norm folded with the convolution bias into an
+        fp32 scale and shift, and the predictions as one bf16 [16, 2 width]
+        matrix (zero where a prediction does not read a branch) with fp32
+        biases; recomputed only when a parameter or buffer changes."""
+        key = tuple((t.data_ptr(), t._version) for t in list(self.parameters()) + list(self.buffers()))
+        cache = getattr(self, "_fused_cache", None)
+        if cache is not None and cache[0] == key:
+            return cache[1]
+        levels = []
+        with torch.no_grad():
+            for lvl in range(len(self.strides)):
+                scs, shs, ws = [], [], []
+                for seq in (self.cls_convs[lvl], self.reg_convs[lvl]):
+                    conv, bn, _ = seq
+                    w = conv.weight.view(conv.out_channels, conv.in_channels)
+                    s = bn.weight.float() / torch.sqrt(bn.running_var.float() + bn.eps)
+                    scs.append(s)
+                    shs.append((conv.bias.float() - bn.running_mean.float()) * s + bn.bias.float())
+                    ws.append(w.to(torch.bfloat16))
+                width = ws[0].shape[0]
+                w_br = torch.cat(ws, 0).contiguous()
+                w_p = torch.zeros(16, 2 * width, dtype=torch.bfloat16, device=w_br.device)
+                b_p = torch.zeros(16, dtype=torch.float32, device=w_br.device)
+                reg, obj, cls = self.reg_preds[lvl], self.obj_preds[lvl], self.cls_preds[lvl]
+                w_p[0:4, width:] = reg.weight.view(4, width)
+                w_p[4:5, width:] = obj.weight.view(1, width)
+                w_p[5:5 + self.num_classes, :width] = cls.weight.view(self.num_classes, width)
+                b_p[0:4], b_p[4:5], b_p[5:5 + self.num_classes] = reg.bias.float(), obj.bias.float(), cls.bias.float()
+                levels.append((w_br, torch.cat(scs).contiguous(), torch.cat(shs).contiguous(), w_p.contiguous(), b_p))
+        self._fused_cache = (key, levels)
+        return levels
 
     def _forward_eager(self, xin: List[torch.Tensor]) -> torch.Tensor:
         # A 1x1 convolution is a linear map of every cell's channels: the
@@ -335,8 +364,7 @@ class AsyncSparseGLA(nn.Module):
                 x = self.pools[i](x)
                 if mark:
                     mark(f"s{i}.pool")
-        grids = [E.events_to_grid(feats[i], self.grid_sizes[i], self.stages[i][0]).to(torch.bfloat16)
-                 for i in self.head_levels]
+        grids = [E.events_to_grid(feats[i], self.grid_sizes[i], self.stages[i][0]) for i in self.head_levels]
         if mark:
             mark("grids")
         out = self.head(grids)

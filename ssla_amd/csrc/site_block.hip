@@ -230,3 +230,147 @@ extern "C" int ssla_site_finish(const uint16_t *o, int64_t n, int hd, const uint
 #undef SITE_FINISH
   return SSLA_ERR_UNSUPPORTED;
 }
+
+// ----------------------------------------------------------- detection head
+// DetectionHead of the asynchronous step (ssla_amd.backbone; the YOLOX
+// head's inference path, reference layers/yolox_head.py:183-230 forward,
+// :234-256 decode) over all its levels in one launch.  Per cell of a level
+// (rows of [batch * h * w]):
+//   f = SiLU(BN(W_br x + b))      (the cls and reg branches side by side,
+//                                   2 width channels; BN folded into
+//                                   scale / shift by the caller)
+//   p = W_pred f + b_pred          (reg 0-3, obj 4, classes 5.. : 16 rows,
+//                                   zero where a prediction ignores a branch)
+//   out = ((p0 + x) s, (p1 + y) s, exp(p2) s, exp(p3) s, p4, p5, ...)
+// x is the fp32 grid [batch, c, h, w] rounded to bf16 (as the module's input
+// is), the GEMMs run on bf16 operands with fp32 sums, the features are
+// rounded to bf16 between the two GEMMs, and everything else is fp32 up to
+// the bf16 output.
+namespace ssla {
+namespace {
+
+constexpr int kHeadMaxW = 256;            // branch width
+constexpr int kHeadF = 2 * kHeadMaxW;     // features per cell
+constexpr int kHeadLdsRow = kHeadF + 8;   // bf16 elements per LDS row (16-byte pad)
+
+struct HeadArgs {
+  ssla_head_level lv[SSLA_HEAD_MAX_LEVELS];
+  int tile0[SSLA_HEAD_MAX_LEVELS + 1];   // first workgroup of each level
+  int anchor0[SSLA_HEAD_MAX_LEVELS];     // first anchor of each level
+  int n_levels, batch, n_anchor, n_out, width;
+};
+
+__global__ __launch_bounds__(64 * kWaves) void detect_head_kernel(HeadArgs a, uint16_t *__restrict__ out) {
+  __shared__ __align__(16) uint16_t feat[kRows][kHeadLdsRow];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int r = lane & 15, kq = 8 * (lane >> 4);
+  int L = 0;
+  while (L + 1 < a.n_levels && static_cast<int>(blockIdx.x) >= a.tile0[L + 1]) ++L;
+  const ssla_head_level &lv = a.lv[L];
+  const int hw = lv.h * lv.w, n_cell = a.batch * hw;
+  const int c0 = (static_cast<int>(blockIdx.x) - a.tile0[L]) * kRows + 16 * wv;   // this wavefront's first cell
+  const int F = 2 * a.width;
+  // ---- branches: 16 cells x F features, K = c in steps of 32
+  {
+    const int cell = c0 + r;
+    const bool ok = cell < n_cell;
+    const int b = ok ? cell / hw : 0, rem = ok ? cell - b * hw : 0;
+    const float *xb = lv.grid + static_cast<int64_t>(b) * lv.c * hw + rem;
+    constexpr int NT = kHeadF / 16;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < lv.c; k0 += 32) {
+      f32x8v xv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[e] = ok ? xb[static_cast<int64_t>(k0 + kq + e) * hw] : 0.f;
+      const bf16x8 av = __builtin_convertvector(xv, bf16x8);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        if (16 * t < F)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bf16_piece(lv.w_br, 16 * t + r, lv.c, k0 + kq, true),
+                                                          acc[t], 0, 0, 0);
+    }
+    // f = SiLU(acc scale + shift), rounded to bf16, into this wavefront's rows
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (16 * t >= F) continue;
+      const int col = 16 * t + r;
+      const float sc = lv.br_scale[col], sh = lv.br_shift[col];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float y = fmaf(acc[t][i], sc, sh);
+        const float f = y / (1.f + expf(-y));
+        feat[16 * wv + 4 * (lane >> 4) + i][col] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+      }
+    }
+  }
+  __syncthreads();
+  // ---- predictions: 16 cells x 16 outputs, K = F
+  f32x4 p = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < F; k0 += 32) {
+    const bf16x8 av = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(&feat[16 * wv + r][k0 + kq]));
+    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bf16_piece(lv.w_pred, r, F, k0 + kq, true), p, 0, 0, 0);
+  }
+  const int j = r;   // output column
+  if (j >= a.n_out) return;
+  const float s = static_cast<float>(lv.stride), bj = lv.b_pred[j];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int cell = c0 + 4 * (lane >> 4) + i;
+    if (cell >= n_cell) continue;
+    const int b = cell / hw, rem = cell - b * hw;
+    float v = p[i] + bj;
+    if (j == 0) v = (v + static_cast<float>(rem % lv.w)) * s;
+    else if (j == 1) v = (v + static_cast<float>(rem / lv.w)) * s;
+    else if (j < 4) v = expf(v) * s;
+    const int64_t o = (static_cast<int64_t>(b) * a.n_anchor + a.anchor0[L] + rem) * a.n_out + j;
+    out[o] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+  }
+}
+
+}  // namespace
+}  // namespace ssla
+
+extern "C" int ssla_detect_head(const ssla_head_level *levels, int n_levels, int batch, int n_out, int width,
+                                uint16_t *out, void *stream) {
+  using namespace ssla;
+  clear_error();
+  SSLA_CHECK_ARG(levels && out && n_levels > 0 && n_levels <= SSLA_HEAD_MAX_LEVELS && batch > 0,
+                 "detect_head: bad arguments (levels=%d batch=%d)", n_levels, batch);
+  if (width <= 0 || width > kHeadMaxW || width % 8 != 0 || n_out < 5 || n_out > 16) {
+    set_error("detect_head: needs a branch width that is a multiple of 8 up to %d and 5..16 outputs "
+              "(width=%d n_out=%d)", kHeadMaxW, width, n_out);
+    return SSLA_ERR_UNSUPPORTED;
+  }
+  HeadArgs a{};
+  a.n_levels = n_levels;
+  a.batch = batch;
+  a.n_out = n_out;
+  a.width = width;
+  int64_t tiles = 0, anchors = 0;
+  for (int l = 0; l < n_levels; ++l) {
+    const ssla_head_level &lv = levels[l];
+    SSLA_CHECK_ARG(lv.grid && lv.w_br && lv.br_scale && lv.br_shift && lv.w_pred && lv.b_pred,
+                   "detect_head: null pointer in level %d", l);
+    SSLA_CHECK_ARG(lv.h > 0 && lv.w > 0 && lv.stride > 0, "detect_head: bad level %d", l);
+    if (lv.c <= 0 || lv.c % 32 != 0) {
+      set_error("detect_head: level %d has %d input channels (a multiple of 32 needed)", l, lv.c);
+      return SSLA_ERR_UNSUPPORTED;
+    }
+    SSLA_CHECK_ARG(aligned(lv.w_br, 16) && aligned(lv.w_pred, 16), "detect_head: weights must be 16-byte aligned");
+    a.lv[l] = lv;
+    a.tile0[l] = static_cast<int>(tiles);
+    a.anchor0[l] = static_cast<int>(anchors);
+    const int64_t cells = static_cast<int64_t>(batch) * lv.h * lv.w;
+    tiles += (cells + kRows - 1) / kRows;
+    anchors += static_cast<int64_t>(lv.h) * lv.w;
+    SSLA_CHECK_ARG(tiles < (int64_t{1} << 30) && anchors * batch * n_out < (int64_t{1} << 31),
+                   "detect_head: too many cells");
+  }
+  a.tile0[n_levels] = static_cast<int>(tiles);
+  a.n_anchor = static_cast<int>(anchors);
+  hipLaunchKernelGGL(detect_head_kernel, dim3(static_cast<unsigned>(tiles)), dim3(64 * kWaves), 0,
+                     static_cast<hipStream_t>(stream), a, out);
+  return launch_status("detect_head");
+}
