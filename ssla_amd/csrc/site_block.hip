@@ -49,51 +49,90 @@ __device__ __forceinline__ float round_bf16(float x) {
   return static_cast<float>(static_cast<__bf16>(x));
 }
 
-// grid (row tiles, 4 outputs q / k / v / g, column chunks of 128); w is
-// [4 hd, cin] (the rows of Wq, Wk, Wv, Wg in turn).
+// grid (row tiles of 64 events, column chunks of 16 NTO); w is [4 hd, cin]
+// (the rows of Wq, Wk, Wv, Wg in turn).  Wavefront w computes output w
+// (q, k, v, g) for all 64 rows of the tile: 4 x NTO MFMA tiles, each weight
+// piece reused by the 4 row tiles.  The tile's inputs are staged once in LDS
+// as bf16 (shared by the 4 wavefronts); the results leave through a
+// wave-private LDS block in 16-byte row pieces.
+template <int NTO>
 __global__ __launch_bounds__(64 * kWaves) void site_project_kernel(const float *__restrict__ x, int64_t n, int cin,
                                                                    const uint16_t *__restrict__ w, int hd,
                                                                    float inv_gn, uint16_t *__restrict__ q,
                                                                    uint16_t *__restrict__ k, uint16_t *__restrict__ v,
                                                                    float *__restrict__ g) {
-  constexpr int NT = 8;   // 128 columns
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  constexpr int NC = 16 * NTO;                          // columns of this launch's chunk
+  __shared__ __align__(16) uint16_t xs[kRows][32 + 8];  // the tile's inputs, one k-step (bf16)
+  __shared__ __align__(16) float ost[kWaves][16][NC + 4];   // one row tile of a wavefront's output
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r = lane & 15, kq = 8 * (lane >> 4);
-  const int which = blockIdx.y;
-  const int c0 = blockIdx.z * 16 * NT;
-  const int ncol = min(16 * NT, hd - c0);
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kRows + 16 * wv;
-  const int64_t row = e0 + r;
-  const bool rok = row < n;
+  const int which = wv;
+  const int c0 = blockIdx.y * NC;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kRows;
   const uint16_t *wb = w + (static_cast<int64_t>(which) * hd + c0) * cin;
-  f32x4 acc[NT];
+  f32x4 acc[4][NTO];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int t = 0; t < NTO; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // staging: thread -> (row tid / 4, inputs 8 (tid % 4) .. + 7)
+  const int sr = tid >> 2, sk = 8 * (tid & 3);
+  const int64_t srow = e0 + sr;
   for (int k0 = 0; k0 < cin; k0 += 32) {
-    const bf16x8 a = a_from_f32(x, row, cin, k0 + kq, rok);
+    const bf16x8 xv = a_from_f32(x, srow, cin, k0 + sk, srow < n);
+    bf16x8 bv[NTO];
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-      if (16 * t < ncol)
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf16_piece(wb, 16 * t + r, cin, k0 + kq, true), acc[t], 0,
-                                                        0, 0);
+    for (int t = 0; t < NTO; ++t) bv[t] = bf16_piece(wb, 16 * t + r, cin, k0 + kq, true);
+    __syncthreads();   // the previous step's reads of xs are done
+    *reinterpret_cast<bf16x8 *>(&xs[sr][sk]) = xv;
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const bf16x8 av = *reinterpret_cast<const bf16x8 *>(&xs[16 * rt + r][kq]);
+#pragma unroll
+      for (int t = 0; t < NTO; ++t) acc[rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv[t], acc[rt][t], 0, 0, 0);
+    }
   }
+  // results: row tile by row tile through this wavefront's LDS block
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if (16 * t >= ncol) continue;
-    const int col = c0 + 16 * t + r;
+  for (int rt = 0; rt < 4; ++rt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t ev = e0 + 4 * (lane >> 4) + i;
-      if (ev >= n) continue;
-      const float val = round_bf16(acc[t][i]);
-      const int64_t o = ev * hd + col;
-      if (which == 3) {
-        g[o] = (fminf(val, 0.f) - log1pf(expf(-fabsf(val)))) * inv_gn;   // logsigmoid
-      } else {
-        uint16_t *dst = which == 0 ? q : which == 1 ? k : v;
-        dst[o] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(val));
+    for (int t = 0; t < NTO; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float val = round_bf16(acc[rt][t][i]);
+        float outv = val;
+        if (which == 3) {   // logsigmoid(val) / gate_normalizer
+          const float e = __builtin_amdgcn_exp2f(-fabsf(val) * kLog2e);
+          outv = (fminf(val, 0.f) - __builtin_amdgcn_logf(1.f + e) * 0.69314718055994531f) * inv_gn;
+        }
+        ost[wv][4 * (lane >> 4) + i][16 * t + r] = outv;
+      }
+    __syncthreads();
+    const int64_t rbase = e0 + 16 * rt;
+    if (which < 3) {
+      // 16 rows x NC bf16: pieces of 8 values
+      uint16_t *dst = which == 0 ? q : which == 1 ? k : v;
+      constexpr int PR = NC / 8;   // pieces per row
+      for (int p = lane; p < 16 * PR; p += 64) {
+        const int rr = p / PR, cc = 8 * (p % PR);
+        if (rbase + rr < n) {
+          const float4 u = *reinterpret_cast<const float4 *>(&ost[wv][rr][cc]);
+          const float4 u2 = *reinterpret_cast<const float4 *>(&ost[wv][rr][cc + 4]);
+          const f32x8v f = {u.x, u.y, u.z, u.w, u2.x, u2.y, u2.z, u2.w};
+          *reinterpret_cast<bf16x8 *>(dst + (rbase + rr) * hd + c0 + cc) = __builtin_convertvector(f, bf16x8);
+        }
+      }
+    } else {
+      constexpr int PR = NC / 4;
+      for (int p = lane; p < 16 * PR; p += 64) {
+        const int rr = p / PR, cc = 4 * (p % PR);
+        if (rbase + rr < n)
+          *reinterpret_cast<float4 *>(g + (rbase + rr) * hd + c0 + cc) =
+              *reinterpret_cast<const float4 *>(&ost[wv][rr][cc]);
       }
     }
+    __syncthreads();   // the block is rewritten by the next row tile
   }
 }
 
@@ -184,16 +223,25 @@ extern "C" int ssla_site_project(const float *x, int64_t n, int cin, const uint1
   clear_error();
   SSLA_CHECK_ARG(n >= 0 && cin > 0 && hd > 0 && gate_normalizer != 0.f,
                  "site_project: bad sizes n=%lld cin=%d hd=%d", (long long)n, cin, hd);
-  if (cin % 32 != 0 || hd % 16 != 0) {
-    set_error("site_project: needs cin a multiple of 32 and hd a multiple of 16 (cin=%d hd=%d)", cin, hd);
+  if (cin % 32 != 0 || hd % 32 != 0) {
+    set_error("site_project: needs cin and hd multiples of 32 (cin=%d hd=%d)", cin, hd);
     return SSLA_ERR_UNSUPPORTED;
   }
   SSLA_CHECK_ARG(n < (int64_t{1} << 31) * kRows, "site_project: too many rows");
   if (n == 0) return SSLA_OK;
   SSLA_CHECK_ARG(x && w && q && k && v && g, "site_project: null pointer");
-  SSLA_CHECK_ARG(aligned(x, 16) && aligned(w, 16), "site_project: x and w must be 16-byte aligned");
-  hipLaunchKernelGGL(site_project_kernel, dim3(row_tiles(n), 4, (hd + 127) / 128), dim3(64 * kWaves), 0,
-                     static_cast<hipStream_t>(stream), x, n, cin, w, hd, 1.f / gate_normalizer, q, k, v, g);
+  SSLA_CHECK_ARG(aligned(x, 16) && aligned(w, 16) && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) &&
+                 aligned(g, 16), "site_project: x, w and the outputs must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // column chunks of 64 (32 when hd is not a multiple of 64): wider chunks
+  // hold more accumulators than three wavefronts per SIMD can
+  const int nto = hd % 64 == 0 ? 4 : 2;
+  const dim3 grid(row_tiles(n), hd / (16 * nto));
+  const float ig = 1.f / gate_normalizer;
+  if (nto == 4)
+    hipLaunchKernelGGL((site_project_kernel<4>), grid, dim3(64 * kWaves), 0, st, x, n, cin, w, hd, ig, q, k, v, g);
+  else
+    hipLaunchKernelGGL((site_project_kernel<2>), grid, dim3(64 * kWaves), 0, st, x, n, cin, w, hd, ig, q, k, v, g);
   return launch_status("site_project");
 }
 
