@@ -136,7 +136,10 @@ __global__ __launch_bounds__(64 * kWaves) void site_project_kernel(const float *
   }
 }
 
-// One wavefront: 16 rows x 16 NT output columns, LayerNorm over them.
+// One wavefront: 16 rows x 16 NT output columns, LayerNorm over them.  The
+// weights of each 32-wide reduction step are staged in LDS once per
+// workgroup (shared by its 4 wavefronts); the next step's pieces are
+// loaded while the current one is multiplied.
 template <int NT>
 __global__ __launch_bounds__(64 * kWaves) void site_finish_kernel(const uint16_t *__restrict__ o, int64_t n, int hd,
                                                                   const uint16_t *__restrict__ wo,
@@ -146,31 +149,60 @@ __global__ __launch_bounds__(64 * kWaves) void site_finish_kernel(const uint16_t
                                                                   const float *__restrict__ ln_b, float eps,
                                                                   float *__restrict__ y) {
   constexpr int C = 16 * NT;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  constexpr int PT = (C * 4 + 64 * kWaves - 1) / (64 * kWaves);   // weight pieces per thread and step
+  __shared__ __align__(16) uint16_t wst[C][32 + 8];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r = lane & 15, kq = 8 * (lane >> 4);
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kRows + 16 * wv;
-  if (e0 >= n) return;   // whole wavefront (no barriers in this kernel)
   const int64_t row = e0 + r;
   const bool rok = row < n;
   f32x4 acc[NT], res[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = res[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // o Wo^T (hd / 32 steps), then x Wr^T (cin / 32 steps) with an input
+  // projection; each step's weights staged in LDS
+  auto fetch = [&](const uint16_t *wm, int ld, int k0, uint4 (&pc)[PT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const int pc_i = tid + 64 * kWaves * j;   // piece: row pc_i / 4, inputs 8 (pc_i % 4) .. + 7
+      pc[j] = pc_i < 4 * C ? *reinterpret_cast<const uint4 *>(wm + static_cast<int64_t>(pc_i >> 2) * ld + k0 +
+                                                              8 * (pc_i & 3))
+                           : uint4{0, 0, 0, 0};
+    }
+  };
+  auto stage = [&](const uint4 (&pc)[PT]) __attribute__((always_inline)) {
+    __syncthreads();   // the previous step's reads of wst are done
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const int pc_i = tid + 64 * kWaves * j;
+      if (pc_i < 4 * C) *reinterpret_cast<uint4 *>(&wst[pc_i >> 2][8 * (pc_i & 3)]) = pc[j];
+    }
+    __syncthreads();
+  };
+  uint4 pcur[PT];
+  fetch(wo, hd, 0, pcur);
   for (int k0 = 0; k0 < hd; k0 += 32) {
+    stage(pcur);
+    if (k0 + 32 < hd) fetch(wo, hd, k0 + 32, pcur);
+    else if (wr) fetch(wr, cin, 0, pcur);
     const bf16x8 a = bf16_piece(o, row, hd, k0 + kq, rok);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf16_piece(wo, 16 * t + r, hd, k0 + kq, true), acc[t], 0, 0,
-                                                      0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, *reinterpret_cast<const bf16x8 *>(&wst[16 * t + r][kq]),
+                                                      acc[t], 0, 0, 0);
   }
   if (wr) {
     for (int k0 = 0; k0 < cin; k0 += 32) {
+      stage(pcur);
+      if (k0 + 32 < cin) fetch(wr, cin, k0 + 32, pcur);
       const bf16x8 a = a_from_f32(x, row, cin, k0 + kq, rok);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        res[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf16_piece(wr, 16 * t + r, cin, k0 + kq, true), res[t], 0,
-                                                        0, 0);
+        res[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, *reinterpret_cast<const bf16x8 *>(&wst[16 * t + r][kq]),
+                                                        res[t], 0, 0, 0);
     }
   }
+  if (e0 >= n) return;   // after the last barrier: nothing of this wavefront to write
   // y = bf16(o Wo^T) + (bf16(x Wr^T) or x); rows 4 (l / 16) + i of this
   // wavefront, columns 16 t + l % 16
   float yv[NT][4];
