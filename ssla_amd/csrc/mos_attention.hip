@@ -260,6 +260,45 @@ __device__ __forceinline__ void fetch_row(float (&e)[CP], const float *__restric
   }
 }
 
+// One step of the segmented scan: every lane combines with the value that
+// the DPP control CTRL brings from an earlier lane, (A, B) of that lane then
+// this one: (A_s A, A B_s + B), unless a patch starts inside this lane's
+// range (F).  Lanes without a source (outside row_mask, or before the
+// shift's reach in their row) receive the identity (1, 0, no start).
+template <int CTRL, int ROWS, int HP>
+__device__ __forceinline__ void seg_scan_step(float (&A)[HP], float (&B)[HP], int &F) {
+  const int Fs = __builtin_amdgcn_update_dpp(0, F, CTRL, ROWS, 0xf, false);
+  const bool take = !F;
+#pragma unroll
+  for (int j = 0; j < HP; ++j) {
+    const float As = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, 1.f), __builtin_bit_cast(int, A[j]), CTRL, ROWS,
+                                           0xf, false));
+    const float Bs = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, B[j]), CTRL, ROWS, 0xf, false));
+    if (take) {
+      B[j] = fmaf(A[j], Bs, B[j]);
+      A[j] = A[j] * As;
+    }
+  }
+  F |= Fs;
+}
+
+// Segmented inclusive scan of the pairs (A, B) over the 64 lanes (lane =
+// row of the window, in order), restarted where a lane's flag is set: shifts
+// by 1, 2, 4, 8 inside each 16-lane row (DPP row_shr), then lane 15 of rows
+// 0 and 2 into rows 1 and 3 (row_bcast:15) and lane 31 into rows 2 and 3
+// (row_bcast:31).  All on the VALU (no LDS permutes).
+template <int HP>
+__device__ __forceinline__ void seg_scan_dpp(float (&A)[HP], float (&B)[HP], int &F) {
+  seg_scan_step<0x111, 0xf, HP>(A, B, F);   // row_shr:1
+  seg_scan_step<0x112, 0xf, HP>(A, B, F);   // row_shr:2
+  seg_scan_step<0x114, 0xf, HP>(A, B, F);   // row_shr:4
+  seg_scan_step<0x118, 0xf, HP>(A, B, F);   // row_shr:8
+  seg_scan_step<0x142, 0xa, HP>(A, B, F);   // row_bcast:15 into rows 1, 3
+  seg_scan_step<0x143, 0xc, HP>(A, B, F);   // row_bcast:31 into rows 2, 3
+}
+
 template <int CP, int HP, bool FOLD>
 __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
     const float *__restrict__ ev, int64_t E, int cin, int hid, const int64_t *__restrict__ src,
@@ -348,26 +387,13 @@ __global__ __launch_bounds__(kThreads) void mos_patch_kernel(
       }
       // segmented inclusive scan of (A, B) across the wavefront
       int F = flag;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int Fp = __shfl_up(F, d);
-        const bool take = lane >= d && !F;
-#pragma unroll
-        for (int j = 0; j < HP; ++j) {
-          const float Ap = __shfl_up(A_[j], d), Bp = __shfl_up(B_[j], d);
-          if (take) {
-            B_[j] = fmaf(A_[j], Bp, B_[j]);
-            A_[j] = A_[j] * Ap;
-          }
-        }
-        if (lane >= d) F |= Fp;
-      }
+      seg_scan_dpp<HP>(A_, B_, F);
       // rows whose patch started before this window continue the carry
       float hq[HP];
 #pragma unroll
       for (int j = 0; j < HP; ++j) {
         const float h = F ? B_[j] : fmaf(A_[j], carry[j], B_[j]);
-        carry[j] = __shfl(h, 63);
+        carry[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, h), 63));
         hq[j] = q[j] * h;
       }
       // o_proj, then the gather projection (folded: one product)
