@@ -33,9 +33,9 @@ __device__ __forceinline__ void skip_sequence(void *o, int64_t bos, int64_t eos,
 }
 
 // ------------------------------------------------------- staged kernel --
-// Each wavefront owns one (sequence, head, 16-column V tile); its lanes are
-// 4 key groups x 16 value columns, each lane holding KPL = K/4 fp32 state
-// rows.  The wavefront walks its sequence in blocks of kSB steps: a
+// Each wavefront owns one (sequence, head, V tile of 16 NC columns); its
+// lanes are 4 key groups x 16 value columns, each lane holding KPL = K/4
+// fp32 state rows of NC columns (col0 and col0 + 16).  The wavefront walks its sequence in blocks of kSB steps: a
 // block's q, k, g rows (this head) and v tile are fetched with 16-byte
 // buffer loads into registers while the previous block is being computed,
 // then parked in a wave-private LDS buffer, from which every step reads its
@@ -50,12 +50,12 @@ __device__ __forceinline__ void skip_sequence(void *o, int64_t bos, int64_t eos,
 constexpr int kSB = 16;   // steps per staged block
 constexpr int kFoldB = 2; // segment states folded per round trip
 
-template <int DT, int GDT, int KPL>
+template <int DT, int GDT, int KPL, int NC>
 struct Staged {
   static constexpr int K = 4 * KPL;
   static constexpr int ES = DT == SSLA_F32 ? 4 : 2;    // bytes per q/k/v element
   static constexpr int GS = GDT == SSLA_F32 ? 4 : 2;   // bytes per g element
-  static constexpr int QB = K * ES, GB = K * GS, VB = kBV * ES;   // row bytes (v: one tile)
+  static constexpr int QB = K * ES, GB = K * GS, VB = kBV * NC * ES;   // row bytes (v: one tile)
   static constexpr int PQ = kSB * QB / 16, PG = kSB * GB / 16, PV = kSB * VB / 16;   // 16-byte pieces
   static constexpr int NQ = (PQ + 63) / 64, NG = (PG + 63) / 64, NV = (PV + 63) / 64;
   static constexpr int DB = K * 4;            // bytes of a row of fp32 decays
@@ -203,23 +203,23 @@ __device__ __forceinline__ void store_out(void *o, int64_t i, float x) {
   else static_cast<float *>(o)[i] = x;
 }
 
-template <int DT, int GDT, int KPL, int MODE>
-__global__ __launch_bounds__(256, KPL <= 8 ? 4 : 2) void gla_recurrent_staged_kernel(
+template <int DT, int GDT, int KPL, int MODE, int NC>
+__global__ __launch_bounds__(256, NC == 1 ? (KPL <= 8 ? 4 : 2) : (KPL <= 4 ? 4 : 3)) void gla_recurrent_staged_kernel(
     const void *__restrict__ q, const void *__restrict__ k,
     const void *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int H, int V,
     float scale, const float *__restrict__ h0, void *__restrict__ o,
     float *__restrict__ ht, const int32_t *__restrict__ state_idx, int n_state_rows,
     int64_t T, int32_t *__restrict__ status, SegWs sw) {
-  typedef Staged<DT, GDT, KPL> G;
+  typedef Staged<DT, GDT, KPL, NC> G;
   constexpr int K = G::K;
-  constexpr int U = 1;   // steps per group (kSB / 2 is a multiple); more costs registers, not time
+  constexpr int TW = kBV * NC;   // value columns of the wavefront's tile
   __shared__ __align__(16) unsigned char smem[4][G::BYTES];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   unsigned char *lds = smem[wv];
   const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wv;
-  const int n_vt = (V + kBV - 1) / kBV;
+  const int n_vt = (V + TW - 1) / TW;
   const int64_t n_units = MODE == kPlain ? static_cast<int64_t>(n_seq) : sw.n_segs_max;
   if (item >= n_units * H * n_vt) return;  // whole wavefront exits (no workgroup barrier)
   const int vt = static_cast<int>(item % n_vt);
@@ -234,59 +234,79 @@ __global__ __launch_bounds__(256, KPL <= 8 ? 4 : 2) void gla_recurrent_staged_ke
     nseg = sw.segoff[n + 1] - sw.segoff[n];
     if (MODE == kSegState && seg == nseg - 1) return;   // the last segment needs no local state
   }
-  const int col = vt * kBV + (lane & 15);
+  // this lane's value columns: col0 + 16 c, c < NC
+  const int col0 = vt * TW + (lane & 15);
   const int kg = lane >> 4;
   const int k0 = kg * KPL;
-  const bool col_ok = col < V;
+  bool col_ok[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) col_ok[c] = col0 + 16 * c < V;
   const int64_t sbos = min(max(cu_seqlens[n], (int64_t)0), T);
   const int64_t seos = min(max(cu_seqlens[n + 1], sbos), T);
   const int64_t bos = MODE == kPlain ? sbos : min(sbos + seg * kSegSteps, seos);      // this unit's steps
   const int64_t eos = MODE == kPlain ? seos : min(bos + kSegSteps, seos);
   const int64_t srow = state_idx ? static_cast<int64_t>(state_idx[n]) : n;
   if (bad_state_row(state_idx, n, srow, n_state_rows)) {
-    if (MODE != kSegState) skip_sequence<DT>(o, bos, eos, H, h, V, col, kg == 0 && col_ok, lane, status);
+    if (MODE != kSegState) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        skip_sequence<DT>(o, bos, eos, H, h, V, col0 + 16 * c, kg == 0 && col_ok[c], lane, status);
+    }
     return;
   }
 
-  float S[KPL];
+  float S[NC][KPL];
   float dprod[KPL];   // product of the decays of this unit (state pass)
 #pragma unroll
   for (int i = 0; i < KPL; ++i) dprod[i] = 1.f;
-  const int64_t e0 = (static_cast<int64_t>(h) * K + k0) * V + col;   // this lane's element (i = 0) of a state
+  const int64_t e0 = (static_cast<int64_t>(h) * K + k0) * V + col0;   // this lane's element (i = 0, c = 0)
   if (MODE == kSegState) {
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) S[i] = 0.f;
-    if (seg == 0 && col_ok) {
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) S[c][i] = 0.f;
+    if (seg == 0) {
       float *dst = sw.h0c + static_cast<int64_t>(n) * H * K * V + e0;
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) dst[i * V] = h0 ? h0[srow * H * K * V + e0 + i * V] : 0.f;
+      for (int c = 0; c < NC; ++c)
+        if (col_ok[c]) {
+#pragma unroll
+          for (int i = 0; i < KPL; ++i)
+            dst[i * V + 16 * c] = h0 ? h0[srow * H * K * V + e0 + i * V + 16 * c] : 0.f;
+        }
     }
   } else {
     const float *src = nullptr;
     if (MODE == kSegOut && nseg > 1) src = sw.h0c + static_cast<int64_t>(n) * H * K * V;
     else if (h0) src = h0 + srow * H * K * V;
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) S[i] = (src && col_ok) ? src[e0 + i * V] : 0.f;
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) S[c][i] = (src && col_ok[c]) ? src[e0 + i * V + 16 * c] : 0.f;
     if (MODE == kSegOut) {
       // fold the earlier segments' local states, kFoldB per round trip (a
       // small batch: these registers count against the whole kernel's
       // allocation, and most sequences have few segments)
       for (int64_t j0 = 0; j0 < seg; j0 += kFoldB) {
-        float L[kFoldB][KPL], P[kFoldB][KPL];
+        float L[kFoldB][NC][KPL], P[kFoldB][KPL];
 #pragma unroll
         for (int u = 0; u < kFoldB; ++u) {
           const int64_t gj = sw.segoff[n] + j0 + u;
+          const bool ok = j0 + u < seg;
 #pragma unroll
           for (int i = 0; i < KPL; ++i) {
-            const bool ok = j0 + u < seg;
-            L[u][i] = (ok && col_ok) ? sw.slot[gj * H * K * V + e0 + i * V] : 0.f;
             P[u][i] = ok ? sw.prod[(gj * H + h) * K + k0 + i] : 1.f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+              L[u][c][i] = (ok && col_ok[c]) ? sw.slot[gj * H * K * V + e0 + i * V + 16 * c] : 0.f;
           }
         }
 #pragma unroll
         for (int u = 0; u < kFoldB; ++u)
 #pragma unroll
-          for (int i = 0; i < KPL; ++i) S[i] = fmaf(P[u][i], S[i], L[u][i]);
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int i = 0; i < KPL; ++i) S[c][i] = fmaf(P[u][i], S[c][i], L[u][c][i]);
       }
     }
   }
@@ -377,90 +397,106 @@ __global__ __launch_bounds__(256, KPL <= 8 ? 4 : 2) void gla_recurrent_staged_ke
     wave_lds_sync();
     if (b + 1 < nblk) issue(t0 + kSB);
     const int ns = static_cast<int>(min(static_cast<int64_t>(kSB), eos - t0));
-    // Steps in groups of U: the k v products of the group first
-    // (independent of the state), then the U state updates (the only
-    // dependency carried from step to step is one fma per state element).
-    // Groups past the block's last step are skipped (a wavefront-uniform
-    // branch); steps of a group past the sequence end read the zero rows
-    // (decay 1, k = 0: no change) and store nothing.  Each step's partial
-    // dot product q . S over this lane's keys stays in a register until its
-    // half block (kHB steps) is done; the sums over the 4 key groups then
-    // run as lane swaps on the VALU, and key group kg stores the steps
-    // s = kg mod 4 of the half.
+    // Steps in groups of kGS: a group runs whole and groups past the block's
+    // last step are skipped (wavefront-uniform branches, one per group).
+    // Steps of a group past the sequence end read the zero rows (decay 1,
+    // k = q = 0: the state is unchanged) and store nothing.  The only
+    // dependency carried from step to step is one fma per state element.
+    // Each step's partial dot products q . S over this lane's keys stay in
+    // registers until its half block (kHB steps) is done; the sums over the
+    // 4 key groups then run as lane swaps on the VALU, and key group kg
+    // stores the steps s = kg mod 4 of the half.
     constexpr int kHB = kSB / 2;
+    constexpr int kGS = 8;
     static_for<2>([&](auto hi) __attribute__((always_inline)) {
       constexpr int h0s = decltype(hi)::value * kHB;   // first step of this half
-      float acc[kHB];
-      static_for<kHB / U>([&](auto gi) __attribute__((always_inline)) {
-        constexpr int sl = decltype(gi)::value * U;     // step within the half: acc index
-        constexpr int s0 = h0s + sl;
-        if (s0 >= ns) return;
-        float d[U][KPL], kv[U][KPL], qs[U][KPL];
+      if (h0s >= ns) return;
+      float acc[NC][kHB];
+      static_for<kHB / kGS>([&](auto gi) __attribute__((always_inline)) {
+        constexpr int sg = decltype(gi)::value * kGS;   // first step of the group within the half
+        if (h0s + sg >= ns) return;
+        static_for<kGS>([&](auto ui) __attribute__((always_inline)) {
+          constexpr int sl = sg + decltype(ui)::value;   // step within the half: acc index
+          constexpr int st = h0s + sl;                   // step within the block
+          float d[KPL], kk[KPL], qs[KPL], vc[NC];
+          if (MODE != kSegState) lds_run<DT, KPL>(lds + G::OQ + st * G::QB + k0 * G::ES, qs);
+          lds_run<DT, KPL>(lds + G::OK + st * G::QB + k0 * G::ES, kk);
+          lds_run<SSLA_F32, KPL>(lds + G::OD + st * G::DB + k0 * 4, d);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int st = s0 + u;
-          if (MODE != kSegState) lds_run<DT, KPL>(lds + G::OQ + st * G::QB + k0 * G::ES, qs[u]);
-          lds_run<DT, KPL>(lds + G::OK + st * G::QB + k0 * G::ES, kv[u]);
-          lds_run<SSLA_F32, KPL>(lds + G::OD + st * G::DB + k0 * 4, d[u]);
-          const float vc = lds_elem<DT>(lds + G::OV + st * G::VB + (lane & 15) * G::ES);
-#pragma unroll
-          for (int i = 0; i < KPL; ++i) kv[u][i] *= vc;
-        }
-        if (MODE == kSegState) {
-#pragma unroll
-          for (int u = 0; u < U; ++u)
+          for (int c = 0; c < NC; ++c)
+            vc[c] = lds_elem<DT>(lds + G::OV + st * G::VB + ((lane & 15) + 16 * c) * G::ES);
+          if (MODE == kSegState) {
 #pragma unroll
             for (int i = 0; i < KPL; ++i) {
-              S[i] = fmaf(d[u][i], S[i], kv[u][i]);
-              dprod[i] *= d[u][i];
+#pragma unroll
+              for (int c = 0; c < NC; ++c) S[c][i] = fmaf(d[i], S[c][i], kk[i] * vc[c]);
+              dprod[i] *= d[i];
             }
-          return;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          float a = 0.f;
-#pragma unroll
-          for (int i = 0; i < KPL; ++i) {
-            S[i] = fmaf(d[u][i], S[i], kv[u][i]);
-            a = fmaf(qs[u][i], S[i], a);
+            return;
           }
-          acc[sl + u] = a;
-        }
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            float a0 = 0.f, a1 = 0.f;   // two chains: half the dependent fma latency
+#pragma unroll
+            for (int i = 0; i < KPL; ++i) {
+              S[c][i] = fmaf(d[i], S[c][i], kk[i] * vc[c]);
+              if (i & 1) a1 = fmaf(qs[i], S[c][i], a1);
+              else a0 = fmaf(qs[i], S[c][i], a0);
+            }
+            acc[c][sl] = a0 + a1;
+            // computed here: otherwise the sums sink past the step branches,
+            // which keeps every step's updated state alive until the half ends
+            asm volatile("" : "+v"(acc[c][sl]));
+          }
+        });
       });
-      if (MODE == kSegState || h0s >= ns) return;
-      static_for<kHB>([&](auto si) __attribute__((always_inline)) {
-        constexpr int sl = decltype(si)::value;
-        if (h0s + sl < ns) acc[sl] = sum_key_groups(acc[sl]);
+      if (MODE == kSegState) return;
+      static_for<kHB / kGS>([&](auto gi) __attribute__((always_inline)) {
+        constexpr int sg = decltype(gi)::value * kGS;
+        if (h0s + sg >= ns) return;
+        static_for<kGS>([&](auto ui) __attribute__((always_inline)) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) acc[c][sg + decltype(ui)::value] = sum_key_groups(acc[c][sg + decltype(ui)::value]);
+        });
       });
       static_for<kHB / 4>([&](auto ji) __attribute__((always_inline)) {
         constexpr int j = decltype(ji)::value;
-        // acc[4 j + kg] by masks (a select chain would be turned into a
+        const int st = h0s + 4 * j + kg;   // steps past ns (or in skipped groups) store nothing
+        // acc[c][4 j + kg] by masks (a select chain would be turned into a
         // run-time index into acc, which moves acc to scratch memory)
         const uint32_t m = static_cast<uint32_t>(kg);
-        const uint32_t bits = (__float_as_uint(acc[4 * j]) & (0u - static_cast<uint32_t>(m == 0))) |
-                              (__float_as_uint(acc[4 * j + 1]) & (0u - static_cast<uint32_t>(m == 1))) |
-                              (__float_as_uint(acc[4 * j + 2]) & (0u - static_cast<uint32_t>(m == 2))) |
-                              (__float_as_uint(acc[4 * j + 3]) & (0u - static_cast<uint32_t>(m == 3)));
-        const int st = h0s + 4 * j + kg;
-        if (col_ok && st < ns) store_out<DT>(o, ((t0 + st) * H + h) * V + col, __uint_as_float(bits) * scale);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const uint32_t bits = (__float_as_uint(acc[c][4 * j]) & (0u - static_cast<uint32_t>(m == 0))) |
+                                (__float_as_uint(acc[c][4 * j + 1]) & (0u - static_cast<uint32_t>(m == 1))) |
+                                (__float_as_uint(acc[c][4 * j + 2]) & (0u - static_cast<uint32_t>(m == 2))) |
+                                (__float_as_uint(acc[c][4 * j + 3]) & (0u - static_cast<uint32_t>(m == 3)));
+          if (col_ok[c] && st < ns) store_out<DT>(o, ((t0 + st) * H + h) * V + col0 + 16 * c, __uint_as_float(bits) * scale);
+        }
       });
     });
   }
   if (MODE == kSegState) {
     const int64_t gs = unit;
-    if (col_ok) {
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) sw.slot[gs * H * K * V + e0 + i * V] = S[i];
-    }
+    for (int c = 0; c < NC; ++c)
+      if (col_ok[c]) {
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) sw.slot[gs * H * K * V + e0 + i * V + 16 * c] = S[c][i];
+      }
     if (vt == 0 && (lane & 15) == 0) {
 #pragma unroll
       for (int i = 0; i < KPL; ++i) sw.prod[(gs * H + h) * K + k0 + i] = dprod[i];
     }
     return;
   }
-  if (ht && col_ok && seg == nseg - 1) {
+  if (ht && seg == nseg - 1) {
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) ht[((srow * H + h) * K + k0 + i) * V + col] = S[i];
+    for (int c = 0; c < NC; ++c)
+      if (col_ok[c]) {
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) ht[((srow * H + h) * K + k0 + i) * V + col0 + 16 * c] = S[c][i];
+      }
   }
 }
 
@@ -582,10 +618,17 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
   const int es = DT == SSLA_F32 ? 4 : 2;
   const bool staged = (K % 16 == 0) && K <= 64 && (V * es) % 16 == 0 && al16(q) && al16(k) && al16(g) && al16(v);
   if (staged) {
+    // two value columns per lane (32-column tiles) where V allows and the
+    // state stays small (K <= 32): the q, k, g staging and the decays are
+    // shared by twice the columns, and each step has two independent chains
+    const int nc = (V % (2 * kBV) == 0 && K <= 32) ? 2 : 1;
+    const int64_t s_items = static_cast<int64_t>(n_seq) * H * (V / (kBV * nc) + (V % (kBV * nc) != 0));
+    const int64_t s_blocks = (s_items + waves_per_block - 1) / waves_per_block;
+    dim3 pgrid(static_cast<unsigned>(s_blocks));
     const SegLayout L = seg_layout(n_seq, T, H, K, V);
     const bool segmented = L.total > 0 && workspace != nullptr && ws_bytes >= L.total;
     SegWs sw{};
-    dim3 sgrid = grid;
+    dim3 sgrid = pgrid;
     if (segmented) {
       char *w = static_cast<char *>(workspace);
       sw.segoff = reinterpret_cast<const int64_t *>(w + L.segoff);
@@ -593,7 +636,8 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
       sw.prod = reinterpret_cast<float *>(w + L.prod);
       sw.h0c = reinterpret_cast<float *>(w + L.h0c);
       sw.n_segs_max = L.n_segs_max;
-      const int64_t sblocks = (L.n_segs_max * H * n_vt + waves_per_block - 1) / waves_per_block;
+      const int n_svt = V / (kBV * nc) + (V % (kBV * nc) != 0);
+      const int64_t sblocks = (L.n_segs_max * H * n_svt + waves_per_block - 1) / waves_per_block;
       if (sblocks > 0x7fffffff) {
         set_error("gla_recurrent_fwd: too many (segment, head, tile) items");
         return SSLA_ERR_UNSUPPORTED;
@@ -602,20 +646,24 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
       hipLaunchKernelGGL(seg_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T,
                          reinterpret_cast<int64_t *>(w + L.segoff));
     }
-#define SSLA_RECS(KPL_)                                                                                     \
-  if (segmented) {                                                                                          \
-    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegState>), sgrid, block, 0, st, q, k, v, \
-                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                  \
-    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegOut>), sgrid, block, 0, st, q, k, v,   \
-                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                  \
-  } else {                                                                                                  \
-    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kPlain>), grid, block, 0, st, q, k, v, g,  \
-                       cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                     \
+#define SSLA_RECS(KPL_, NC_)                                                                                      \
+  if (segmented) {                                                                                                \
+    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegState, NC_>), sgrid, block, 0, st, q, k, v, \
+                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                        \
+    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegOut, NC_>), sgrid, block, 0, st, q, k, v,   \
+                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                        \
+  } else {                                                                                                        \
+    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kPlain, NC_>), pgrid, block, 0, st, q, k, v, g,  \
+                       cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                           \
   }
-    switch (K / kKG) {
-      case 4: SSLA_RECS(4); return launch_status("gla_recurrent_fwd");
-      case 8: SSLA_RECS(8); return launch_status("gla_recurrent_fwd");
-      case 16: SSLA_RECS(16); return launch_status("gla_recurrent_fwd");
+    switch ((K / kKG) * nc) {
+      case 4: SSLA_RECS(4, 1); return launch_status("gla_recurrent_fwd");
+      case 8:
+        if (nc == 2) { SSLA_RECS(4, 2) } else { SSLA_RECS(8, 1) }
+        return launch_status("gla_recurrent_fwd");
+      case 16:
+        if (nc == 2) { SSLA_RECS(8, 2) } else { SSLA_RECS(16, 1) }
+        return launch_status("gla_recurrent_fwd");
       default: break;   // other K: the general kernel
     }
 #undef SSLA_RECS
