@@ -33,12 +33,12 @@ __device__ __forceinline__ void skip_sequence(void *o, int64_t bos, int64_t eos,
 }
 
 // ------------------------------------------------------- staged kernel --
-// Each wavefront owns one (sequence, head, V tile of 16 NC columns); its
-// lanes are 4 key groups x 16 value columns, each lane holding KPL = K/4
-// fp32 state rows of NC columns (col0 and col0 + 16).  The wavefront walks its sequence in blocks of kSB steps: a
-// block's q, k, g rows (this head) and v tile are fetched with 16-byte
-// buffer loads into registers while the previous block is being computed,
-// then parked in a wave-private LDS buffer, from which every step reads its
+// Each wavefront owns one unit: (sequence, head, 16-column V tile), or a
+// segment of a sequence in the segmented schedule; its lanes are 4 key
+// groups x 16 value columns, each lane holding KPL = K/4 fp32 state rows.
+// A unit is walked in blocks of kSB steps: a block's q, k, g rows (this
+// head) and v tile are fetched with 16-byte buffer loads into registers
+// while the previous block is being computed, then parked in a wave-private LDS buffer, from which every step reads its
 // KPL keys (the 16 lanes of a key group read the same address: one
 // broadcast).  A sequence of n steps therefore waits on about n / kSB
 // memory round trips instead of n.  The decays exp(g) of a block are
@@ -50,12 +50,12 @@ __device__ __forceinline__ void skip_sequence(void *o, int64_t bos, int64_t eos,
 constexpr int kSB = 16;   // steps per staged block
 constexpr int kFoldB = 2; // segment states folded per round trip
 
-template <int DT, int GDT, int KPL, int NC>
+template <int DT, int GDT, int KPL>
 struct Staged {
   static constexpr int K = 4 * KPL;
   static constexpr int ES = DT == SSLA_F32 ? 4 : 2;    // bytes per q/k/v element
   static constexpr int GS = GDT == SSLA_F32 ? 4 : 2;   // bytes per g element
-  static constexpr int QB = K * ES, GB = K * GS, VB = kBV * NC * ES;   // row bytes (v: one tile)
+  static constexpr int QB = K * ES, GB = K * GS, VB = kBV * ES;   // row bytes (v: one tile)
   static constexpr int PQ = kSB * QB / 16, PG = kSB * GB / 16, PV = kSB * VB / 16;   // 16-byte pieces
   static constexpr int NQ = (PQ + 63) / 64, NG = (PG + 63) / 64, NV = (PV + 63) / 64;
   static constexpr int DB = K * 4;            // bytes of a row of fp32 decays
@@ -183,138 +183,132 @@ __device__ __forceinline__ void static_for(F &&f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// x summed over the four 16-lane rows of the wavefront (lane l gets the
-// sum over lanes l mod 16 + 16 r), with v_permlane16_swap (rows 0 <-> 1,
-// 2 <-> 3) and v_permlane32_swap (halves): VALU lane swaps, no LDS.
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ float sum_key_groups(float x) {
-  const u32x2 a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float y = __uint_as_float(a.x) + __uint_as_float(a.y);
-  const u32x2 b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-  return __uint_as_float(b.x) + __uint_as_float(b.y);
+
+// Four values summed over the four 16-lane rows (key groups) at once, row r
+// receiving the total of value r: v_permlane16_swap(a, b) swaps a's odd rows
+// with b's even rows, so a + b then holds (a0 + a1, b0 + b1, a2 + a3,
+// b2 + b3) by row; v_permlane32_swap of two such sums puts the row pairs
+// side by side.  VALU lane swaps, no LDS; three swaps and three adds for
+// four values, each summed as (x0 + x1) + (x2 + x3).
+__device__ __forceinline__ float sum4_key_groups(float a, float b, float c, float d) {
+  const u32x2 p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const u32x2 q = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(d), false, false);
+  const float ab = __uint_as_float(p.x) + __uint_as_float(p.y);   // rows: a01, b01, a23, b23
+  const float cd = __uint_as_float(q.x) + __uint_as_float(q.y);   // rows: c01, d01, c23, d23
+  const u32x2 r = __builtin_amdgcn_permlane32_swap(__float_as_uint(ab), __float_as_uint(cd), false, false);
+  return __uint_as_float(r.x) + __uint_as_float(r.y);             // rows: a, b, c, d
 }
 
 // One output element, rounded to nearest even by the conversion
 // instructions (no branches).
+// (rs: the rows' buffer resource, off: this lane's byte offset; stores
+// past the resource's end are dropped by the hardware range check)
 template <int DT>
-__device__ __forceinline__ void store_out(void *o, int64_t i, float x) {
-  if constexpr (DT == SSLA_BF16) static_cast<__bf16 *>(o)[i] = static_cast<__bf16>(x);
-  else if constexpr (DT == SSLA_F16) static_cast<_Float16 *>(o)[i] = static_cast<_Float16>(x);
-  else static_cast<float *>(o)[i] = x;
+__device__ __forceinline__ void store_out(__amdgpu_buffer_rsrc_t rs, uint32_t off, float x) {
+  if constexpr (DT == SSLA_BF16) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<__bf16>(x)), rs, off, 0, 0);
+  } else if constexpr (DT == SSLA_F16) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<_Float16>(x)), rs, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rs, off, 0, 0);
+  }
 }
 
-template <int DT, int GDT, int KPL, int MODE, int NC>
-__global__ __launch_bounds__(256, NC == 1 ? (KPL <= 8 ? 4 : 2) : (KPL <= 4 ? 4 : 3)) void gla_recurrent_staged_kernel(
+// One unit of work of a wavefront: (sequence or segment, head, V tile).
+struct Unit {
+  int64_t bos, eos;   // this unit's steps
+  int srow;           // state row of the sequence
+  int gseg;           // global segment index (segmented modes)
+  int seg, nseg;      // segment of its sequence, segments of the sequence
+  int n, h, vt;
+  bool run;           // steps to run (false: past the unit count, or nothing to do in this mode)
+  bool bad;           // state row outside the table or out of order: skipped, reported
+};
+
+template <int DT, int GDT, int KPL, int MODE>
+__global__ __launch_bounds__(256, KPL <= 8 ? 4 : 3) void gla_recurrent_staged_kernel(
     const void *__restrict__ q, const void *__restrict__ k,
     const void *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int H, int V,
     float scale, const float *__restrict__ h0, void *__restrict__ o,
     float *__restrict__ ht, const int32_t *__restrict__ state_idx, int n_state_rows,
     int64_t T, int32_t *__restrict__ status, SegWs sw) {
-  typedef Staged<DT, GDT, KPL, NC> G;
+  typedef Staged<DT, GDT, KPL> G;
   constexpr int K = G::K;
-  constexpr int TW = kBV * NC;   // value columns of the wavefront's tile
   __shared__ __align__(16) unsigned char smem[4][G::BYTES];
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  // wavefront-uniform (SGPR): the unit indexing below runs on the scalar unit
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   unsigned char *lds = smem[wv];
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wv;
-  const int n_vt = (V + TW - 1) / TW;
-  const int64_t n_units = MODE == kPlain ? static_cast<int64_t>(n_seq) : sw.n_segs_max;
-  if (item >= n_units * H * n_vt) return;  // whole wavefront exits (no workgroup barrier)
-  const int vt = static_cast<int>(item % n_vt);
-  const int h = static_cast<int>((item / n_vt) % H);
-  const int64_t unit = item / (static_cast<int64_t>(n_vt) * H);   // sequence, or global segment
-  int n = static_cast<int>(unit);
-  int64_t seg = 0, nseg = 1;
-  if (MODE != kPlain) {
-    if (unit >= sw.segoff[n_seq]) return;   // past the actual segment count
-    n = find_seg_seq(sw.segoff, n_seq, unit);
-    seg = unit - sw.segoff[n];
-    nseg = sw.segoff[n + 1] - sw.segoff[n];
-    if (MODE == kSegState && seg == nseg - 1) return;   // the last segment needs no local state
-  }
-  // this lane's value columns: col0 + 16 c, c < NC
-  const int col0 = vt * TW + (lane & 15);
+  const int n_vt = (V + kBV - 1) / kBV;
+  // items (unit, head, V tile) fit in 31 bits (checked by the host)
+  const int n_units = MODE == kPlain ? n_seq : static_cast<int>(sw.n_segs_max);
+  const int n_items = n_units * H * n_vt;
   const int kg = lane >> 4;
   const int k0 = kg * KPL;
-  bool col_ok[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) col_ok[c] = col0 + 16 * c < V;
-  const int64_t sbos = min(max(cu_seqlens[n], (int64_t)0), T);
-  const int64_t seos = min(max(cu_seqlens[n + 1], sbos), T);
-  const int64_t bos = MODE == kPlain ? sbos : min(sbos + seg * kSegSteps, seos);      // this unit's steps
-  const int64_t eos = MODE == kPlain ? seos : min(bos + kSegSteps, seos);
-  const int64_t srow = state_idx ? static_cast<int64_t>(state_idx[n]) : n;
-  if (bad_state_row(state_idx, n, srow, n_state_rows)) {
-    if (MODE != kSegState) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-        skip_sequence<DT>(o, bos, eos, H, h, V, col0 + 16 * c, kg == 0 && col_ok[c], lane, status);
-    }
-    return;
-  }
 
-  float S[NC][KPL];
-  float dprod[KPL];   // product of the decays of this unit (state pass)
-#pragma unroll
-  for (int i = 0; i < KPL; ++i) dprod[i] = 1.f;
-  const int64_t e0 = (static_cast<int64_t>(h) * K + k0) * V + col0;   // this lane's element (i = 0, c = 0)
-  if (MODE == kSegState) {
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int i = 0; i < KPL; ++i) S[c][i] = 0.f;
-    if (seg == 0) {
-      float *dst = sw.h0c + static_cast<int64_t>(n) * H * K * V + e0;
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-        if (col_ok[c]) {
-#pragma unroll
-          for (int i = 0; i < KPL; ++i)
-            dst[i * V + 16 * c] = h0 ? h0[srow * H * K * V + e0 + i * V + 16 * c] : 0.f;
-        }
+  auto unit_at = [&](int item) __attribute__((always_inline)) {
+    Unit u{};
+    u.run = false;
+    u.bad = false;
+    if (item >= n_items) return u;
+    u.vt = item % n_vt;
+    u.h = (item / n_vt) % H;
+    const int un = item / (n_vt * H);   // sequence, or global segment
+    u.n = un;
+    u.gseg = un;
+    u.seg = 0;
+    u.nseg = 1;
+    if (MODE != kPlain) {
+      if (un >= sw.segoff[n_seq]) return u;   // past the actual segment count
+      u.n = find_seg_seq(sw.segoff, n_seq, un);
+      u.seg = static_cast<int>(un - sw.segoff[u.n]);
+      u.nseg = static_cast<int>(sw.segoff[u.n + 1] - sw.segoff[u.n]);
+      if (MODE == kSegState && u.seg == u.nseg - 1) return u;   // the last segment needs no local state
     }
-  } else {
-    const float *src = nullptr;
-    if (MODE == kSegOut && nseg > 1) src = sw.h0c + static_cast<int64_t>(n) * H * K * V;
-    else if (h0) src = h0 + srow * H * K * V;
+    const int64_t sbos = min(max(cu_seqlens[u.n], (int64_t)0), T);
+    const int64_t seos = min(max(cu_seqlens[u.n + 1], sbos), T);
+    u.bos = MODE == kPlain ? sbos : min(sbos + static_cast<int64_t>(u.seg) * kSegSteps, seos);
+    u.eos = MODE == kPlain ? seos : min(u.bos + kSegSteps, seos);
+    u.srow = state_idx ? state_idx[u.n] : u.n;
+    u.bad = bad_state_row(state_idx, u.n, u.srow, n_state_rows);
+    u.run = !u.bad;
+    return u;
+  };
+  auto col_of = [&](const Unit &u) __attribute__((always_inline)) { return u.vt * kBV + (lane & 15); };
+  auto elem0 = [&](const Unit &u) __attribute__((always_inline)) {   // this lane's element (i = 0) of a state
+    return (static_cast<int64_t>(u.h) * K + k0) * V + col_of(u);
+  };
+
+  // The state a unit starts from: h0 (or its copy) for a whole sequence or a
+  // first segment, zero for a state-pass segment.  The first state-pass
+  // segment of a sequence also copies h0 into the workspace.
+  auto init_state = [&](const Unit &u, float (&S)[KPL]) __attribute__((always_inline)) {
+    const bool col_ok = col_of(u) < V;
+    const int64_t e0 = elem0(u);
+    if (MODE == kSegState) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+      for (int i = 0; i < KPL; ++i) S[i] = 0.f;
+      if (u.seg == 0 && col_ok) {
+        float *dst = sw.h0c + static_cast<int64_t>(u.n) * H * K * V + e0;
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) S[c][i] = (src && col_ok[c]) ? src[e0 + i * V + 16 * c] : 0.f;
-    if (MODE == kSegOut) {
-      // fold the earlier segments' local states, kFoldB per round trip (a
-      // small batch: these registers count against the whole kernel's
-      // allocation, and most sequences have few segments)
-      for (int64_t j0 = 0; j0 < seg; j0 += kFoldB) {
-        float L[kFoldB][NC][KPL], P[kFoldB][KPL];
-#pragma unroll
-        for (int u = 0; u < kFoldB; ++u) {
-          const int64_t gj = sw.segoff[n] + j0 + u;
-          const bool ok = j0 + u < seg;
-#pragma unroll
-          for (int i = 0; i < KPL; ++i) {
-            P[u][i] = ok ? sw.prod[(gj * H + h) * K + k0 + i] : 1.f;
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-              L[u][c][i] = (ok && col_ok[c]) ? sw.slot[gj * H * K * V + e0 + i * V + 16 * c] : 0.f;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < kFoldB; ++u)
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int i = 0; i < KPL; ++i) S[c][i] = fmaf(P[u][i], S[c][i], L[u][c][i]);
+        for (int i = 0; i < KPL; ++i) dst[i * V] = h0 ? h0[static_cast<int64_t>(u.srow) * H * K * V + e0 + i * V] : 0.f;
       }
+    } else {
+      const float *src = nullptr;
+      if (MODE == kSegOut && u.nseg > 1) src = sw.h0c + static_cast<int64_t>(u.n) * H * K * V;
+      else if (h0) src = h0 + static_cast<int64_t>(u.srow) * H * K * V;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) S[i] = (src && col_ok) ? src[e0 + i * V] : 0.f;
     }
-  }
+  };
 
   // this lane's pieces of a block: piece p = lane + 64 j of each array
   uint4 rq[G::NQ], rk[G::NQ], rg[G::NG], rv[G::NV];
-  auto issue = [&](int64_t t0) __attribute__((always_inline)) {
-    const int64_t rows = eos - t0;
+  auto issue = [&](const Unit &u, int64_t t0) __attribute__((always_inline)) {
+    const int64_t rows = u.eos - t0;
+    const int h = u.h;
     const char *qb = static_cast<const char *>(q) + t0 * H * G::QB;
     const char *kb = static_cast<const char *>(k) + t0 * H * G::QB;
     const char *gb = static_cast<const char *>(g) + t0 * H * G::GB;
@@ -342,7 +336,7 @@ __global__ __launch_bounds__(256, NC == 1 ? (KPL <= 8 ? 4 : 2) : (KPL <= 4 ? 4 :
       const int p = lane + 64 * j;
       const int st = p / (G::VB / 16), c = p % (G::VB / 16);
       const uint32_t off = p < G::PV ? static_cast<uint32_t>((static_cast<int64_t>(st) * H + h) * V * G::ES +
-                                                             vt * G::VB + 16 * c)
+                                                             u.vt * G::VB + 16 * c)
                                      : kNoRow;
       rv[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0));
     }
@@ -387,116 +381,117 @@ __global__ __launch_bounds__(256, NC == 1 ? (KPL <= 8 ? 4 : 2) : (KPL <= 4 ? 4 :
     }
   };
 
-  typedef Elem<DT> E;
-  const int64_t nblk = (eos - bos + kSB - 1) / kSB;
-  if (nblk > 0) issue(bos);
+  const Unit cur = unit_at(static_cast<int>(blockIdx.x) * 4 + wv);
+  if (cur.bad && MODE != kSegState)
+    skip_sequence<DT>(o, cur.bos, cur.eos, H, cur.h, V, col_of(cur), kg == 0 && col_of(cur) < V, lane, status);
+  if (!cur.run) return;   // whole wavefront exits (no workgroup barrier)
+  float S[KPL];
+  init_state(cur, S);
+  const int h = cur.h;
+  const int col = col_of(cur);
+  const bool col_ok = col < V;
+  const int64_t e0 = elem0(cur);
+  if (MODE == kSegOut) {
+    // fold the earlier segments' local states, kFoldB per round trip (a
+    // small batch: these registers count against the whole kernel's
+    // allocation, and most sequences have few segments)
+    for (int64_t j0 = 0; j0 < cur.seg; j0 += kFoldB) {
+      float L[kFoldB][KPL], P[kFoldB][KPL];
+#pragma unroll
+      for (int u = 0; u < kFoldB; ++u) {
+        const int64_t gj = sw.segoff[cur.n] + j0 + u;
+        const bool ok = j0 + u < cur.seg;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) {
+          P[u][i] = ok ? sw.prod[(gj * H + h) * K + k0 + i] : 1.f;
+          L[u][i] = (ok && col_ok) ? sw.slot[gj * H * K * V + e0 + i * V] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kFoldB; ++u)
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) S[i] = fmaf(P[u][i], S[i], L[u][i]);
+    }
+  }
+  float dprod[KPL];   // product of the decays of this unit (state pass)
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) dprod[i] = 1.f;
+  const int64_t nblk = (cur.eos - cur.bos + kSB - 1) / kSB;
+  if (nblk > 0) issue(cur, cur.bos);
   for (int64_t b = 0; b < nblk; ++b) {
-    const int64_t t0 = bos + b * kSB;
+    const int64_t t0 = cur.bos + b * kSB;
     wave_lds_sync();   // the previous block's reads are done
     park();
     wave_lds_sync();
-    if (b + 1 < nblk) issue(t0 + kSB);
-    const int ns = static_cast<int>(min(static_cast<int64_t>(kSB), eos - t0));
-    // Steps in groups of kGS: a group runs whole and groups past the block's
-    // last step are skipped (wavefront-uniform branches, one per group).
-    // Steps of a group past the sequence end read the zero rows (decay 1,
+    if (b + 1 < nblk) issue(cur, t0 + kSB);
+    const int ns = static_cast<int>(min(static_cast<int64_t>(kSB), cur.eos - t0));
+    // o rows of this block's steps (step st of the block at (st H + h) V)
+    const auto rso = rows_rsrc(static_cast<char *>(o) + (t0 * H + h) * static_cast<int64_t>(V) * G::ES,
+                               ((ns - 1) * static_cast<int64_t>(H) + 1) * V * G::ES);
+    // The steps of each half block (kHB steps) run without branches;
+    // halves past the block's last step are skipped (a wavefront-uniform
+    // branch).  Steps past the sequence end read the zero rows (decay 1,
     // k = q = 0: the state is unchanged) and store nothing.  The only
-    // dependency carried from step to step is one fma per state element.
-    // Each step's partial dot products q . S over this lane's keys stay in
-    // registers until its half block (kHB steps) is done; the sums over the
+    // dependency carried from step to step is one fma per state
+    // element.  Each step's partial dot product q . S over this lane's
+    // keys stays in a register until the half is done; the sums over the
     // 4 key groups then run as lane swaps on the VALU, and key group kg
     // stores the steps s = kg mod 4 of the half.
     constexpr int kHB = kSB / 2;
-    constexpr int kGS = 8;
     static_for<2>([&](auto hi) __attribute__((always_inline)) {
       constexpr int h0s = decltype(hi)::value * kHB;   // first step of this half
       if (h0s >= ns) return;
-      float acc[NC][kHB];
-      static_for<kHB / kGS>([&](auto gi) __attribute__((always_inline)) {
-        constexpr int sg = decltype(gi)::value * kGS;   // first step of the group within the half
-        if (h0s + sg >= ns) return;
-        static_for<kGS>([&](auto ui) __attribute__((always_inline)) {
-          constexpr int sl = sg + decltype(ui)::value;   // step within the half: acc index
-          constexpr int st = h0s + sl;                   // step within the block
-          float d[KPL], kk[KPL], qs[KPL], vc[NC];
-          if (MODE != kSegState) lds_run<DT, KPL>(lds + G::OQ + st * G::QB + k0 * G::ES, qs);
-          lds_run<DT, KPL>(lds + G::OK + st * G::QB + k0 * G::ES, kk);
-          lds_run<SSLA_F32, KPL>(lds + G::OD + st * G::DB + k0 * 4, d);
+      float acc[kHB];
+      static_for<kHB>([&](auto si) __attribute__((always_inline)) {
+        constexpr int sl = decltype(si)::value;   // step within the half: acc index
+        constexpr int st = h0s + sl;              // step within the block
+        float d[KPL], kk[KPL], qs[KPL];
+        if (MODE != kSegState) lds_run<DT, KPL>(lds + G::OQ + st * G::QB + k0 * G::ES, qs);
+        lds_run<DT, KPL>(lds + G::OK + st * G::QB + k0 * G::ES, kk);
+        lds_run<SSLA_F32, KPL>(lds + G::OD + st * G::DB + k0 * 4, d);
+        const float vc = lds_elem<DT>(lds + G::OV + st * G::VB + (lane & 15) * G::ES);
+        if (MODE == kSegState) {
 #pragma unroll
-          for (int c = 0; c < NC; ++c)
-            vc[c] = lds_elem<DT>(lds + G::OV + st * G::VB + ((lane & 15) + 16 * c) * G::ES);
-          if (MODE == kSegState) {
-#pragma unroll
-            for (int i = 0; i < KPL; ++i) {
-#pragma unroll
-              for (int c = 0; c < NC; ++c) S[c][i] = fmaf(d[i], S[c][i], kk[i] * vc[c]);
-              dprod[i] *= d[i];
-            }
-            return;
+          for (int i = 0; i < KPL; ++i) {
+            S[i] = fmaf(d[i], S[i], kk[i] * vc);
+            dprod[i] *= d[i];
           }
+          return;
+        }
+        float a0 = 0.f, a1 = 0.f;   // two chains: half the dependent fma latency
 #pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            float a0 = 0.f, a1 = 0.f;   // two chains: half the dependent fma latency
-#pragma unroll
-            for (int i = 0; i < KPL; ++i) {
-              S[c][i] = fmaf(d[i], S[c][i], kk[i] * vc[c]);
-              if (i & 1) a1 = fmaf(qs[i], S[c][i], a1);
-              else a0 = fmaf(qs[i], S[c][i], a0);
-            }
-            acc[c][sl] = a0 + a1;
-            // computed here: otherwise the sums sink past the step branches,
-            // which keeps every step's updated state alive until the half ends
-            asm volatile("" : "+v"(acc[c][sl]));
-          }
-        });
+        for (int i = 0; i < KPL; ++i) {
+          S[i] = fmaf(d[i], S[i], kk[i] * vc);
+          if (i & 1) a1 = fmaf(qs[i], S[i], a1);
+          else a0 = fmaf(qs[i], S[i], a0);
+        }
+        acc[sl] = a0 + a1;
+        // computed here: otherwise the sums sink to the end of the half,
+        // which keeps every step's updated state alive until then
+        asm volatile("" : "+v"(acc[sl]));
       });
       if (MODE == kSegState) return;
-      static_for<kHB / kGS>([&](auto gi) __attribute__((always_inline)) {
-        constexpr int sg = decltype(gi)::value * kGS;
-        if (h0s + sg >= ns) return;
-        static_for<kGS>([&](auto ui) __attribute__((always_inline)) {
-#pragma unroll
-          for (int c = 0; c < NC; ++c) acc[c][sg + decltype(ui)::value] = sum_key_groups(acc[c][sg + decltype(ui)::value]);
-        });
-      });
       static_for<kHB / 4>([&](auto ji) __attribute__((always_inline)) {
         constexpr int j = decltype(ji)::value;
-        const int st = h0s + 4 * j + kg;   // steps past ns (or in skipped groups) store nothing
-        // acc[c][4 j + kg] by masks (a select chain would be turned into a
-        // run-time index into acc, which moves acc to scratch memory)
-        const uint32_t m = static_cast<uint32_t>(kg);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const uint32_t bits = (__float_as_uint(acc[c][4 * j]) & (0u - static_cast<uint32_t>(m == 0))) |
-                                (__float_as_uint(acc[c][4 * j + 1]) & (0u - static_cast<uint32_t>(m == 1))) |
-                                (__float_as_uint(acc[c][4 * j + 2]) & (0u - static_cast<uint32_t>(m == 2))) |
-                                (__float_as_uint(acc[c][4 * j + 3]) & (0u - static_cast<uint32_t>(m == 3)));
-          if (col_ok[c] && st < ns) store_out<DT>(o, ((t0 + st) * H + h) * V + col0 + 16 * c, __uint_as_float(bits) * scale);
-        }
+        const int st = h0s + 4 * j + kg;   // this key group's step; past ns: nothing stored
+        const float x = sum4_key_groups(acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]);
+        if (col_ok && st < ns)
+          store_out<DT>(rso, static_cast<uint32_t>((st * H * V + col) * G::ES), x * scale);
       });
     });
   }
   if (MODE == kSegState) {
-    const int64_t gs = unit;
+    if (col_ok) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-      if (col_ok[c]) {
-#pragma unroll
-        for (int i = 0; i < KPL; ++i) sw.slot[gs * H * K * V + e0 + i * V + 16 * c] = S[c][i];
-      }
-    if (vt == 0 && (lane & 15) == 0) {
-#pragma unroll
-      for (int i = 0; i < KPL; ++i) sw.prod[(gs * H + h) * K + k0 + i] = dprod[i];
+      for (int i = 0; i < KPL; ++i) sw.slot[static_cast<int64_t>(cur.gseg) * H * K * V + e0 + i * V] = S[i];
     }
-    return;
-  }
-  if (ht && seg == nseg - 1) {
+    if (cur.vt == 0 && (lane & 15) == 0) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-      if (col_ok[c]) {
+      for (int i = 0; i < KPL; ++i) sw.prod[(static_cast<int64_t>(cur.gseg) * H + h) * K + k0 + i] = dprod[i];
+    }
+  } else if (ht && col_ok && cur.seg == cur.nseg - 1) {
 #pragma unroll
-        for (int i = 0; i < KPL; ++i) ht[((srow * H + h) * K + k0 + i) * V + col0 + 16 * c] = S[c][i];
-      }
+    for (int i = 0; i < KPL; ++i) ht[((static_cast<int64_t>(cur.srow) * H + h) * K + k0 + i) * V + col] = S[i];
   }
 }
 
@@ -618,17 +613,15 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
   const int es = DT == SSLA_F32 ? 4 : 2;
   const bool staged = (K % 16 == 0) && K <= 64 && (V * es) % 16 == 0 && al16(q) && al16(k) && al16(g) && al16(v);
   if (staged) {
-    // two value columns per lane (32-column tiles) where V allows and the
-    // state stays small (K <= 32): the q, k, g staging and the decays are
-    // shared by twice the columns, and each step has two independent chains
-    const int nc = (V % (2 * kBV) == 0 && K <= 32) ? 2 : 1;
-    const int64_t s_items = static_cast<int64_t>(n_seq) * H * (V / (kBV * nc) + (V % (kBV * nc) != 0));
-    const int64_t s_blocks = (s_items + waves_per_block - 1) / waves_per_block;
-    dim3 pgrid(static_cast<unsigned>(s_blocks));
+    // one wavefront per unit; unit indices are 32-bit in the kernel
     const SegLayout L = seg_layout(n_seq, T, H, K, V);
     const bool segmented = L.total > 0 && workspace != nullptr && ws_bytes >= L.total;
+    if (items > 0x7fffffff || (segmented && L.n_segs_max * H * n_vt > 0x7fffffff)) {
+      set_error("gla_recurrent_fwd: too many (sequence or segment, head, tile) items");
+      return SSLA_ERR_UNSUPPORTED;
+    }
     SegWs sw{};
-    dim3 sgrid = pgrid;
+    dim3 sgrid = grid;
     if (segmented) {
       char *w = static_cast<char *>(workspace);
       sw.segoff = reinterpret_cast<const int64_t *>(w + L.segoff);
@@ -636,34 +629,24 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
       sw.prod = reinterpret_cast<float *>(w + L.prod);
       sw.h0c = reinterpret_cast<float *>(w + L.h0c);
       sw.n_segs_max = L.n_segs_max;
-      const int n_svt = V / (kBV * nc) + (V % (kBV * nc) != 0);
-      const int64_t sblocks = (L.n_segs_max * H * n_svt + waves_per_block - 1) / waves_per_block;
-      if (sblocks > 0x7fffffff) {
-        set_error("gla_recurrent_fwd: too many (segment, head, tile) items");
-        return SSLA_ERR_UNSUPPORTED;
-      }
-      sgrid = dim3(static_cast<unsigned>(sblocks));
+      sgrid = dim3(static_cast<unsigned>((L.n_segs_max * H * n_vt + waves_per_block - 1) / waves_per_block));
       hipLaunchKernelGGL(seg_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T,
                          reinterpret_cast<int64_t *>(w + L.segoff));
     }
-#define SSLA_RECS(KPL_, NC_)                                                                                      \
-  if (segmented) {                                                                                                \
-    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegState, NC_>), sgrid, block, 0, st, q, k, v, \
-                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                        \
-    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegOut, NC_>), sgrid, block, 0, st, q, k, v,   \
-                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                        \
-  } else {                                                                                                        \
-    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kPlain, NC_>), pgrid, block, 0, st, q, k, v, g,  \
-                       cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                           \
+#define SSLA_RECS(KPL_)                                                                                     \
+  if (segmented) {                                                                                          \
+    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegState>), sgrid, block, 0, st, q, k, v, \
+                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                  \
+    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kSegOut>), sgrid, block, 0, st, q, k, v,   \
+                       g, cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                  \
+  } else {                                                                                                  \
+    hipLaunchKernelGGL((gla_recurrent_staged_kernel<DT, GDT, KPL_, kPlain>), grid, block, 0, st, q, k, v, g,  \
+                       cu, n_seq, H, V, scale, h0, o, ht, sidx, n_rows, T, status, sw);                     \
   }
-    switch ((K / kKG) * nc) {
-      case 4: SSLA_RECS(4, 1); return launch_status("gla_recurrent_fwd");
-      case 8:
-        if (nc == 2) { SSLA_RECS(4, 2) } else { SSLA_RECS(8, 1) }
-        return launch_status("gla_recurrent_fwd");
-      case 16:
-        if (nc == 2) { SSLA_RECS(8, 2) } else { SSLA_RECS(16, 1) }
-        return launch_status("gla_recurrent_fwd");
+    switch (K / kKG) {
+      case 4: SSLA_RECS(4); return launch_status("gla_recurrent_fwd");
+      case 8: SSLA_RECS(8); return launch_status("gla_recurrent_fwd");
+      case 16: SSLA_RECS(16); return launch_status("gla_recurrent_fwd");
       default: break;   // other K: the general kernel
     }
 #undef SSLA_RECS
