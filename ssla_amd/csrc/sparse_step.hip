@@ -24,6 +24,26 @@
 namespace ssla {
 namespace {
 
+// Sum over the lanes l, l ^ VL, l ^ 2 VL, ... (the row groups that hold one
+// float4 column): rotations inside each 16-lane DPP row (by 8, then by 4:
+// a sum is the same under either pairing), then v_permlane16_swap /
+// v_permlane32_swap across rows -- VALU lane moves, no LDS round trips.
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, x), 0x120 + N, 0xf, 0xf, false));
+}
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+template <int VL>
+__device__ __forceinline__ float sum_row_groups(float x) {
+  if constexpr (VL <= 8) x += row_ror<8>(x);
+  if constexpr (VL <= 4) x += row_ror<4>(x);
+  const u32x2 a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a.x) + __uint_as_float(a.y);
+  const u32x2 b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b.x) + __uint_as_float(b.y);
+}
+
 template <int K, int V>
 __global__ __launch_bounds__(256) void sparse_gla_step_kernel(
     const int32_t *__restrict__ site_idx, int n_active, const float *__restrict__ q,
@@ -33,22 +53,34 @@ __global__ __launch_bounds__(256) void sparse_gla_step_kernel(
   constexpr int VL = V / 4;          // lanes per state row (float4 each)
   constexpr int RG = 64 / VL;        // row groups per wavefront
   constexpr int RPL = K / RG;        // rows per lane
-  static_assert(RPL >= 1 && RG * RPL == K, "unsupported K/V");
+  static_assert(RPL >= 1 && RG * RPL == K && VL >= 4 && VL <= 16, "unsupported K/V");
   const int lane = threadIdx.x & 63;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (item >= static_cast<int64_t>(n_active) * H) return;
-  const int i = static_cast<int>(item / H);
-  const int h = static_cast<int>(item % H);
-  const int site = site_idx[i];
+  // wavefront-uniform: the (site, head) indexing runs on the scalar unit
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int item = static_cast<int>(blockIdx.x) * 4 + wv;   // n_active * H < 2^31 (host check)
+  if (item >= n_active * H) return;
+  const int i = item / H;
+  const int h = item % H;
   const int vc = lane % VL;          // float4 column
   const int rg = lane / VL;          // row group: rows rg*RPL .. rg*RPL+RPL-1
   const int64_t io = static_cast<int64_t>(i) * H + h;
+  // this (site, head)'s inputs first: they do not depend on the site index,
+  // so their loads overlap its load
+  const float4 vv = reinterpret_cast<const float4 *>(v + io * V)[vc];
+  float gg[RPL], kk[RPL], qq[RPL];
+#pragma unroll
+  for (int r = 0; r < RPL; ++r) {
+    const int row = rg * RPL + r;
+    gg[r] = g[io * K + row];
+    kk[r] = k[io * K + row];
+    qq[r] = q[io * K + row];
+  }
+  const int site = site_idx[i];
   if (site < 0 || site >= n_sites || (i > 0 && site_idx[i - 1] >= site)) {
     if (rg == 0) reinterpret_cast<float4 *>(o + io * V)[vc] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (status && lane == 0) __hip_atomic_store(status, SSLA_ERR_ARG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  const float4 vv = reinterpret_cast<const float4 *>(v + io * V)[vc];
   float4 *S = reinterpret_cast<float4 *>(state + (static_cast<int64_t>(site) * H + h) * K * V);
 
   float4 s[RPL];
@@ -58,30 +90,24 @@ __global__ __launch_bounds__(256) void sparse_gla_step_kernel(
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
-    const int row = rg * RPL + r;
-    const float gg = g[io * K + row];
-    const float kk = k[io * K + row];
-    const float qq = q[io * K + row] * scale;
-    const float d = fast_exp2(gg * kLog2e);
-    s[r].x = fmaf(d, s[r].x, kk * vv.x);
-    s[r].y = fmaf(d, s[r].y, kk * vv.y);
-    s[r].z = fmaf(d, s[r].z, kk * vv.z);
-    s[r].w = fmaf(d, s[r].w, kk * vv.w);
-    acc.x = fmaf(qq, s[r].x, acc.x);
-    acc.y = fmaf(qq, s[r].y, acc.y);
-    acc.z = fmaf(qq, s[r].z, acc.z);
-    acc.w = fmaf(qq, s[r].w, acc.w);
+    const float d = fast_exp2(gg[r] * kLog2e);
+    const float qs = qq[r] * scale;
+    s[r].x = fmaf(d, s[r].x, kk[r] * vv.x);
+    s[r].y = fmaf(d, s[r].y, kk[r] * vv.y);
+    s[r].z = fmaf(d, s[r].z, kk[r] * vv.z);
+    s[r].w = fmaf(d, s[r].w, kk[r] * vv.w);
+    acc.x = fmaf(qs, s[r].x, acc.x);
+    acc.y = fmaf(qs, s[r].y, acc.y);
+    acc.z = fmaf(qs, s[r].z, acc.z);
+    acc.w = fmaf(qs, s[r].w, acc.w);
   }
 #pragma unroll
   for (int r = 0; r < RPL; ++r) S[(rg * RPL + r) * VL + vc] = s[r];
 
-#pragma unroll
-  for (int m = VL; m < 64; m <<= 1) {
-    acc.x += __shfl_xor(acc.x, m);
-    acc.y += __shfl_xor(acc.y, m);
-    acc.z += __shfl_xor(acc.z, m);
-    acc.w += __shfl_xor(acc.w, m);
-  }
+  acc.x = sum_row_groups<VL>(acc.x);
+  acc.y = sum_row_groups<VL>(acc.y);
+  acc.z = sum_row_groups<VL>(acc.z);
+  acc.w = sum_row_groups<VL>(acc.w);
   if (rg == 0) reinterpret_cast<float4 *>(o + io * V)[vc] = acc;
 }
 
@@ -104,7 +130,7 @@ extern "C" int ssla_sparse_gla_step(const int32_t *site_idx, int n_active, const
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t items = static_cast<int64_t>(n_active) * H;
   const int64_t blocks = (items + 3) / 4;
-  SSLA_CHECK_ARG(blocks <= 0x7fffffff, "sparse_gla_step: too many active sites");
+  SSLA_CHECK_ARG(items <= 0x7fffffff, "sparse_gla_step: too many active sites");
   dim3 grid(static_cast<unsigned>(blocks)), block(256);
 #define SSLA_STEP(KK, VV)                                                                       \
   if (K == KK && V == VV) {                                                                     \
