@@ -77,7 +77,9 @@ int ssla_status_read(const int32_t *status, int *value_out, void *stream);
  * together with chunk_local_cumsum (ops/utils/cumsum.py:346-364),
  * chunk_fwd_h (ops/common/chunk_h.py:242-294) and the intra-chunk /
  * output kernels (ops/gla/chunk.py:33-249, :644-743).  Supported: dtype
- * BF16 or F16, K == 64, V a multiple of 16 (<= 256); one sequence below
+ * BF16 or F16, K == 64, V a multiple of 16 (<= 256) -- other key widths
+ * run as groups of 64 keys (the last one zero-padded) whose o add up, since
+ * each key's decay only touches its own state row; one sequence below
  * 2^31 bytes per tensor (rows * H * max(K, V) * 4), SSLA_ERR_UNSUPPORTED
  * otherwise.  Only a batch with T * H * max(K, V) * 4 >= 2^31 can hold such
  * a sequence: then cu_seqlens is read back to check (one host
@@ -122,7 +124,8 @@ int ssla_gla_chunk_fwd_noalloc(const void *q, const void *k, const void *v,
  * forward (NULL = zero).  Writes dq, dk [T, H, K] and dv [T, H, V] in the
  * input dtype, dg [T, H, K] in g's dtype, dh0 [N, H, K, V] fp32 (skipped when
  * NULL).  Rows outside [cu_seqlens[0], cu_seqlens[n_seq]) are not written.
- * Supported: dtype BF16 or F16, K == 64, V a multiple of 16 up to 64.
+ * Supported: dtype BF16 or F16, K == 64, V a multiple of 16 up to 64
+ * (other key widths: per group of 64 keys, as in the forward, summing dv).
  * Workspace: ssla_gla_chunk_bwd_workspace_size bytes (16-byte aligned, no
  * initialisation needed): chunk offsets and two fp32 states per chunk
  * (every chunk's entering state and leaving-state gradient). */

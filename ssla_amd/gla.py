@@ -10,10 +10,13 @@ Drop-in for the reference's GLA API (haohq19/ssla ``ops/gla``):
   (reference ops/gla/naive.py:50-111).
 
 They run hand-written gfx950 kernels through libssla_amd.so; there is no
-CPU or Triton fallback.  ``chunk_gla`` is differentiable
-(:class:`ChunkGLAFunction`, backward ``ssla_gla_chunk_bwd``) for the shapes
-the backward kernels take (bf16/fp16, K == 64, V a multiple of 16 up to
-64); the recurrent form is forward-only.  Layouts are the
+CPU or Triton fallback.  The chunk kernels work on 64 keys: other key
+widths (multiples of 16 up to 256) run as groups of 64 keys, the last one
+zero-padded -- the decay is per key, so each key group is an independent
+GLA whose outputs add up (o = sum of the groups' o, ht = the groups' rows).
+``chunk_gla`` is differentiable (:class:`ChunkGLAFunction`, backward
+``ssla_gla_chunk_bwd``) for the shapes the backward kernels take (bf16/fp16,
+V a multiple of 16 up to 64); the recurrent form is forward-only.  Layouts are the
 reference's packed varlen layouts: q, k, g ``[T, H, K]``, v ``[T, H, V]``,
 ``cu_seqlens`` int64 ``[N + 1]``, states ``[N, H, K, V]`` fp32.
 """
@@ -29,17 +32,40 @@ __all__ = ["chunk_gla", "ChunkGLAFunction", "fused_recurrent_gla", "naive_gla_re
            "chunk_backward_supports"]
 
 
+KD = 64   # keys of one chunk-kernel call
+
+
 def chunk_kernel_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
-    """True when the fused MFMA chunk kernel handles this dtype/shape
-    (bf16/fp16, K == 64, V a multiple of 16 up to 256)."""
-    return (q.dtype in (torch.bfloat16, torch.float16) and q.shape[-1] == 64
+    """True when the fused MFMA chunk kernels handle this dtype/shape
+    (bf16/fp16, K a multiple of 16 up to 256 -- run in groups of 64 keys --
+    and V a multiple of 16 up to 256)."""
+    K = q.shape[-1]
+    return (q.dtype in (torch.bfloat16, torch.float16) and K % 16 == 0 and 0 < K <= 256
             and v.shape[-1] % 16 == 0 and v.shape[-1] <= 256)
 
 
 def chunk_backward_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
     """True when ``ssla_gla_chunk_bwd`` handles this dtype/shape (bf16/fp16,
-    K == 64, V a multiple of 16 up to 64)."""
+    K a multiple of 16 up to 256, V a multiple of 16 up to 64)."""
     return chunk_kernel_supports(q, v) and v.shape[-1] <= 64
+
+
+def _key_groups(K: int):
+    """(first key, keys) of the 64-key groups that cover K keys."""
+    return [(s, min(KD, K - s)) for s in range(0, K, KD)]
+
+
+def _keys_of(x: Optional[torch.Tensor], s: int, w: int, dim: int) -> Optional[torch.Tensor]:
+    """Keys s .. s + w - 1 of x along ``dim``, zero-padded to KD keys."""
+    if x is None:
+        return None
+    if s == 0 and w == KD and x.shape[dim] == KD:
+        return x
+    shape = list(x.shape)
+    shape[dim] = KD
+    out = x.new_zeros(shape)
+    out.narrow(dim, 0, w).copy_(x.narrow(dim, s, w))
+    return out
 
 
 def _prep(name, q, k, v, g, cu_seqlens, initial_state, allow_grad=False):
@@ -86,9 +112,9 @@ def chunk_gla(
     outside ``[cu_seqlens[0], cu_seqlens[-1])`` are unspecified, as in the
     reference (``torch.empty_like``).
 
-    bf16/fp16 inputs with K == 64 run the fused MFMA chunk kernel; other
-    shapes and fp32 inputs run the fused recurrent kernel (same math, fp32
-    state, serial over time).
+    bf16/fp16 inputs with K a multiple of 16 up to 256 run the fused MFMA
+    chunk kernels (in groups of 64 keys); other shapes and fp32 inputs run
+    the fused recurrent kernel (same math, fp32 state, serial over time).
     """
     if initial_state is not None and initial_state.shape[0] != len(cu_seqlens) - 1:
         raise ValueError(
@@ -103,7 +129,7 @@ def chunk_gla(
     if grad:
         if not chunk_backward_supports(q, v):
             raise NotImplementedError(
-                "chunk_gla backward needs bf16/fp16 inputs with K == 64 and V a multiple of 16 up to 64 "
+                "chunk_gla backward needs bf16/fp16 inputs with K a multiple of 16 up to 256 and V a multiple of 16 up to 64 "
                 f"(got {q.dtype}, K={q.shape[-1]}, V={v.shape[-1]})")
         return ChunkGLAFunction.apply(q, k, v, g, float(scale), h0, output_final_state, cu)
     return _chunk_fwd(q, k, v, g, cu, float(scale), h0, output_final_state)
@@ -115,10 +141,32 @@ def _chunk_fwd(q, k, v, g, cu, scale, h0, output_final_state):
     N = cu.numel() - 1
     if h0 is not None and h0.shape != (N, H, K, V):
         raise ValueError(f"chunk_gla: initial_state must be {(N, H, K, V)}, got {tuple(h0.shape)}")
+    if not chunk_kernel_supports(q, v):
+        o = torch.empty_like(v)
+        ht = torch.empty(N, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
+        return _recurrent(q, k, v, g, cu, float(scale), h0, o, ht, None, 0)
+    if K == KD:
+        return _chunk_call(q, k, v, g, cu, scale, h0, output_final_state)
+    # key groups: o adds up over the groups (in fp32, rounded once more),
+    # ht stacks their key rows
+    os, hts = [], []
+    for s, w in _key_groups(K):
+        o_i, ht_i = _chunk_call(_keys_of(q, s, w, 2), _keys_of(k, s, w, 2), v, _keys_of(g, s, w, 2), cu, scale,
+                                _keys_of(h0, s, w, 2), output_final_state)
+        os.append(o_i)
+        if ht_i is not None:
+            hts.append(ht_i[:, :, :w])
+    o = os[0] if len(os) == 1 else torch.stack(os).float().sum(0).to(v.dtype)
+    return o, (torch.cat(hts, dim=2) if output_final_state else None)
+
+
+def _chunk_call(q, k, v, g, cu, scale, h0, output_final_state):
+    """One ssla_gla_chunk_fwd call (K == KD)."""
+    T, H, K = q.shape
+    V = v.shape[-1]
+    N = cu.numel() - 1
     o = torch.empty_like(v)
     ht = torch.empty(N, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
-    if not chunk_kernel_supports(q, v):
-        return _recurrent(q, k, v, g, cu, float(scale), h0, o, ht, None, 0)
     lib = _lib.load()
     ws_bytes = lib.ssla_gla_chunk_workspace_size(N, T, H, K, V)
     ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
@@ -147,23 +195,40 @@ class ChunkGLAFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do, dht):
         q, k, v, g, h0, cu = ctx.saved_tensors
-        T, H, K = q.shape
-        V = v.shape[-1]
-        N = cu.numel() - 1
         do = do.to(v.dtype).contiguous()
         dht = None if dht is None else dht.to(torch.float32).contiguous()
-        dq, dk = torch.empty_like(q), torch.empty_like(k)
-        dv, dg = torch.empty_like(v), torch.empty_like(g)
-        dh0 = torch.empty_like(h0) if h0 is not None else None
-        lib = _lib.load()
-        ws_bytes = lib.ssla_gla_chunk_bwd_workspace_size(N, T, H, K, V)
-        ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
-        st = lib.ssla_gla_chunk_bwd(
-            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.DTYPE_CODE[g.dtype], _lib.ptr(cu), N, T, H, K, V,
-            float(ctx.scale), _lib.ptr(h0), _lib.ptr(do), _lib.ptr(dht), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
-            _lib.ptr(dg), _lib.ptr(dh0), _lib.DTYPE_CODE[q.dtype], _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
-        _lib.check(st, "ssla_gla_chunk_bwd")
-        return dq, dk, dv, dg, None, dh0, None, None
+        K = q.shape[-1]
+        if K == KD:
+            dq, dk, dv, dg, dh0 = _chunk_bwd_call(q, k, v, g, h0, cu, do, dht, ctx.scale)
+            return dq, dk, dv, dg, None, dh0, None, None
+        # key groups: each group's gradients are its keys' rows; dv adds up
+        parts = [_chunk_bwd_call(_keys_of(q, s, w, 2), _keys_of(k, s, w, 2), v, _keys_of(g, s, w, 2),
+                                 _keys_of(h0, s, w, 2), cu, do, _keys_of(dht, s, w, 2), ctx.scale)
+                 for s, w in _key_groups(K)]
+        widths = [w for _, w in _key_groups(K)]
+        cat = lambda i, dim: torch.cat([p[i].narrow(dim, 0, w) for p, w in zip(parts, widths)], dim=dim)
+        dv = parts[0][2] if len(parts) == 1 else torch.stack([p[2] for p in parts]).float().sum(0).to(v.dtype)
+        dh0 = cat(4, 2) if h0 is not None else None
+        return cat(0, 2), cat(1, 2), dv, cat(3, 2), None, dh0, None, None
+
+
+def _chunk_bwd_call(q, k, v, g, h0, cu, do, dht, scale):
+    """One ssla_gla_chunk_bwd call (K == KD): dq, dk, dv, dg, dh0."""
+    T, H, K = q.shape
+    V = v.shape[-1]
+    N = cu.numel() - 1
+    dq, dk = torch.empty_like(q), torch.empty_like(k)
+    dv, dg = torch.empty_like(v), torch.empty_like(g)
+    dh0 = torch.empty_like(h0) if h0 is not None else None
+    lib = _lib.load()
+    ws_bytes = lib.ssla_gla_chunk_bwd_workspace_size(N, T, H, K, V)
+    ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    st = lib.ssla_gla_chunk_bwd(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.DTYPE_CODE[g.dtype], _lib.ptr(cu), N, T, H, K, V,
+        float(scale), _lib.ptr(h0), _lib.ptr(do), _lib.ptr(dht), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+        _lib.ptr(dg), _lib.ptr(dh0), _lib.DTYPE_CODE[q.dtype], _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
+    _lib.check(st, "ssla_gla_chunk_bwd")
+    return dq, dk, dv, dg, dh0
 
 
 def _recurrent(q, k, v, g, cu, scale, h0, o, ht, state_idx, n_rows, status=None):

@@ -120,6 +120,28 @@ def test_chunk_fp16_and_bf16_gates(dev):
         assert_close(ht, rht, 0.0, f"ht[{dtype}]", band=hb, ratio_max=hrat)
 
 
+# (o band, o ratio, ht band, ht ratio) for key widths other than 64, <= 2x
+# measured (K > 64 adds the key groups' bf16 outputs in fp32)
+KW_BANDS = {16: (0.095, 6.7e-3, 0.019, 1.5e-3), 32: (0.06, 6.7e-3, 0.02, 1.5e-3), 48: (0.062, 6.6e-3, 0.024, 1.5e-3),
+            96: (0.088, 7.4e-3, 0.019, 1.4e-3), 128: (0.083, 7.4e-3, 0.022, 1.4e-3)}
+
+
+@pytest.mark.parametrize("K", [16, 32, 48, 96, 128])
+def test_chunk_key_widths(dev, K):
+    """K other than 64 (the D = 32 heads of configs 3 and 5 among them) runs
+    the chunk kernels in groups of 64 keys, the last one zero-padded."""
+    from ssla_amd.gla import chunk_gla, chunk_kernel_supports
+    lens = [0, 1, 63, 64, 65, 200, 7]
+    q, k, v, g, cu, s0 = _inputs(lens, 3, K, 32, torch.bfloat16, seed=K)
+    assert chunk_kernel_supports(q, v)
+    print(f"chunk key width K={K}", flush=True)
+    o, ht = _run(chunk_gla, q, k, v, g, cu, s0, K ** -0.5, dev)
+    ro, rht = _oracle(q, k, v, g, cu, s0, K ** -0.5)
+    ob, orat, hb, hrat = KW_BANDS[K]
+    assert_close(o, ro, 0.0, f"o[K={K}]", band=ob, ratio_max=orat)
+    assert_close(ht, rht, 0.0, f"ht[K={K}]", band=hb, ratio_max=hrat)
+
+
 def test_chunk_no_initial_state_no_final(dev):
     from ssla_amd.gla import chunk_gla
     q, k, v, g, cu, _ = _inputs([150], 2, 64, 32, torch.bfloat16, seed=5, h0=False)

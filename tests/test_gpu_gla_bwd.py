@@ -35,28 +35,32 @@ BANDS = {
              "dh0": (6e-5, 5e-6)},
     "16-bit g bf16": {"dq": (0.11, 3.2e-3), "dk": (0.22, 3.4e-3), "dv": (0.099, 3.4e-3), "dg": (0.14, 3.1e-3),
                       "dh0": (2.4e-4, 4.8e-6)},
+    "K=32": {"dq": (0.042, 3.3e-3), "dk": (0.027, 3.4e-3), "dv": (0.05, 3.3e-3), "dg": (6.6e-4, 9.5e-5),
+             "dh0": (7.9e-5, 4.6e-6)},
+    "K=128": {"dq": (0.053, 3.3e-3), "dk": (0.051, 3.3e-3), "dv": (0.058, 4.9e-3), "dg": (6.2e-4, 1e-4),
+              "dh0": (6.9e-5, 3.7e-6)},
     "16-bit g fp16": {"dq": (0.02, 4.3e-4), "dk": (0.016, 4.1e-4), "dv": (8.4e-3, 4.2e-4), "dg": (0.016, 3.8e-4),
                       "dh0": (3.6e-4, 6.8e-6)},
 }
 
 
-def _inputs(lens, H, V, dtype, seed, gate="logsig", h0=True):
+def _inputs(lens, H, V, dtype, seed, gate="logsig", h0=True, K=64):
     gen = torch.Generator().manual_seed(seed)
     T = int(sum(lens))
-    q, k = torch.randn(T, H, 64, generator=gen), torch.randn(T, H, 64, generator=gen)
+    q, k = torch.randn(T, H, K, generator=gen), torch.randn(T, H, K, generator=gen)
     v = torch.randn(T, H, V, generator=gen)
     if gate == "logsig":
-        g = F.logsigmoid(torch.randn(T, H, 64, generator=gen) / 16)
+        g = F.logsigmoid(torch.randn(T, H, K, generator=gen) / 16)
     elif gate == "randn-1":
-        g = torch.randn(T, H, 64, generator=gen) - 1.0
+        g = torch.randn(T, H, K, generator=gen) - 1.0
     elif gate == "strong":
-        g = -5.0 - torch.rand(T, H, 64, generator=gen)
+        g = -5.0 - torch.rand(T, H, K, generator=gen)
     else:
-        g = torch.zeros(T, H, 64)
+        g = torch.zeros(T, H, K)
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64)
-    s0 = torch.randn(len(lens), H, 64, V, generator=gen) * 0.1 if h0 else None
+    s0 = torch.randn(len(lens), H, K, V, generator=gen) * 0.1 if h0 else None
     do = torch.randn(T, H, V, generator=gen)
-    dht = torch.randn(len(lens), H, 64, V, generator=gen) * 0.1 if h0 else None
+    dht = torch.randn(len(lens), H, K, V, generator=gen) * 0.1 if h0 else None
     return q.to(dtype), k.to(dtype), v.to(dtype), g, cu, s0, do.to(dtype), dht
 
 
@@ -74,8 +78,8 @@ def _gpu_grads(dev, q, k, v, g, cu, s0, do, dht, scale):
     return out
 
 
-def _check(dev, lens, H, V, dtype, seed, gate="logsig", h0=True, scale=64 ** -0.5, tag="", case=None):
-    q, k, v, g, cu, s0, do, dht = _inputs(lens, H, V, dtype, seed, gate, h0)
+def _check(dev, lens, H, V, dtype, seed, gate="logsig", h0=True, scale=64 ** -0.5, tag="", case=None, K=64):
+    q, k, v, g, cu, s0, do, dht = _inputs(lens, H, V, dtype, seed, gate, h0, K=K)
     print(f"gla bwd {tag}: lens={lens} H={H} V={V} {dtype} gate={gate} h0={h0}", flush=True)
     got = _gpu_grads(dev, q, k, v, g, cu, s0, do, dht, scale)
     ref = oracle.gla_recurrent_bwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), g.numpy(), cu.numpy(),
@@ -107,6 +111,14 @@ def test_chunk_bwd_long_sequences(dev):
     """Two 4096-token sequences (64 chunks each), H = 4: the state passes
     carry 64 chunks."""
     _check(dev, [4096, 4096], 4, 64, torch.bfloat16, seed=5, tag="long", case="long")
+
+
+@pytest.mark.parametrize("K", [32, 128])
+def test_chunk_bwd_key_widths(dev, K):
+    """K other than 64: the backward runs per group of 64 keys (the last one
+    zero-padded) and dv adds up over the groups."""
+    _check(dev, [0, 1, 63, 64, 65, 200, 7], 3, 32, torch.bfloat16, seed=K, tag=f"K={K}", case=f"K={K}", K=K,
+           scale=K ** -0.5)
 
 
 def test_chunk_bwd_unsupported_raises(dev):
