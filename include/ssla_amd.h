@@ -249,7 +249,7 @@ int ssla_site_finish(const uint16_t *o, int64_t n, int hd, const uint16_t *wo, c
  * objectness, then the classes; zero where a prediction does not read a
  * branch) and b_pred fp32 [16]; stride.  out bf16 [batch, sum h w, n_out]:
  * ((p0 + x) s, (p1 + y) s, exp(p2) s, exp(p3) s, p4, p5 ...) per cell in
- * row-major cell order, levels in turn.  width a multiple of 8 up to 256,
+ * row-major cell order, levels in turn.  width a multiple of 16 up to 256,
  * c a multiple of 32, 5 <= n_out <= 16.  No reference C function. */
 #define SSLA_HEAD_MAX_LEVELS 4
 typedef struct {

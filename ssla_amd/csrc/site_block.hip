@@ -340,23 +340,33 @@ struct HeadArgs {
   int n_levels, batch, n_anchor, n_out, width;
 };
 
+// One workgroup per 16 cells of a level, 4 wavefronts: wavefront w computes
+// the feature tiles t = w, w + 4, ... (16 features each) of the 16 cells,
+// then the prediction GEMM's K range [128 w, 128 w + 128) of the features;
+// the four partial predictions are summed through LDS and wavefront 0
+// decodes and stores.  Splitting the features across the wavefronts (not
+// the cells) keeps each wavefront's chain of dependent MFMAs short: the
+// call is a few hundred workgroups with short chains instead of a few
+// dozen with long ones.
+constexpr int kHeadCells = 16;
 __global__ __launch_bounds__(64 * kWaves) void detect_head_kernel(HeadArgs a, uint16_t *__restrict__ out) {
-  __shared__ __align__(16) uint16_t feat[kRows][kHeadLdsRow];
+  __shared__ __align__(16) uint16_t feat[kHeadCells][kHeadLdsRow];
+  __shared__ f32x4 part[kWaves][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int r = lane & 15, kq = 8 * (lane >> 4);
   int L = 0;
   while (L + 1 < a.n_levels && static_cast<int>(blockIdx.x) >= a.tile0[L + 1]) ++L;
   const ssla_head_level &lv = a.lv[L];
   const int hw = lv.h * lv.w, n_cell = a.batch * hw;
-  const int c0 = (static_cast<int>(blockIdx.x) - a.tile0[L]) * kRows + 16 * wv;   // this wavefront's first cell
+  const int c0 = (static_cast<int>(blockIdx.x) - a.tile0[L]) * kHeadCells;   // this workgroup's first cell
   const int F = 2 * a.width;
-  // ---- branches: 16 cells x F features, K = c in steps of 32
+  // ---- branches: 16 cells x this wavefront's feature tiles, K = c in steps of 32
   {
     const int cell = c0 + r;
     const bool ok = cell < n_cell;
     const int b = ok ? cell / hw : 0, rem = ok ? cell - b * hw : 0;
     const float *xb = lv.grid + static_cast<int64_t>(b) * lv.c * hw + rem;
-    constexpr int NT = kHeadF / 16;
+    constexpr int NT = kHeadF / 16 / kWaves;   // tiles per wavefront
     f32x4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -366,32 +376,43 @@ __global__ __launch_bounds__(64 * kWaves) void detect_head_kernel(HeadArgs a, ui
       for (int e = 0; e < 8; ++e) xv[e] = ok ? xb[static_cast<int64_t>(k0 + kq + e) * hw] : 0.f;
       const bf16x8 av = __builtin_convertvector(xv, bf16x8);
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-        if (16 * t < F)
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bf16_piece(lv.w_br, 16 * t + r, lv.c, k0 + kq, true),
+      for (int t = 0; t < NT; ++t) {
+        const int tile = kWaves * t + wv;
+        if (16 * tile < F)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bf16_piece(lv.w_br, 16 * tile + r, lv.c, k0 + kq, true),
                                                           acc[t], 0, 0, 0);
+      }
     }
-    // f = SiLU(acc scale + shift), rounded to bf16, into this wavefront's rows
+    // f = SiLU(acc scale + shift), rounded to bf16, into the features' rows
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      if (16 * t >= F) continue;
-      const int col = 16 * t + r;
+      const int tile = kWaves * t + wv;
+      if (16 * tile >= F) continue;
+      const int col = 16 * tile + r;
       const float sc = lv.br_scale[col], sh = lv.br_shift[col];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float y = fmaf(acc[t][i], sc, sh);
         const float f = y / (1.f + expf(-y));
-        feat[16 * wv + 4 * (lane >> 4) + i][col] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+        feat[4 * (lane >> 4) + i][col] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
       }
     }
   }
   __syncthreads();
-  // ---- predictions: 16 cells x 16 outputs, K = F
-  f32x4 p = {0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < F; k0 += 32) {
-    const bf16x8 av = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(&feat[16 * wv + r][k0 + kq]));
-    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bf16_piece(lv.w_pred, r, F, k0 + kq, true), p, 0, 0, 0);
+  // ---- predictions: 16 cells x 16 outputs, this wavefront's quarter of K = F
+  {
+    f32x4 p = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 32 * wv; k0 < F; k0 += 32 * kWaves) {   // F is a multiple of 32 (host check)
+      const bf16x8 av = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(&feat[r][k0 + kq]));
+      p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bf16_piece(lv.w_pred, r, F, k0 + kq, true), p, 0, 0, 0);
+    }
+    part[wv][lane] = p;
   }
+  __syncthreads();
+  if (wv != 0) return;
+  f32x4 p = part[0][lane];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) p += part[w][lane];
   const int j = r;   // output column
   if (j >= a.n_out) return;
   const float s = static_cast<float>(lv.stride), bj = lv.b_pred[j];
@@ -418,8 +439,8 @@ extern "C" int ssla_detect_head(const ssla_head_level *levels, int n_levels, int
   clear_error();
   SSLA_CHECK_ARG(levels && out && n_levels > 0 && n_levels <= SSLA_HEAD_MAX_LEVELS && batch > 0,
                  "detect_head: bad arguments (levels=%d batch=%d)", n_levels, batch);
-  if (width <= 0 || width > kHeadMaxW || width % 8 != 0 || n_out < 5 || n_out > 16) {
-    set_error("detect_head: needs a branch width that is a multiple of 8 up to %d and 5..16 outputs "
+  if (width <= 0 || width > kHeadMaxW || width % 16 != 0 || n_out < 5 || n_out > 16) {
+    set_error("detect_head: needs a branch width that is a multiple of 16 up to %d and 5..16 outputs "
               "(width=%d n_out=%d)", kHeadMaxW, width, n_out);
     return SSLA_ERR_UNSUPPORTED;
   }
@@ -443,7 +464,7 @@ extern "C" int ssla_detect_head(const ssla_head_level *levels, int n_levels, int
     a.tile0[l] = static_cast<int>(tiles);
     a.anchor0[l] = static_cast<int>(anchors);
     const int64_t cells = static_cast<int64_t>(batch) * lv.h * lv.w;
-    tiles += (cells + kRows - 1) / kRows;
+    tiles += (cells + kHeadCells - 1) / kHeadCells;
     anchors += static_cast<int64_t>(lv.h) * lv.w;
     SSLA_CHECK_ARG(tiles < (int64_t{1} << 30) && anchors * batch * n_out < (int64_t{1} << 31),
                    "detect_head: too many cells");
