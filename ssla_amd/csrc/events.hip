@@ -420,15 +420,19 @@ __global__ void rf_fields(const int64_t *__restrict__ act, const int64_t *__rest
   }
 }
 
+// o_fidx (optional): the active-field index of every row, the high part of
+// its sorted key (active index * t_stride + time).
 __global__ void rf_emit(const int32_t *__restrict__ perm, int64_t E_out, const int64_t *__restrict__ pre_src,
                         const int64_t *__restrict__ pre_pos, const int64_t *__restrict__ time,
-                        int64_t *__restrict__ o_src, int64_t *__restrict__ o_time, int64_t *__restrict__ o_pos) {
+                        int64_t *__restrict__ o_src, int64_t *__restrict__ o_time, int64_t *__restrict__ o_pos,
+                        const uint64_t *__restrict__ skey, uint64_t t_stride, int32_t *__restrict__ o_fidx) {
   GRID_STRIDE(i, E_out) {
     const int32_t k = perm[i];
     const int64_t s = pre_src[k];
     o_src[i] = s;
     if (o_time) o_time[i] = time[s];
-    o_pos[i] = pre_pos[k];
+    if (o_pos) o_pos[i] = pre_pos[k];
+    if (o_fidx) o_fidx[i] = static_cast<int32_t>(skey[i] / t_stride);
   }
 }
 
@@ -829,7 +833,8 @@ __device__ __forceinline__ int64_t run_count(const int64_t *__restrict__ time, i
   return lo;
 }
 
-// one thread per (event, kernel position)
+// One thread per (event, kernel position).  o_time, o_pos, dst_map and
+// o_fidx (the row's active-field index, act_pre of its field) are optional.
 __global__ void rf_merge(const int32_t *__restrict__ ev2g, const int64_t *__restrict__ gb,
                          const int64_t *__restrict__ gh, const int64_t *__restrict__ gw,
                          const int64_t *__restrict__ gstart, const int64_t *__restrict__ glen,
@@ -837,7 +842,8 @@ __global__ void rf_merge(const int32_t *__restrict__ ev2g, const int64_t *__rest
                          const int64_t *__restrict__ lut, int64_t n_rf, int A, int H, int W,
                          const int64_t *__restrict__ ev_pre, const int64_t *__restrict__ time, int64_t E_in,
                          int64_t E_out, int64_t *__restrict__ o_src, int64_t *__restrict__ o_time,
-                         int64_t *__restrict__ o_pos, int32_t *__restrict__ dst_map) {
+                         int64_t *__restrict__ o_pos, int32_t *__restrict__ dst_map,
+                         const int64_t *__restrict__ act_pre, int32_t *__restrict__ o_fidx) {
   const int64_t HW = static_cast<int64_t>(H) * W;
   GRID_STRIDE(t, E_in * A) {
     const int64_t e = t / A;
@@ -862,8 +868,9 @@ __global__ void rf_merge(const int32_t *__restrict__ ev2g, const int64_t *__rest
     if (row < 0 || row >= E_out) continue;   // inconsistent inputs: drop, never write out of range
     o_src[row] = e;
     if (o_time) o_time[row] = time[e];
-    o_pos[row] = a;
+    if (o_pos) o_pos[row] = a;
     if (dst_map) dst_map[e * A + a] = static_cast<int32_t>(row);
+    if (o_fidx) o_fidx[row] = static_cast<int32_t>(act_pre[b * n_rf + rf]);
   }
 }
 }  // namespace
@@ -1005,7 +1012,8 @@ extern "C" int ssla_rf_scatter_fill(const int64_t *gr_len, int64_t G, const int6
   if (s) return s;
   if (E_out > 0)
     hipLaunchKernelGGL(rf_emit, dim3(grid_for(E_out)), dim3(kThreads), 0, st, L.perm, E_out, L.pre_src, L.pre_pos,
-                       time, out_src, out_time, out_pos);
+                       time, out_src, out_time, out_pos, static_cast<const uint64_t *>(nullptr), t_stride,
+                       static_cast<int32_t *>(nullptr));
   if (n_active > 0) {
     hipError_t e = hipMemcpyAsync(f_index, L.f_index, sizeof(int64_t) * n_active, hipMemcpyDeviceToDevice, st);
     if (e == hipSuccess) e = hipMemcpyAsync(f_len, L.f_len, sizeof(int64_t) * n_active, hipMemcpyDeviceToDevice, st);
@@ -1054,9 +1062,226 @@ extern "C" int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_
     if (E_out > 0)
       hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.val, gr_batch, gr_h, gr_w,
                          L.gstart, gr_len, L.pixmap, inv, lut, n_rf, A, H, W, L.ev_pre, time, E_in, E_out, out_src,
-                         out_time, out_pos, dst_map);
+                         out_time, out_pos, dst_map, static_cast<const int64_t *>(nullptr),
+                         static_cast<int32_t *>(nullptr));
   }
   return launch_status("rf_scatter_fill_sorted");
+}
+
+// ---- SparsePool in two calls --------------------------------------------------------
+// SparsePool.forward (reference layers/sparse_pooling.py:14-48) with the
+// receptive-field gather in front of it (utils/farsecnn_utils.py:177-265),
+// for callers that need only the pooled sequences: the field rows are never
+// stored as [rows, C] features -- the reduction reads the pixel events
+// through each row's source index.
+//   plan: the field plan, the (field, time)-ordered rows (source event,
+//         time, active field), the segment heads (a field's first row, or
+//         a time change inside a field) and their exclusive prefix sum.
+//   emit: per segment the max or mean of its rows' features and its time;
+//         per active field its segment count, batch, h and w.
+namespace {
+struct PoolWs {
+  RfWs rf;
+  int64_t *src, *tim, *head, *segx;
+  int32_t *fidx, *inv;
+  void *tmp;
+  size_t tmp_bytes, total;
+};
+PoolWs pool_layout(void *ws, int64_t G, int B, int H, int W, int64_t n_rf, int A, int64_t E_cap) {
+  PoolWs L;
+  L.rf = rf_layout(ws, G, static_cast<int64_t>(B) * H * W, static_cast<int64_t>(B) * n_rf, E_cap);
+  Carve c{static_cast<char *>(ws), L.rf.total};
+  L.src = c.take<int64_t>(E_cap);
+  L.tim = c.take<int64_t>(E_cap);
+  L.head = c.take<int64_t>(E_cap);
+  L.segx = c.take<int64_t>(E_cap);
+  L.fidx = c.take<int32_t>(E_cap);
+  L.inv = c.take<int32_t>(static_cast<int64_t>(H) * W * A);
+  L.tmp_bytes = scan_temp_bytes(E_cap);
+  L.tmp = c.take<char>(L.tmp_bytes);
+  L.total = c.off;
+  return L;
+}
+
+// head[r] = 1 where row r starts a pooling segment: the first row, a new
+// field, or a time different from the row before (reference
+// sparse_pooling.py:26-31: unique_consecutive of time + field * max_v).
+__global__ void pool_row_heads(const int32_t *__restrict__ fidx, const int64_t *__restrict__ tim, int64_t n,
+                               int64_t *__restrict__ head) {
+  GRID_STRIDE(r, n) head[r] = (r == 0 || fidx[r] != fidx[r - 1] || tim[r] != tim[r - 1]) ? 1 : 0;
+}
+
+// One thread per (row, channel); the threads of a segment's first row walk
+// the segment.  MEAN: the fp64 sum in row order over the count, rounded
+// once.  Max: the first row among equal maxima; NaN never wins; a segment
+// whose values are all NaN gives 0 (scatter_max's rule for a row that no
+// event wins).  Then per active field its segment count and coordinates.
+template <bool MEAN>
+__global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C, const int64_t *__restrict__ src,
+                               const int64_t *__restrict__ tim, const int64_t *__restrict__ head,
+                               const int64_t *__restrict__ segx, int64_t E_out, int64_t n_seg,
+                               const int64_t *__restrict__ f_index, const int64_t *__restrict__ f_len,
+                               const int64_t *__restrict__ ev_pre, int64_t n_act, int64_t n_rf,
+                               const int64_t *__restrict__ outcoord, float *__restrict__ o_ev,
+                               int64_t *__restrict__ o_time, int64_t *__restrict__ o_len, int64_t *__restrict__ o_b,
+                               int64_t *__restrict__ o_h, int64_t *__restrict__ o_w) {
+  GRID_STRIDE(t, E_out * C) {
+    const int64_t r = t / C;
+    const int c = static_cast<int>(t - r * C);
+    if (!head[r]) continue;
+    const int64_t s = segx[r];
+    if (s < 0 || s >= n_seg) continue;
+    double sum = 0.0;
+    float best = -INFINITY;
+    bool found = false;
+    int64_t r2 = r;
+    do {
+      const int64_t e = src[r2];
+      const float x = (e >= 0 && e < E_in) ? ev[e * C + c] : 0.f;
+      if constexpr (MEAN) {
+        sum += static_cast<double>(x);
+      } else {
+        const bool take = x > best || (!found && x == best);
+        best = take ? x : best;
+        found = found || take;
+      }
+      ++r2;
+    } while (r2 < E_out && !head[r2]);
+    if constexpr (MEAN) o_ev[s * C + c] = static_cast<float>(sum / static_cast<double>(r2 - r));
+    else o_ev[s * C + c] = found ? best : 0.f;
+    if (c == 0) o_time[s] = tim[r];
+  }
+  GRID_STRIDE(j, n_act) {
+    const int64_t f = f_index[j], len = f_len[j];
+    const int64_t st = ev_pre[f];
+    int64_t segs = 0;
+    if (len > 0 && st >= 0 && st + len <= E_out) segs = segx[st + len - 1] + head[st + len - 1] - segx[st];
+    const int64_t rf = f % n_rf;
+    o_len[j] = segs;
+    o_b[j] = f / n_rf;
+    o_h[j] = outcoord[rf * 2 + 1];
+    o_w[j] = outcoord[rf * 2];
+  }
+}
+}  // namespace
+
+extern "C" size_t ssla_sparse_pool_workspace_size(int64_t G, int64_t E_in, int B, int H, int W, int64_t n_rf, int A) {
+  if (G < 0 || E_in < 0 || B <= 0 || H <= 0 || W <= 0 || n_rf <= 0 || A <= 0) return 0;
+  return pool_layout(nullptr, G, B, H, W, n_rf, A, E_in * A).total;
+}
+
+// counts_out[0..3] = active fields, segments, field rows, and 1 if a group
+// coordinate or run was out of range (then nothing else was computed).
+extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
+                                     const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
+                                     int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t *counts_out,
+                                     void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 && counts_out,
+                 "sparse_pool_plan: bad arguments");
+  const int64_t E_cap = E_in * A, n_f = static_cast<int64_t>(B) * n_rf;
+  SSLA_CHECK_ARG(E_cap < 0x7fffffff, "sparse_pool_plan: events x kernel positions must stay below 2^31");
+  const PoolWs L = pool_layout(workspace, G, B, H, W, n_rf, A, E_cap);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("sparse_pool_plan: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int s = ssla_rf_scatter_plan(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, workspace,
+                               L.rf.total, stream);
+  if (s) return s;
+  int64_t c[8] = {};
+  int bad = 0;
+  s = ssla_events_counts(workspace, c, 4, &bad, stream);
+  if (s) return s;
+  for (int i = 0; i < 4; ++i) counts_out[i] = 0;
+  if (bad) {
+    counts_out[3] = 1;
+    return SSLA_OK;
+  }
+  const int64_t n_act = c[0], E_out = c[1], t_max = c[2];
+  if (n_act < 0 || n_act > n_f || E_out < 0 || E_out > E_cap || t_max < 0) {
+    set_error("sparse_pool_plan: plan counts outside their bounds");
+    return SSLA_ERR_LAUNCH;
+  }
+  int64_t n_seg = 0;
+  if (E_out > 0) {
+    if (c[3] == 0) {   // every pixel run sorted by time: the counting fill
+      const int64_t HW = static_cast<int64_t>(H) * W;
+      hipLaunchKernelGGL(fill_i32, dim3(grid_for(HW * A)), dim3(kThreads), 0, st, L.inv, HW * A, -1);
+      hipLaunchKernelGGL(rf_inv_lut, dim3(grid_for(n_rf * A)), dim3(kThreads), 0, st, lut, n_rf, A, HW, L.inv);
+      hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.rf.val, gr_batch, gr_h, gr_w,
+                         L.rf.gstart, gr_len, L.rf.pixmap, L.inv, lut, n_rf, A, H, W, L.rf.ev_pre, time, E_in, E_out,
+                         L.src, L.tim, static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr),
+                         L.rf.act_pre, L.fidx);
+    } else {           // the sort fill
+      const uint64_t t_stride = static_cast<uint64_t>(t_max) + 1;
+      hipLaunchKernelGGL(rf_enumerate, dim3(grid_for(n_f * A)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W,
+                         L.rf.pixmap, gr_len, L.rf.gstart, L.rf.act, L.rf.act_pre, L.rf.ev_pre, time, E_in, t_stride,
+                         L.rf.key, L.rf.val, L.rf.pre_src, L.rf.pre_pos);
+      const int end_bit = bits_for(static_cast<uint64_t>(std::max<int64_t>(n_act, 1)) * t_stride);
+      s = sort_pairs(L.rf.tmp, L.rf.tmp_bytes, L.rf.key, L.rf.skey, L.rf.val, L.rf.perm, E_out, end_bit, st);
+      if (s) return s;
+      hipLaunchKernelGGL(rf_emit, dim3(grid_for(E_out)), dim3(kThreads), 0, st, L.rf.perm, E_out, L.rf.pre_src,
+                         L.rf.pre_pos, time, L.src, L.tim, static_cast<int64_t *>(nullptr), L.rf.skey, t_stride,
+                         L.fidx);
+    }
+    hipLaunchKernelGGL(pool_row_heads, dim3(grid_for(E_out)), dim3(kThreads), 0, st, L.fidx, L.tim, E_out, L.head);
+    s = excl_scan(L.tmp, L.tmp_bytes, L.head, L.segx, E_out, st);
+    if (s) return s;
+    hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.segx, L.head, E_out, L.rf.counts + 4);
+    s = ssla_events_counts(workspace, c, 5, nullptr, stream);
+    if (s) return s;
+    n_seg = c[4];
+    if (n_seg < 0 || n_seg > E_out) {
+      set_error("sparse_pool_plan: segment count outside its bounds");
+      return SSLA_ERR_LAUNCH;
+    }
+  }
+  counts_out[0] = n_act;
+  counts_out[1] = n_seg;
+  counts_out[2] = E_out;
+  return launch_status("sparse_pool_plan");
+}
+
+// After ssla_sparse_pool_plan on the same workspace and sizes: out_events
+// [n_seg, C] (mode 0 max, 1 mean), out_time [n_seg], and per active field
+// out_len / out_batch / out_h / out_w [n_act]; outcoord is the [n_rf, 2]
+// (w, h) output coordinate table of the fields.
+extern "C" int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int64_t E_in, int B, int H, int W,
+                                     int64_t n_rf, int A, const int64_t *outcoord, int mode, int64_t n_act,
+                                     int64_t n_seg, int64_t E_out, float *out_events, int64_t *out_time,
+                                     int64_t *out_len, int64_t *out_batch, int64_t *out_h, int64_t *out_w,
+                                     void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(C > 0 && G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 &&
+                     (mode == 0 || mode == 1),
+                 "sparse_pool_emit: bad arguments");
+  const int64_t E_cap = E_in * A;
+  SSLA_CHECK_ARG(E_cap < 0x7fffffff, "sparse_pool_emit: events x kernel positions must stay below 2^31");
+  SSLA_CHECK_ARG(E_out >= 0 && E_out <= E_cap && n_seg >= 0 && n_seg <= E_out && n_act >= 0 &&
+                     n_act <= static_cast<int64_t>(B) * n_rf,
+                 "sparse_pool_emit: counts outside the plan's bounds");
+  const PoolWs L = pool_layout(workspace, G, B, H, W, n_rf, A, E_cap);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("sparse_pool_emit: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  SSLA_CHECK_ARG((n_seg == 0 || (events && out_events && out_time)) &&
+                     (n_act == 0 || (outcoord && out_len && out_batch && out_h && out_w)),
+                 "sparse_pool_emit: null pointer");
+  if (E_out * C == 0 && n_act == 0) return SSLA_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned grid = grid_for(std::max(E_out * C, n_act));
+  if (mode == 1)
+    hipLaunchKernelGGL(pool_emit_rows<true>, dim3(grid), dim3(kThreads), 0, st, events, E_in, C, L.src, L.tim,
+                       L.head, L.segx, E_out, n_seg, L.rf.f_index, L.rf.f_len, L.rf.ev_pre, n_act, n_rf, outcoord,
+                       out_events, out_time, out_len, out_batch, out_h, out_w);
+  else
+    hipLaunchKernelGGL(pool_emit_rows<false>, dim3(grid), dim3(kThreads), 0, st, events, E_in, C, L.src, L.tim,
+                       L.head, L.segx, E_out, n_seg, L.rf.f_index, L.rf.f_len, L.rf.ev_pre, n_act, n_rf, outcoord,
+                       out_events, out_time, out_len, out_batch, out_h, out_w);
+  return launch_status("sparse_pool_emit");
 }
 
 // ---- rows ------------------------------------------------------------------------

@@ -35,7 +35,7 @@ __all__ = [
     "group_events", "compute_rf2pixels", "get_patch2pixel_lut", "gather_receptive_fields",
     "scatter_group_events_to_patch", "gather_patch_events_to_group", "truncate_packed_sequence",
     "temporal_dropout_index", "pool_segments", "events_to_grid", "preprocess_inputs", "gather_rows",
-    "sort_pairs", "expand_segments", "GatherRows", "IndexAddRows",
+    "sort_pairs", "expand_segments", "GatherRows", "IndexAddRows", "sparse_pool",
 ]
 
 
@@ -348,6 +348,47 @@ def pool_segments(time: torch.Tensor, lengths: torch.Tensor):
                                       st), "pool_segments")
     (n_seg,) = _counts(ws, 1, st, "pool_segments", check_bad=False)
     return seg[:E], seg_t[:n_seg], new_len
+
+
+def sparse_pool(inputs, frame_size, rf2pixel_lut, rf_outcoord, mean: bool = False) -> Dict[str, torch.Tensor]:
+    """SparsePool.forward on pixel groups (reference layers/sparse_pooling.py:
+    14-48 after gather_receptive_fields) in two library calls, without
+    gradient: the receptive-field rows are never stored as features.  The
+    returned dict equals that of gather_receptive_fields -> pool_segments ->
+    scatter_max / scatter_mean with a sorted index."""
+    lib = _lib.load()
+    gb, gh, gw, gl = (_i64(inputs[k]) for k in ("batch_id", "h", "w", "lengths"))
+    time = _i64(inputs["time"])
+    ev = inputs["events"]
+    if ev.dim() != 2 or ev.dtype != torch.float32:
+        raise TypeError("sparse_pool: events must be fp32 [E, C]")
+    ev = ev.contiguous()
+    dev = _lib.require_cuda(gb, gl, time, ev, rf2pixel_lut)
+    B = int(inputs["batch_size"])
+    H, W = int(frame_size[0]), int(frame_size[1])
+    lut, outc = _i64(rf2pixel_lut), _i64(rf_outcoord)
+    n_rf, A = lut.shape
+    G, E_in, C = gl.numel(), time.numel(), ev.shape[1]
+    if ev.shape[0] != E_in:
+        raise ValueError(f"sparse_pool: {ev.shape[0]} event rows for {E_in} times")
+    ws = _ws(lib.ssla_sparse_pool_workspace_size(G, E_in, B, H, W, n_rf, A), dev)
+    st = _lib.stream_of(time)
+    cnt = (ctypes.c_int64 * 4)()
+    _lib.check(lib.ssla_sparse_pool_plan(_lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), _lib.ptr(gl), G, _lib.ptr(time),
+                                         E_in, B, H, W, _lib.ptr(lut), n_rf, A, cnt, _lib.ptr(ws), ws.numel(), st),
+               "sparse_pool_plan")
+    n_act, n_seg, E_out, bad = (int(v) for v in cnt)
+    if bad:
+        raise ValueError("sparse_pool: input indices or coordinates out of range")
+    out_ev = torch.empty(n_seg, C, dtype=torch.float32, device=dev)
+    out_t = torch.empty(n_seg, dtype=torch.int64, device=dev)
+    fl = torch.empty(4, n_act, dtype=torch.int64, device=dev)
+    _lib.check(lib.ssla_sparse_pool_emit(_lib.ptr(ev), C, G, E_in, B, H, W, n_rf, A, _lib.ptr(outc), 1 if mean else 0,
+                                         n_act, n_seg, E_out, _lib.ptr(out_ev), _lib.ptr(out_t), _lib.ptr(fl[0]),
+                                         _lib.ptr(fl[1]), _lib.ptr(fl[2]), _lib.ptr(fl[3]), _lib.ptr(ws), ws.numel(),
+                                         st), "sparse_pool_emit")
+    return {"events": out_ev, "time": out_t, "lengths": fl[0], "batch_id": fl[1], "h": fl[2], "w": fl[3],
+            "batch_size": inputs["batch_size"]}
 
 
 def events_to_grid(x: Dict[str, torch.Tensor], grid_size, channels: int) -> torch.Tensor:

@@ -303,12 +303,28 @@ class SparsePool(AsyncSparseModule):
         self.pool_func = pool_func
 
     def forward(self, inputs, grouped_events=True):
+        if grouped_events and self._one_call(inputs):
+            dev = inputs["time"].device
+            _ensure_lut(self, "rf2pixel_lut", "rf_outcoord", self.frame_size, self.kernel_size, self.stride, dev)
+            return E.sparse_pool(inputs, self.frame_size, self.rf2pixel_lut, self.rf_outcoord,
+                                 mean=self.pool_func is scatter_mean)
         x = self.prepare_inputs(inputs, grouped_events)
         seg, seg_time, new_len = E.pool_segments(x["time"], x["lengths"])
         res = self.pool_func(x["events"], seg, dim=0, dim_size=int(seg_time.numel()), sorted_index=True)
         new_events = res[0] if isinstance(res, tuple) else res
         return {"events": new_events, "time": seg_time, "lengths": new_len, "batch_id": x["batch_id"],
                 "h": x["h"], "w": x["w"], "batch_size": x["batch_size"]}
+
+
+    def _one_call(self, inputs) -> bool:
+        """The two-call pooling (ssla_sparse_pool_plan / _emit) takes grouped
+        fp32 device events with no gradient to record and a receptive field
+        larger than one pixel (a 1 x 1 field pools the pixel groups as they
+        are, without the gather)."""
+        ev = inputs["events"]
+        return (self.pool_func in (scatter_max, scatter_mean) and ev.is_cuda and ev.dim() == 2
+                and ev.dtype == torch.float32 and not (torch.is_grad_enabled() and ev.requires_grad)
+                and not (self.kernel_size == (1, 1) and self.stride == (1, 1)))
 
 
 class SparseMaxPool(SparsePool):
