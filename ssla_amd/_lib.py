@@ -56,6 +56,9 @@ SIGNATURES = {
     "ssla_status_read": (_i32, [_vp, C.POINTER(_i32), _vp]),
     "ssla_site_project": (_i32, [_vp, _i64, _i32, _vp, _i32, _f32, _vp, _vp, _vp, _vp, _vp]),
     "ssla_site_finish": (_i32, [_vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _f32, _i32, _vp, _vp]),
+    "ssla_site_gla_block_workspace_size": (_sz, [_i64, _i64, _i32, _i32]),
+    "ssla_site_gla_block": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _i32, _i32, _i32, _vp,
+                                   _f32, _f32, _vp, _vp, _vp, _vp, _f32, _i32, _vp, _vp, _vp, _sz, _vp]),
     "ssla_detect_head": (_i32, [C.POINTER(HeadLevel), _i32, _i32, _i32, _i32, _vp, _vp]),
     "ssla_scatter_workspace_size": (_sz, [_i64, _i32, _i64]),
     "ssla_scatter_max": (_i32, [_vp, _vp, _i64, _i32, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
@@ -67,6 +70,8 @@ SIGNATURES = {
     "ssla_group_events_workspace_size": (_sz, [_i32, _i64]),
     "ssla_group_events": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                  _vp, _sz, _vp]),
+    "ssla_preprocess_events": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _i64, _vp, _vp, _vp, _vp,
+                                      _vp, _vp, _vp, _sz, _vp]),
     "ssla_rf_scatter_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i64, _i64]),
     "ssla_rf_scatter_plan": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _i32, _i64,
                                     _vp, _sz, _vp]),

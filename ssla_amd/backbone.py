@@ -159,8 +159,12 @@ class SiteGLABlock(nn.Module):
     def forward(self, inputs: Dict[str, torch.Tensor], state: torch.Tensor, grid_size: Sequence[int],
                 check: bool = False, mark=None) -> Dict[str, torch.Tensor]:
         """``mark(name)`` (optional) is called after each piece: "project",
-        "scan", "finish" (a timing hook; it must not touch the tensors)."""
+        "scan", "finish" (a timing hook; it must not touch the tensors).
+        Without it, a block the one-launch kernels take runs as one library
+        call (ssla_site_gla_block)."""
         x = inputs["events"].to(torch.float32)
+        if mark is None and self._fused(x):
+            return self._forward_one_call(inputs, x, state, grid_size, check)
         lengths = inputs["lengths"]
         cu = F.pad(torch.cumsum(lengths, 0), (1, 0))
         q, k, v, g = self.project(x)
@@ -174,6 +178,35 @@ class SiteGLABlock(nn.Module):
         out["events"] = self.finish(o, x)
         if mark:
             mark("finish")
+        return out
+
+
+    def _forward_one_call(self, inputs, x, state, grid_size, check):
+        from . import _lib
+        H, D = self.heads, self.head_dim
+        if state.dim() != 4 or state.shape[1:] != (H, D, D) or state.dtype != torch.float32 \
+                or not state.is_contiguous() or not state.is_cuda:
+            raise ValueError(f"SiteGLABlock: state must be contiguous fp32 [n_sites, {H}, {D}, {D}] on the device")
+        w = self._bf16()
+        n = x.shape[0]
+        x = x.contiguous()
+        ln, gb, gh, gw = (inputs[k].to(torch.int64).contiguous() for k in ("lengths", "batch_id", "h", "w"))
+        G = ln.numel()
+        lib = _lib.load()
+        ws = torch.empty(max(lib.ssla_site_gla_block_workspace_size(n, G, H, D), 1), dtype=torch.uint8,
+                         device=x.device)
+        y = torch.empty(n, self.out_channels, dtype=torch.float32, device=x.device)
+        status = _lib.new_status(x.device) if check and G else None
+        _lib.check(lib.ssla_site_gla_block(
+            _lib.ptr(x), n, self.in_channels, _lib.ptr(ln), _lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), G,
+            int(grid_size[0]), int(grid_size[1]), _lib.ptr(state), state.shape[0], H, D, _lib.ptr(w["qkvg"]),
+            float(self.gate_normalizer), float(D ** -0.5), _lib.ptr(w["o"]), _lib.ptr(w.get("r")),
+            _lib.ptr(self.norm.weight), _lib.ptr(self.norm.bias), float(self.norm.eps), self.out_channels,
+            _lib.ptr(y), _lib.ptr(status), _lib.ptr(ws), ws.numel(), _lib.stream_of(x)), "ssla_site_gla_block")
+        if status is not None and _lib.read_status(status) != _lib.SSLA_OK:
+            raise ValueError(f"SiteGLABlock: site rows must be strictly increasing and inside [0, {state.shape[0]})")
+        out = dict(inputs)
+        out["events"] = y
         return out
 
 

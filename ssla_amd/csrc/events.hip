@@ -248,11 +248,13 @@ __global__ void ge_starts(const int64_t *__restrict__ head, const int64_t *__res
 }
 
 // per group: kept length and the group's pixel attributes (kept = 0 beyond G)
+// kept[g]: the group's latest cap_px events, of which the first keep_first
+// stay (keep_first = INT64_MAX: all of them).
 __global__ void ge_groups(const int64_t *__restrict__ counts, const int64_t *__restrict__ start, int64_t cap,
                           const int32_t *__restrict__ order, const int64_t *__restrict__ row_of,
-                          const float *__restrict__ ev, int64_t N, int C, int cap_px, int64_t *__restrict__ kept,
-                          int64_t *__restrict__ gr_batch, int64_t *__restrict__ gr_h, int64_t *__restrict__ gr_w,
-                          int64_t *__restrict__ gr_len) {
+                          const float *__restrict__ ev, int64_t N, int C, int cap_px, int64_t keep_first,
+                          int64_t *__restrict__ kept, int64_t *__restrict__ gr_batch, int64_t *__restrict__ gr_h,
+                          int64_t *__restrict__ gr_w, int64_t *__restrict__ gr_len) {
   const int64_t G = counts[0];
   GRID_STRIDE(g, cap) {
     if (g >= G) {
@@ -260,7 +262,7 @@ __global__ void ge_groups(const int64_t *__restrict__ counts, const int64_t *__r
       continue;
     }
     const int64_t s = start[g], e = start[g + 1];
-    const int64_t k = min(e - s, static_cast<int64_t>(cap_px));
+    const int64_t k = min(min(e - s, static_cast<int64_t>(cap_px)), keep_first);
     kept[g] = k;
     gr_len[g] = k;
     const int64_t r = row_of[order[s]];
@@ -270,25 +272,36 @@ __global__ void ge_groups(const int64_t *__restrict__ counts, const int64_t *__r
   }
 }
 
-// emit the kept (latest cap_px) events of every group
+// Emit the kept events of every group (its latest cap_px, then the first
+// kept[g] of those): features are columns fc .. C-1.  DELAYS: column fc (a
+// timestamp) becomes the delay since the group's previous event, (t - t')
+// / 1e5 in fp32 capped at 1, and 1 for the first of the latest cap_px
+// (MosModel.preprocess_inputs, model_mos.py:194-201).
+template <bool DELAYS>
 __global__ void ge_emit(const int64_t *__restrict__ head, const int64_t *__restrict__ gpos,
                         const int64_t *__restrict__ start, const int64_t *__restrict__ kept,
                         const int64_t *__restrict__ kpre, const int32_t *__restrict__ order,
                         const int64_t *__restrict__ row_of, const float *__restrict__ ev, int64_t cap,
-                        const int64_t *__restrict__ Ep, int C, float *__restrict__ out_ev,
+                        const int64_t *__restrict__ Ep, int C, int cap_px, int fc, float *__restrict__ out_ev,
                         int64_t *__restrict__ out_t) {
   const int64_t E = *Ep;
+  const int F = C - fc;
   GRID_STRIDE(i, cap) {
     if (i >= E) continue;
     const int64_t g = gpos[i] + head[i] - 1;
     const int64_t s = start[g], e = start[g + 1];
-    const int64_t drop = (e - s) - kept[g];
-    const int64_t rank = i - s;
-    if (rank < drop) continue;
-    const int64_t o = kpre[g] + rank - drop;
+    const int64_t drop = (e - s) - min(e - s, static_cast<int64_t>(cap_px));
+    const int64_t rank = i - s - drop;
+    if (rank < 0 || rank >= kept[g]) continue;
+    const int64_t o = kpre[g] + rank;
     const int64_t r = row_of[order[i]];
     const float *src = ev + r * C;
-    for (int c = 3; c < C; ++c) out_ev[o * (C - 3) + (c - 3)] = src[c];
+    for (int c = fc; c < C; ++c) out_ev[o * F + (c - fc)] = src[c];
+    if constexpr (DELAYS) {
+      float d = 1.f;
+      if (rank > 0) d = fminf((src[fc] - ev[row_of[order[i - 1]] * C + fc]) / 1e5f, 1.f);
+      out_ev[o * F] = d;
+    }
     out_t[o] = static_cast<int64_t>(src[2]);
   }
 }
@@ -698,29 +711,32 @@ extern "C" size_t ssla_group_events_workspace_size(int B, int64_t N) {
   return ge_layout(nullptr, B, static_cast<int64_t>(B) * N).total;
 }
 
-extern "C" int ssla_group_events(const float *events, const int64_t *lengths, int B, int64_t N, int C, int H, int W,
-                                 int max_per_px, float *out_events, int64_t *out_time, int64_t *gr_batch,
-                                 int64_t *gr_h, int64_t *gr_w, int64_t *gr_len, void *workspace,
-                                 size_t workspace_bytes, void *stream) {
-  clear_error();
-  SSLA_CHECK_ARG(B > 0 && N >= 0 && C >= 4 && H > 0 && W > 0 && max_per_px > 0, "group_events: bad sizes");
+namespace {
+// group_events with the kept window (latest max_per_px, then the first
+// keep_first), features from column fc and, with delays, the per-pixel
+// delays of MosModel.preprocess_inputs in column fc.
+int group_events_impl(const char *what, const float *events, const int64_t *lengths, int B, int64_t N, int C, int H,
+                      int W, int max_per_px, int64_t keep_first, int fc, bool delays, float *out_events,
+                      int64_t *out_time, int64_t *gr_batch, int64_t *gr_h, int64_t *gr_w, int64_t *gr_len,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+  SSLA_CHECK_ARG(B > 0 && N >= 0 && C >= 4 && H > 0 && W > 0 && max_per_px > 0, "%s: bad sizes", what);
   SSLA_CHECK_ARG(static_cast<int64_t>(B) * H * W < (1LL << 24),
-                 "group_events: B*H*W must stay below 2^24 (pixel ids are formed in fp32)");
+                 "%s: B*H*W must stay below 2^24 (pixel ids are formed in fp32)", what);
   const int64_t cap = static_cast<int64_t>(B) * N;
-  SSLA_CHECK_ARG(cap < 0x7fffffff, "group_events: B*N must stay below 2^31");
+  SSLA_CHECK_ARG(cap < 0x7fffffff, "%s: B*N must stay below 2^31", what);
   const GeWs L = ge_layout(workspace, B, cap);
   if (!workspace || workspace_bytes < L.total) {
-    set_error("group_events: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    set_error("%s: workspace of %zu bytes needed, %zu given", what, L.total, workspace_bytes);
     return SSLA_ERR_WORKSPACE;
   }
   SSLA_CHECK_ARG(events && lengths && out_events && out_time && gr_batch && gr_h && gr_w && gr_len,
-                 "group_events: null pointer");
+                 "%s: null pointer", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t *Ep = L.off + B;
   if (cap == 0) {
     hipLaunchKernelGGL(clear_and_fill, dim3(1), dim3(kThreads), 0, st, L.counts, L.bad, nullptr, (int64_t)0,
                        (int64_t)0, nullptr, (int64_t)0, 0);
-    return launch_status("group_events");
+    return launch_status(what);
   }
   // sample offsets: exclusive scan of the lengths clamped to [0, N]
   hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max<int64_t>(8, B + 1))), dim3(kThreads), 0, st, L.counts,
@@ -743,13 +759,39 @@ extern "C" int ssla_group_events(const float *events, const int64_t *lengths, in
   hipLaunchKernelGGL(ge_starts, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, cap, Ep, L.start,
                      L.counts);
   hipLaunchKernelGGL(ge_groups, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.counts, L.start, cap, L.order,
-                     L.row_of, events, N, C, max_per_px, L.kept, gr_batch, gr_h, gr_w, gr_len);
+                     L.row_of, events, N, C, max_per_px, keep_first, L.kept, gr_batch, gr_h, gr_w, gr_len);
   s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.kpre, cap, st);
   if (s) return s;
-  hipLaunchKernelGGL(ge_emit, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, L.start, L.kept, L.kpre,
-                     L.order, L.row_of, events, cap, Ep, C, out_events, out_time);
+  if (delays)
+    hipLaunchKernelGGL(ge_emit<true>, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, L.start, L.kept,
+                       L.kpre, L.order, L.row_of, events, cap, Ep, C, max_per_px, fc, out_events, out_time);
+  else
+    hipLaunchKernelGGL(ge_emit<false>, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, L.start, L.kept,
+                       L.kpre, L.order, L.row_of, events, cap, Ep, C, max_per_px, fc, out_events, out_time);
   hipLaunchKernelGGL(ge_finish, dim3(1), dim3(64), 0, st, L.kpre, L.kept, L.counts, Ep);
-  return launch_status("group_events");
+  return launch_status(what);
+}
+}  // namespace
+
+extern "C" int ssla_group_events(const float *events, const int64_t *lengths, int B, int64_t N, int C, int H, int W,
+                                 int max_per_px, float *out_events, int64_t *out_time, int64_t *gr_batch,
+                                 int64_t *gr_h, int64_t *gr_w, int64_t *gr_len, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+  clear_error();
+  return group_events_impl("group_events", events, lengths, B, N, C, H, W, max_per_px, INT64_MAX, 3, false,
+                           out_events, out_time, gr_batch, gr_h, gr_w, gr_len, workspace, workspace_bytes, stream);
+}
+
+// MosModel.preprocess_inputs in one call: out_events [cap, C - 2] holds
+// (delay, features after t) per kept event.
+extern "C" int ssla_preprocess_events(const float *events, const int64_t *lengths, int B, int64_t N, int C, int H,
+                                      int W, int max_per_px, int64_t hot_pixel_thres, float *out_events,
+                                      int64_t *out_time, int64_t *gr_batch, int64_t *gr_h, int64_t *gr_w,
+                                      int64_t *gr_len, void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  return group_events_impl("preprocess_events", events, lengths, B, N, C, H, W, max_per_px,
+                           hot_pixel_thres > 0 ? hot_pixel_thres : INT64_MAX, 2, true, out_events, out_time, gr_batch,
+                           gr_h, gr_w, gr_len, workspace, workspace_bytes, stream);
 }
 
 // counts of the last data-dependent call that used `workspace` (the first

@@ -475,3 +475,132 @@ extern "C" int ssla_detect_head(const ssla_head_level *levels, int n_levels, int
                      static_cast<hipStream_t>(stream), a, out);
   return launch_status("detect_head");
 }
+
+// ------------------------------------------------------- the whole block
+// SiteGLABlock.forward on the sites of one window in one call: the sequence
+// offsets and state rows of the groups, ssla_site_project, the per-site
+// recurrence (ssla_gla_recurrent_fwd with state_idx, the states updated in
+// place) and ssla_site_finish.
+namespace ssla {
+namespace {
+constexpr int kKeyThreads = 1024, kKeyPer = 8;
+
+// cu[0..G] = exclusive prefix of the group lengths (cu[G] the total) and
+// sites[g] = (b * grid_h + h) * grid_w + w, in one workgroup: chunks of
+// kKeyThreads * kKeyPer lengths in turn, each scanned across the
+// wavefronts through LDS, the running total carried between chunks.
+__global__ __launch_bounds__(kKeyThreads) void site_keys_kernel(const int64_t *__restrict__ len,
+                                                                const int64_t *__restrict__ gb,
+                                                                const int64_t *__restrict__ gh,
+                                                                const int64_t *__restrict__ gw, int64_t G, int grid_h,
+                                                                int grid_w, int64_t *__restrict__ cu,
+                                                                int32_t *__restrict__ sites) {
+  __shared__ int64_t wsum[kKeyThreads / 64];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int64_t carry = 0;
+  for (int64_t base = 0; base < G; base += static_cast<int64_t>(kKeyThreads) * kKeyPer) {
+    int64_t v[kKeyPer];
+    int64_t s = 0;
+#pragma unroll
+    for (int e = 0; e < kKeyPer; ++e) {
+      const int64_t i = base + static_cast<int64_t>(t) * kKeyPer + e;
+      v[e] = i < G ? len[i] : 0;
+      s += v[e];
+    }
+    int64_t x = s;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int64_t y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    int64_t run = carry + x - s, total = carry;
+    for (int j = 0; j < kKeyThreads / 64; ++j) {
+      if (j < w) run += wsum[j];
+      total += wsum[j];
+    }
+#pragma unroll
+    for (int e = 0; e < kKeyPer; ++e) {
+      const int64_t i = base + static_cast<int64_t>(t) * kKeyPer + e;
+      if (i < G) cu[i] = run;
+      run += v[e];
+    }
+    carry = total;
+    __syncthreads();   // wsum is rewritten by the next chunk
+  }
+  if (t == 0) cu[G] = carry;
+  for (int64_t g = t; g < G; g += kKeyThreads)
+    sites[g] = static_cast<int32_t>((gb[g] * grid_h + gh[g]) * grid_w + gw[g]);
+}
+
+struct BlockWs {
+  uint16_t *q, *k, *v, *o;
+  float *g;
+  int64_t *cu;
+  int32_t *sites;
+  void *rec;
+  size_t rec_bytes, total;
+};
+BlockWs block_layout(void *ws, int64_t n, int64_t G, int heads, int head_dim) {
+  auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+  char *b = static_cast<char *>(ws);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    void *p = b ? b + off : nullptr;
+    off = up(off + std::max<size_t>(bytes, 1));
+    return p;
+  };
+  const size_t rows = static_cast<size_t>(n) * heads * head_dim;
+  BlockWs L;
+  L.q = static_cast<uint16_t *>(take(2 * rows));
+  L.k = static_cast<uint16_t *>(take(2 * rows));
+  L.v = static_cast<uint16_t *>(take(2 * rows));
+  L.o = static_cast<uint16_t *>(take(2 * rows));
+  L.g = static_cast<float *>(take(4 * rows));
+  L.cu = static_cast<int64_t *>(take(8 * (G + 1)));
+  L.sites = static_cast<int32_t *>(take(4 * G));
+  L.rec_bytes = ssla_gla_recurrent_workspace_size(static_cast<int>(std::min<int64_t>(G, 0x7fffffff)), n, heads,
+                                                  head_dim, head_dim);
+  L.rec = L.rec_bytes ? take(L.rec_bytes) : nullptr;
+  L.total = off;
+  return L;
+}
+}  // namespace
+}  // namespace ssla
+
+extern "C" size_t ssla_site_gla_block_workspace_size(int64_t n, int64_t G, int heads, int head_dim) {
+  if (n < 0 || G < 0 || heads <= 0 || head_dim <= 0) return 0;
+  return ssla::block_layout(nullptr, n, G, heads, head_dim).total;
+}
+
+extern "C" int ssla_site_gla_block(const float *x, int64_t n, int cin, const int64_t *lengths, const int64_t *gr_batch,
+                                   const int64_t *gr_h, const int64_t *gr_w, int64_t G, int grid_h, int grid_w,
+                                   float *state, int n_sites, int heads, int head_dim, const uint16_t *w_qkvg,
+                                   float gate_normalizer, float scale, const uint16_t *w_o, const uint16_t *w_r,
+                                   const float *ln_w, const float *ln_b, float eps, int cout, float *y,
+                                   int32_t *status, void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace ssla;
+  clear_error();
+  SSLA_CHECK_ARG(n >= 0 && G >= 0 && G < 0x7fffffff && cin > 0 && cout > 0 && heads > 0 && head_dim > 0 &&
+                     grid_h > 0 && grid_w > 0 && n_sites > 0,
+                 "site_gla_block: bad sizes");
+  const BlockWs L = block_layout(workspace, n, G, heads, head_dim);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("site_gla_block: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  if (n == 0 || G == 0) return SSLA_OK;
+  SSLA_CHECK_ARG(lengths && gr_batch && gr_h && gr_w && state, "site_gla_block: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int hd = heads * head_dim;
+  hipLaunchKernelGGL(site_keys_kernel, dim3(1), dim3(kKeyThreads), 0, st, lengths, gr_batch, gr_h, gr_w, G, grid_h,
+                     grid_w, L.cu, L.sites);
+  int s = ssla_site_project(x, n, cin, w_qkvg, hd, gate_normalizer, L.q, L.k, L.v, L.g, stream);
+  if (s) return s;
+  s = ssla_gla_recurrent_fwd(L.q, L.k, L.v, L.g, SSLA_F32, L.cu, static_cast<int>(G), n, heads, head_dim, head_dim,
+                             scale, state, L.o, state, L.sites, n_sites, status, SSLA_BF16, L.rec, L.rec_bytes,
+                             stream);
+  if (s) return s;
+  return ssla_site_finish(L.o, n, hd, w_o, x, cin, w_r, ln_w, ln_b, eps, cout, y, stream);
+}

@@ -411,11 +411,45 @@ def events_to_grid(x: Dict[str, torch.Tensor], grid_size, channels: int) -> torc
     return grid
 
 
+def _preprocess_one_call(events, lengths, frame_size, hot_pixel_thres, max_events_per_px: int = 512):
+    """preprocess_inputs as one library call (ssla_preprocess_events): the
+    grouping, the delays and the truncation share one device pass and one
+    read of the counts."""
+    ev = events.to(torch.float32).contiguous()
+    ln = _i64(lengths)
+    dev = _lib.require_cuda(ev, ln)
+    B, N, C = ev.shape
+    H, W = int(frame_size[0]), int(frame_size[1])
+    lib = _lib.load()
+    cap = B * N
+    ws = _ws(lib.ssla_group_events_workspace_size(B, N), dev)
+    out_ev = torch.empty(cap, C - 2, dtype=torch.float32, device=dev)
+    out_t = torch.empty(cap, dtype=torch.int64, device=dev)
+    grp = torch.empty(4, cap, dtype=torch.int64, device=dev)
+    st = _lib.stream_of(ev)
+    _lib.check(lib.ssla_preprocess_events(_lib.ptr(ev), _lib.ptr(ln), B, N, C, H, W, int(max_events_per_px),
+                                          int(hot_pixel_thres), _lib.ptr(out_ev), _lib.ptr(out_t), _lib.ptr(grp[0]),
+                                          _lib.ptr(grp[1]), _lib.ptr(grp[2]), _lib.ptr(grp[3]), _lib.ptr(ws),
+                                          ws.numel(), st), "preprocess_events")
+    G, E, _ = _counts(ws, 3, st, "preprocess_events")
+    return {"events": out_ev[:E], "time": out_t[:E], "batch_id": grp[0, :G], "h": grp[1, :G], "w": grp[2, :G],
+            "lengths": grp[3, :G], "batch_size": B}
+
+
 def preprocess_inputs(events: torch.Tensor, lengths: torch.Tensor, frame_size, hot_pixel_thres: int = 50):
     """MosModel.preprocess_inputs (reference model_mos.py:173-209):
     <x, y, t, p> -> grouped pixels with features <dt, p>, dt the per-pixel
     delay clamped at 100 ms and normalised to [0, 1] (1 for the first event
     of a pixel), hot pixels truncated to their first `hot_pixel_thres`."""
+    if events.is_cuda and events.dim() == 3 and events.size(2) >= 4 and lengths.dim() == 1 \
+            and lengths.size(0) == events.size(0):
+        return _preprocess_one_call(events, lengths, frame_size, hot_pixel_thres)
+    return _preprocess_composed(events, lengths, frame_size, hot_pixel_thres)
+
+
+def _preprocess_composed(events, lengths, frame_size, hot_pixel_thres):
+    """preprocess_inputs step by step: group_events of the duplicated-time
+    layout, ssla_pixel_delays, truncate_packed_sequence."""
     ev = events.to(torch.float32)
     ev = torch.cat([ev[..., :3], ev[..., 2:3], ev[..., 3:]], dim=-1).contiguous()
     gr = group_events((ev, lengths), frame_size)

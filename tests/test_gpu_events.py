@@ -137,6 +137,29 @@ def test_preprocess_and_fields_synthetic(dev):
     np.testing.assert_array_equal(_np(grid), OE.event_to_grid(ro, (H, W), ro["events"].shape[1]))
 
 
+@pytest.mark.parametrize("thres,extra", [(20, 0), (0, 0), (3, 2), (600, 0)])
+def test_preprocess_one_call_vs_composed(dev, thres, extra):
+    """ssla_preprocess_events (grouping, delays and truncation in one pass)
+    against the step-by-step path and the oracle, with a hot pixel beyond the
+    512-event cap (its latest 512 kept, then the first `thres` of those) and
+    extra feature columns after p."""
+    from ssla_amd import events as E
+    H, W = 32, 40
+    ev, lens = _synthetic(11, 3, 2500, H, W, dev)
+    ev[1, :700, 0], ev[1, :700, 1] = 5.0, 7.0
+    if extra:
+        rng = np.random.default_rng(4)
+        ev = np.concatenate([ev, rng.standard_normal(ev.shape[:2] + (extra,)).astype(np.float32)], -1)
+    print(f"preprocess one call thres={thres} extra={extra}", flush=True)
+    one = E.preprocess_inputs(_t(ev, dev), _t(lens, dev), (H, W), hot_pixel_thres=thres)
+    comp = E._preprocess_composed(_t(ev, dev), _t(lens, dev), (H, W), thres)
+    ro = OE.preprocess_events(ev, lens, (H, W), hot_pixel_thres=thres)
+    for key in ("events", "time", "batch_id", "h", "w", "lengths"):
+        np.testing.assert_array_equal(_np(one[key]), _np(comp[key]), err_msg=key)
+        np.testing.assert_array_equal(_np(one[key]), ro[key], err_msg=key)
+    assert int(_np(one["lengths"]).max()) == min(512, thres if thres > 0 else 512)
+
+
 def test_patch_scatter_synthetic(dev):
     from ssla_amd import events as E
     H, W = 40, 48
