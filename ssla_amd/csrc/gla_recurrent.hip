@@ -109,8 +109,10 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // ---------------------------------------------------- segmented schedule --
-// Long sequences are cut into segments of kSegSteps steps (at least one per
-// sequence, so empty sequences still pass h0 to ht), numbered globally
+// Long sequences are cut into segments of seg_steps steps (kSegSteps,
+// halved down to kSegStepsMin while the grid would hold fewer than
+// kSegUnits wavefronts; at least one segment per sequence, so empty
+// sequences still pass h0 to ht), numbered globally
 // (segoff[n] = first segment of sequence n, computed on the device).
 // * state pass (kSegState): every segment but the last of its sequence runs
 //   from a zero state and leaves its local end state L_j and the product
@@ -122,7 +124,10 @@ __device__ __forceinline__ void wave_lds_sync() {
 //   steps writing o, and the last segment writes ht.  Multi-segment
 //   sequences read h0 from the copy, so an in-place update (ht == h0) never
 //   races with a segment that has not read it yet.
-constexpr int kSegSteps = 128;
+constexpr int kSegSteps = 128;   // the longest segment
+constexpr int kSegStepsMin = 32;
+constexpr int64_t kSegUnits = 8192;   // wavefront units the segment length aims at (8 per SIMD)
+constexpr int64_t kSegFoldMax = 8;    // average segments per sequence at most, when halving
 enum { kPlain = 0, kSegState = 1, kSegOut = 2 };
 
 struct SegWs {
@@ -131,6 +136,7 @@ struct SegWs {
   float *prod;             // [n_segs_max, H, K]: P_j
   float *h0c;              // [n_seq, H, K, V]: copy of the initial states
   int64_t n_segs_max;      // upper bound of the segment count (grid size)
+  int seg_steps;           // steps per segment (the last of a sequence may be shorter)
 };
 
 __device__ __forceinline__ int find_seg_seq(const int64_t *off, int n_seq, int64_t i) {
@@ -146,7 +152,7 @@ __device__ __forceinline__ int find_seg_seq(const int64_t *off, int n_seq, int64
 // segoff[n] = segments of sequences 0..n-1 (segoff[n_seq]: the total).  One
 // workgroup of 256 threads.
 __global__ __launch_bounds__(256) void seg_offsets_kernel(const int64_t *__restrict__ cu, int n_seq, int64_t T,
-                                                          int64_t *__restrict__ segoff) {
+                                                          int seg_steps, int64_t *__restrict__ segoff) {
   __shared__ int64_t ps[256];
   int64_t carry = 0;
   for (int base = 0; base < n_seq; base += 256) {
@@ -155,7 +161,7 @@ __global__ __launch_bounds__(256) void seg_offsets_kernel(const int64_t *__restr
     if (n < n_seq) {
       const int64_t bos = min(max(cu[n], (int64_t)0), T);
       const int64_t eos = min(max(cu[n + 1], bos), T);
-      c = max((eos - bos + kSegSteps - 1) / kSegSteps, (int64_t)1);
+      c = max((eos - bos + seg_steps - 1) / seg_steps, (int64_t)1);
     }
     ps[threadIdx.x] = c;
     __syncthreads();
@@ -269,8 +275,8 @@ __global__ __launch_bounds__(256, KPL <= 8 ? 4 : 3) void gla_recurrent_staged_ke
     }
     const int64_t sbos = min(max(cu_seqlens[u.n], (int64_t)0), T);
     const int64_t seos = min(max(cu_seqlens[u.n + 1], sbos), T);
-    u.bos = MODE == kPlain ? sbos : min(sbos + static_cast<int64_t>(u.seg) * kSegSteps, seos);
-    u.eos = MODE == kPlain ? seos : min(u.bos + kSegSteps, seos);
+    u.bos = MODE == kPlain ? sbos : min(sbos + static_cast<int64_t>(u.seg) * sw.seg_steps, seos);
+    u.eos = MODE == kPlain ? seos : min(u.bos + sw.seg_steps, seos);
     u.srow = state_idx ? state_idx[u.n] : u.n;
     u.bad = bad_state_row(state_idx, u.n, u.srow, n_state_rows);
     u.run = !u.bad;
@@ -570,6 +576,7 @@ __global__ __launch_bounds__(256) void gla_recurrent_kernel(
 struct SegLayout {
   size_t segoff, slot, prod, h0c, total;
   int64_t n_segs_max;
+  int seg_steps;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -578,7 +585,18 @@ inline SegLayout seg_layout(int n_seq, int64_t T, int H, int K, int V) {
   SegLayout L{};
   if (n_seq <= 0 || T <= 0 || K % 16 != 0 || K > 64 || V <= 0) return L;
   if (T < static_cast<int64_t>(n_seq) * (kSegSteps / 4)) return L;
-  L.n_segs_max = T / kSegSteps + n_seq + 1;
+  // halve the segments (down to kSegStepsMin steps) while the grid holds
+  // fewer than kSegUnits wavefronts -- shorter serial walks, more of them --
+  // and sequences keep at most kSegFoldMax segments on average: segment s
+  // folds the s local states before it, so the output pass grows with the
+  // square of the segment count (at 20 per sequence it took longer than
+  // the walks it saved)
+  const int64_t n_vt = (V + kBV - 1) / kBV;
+  L.seg_steps = kSegSteps;
+  while (L.seg_steps > kSegStepsMin && (T / L.seg_steps + n_seq) * H * n_vt < kSegUnits &&
+         T / (static_cast<int64_t>(n_seq) * (L.seg_steps / 2)) <= kSegFoldMax)
+    L.seg_steps /= 2;
+  L.n_segs_max = T / L.seg_steps + n_seq + 1;
   const size_t hkv = static_cast<size_t>(H) * K * V;
   size_t p = 0;
   L.segoff = p; p = align256(p + sizeof(int64_t) * (n_seq + 1));
@@ -629,8 +647,9 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
       sw.prod = reinterpret_cast<float *>(w + L.prod);
       sw.h0c = reinterpret_cast<float *>(w + L.h0c);
       sw.n_segs_max = L.n_segs_max;
+      sw.seg_steps = L.seg_steps;
       sgrid = dim3(static_cast<unsigned>((L.n_segs_max * H * n_vt + waves_per_block - 1) / waves_per_block));
-      hipLaunchKernelGGL(seg_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T,
+      hipLaunchKernelGGL(seg_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T, L.seg_steps,
                          reinterpret_cast<int64_t *>(w + L.segoff));
     }
 #define SSLA_RECS(KPL_)                                                                                     \
