@@ -492,22 +492,27 @@ int ssla_pool_segments(const int64_t *time, const int64_t *lengths, int64_t n_f,
  * layers/async_sparse_module.py:23-41 -> utils/farsecnn_utils.py:177-265)
  * in two calls, for callers that need no gradient: the field rows are never
  * stored as features, the reduction reads the pixel events [E_in, C]
- * through each row's source event.  plan: counts_out[0] active fields,
- * [1] pooling segments, [2] field rows, [3] 1 if a group coordinate or run
- * is out of range (nothing else computed); it reads counts from the device
- * twice.  emit (same workspace and sizes, mode 0 scatter_max / 1
- * scatter_mean): out_events [segments, C], out_time [segments], and per
- * active field out_len (segments), out_batch, out_h, out_w (outcoord
- * [n_rf, 2] holds (w, h) per field) -- the dict SparsePool.forward returns. */
-size_t ssla_sparse_pool_workspace_size(int64_t G, int64_t E_in, int B, int H, int W, int64_t n_rf, int A);
+ * through each row's source event.  E_cap bounds the field rows: E_in times
+ * the fields one pixel can belong to (ceil(kh/sh) * ceil(kw/sw)); more rows
+ * than that is SSLA_ERR_ARG.  plan: counts_out[0] active fields, [1]
+ * pooling segments, [2] field rows, [3] 1 if a group coordinate or run is
+ * out of range (nothing else computed); it reads counts from the device
+ * once (twice when a pixel run is not sorted by time).  emit (same
+ * workspace and sizes, mode 0 scatter_max / 1 scatter_mean): out_events
+ * [segments, C], out_time [segments], and per active field out_len
+ * (segments), out_batch, out_h, out_w (outcoord [n_rf, 2] holds (w, h) per
+ * field) -- the dict SparsePool.forward returns. */
+size_t ssla_sparse_pool_workspace_size(int64_t G, int64_t E_in, int B, int H, int W, int64_t n_rf, int A,
+                                       int64_t E_cap);
 int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
                           const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B, int H,
-                          int W, const int64_t *lut, int64_t n_rf, int A, int64_t *counts_out, void *workspace,
-                          size_t workspace_bytes, void *stream);
+                          int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap, int64_t *counts_out,
+                          void *workspace, size_t workspace_bytes, void *stream);
 int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int64_t E_in, int B, int H, int W, int64_t n_rf,
-                          int A, const int64_t *outcoord, int mode, int64_t n_act, int64_t n_seg, int64_t E_out,
-                          float *out_events, int64_t *out_time, int64_t *out_len, int64_t *out_batch,
-                          int64_t *out_h, int64_t *out_w, void *workspace, size_t workspace_bytes, void *stream);
+                          int A, int64_t E_cap, const int64_t *outcoord, int mode, int64_t n_act, int64_t n_seg,
+                          int64_t E_out, float *out_events, int64_t *out_time, int64_t *out_len,
+                          int64_t *out_batch, int64_t *out_h, int64_t *out_w, void *workspace,
+                          size_t workspace_bytes, void *stream);
 
 /* Per-pixel delays in place (MosModel.preprocess_inputs, model_mos.py:
  * 195-201): column 0 of feat [E, C] (timestamps) becomes

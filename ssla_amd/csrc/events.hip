@@ -1148,9 +1148,12 @@ PoolWs pool_layout(void *ws, int64_t G, int B, int H, int W, int64_t n_rf, int A
 // head[r] = 1 where row r starts a pooling segment: the first row, a new
 // field, or a time different from the row before (reference
 // sparse_pooling.py:26-31: unique_consecutive of time + field * max_v).
-__global__ void pool_row_heads(const int32_t *__restrict__ fidx, const int64_t *__restrict__ tim, int64_t n,
-                               int64_t *__restrict__ head) {
-  GRID_STRIDE(r, n) head[r] = (r == 0 || fidx[r] != fidx[r - 1] || tim[r] != tim[r - 1]) ? 1 : 0;
+// Rows at or past the row count *n_rows (read on the device) get 0, so the
+// prefix sum may run over the capacity cap.
+__global__ void pool_row_heads(const int32_t *__restrict__ fidx, const int64_t *__restrict__ tim,
+                               const int64_t *__restrict__ n_rows, int64_t cap, int64_t *__restrict__ head) {
+  const int64_t n = min(*n_rows, cap);
+  GRID_STRIDE(r, cap) head[r] = (r < n && (r == 0 || fidx[r] != fidx[r - 1] || tim[r] != tim[r - 1])) ? 1 : 0;
 }
 
 // One thread per (row, channel); the threads of a segment's first row walk
@@ -1207,22 +1210,31 @@ __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C
 }
 }  // namespace
 
-extern "C" size_t ssla_sparse_pool_workspace_size(int64_t G, int64_t E_in, int B, int H, int W, int64_t n_rf, int A) {
-  if (G < 0 || E_in < 0 || B <= 0 || H <= 0 || W <= 0 || n_rf <= 0 || A <= 0) return 0;
-  return pool_layout(nullptr, G, B, H, W, n_rf, A, E_in * A).total;
+// E_cap bounds the field rows: E_in times the fields a pixel can belong to
+// (ceil(kh / sh) * ceil(kw / sw) for a k x k, stride s field grid).
+extern "C" size_t ssla_sparse_pool_workspace_size(int64_t G, int64_t E_in, int B, int H, int W, int64_t n_rf, int A,
+                                                  int64_t E_cap) {
+  if (G < 0 || E_in < 0 || B <= 0 || H <= 0 || W <= 0 || n_rf <= 0 || A <= 0 || E_cap < E_in) return 0;
+  return pool_layout(nullptr, G, B, H, W, n_rf, A, E_cap).total;
 }
 
 // counts_out[0..3] = active fields, segments, field rows, and 1 if a group
 // coordinate or run was out of range (then nothing else was computed).
+// The rows are filled by counting, on the premise that every pixel run is
+// sorted by time (as group_events and pooled outputs leave them), and the
+// segment heads and their prefix sum run over the capacity E_cap, so one
+// read of the counts covers the plan, the premise and the segments; runs
+// that are not sorted send the call through the sort fill and a second read.
 extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
                                      const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
-                                     int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t *counts_out,
-                                     void *workspace, size_t workspace_bytes, void *stream) {
+                                     int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
+                                     int64_t *counts_out, void *workspace, size_t workspace_bytes, void *stream) {
   clear_error();
-  SSLA_CHECK_ARG(G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 && counts_out,
+  SSLA_CHECK_ARG(G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 && counts_out &&
+                     E_cap >= E_in,
                  "sparse_pool_plan: bad arguments");
-  const int64_t E_cap = E_in * A, n_f = static_cast<int64_t>(B) * n_rf;
-  SSLA_CHECK_ARG(E_cap < 0x7fffffff, "sparse_pool_plan: events x kernel positions must stay below 2^31");
+  const int64_t n_f = static_cast<int64_t>(B) * n_rf;
+  SSLA_CHECK_ARG(E_cap < 0x7fffffff, "sparse_pool_plan: the row capacity must stay below 2^31");
   const PoolWs L = pool_layout(workspace, G, B, H, W, n_rf, A, E_cap);
   if (!workspace || workspace_bytes < L.total) {
     set_error("sparse_pool_plan: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
@@ -1232,9 +1244,28 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
   int s = ssla_rf_scatter_plan(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, workspace,
                                L.rf.total, stream);
   if (s) return s;
+  const int64_t HW = static_cast<int64_t>(H) * W;
+  if (E_in > 0) {   // the counting fill, rows bounded by the capacity
+    hipLaunchKernelGGL(fill_i32, dim3(grid_for(HW * A)), dim3(kThreads), 0, st, L.inv, HW * A, -1);
+    hipLaunchKernelGGL(rf_inv_lut, dim3(grid_for(n_rf * A)), dim3(kThreads), 0, st, lut, n_rf, A, HW, L.inv);
+    hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.rf.val, gr_batch, gr_h, gr_w,
+                       L.rf.gstart, gr_len, L.rf.pixmap, L.inv, lut, n_rf, A, H, W, L.rf.ev_pre, time, E_in, E_cap,
+                       L.src, L.tim, static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr), L.rf.act_pre,
+                       L.fidx);
+  }
+  auto segments = [&]() -> int {
+    hipLaunchKernelGGL(pool_row_heads, dim3(grid_for(E_cap)), dim3(kThreads), 0, st, L.fidx, L.tim, L.rf.counts + 1,
+                       E_cap, L.head);
+    const int r = excl_scan(L.tmp, L.tmp_bytes, L.head, L.segx, E_cap, st);
+    if (r) return r;
+    hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.segx, L.head, E_cap, L.rf.counts + 4);
+    return SSLA_OK;
+  };
+  s = segments();
+  if (s) return s;
   int64_t c[8] = {};
   int bad = 0;
-  s = ssla_events_counts(workspace, c, 4, &bad, stream);
+  s = ssla_events_counts(workspace, c, 5, &bad, stream);
   if (s) return s;
   for (int i = 0; i < 4; ++i) counts_out[i] = 0;
   if (bad) {
@@ -1242,43 +1273,34 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
     return SSLA_OK;
   }
   const int64_t n_act = c[0], E_out = c[1], t_max = c[2];
-  if (n_act < 0 || n_act > n_f || E_out < 0 || E_out > E_cap || t_max < 0) {
+  if (n_act < 0 || n_act > n_f || E_out < 0 || t_max < 0) {
     set_error("sparse_pool_plan: plan counts outside their bounds");
     return SSLA_ERR_LAUNCH;
   }
-  int64_t n_seg = 0;
-  if (E_out > 0) {
-    if (c[3] == 0) {   // every pixel run sorted by time: the counting fill
-      const int64_t HW = static_cast<int64_t>(H) * W;
-      hipLaunchKernelGGL(fill_i32, dim3(grid_for(HW * A)), dim3(kThreads), 0, st, L.inv, HW * A, -1);
-      hipLaunchKernelGGL(rf_inv_lut, dim3(grid_for(n_rf * A)), dim3(kThreads), 0, st, lut, n_rf, A, HW, L.inv);
-      hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.rf.val, gr_batch, gr_h, gr_w,
-                         L.rf.gstart, gr_len, L.rf.pixmap, L.inv, lut, n_rf, A, H, W, L.rf.ev_pre, time, E_in, E_out,
-                         L.src, L.tim, static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr),
-                         L.rf.act_pre, L.fidx);
-    } else {           // the sort fill
-      const uint64_t t_stride = static_cast<uint64_t>(t_max) + 1;
-      hipLaunchKernelGGL(rf_enumerate, dim3(grid_for(n_f * A)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W,
-                         L.rf.pixmap, gr_len, L.rf.gstart, L.rf.act, L.rf.act_pre, L.rf.ev_pre, time, E_in, t_stride,
-                         L.rf.key, L.rf.val, L.rf.pre_src, L.rf.pre_pos);
-      const int end_bit = bits_for(static_cast<uint64_t>(std::max<int64_t>(n_act, 1)) * t_stride);
-      s = sort_pairs(L.rf.tmp, L.rf.tmp_bytes, L.rf.key, L.rf.skey, L.rf.val, L.rf.perm, E_out, end_bit, st);
-      if (s) return s;
-      hipLaunchKernelGGL(rf_emit, dim3(grid_for(E_out)), dim3(kThreads), 0, st, L.rf.perm, E_out, L.rf.pre_src,
-                         L.rf.pre_pos, time, L.src, L.tim, static_cast<int64_t *>(nullptr), L.rf.skey, t_stride,
-                         L.fidx);
-    }
-    hipLaunchKernelGGL(pool_row_heads, dim3(grid_for(E_out)), dim3(kThreads), 0, st, L.fidx, L.tim, E_out, L.head);
-    s = excl_scan(L.tmp, L.tmp_bytes, L.head, L.segx, E_out, st);
+  if (E_out > E_cap) {
+    set_error("sparse_pool_plan: %lld field rows exceed the capacity %lld", (long long)E_out, (long long)E_cap);
+    return SSLA_ERR_ARG;
+  }
+  if (c[3] != 0 && E_out > 0) {   // a pixel run not sorted by time: the sort fill
+    const uint64_t t_stride = static_cast<uint64_t>(t_max) + 1;
+    hipLaunchKernelGGL(rf_enumerate, dim3(grid_for(n_f * A)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W,
+                       L.rf.pixmap, gr_len, L.rf.gstart, L.rf.act, L.rf.act_pre, L.rf.ev_pre, time, E_in, t_stride,
+                       L.rf.key, L.rf.val, L.rf.pre_src, L.rf.pre_pos);
+    const int end_bit = bits_for(static_cast<uint64_t>(std::max<int64_t>(n_act, 1)) * t_stride);
+    s = sort_pairs(L.rf.tmp, L.rf.tmp_bytes, L.rf.key, L.rf.skey, L.rf.val, L.rf.perm, E_out, end_bit, st);
     if (s) return s;
-    hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.segx, L.head, E_out, L.rf.counts + 4);
+    hipLaunchKernelGGL(rf_emit, dim3(grid_for(E_out)), dim3(kThreads), 0, st, L.rf.perm, E_out, L.rf.pre_src,
+                       L.rf.pre_pos, time, L.src, L.tim, static_cast<int64_t *>(nullptr), L.rf.skey, t_stride,
+                       L.fidx);
+    s = segments();
+    if (s) return s;
     s = ssla_events_counts(workspace, c, 5, nullptr, stream);
     if (s) return s;
-    n_seg = c[4];
-    if (n_seg < 0 || n_seg > E_out) {
-      set_error("sparse_pool_plan: segment count outside its bounds");
-      return SSLA_ERR_LAUNCH;
-    }
+  }
+  const int64_t n_seg = c[4];
+  if (n_seg < 0 || n_seg > E_out) {
+    set_error("sparse_pool_plan: segment count outside its bounds");
+    return SSLA_ERR_LAUNCH;
   }
   counts_out[0] = n_act;
   counts_out[1] = n_seg;
@@ -1291,16 +1313,15 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
 // out_len / out_batch / out_h / out_w [n_act]; outcoord is the [n_rf, 2]
 // (w, h) output coordinate table of the fields.
 extern "C" int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int64_t E_in, int B, int H, int W,
-                                     int64_t n_rf, int A, const int64_t *outcoord, int mode, int64_t n_act,
-                                     int64_t n_seg, int64_t E_out, float *out_events, int64_t *out_time,
+                                     int64_t n_rf, int A, int64_t E_cap, const int64_t *outcoord, int mode,
+                                     int64_t n_act, int64_t n_seg, int64_t E_out, float *out_events, int64_t *out_time,
                                      int64_t *out_len, int64_t *out_batch, int64_t *out_h, int64_t *out_w,
                                      void *workspace, size_t workspace_bytes, void *stream) {
   clear_error();
   SSLA_CHECK_ARG(C > 0 && G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 &&
                      (mode == 0 || mode == 1),
                  "sparse_pool_emit: bad arguments");
-  const int64_t E_cap = E_in * A;
-  SSLA_CHECK_ARG(E_cap < 0x7fffffff, "sparse_pool_emit: events x kernel positions must stay below 2^31");
+  SSLA_CHECK_ARG(E_cap >= E_in && E_cap < 0x7fffffff, "sparse_pool_emit: bad row capacity");
   SSLA_CHECK_ARG(E_out >= 0 && E_out <= E_cap && n_seg >= 0 && n_seg <= E_out && n_act >= 0 &&
                      n_act <= static_cast<int64_t>(B) * n_rf,
                  "sparse_pool_emit: counts outside the plan's bounds");

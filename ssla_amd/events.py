@@ -350,12 +350,15 @@ def pool_segments(time: torch.Tensor, lengths: torch.Tensor):
     return seg[:E], seg_t[:n_seg], new_len
 
 
-def sparse_pool(inputs, frame_size, rf2pixel_lut, rf_outcoord, mean: bool = False) -> Dict[str, torch.Tensor]:
+def sparse_pool(inputs, frame_size, rf2pixel_lut, rf_outcoord, mean: bool = False,
+                fields_per_pixel: Optional[int] = None) -> Dict[str, torch.Tensor]:
     """SparsePool.forward on pixel groups (reference layers/sparse_pooling.py:
     14-48 after gather_receptive_fields) in two library calls, without
     gradient: the receptive-field rows are never stored as features.  The
     returned dict equals that of gather_receptive_fields -> pool_segments ->
-    scatter_max / scatter_mean with a sorted index."""
+    scatter_max / scatter_mean with a sorted index.  ``fields_per_pixel``
+    bounds the fields one pixel belongs to (ceil(kh/sh) * ceil(kw/sw); the
+    kernel positions when not given): it sizes the row capacity."""
     lib = _lib.load()
     gb, gh, gw, gl = (_i64(inputs[k]) for k in ("batch_id", "h", "w", "lengths"))
     time = _i64(inputs["time"])
@@ -371,19 +374,21 @@ def sparse_pool(inputs, frame_size, rf2pixel_lut, rf_outcoord, mean: bool = Fals
     G, E_in, C = gl.numel(), time.numel(), ev.shape[1]
     if ev.shape[0] != E_in:
         raise ValueError(f"sparse_pool: {ev.shape[0]} event rows for {E_in} times")
-    ws = _ws(lib.ssla_sparse_pool_workspace_size(G, E_in, B, H, W, n_rf, A), dev)
+    E_cap = E_in * min(A, int(fields_per_pixel) if fields_per_pixel else A)
+    ws = _ws(lib.ssla_sparse_pool_workspace_size(G, E_in, B, H, W, n_rf, A, E_cap), dev)
     st = _lib.stream_of(time)
     cnt = (ctypes.c_int64 * 4)()
     _lib.check(lib.ssla_sparse_pool_plan(_lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), _lib.ptr(gl), G, _lib.ptr(time),
-                                         E_in, B, H, W, _lib.ptr(lut), n_rf, A, cnt, _lib.ptr(ws), ws.numel(), st),
-               "sparse_pool_plan")
+                                         E_in, B, H, W, _lib.ptr(lut), n_rf, A, E_cap, cnt, _lib.ptr(ws), ws.numel(),
+                                         st), "sparse_pool_plan")
     n_act, n_seg, E_out, bad = (int(v) for v in cnt)
     if bad:
         raise ValueError("sparse_pool: input indices or coordinates out of range")
     out_ev = torch.empty(n_seg, C, dtype=torch.float32, device=dev)
     out_t = torch.empty(n_seg, dtype=torch.int64, device=dev)
     fl = torch.empty(4, n_act, dtype=torch.int64, device=dev)
-    _lib.check(lib.ssla_sparse_pool_emit(_lib.ptr(ev), C, G, E_in, B, H, W, n_rf, A, _lib.ptr(outc), 1 if mean else 0,
+    _lib.check(lib.ssla_sparse_pool_emit(_lib.ptr(ev), C, G, E_in, B, H, W, n_rf, A, E_cap, _lib.ptr(outc),
+                                         1 if mean else 0,
                                          n_act, n_seg, E_out, _lib.ptr(out_ev), _lib.ptr(out_t), _lib.ptr(fl[0]),
                                          _lib.ptr(fl[1]), _lib.ptr(fl[2]), _lib.ptr(fl[3]), _lib.ptr(ws), ws.numel(),
                                          st), "sparse_pool_emit")

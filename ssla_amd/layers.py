@@ -306,8 +306,9 @@ class SparsePool(AsyncSparseModule):
         if grouped_events and self._one_call(inputs):
             dev = inputs["time"].device
             _ensure_lut(self, "rf2pixel_lut", "rf_outcoord", self.frame_size, self.kernel_size, self.stride, dev)
+            per_px = (-(-self.kernel_size[0] // self.stride[0])) * (-(-self.kernel_size[1] // self.stride[1]))
             return E.sparse_pool(inputs, self.frame_size, self.rf2pixel_lut, self.rf_outcoord,
-                                 mean=self.pool_func is scatter_mean)
+                                 mean=self.pool_func is scatter_mean, fields_per_pixel=per_px)
         x = self.prepare_inputs(inputs, grouped_events)
         seg, seg_time, new_len = E.pool_segments(x["time"], x["lengths"])
         res = self.pool_func(x["events"], seg, dim=0, dim_size=int(seg_time.numel()), sorted_index=True)

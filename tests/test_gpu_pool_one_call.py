@@ -118,3 +118,19 @@ def test_pool_one_call_empty_and_bad():
     gr["h"][2] = frame[0] + 3   # a pixel outside the frame
     with torch.no_grad(), pytest.raises(ValueError):
         layer(_dev(gr))
+
+
+def test_pool_one_call_row_capacity():
+    """A row capacity below the rows the fields hold is an error, not a
+    write past the workspace: 3 x 3 fields at stride 1 put a pixel in up to
+    9 fields, promised as 1."""
+    from ssla_amd import events as E
+    frame = (10, 12)
+    gr = _groups(6, 1, *frame, n_px=50, max_len=4, t_levels=100, C=8)
+    lut, outc = E.compute_rf2pixels(frame, (3, 3), (1, 1), device="cuda")
+    with torch.no_grad():
+        ok = E.sparse_pool(_dev(gr), frame, lut, outc, fields_per_pixel=9)
+        with pytest.raises(ValueError, match="capacity"):
+            E.sparse_pool(_dev(gr), frame, lut, outc, fields_per_pixel=1)
+    rf = OE.gather_receptive_fields(gr, frame, lut.cpu().numpy(), outc.cpu().numpy())
+    np.testing.assert_array_equal(ok["events"].cpu().numpy(), OE.sparse_pool(rf, "max")["events"])
