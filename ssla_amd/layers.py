@@ -15,7 +15,9 @@ normalisation a library LayerNorm.  The layers train: the scan, the row
 gathers / ordered index-adds and the scatter reductions have backward
 passes, so autograd runs through the composed MosAttention forward,
 LinearAttention and the SparsePool family (the fused MosAttention forward is
-inference only and is skipped whenever a gradient is recorded).
+inference only and is skipped whenever a gradient is recorded; so is the
+two-call SparsePool, ssla_sparse_pool_plan / _emit, which pools straight
+from the pixel events without storing the receptive-field rows).
 
 Deviations, all deliberate: every ordering is stable (the reference's
 unstable field sorts have implementation-defined tie order); SparsePool does
