@@ -144,16 +144,17 @@ __global__ void fill_i32(int32_t *p, int64_t n, int32_t v) { GRID_STRIDE(i, n) p
 __global__ void iota_i32(int32_t *p, int64_t n) { GRID_STRIDE(i, n) p[i] = static_cast<int32_t>(i); }
 
 // One launch for a call's set-up fills: the 8 count words and 8 status
-// flags to zero, a[0..na) = va and b[0..nb) = vb (either range may be
-// empty).  Grid: grid_for(max(8, na, nb)).
+// flags to zero, a[0..na) = va, b[0..nb) = vb and c[0..nc) = vb (any range
+// may be empty).  Grid: grid_for(max(8, na, nb, nc)).
 __global__ void clear_and_fill(int64_t *counts, int32_t *bad, int64_t *a, int64_t na, int64_t va, int32_t *b,
-                               int64_t nb, int32_t vb) {
+                               int64_t nb, int32_t vb, int32_t *c, int64_t nc) {
   GRID_STRIDE(i, 8) {
     counts[i] = 0;
     bad[i] = 0;
   }
   GRID_STRIDE(i, na) a[i] = va;
   GRID_STRIDE(i, nb) b[i] = vb;
+  GRID_STRIDE(i, nc) c[i] = vb;
 }
 
 // Sorted-fill set-up in one launch: inv and dst to -1, and the field
@@ -333,9 +334,12 @@ __global__ void lut_kernel(int H, int W, int kh, int kw, int sh, int sw, int top
 
 // ---------------------------------------------------- field / patch scatter --
 // pixel map: pixmap[b*H*W + h*W + w] = group index
+// (inv non-null: also inv[p * A + a] = rf with lut[rf * A + a] == p, the
+// inverse table of the counting fill, in the same launch)
 __global__ void rf_pixmap(const int64_t *__restrict__ gb, const int64_t *__restrict__ gh,
                           const int64_t *__restrict__ gw, int64_t G, int H, int W, int64_t n_pix,
-                          int32_t *__restrict__ pixmap, int32_t *__restrict__ bad) {
+                          int32_t *__restrict__ pixmap, int32_t *__restrict__ bad, const int64_t *__restrict__ lut,
+                          int64_t n_rf, int A, int32_t *__restrict__ inv) {
   GRID_STRIDE(g, G) {
     const int64_t p = gb[g] * H * W + gh[g] * W + gw[g];
     if (gh[g] < 0 || gh[g] >= H || gw[g] < 0 || gw[g] >= W || p < 0 || p >= n_pix) {
@@ -343,6 +347,13 @@ __global__ void rf_pixmap(const int64_t *__restrict__ gb, const int64_t *__restr
       continue;
     }
     pixmap[p] = static_cast<int32_t>(g);
+  }
+  if (inv) {
+    const int64_t HW = static_cast<int64_t>(H) * W;
+    GRID_STRIDE(t, n_rf * A) {
+      const int64_t p = lut[t];
+      if (p >= 0 && p < HW) inv[p * A + t % A] = static_cast<int32_t>(t / A);
+    }
   }
 }
 
@@ -735,12 +746,12 @@ int group_events_impl(const char *what, const float *events, const int64_t *leng
   const int64_t *Ep = L.off + B;
   if (cap == 0) {
     hipLaunchKernelGGL(clear_and_fill, dim3(1), dim3(kThreads), 0, st, L.counts, L.bad, nullptr, (int64_t)0,
-                       (int64_t)0, nullptr, (int64_t)0, 0);
+                       (int64_t)0, nullptr, (int64_t)0, 0, nullptr, (int64_t)0);
     return launch_status(what);
   }
   // sample offsets: exclusive scan of the lengths clamped to [0, N]
   hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max<int64_t>(8, B + 1))), dim3(kThreads), 0, st, L.counts,
-                     L.bad, L.kept, (int64_t)(B + 1), (int64_t)0, nullptr, (int64_t)0, 0);
+                     L.bad, L.kept, (int64_t)(B + 1), (int64_t)0, nullptr, (int64_t)0, 0, nullptr, (int64_t)0);
   hipLaunchKernelGGL(trunc_len, dim3(grid_for(B)), dim3(kThreads), 0, st, lengths, (int64_t)B, N, L.kept);
   int s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.off, B + 1, st);
   if (s) return s;
@@ -965,11 +976,14 @@ extern "C" size_t ssla_rf_scatter_workspace_size(int64_t G, int B, int H, int W,
 // counts[0] = active fields, counts[1] = field events, counts[2] = max time,
 // counts[3] = pixel runs that are not non-decreasing in time (0: the
 // sort-free fill applies).
-extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
-                                    const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
-                                    int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
-                                    void *workspace, size_t workspace_bytes, void *stream) {
-  clear_error();
+namespace {
+// The plan; inv (H * W * A int32, or NULL) also receives the inverse table of
+// the counting fill in the same launches, and with_tmax = false leaves
+// counts[2] (the largest time, which only the sort fill needs) at 0.
+int rf_plan_impl(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w, const int64_t *gr_len, int64_t G,
+                 const int64_t *time, int64_t E_in, int B, int H, int W, const int64_t *lut, int64_t n_rf, int A,
+                 int64_t E_cap, int32_t *inv, bool with_tmax, void *workspace, size_t workspace_bytes,
+                 hipStream_t st) {
   SSLA_CHECK_ARG(G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 && E_cap >= 0,
                  "rf_scatter_plan: bad sizes");
   SSLA_CHECK_ARG(E_cap < 0x7fffffff, "rf_scatter_plan: E_cap must stay below 2^31");
@@ -981,12 +995,13 @@ extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h
   }
   SSLA_CHECK_ARG(lut && (G == 0 || (gr_batch && gr_h && gr_w && gr_len)) && (E_in == 0 || time),
                  "rf_scatter_plan: null pointer");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max<int64_t>(8, n_pix))), dim3(kThreads), 0, st, L.counts,
-                     L.bad, reinterpret_cast<int64_t *>(L.tmax), (int64_t)1, (int64_t)0, L.pixmap, n_pix, -1);
-  if (G > 0)
-    hipLaunchKernelGGL(rf_pixmap, dim3(grid_for(G)), dim3(kThreads), 0, st, gr_batch, gr_h, gr_w, G, H, W, n_pix,
-                       L.pixmap, L.bad);
+  const int64_t n_inv = inv ? static_cast<int64_t>(H) * W * A : 0;
+  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max(std::max<int64_t>(8, n_pix), n_inv))), dim3(kThreads), 0,
+                     st, L.counts, L.bad, reinterpret_cast<int64_t *>(L.tmax), (int64_t)1, (int64_t)0, L.pixmap, n_pix,
+                     -1, inv, n_inv);
+  if (G > 0 || inv)
+    hipLaunchKernelGGL(rf_pixmap, dim3(grid_for(std::max(G, inv ? n_rf * A : 0))), dim3(kThreads), 0, st, gr_batch,
+                       gr_h, gr_w, G, H, W, n_pix, L.pixmap, L.bad, lut, n_rf, A, inv);
   int s = excl_scan(L.tmp, L.tmp_bytes, gr_len, L.gstart, G, st);
   if (s) return s;
   // one prefix sum of the packed (events, active) pairs while the active
@@ -1007,12 +1022,12 @@ extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h
     hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.act_pre, L.act, n_f, L.counts + 0);
     hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.ev_pre, L.nev, n_f, L.counts + 1);
   }
-  if (E_in > 0)
+  if (E_in > 0 && with_tmax)
     hipLaunchKernelGGL(max_i64, dim3(grid_for(std::min<int64_t>(E_in, 1 << 16))), dim3(kThreads), 0, st, time, E_in,
                        L.tmax);
   hipLaunchKernelGGL(rf_fields, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.act, L.act_pre, L.nev, n_f, L.f_index,
                      L.f_len);
-  hipLaunchKernelGGL(store_u64_as_i64, dim3(1), dim3(64), 0, st, L.tmax, L.counts + 2);
+  if (with_tmax) hipLaunchKernelGGL(store_u64_as_i64, dim3(1), dim3(64), 0, st, L.tmax, L.counts + 2);
   // event -> group table (the sort-free fill's input; kept in the value
   // buffer of the sort path, which needs E_in <= E_cap) and the count of
   // unsorted runs
@@ -1024,6 +1039,16 @@ extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h
                        st, L.gstart, gr_len, G, time, E_in, L.val, store,
                        reinterpret_cast<unsigned long long *>(L.counts + 3));
   return launch_status("rf_scatter_plan");
+}
+}  // namespace
+
+extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
+                                    const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
+                                    int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
+                                    void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  return rf_plan_impl(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, nullptr, true,
+                      workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 // Fill (after the plan; n_active / E_out / t_max are the plan's counts):
@@ -1241,13 +1266,12 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
     return SSLA_ERR_WORKSPACE;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int s = ssla_rf_scatter_plan(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, workspace,
-                               L.rf.total, stream);
+  // the plan with the counting fill's inverse table, without the largest
+  // time (only the sort fill needs it)
+  int s = rf_plan_impl(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, L.inv, false,
+                       workspace, L.rf.total, st);
   if (s) return s;
-  const int64_t HW = static_cast<int64_t>(H) * W;
   if (E_in > 0) {   // the counting fill, rows bounded by the capacity
-    hipLaunchKernelGGL(fill_i32, dim3(grid_for(HW * A)), dim3(kThreads), 0, st, L.inv, HW * A, -1);
-    hipLaunchKernelGGL(rf_inv_lut, dim3(grid_for(n_rf * A)), dim3(kThreads), 0, st, lut, n_rf, A, HW, L.inv);
     hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.rf.val, gr_batch, gr_h, gr_w,
                        L.rf.gstart, gr_len, L.rf.pixmap, L.inv, lut, n_rf, A, H, W, L.rf.ev_pre, time, E_in, E_cap,
                        L.src, L.tim, static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr), L.rf.act_pre,
@@ -1272,8 +1296,8 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
     counts_out[3] = 1;
     return SSLA_OK;
   }
-  const int64_t n_act = c[0], E_out = c[1], t_max = c[2];
-  if (n_act < 0 || n_act > n_f || E_out < 0 || t_max < 0) {
+  const int64_t n_act = c[0], E_out = c[1];
+  if (n_act < 0 || n_act > n_f || E_out < 0) {
     set_error("sparse_pool_plan: plan counts outside their bounds");
     return SSLA_ERR_LAUNCH;
   }
@@ -1282,6 +1306,16 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
     return SSLA_ERR_ARG;
   }
   if (c[3] != 0 && E_out > 0) {   // a pixel run not sorted by time: the sort fill
+    hipLaunchKernelGGL(max_i64, dim3(grid_for(std::min<int64_t>(E_in, 1 << 16))), dim3(kThreads), 0, st, time, E_in,
+                       L.rf.tmax);
+    hipLaunchKernelGGL(store_u64_as_i64, dim3(1), dim3(64), 0, st, L.rf.tmax, L.rf.counts + 2);
+    s = ssla_events_counts(workspace, c, 5, nullptr, stream);
+    if (s) return s;
+    const int64_t t_max = c[2];
+    if (t_max < 0) {
+      set_error("sparse_pool_plan: negative largest time");
+      return SSLA_ERR_LAUNCH;
+    }
     const uint64_t t_stride = static_cast<uint64_t>(t_max) + 1;
     hipLaunchKernelGGL(rf_enumerate, dim3(grid_for(n_f * A)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W,
                        L.rf.pixmap, gr_len, L.rf.gstart, L.rf.act, L.rf.act_pre, L.rf.ev_pre, time, E_in, t_stride,
