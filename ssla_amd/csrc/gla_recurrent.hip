@@ -58,8 +58,8 @@ struct Staged {
   static constexpr int QB = K * ES, GB = K * GS, VB = kBV * ES;   // row bytes (v: one tile)
   static constexpr int PQ = kSB * QB / 16, PG = kSB * GB / 16, PV = kSB * VB / 16;   // 16-byte pieces
   static constexpr int NQ = (PQ + 63) / 64, NG = (PG + 63) / 64, NV = (PV + 63) / 64;
-  static constexpr int DB = K * 4;            // bytes of a row of fp32 decays
-  static constexpr int OQ = 0, OK = kSB * QB, OD = 2 * kSB * QB, OV = 2 * kSB * QB + kSB * DB;
+  static constexpr int DB = K * 4;            // bytes of a row of fp32 decays, and of parked q / k rows
+  static constexpr int OQ = 0, OK = kSB * DB, OD = 2 * kSB * DB, OV = 3 * kSB * DB;
   static constexpr int BYTES = OV + kSB * VB;   // LDS per wavefront
 };
 
@@ -347,13 +347,32 @@ __global__ __launch_bounds__(256, KPL <= 8 ? 4 : 3) void gla_recurrent_staged_ke
       rv[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0));
     }
   };
+  // q and k are parked as fp32: converted once per block element here, not
+  // once per (step, lane) in the walk (the 16 lanes of a key group read the
+  // same values)
+  auto park_f32 = [&](unsigned char *dst, const uint4 &x) __attribute__((always_inline)) {
+    if constexpr (DT == SSLA_F32) {
+      *reinterpret_cast<uint4 *>(dst) = x;
+    } else {
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+      float f[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint16_t b = static_cast<uint16_t>(w[c >> 1] >> (16 * (c & 1)));
+        f[c] = DT == SSLA_BF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+      }
+      *reinterpret_cast<float4 *>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+      *reinterpret_cast<float4 *>(dst + 16) = make_float4(f[4], f[5], f[6], f[7]);
+    }
+  };
   auto park = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < G::NQ; ++j) {
       const int p = lane + 64 * j;
-      if (p < G::PQ) {
-        *reinterpret_cast<uint4 *>(lds + G::OQ + 16 * p) = rq[j];
-        *reinterpret_cast<uint4 *>(lds + G::OK + 16 * p) = rk[j];
+      if (p < G::PQ) {   // piece p: row p / (QB / 16), elements 16 / ES * (p % (QB / 16)) ..
+        const int off = (p / (G::QB / 16)) * G::DB + (p % (G::QB / 16)) * (16 / G::ES) * 4;
+        park_f32(lds + G::OQ + off, rq[j]);
+        park_f32(lds + G::OK + off, rk[j]);
       }
     }
     // decays of the block's gates: piece p holds 16 / GS gates, i.e.
@@ -452,8 +471,8 @@ __global__ __launch_bounds__(256, KPL <= 8 ? 4 : 3) void gla_recurrent_staged_ke
         constexpr int sl = decltype(si)::value;   // step within the half: acc index
         constexpr int st = h0s + sl;              // step within the block
         float d[KPL], kk[KPL], qs[KPL];
-        if (MODE != kSegState) lds_run<DT, KPL>(lds + G::OQ + st * G::QB + k0 * G::ES, qs);
-        lds_run<DT, KPL>(lds + G::OK + st * G::QB + k0 * G::ES, kk);
+        if (MODE != kSegState) lds_run<SSLA_F32, KPL>(lds + G::OQ + st * G::DB + k0 * 4, qs);
+        lds_run<SSLA_F32, KPL>(lds + G::OK + st * G::DB + k0 * 4, kk);
         lds_run<SSLA_F32, KPL>(lds + G::OD + st * G::DB + k0 * 4, d);
         const float vc = lds_elem<DT>(lds + G::OV + st * G::VB + (lane & 15) * G::ES);
         if (MODE == kSegState) {
