@@ -245,3 +245,37 @@ def test_site_block_kernels_match_torch(dev):
             assert np.all(np.abs(a - b) <= 2.0 ** -8 * np.abs(b) + 1e-30), f"stage {i} {nm}: beyond one bf16 unit"
         assert_close(_np(g), _np(rg), 0.0, f"stage {i} g", band=1e-3, ratio_max=1e-3)
         assert_close(_np(y), _np(ry), 0.0, f"stage {i} y", band=1e-3, ratio_max=1e-3)
+
+
+def test_site_block_one_call_checks(dev):
+    """ssla_site_gla_block: equal to the composed block bit for bit (y and the
+    states); with check=True a site list that is not strictly increasing
+    raises ValueError after the call and leaves those sequences' states
+    untouched; a state of the wrong shape is refused before any launch."""
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(7)
+    model = AsyncSparseGLA().to(dev)
+    blk, grid = model.blocks[1], model.grid_sizes[1]
+    gen = torch.Generator(device=dev).manual_seed(3)
+    G = 200
+    cells = torch.randperm(grid[0] * grid[1], generator=gen, device=dev)[:G].sort().values
+    lengths = torch.randint(1, 9, (G,), generator=gen, device=dev)
+    n = int(lengths.sum())
+    x = {"events": torch.randn(n, blk.in_channels, device=dev, generator=gen), "lengths": lengths,
+         "batch_id": torch.zeros(G, dtype=torch.int64, device=dev), "h": cells // grid[1], "w": cells % grid[1],
+         "time": torch.zeros(n, dtype=torch.int64, device=dev), "batch_size": 1}
+    st0 = torch.randn(grid[0] * grid[1], blk.heads, blk.head_dim, blk.head_dim, device=dev, generator=gen) * 0.1
+    s1, s2 = st0.clone(), st0.clone()
+    with torch.no_grad():
+        one = blk(x, s1, grid, check=True)
+        comp = blk(x, s2, grid, check=True, mark=lambda name: None)   # the composed path
+    assert torch.equal(one["events"], comp["events"]) and torch.equal(s1, s2)
+    bad = dict(x)
+    bad["w"] = x["w"].clone()
+    bad["h"] = x["h"].clone()
+    bad["h"][5], bad["w"][5] = bad["h"][4], bad["w"][4]   # a repeated site
+    s3 = st0.clone()
+    with torch.no_grad(), pytest.raises(ValueError):
+        blk(bad, s3, grid, check=True)
+    with torch.no_grad(), pytest.raises(ValueError):
+        blk(x, st0[:, :, :16].contiguous(), grid)
