@@ -318,7 +318,6 @@ class SparsePool(AsyncSparseModule):
         return {"events": new_events, "time": seg_time, "lengths": new_len, "batch_id": x["batch_id"],
                 "h": x["h"], "w": x["w"], "batch_size": x["batch_size"]}
 
-
     def _one_call(self, inputs) -> bool:
         """The two-call pooling (ssla_sparse_pool_plan / _emit) takes grouped
         fp32 device events with no gradient to record and a receptive field
