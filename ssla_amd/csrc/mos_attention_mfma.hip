@@ -16,7 +16,7 @@
 //   row sort or gather.
 // * mos_scan_kernel: h = a h + v along each patch's rows (zero start), and
 //   q h written over q.
-// * mos_out_kernel: per event, y = sum over a of Wb[a] (q h)[dst[e A + a]]
+// * mos_out_split_kernel: per event, y = sum over a of Wb[a] (q h)[dst[e A + a]]
 //   (+ Win e, or + e), i.e. [E, A H (+ Cin)] x [A H (+ Cin), H] with the
 //   rows gathered, then LayerNorm over the event's H outputs in the same
 //   workgroup.
@@ -262,153 +262,125 @@ __global__ __launch_bounds__(kThreads) void mos_scan_kernel(const int64_t *__res
   }
 }
 
-// The output GEMM with the copy sum, residual and LayerNorm.  Workgroup:
-// kTile events x all HP (H padded to a multiple of 32) outputs; wavefront w
-// owns rows 32 (w & 1) .. +31 and columns (HP / 2) (w >> 1) .. + HP / 2 - 1
-// (2 x HP / 32 MFMA tiles).  The reduction runs over the positions a (the H
-// channels of row dst[e A + a] of q h, zero for a missing copy, against
-// Wb[a]) and then, with an input projection, over the event's Cin inputs
-// against Win.  Each step stages kKc reduction elements.
-template <int HP>
-__global__ __launch_bounds__(kThreads) void mos_out_kernel(
+// The output GEMM with the copy sum, residual and LayerNorm, 16 events per
+// workgroup: the reduction (the H channels of row dst[e A + a] of q h
+// against Wb[a] for every position a, then the event's Cin inputs against
+// Win) runs in chunks of 16 channels dealt round-robin to the four
+// wavefronts.  Each wavefront accumulates all NT column tiles of the 16
+// events from operands loaded straight from global memory in the MFMA
+// layout (lane group g holding channels 4 g .. 4 g + 3 of a chunk in both
+// operands), the next chunk's loads in flight while the current one is
+// multiplied: no per-chunk barrier.  (A ring of three chunks in flight was
+// slower: 54.0 / 62.9 against 49.7 / 58.3 µs at hidden 48 / 96, fewer
+// wavefronts per SIMD.)  The four partial sums meet in LDS,
+// and wavefront w finishes events 4 w .. 4 w + 3 (sum, identity residual,
+// LayerNorm over H, store).
+template <int NT>
+__global__ __launch_bounds__(kThreads) void mos_out_split_kernel(
     const float *__restrict__ qh, int64_t R, const float *__restrict__ X, int64_t E, int cin, int H, int A,
     const int32_t *__restrict__ dst, const float *__restrict__ Wb, int Ag, const float *__restrict__ win,
     const float *__restrict__ ln_w, const float *__restrict__ ln_b, float eps, float *__restrict__ out) {
-  constexpr int NT = HP / 32;            // column tiles per wavefront
-  constexpr int NW = (HP + 63) / 64;     // weight pieces staged per thread
-  __shared__ __align__(16) float xs[kTile][kKc + kPad];
-  __shared__ __align__(16) float wsm[HP][kKc + kPad];
-  __shared__ int32_t s_dst[kTile * kMaxPosM];
-  __shared__ float s_part[2][kTile];
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  constexpr int HP = 16 * NT;
+  __shared__ int32_t s_dst[16 * kMaxPosM];
+  __shared__ __align__(16) float part[4][16][HP + 4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  for (int i = tid; i < kTile * A; i += kThreads) {
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * 16;
+  for (int i = tid; i < 16 * A; i += kThreads) {
     const int64_t e = e0 + i / A;
     const int32_t r = e < E ? dst[e0 * A + i] : -1;
     s_dst[i] = (r >= 0 && r < R) ? r : -1;
   }
-  const int sr = tid >> 2, sk = 4 * (tid & 3);
-  f32x4 acc[2][NT];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  const int rb = 32 * (wv & 1), cb = (HP / 2) * (wv >> 1);
-  const int steps_h = (H + kKc - 1) / kKc;
-  const int steps_in = win ? (cin + kKc - 1) / kKc : 0;
-  const int n_steps = A * steps_h + steps_in;
-  __syncthreads();   // s_dst
-  for (int s = 0; s < n_steps; ++s) {
-    const bool res = s >= A * steps_h;
-    const int a = res ? 0 : s / steps_h;
-    const int k = (res ? (s - A * steps_h) : (s - a * steps_h)) * kKc + sk;
+  __syncthreads();
+  const int ch_h = (H + 15) / 16, ch_in = win ? (cin + 15) / 16 : 0;
+  const int n_ch = A * ch_h + ch_in;
+  const int64_t ev = e0 + c16;   // this lane's event (row of the first operand)
+  auto load = [&](int s, f32x4 &xa, f32x4 (&wb)[NT]) __attribute__((always_inline)) {
+    const bool res = s >= A * ch_h;
+    const int a = res ? 0 : s / ch_h;
+    const int k = (res ? s - A * ch_h : s - a * ch_h) * 16 + 4 * g;
     const int kd = res ? cin : H;
-    f32x4 xv = {0.f, 0.f, 0.f, 0.f};
+    xa = (f32x4){0.f, 0.f, 0.f, 0.f};
     if (k < kd) {   // H and cin are multiples of 4: a piece is all in or all out
       if (res) {
-        const int64_t e = e0 + sr;
-        if (e < E) xv = *reinterpret_cast<const f32x4 *>(X + e * cin + k);
+        if (ev < E) xa = *reinterpret_cast<const f32x4 *>(X + ev * cin + k);
       } else {
-        const int32_t r = s_dst[sr * A + a];
-        if (r >= 0) xv = *reinterpret_cast<const f32x4 *>(qh + static_cast<int64_t>(r) * H + k);
+        const int32_t r = s_dst[c16 * A + a];
+        if (r >= 0) xa = *reinterpret_cast<const f32x4 *>(qh + static_cast<int64_t>(r) * H + k);
       }
     }
     const float *Wk = res ? win : Wb + (Ag > 1 ? static_cast<int64_t>(a) * H * H : 0);
-    f32x4 wr[NW];
 #pragma unroll
-    for (int p = 0; p < NW; ++p) {
-      const int n = sr + 64 * p;
-      wr[p] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      if (n < H && k < kd) wr[p] = *reinterpret_cast<const f32x4 *>(Wk + static_cast<int64_t>(n) * kd + k);
+    for (int j = 0; j < NT; ++j) {
+      const int n = 16 * j + c16;
+      wb[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      if (n < H && k < kd) wb[j] = *reinterpret_cast<const f32x4 *>(Wk + static_cast<int64_t>(n) * kd + k);
     }
-    __syncthreads();   // the previous step's operand reads are done
-    *reinterpret_cast<f32x4 *>(&xs[sr][sk]) = xv;
+  };
+  f32x4 acc[NT];
 #pragma unroll
-    for (int p = 0; p < NW; ++p)
-      if (sr + 64 * p < HP) *reinterpret_cast<f32x4 *>(&wsm[sr + 64 * p][sk]) = wr[p];
-    __syncthreads();
+  for (int j = 0; j < NT; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  f32x4 xa = {0.f, 0.f, 0.f, 0.f}, wb[NT];
 #pragma unroll
-    for (int kk = 0; kk < kKc / 4; ++kk) {
-      const int kl = 4 * kk + (lane >> 4);
-      float av[2], bv[NT];
+  for (int j = 0; j < NT; ++j) wb[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  if (wv < n_ch) load(wv, xa, wb);
+  for (int s = wv; s < n_ch; s += 4) {
+    const bool more = s + 4 < n_ch;
+    f32x4 xn = {0.f, 0.f, 0.f, 0.f}, wn[NT];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) av[i] = xs[rb + 16 * i + (lane & 15)][kl];
+    for (int j = 0; j < NT; ++j) wn[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (more) load(s + 4, xn, wn);
 #pragma unroll
-      for (int j = 0; j < NT; ++j) bv[j] = wsm[cb + 16 * j + (lane & 15)][kl];
+    for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < NT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[jj], wb[j][jj], acc[j], 0, 0, 0);
+    xa = xn;
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    for (int j = 0; j < NT; ++j) wb[j] = wn[j];
+  }
+  // acc[j][i] is event 4 g + i, column 16 j + c16
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[wv][4 * g + i][16 * j + c16] = acc[j][i];
+  __syncthreads();
+  // LayerNorm over the columns < H of events 4 wv .. 4 wv + 3; lane l holds
+  // columns l and l + 64: the mean, then the mean square deviation from it
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int er = 4 * wv + i;
+    const int64_t e = e0 + er;
+    float y[2];
+    float s1 = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int col = lane + 64 * hh;
+      y[hh] = 0.f;
+      if (col < H) {
+        y[hh] = (part[0][er][col] + part[1][er][col]) + (part[2][er][col] + part[3][er][col]);
+        if (!win && e < E) y[hh] += X[e * cin + col];
+        s1 += y[hh];
+      }
     }
-  }
-  // identity residual (cin == H)
-  if (!win) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int m = 1; m < 64; m <<= 1) s1 += __shfl_xor(s1, m);
+    const float mean = s1 / static_cast<float>(H);
+    float s2 = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t ev = e0 + rb + 16 * i + 4 * (lane >> 4) + e;
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          const int col = cb + 16 * j + (lane & 15);
-          if (ev < E && col < H) acc[i][j][e] += X[ev * cin + col];
-        }
-      }
-  }
-  // LayerNorm over the columns < H: row sums over the 16 lanes of a lane
-  // group, then over the two column halves through LDS; the mean first,
-  // then the mean square deviation from it.
-  float mean[2][4] = {}, rstd[2][4] = {};
-#pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    float part[2][4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float s = 0.f;
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          const int col = cb + 16 * j + (lane & 15);
-          const float y = acc[i][j][e];
-          const float d = pass == 0 ? y : (y - mean[i][e]) * (y - mean[i][e]);
-          s += col < H ? d : 0.f;
-        }
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) s += __shfl_xor(s, m);
-        part[i][e] = s;
-      }
-    __syncthreads();   // the previous pass's reads of s_part are done
-    if ((lane & 15) == 0) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s_part[wv >> 1][rb + 16 * i + 4 * (lane >> 4) + e] = part[i][e];
+    for (int hh = 0; hh < 2; ++hh) {
+      const int col = lane + 64 * hh;
+      if (col < H) s2 += (y[hh] - mean) * (y[hh] - mean);
     }
-    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int m = 1; m < 64; m <<= 1) s2 += __shfl_xor(s2, m);
+    const float rstd = 1.f / sqrtf(s2 / static_cast<float>(H) + eps);
+    if (e < E) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = rb + 16 * i + 4 * (lane >> 4) + e;
-        const float tot = s_part[0][row] + s_part[1][row];
-        if (pass == 0) mean[i][e] = tot / static_cast<float>(H);
-        else rstd[i][e] = 1.f / sqrtf(tot / static_cast<float>(H) + eps);
+      for (int hh = 0; hh < 2; ++hh) {
+        const int col = lane + 64 * hh;
+        if (col < H) out[e * H + col] = (y[hh] - mean) * rstd * ln_w[col] + ln_b[col];
       }
-  }
-#pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const int col = cb + 16 * j + (lane & 15);
-    if (col >= H) continue;
-    const float lw = ln_w[col], lb = ln_b[col];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t ev = e0 + rb + 16 * i + 4 * (lane >> 4) + e;
-        if (ev < E) out[ev * H + col] = (acc[i][j][e] - mean[i][e]) * rstd[i][e] * lw + lb;
-      }
+    }
   }
 }
 
@@ -421,9 +393,10 @@ bool supported(int cin, int H, int A) {
 // LDS of the largest kernel (the output GEMM at the padded hidden size).
 size_t lds_bytes(int cin, int H) {
   (void)cin;
-  const size_t hp = (H + 31) / 32 * 32;
-  return sizeof(float) * (kTile + hp) * (kKc + kPad) + sizeof(int32_t) * kTile * kMaxPosM +
-         sizeof(float) * 2 * kTile;
+  const size_t hp = (H + 15) / 16 * 16;
+  const size_t in_k = sizeof(float) * (kTile + kCols) * (kKc + kPad);
+  const size_t out_k = sizeof(int32_t) * 16 * kMaxPosM + sizeof(float) * 4 * 16 * (hp + 4);
+  return std::max(in_k, out_k);
 }
 
 size_t workspace_bytes(int64_t E, int cin, int H, int A, int64_t R, int64_t P) {
@@ -476,13 +449,23 @@ int forward(const float *events, int64_t E, int cin, const int64_t *row_src, con
                          w.q, w.v, w.a);
     }
   }
-  const int hp = (H + 31) / 32 * 32;
-#define MOSM_OUT(HPV)                                                                                              \
-  if (hp == HPV)                                                                                                   \
-    hipLaunchKernelGGL((mos_out_kernel<HPV>), dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, st, w.q, R,   \
-                       events, E, cin, H, A, w.dst, w.wb, Ag, w_in, ln_w, ln_b, eps, out);
-  MOSM_OUT(32) MOSM_OUT(64) MOSM_OUT(96) MOSM_OUT(128)
+  const int64_t tiles16 = (E + 15) / 16;
+  if (tiles16 > 0x7fffffff) {
+    set_error("mos_attention_fwd: too many events");
+    return SSLA_ERR_UNSUPPORTED;
+  }
+  switch ((H + 15) / 16) {
+#define MOSM_OUT(NTV)                                                                                              \
+  case NTV:                                                                                                        \
+    hipLaunchKernelGGL((mos_out_split_kernel<NTV>), dim3(static_cast<unsigned>(tiles16)), dim3(kThreads), 0, st,  \
+                       w.q, R, events, E, cin, H, A, w.dst, w.wb, Ag, w_in, ln_w, ln_b, eps, out);                 \
+    break;
+    MOSM_OUT(1) MOSM_OUT(2) MOSM_OUT(3) MOSM_OUT(4) MOSM_OUT(5) MOSM_OUT(6) MOSM_OUT(7) MOSM_OUT(8)
 #undef MOSM_OUT
+    default:
+      set_error("mos_attention_fwd: hidden %d above 128", H);
+      return SSLA_ERR_UNSUPPORTED;
+  }
   return launch_status("mos_attention_fwd");
 }
 
