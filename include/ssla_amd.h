@@ -494,7 +494,9 @@ int ssla_pool_segments(const int64_t *time, const int64_t *lengths, int64_t n_f,
  * stored as features, the reduction reads the pixel events [E_in, C]
  * through each row's source event.  E_cap bounds the field rows: E_in times
  * the fields one pixel can belong to (ceil(kh/sh) * ceil(kw/sw)); more rows
- * than that is SSLA_ERR_ARG.  plan: counts_out[0] active fields, [1]
+ * than that is SSLA_ERR_ARG, and E_cap == E_in (one field per pixel) takes
+ * a fill with one thread per event (a pixel found in two fields is
+ * SSLA_ERR_ARG).  plan: counts_out[0] active fields, [1]
  * pooling segments, [2] field rows, [3] 1 if a group coordinate or run is
  * out of range (nothing else computed); it reads counts from the device
  * once (twice when a pixel run is not sorted by time).  emit (same

@@ -335,11 +335,14 @@ __global__ void lut_kernel(int H, int W, int kh, int kw, int sh, int sw, int top
 // ---------------------------------------------------- field / patch scatter --
 // pixel map: pixmap[b*H*W + h*W + w] = group index
 // (inv non-null: also inv[p * A + a] = rf with lut[rf * A + a] == p, the
-// inverse table of the counting fill, in the same launch)
+// inverse table of the counting fill, in the same launch; with one_field,
+// for layouts where every pixel lies in at most one field, inv[p] = rf * A
+// + a instead, and *overlap = 1 if a pixel turns out to lie in two)
 __global__ void rf_pixmap(const int64_t *__restrict__ gb, const int64_t *__restrict__ gh,
                           const int64_t *__restrict__ gw, int64_t G, int H, int W, int64_t n_pix,
                           int32_t *__restrict__ pixmap, int32_t *__restrict__ bad, const int64_t *__restrict__ lut,
-                          int64_t n_rf, int A, int32_t *__restrict__ inv) {
+                          int64_t n_rf, int A, int32_t *__restrict__ inv, int one_field,
+                          int64_t *__restrict__ overlap) {
   GRID_STRIDE(g, G) {
     const int64_t p = gb[g] * H * W + gh[g] * W + gw[g];
     if (gh[g] < 0 || gh[g] >= H || gw[g] < 0 || gw[g] >= W || p < 0 || p >= n_pix) {
@@ -352,7 +355,13 @@ __global__ void rf_pixmap(const int64_t *__restrict__ gb, const int64_t *__restr
     const int64_t HW = static_cast<int64_t>(H) * W;
     GRID_STRIDE(t, n_rf * A) {
       const int64_t p = lut[t];
-      if (p >= 0 && p < HW) inv[p * A + t % A] = static_cast<int32_t>(t / A);
+      if (p >= 0 && p < HW) {
+        if (one_field) {   // a second field at the same pixel breaks the promise: reported
+          if (atomicCAS(&inv[p], -1, static_cast<int32_t>(t)) != -1) *overlap = 1;
+        } else {
+          inv[p * A + t % A] = static_cast<int32_t>(t / A);
+        }
+      }
     }
   }
 }
@@ -873,49 +882,85 @@ __global__ void rf_inv_lut(const int64_t *__restrict__ lut, int64_t n_rf, int A,
   }
 }
 
-// number of run elements < t (lower) or <= t (upper), times clamped at 0
-__device__ __forceinline__ int64_t run_count(const int64_t *__restrict__ time, int64_t s, int64_t n, int64_t t,
-                                             bool upper) {
-  int64_t lo = 0, hi = n;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    const int64_t v = max(time[s + mid], (int64_t)0);
-    if (upper ? v <= t : v < t) lo = mid + 1;
-    else hi = mid;
-  }
-  return lo;
-}
-
 // One thread per (event, kernel position).  o_time, o_pos, dst_map and
 // o_fidx (the row's active-field index, act_pre of its field) are optional.
+template <bool ONE>
 __global__ void rf_merge(const int32_t *__restrict__ ev2g, const int64_t *__restrict__ gb,
                          const int64_t *__restrict__ gh, const int64_t *__restrict__ gw,
                          const int64_t *__restrict__ gstart, const int64_t *__restrict__ glen,
                          const int32_t *__restrict__ pixmap, const int32_t *__restrict__ inv,
-                         const int64_t *__restrict__ lut, int64_t n_rf, int A, int H, int W,
+                         const int64_t *__restrict__ lut, int64_t n_rf, int A, int B, int H, int W,
                          const int64_t *__restrict__ ev_pre, const int64_t *__restrict__ time, int64_t E_in,
                          int64_t E_out, int64_t *__restrict__ o_src, int64_t *__restrict__ o_time,
                          int64_t *__restrict__ o_pos, int32_t *__restrict__ dst_map,
                          const int64_t *__restrict__ act_pre, int32_t *__restrict__ o_fidx) {
   const int64_t HW = static_cast<int64_t>(H) * W;
-  GRID_STRIDE(t, E_in * A) {
-    const int64_t e = t / A;
-    const int a = static_cast<int>(t % A);
+  // ONE: one thread per event, its only (field, position) from inv[p]
+  // (every pixel in at most one field); else one per (event, position)
+  GRID_STRIDE(t, ONE ? E_in : E_in * A) {
+    // E_in * A < 2^31 (checked by the callers): 32-bit division, not the
+    // 64-bit emulation
+    const uint32_t t32 = static_cast<uint32_t>(t);
+    const int64_t e = ONE ? t : static_cast<int64_t>(t32 / static_cast<uint32_t>(A));
+    int a = ONE ? 0 : static_cast<int>(t32 - static_cast<uint32_t>(e) * static_cast<uint32_t>(A));
     const int32_t g = ev2g[e];
     if (g < 0) continue;
     const int64_t b = gb[g], p = gh[g] * W + gw[g];
-    if (p < 0 || p >= HW) continue;
-    const int32_t rf = inv[p * A + a];
-    if (rf < 0) continue;
+    // (inputs the plan reports as bad are only kept in range here: the
+    // counting fill may run before the plan's counts are read)
+    if (b < 0 || b >= B || p < 0 || p >= HW) continue;
+    int32_t rf;
+    if constexpr (ONE) {
+      const int32_t pf = inv[p];
+      if (pf < 0) continue;
+      rf = static_cast<int32_t>(static_cast<uint32_t>(pf) / static_cast<uint32_t>(A));
+      a = pf - rf * A;
+    } else {
+      rf = inv[p * A + a];
+      if (rf < 0) continue;
+    }
     const int64_t tt = max(time[e], (int64_t)0);
     int64_t rank = e - gstart[g];
-    for (int a2 = 0; a2 < A; ++a2) {
-      if (a2 == a) continue;
-      const int64_t p2 = lut[static_cast<int64_t>(rf) * A + a2];
-      if (p2 < 0) continue;
-      const int32_t g2 = pixmap[b * HW + p2];
-      if (g2 < 0) continue;
-      rank += run_count(time, gstart[g2], glen[g2], tt, a2 < a);
+    // the other positions kMB at a time: their table entries, groups and
+    // runs are loaded side by side, then their binary searches advance in
+    // lockstep, so the chain of dependent loads is about as long as one
+    // position's instead of the sum over all of them
+    constexpr int kMB = 8;
+    for (int a0 = 0; a0 < A; a0 += kMB) {
+      int64_t p2[kMB];
+#pragma unroll
+      for (int u = 0; u < kMB; ++u) {
+        const int a2 = a0 + u;
+        p2[u] = (a2 < A && a2 != a) ? lut[static_cast<int64_t>(rf) * A + a2] : -1;
+      }
+      int32_t g2[kMB];
+#pragma unroll
+      for (int u = 0; u < kMB; ++u) g2[u] = p2[u] >= 0 ? pixmap[b * HW + p2[u]] : -1;
+      int64_t s2[kMB];
+      int32_t lo[kMB], hi[kMB];
+#pragma unroll
+      for (int u = 0; u < kMB; ++u) {
+        s2[u] = g2[u] >= 0 ? min(max(gstart[g2[u]], (int64_t)0), E_in) : 0;
+        lo[u] = 0;
+        hi[u] = g2[u] >= 0 ? static_cast<int32_t>(min(max(glen[g2[u]], (int64_t)0), E_in - s2[u])) : 0;
+      }
+      bool more = true;
+      while (more) {
+        more = false;
+#pragma unroll
+        for (int u = 0; u < kMB; ++u) {
+          if (lo[u] < hi[u]) {   // elements < tt (<= tt for earlier positions), times clamped at 0
+            const int32_t mid = (lo[u] + hi[u]) >> 1;
+            const int64_t v = max(time[s2[u] + mid], (int64_t)0);
+            const bool le = a0 + u < a ? v <= tt : v < tt;
+            lo[u] = le ? mid + 1 : lo[u];
+            hi[u] = le ? hi[u] : mid;
+            more = true;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kMB; ++u) rank += lo[u];
     }
     const int64_t row = ev_pre[b * n_rf + rf] + rank;
     if (row < 0 || row >= E_out) continue;   // inconsistent inputs: drop, never write out of range
@@ -982,8 +1027,8 @@ namespace {
 // counts[2] (the largest time, which only the sort fill needs) at 0.
 int rf_plan_impl(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w, const int64_t *gr_len, int64_t G,
                  const int64_t *time, int64_t E_in, int B, int H, int W, const int64_t *lut, int64_t n_rf, int A,
-                 int64_t E_cap, int32_t *inv, bool with_tmax, void *workspace, size_t workspace_bytes,
-                 hipStream_t st) {
+                 int64_t E_cap, int32_t *inv, bool one_field, bool with_tmax, void *workspace,
+                 size_t workspace_bytes, hipStream_t st) {
   SSLA_CHECK_ARG(G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 && E_cap >= 0,
                  "rf_scatter_plan: bad sizes");
   SSLA_CHECK_ARG(E_cap < 0x7fffffff, "rf_scatter_plan: E_cap must stay below 2^31");
@@ -995,13 +1040,14 @@ int rf_plan_impl(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr
   }
   SSLA_CHECK_ARG(lut && (G == 0 || (gr_batch && gr_h && gr_w && gr_len)) && (E_in == 0 || time),
                  "rf_scatter_plan: null pointer");
-  const int64_t n_inv = inv ? static_cast<int64_t>(H) * W * A : 0;
+  const int64_t n_inv = inv ? static_cast<int64_t>(H) * W * (one_field ? 1 : A) : 0;
   hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max(std::max<int64_t>(8, n_pix), n_inv))), dim3(kThreads), 0,
                      st, L.counts, L.bad, reinterpret_cast<int64_t *>(L.tmax), (int64_t)1, (int64_t)0, L.pixmap, n_pix,
                      -1, inv, n_inv);
   if (G > 0 || inv)
     hipLaunchKernelGGL(rf_pixmap, dim3(grid_for(std::max(G, inv ? n_rf * A : 0))), dim3(kThreads), 0, st, gr_batch,
-                       gr_h, gr_w, G, H, W, n_pix, L.pixmap, L.bad, lut, n_rf, A, inv);
+                       gr_h, gr_w, G, H, W, n_pix, L.pixmap, L.bad, lut, n_rf, A, inv, one_field ? 1 : 0,
+                       L.counts + 5);
   int s = excl_scan(L.tmp, L.tmp_bytes, gr_len, L.gstart, G, st);
   if (s) return s;
   // one prefix sum of the packed (events, active) pairs while the active
@@ -1047,8 +1093,8 @@ extern "C" int ssla_rf_scatter_plan(const int64_t *gr_batch, const int64_t *gr_h
                                     int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
                                     void *workspace, size_t workspace_bytes, void *stream) {
   clear_error();
-  return rf_plan_impl(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, nullptr, true,
-                      workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  return rf_plan_impl(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, nullptr, false,
+                      true, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 // Fill (after the plan; n_active / E_out / t_max are the plan's counts):
@@ -1117,7 +1163,8 @@ extern "C" int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_
   SSLA_CHECK_ARG(out_src && out_pos && f_index && f_len && inv, "rf_scatter_fill_sorted: null pointer");
   SSLA_CHECK_ARG(E_in <= E_cap, "rf_scatter_fill_sorted: needs E_in <= E_cap (the plan's event table)");
   SSLA_CHECK_ARG(G == 0 || (gr_batch && gr_h && gr_w && gr_len), "rf_scatter_fill_sorted: null group arrays");
-  SSLA_CHECK_ARG(E_out < 0x7fffffff, "rf_scatter_fill_sorted: E_out must stay below 2^31");
+  SSLA_CHECK_ARG(E_out < 0x7fffffff && E_in * A < 0x7fffffff,
+                 "rf_scatter_fill_sorted: E_out and E_in * A must stay below 2^31");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t HW = static_cast<int64_t>(H) * W;
   const int64_t n_dst = dst_map ? E_in * A : 0;
@@ -1127,8 +1174,8 @@ extern "C" int ssla_rf_scatter_fill_sorted(const int64_t *gr_batch, const int64_
   hipLaunchKernelGGL(rf_inv_lut, dim3(grid_for(n_rf * A)), dim3(kThreads), 0, st, lut, n_rf, A, HW, inv);
   if (E_in > 0) {
     if (E_out > 0)
-      hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.val, gr_batch, gr_h, gr_w,
-                         L.gstart, gr_len, L.pixmap, inv, lut, n_rf, A, H, W, L.ev_pre, time, E_in, E_out, out_src,
+      hipLaunchKernelGGL(rf_merge<false>, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.val, gr_batch, gr_h, gr_w,
+                         L.gstart, gr_len, L.pixmap, inv, lut, n_rf, A, B, H, W, L.ev_pre, time, E_in, E_out, out_src,
                          out_time, out_pos, dst_map, static_cast<const int64_t *>(nullptr),
                          static_cast<int32_t *>(nullptr));
   }
@@ -1186,7 +1233,7 @@ __global__ void pool_row_heads(const int32_t *__restrict__ fidx, const int64_t *
 // once.  Max: the first row among equal maxima; NaN never wins; a segment
 // whose values are all NaN gives 0 (scatter_max's rule for a row that no
 // event wins).  Then per active field its segment count and coordinates.
-template <bool MEAN>
+template <bool MEAN, int VW>
 __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C, const int64_t *__restrict__ src,
                                const int64_t *__restrict__ tim, const int64_t *__restrict__ head,
                                const int64_t *__restrict__ segx, int64_t E_out, int64_t n_seg,
@@ -1195,30 +1242,58 @@ __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C
                                const int64_t *__restrict__ outcoord, float *__restrict__ o_ev,
                                int64_t *__restrict__ o_time, int64_t *__restrict__ o_len, int64_t *__restrict__ o_b,
                                int64_t *__restrict__ o_h, int64_t *__restrict__ o_w) {
-  GRID_STRIDE(t, E_out * C) {
-    const int64_t r = t / C;
-    const int c = static_cast<int>(t - r * C);
+  // VW consecutive channels per thread (C / VW threads per row; E_out * C
+  // < 2^31, checked by the caller)
+  const uint32_t CV = static_cast<uint32_t>(C / VW);
+  GRID_STRIDE(t, E_out * CV) {
+    const uint32_t t32 = static_cast<uint32_t>(t);
+    const int64_t r = static_cast<int64_t>(t32 / CV);
+    const int c = static_cast<int>(t32 - static_cast<uint32_t>(r) * CV) * VW;
     if (!head[r]) continue;
     const int64_t s = segx[r];
     if (s < 0 || s >= n_seg) continue;
-    double sum = 0.0;
-    float best = -INFINITY;
-    bool found = false;
+    double sum[VW];
+    float best[VW];
+    bool found[VW];
+#pragma unroll
+    for (int v = 0; v < VW; ++v) {
+      sum[v] = 0.0;
+      best[v] = -INFINITY;
+      found[v] = false;
+    }
     int64_t r2 = r;
     do {
       const int64_t e = src[r2];
-      const float x = (e >= 0 && e < E_in) ? ev[e * C + c] : 0.f;
-      if constexpr (MEAN) {
-        sum += static_cast<double>(x);
+      float x[VW];
+      if (e >= 0 && e < E_in) {
+        if constexpr (VW == 4) {
+          const float4 q = *reinterpret_cast<const float4 *>(ev + e * C + c);
+          x[0] = q.x, x[1] = q.y, x[2] = q.z, x[3] = q.w;
+        } else {
+#pragma unroll
+          for (int v = 0; v < VW; ++v) x[v] = ev[e * C + c + v];
+        }
       } else {
-        const bool take = x > best || (!found && x == best);
-        best = take ? x : best;
-        found = found || take;
+#pragma unroll
+        for (int v = 0; v < VW; ++v) x[v] = 0.f;
+      }
+#pragma unroll
+      for (int v = 0; v < VW; ++v) {
+        if constexpr (MEAN) {
+          sum[v] += static_cast<double>(x[v]);
+        } else {
+          const bool take = x[v] > best[v] || (!found[v] && x[v] == best[v]);
+          best[v] = take ? x[v] : best[v];
+          found[v] = found[v] || take;
+        }
       }
       ++r2;
     } while (r2 < E_out && !head[r2]);
-    if constexpr (MEAN) o_ev[s * C + c] = static_cast<float>(sum / static_cast<double>(r2 - r));
-    else o_ev[s * C + c] = found ? best : 0.f;
+#pragma unroll
+    for (int v = 0; v < VW; ++v) {
+      if constexpr (MEAN) o_ev[s * C + c + v] = static_cast<float>(sum[v] / static_cast<double>(r2 - r));
+      else o_ev[s * C + c + v] = found[v] ? best[v] : 0.f;
+    }
     if (c == 0) o_time[s] = tim[r];
   }
   GRID_STRIDE(j, n_act) {
@@ -1259,7 +1334,8 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
                      E_cap >= E_in,
                  "sparse_pool_plan: bad arguments");
   const int64_t n_f = static_cast<int64_t>(B) * n_rf;
-  SSLA_CHECK_ARG(E_cap < 0x7fffffff, "sparse_pool_plan: the row capacity must stay below 2^31");
+  SSLA_CHECK_ARG(E_cap < 0x7fffffff && E_in * A < 0x7fffffff,
+                 "sparse_pool_plan: the row capacity and E_in * A must stay below 2^31");
   const PoolWs L = pool_layout(workspace, G, B, H, W, n_rf, A, E_cap);
   if (!workspace || workspace_bytes < L.total) {
     set_error("sparse_pool_plan: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
@@ -1268,14 +1344,23 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
   hipStream_t st = static_cast<hipStream_t>(stream);
   // the plan with the counting fill's inverse table, without the largest
   // time (only the sort fill needs it)
-  int s = rf_plan_impl(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, L.inv, false,
+  // a capacity of one row per event promises one field per pixel (more rows
+  // than that are reported below): one thread per event in the fill
+  const bool one = E_cap == E_in;
+  int s = rf_plan_impl(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, L.inv, one, false,
                        workspace, L.rf.total, st);
   if (s) return s;
   if (E_in > 0) {   // the counting fill, rows bounded by the capacity
-    hipLaunchKernelGGL(rf_merge, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.rf.val, gr_batch, gr_h, gr_w,
-                       L.rf.gstart, gr_len, L.rf.pixmap, L.inv, lut, n_rf, A, H, W, L.rf.ev_pre, time, E_in, E_cap,
-                       L.src, L.tim, static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr), L.rf.act_pre,
-                       L.fidx);
+    if (one)
+      hipLaunchKernelGGL(rf_merge<true>, dim3(grid_for(E_in)), dim3(kThreads), 0, st, L.rf.val, gr_batch, gr_h,
+                         gr_w, L.rf.gstart, gr_len, L.rf.pixmap, L.inv, lut, n_rf, A, B, H, W, L.rf.ev_pre, time,
+                         E_in, E_cap, L.src, L.tim, static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr),
+                         L.rf.act_pre, L.fidx);
+    else
+      hipLaunchKernelGGL(rf_merge<false>, dim3(grid_for(E_in * A)), dim3(kThreads), 0, st, L.rf.val, gr_batch, gr_h,
+                         gr_w, L.rf.gstart, gr_len, L.rf.pixmap, L.inv, lut, n_rf, A, B, H, W, L.rf.ev_pre, time,
+                         E_in, E_cap, L.src, L.tim, static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr),
+                         L.rf.act_pre, L.fidx);
   }
   auto segments = [&]() -> int {
     hipLaunchKernelGGL(pool_row_heads, dim3(grid_for(E_cap)), dim3(kThreads), 0, st, L.fidx, L.tim, L.rf.counts + 1,
@@ -1289,12 +1374,17 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
   if (s) return s;
   int64_t c[8] = {};
   int bad = 0;
-  s = ssla_events_counts(workspace, c, 5, &bad, stream);
+  s = ssla_events_counts(workspace, c, 6, &bad, stream);
   if (s) return s;
   for (int i = 0; i < 4; ++i) counts_out[i] = 0;
   if (bad) {
     counts_out[3] = 1;
     return SSLA_OK;
+  }
+  if (c[5] != 0) {
+    set_error("sparse_pool_plan: a pixel lies in more than one field, but the row capacity (E_cap == E_in) "
+              "promises one");
+    return SSLA_ERR_ARG;
   }
   const int64_t n_act = c[0], E_out = c[1];
   if (n_act < 0 || n_act > n_f || E_out < 0) {
@@ -1369,15 +1459,21 @@ extern "C" int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int6
                  "sparse_pool_emit: null pointer");
   if (E_out * C == 0 && n_act == 0) return SSLA_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned grid = grid_for(std::max(E_out * C, n_act));
-  if (mode == 1)
-    hipLaunchKernelGGL(pool_emit_rows<true>, dim3(grid), dim3(kThreads), 0, st, events, E_in, C, L.src, L.tim,
-                       L.head, L.segx, E_out, n_seg, L.rf.f_index, L.rf.f_len, L.rf.ev_pre, n_act, n_rf, outcoord,
-                       out_events, out_time, out_len, out_batch, out_h, out_w);
-  else
-    hipLaunchKernelGGL(pool_emit_rows<false>, dim3(grid), dim3(kThreads), 0, st, events, E_in, C, L.src, L.tim,
-                       L.head, L.segx, E_out, n_seg, L.rf.f_index, L.rf.f_len, L.rf.ev_pre, n_act, n_rf, outcoord,
-                       out_events, out_time, out_len, out_batch, out_h, out_w);
+  SSLA_CHECK_ARG(E_out * C < 0x7fffffff, "sparse_pool_emit: rows x channels must stay below 2^31");
+  const bool vec = C % 4 == 0 && aligned(events, 16) && aligned(out_events, 16);
+  const unsigned grid = grid_for(std::max(E_out * (vec ? C / 4 : C), n_act));
+#define SSLA_POOL_EMIT(MEANV, VWV)                                                                                \
+  hipLaunchKernelGGL((pool_emit_rows<MEANV, VWV>), dim3(grid), dim3(kThreads), 0, st, events, E_in, C, L.src,       \
+                     L.tim, L.head, L.segx, E_out, n_seg, L.rf.f_index, L.rf.f_len, L.rf.ev_pre, n_act, n_rf,       \
+                     outcoord, out_events, out_time, out_len, out_batch, out_h, out_w)
+  if (mode == 1) {
+    if (vec) SSLA_POOL_EMIT(true, 4);
+    else SSLA_POOL_EMIT(true, 1);
+  } else {
+    if (vec) SSLA_POOL_EMIT(false, 4);
+    else SSLA_POOL_EMIT(false, 1);
+  }
+#undef SSLA_POOL_EMIT
   return launch_status("sparse_pool_emit");
 }
 

@@ -84,12 +84,14 @@ def test_pool_one_call_vs_composed_and_oracle(kind, k, s, t_levels, sorted_runs)
     np.testing.assert_array_equal(one["batch_id"].cpu().numpy(), rf["batch_id"])
 
 
-def test_pool_one_call_special_values():
+@pytest.mark.parametrize("C", [16, 6])
+def test_pool_one_call_special_values(C):
     """NaN never wins, equal maxima keep the first row (+0 / -0 bits), -inf
-    is a value: the same bits as scatter_max on the composed path."""
+    is a value: the same bits as scatter_max on the composed path (four
+    channels per thread, and one for a width that is not a multiple of 4)."""
     from ssla_amd.layers import SparseMaxPool
     frame = (9, 11)
-    gr = _groups(5, 1, *frame, n_px=40, max_len=5, t_levels=3, C=16)
+    gr = _groups(5, 1, *frame, n_px=40, max_len=5, t_levels=3, C=C)
     ev = gr["events"]
     rng = np.random.default_rng(9)
     pick = rng.random(ev.shape)
