@@ -183,11 +183,28 @@ __global__ void total_from_scan(const int64_t *excl, const int64_t *val, int64_t
   if (blockIdx.x == 0 && threadIdx.x == 0) *dst = n > 0 ? excl[n - 1] + val[n - 1] : 0;
 }
 
+// (q, r) = (t / d, t % d): in 32 bits when the kernel's whole index range
+// fits (`small`, the same for every thread of a launch) instead of through
+// the 64-bit division's emulation
+__device__ __forceinline__ void div_index(int64_t t, int d, bool small, int64_t &q, int &r) {
+  if (small) {
+    const uint32_t t32 = static_cast<uint32_t>(t), qq = t32 / static_cast<uint32_t>(d);
+    q = qq;
+    r = static_cast<int>(t32 - qq * static_cast<uint32_t>(d));
+  } else {
+    q = t / d;
+    r = static_cast<int>(t - q * d);
+  }
+}
+
 // out[j, :] = src[idx[j], :] (rows of C floats); idx outside [0, n_src) -> 0.
 __global__ void gather_rows_kernel(const float *__restrict__ src, const int64_t *__restrict__ idx, int64_t m,
                                    int64_t n_src, int C, float *__restrict__ out) {
+  const bool small = m * C < 0x7fffffff;
   GRID_STRIDE(t, m * C) {
-    const int64_t j = t / C, c = t % C;
+    int64_t j;
+    int c;
+    div_index(t, C, small, j, c);
     const int64_t r = idx[j];
     out[t] = (r >= 0 && r < n_src) ? src[r * C + c] : 0.f;
   }
@@ -648,9 +665,11 @@ __global__ void pixel_delays(float *__restrict__ feat, const int64_t *__restrict
 __global__ void grid_place(const float *__restrict__ ev, const int64_t *__restrict__ gend, const int64_t *__restrict__ gb,
                            const int64_t *__restrict__ gh, const int64_t *__restrict__ gw, int64_t G, int64_t E, int C,
                            int B, int Hg, int Wg, float *__restrict__ grid, int32_t *__restrict__ bad) {
+  const bool small = G * C < 0x7fffffff;
   GRID_STRIDE(t, G * C) {
-    const int64_t g = t / C;
-    const int c = static_cast<int>(t % C);
+    int64_t g;
+    int c;
+    div_index(t, C, small, g, c);
     const int64_t b = gb[g], h = gh[g], w = gw[g];
     const int64_t last = gend[g] - 1;
     if (b < 0 || b >= B || h < 0 || h >= Hg || w < 0 || w >= Wg || last < 0 || last >= E) {

@@ -111,19 +111,22 @@ __global__ void fold_kernel(const float *__restrict__ ws, int As, const float *_
   MOSM_GRID_STRIDE(i, na + nb) {
     const float *w1, *w2;
     int64_t stride;
+    // (na + nb < 2^31, checked by the host: 32-bit index arithmetic)
+    const uint32_t i32 = static_cast<uint32_t>(i);
     if (i < na) {
-      const int c = static_cast<int>(i % cin);
-      const int n = static_cast<int>((i / cin) % (3 * H));
-      const int64_t a = i / (static_cast<int64_t>(cin) * 3 * H);
+      const uint32_t ucin = static_cast<uint32_t>(cin), row = i32 / ucin;
+      const int c = static_cast<int>(i32 - row * ucin);
+      const uint32_t a = row / static_cast<uint32_t>(3 * H);
+      const int n = static_cast<int>(row - a * static_cast<uint32_t>(3 * H));
       w1 = (n < H ? wq : n < 2 * H ? wv : wg) + static_cast<int64_t>(n % H) * H;
-      w2 = ws + a * H * cin + c;
+      w2 = ws + static_cast<int64_t>(a) * H * cin + c;
       stride = cin;
     } else {
-      const int64_t k = i - na;
-      const int c = static_cast<int>(k % H);
-      const int n = static_cast<int>((k / H) % H);
-      const int64_t a = k / (static_cast<int64_t>(H) * H);
-      w1 = wgp + (a * H + n) * H;
+      const uint32_t k = i32 - static_cast<uint32_t>(na), uh = static_cast<uint32_t>(H), row = k / uh;
+      const int c = static_cast<int>(k - row * uh);
+      const uint32_t a = row / uh;
+      const int n = static_cast<int>(row - a * uh);
+      w1 = wgp + (static_cast<int64_t>(a) * H + n) * H;
       w2 = wo + c;
       stride = H;
     }
@@ -433,6 +436,10 @@ int forward(const float *events, int64_t E, int cin, const int64_t *row_src, con
     hipLaunchKernelGGL(dst_fill, dim3(grid_for(R)), dim3(kThreads), 0, st, row_src, row_pos, R, E, A, w.dst, w.cu, P);
   }
   const int64_t nf = static_cast<int64_t>(As) * 3 * H * cin + static_cast<int64_t>(Ag) * H * H;
+  if (nf >= 0x7fffffff) {
+    set_error("mos_attention_fwd: folded weights too large");
+    return SSLA_ERR_UNSUPPORTED;
+  }
   hipLaunchKernelGGL(fold_kernel, dim3(grid_for(nf)), dim3(kThreads), 0, st, w_scatter, As, w_q, w_v, w_g, w_o,
                      w_gather, Ag, cin, H, w.wa, w.wb);
   if (R > 0) {
