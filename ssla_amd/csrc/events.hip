@@ -228,8 +228,9 @@ __global__ void ge_keys(const float *__restrict__ ev, const int64_t *__restrict_
                         const int64_t *__restrict__ off, int B, int64_t N, int C, int H, int W,
                         uint64_t *__restrict__ key, int32_t *__restrict__ val, int64_t *__restrict__ row_of,
                         int32_t *__restrict__ bad) {
-  GRID_STRIDE(s, static_cast<int64_t>(B) * N) {
-    const int64_t b = s / N, j = s % N;
+  GRID_STRIDE(s, static_cast<int64_t>(B) * N) {   // B * N < 2^31 (checked by the caller)
+    const uint32_t s32 = static_cast<uint32_t>(s), b32 = s32 / static_cast<uint32_t>(N);
+    const int64_t b = b32, j = s32 - b32 * static_cast<uint32_t>(N);
     if (j >= min(max(lengths[b], (int64_t)0), N)) continue;
     const int64_t f = off[b] + j;
     const float x = ev[s * C + 0], y = ev[s * C + 1];
