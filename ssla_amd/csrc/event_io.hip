@@ -25,8 +25,10 @@ __global__ __launch_bounds__(kDecThreads) void dat_decode_kernel(const uint2 *__
                                                                  float4 *__restrict__ out) {
   const int64_t n_rows = static_cast<int64_t>(B) * L;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kDecThreads;
+  const bool small = n_rows < 0x7fffffff;   // 32-bit division, not the 64-bit emulation
   for (int64_t g = static_cast<int64_t>(blockIdx.x) * kDecThreads + threadIdx.x; g < n_rows; g += stride) {
-    const int64_t b = g / L, i = g - b * L;
+    const int64_t b = small ? static_cast<int64_t>(static_cast<uint32_t>(g) / static_cast<uint32_t>(L)) : g / L;
+    const int64_t i = g - b * L;
     const int64_t s0 = start[b], n = start[b + 1] - s0;
     // padding rows: zeros, then (Gen1 layout) p = 0 * 2 - 1 like every row
     float4 v = make_float4(0.f, 0.f, 0.f, layout == SSLA_EVENTS_XYTP ? -1.f : 0.f);
