@@ -469,9 +469,12 @@ int ssla_truncate_packed(const float *data, const int64_t *seqlens, int64_t n_se
 
 /* TemporalDropout.forward keep indices (layers/temporal_dropout.py:30-53):
  * ceil(len / window) rows per sequence, every window-th, the last kept.
- * counts[0] = rows kept. */
+ * counts[0] = rows kept; out_idx holds idx_cap rows (sum(len) + n_seq
+ * always suffices) and a count above idx_cap means the rows past it were
+ * not written: the caller reports that as an error. */
 int ssla_temporal_dropout_index(const int64_t *lengths, int64_t n_seq, int64_t window, int64_t *out_idx,
-                                int64_t *out_lengths, void *workspace, size_t workspace_bytes, void *stream);
+                                int64_t idx_cap, int64_t *out_lengths, void *workspace, size_t workspace_bytes,
+                                void *stream);
 
 /* repeat_interleave(values, lengths) into out [n] (layers/linear_attention.py:60,
  * layers/sparse_pooling.py:27). */

@@ -90,7 +90,7 @@ SIGNATURES = {
     "ssla_sort_pairs": (_i32, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
     "ssla_segments_workspace_size": (_sz, [_i64]),
     "ssla_truncate_packed": (_i32, [_vp, _vp, _i64, _i64, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
-    "ssla_temporal_dropout_index": (_i32, [_vp, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
+    "ssla_temporal_dropout_index": (_i32, [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _sz, _vp]),
     "ssla_expand_segments": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
     "ssla_pool_segments": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ssla_sparse_pool_workspace_size": (_sz, [_i64, _i64, _i32, _i32, _i32, _i64, _i32, _i64]),

@@ -567,11 +567,12 @@ __global__ void td_len(const int64_t *__restrict__ len, int64_t n, int64_t w, in
 }
 __global__ void td_index(const int64_t *__restrict__ len, const int64_t *__restrict__ start,
                          const int64_t *__restrict__ kl, const int64_t *__restrict__ kpre, int64_t n, int64_t w,
-                         int64_t *__restrict__ idx) {
+                         int64_t cap, int64_t *__restrict__ idx) {
   GRID_STRIDE(s, n) {
     const int64_t L = max(len[s], (int64_t)0);
     const int64_t off = ((L % w - 1) % w + w) % w;
-    for (int64_t j = 0; j < kl[s]; ++j) idx[kpre[s] + j] = start[s] + off + j * w;
+    const int64_t end = min(kpre[s] + kl[s], cap);   // rows past the capacity are counted, not written
+    for (int64_t j = kpre[s]; j < end; ++j) idx[j] = start[s] + off + (j - kpre[s]) * w;
   }
 }
 
@@ -1653,12 +1654,14 @@ extern "C" int ssla_truncate_packed(const float *data, const int64_t *seqlens, i
 }
 
 // TemporalDropout keep indices: per sequence ceil(len / w) indices, every
-// w-th row, aligned so that the last row is kept.  counts[0] = kept rows.
+// w-th row, aligned so that the last row is kept.  counts[0] = kept rows;
+// out_idx holds idx_cap rows, and a count above idx_cap means the rows past
+// it were not written.
 extern "C" int ssla_temporal_dropout_index(const int64_t *lengths, int64_t n_seq, int64_t window, int64_t *out_idx,
-                                           int64_t *out_lengths, void *workspace, size_t workspace_bytes,
-                                           void *stream) {
+                                           int64_t idx_cap, int64_t *out_lengths, void *workspace,
+                                           size_t workspace_bytes, void *stream) {
   clear_error();
-  SSLA_CHECK_ARG(n_seq >= 0 && window > 0, "temporal_dropout_index: bad arguments");
+  SSLA_CHECK_ARG(n_seq >= 0 && window > 0 && idx_cap >= 0, "temporal_dropout_index: bad arguments");
   const SegWs L = seg_layout(workspace, n_seq);
   if (!workspace || workspace_bytes < L.total) {
     set_error("temporal_dropout_index: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
@@ -1675,7 +1678,7 @@ extern "C" int ssla_temporal_dropout_index(const int64_t *lengths, int64_t n_seq
   if (s) return s;
   hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.kpre, L.kl, n_seq, L.counts);
   hipLaunchKernelGGL(td_index, dim3(grid_for(n_seq)), dim3(kThreads), 0, st, lengths, L.start, L.kl, L.kpre, n_seq,
-                     window, out_idx);
+                     window, idx_cap, out_idx);
   if (hipMemcpyAsync(out_lengths, L.kl, sizeof(int64_t) * n_seq, hipMemcpyDeviceToDevice, st) != hipSuccess) {
     set_error("temporal_dropout_index: copy of the lengths failed");
     return SSLA_ERR_LAUNCH;

@@ -280,21 +280,27 @@ def truncate_packed_sequence(data: torch.Tensor, seqlens: torch.Tensor, threshol
     return nd, out_l
 
 
-def temporal_dropout_index(lengths: torch.Tensor, window_size: int):
+def temporal_dropout_index(lengths: torch.Tensor, window_size: int, total: Optional[int] = None):
     """Keep indices and new lengths of TemporalDropout (reference
-    layers/temporal_dropout.py:30-53)."""
+    layers/temporal_dropout.py:30-53).  ``total`` is the number of rows the
+    sequences index (the events tensor's rows): given, it sizes the output
+    without reading sum(lengths) back from the device, and lengths that keep
+    more rows than it allows raise ValueError."""
     ln = _i64(lengths)
     dev = _lib.require_cuda(ln)
     lib = _lib.load()
     ws = _ws(lib.ssla_segments_workspace_size(ln.numel()), dev)
     # capacity: sum(ceil(len / w)) <= sum(len) + n
-    cap_t = int(ln.sum().item()) + ln.numel()
+    cap_t = (int(ln.sum().item()) if total is None else int(total)) + ln.numel()
     idx = torch.empty(max(cap_t, 1), dtype=torch.int64, device=dev)
     kl = torch.empty(ln.numel(), dtype=torch.int64, device=dev)
     st = _lib.stream_of(ln)
-    _lib.check(lib.ssla_temporal_dropout_index(_lib.ptr(ln), ln.numel(), int(window_size), _lib.ptr(idx),
+    _lib.check(lib.ssla_temporal_dropout_index(_lib.ptr(ln), ln.numel(), int(window_size), _lib.ptr(idx), cap_t,
                                                _lib.ptr(kl), _lib.ptr(ws), ws.numel(), st), "temporal_dropout_index")
     (n,) = _counts(ws, 1, st, "temporal_dropout_index", check_bad=False)
+    if n > cap_t:
+        raise ValueError(f"temporal_dropout_index: the lengths keep {n} rows, more than {cap_t} "
+                         f"({total} rows and {ln.numel()} sequences) allow")
     return idx[:n], kl
 
 

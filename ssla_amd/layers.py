@@ -367,7 +367,7 @@ class TemporalDropout(AsyncSparseModule):
 
     def forward(self, inputs, grouped_events=True):
         x = self.prepare_inputs(inputs, grouped_events)
-        idx, kl = E.temporal_dropout_index(x["lengths"], self.window_size)
+        idx, kl = E.temporal_dropout_index(x["lengths"], self.window_size, total=x["events"].shape[0])
         events = E.gather_rows(x["events"], idx)
         time = x["time"][idx]
         return {"events": events, "time": time, "lengths": kl, "batch_id": x["batch_id"], "h": x["h"], "w": x["w"],

@@ -248,3 +248,19 @@ def test_prefix_sums_across_the_one_workgroup_limit(dev, n):
     want_idx, want_kl = OE.temporal_dropout_index(ln, 3)
     assert np.array_equal(kl.cpu().numpy(), want_kl)
     assert np.array_equal(idx.cpu().numpy(), want_idx)
+
+
+def test_temporal_dropout_index_row_total(dev):
+    """With the events' row count given (the path TemporalDropout takes, no
+    read of sum(lengths)) the indices equal the oracle's; lengths that keep
+    more rows than that count and the sequences allow raise ValueError."""
+    from ssla_amd import events as E
+    rng = np.random.default_rng(11)
+    ln = rng.integers(0, 9, size=500)
+    for w in (1, 3, 4):
+        idx, kl = E.temporal_dropout_index(torch.from_numpy(ln).to(dev), w, total=int(ln.sum()))
+        want_idx, want_kl = OE.temporal_dropout_index(ln, w)
+        assert np.array_equal(kl.cpu().numpy(), want_kl)
+        assert np.array_equal(idx.cpu().numpy(), want_idx)
+    with pytest.raises(ValueError, match="more than"):
+        E.temporal_dropout_index(torch.from_numpy(ln).to(dev), 1, total=10)
