@@ -153,7 +153,10 @@ int ssla_gla_chunk_bwd(const void *q, const void *k, const void *v,
  * int32, may be NULL; see ssla_status_read).  This is the batched form of
  * the per-site sparse GLA step over many time bins.
  * Sequences are clamped to [0, T) on the device, so a malformed cu_seqlens
- * cannot address memory outside the tensors.
+ * cannot address memory outside the tensors.  cu_seqlens must be
+ * non-decreasing: with the segmented schedule below, sequences that overlap
+ * can need more segments than the grid holds; the segments past it are not
+ * run and SSLA_ERR_ARG is stored in *status.
  *
  * workspace (optional; NULL, 0 for none): with ssla_gla_recurrent_workspace_size
  * bytes (16-byte aligned, no initialisation needed) long sequences are cut
@@ -224,7 +227,7 @@ int ssla_sparse_gla_step(const int32_t *site_idx, int n_active,
  * ssla_site_project: x fp32 [n, cin]; w bf16 [4 hd, cin] (the rows of Wq,
  *   Wk, Wv, Wg in turn); q, k, v = bf16(bf16(x) W^T) as bf16 [n, hd];
  *   g = logsigmoid(bf16(bf16(x) Wg^T)) / gate_normalizer as fp32 [n, hd].
- *   cin a multiple of 32, hd of 16.
+ *   cin a multiple of 32, hd a multiple of 32.
  * ssla_site_finish: o bf16 [n, hd]; wo bf16 [cout, hd]; x fp32 [n, cin];
  *   wr bf16 [cout, cin] or NULL (then cin == cout);
  *   y = LayerNorm(bf16(o Wo^T) + (bf16(bf16(x) Wr^T) or x)) * ln_w + ln_b

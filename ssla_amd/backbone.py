@@ -251,7 +251,7 @@ class DetectionHead(nn.Module):
         convolutions as one bf16 GEMM, batch norm and SiLU in fp32, the
         predictions as a second GEMM, the decode); otherwise the module's
         bf16 ops run one by one."""
-        if not (fused and xin and xin[0].is_cuda and not torch.is_grad_enabled()):
+        if not (fused and xin and xin[0].is_cuda and not torch.is_grad_enabled() and self._kernel_fits(xin)):
             dt = self.cls_convs[0][0].weight.dtype
             return self._forward_eager([x.to(dt) for x in xin])
         from . import _lib
@@ -271,6 +271,15 @@ class DetectionHead(nn.Module):
         _lib.check(_lib.load().ssla_detect_head(lv, len(grids), B, n_out, width, _lib.ptr(out),
                                                 _lib.stream_of(grids[0])), "ssla_detect_head")
         return out
+
+    def _kernel_fits(self, xin) -> bool:
+        """The sizes ssla_detect_head takes: at most SSLA_HEAD_MAX_LEVELS
+        levels, 5 + classes <= 16 outputs, a branch width that is a multiple
+        of 16 up to 256 and level channels that are multiples of 32; other
+        heads (e.g. 80 classes) run the module's ops one by one."""
+        width = self.cls_convs[0][0].out_channels
+        return (len(xin) <= 4 and 5 + self.num_classes <= 16 and width % 16 == 0 and 0 < width <= 256
+                and all(x.dim() == 4 and int(x.shape[1]) % 32 == 0 for x in xin))
 
     def _fused_params(self):
         """Per level: the two branch convolutions' weights stacked (bf16

@@ -150,9 +150,14 @@ __device__ __forceinline__ int find_seg_seq(const int64_t *off, int n_seq, int64
 }
 
 // segoff[n] = segments of sequences 0..n-1 (segoff[n_seq]: the total).  One
-// workgroup of 256 threads.
+// workgroup of 256 threads.  The grid holds n_segs_max segments, which
+// bounds the total when cu_seqlens is non-decreasing (the sequences then
+// share the T rows); with sequences that overlap the total can exceed it,
+// and the segments past the grid would not run: the total is then capped at
+// n_segs_max and SSLA_ERR_ARG goes to the status word (when one is given).
 __global__ __launch_bounds__(256) void seg_offsets_kernel(const int64_t *__restrict__ cu, int n_seq, int64_t T,
-                                                          int seg_steps, int64_t *__restrict__ segoff) {
+                                                          int seg_steps, int64_t n_segs_max,
+                                                          int64_t *__restrict__ segoff, int32_t *__restrict__ status) {
   __shared__ int64_t ps[256];
   int64_t carry = 0;
   for (int base = 0; base < n_seq; base += 256) {
@@ -171,11 +176,14 @@ __global__ __launch_bounds__(256) void seg_offsets_kernel(const int64_t *__restr
       ps[threadIdx.x] += x;
       __syncthreads();
     }
-    if (n < n_seq) segoff[n] = carry + ps[threadIdx.x] - c;
+    if (n < n_seq) segoff[n] = min(carry + ps[threadIdx.x] - c, n_segs_max);
     carry += ps[255];
     __syncthreads();
   }
-  if (threadIdx.x == 0) segoff[n_seq] = carry;
+  if (threadIdx.x == 0) {
+    segoff[n_seq] = min(carry, n_segs_max);
+    if (carry > n_segs_max && status != nullptr) *status = SSLA_ERR_ARG;
+  }
 }
 
 // f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile
@@ -668,8 +676,8 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
       sw.n_segs_max = L.n_segs_max;
       sw.seg_steps = L.seg_steps;
       sgrid = dim3(static_cast<unsigned>((L.n_segs_max * H * n_vt + waves_per_block - 1) / waves_per_block));
-      hipLaunchKernelGGL(seg_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T, L.seg_steps,
-                         reinterpret_cast<int64_t *>(w + L.segoff));
+      hipLaunchKernelGGL(seg_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T, L.seg_steps, L.n_segs_max,
+                         reinterpret_cast<int64_t *>(w + L.segoff), status);
     }
 #define SSLA_RECS(KPL_)                                                                                     \
   if (segmented) {                                                                                          \

@@ -28,8 +28,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["chunk_gla", "ChunkGLAFunction", "fused_recurrent_gla", "naive_gla_recurrent", "chunk_kernel_supports",
-           "chunk_backward_supports"]
+__all__ = ["chunk_gla", "ChunkGLAFunction", "fused_recurrent_gla", "fused_recurrent_gla_rows", "naive_gla_recurrent",
+           "chunk_kernel_supports", "chunk_backward_supports"]
 
 
 KD = 64   # keys of one chunk-kernel call
@@ -262,9 +262,11 @@ def fused_recurrent_gla(
     ``S_t = exp(g_t) * S_{t-1} + k_t v_t^T``, ``o_t = (scale q_t) . S_t``;
     o has q's dtype, the final state is fp32.  As the reference concatenates
     the outputs of its sequences (naive.py:106), o holds the rows
-    ``cu_seqlens[0]:cu_seqlens[-1]`` (all T rows when the sequences cover
-    the batch, the usual case; reading the two bounds is one host sync
-    otherwise, as the reference's ``.item()`` calls are)."""
+    ``cu_seqlens[0]:cu_seqlens[-1]``.  Finding them reads the two bounds
+    back, one host sync per call (as the reference's ``.item()`` calls do),
+    unless ``cu_seqlens`` is a CPU tensor; :func:`fused_recurrent_gla_rows`
+    makes no sync and returns all T rows (for callers whose sequences cover
+    the batch, e.g. under HIP graph capture)."""
     if scale is None:
         scale = q.shape[-1] ** -0.5
     q, k, v, g, cu, h0 = _prep("fused_recurrent_gla", q, k, v, g, cu_seqlens, initial_state)
@@ -281,6 +283,33 @@ def fused_recurrent_gla(
     if (lo, hi) != (0, T):
         o = o[lo:hi]
     return o, ht
+
+
+def fused_recurrent_gla_rows(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    cu_seqlens: torch.LongTensor,
+    scale: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+    output_final_state: bool = False,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """:func:`fused_recurrent_gla` without the host sync: o has all T rows
+    (rows outside every sequence are unspecified), so nothing is read back
+    and the call can be captured in a HIP graph."""
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    q, k, v, g, cu, h0 = _prep("fused_recurrent_gla", q, k, v, g, cu_seqlens, initial_state)
+    T, H, K = q.shape
+    V = v.shape[-1]
+    N = cu.numel() - 1
+    if h0 is not None and h0.shape != (N, H, K, V):
+        raise ValueError(f"fused_recurrent_gla: initial_state must be {(N, H, K, V)}, "
+                         f"got {tuple(h0.shape)}")
+    o = torch.empty(T, H, V, device=q.device, dtype=q.dtype)
+    ht = torch.empty(N, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
+    return _recurrent(q, k, v, g, cu, float(scale), h0, o, ht, None, 0)
 
 
 naive_gla_recurrent = fused_recurrent_gla

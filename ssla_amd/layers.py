@@ -201,6 +201,26 @@ class MosAttention(nn.Module):
         return {"events": out, "time": inputs["time"], "w": inputs["w"], "h": inputs["h"],
                 "batch_id": inputs["batch_id"], "lengths": lengths, "batch_size": inputs["batch_size"]}
 
+    def compute_flops(self, inputs):
+        """Analytic flop count of one forward on these inputs, term for term
+        the reference's (layers/mos_attention.py:169-199): every pixel event
+        is counted once per kernel position (k_h * k_w patch copies)."""
+        n_group = int(inputs["events"].shape[0])
+        n_patch = n_group * self.kernel_size[0] * self.kernel_size[1]
+        hs, ins = self.hidden_size, self.input_size
+        flops = n_patch * hs * (2 * ins - 1)            # scatter projection
+        flops += 3 * n_patch * hs * (2 * hs - 1)        # q, v, g
+        flops += n_patch * hs * 4                       # sigmoid
+        flops += n_patch * hs * 2                       # h = g * h + u
+        flops += n_patch * hs                           # q * h
+        flops += n_patch * hs * (2 * hs - 1)            # output projection
+        flops += n_patch * hs * (2 * hs - 1)            # gather projection
+        flops += n_patch * hs                           # gather back (index_add)
+        flops += n_group * hs * (2 * ins - 1) if self.input_proj is not None else 0
+        flops += n_group * hs                           # residual
+        flops += n_group * (8 * hs + 1)                 # layer norm
+        return flops
+
 
 class LinearAttention(nn.Module):
     """Per-sample linear attention over events ordered by time; reference
@@ -254,6 +274,25 @@ class LinearAttention(nn.Module):
         return {"events": out, "time": gr_time, "w": inputs["w"], "h": inputs["h"], "batch_id": gr_b,
                 "lengths": gr_len, "batch_size": B}
 
+    def compute_flops(self, inputs):
+        """Analytic flop count of one forward, with the terms of the
+        reference (layers/linear_attention.py:105-124).  The reference
+        method names two counts it never defines (``num_patch_events``,
+        ``num_group_events``) and raises NameError; here both are the event
+        count, since this layer scans every event once."""
+        n = int(inputs["events"].shape[0])
+        hs, ins = self.hidden_size, self.input_size
+        flops = 3 * n * hs * (2 * hs - 1)               # q, v, g
+        flops += n * hs * 4                             # sigmoid
+        flops += n * hs * 2                             # h = g * h + u
+        flops += n * hs                                 # q * h
+        flops += n * hs * (2 * hs - 1)                  # output projection
+        flops += n * hs * (2 * ins - 1) if self.input_proj is not None else 0
+        flops += n * hs * (2 * ins - 1) if self.residual_proj is not None else 0
+        flops += n * hs                                 # residual
+        flops += n * (8 * hs + 1)                       # layer norm
+        return flops
+
 
 # ------------------------------------------------------------------ pooling --
 class AsyncSparseModule(nn.Module):
@@ -292,6 +331,8 @@ class AsyncSparseModule(nn.Module):
         return E.gather_receptive_fields(inputs, self.frame_size, self.rf2pixel_lut, self.rf_outcoord)
 
     def compute_flops(self, inputs, grouped_events=True):
+        """Modules without a flop cost of their own count 0, as the
+        reference's fallback does (layers/async_sparse_module.py:44-46)."""
         return 0
 
 
@@ -318,6 +359,15 @@ class SparsePool(AsyncSparseModule):
         return {"events": new_events, "time": seg_time, "lengths": new_len, "batch_id": x["batch_id"],
                 "h": x["h"], "w": x["w"], "batch_size": x["batch_size"]}
 
+    def compute_flops(self, inputs, grouped_events=True, elementwise_agg_flops=0):
+        """Flops of the aggregation (reference layers/sparse_pooling.py:53-70):
+        every receptive-field event that joins another one of the same field
+        and time costs ``elementwise_agg_flops`` per channel."""
+        x = self.prepare_inputs(inputs, grouped_events)
+        _seg, seg_time, _len = E.pool_segments(x["time"], x["lengths"])
+        agg_n = int(x["time"].numel()) - int(seg_time.numel())
+        return agg_n * int(x["events"].shape[-1]) * elementwise_agg_flops
+
     def _one_call(self, inputs) -> bool:
         """The two-call pooling (ssla_sparse_pool_plan / _emit) takes grouped
         fp32 device events with no gradient to record and a receptive field
@@ -333,10 +383,18 @@ class SparseMaxPool(SparsePool):
     def __init__(self, *args, **kwargs):
         super().__init__(scatter_max, *args, **kwargs)
 
+    def compute_flops(self, inputs, grouped_events=True):
+        """One compare per aggregated channel (reference sparse_pooling.py:78-79)."""
+        return super().compute_flops(inputs, grouped_events=grouped_events, elementwise_agg_flops=1)
+
 
 class SparseAvgPool(SparsePool):
     def __init__(self, *args, **kwargs):
         super().__init__(scatter_mean, *args, **kwargs)
+
+    def compute_flops(self, inputs, grouped_events=True):
+        """An add and a divide per aggregated channel (reference sparse_pooling.py:86-87)."""
+        return super().compute_flops(inputs, grouped_events=grouped_events, elementwise_agg_flops=2)
 
 
 class SparseAdaptiveMaxPool(SparseMaxPool):

@@ -57,31 +57,38 @@ class SequentialScan(torch.autograd.Function):
 
 
 def scan(u: torch.Tensor, g: torch.Tensor, cu_seqlens: torch.Tensor) -> torch.Tensor:
-    """Varlen diagonal scan; u, g fp32 ``[T, C]`` -> h ``[T, C]`` (rows in no
-    sequence are zero, as with the reference's ``zeros_like``).  Differentiable
-    in u and g (``ssla_diag_scan_bwd``)."""
+    """Varlen diagonal scan; u, g ``[T, C]`` -> h ``[T, C]`` in u's dtype
+    (reference ops/common/scan.py:101, ``torch.zeros_like(u)``; rows in no
+    sequence are zero).  The running state is fp32 and each stored row is
+    rounded once to u's dtype, as the reference kernel's fp32 ``b_h`` is
+    (scan.py:35-43).  Differentiable in u and g (``ssla_diag_scan_bwd``)."""
     if u.dim() != 2 or u.shape != g.shape:
         raise ValueError(f"scan: u and g must both be [T, C], got {tuple(u.shape)}, {tuple(g.shape)}")
     dev = _lib.require_cuda(u, g)
+    out_dtype = u.dtype
     u = u.to(torch.float32).contiguous()
     g = g.to(torch.float32).contiguous()
     cu = cu_seqlens.to(device=dev, dtype=torch.int64).contiguous()
     if torch.is_grad_enabled() and (u.requires_grad or g.requires_grad):
-        return SequentialScan.apply(u, g, cu)
-    return _scan_fwd(u, g, cu)
+        h = SequentialScan.apply(u, g, cu)
+    else:
+        h = _scan_fwd(u, g, cu)
+    return h if out_dtype == torch.float32 else h.to(out_dtype)
 
 
 def sparse_gla_step(site_idx: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     g: torch.Tensor, state: torch.Tensor, scale: Optional[float] = None,
-                    check: bool = True) -> torch.Tensor:
+                    check: bool = False) -> torch.Tensor:
     """Update ``state[site_idx]`` in place for one time bin and return o.
 
     site_idx: int32 ``[n]`` (strictly increasing, inside ``[0, n_sites)``);
     q, k, g: fp32 ``[n, H, K]``; v: fp32 ``[n, H, V]``; state: fp32
     ``[n_sites, H, K, V]``.  Rows of inactive sites are neither read nor
     written.  An entry out of range or not above the one before it is
-    skipped (its o rows are zero, no state changes); with ``check`` (one host
-    sync) that raises ValueError after the call.
+    skipped (its o rows are zero, no state changes).  ``check=True`` reads
+    the status word back after the call (one host sync) and raises
+    ValueError for such an entry; the default makes no host sync, so a
+    caller stepping through many bins pays none.
     """
     n, H, K = q.shape
     V = v.shape[-1]
@@ -113,14 +120,14 @@ def sparse_gla_step(site_idx: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v:
 
 def sparse_gla_scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
                     cu_seqlens: torch.Tensor, seq_site: torch.Tensor, state: torch.Tensor,
-                    scale: Optional[float] = None, check: bool = True) -> torch.Tensor:
+                    scale: Optional[float] = None, check: bool = False) -> torch.Tensor:
     """Many bins at once: sequence n (rows ``cu_seqlens[n]:cu_seqlens[n+1]``,
     ordered in time) is the history of site ``seq_site[n]``; its state row
     is read from and written back to ``state`` in place.  Returns o with
     q's dtype.  ``seq_site`` must be strictly increasing and inside
     ``[0, n_sites)``; a sequence whose entry is not is skipped (zero o rows,
-    state untouched) and, with ``check`` (one host sync), ValueError is
-    raised after the call."""
+    state untouched); ``check=True`` reads the status back after the call
+    (one host sync) and raises ValueError for such a sequence."""
     T, H, K = q.shape
     V = v.shape[-1]
     if state.dim() != 4 or state.shape[1:] != (H, K, V) or state.dtype != torch.float32 \

@@ -148,6 +148,29 @@ def test_async_step_windows_vs_oracle(dev):
             assert torch.equal(states_fwd[i], states[i]), f"forward() states differ (stage {i}, window {w})"
 
 
+def test_async_step_full_window_vs_oracle(dev):
+    """Config 5 at full size: two consecutive 50k-event windows, every piece
+    against the oracle on the GPU's own input to it (the same checks as the
+    5k-event windows), states carried, and forward() == the piecewise run."""
+    import oracle.events  # noqa: F401
+    from ssla_amd import synthetic
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(3)
+    model = AsyncSparseGLA().to(dev)
+    params = _params(model)
+    states = model.init_states(1, dev)
+    for w, ev in enumerate(synthetic.async_windows(2, 50_000, seed=4)):
+        ln = torch.tensor([ev.shape[1]])
+        print(f"async step full window {w}: {ev.shape[1]} events", flush=True)
+        states_fwd = [s.clone() for s in states]
+        out, _ = _window_piecewise(model, ev, ln, states, params, dev, tag=f" full w{w}")
+        with torch.no_grad():
+            out_f, _ = model(ev.to(dev), ln.to(dev), states_fwd)
+        assert torch.equal(out_f, out), f"forward() differs from the piecewise run in full window {w}"
+        for i in range(4):
+            assert torch.equal(states_fwd[i], states[i]), f"forward() states differ (stage {i}, full window {w})"
+
+
 def test_async_step_full_size_properties(dev):
     """Four windows of 50k events at full size: head output [1, 1505, 7]
     and finite, every state row either unchanged (inactive site) or
@@ -215,6 +238,25 @@ def test_head_kernel_matches_module(dev):
         assert_close(_np(got), _np(eager), 0.0, f"head kernel vs module rep {rep}", band=0.05, ratio_max=7e-3)
 
 
+def test_head_outside_kernel_sizes_runs_module(dev):
+    """A head the kernel does not take (80 classes: 85 outputs) runs the
+    module's ops instead of raising, with the oracle's decode."""
+    from ssla_amd.backbone import DetectionHead
+    torch.manual_seed(5)
+    head = DetectionHead(80, (8, 16), (64, 128), 64).to(dev).to(torch.bfloat16).eval()
+    gen = torch.Generator(device=dev).manual_seed(2)
+    xin = [torch.randn(1, 64, 6, 8, device=dev, generator=gen), torch.randn(1, 128, 3, 4, device=dev, generator=gen)]
+    print("head with 80 classes", flush=True)
+    with torch.no_grad():
+        got = head(xin)
+        eager = head(xin, fused=False)
+    assert got.shape == (1, 6 * 8 + 3 * 4, 85)
+    assert torch.equal(got, eager)
+    hp = {k: v.detach().float().cpu().numpy() for k, v in head.state_dict().items()}
+    ref = ob.head(hp, [_np(x) for x in xin], (8, 16))
+    assert_close(_np(got), ref, 2 ** -7, "80-class head vs oracle", band=0.05, ratio_max=1e-2)
+
+
 def test_site_block_kernels_match_torch(dev):
     """ssla_site_project / ssla_site_finish against the same block run as
     torch's bf16 F.linear calls (the rounding points the kernels follow) for
@@ -277,5 +319,13 @@ def test_site_block_one_call_checks(dev):
     s3 = st0.clone()
     with torch.no_grad(), pytest.raises(ValueError):
         blk(bad, s3, grid, check=True)
+    # the bad sequence (index 5) is skipped: the cell it originally named is
+    # untouched, its repeated cell holds sequence 4's update only, and every
+    # other row is what the good call wrote
+    c5 = int(cells[5])
+    assert torch.equal(s3[c5], st0[c5]), "the skipped sequence's original cell changed"
+    keep = torch.ones(st0.shape[0], dtype=torch.bool, device=dev)
+    keep[c5] = False
+    assert torch.equal(s3[keep], s1[keep]), "rows of the valid sequences differ from the good call"
     with torch.no_grad(), pytest.raises(ValueError):
         blk(x, st0[:, :, :16].contiguous(), grid)

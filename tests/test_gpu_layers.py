@@ -191,3 +191,26 @@ def test_pool_from_ungrouped_events(efx):
     want = OE.sparse_pool(OE.gather_receptive_fields(gr, frame, lut, outc), "max")
     np.testing.assert_array_equal(r["events"].cpu().numpy(), want["events"])
     np.testing.assert_array_equal(r["time"].cpu().numpy(), want["time"])
+
+
+@pytest.mark.parametrize("kind", ["max", "mean"])
+@pytest.mark.parametrize("k,s", [((2, 2), None), ((3, 3), (2, 2))])
+def test_sparse_pool_compute_flops(efx, kind, k, s):
+    """SparseMaxPool / SparseAvgPool.compute_flops (reference
+    layers/sparse_pooling.py:53-87): the receptive-field events that join an
+    earlier event of the same field and time, times the channels, times 1
+    (max) or 2 (mean); the count is taken from the oracle's field gather."""
+    from ssla_amd.layers import SparseMaxPool, SparseAvgPool
+    frame = tuple(int(v) for v in efx["ge_frame"])
+    cls = SparseMaxPool if kind == "max" else SparseAvgPool
+    layer = cls(frame, kernel_size=k, stride=s).cuda()
+    d, gr = _grouped_dev(efx)
+    gr["events"] = efx["sp_pix_events"]
+    lut, outc = OE.rf2pixels(frame, k, s or k)
+    rf = OE.gather_receptive_fields(gr, frame, lut, outc)
+    field = np.repeat(np.arange(len(rf["lengths"])), rf["lengths"])
+    t = np.asarray(rf["time"])
+    joins = int(np.sum((field[1:] == field[:-1]) & (t[1:] == t[:-1])))
+    C = efx["sp_pix_events"].shape[1]
+    print(f"pool compute_flops {kind} k={k}", flush=True)
+    assert layer.compute_flops(d) == joins * C * (1 if kind == "max" else 2)

@@ -84,14 +84,17 @@ def test_scan_layer_shapes(dev):
 
 
 def test_sparse_step_c3_bins(dev):
-    """Config 3 (C3: 76x60 sites, H=4, D=32), first 16 bins: o and all
-    states checked after every bin; inactive states bit-identical."""
+    """Config 3 (C3: 76x60 sites, H=4, D=32) at full size, all 64 bins: o
+    checked after every bin against the oracle, inactive states
+    bit-identical in every bin, all states against the oracle at the end."""
     from ssla_amd import synthetic
     from ssla_amd.scan import sparse_gla_step
-    sb = synthetic.sparse_scan_bins(n_bins=16)
+    sb = synthetic.sparse_scan_bins()
+    assert len(sb.sites) == 64
     st_gpu = sb.state0.clone().to(dev)
     st_ref = sb.state0.numpy().copy()
-    for b in range(16):
+    print("C3 per-bin steps, 64 bins", flush=True)
+    for b in range(64):
         sites = sb.sites[b]
         prev = st_gpu.clone()
         with torch.no_grad():
@@ -104,6 +107,36 @@ def test_sparse_step_c3_bins(dev):
         inact = torch.from_numpy(inactive).to(dev)
         assert torch.equal(st_gpu[inact], prev[inact]), f"inactive states changed in bin {b}"
     assert_close(st_gpu.cpu().numpy(), st_ref, 1e-4, "states")
+
+
+def test_sparse_scan_c3_full_vs_oracle(dev):
+    """Config 3 at full size through the one-call path (all 64 bins as one
+    ssla_gla_recurrent_fwd with state_idx, the bench's batched line): the
+    rows regrouped by site (stable in time), o and the updated states
+    against the oracle recurrence from each site's stored state, and every
+    state row of a site that was never active bit-identical."""
+    from ssla_amd import synthetic
+    from ssla_amd.scan import sparse_gla_scan
+    sb = synthetic.sparse_scan_bins()
+    site_all = np.concatenate(sb.sites)
+    order = np.argsort(site_all, kind="stable")
+    uniq, counts = np.unique(site_all[order], return_counts=True)
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    cat = lambda xs: torch.cat(xs)[torch.from_numpy(order)]   # noqa: E731
+    q, k, v, g = cat(sb.q), cat(sb.k), cat(sb.v), cat(sb.g)
+    st = sb.state0.clone().to(dev)
+    print(f"C3 one call: {len(uniq)} sites, {int(cu[-1])} site-steps", flush=True)
+    with torch.no_grad():
+        o = sparse_gla_scan(q.to(dev), k.to(dev), v.to(dev), g.to(dev), torch.from_numpy(cu).to(dev),
+                            torch.from_numpy(uniq.astype(np.int32)).to(dev), st, scale=sb.scale, check=True)
+    ro, rht = oracle.gla_recurrent(q.numpy(), k.numpy(), v.numpy(), g.numpy(), cu, sb.scale,
+                                   sb.state0.numpy()[uniq], True)
+    assert_close(o.cpu().numpy(), ro, 1e-4, "o (one call, 64 bins)")
+    st = st.cpu()
+    assert_close(st.numpy()[uniq], rht, 1e-4, "states of the active sites")
+    never = np.setdiff1d(np.arange(sb.n_sites), uniq)
+    assert torch.equal(st[torch.from_numpy(never)], sb.state0[torch.from_numpy(never)]), \
+        "states of sites never active changed"
 
 
 def test_sparse_scan_matches_steps(dev):
@@ -196,7 +229,7 @@ def test_sparse_step_rejects_bad_site_lists(dev):
     st = state0.clone().to(dev)
     print("sparse step: bad site list through the wrapper", flush=True)
     with torch.no_grad(), pytest.raises(ValueError, match="strictly increasing"):
-        sparse_gla_step(torch.from_numpy(sites).to(dev), q.to(dev), k.to(dev), v.to(dev), g.to(dev), st)
+        sparse_gla_step(torch.from_numpy(sites).to(dev), q.to(dev), k.to(dev), v.to(dev), g.to(dev), st, check=True)
     # the same call through the C-ABI: status word, zero rows, state effects
     lib = _lib.load()
     st = state0.clone().to(dev)
@@ -234,7 +267,7 @@ def test_sparse_scan_rejects_bad_site_lists(dev):
     state0 = (torch.randn(n_sites, H, K, V, generator=gen) * 0.1).to(dev)
     print("sparse scan: repeated site", flush=True)
     with torch.no_grad(), pytest.raises(ValueError, match="strictly increasing"):
-        sparse_gla_scan(q, k, v, g, cu, torch.tensor([4, 9, 9], device=dev), state0.clone())
+        sparse_gla_scan(q, k, v, g, cu, torch.tensor([4, 9, 9], device=dev), state0.clone(), check=True)
     st = state0.clone()
     o = torch.full((T, H, V), float("nan"), device=dev)
     status = _lib.new_status(dev)
@@ -246,6 +279,44 @@ def test_sparse_scan_rejects_bad_site_lists(dev):
     assert torch.isfinite(o[:5]).all()
     untouched = [i for i in range(n_sites) if i not in (4, 9)]
     assert torch.equal(st[untouched], state0[untouched])
+
+
+@pytest.mark.parametrize("bad", ["repeat", "range"])
+def test_sparse_scan_rejects_bad_site_lists_segmented(dev, bad):
+    """The segmented schedule (long histories: the workspace query is
+    non-zero) with a repeated or out-of-range site: SSLA_ERR_ARG in the
+    status word, every o row of the bad sequence's segments zero, the states
+    of the bad entry untouched, and the valid sequences against the
+    oracle."""
+    from ssla_amd import _lib
+    from ssla_amd.gla import _recurrent
+    gen = torch.Generator().manual_seed(33)
+    H, K, V, n_sites = 2, 32, 32, 12
+    lens = [700, 300, 1000]
+    sites = [2, 5, 5] if bad == "repeat" else [2, 5, 40]
+    T = sum(lens)
+    assert _lib.load().ssla_gla_recurrent_workspace_size(len(lens), T, H, K, V) > 0
+    q, k, v = (torch.randn(T, H, D, generator=gen) for D in (K, K, V))
+    g = F.logsigmoid(torch.randn(T, H, K, generator=gen) / 4)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64)
+    state0 = torch.randn(n_sites, H, K, V, generator=gen) * 0.1
+    st = state0.clone().to(dev)
+    o = torch.full((T, H, V), float("nan"), device=dev)
+    status = _lib.new_status(dev)
+    print(f"sparse scan segmented, bad site list ({bad})", flush=True)
+    with torch.no_grad():
+        _recurrent(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev), K ** -0.5, st, o, st,
+                   torch.tensor(sites, device=dev, dtype=torch.int32), n_sites, status)
+    assert _lib.read_status(status) == _lib.SSLA_ERR_ARG
+    o = o.cpu()
+    assert torch.equal(o[1000:], torch.zeros(1000, H, V)), "o rows of the bad sequence must be zero"
+    ro, rht = oracle.gla_recurrent(q.numpy()[:1000], k.numpy()[:1000], v.numpy()[:1000], g.numpy()[:1000],
+                                   np.array([0, 700, 1000]), K ** -0.5, state0.numpy()[[2, 5]], True)
+    assert_close(o.numpy()[:1000], ro, 1e-4, "o of the valid sequences")
+    st = st.cpu()
+    assert_close(st.numpy()[[2, 5]], rht, 1e-4, "states of the valid sequences")
+    others = [i for i in range(n_sites) if i not in (2, 5)]
+    assert torch.equal(st[others], state0[others]), "rows outside the valid sequences changed"
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -287,3 +358,26 @@ def test_sparse_scan_long_sequences_in_place(dev, dtype):
         o2 = sparse_gla_scan(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev),
                              torch.tensor(sites, dtype=torch.int32, device=dev), st2, scale=K ** -0.5)
     assert torch.equal(o2, o) and torch.equal(st2, st), "segmented scan not repeatable"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_scan_returns_input_dtype(dev, dtype):
+    """scan returns h in u's dtype (reference ops/common/scan.py:101,
+    ``zeros_like(u)``): the fp32 running state rounded once per stored row,
+    so the result equals the fp32 scan of the same inputs rounded to u's
+    dtype, bit for bit; the gradients come back in the inputs' dtypes."""
+    from ssla_amd.scan import scan
+    gen = torch.Generator().manual_seed(71)
+    lens = [5, 0, 40, 7]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=dev)
+    T, C = sum(lens), 24
+    u = torch.randn(T, C, generator=gen).to(dtype).to(dev)
+    g = torch.sigmoid(torch.randn(T, C, generator=gen)).to(dtype).to(dev)
+    with torch.no_grad():
+        h = scan(u, g, cu)
+        h32 = scan(u.float(), g.float(), cu)
+    assert h.dtype == dtype
+    assert torch.equal(h, h32.to(dtype))
+    ud, gd = u.clone().requires_grad_(), g.clone().requires_grad_()
+    scan(ud, gd, cu).float().sum().backward()
+    assert ud.grad.dtype == dtype and gd.grad.dtype == dtype

@@ -74,3 +74,44 @@ def test_layers_refuse_cpu_tensors(fx):
     with pytest.raises(Exception, match="(?i)cuda|device|gpu"):
         with torch.no_grad():
             layer(inp)
+
+
+@pytest.mark.parametrize("ins,hs,k", [(2, 12, (3, 3)), (12, 12, (1, 1)), (24, 48, (3, 3)), (48, 48, (5, 3))])
+def test_mos_attention_compute_flops(ins, hs, k):
+    """MosAttention.compute_flops (reference layers/mos_attention.py:169-199)
+    against the count collected per event: each of the n * kh * kw patch
+    copies costs hs (2 ins + 10 hs + 2) flops, each pixel event hs (9) + 1
+    more, plus hs (2 ins - 1) for the input projection when ins != hs."""
+    import torch
+    from ssla_amd.layers import MosAttention
+    layer = MosAttention(ins, hs, (16, 20), k)
+    n = 137
+    x = {"events": torch.zeros(n, ins)}
+    want = n * k[0] * k[1] * hs * (2 * ins + 10 * hs + 2) + n * (9 * hs + 1)
+    if ins != hs:
+        want += n * hs * (2 * ins - 1)
+    assert layer.compute_flops(x) == want
+
+
+@pytest.mark.parametrize("ins,hs", [(2, 12), (24, 24)])
+def test_linear_attention_compute_flops(ins, hs):
+    """LinearAttention.compute_flops (terms of reference
+    layers/linear_attention.py:105-124, one scan row per event), collected
+    per event: hs (8 hs + 3) for q, v, g, the gates, the scan, q * h and the
+    output projection, hs for the residual and 8 hs + 1 for the norm, plus
+    2 hs (2 ins - 1) for the input and residual projections when ins != hs."""
+    import torch
+    from ssla_amd.layers import LinearAttention
+    layer = LinearAttention(ins, hs, (16, 20))
+    n = 53
+    want = n * (hs * (8 * hs + 3) + hs + 8 * hs + 1)
+    if ins != hs:
+        want += 2 * n * hs * (2 * ins - 1)
+    assert layer.compute_flops({"events": torch.zeros(n, ins)}) == want
+
+
+def test_async_module_compute_flops_fallback():
+    """TemporalDropout and other modules without a cost of their own count 0
+    (reference layers/async_sparse_module.py:44-46)."""
+    from ssla_amd.layers import TemporalDropout
+    assert TemporalDropout(4, (16, 20)).compute_flops({}) == 0

@@ -409,3 +409,46 @@ def test_gla_bwd_dg_identity_and_finite_differences():
         return float((o * dout).sum() + (s * dht).sum())
     fd = (loss(g + eps * d) - loss(g - eps * d)) / (2 * eps)
     assert abs(fd - float((dg * d).sum())) < 2e-3 * (1 + abs(fd))
+
+
+def test_chunk_rounding_emulation_pinned():
+    """oracle.chunk_ref (the reference's chunk pipeline with its rounding
+    points) pinned two ways: with every rounding dropped it equals the fp64
+    recurrence to fp32 precision on ragged sequences with chunk remainders
+    and an initial state (so its chunk algebra -- sub-chunk A with the
+    re-centred decays, the diagonal blocks, the entering states, the state
+    update -- is right); with the roundings on, its error is that of bf16
+    operands (an RMS ratio of a few 1e-3, and not zero), and its o values are
+    bf16 values."""
+    from oracle import chunk_ref
+    rng = np.random.default_rng(5)
+    lens = [70, 1, 64, 130, 17]
+    T, H, K, V = sum(lens), 2, 32, 48
+    q = (rng.standard_normal((T, H, K)) * K ** -0.5).astype(np.float32)
+    k = rng.standard_normal((T, H, K)).astype(np.float32)
+    v = rng.standard_normal((T, H, V)).astype(np.float32)
+    g = np.log(1 / (1 + np.exp(-rng.standard_normal((T, H, K)) / 2))).astype(np.float32)   # logsigmoid
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    h0 = (rng.standard_normal((len(lens), H, K, V)) * 0.1).astype(np.float32)
+    qb, kb, vb = (chunk_ref.bf16(x) for x in (q, k, v))
+    ro, rht = oracle.gla_recurrent(qb, kb, vb, g, cu, 1.0, h0, True)
+    eo, eht = chunk_ref.chunk_gla(qb, kb, vb, g, cu, 1.0, h0, exact=True)
+    np.testing.assert_allclose(eo, ro, rtol=2e-4, atol=2e-4 * np.sqrt(np.mean(ro ** 2)))
+    np.testing.assert_allclose(eht, rht, rtol=2e-4, atol=2e-4 * np.sqrt(np.mean(rht ** 2)))
+    bo, bht = chunk_ref.chunk_gla(q, k, v, g, cu, 1.0, h0)
+    ratio = np.sqrt(np.mean((bo - ro) ** 2) / np.mean(ro ** 2))
+    assert 1e-4 < ratio < 1e-2, ratio
+    assert np.array_equal(chunk_ref.bf16(bo), bo)
+    # a planted mistake in the emulation (the state entering a chunk taken
+    # after the chunk's update) is caught by the exact comparison
+    bad = chunk_ref._chunk
+    try:
+        def swapped(q_, k_, v_, G_, S_, scale_, rb, rt):
+            _, S2 = bad(q_, k_, v_, G_, S_, scale_, rb, rt)
+            o2, _ = bad(q_, k_, v_, G_, S2, scale_, rb, rt)
+            return o2, S2
+        chunk_ref._chunk = swapped
+        wo, _ = chunk_ref.chunk_gla(qb, kb, vb, g, cu, 1.0, h0, exact=True)
+    finally:
+        chunk_ref._chunk = bad
+    assert not np.allclose(wo, ro, rtol=2e-4, atol=2e-4 * np.sqrt(np.mean(ro ** 2)))
