@@ -611,8 +611,16 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
     // q~ = q 2^(G - M), k~ = k 2^(M - G) with G relative to the block start
     // (G2 - (M - E_I-1) = G_abs - M); q0 = q~ 2^M, k^ = k~ 2^(G_last - M),
     // kt = k~ 2^(E_I - M).  One K=32 half at a time keeps few registers live.
-    QK::Vec qd[2], kd[2];   // diagonal-block operands (bf16)
+    QK::Vec qd[2];          // q~ in the input dtype (diagonal and, rescaled, off-diagonal blocks)
     MV q0b[2];
+    // Diagonal block of A, with q~ and k~ each split into a hi and a lo part
+    // in the input dtype (x = hi + lo to ~2^-16): A_II = hi.hi + lo.hi +
+    // hi.lo.  Its entries are the chunk's largest (undecayed), and a single
+    // bf16 rounding of both operands left o's RMS error at 3.3e-3 of its RMS
+    // against 2.35e-3 for the reference's fp32 diagonal sub-chunks
+    // (ops/gla/chunk.py:112-176) on the same inputs; with the split the two
+    // agree.  Off-diagonal blocks are decayed and stay single products.
+    f32x4 dg = (f32x4){0.f, 0.f, 0.f, 0.f};
     auto operand_half = [&](const int jj) {
       const f32x8 half = *reinterpret_cast<const f32x8 *>(&sm.fac[wv][kFacHalf][32 * jj + kq]);
       const f32x8 qf = M::widen(from_bits<MV>(cur.q[jj]));
@@ -626,7 +634,12 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
       }
       const f32x8 qt = qf * eq, kt = kf * ek;
       qd[jj] = QK::cvt(qt);
-      kd[jj] = QK::cvt(kt);
+      const QK::Vec kd = QK::cvt(kt);
+      const QK::Vec ql = QK::cvt(qt - QK::widen(qd[jj]));
+      const QK::Vec kl = QK::cvt(kt - QK::widen(kd));
+      dg = QK::mma(kd, qd[jj], dg);
+      dg = QK::mma(kl, qd[jj], dg);
+      dg = QK::mma(kd, ql, dg);
       q0b[jj] = M::cvt(qt * *reinterpret_cast<const f32x8 *>(&sm.fac[wv][kFacQ0][32 * jj + kq]));
       tile_store8(sm.kh, row, 32 * jj + kq,
                   to_bits(M::cvt(kt * *reinterpret_cast<const f32x8 *>(&sm.fac[wv][kFacKh][32 * jj + kq]))));
@@ -656,9 +669,6 @@ __device__ __forceinline__ void segment_loop(SmemA &sm, const ChunkArgs &a, cons
       }
     }
     {
-      f32x4 dg = (f32x4){0.f, 0.f, 0.f, 0.f};
-      dg = QK::mma(kd[0], qd[0], dg);
-      dg = QK::mma(kd[1], qd[1], dg);
       // causal mask on the diagonal block (row i = r, column j = 4gq + ii)
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)

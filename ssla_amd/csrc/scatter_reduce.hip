@@ -4,86 +4,99 @@
 // un-vendored dependency, so the semantics implemented are its documented
 // ones: empty rows give 0 (max: argmax = E), mean = sum / max(count, 1)).
 //
-// Pipeline (all on the caller's stream, no host synchronisation, no memset):
-//   sorted index:    seg_reduce -> seg_fixup
-//   unsorted index:  hist -> scan -> bucket -> seg_reduce -> seg_fixup
-// * hist   : each workgroup counts the rows of a contiguous event range in an
-//            LDS histogram (LDS-privatised atomics; no contended global
-//            atomics) and writes it as one row of a [n_hist, n_out] matrix.
-// * scan   : one thread per output row sums its matrix column (turning the
-//            column into per-workgroup start offsets), then a single-pass
-//            chained scan (decoupled look-back over dynamically numbered
-//            workgroups) gives the row offsets `off`.
-// * bucket : each workgroup re-reads its event range and places (event id,
-//            row) pairs at their row-grouped positions with LDS atomics on
-//            its own start offsets (one 8-byte store per event).
-// * seg_reduce: one wavefront per tile of 64 consecutive positions (events
-//            of a sorted index, or counting-sort positions) and block of 64
-//            channels: the tile's rows are loaded into registers (lane =
-//            channel, one coalesced row per load, all in flight at once),
-//            then walked in order; rows inside the tile are written, rows
-//            crossing the tile's edges leave pieces and a flag; empty rows
-//            are written as such.  It also checks a sorted index for range
-//            and order.
-// * seg_fixup: one wavefront per 8 tiles loads their flags and pieces in one
-//            batch, folds each crossing row's pieces in tile order and
-//            writes the row.
-// Max/argmax use an explicit (value, smallest event id) comparison (NaN
-// never wins), so the result does not depend on the order in which events
-// are visited: it is bit-exact and deterministic.  Mean sums in fp64 and
-// rounds once (the unsorted path's fp64 sum order follows the LDS-atomic
-// placement, so its last fp64 bits may vary between runs).
+// Two pipelines, all on the caller's stream, no host synchronisation, no
+// memset:
+//
+// Sorted index (the reference's own call: segment ids from
+// unique_consecutive are non-decreasing):   seg_range -> seg_link
+// * seg_range: one workgroup of 8 wavefronts per range of 2048 positions
+//   (every workgroup the same size of work, however the rows are spread).
+//   Each wavefront walks a contiguous quarter-kilo of positions in batches of
+//   64 (lane = channel: each position is one coalesced row load, 64 in
+//   flight at once) and writes the rows that start and end inside its part;
+//   rows that cross a wavefront edge are merged through LDS; a row that
+//   crosses the workgroup's start or end leaves one 512-byte piece, and every
+//   workgroup writes its tail flag (state, row, event count, bad-index bit).
+// * seg_link: one wavefront per range; a range whose last row continues
+//   reads the flags of the ranges after it (64 at a time), folds the pieces
+//   of the row in range order and writes it; also raises the status word for
+//   a bad index.  At C4 there are ~500 range edges (against ~16k tile edges
+//   with one 64-position tile per wavefront), so the link is a small pass.
+//
+// Unsorted index:   hist -> scan -> bucket -> bucket_reduce -> bucket_finalize
+// * hist  : LDS histogram of buckets of 64 consecutive rows per event range
+//           (a few hundred buckets, so the histogram is small and the
+//           workgroups many).
+// * scan  : per-bucket start offsets (and per-workgroup offsets inside each
+//           bucket) and the prefix of each bucket's chunk count, by a
+//           single-pass decoupled look-back; both counts travel in the flag
+//           word.
+// * bucket: (event, row) pairs placed at their bucket-grouped positions.
+// * bucket_reduce: one workgroup per chunk of at most 8192 events of one
+//           bucket: a 64-row x 64-channel tile in LDS takes every event with
+//           LDS atomics (max: ds_max_u64 on a packed (orderable value,
+//           inverted event id) key, so the result does not depend on the
+//           order the events arrive in; mean: ds_add_f64 and a row count).
+//           A bucket of one chunk is written out directly; the chunks of a
+//           larger bucket leave their tile.
+// * bucket_finalize: one workgroup per multi-chunk bucket folds its chunks'
+//           tiles and writes the rows.
+// Max/argmax select (value, smallest event id), NaN never wins, -0.0 ties
+// +0.0 and out keeps the sign of the winner's zero: bit-exact and
+// deterministic on both paths.  Mean sums in fp64 and rounds once (the
+// unsorted path's fp64 sum order follows the LDS atomics, so its last fp64
+// bits may vary between runs).
 #include "common.h"
 
 namespace ssla {
 namespace {
 
-#ifndef SSLA_SR_EV_THREADS
-#define SSLA_SR_EV_THREADS 1024
+#ifndef SSLA_SR_CHUNK
+#define SSLA_SR_CHUNK 4096
 #endif
-#ifndef SSLA_SR_MAX_HIST
-#define SSLA_SR_MAX_HIST 64
+#ifndef SSLA_SR_RANGE
+#define SSLA_SR_RANGE 512
 #endif
-#ifndef SSLA_SR_EV_PER_BLOCK
-#define SSLA_SR_EV_PER_BLOCK 16384
+constexpr int kBucketShift = 6;                    // 64 output rows per bucket
+constexpr int kBucketRows = 1 << kBucketShift;
+constexpr int kEvThreads = 1024;                   // hist / bucket workgroup size
+constexpr int kMaxHist = 256;                      // histogram rows (workgroups) at most
+constexpr int kEvPerBlock = 4096;                  // events per histogram workgroup (target)
+constexpr int kLdsBuckets = 4096;                  // buckets counted in LDS (16 KB); more: global counters
+constexpr int kScanCells = 64;                     // buckets per scan workgroup
+constexpr int kScanTpc = 1024 / kScanCells;        // scan threads per bucket
+constexpr int kChunk = SSLA_SR_CHUNK;              // events per bucket_reduce workgroup at most
+constexpr int kRedWaves = 16;                      // bucket_reduce / finalize wavefronts
+#ifndef SSLA_SR_RWAVES
+#define SSLA_SR_RWAVES 8
 #endif
-#ifndef SSLA_SR_SCAN_CELLS
-#define SSLA_SR_SCAN_CELLS 256
-#endif
-#ifndef SSLA_SR_LDS_CELLS
-#define SSLA_SR_LDS_CELLS 24576
-#endif
-constexpr int kLdsCells = SSLA_SR_LDS_CELLS;         // LDS histogram capacity (96 KB)
-constexpr int kEvThreads = SSLA_SR_EV_THREADS;       // hist / bucket workgroup size
-constexpr int kMaxHist = SSLA_SR_MAX_HIST;           // histogram rows (workgroups) at most
-constexpr int kEvPerBlock = SSLA_SR_EV_PER_BLOCK;    // events per histogram workgroup (target)
-constexpr int kScanCells = SSLA_SR_SCAN_CELLS;       // output rows per scan workgroup
-constexpr int kScanTpc = 1024 / SSLA_SR_SCAN_CELLS;  // scan threads per output row
-#ifndef SSLA_SR_TILE
-#define SSLA_SR_TILE 64
-#endif
-#ifndef SSLA_SR_SEG_WAVES
-#define SSLA_SR_SEG_WAVES 4
-#endif
-constexpr int kTile = SSLA_SR_TILE;            // positions per tile (<= 64: one per lane)
-constexpr int kSegWaves = SSLA_SR_SEG_WAVES;   // wavefronts (tiles) per workgroup
+constexpr int kRangeWaves = SSLA_SR_RWAVES;        // seg_range wavefronts
+constexpr int kRange = SSLA_SR_RANGE;              // positions per seg_range workgroup
+constexpr int kPart = kRange / kRangeWaves;        // positions per seg_range wavefront
+static_assert(kPart % 64 == 0, "a wavefront part is whole batches of 64 positions");
+constexpr int kLinkWaves = 4;
+
+inline int64_t n_buckets(int64_t n_out) { return (n_out + kBucketRows - 1) >> kBucketShift; }
+inline int64_t n_ranges(int64_t E) { return std::max<int64_t>(1, (E + kRange - 1) / kRange); }
+inline int64_t n_chunks_max(int64_t E, int64_t NB) { return NB + (E + kChunk - 1) / kChunk; }
 
 struct WsLayout {
-  size_t status, errs, off, flags, hist, perm, seg_flags, pieces, total;
+  size_t status, errs, off, coff, flags, hist, perm, parts, pcnt, rflags, rpieces, total;
   int n_hist;
-  int64_t n_tiles;   // tiles of kTile positions (for E positions)
-  int64_t n_seg;     // (tile, channel block) pairs
+  int64_t NB, n_chunks, n_rseg;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-inline int hist_rows(int64_t E, int64_t n_out) {
-  if (n_out > kLdsCells) return 1;   // global-atomic counting (rows too many for LDS)
+inline bool lds_hist(int64_t NB) { return NB <= kLdsBuckets; }
+
+inline int hist_rows(int64_t E, int64_t NB) {
+  if (!lds_hist(NB)) return 1;   // global-atomic counting (buckets too many for LDS)
   const int64_t r = (E + kEvPerBlock - 1) / kEvPerBlock;
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kMaxHist, r)));
 }
 
-inline int64_t scan_blocks(int64_t n_out) { return (n_out + kScanCells - 1) / kScanCells; }
+inline int64_t scan_blocks(int64_t NB) { return (NB + kScanCells - 1) / kScanCells; }
 
 // Histogram workgroups of the global-counter mode (also their error slots).
 inline int global_hist_blocks(int64_t E) {
@@ -92,21 +105,27 @@ inline int global_hist_blocks(int64_t E) {
 
 inline WsLayout ws_layout(int64_t E, int C, int64_t n_out) {
   WsLayout L;
-  L.n_hist = hist_rows(E, n_out);
+  L.NB = std::max<int64_t>(1, n_buckets(n_out));
+  L.n_hist = hist_rows(E, L.NB);
+  L.n_chunks = n_chunks_max(E, L.NB);
+  const int64_t ncb = (C + 63) / 64;
+  L.n_rseg = n_ranges(E) * ncb;
   const int n_err = std::max(L.n_hist, global_hist_blocks(E));
   size_t p = 0;
   L.status = p; p += 256;   // [0] status word, [1] scan ticket
   L.errs = p;  p = align256(p + sizeof(int32_t) * n_err);
-  L.off = p;   p = align256(p + sizeof(int32_t) * (n_out + 1));
-  L.n_tiles = (E + kTile - 1) / kTile;
-  L.n_seg = L.n_tiles * ((C + 63) / 64);
-  L.flags = p; p = align256(p + sizeof(uint64_t) * (scan_blocks(n_out) + 1));
-  L.hist = p;  p = align256(p + sizeof(int32_t) * static_cast<size_t>(L.n_hist) * (n_out + 1));
-  L.perm = p;  p = align256(p + sizeof(int2) * (E > 0 ? E : 1));   // (event, row) per sorted position
-  // per (tile, channel block): tail and head flags, and two pieces (tail,
-  // head) of 64 packed 8-byte values each
-  L.seg_flags = p; p = align256(p + sizeof(uint64_t) * 2 * static_cast<size_t>(L.n_seg));
-  L.pieces = p; p = align256(p + static_cast<size_t>(L.n_seg) * 2 * 64 * 8);
+  L.off = p;   p = align256(p + sizeof(int32_t) * (L.NB + 1));
+  L.coff = p;  p = align256(p + sizeof(int32_t) * (L.NB + 1));
+  L.flags = p; p = align256(p + sizeof(uint64_t) * (scan_blocks(L.NB) + 1));
+  L.hist = p;  p = align256(p + sizeof(int32_t) * static_cast<size_t>(L.n_hist) * (L.NB + 1));
+  L.perm = p;  p = align256(p + sizeof(int2) * (E > 0 ? E : 1));   // (event, row) per bucket-grouped position
+  // per (chunk, channel block): a 64 x 64 tile of 8-byte keys / fp64 sums;
+  // per chunk: 64 row counts
+  L.parts = p; p = align256(p + sizeof(uint64_t) * static_cast<size_t>(L.n_chunks) * ncb * 64 * 64);
+  L.pcnt = p;  p = align256(p + sizeof(int32_t) * static_cast<size_t>(L.n_chunks) * 64);
+  // per (range, channel block): tail flag and head count, tail and head pieces
+  L.rflags = p; p = align256(p + sizeof(uint64_t) * 2 * static_cast<size_t>(L.n_rseg));
+  L.rpieces = p; p = align256(p + sizeof(uint64_t) * 2 * 64 * static_cast<size_t>(L.n_rseg));
   L.total = p;
   return L;
 }
@@ -129,21 +148,27 @@ __device__ __forceinline__ void clear_scan_state(int32_t *ticket, uint64_t *flag
     flags[i] = 0;
 }
 
+// 64-bit value of lane k (a scalar)
+__device__ __forceinline__ uint64_t rl64(uint64_t v, int k) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(v), k));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(v >> 32), k));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
 // ---------------------------------------------------------------- hist --
-// LDS mode: row b of hist = counts of the events of range b.
-// Global mode (n_out > kLdsCells): one shared row of global counters, which
-// the preceding fill kernel cleared.
+// LDS mode: row b of hist = bucket counts of the events of range b.
+// Global mode (more buckets than LDS holds): one shared row of global
+// counters, which the preceding fill kernel cleared.
 template <bool LDS>
 __global__ __launch_bounds__(kEvThreads) void hist_kernel(
-    const int64_t *__restrict__ index, int64_t E, int64_t n_out, int n_hist,
+    const int64_t *__restrict__ index, int64_t E, int64_t n_out, int64_t NB, int n_hist,
     int32_t *__restrict__ hist, int32_t *__restrict__ errs, int32_t *ticket, uint64_t *flags,
     int64_t n_flags) {
   clear_scan_state(ticket, flags, n_flags);
   bool bad = false;
   if constexpr (LDS) {
-    __shared__ int32_t lh[kLdsCells];
-#pragma unroll 8
-    for (int64_t c = threadIdx.x; c < n_out; c += kEvThreads) lh[c] = 0;
+    __shared__ int32_t lh[kLdsBuckets];
+    for (int64_t c = threadIdx.x; c < NB; c += kEvThreads) lh[c] = 0;
     __syncthreads();
     int64_t e0, e1;
     event_range(E, n_hist, blockIdx.x, e0, e1);
@@ -155,102 +180,119 @@ __global__ __launch_bounds__(kEvThreads) void hist_kernel(
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         if (bad_row(r[u], n_out)) bad = true;
-        else atomicAdd(&lh[r[u]], 1);
+        else atomicAdd(&lh[r[u] >> kBucketShift], 1);
       }
     }
     for (; e < e1; e += kEvThreads) {
       const int64_t r = index[e];
       if (bad_row(r, n_out)) bad = true;
-      else atomicAdd(&lh[r], 1);
+      else atomicAdd(&lh[r >> kBucketShift], 1);
     }
     __syncthreads();
-    int32_t *row = hist + static_cast<int64_t>(blockIdx.x) * (n_out + 1);
-#pragma unroll 8
-    for (int64_t c = threadIdx.x; c < n_out; c += kEvThreads) row[c] = lh[c];
+    int32_t *row = hist + static_cast<int64_t>(blockIdx.x) * (NB + 1);
+    for (int64_t c = threadIdx.x; c < NB; c += kEvThreads) row[c] = lh[c];
   } else {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kEvThreads;
     for (int64_t e = static_cast<int64_t>(blockIdx.x) * kEvThreads + threadIdx.x; e < E; e += stride) {
       const int64_t r = index[e];
       if (bad_row(r, n_out)) bad = true;
-      else atomicAdd(&hist[r], 1);
+      else atomicAdd(&hist[r >> kBucketShift], 1);
     }
   }
   const int any_bad = __syncthreads_or(bad ? 1 : 0);
   if (threadIdx.x == 0) errs[blockIdx.x] = any_bad ? SSLA_ERR_ARG : SSLA_OK;
 }
 
-// -------------------------------------------------------------- bounds --
-// Sorted index: start[r] = first e with index[e] >= r for r in [0, n_out],
-// start[n_out] = E.  Every r is written by exactly one e when the index is
-// sorted and in range; otherwise the error slot is set and the reduce
-// kernel's clamps keep every access inside the tensors.
 // ---------------------------------------------------------------- scan --
 // Look-back word: [63:62] state (0 none, 1 aggregate, 2 inclusive prefix),
-// [30:0] event count.  The count saturates at 2^31 - 1, so inconsistent
-// input can give wrong offsets but never touches the state bits, and the
-// look-back always terminates.
+// [61:31] chunk count, [30:0] event count.  Counts saturate at 2^31 - 1, so
+// inconsistent input can give wrong offsets but never touches the state
+// bits, and the look-back always terminates.
 constexpr uint64_t kFlagAgg = 1ull << 62, kFlagIncl = 2ull << 62;
 constexpr uint64_t kMask31 = 0x7fffffffull;
 
-__device__ __forceinline__ uint64_t pack_count(int64_t cnt) {
-  return static_cast<uint64_t>(min(max(cnt, (int64_t)0), (int64_t)kMask31));
+__device__ __forceinline__ uint64_t pack_counts(int64_t cnt, int64_t chk) {
+  const uint64_t a = static_cast<uint64_t>(min(max(cnt, (int64_t)0), (int64_t)kMask31));
+  const uint64_t b = static_cast<uint64_t>(min(max(chk, (int64_t)0), (int64_t)kMask31));
+  return (b << 31) | a;
 }
 
-// Counts are column sums of the [n_hist, n_out] histogram matrix; each
-// column is rewritten with its exclusive prefix (the start offset of each
-// histogram workgroup inside the row), and off = exclusive prefix of the
-// counts over rows (off[n_out] = events kept).
+// Chunks of a bucket of n events: at least one (so every bucket, empty or
+// not, has a workgroup that writes its rows).
+__device__ __forceinline__ int64_t bucket_chunks(int64_t n) { return max((n + kChunk - 1) / kChunk, (int64_t)1); }
+
+// Counts are column sums of the [n_hist, NB] histogram matrix; each column
+// is rewritten with its exclusive prefix (the start offset of each histogram
+// workgroup inside the bucket); off = exclusive prefix of the counts over
+// buckets (off[NB] = events kept) and coff = that of the chunk counts
+// (coff[NB] = chunks).
 __global__ __launch_bounds__(kScanCells *kScanTpc) void scan_kernel(
-    int32_t *__restrict__ hist, int n_hist, int64_t n_out, int32_t *__restrict__ off, int32_t *ticket,
-    uint64_t *flags, const int32_t *__restrict__ errs, int n_err, int32_t *__restrict__ status) {
+    int32_t *__restrict__ hist, int n_hist, int64_t NB, int32_t *__restrict__ off, int32_t *__restrict__ coff,
+    int32_t *ticket, uint64_t *flags, const int32_t *__restrict__ errs, int n_err, int32_t *__restrict__ status) {
   __shared__ int s_bid;
   __shared__ int32_t s_part[kScanTpc][kScanCells];
-  __shared__ int64_t s_cnt[kScanCells];
-  __shared__ int64_t s_wc[kScanCells / 64];
-  __shared__ int64_t s_excl;
+  __shared__ int64_t s_cnt[kScanCells], s_chk[kScanCells];
+  __shared__ int64_t s_wc[kScanCells / 64], s_wk[kScanCells / 64];
+  __shared__ int64_t s_excl, s_excl_chk;
   const int tid = threadIdx.x;
   if (tid == 0) s_bid = atomicAdd(ticket, 1);
   __syncthreads();
   const int64_t bid = s_bid;
   const int lc = tid % kScanCells, grp = tid / kScanCells;
   const int64_t cell = bid * kScanCells + lc;
-  const bool live = cell < n_out;
+  const bool live = cell < NB;
 
   // column segment [b0, b1) of this thread
+  constexpr int kPer = (kMaxHist + kScanTpc - 1) / kScanTpc;
   const int per = (n_hist + kScanTpc - 1) / kScanTpc;
   const int b0 = min(n_hist, grp * per), b1 = min(n_hist, b0 + per);
-  int32_t v[(kMaxHist + kScanTpc - 1) / kScanTpc];
+  int32_t v[kPer];
   int32_t sum = 0;
 #pragma unroll
-  for (int i = 0; i < (kMaxHist + kScanTpc - 1) / kScanTpc; ++i)
-    v[i] = (live && b0 + i < b1) ? hist[static_cast<int64_t>(b0 + i) * (n_out + 1) + cell] : 0;
+  for (int i = 0; i < kPer; ++i)
+    v[i] = (live && b0 + i < b1) ? hist[static_cast<int64_t>(b0 + i) * (NB + 1) + cell] : 0;
 #pragma unroll
-  for (int i = 0; i < (kMaxHist + kScanTpc - 1) / kScanTpc; ++i) sum += v[i];
+  for (int i = 0; i < kPer; ++i) sum += v[i];
   s_part[grp][lc] = sum;
   __syncthreads();
   int32_t run = 0;
   for (int g2 = 0; g2 < grp; ++g2) run += s_part[g2][lc];
 #pragma unroll
-  for (int i = 0; i < (kMaxHist + kScanTpc - 1) / kScanTpc; ++i) {
-    if (live && b0 + i < b1) hist[static_cast<int64_t>(b0 + i) * (n_out + 1) + cell] = run;
+  for (int i = 0; i < kPer; ++i) {
+    if (live && b0 + i < b1) hist[static_cast<int64_t>(b0 + i) * (NB + 1) + cell] = run;
     run += v[i];
   }
-  if (grp == kScanTpc - 1) s_cnt[lc] = run;   // column total
+  if (grp == kScanTpc - 1) {   // column total
+    s_cnt[lc] = run;
+    s_chk[lc] = live ? bucket_chunks(run) : 0;
+  }
   __syncthreads();
-  // inclusive scan over the block's cells: wavefront scans, then carries
-  int64_t c = 0;
+  // inclusive scans over the block's buckets: wavefront scans, then carries
+  int64_t c = 0, k = 0;
   if (tid < kScanCells) {
     c = s_cnt[tid];
+    k = s_chk[tid];
     for (int d = 1; d < 64; d <<= 1) {
       const int64_t c2 = __shfl_up(c, d);
-      if ((tid & 63) >= d) c += c2;
+      const int64_t k2 = __shfl_up(k, d);
+      if ((tid & 63) >= d) {
+        c += c2;
+        k += k2;
+      }
     }
-    if ((tid & 63) == 63) s_wc[tid >> 6] = c;
+    if ((tid & 63) == 63) {
+      s_wc[tid >> 6] = c;
+      s_wk[tid >> 6] = k;
+    }
   }
   __syncthreads();
   if (tid < kScanCells) {
-    for (int q = 0; q < (tid >> 6); ++q) c += s_wc[q];
+    for (int q = 0; q < (tid >> 6); ++q) {
+      c += s_wc[q];
+      k += s_wk[q];
+    }
     s_cnt[tid] = c;
+    s_chk[tid] = k;
   }
   __syncthreads();
   // Windowed look-back by the first wavefront: lane l reads the flag of
@@ -258,11 +300,12 @@ __global__ __launch_bounds__(kScanCells *kScanTpc) void scan_kernel(
   // payload travels inside the flag word, so relaxed agent-scope atomics
   // suffice (no fences, which would write back / invalidate the L2).
   if (tid < 64) {
-    const int64_t agg = s_cnt[kScanCells - 1];
-    int64_t ex = 0;
+    const int64_t agg = s_cnt[kScanCells - 1], agg_k = s_chk[kScanCells - 1];
+    int64_t ex = 0, ex_k = 0;
     if (bid > 0) {
       if (tid == 0)
-        __hip_atomic_store(&flags[bid], kFlagAgg | pack_count(agg), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&flags[bid], kFlagAgg | pack_counts(agg, agg_k), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
       // Predecessors took their tickets before this block, so they are
       // resident and publish without waiting on later blocks: the spin ends.
       int64_t j_end = bid;   // blocks [0, j_end) not folded yet
@@ -280,8 +323,13 @@ __global__ __launch_bounds__(kScanCells *kScanTpc) void scan_kernel(
           continue;
         }
         int64_t vc = tid <= last ? static_cast<int64_t>(w & kMask31) : 0;
-        for (int d = 32; d >= 1; d >>= 1) vc += __shfl_xor(vc, d);
+        int64_t vk = tid <= last ? static_cast<int64_t>((w >> 31) & kMask31) : 0;
+        for (int d = 32; d >= 1; d >>= 1) {
+          vc += __shfl_xor(vc, d);
+          vk += __shfl_xor(vk, d);
+        }
         ex += vc;
+        ex_k += vk;
         if (incl) break;
         j_end -= 64;
       }
@@ -298,31 +346,36 @@ __global__ __launch_bounds__(kScanCells *kScanTpc) void scan_kernel(
       if (tid == 0) *status = st;
     }
     if (tid == 0) {
-      __hip_atomic_store(&flags[bid], kFlagIncl | pack_count(ex + agg), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&flags[bid], kFlagIncl | pack_counts(ex + agg, ex_k + agg_k), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
       s_excl = ex;
-      if (bid == static_cast<int64_t>(gridDim.x) - 1) off[n_out] = static_cast<int32_t>(ex + agg);
+      s_excl_chk = ex_k;
+      if (bid == static_cast<int64_t>(gridDim.x) - 1) {
+        off[NB] = static_cast<int32_t>(ex + agg);
+        coff[NB] = static_cast<int32_t>(ex_k + agg_k);
+      }
     }
   }
   __syncthreads();
   if (grp == 0 && live) {
     const int64_t mine = lc > 0 ? s_cnt[lc] - s_cnt[lc - 1] : s_cnt[0];
+    const int64_t mine_k = lc > 0 ? s_chk[lc] - s_chk[lc - 1] : s_chk[0];
     off[cell] = static_cast<int32_t>(s_excl + s_cnt[lc] - mine);
+    coff[cell] = static_cast<int32_t>(s_excl_chk + s_chk[lc] - mine_k);
   }
 }
 
 // -------------------------------------------------------------- bucket --
-// perm[off[r] + start of this workgroup in row r + rank] = (e, r): one
-// 8-byte store per event (the positions are scattered, so each store is a
-// partial line of its own).
+// perm[off[b] + start of this workgroup in bucket b + rank] = (e, row): one
+// 8-byte store per event.
 template <bool LDS>
 __global__ __launch_bounds__(kEvThreads) void bucket_kernel(
-    const int64_t *__restrict__ index, int64_t E, int64_t n_out, int n_hist,
+    const int64_t *__restrict__ index, int64_t E, int64_t n_out, int64_t NB, int n_hist,
     const int32_t *__restrict__ off, int32_t *__restrict__ hist, int2 *__restrict__ perm) {
   if constexpr (LDS) {
-    __shared__ int32_t lc[kLdsCells];
-    const int32_t *row = hist + static_cast<int64_t>(blockIdx.x) * (n_out + 1);
-#pragma unroll 8
-    for (int64_t c = threadIdx.x; c < n_out; c += kEvThreads) lc[c] = off[c] + row[c];
+    __shared__ int32_t lc[kLdsBuckets];
+    const int32_t *row = hist + static_cast<int64_t>(blockIdx.x) * (NB + 1);
+    for (int64_t c = threadIdx.x; c < NB; c += kEvThreads) lc[c] = off[c] + row[c];
     __syncthreads();
     int64_t e0, e1;
     event_range(E, n_hist, blockIdx.x, e0, e1);
@@ -334,14 +387,14 @@ __global__ __launch_bounds__(kEvThreads) void bucket_kernel(
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         if (bad_row(r[u], n_out)) continue;
-        const int32_t pos = atomicAdd(&lc[r[u]], 1);
+        const int32_t pos = atomicAdd(&lc[r[u] >> kBucketShift], 1);
         if (pos >= 0 && pos < E) perm[pos] = make_int2(static_cast<int32_t>(e + u * kEvThreads), static_cast<int32_t>(r[u]));
       }
     }
     for (; e < e1; e += kEvThreads) {
       const int64_t r = index[e];
       if (bad_row(r, n_out)) continue;
-      const int32_t pos = atomicAdd(&lc[r], 1);
+      const int32_t pos = atomicAdd(&lc[r >> kBucketShift], 1);
       if (pos >= 0 && pos < E) perm[pos] = make_int2(static_cast<int32_t>(e), static_cast<int32_t>(r));
     }
   } else {
@@ -349,45 +402,48 @@ __global__ __launch_bounds__(kEvThreads) void bucket_kernel(
     for (int64_t e = static_cast<int64_t>(blockIdx.x) * kEvThreads + threadIdx.x; e < E; e += stride) {
       const int64_t r = index[e];
       if (bad_row(r, n_out)) continue;
-      const int32_t pos = off[r] + atomicAdd(&hist[r], 1);
+      const int64_t b = r >> kBucketShift;
+      const int32_t pos = off[b] + atomicAdd(&hist[b], 1);
       if (pos >= 0 && pos < E) perm[pos] = make_int2(static_cast<int32_t>(e), static_cast<int32_t>(r));
     }
   }
 }
 
-// ------------------------------------------------------------ segments --
-// One wavefront per (tile of kTile consecutive positions, block of 64
-// channels); positions are events of a sorted index, or counting-sort
-// positions (rows non-decreasing either way).  Lane = channel: each position
-// is one coalesced row load, and all kTile loads of the tile are in flight
-// at once, into registers (no LDS: occupancy is bounded by registers only).
-// The wavefront then walks the positions in order.  A row that begins and ends inside the tile is written directly.
-// A row that crosses tile edges (tiles ts < ... < te) leaves one piece per
-// tile: the "tail" piece of ts (the row leaves through its end), tail
-// pieces of the "through" tiles between (each wholly that row) and the
-// "head" piece of te (the row entered through its start).  Every tile
-// writes its tail flag (state, row, event count, bad-index bit) whether or
-// not it has a tail piece, so no clearing is needed; seg_fixup_kernel then
-// folds each crossing row's pieces in tile order (deterministic) and writes
-// it.  Rows without events between a tile's rows (and before the first /
-// after the last row of the input) are written as empty rows.
-// Tail flag: bits 62-63 state, bit 61 bad index seen, bits 31-60 row (n_out
-// < 2^30), bits 0-30 events of the piece.  Head flag: events of the head
-// piece.
-constexpr uint64_t kSegThrough = 1ull << 62, kSegPiece = 2ull << 62, kSegBad = 1ull << 61;
-__device__ __forceinline__ uint64_t seg_state(uint64_t f) { return f >> 62; }
-__device__ __forceinline__ int32_t seg_row(uint64_t f) { return static_cast<int32_t>((f >> 31) & 0x3fffffffu); }
-__device__ __forceinline__ int64_t seg_count(uint64_t f) { return static_cast<int64_t>(f & 0x7fffffffu); }
+// ---------------------------------------------------------- max / mean --
+// Order-independent max key of (value x, event e): the value's bits made
+// unsigned-orderable (-0.0 taken as +0.0) in the high word; in the low word
+// the inverted event id (so the smallest id wins a tie) above the sign of a
+// zero (so the winner's -0.0 comes back).  NaN gives 0, which every event
+// beats: NaN never wins, and a row with no winner reads 0.  E < 2^31.
+__device__ __forceinline__ uint64_t max_key(float x, int32_t e) {
+  uint32_t u = __float_as_uint(x);
+  const bool zero = (u & 0x7fffffffu) == 0u;
+  const uint32_t neg_zero = (u == 0x80000000u) ? 1u : 0u;
+  if (zero) u = 0u;
+  const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  const uint32_t lo = ((0x7fffffffu - static_cast<uint32_t>(e)) << 1) | neg_zero;
+  const uint64_t key = (static_cast<uint64_t>(ord) << 32) | lo;
+  return (x != x) ? 0ull : key;
+}
+// (value, event) of a key != 0
+__device__ __forceinline__ void key_value(uint64_t key, float &x, int64_t &e) {
+  const uint32_t ord = static_cast<uint32_t>(key >> 32);
+  const uint32_t lo = static_cast<uint32_t>(key);
+  uint32_t u = (ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord;
+  if (lo & 1u) u = 0x80000000u;
+  x = __uint_as_float(u);
+  e = static_cast<int64_t>(0x7fffffffu - (lo >> 1));
+}
 
+// Walk accumulators of the sorted path: (value, smallest event id) maximum
+// by comparison (NaN never wins: -1 as unsigned is above every event id),
+// or an fp64 sum.
 template <bool MEAN>
 struct SegAcc;
 template <> struct SegAcc<false> {
   float best;
   int32_t idx;   // -1: no event yet
   __device__ __forceinline__ void reset() { best = -INFINITY; idx = -1; }
-  // (value, smallest event id) maximum, independent of visiting order; NaN
-  // never wins (-1 as unsigned is above every event id).  Branch-free: two
-  // compares and two selects per event.
   __device__ __forceinline__ void add(float x, int32_t e) {
     const bool take = (x > best) | ((x == best) & (static_cast<uint32_t>(e) < static_cast<uint32_t>(idx)));
     best = take ? x : best;
@@ -426,279 +482,446 @@ __device__ __forceinline__ void seg_store(float *out, int64_t *argmax, int64_t o
   }
 }
 
+// Rows [r0, r1) (clamped to the output) of one channel written as empty.
 template <bool MEAN>
-__device__ __forceinline__ void seg_empty_rows(float *out, int64_t *argmax, int64_t r0, int64_t r1, int C, int col,
-                                               bool act, int64_t E) {
+__device__ __forceinline__ void seg_empty_rows(float *out, int64_t *argmax, int64_t r0, int64_t r1, int64_t n_out,
+                                               int C, int col, bool act, int64_t E) {
+  r0 = max(r0, (int64_t)0);
+  r1 = min(r1, n_out);
+  if (!act) return;
   for (int64_t r = r0; r < r1; ++r) {
-    if (act) {
-      out[r * C + col] = 0.f;
-      if constexpr (!MEAN) argmax[r * C + col] = E;
-    }
+    out[r * C + col] = 0.f;
+    if constexpr (!MEAN) argmax[r * C + col] = E;
   }
 }
 
-// PERM: positions are those of the counting sort (perm[p] = (event id,
-// row), n_valid = positions kept); otherwise positions are events and
-// rows come from the sorted index.  n_seg = (tile, block) pairs for E
-// positions; flags [2][n_seg] (tail, head); pieces [2][n_seg][64].
-template <bool MEAN, bool PERM>
-__global__ __launch_bounds__(64 * kSegWaves) void seg_reduce_kernel(
-    const float *__restrict__ src, const int64_t *__restrict__ index, const int2 *__restrict__ perm,
-    const int32_t *__restrict__ n_valid, int64_t E, int C, int64_t n_out,
-    float *__restrict__ out, int64_t *__restrict__ argmax, int64_t n_seg, uint64_t *__restrict__ flags,
-    uint64_t *__restrict__ pieces, int32_t *__restrict__ status) {
+// ------------------------------------------------------------ seg_range --
+// Range flag (tail flag): bits 62-63 state (0: the range's last row ends at
+// the range's end or inside it; 1: the whole range is one row that began
+// before it and continues after it; 2: the last row continues past the end:
+// a tail piece), bit 61 a bad index seen in the range, bits 31-60 the row
+// (clamped, n_out < 2^30), bits 0-30 the events of the tail piece (or of the
+// range when state 1).  The second flag word of a range is its head count
+// (events of its first row's piece, when that row began before it).
+constexpr uint64_t kSegThrough = 1ull << 62, kSegPiece = 2ull << 62, kSegBad = 1ull << 61;
+__device__ __forceinline__ uint64_t seg_state(uint64_t f) { return f >> 62; }
+__device__ __forceinline__ int64_t seg_row(uint64_t f) { return static_cast<int64_t>((f >> 31) & 0x3fffffffu); }
+__device__ __forceinline__ int64_t seg_count(uint64_t f) { return static_cast<int64_t>(f & 0x7fffffffu); }
+
+// wavefront part flags (LDS)
+constexpr int kPartLive = 1, kPartOpenStart = 2, kPartOpenEnd = 4, kPartThrough = 8;
+
+constexpr int kRsrcWord3 = 0x00020000;   // raw 32-bit data, range checked
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// Buffer resource over [base, base + bytes): loads past the end read 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                           static_cast<int>(min(max(bytes, (int64_t)0), (int64_t)0x7fffffff)),
+                                           kRsrcWord3);
+}
+
+// A row index saturated to int32: -1 below the output, n_out above it (both
+// bad); distinct valid rows stay distinct, so every boundary and order test
+// agrees between the workgroups that look at the same positions.
+__device__ __forceinline__ int32_t sat_row(int64_t r, int32_t n_out) {
+  return r < 0 ? -1 : (r >= n_out ? n_out : static_cast<int32_t>(r));
+}
+
+// CT: the channel count at compile time (64: one channel block, row
+// offsets become immediates) or 0 (any C, channel blocks of 64).
+template <bool MEAN, int CT>
+__global__ __launch_bounds__(64 * kRangeWaves) void seg_range_kernel(
+    const float *__restrict__ src, const int64_t *__restrict__ index, int32_t E, int C, int32_t n_out,
+    float *__restrict__ out, int64_t *__restrict__ argmax, uint64_t *__restrict__ rflags,
+    uint64_t *__restrict__ rpieces, int32_t n_rseg, int32_t *__restrict__ status) {
+  __shared__ uint64_t s_head[kRangeWaves][64], s_tail[kRangeWaves][64];
+  __shared__ int32_t s_hcnt[kRangeWaves], s_tcnt[kRangeWaves], s_trow[kRangeWaves], s_fl[kRangeWaves];
+  const int Cc = CT ? CT : C;
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int ncb = (C + 63) / 64;
-  const int64_t Ev = PERM ? min(max(static_cast<int64_t>(*n_valid), static_cast<int64_t>(0)), E) : E;
-  const int64_t n_tiles = (Ev + kTile - 1) / kTile;
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * kSegWaves + w;
-  if (q == 0 && !PERM && lane == 0) *status = SSLA_OK;   // bad indices are raised by the fixup kernel
-  if (n_tiles == 0) {   // no (valid) events: every row is empty
-    if (q == 0)
-      for (int cb = 0; cb < C; cb += 64) seg_empty_rows<MEAN>(out, argmax, 0, n_out, C, cb + lane, cb + lane < C, E);
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int ncb = CT ? 1 : (C + 63) / 64;
+  const int rg = static_cast<int>(blockIdx.x) / ncb;
+  const int cb = static_cast<int>(blockIdx.x) - rg * ncb;
+  const int seg = static_cast<int>(blockIdx.x);   // this workgroup's flags / pieces
+  const int col = cb * 64 + lane;
+  const bool act = CT ? true : col < C;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *status = SSLA_OK;   // bad indices are raised by seg_link
+  if (E == 0) {   // no events: every row is empty
+    if (w == 0) seg_empty_rows<MEAN>(out, argmax, 0, n_out, n_out, Cc, col, act, E);
     return;
   }
-  const int64_t t = q / ncb;
-  if (t >= n_tiles) return;   // wavefront-uniform
-  const int cb = static_cast<int>(q - t * ncb);
-  const int64_t seg = t * ncb + cb;   // this wavefront's flag / piece
-  const int64_t e0 = t * kTile;
-  const int ne = static_cast<int>(min(static_cast<int64_t>(kTile), Ev - e0));
-  const int ne_u = __builtin_amdgcn_readfirstlane(ne);   // the same in every lane
-  auto row_at = [&](int64_t p) -> int64_t { return PERM ? static_cast<int64_t>(perm[p].y) : index[p]; };
-  auto clamp_row = [&](int64_t r) { return static_cast<int32_t>(min(max(r, static_cast<int64_t>(0)), n_out - 1)); };
-  // row ids: one per lane, checked for range and order
-  const int64_t prev = e0 > 0 ? row_at(e0 - 1) : -1;
-  const int64_t next = e0 + ne < Ev ? row_at(e0 + ne) : n_out;
-  const int64_t rr = lane < ne ? row_at(e0 + lane) : n_out;
-  const int64_t rl = __shfl_up(rr, 1);
-  const int64_t rbefore = lane == 0 ? max(prev, static_cast<int64_t>(-1)) : rl;
-  const bool bad_l = lane < ne && (rr < 0 || rr >= n_out || rr < rbefore);
-  const bool bad = !PERM && __builtin_amdgcn_ballot_w64(bad_l) != 0;
-  // clamped (memory-safe) rows; with bad input the result is unspecified,
-  // but the tile links below stay consistent, so every look-back ends
-  const int32_t row = clamp_row(rr);
-  // event id of each position (argmax value and source row)
-  const int32_t ev = lane < ne ? (PERM ? min(max(perm[e0 + lane].x, 0), static_cast<int32_t>(E - 1))
-                                       : static_cast<int32_t>(e0 + lane))
-                               : (PERM ? 0 : static_cast<int32_t>(e0));
-  const int32_t first = __builtin_amdgcn_readfirstlane(row);
-  const int32_t last = __builtin_amdgcn_readlane(row, ne - 1);
-  // tile t's first row continues tile t-1's last row exactly when tile t-1's
-  // last row continues into tile t (the same clamped comparison)
-  const bool open_start = e0 > 0 && clamp_row(prev) == first;
-  const bool open_end = e0 + ne < Ev && clamp_row(next) == last;
-  // positions (after the first) where the row changes; the shuffle runs
-  // with every lane active (a lane masked off by a condition would read 0)
-  const int32_t row_up = __shfl_up(row, 1);
-  const uint64_t bnd = __builtin_amdgcn_ballot_w64(lane > 0 && lane < ne && row != row_up);
-  const bool through = open_start && open_end && bnd == 0;   // the whole tile is one continuing row
-  const int col = cb * 64 + lane;
-  const bool act = col < C;
+  const int s0 = rg * kRange, s1 = min(s0 + kRange, E);
+  const int pa = min(s0 + w * kPart, s1), pb = min(pa + kPart, s1);
+  // the range's rows of this channel block and its indices: loads past the
+  // range read 0 (and are never used)
+  const __amdgpu_buffer_rsrc_t rs_src =
+      make_rsrc(src + static_cast<int64_t>(s0) * Cc + cb * 64, (static_cast<int64_t>(s1 - s0) * Cc - cb * 64) * 4);
+  const __amdgpu_buffer_rsrc_t rs_idx = make_rsrc(index + s0, static_cast<int64_t>(s1 - s0) * 8);
 
-  // load the tile's rows of this channel block (positions past the tile
-  // re-read its first event's row and are never used)
-  const float *pc = src + min(col, C - 1);
-  float xr[kTile];
-#pragma unroll
-  for (int e = 0; e < kTile; ++e) {
-    const int32_t id = __builtin_amdgcn_readlane(ev, e < ne_u ? e : 0);
-    xr[e] = pc[static_cast<int64_t>(id) * C];
-  }
-  // empty rows between the previous tile's last row and this tile's first
-  if (!open_start) {
-    const int64_t gap0 = e0 > 0 ? static_cast<int64_t>(clamp_row(prev)) + 1 : 0;
-    seg_empty_rows<MEAN>(out, argmax, gap0, first, C, col, act, E);
-  }
-  SegAcc<MEAN> acc, head;   // head: the first row's piece when it began before the tile
+  auto store_row = [&](int32_t r, const SegAcc<MEAN> &a, int32_t cnt) __attribute__((always_inline)) {
+    if (act) seg_store<MEAN>(out, argmax, static_cast<int64_t>(min(max(r, 0), n_out - 1)) * Cc + col, a, cnt, E);
+  };
+
+  int fl = 0;
+  bool bad = false;
+  SegAcc<MEAN> acc, head;
   acc.reset();
   head.reset();
-  int head_cnt = 0;
-  bool in_head = open_start;   // the walk is still in that first row
-  int32_t cur = first;
-  int c0 = 0;   // first position of the current row inside the tile
-  // a row that ends inside the tile: keep it as the head piece, or write it
-  auto close_row = [&](int32_t r, int cnt) __attribute__((always_inline)) {
-    if (in_head) {
-      head = acc;
-      head_cnt = cnt;
-      in_head = false;
-    } else if (act) {
-      seg_store<MEAN>(out, argmax, static_cast<int64_t>(r) * C + col, acc, cnt, E);
-    }
-  };
-  // event id of position e (a scalar): consecutive ids without a permutation
-  auto ev_at = [&](int e) __attribute__((always_inline)) {
-    return PERM ? __builtin_amdgcn_readlane(ev, e) : static_cast<int32_t>(e0) + e;
-  };
-  // eight positions per step (the loop is unrolled: registers are named
-  // statically); a full step without a row boundary (the common case) runs
-  // without any per-position test
-#pragma unroll
-  for (int e8 = 0; e8 < kTile; e8 += 8) {   // kTile is a multiple of 8
-    if (e8 >= ne_u) break;
-    float xv[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) xv[k] = xr[e8 + k];
-    const uint32_t bb = static_cast<uint32_t>(bnd >> e8) & 0xffu;   // boundaries in this step
-    if (bb == 0 && e8 + 8 <= ne_u) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) acc.add(xv[k], ev_at(e8 + k));
-      continue;
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int e = e8 + k;
-      if (e < ne_u) {
-        if ((bb >> k) & 1) {   // wavefront-uniform: a new row starts at position e
-          const int32_t r = __builtin_amdgcn_readlane(row, e);
-          close_row(cur, e - c0);
-          seg_empty_rows<MEAN>(out, argmax, static_cast<int64_t>(cur) + 1, r, C, col, act, E);
-          cur = r;
-          c0 = e;
-          acc.reset();
+  int32_t cnt = 0, hcnt = 0, cur = 0;
+  if (pa < pb) {
+    fl = kPartLive;
+    const int32_t prev = pa > 0 ? sat_row(index[pa - 1], n_out) : -1;
+    const bool open_start = pa > 0 && sat_row(index[pa], n_out) == prev;
+    bool in_head = open_start;   // the walk is still in a row that began before this part
+    if (open_start) fl |= kPartOpenStart;
+    // the open row (open start), or the row before the part: a part that
+    // starts a row writes the empty rows between that row and its first
+    cur = prev;
+    int32_t rlast = prev;   // row of the position before the batch
+    auto close_row = [&]() __attribute__((always_inline)) {
+      if (cnt > 0) {
+        if (in_head) {
+          head = acc;
+          hcnt = cnt;
+          in_head = false;
+        } else {
+          store_row(cur, acc, cnt);
         }
-        acc.add(xv[k], ev_at(e));
+      }
+    };
+    for (int s = pa; s < pb; s += 64) {
+      const int ne = min(64, pb - s);
+      // the 64 row loads first (they do not depend on the index), then the
+      // index: one memory round trip per batch, not two
+      const uint32_t vb = static_cast<uint32_t>(s - s0) * static_cast<uint32_t>(Cc * 4) + lane * 4u;
+      float xr[64];
+#pragma unroll
+      for (int e = 0; e < 64; ++e)
+        xr[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs_src, vb + e * (Cc * 4), 0, 0));
+      asm volatile("" ::: "memory");   // the row loads stay ahead of the index load
+      const u32x2 raw = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs_idx, static_cast<uint32_t>(s - s0 + lane) * 8u, 0, 0));
+      const int32_t rr = sat_row(static_cast<int64_t>((static_cast<uint64_t>(raw.y) << 32) | raw.x), n_out);
+      const int32_t rup = __shfl_up(rr, 1);   // every lane active
+      const int32_t rbefore = lane == 0 ? rlast : rup;
+      if (lane < ne && (rr < 0 || rr >= n_out || rr < rbefore)) bad = true;
+      // positions where a new row starts; the part's first position starts
+      // one unless the part is open at its start
+      bool st = lane < ne && rr != rbefore;
+      if (s == pa && lane == 0) st = !open_start;
+      const uint64_t bnd = __builtin_amdgcn_ballot_w64(st);
+      const int32_t rfirst_before = s == pa ? prev : rlast;   // row before the batch
+      rlast = __builtin_amdgcn_readlane(rr, ne - 1);
+      // eight positions per step; a step without a row start (the common
+      // case) runs without any per-position test
+#pragma unroll
+      for (int e8 = 0; e8 < 64; e8 += 8) {
+        if (e8 >= ne) break;
+        const uint32_t bb = static_cast<uint32_t>(bnd >> e8) & 0xffu;
+        if (bb == 0 && e8 + 8 <= ne) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) acc.add(xr[e8 + k], s + e8 + k);
+          cnt += 8;
+          continue;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int e = e8 + k;
+          if (e < ne) {
+            if ((bb >> k) & 1) {   // wavefront-uniform: a new row starts at position s + e
+              close_row();
+              cur = __builtin_amdgcn_readlane(rr, e);
+              acc.reset();
+              cnt = 0;
+            }
+            acc.add(xr[e], s + e);
+            ++cnt;
+          }
+        }
+      }
+      // empty rows between consecutive rows of the batch (and between the
+      // row before it and its first), after the walk: one loop, not one per
+      // unrolled position
+      for (uint64_t m = bnd; m != 0; m &= m - 1) {
+        const int e = static_cast<int>(__builtin_ctzll(m));
+        const int32_t q = e == 0 ? rfirst_before : __builtin_amdgcn_readlane(rr, e - 1);
+        const int32_t r = __builtin_amdgcn_readlane(rr, e);
+        if (r > q + 1) seg_empty_rows<MEAN>(out, argmax, static_cast<int64_t>(q) + 1, r, n_out, Cc, col, act, E);
       }
     }
+    const bool open_end = pb < E && sat_row(index[pb], n_out) == rlast;
+    if (open_end) {
+      fl |= kPartOpenEnd | (in_head ? kPartThrough : 0);
+    } else {
+      close_row();
+      if (pb == E) seg_empty_rows<MEAN>(out, argmax, static_cast<int64_t>(cur) + 1, n_out, n_out, Cc, col, act, E);
+    }
   }
-  // pieces of crossing rows and this tile's flags (plain stores: the fixup
-  // kernel runs after this one)
-  const bool head_open = open_start && !through;   // first row entered through the start, ends here
-  uint64_t *tails = pieces, *heads = pieces + n_seg * 64;   // [n_seg][64] each
-  uint64_t *tail_f = flags, *head_f = flags + n_seg;          // [n_seg] each
-  uint64_t tf = (bad ? kSegBad : 0) | (static_cast<uint64_t>(last) << 31);
-  if (open_end) {
-    tails[seg * 64 + lane] = acc.pack();
-    tf |= (through ? kSegThrough : kSegPiece) | static_cast<uint64_t>(ne_u - c0);
-  } else {
-    close_row(cur, ne_u - c0);
+  s_head[w][lane] = head.pack();
+  s_tail[w][lane] = acc.pack();
+  if (lane == 0) {
+    s_fl[w] = fl;
+    s_hcnt[w] = hcnt;
+    s_tcnt[w] = cnt;
+    s_trow[w] = cur;
   }
-  if (lane == 0) tail_f[seg] = tf;
-  if (head_open) {
-    heads[seg * 64 + lane] = head.pack();
-    if (lane == 0) head_f[seg] = static_cast<uint64_t>(head_cnt);
+  const int any_bad = __syncthreads_or(bad ? 1 : 0);
+  if (w != 0) return;
+  // ---- fold the parts in order (wavefront 0) ----------------------------
+  // `run` is the row open between parts; `from_start` says it began before
+  // this range (then it is the range's head piece, or with no end inside the
+  // range, the whole range).
+  SegAcc<MEAN> run;
+  run.reset();
+  int32_t rcnt = 0, rrow = 0;
+  bool from_start = (s_fl[0] & kPartOpenStart) != 0;
+  int last_fl = 0;
+  uint64_t *tails = rpieces, *heads = rpieces + static_cast<int64_t>(n_rseg) * 64;
+  for (int ww = 0; ww < kRangeWaves; ++ww) {
+    const int f = s_fl[ww];
+    if (!(f & kPartLive)) break;   // parts past the range's end
+    last_fl = f;
+    if (f & kPartThrough) {        // the whole part continues the open row
+      run.merge(s_tail[ww][lane]);
+      rcnt += s_tcnt[ww];
+      continue;
+    }
+    if (f & kPartOpenStart) {      // the open row ends inside this part
+      run.merge(s_head[ww][lane]);
+      rcnt += s_hcnt[ww];
+      if (from_start) {
+        heads[static_cast<int64_t>(seg) * 64 + lane] = run.pack();
+        if (lane == 0) rflags[n_rseg + seg] = static_cast<uint64_t>(rcnt);
+      } else {
+        store_row(rrow, run, rcnt);
+      }
+      from_start = false;
+    }
+    if (f & kPartOpenEnd) {
+      run.reset();
+      run.merge(s_tail[ww][lane]);
+      rcnt = s_tcnt[ww];
+      rrow = s_trow[ww];
+    }
   }
-  if (t == n_tiles - 1) seg_empty_rows<MEAN>(out, argmax, static_cast<int64_t>(last) + 1, n_out, C, col, act, E);
+  uint64_t tf = any_bad ? kSegBad : 0;
+  if (last_fl & kPartOpenEnd) {
+    tails[static_cast<int64_t>(seg) * 64 + lane] = run.pack();
+    tf |= (from_start ? kSegThrough : kSegPiece) | (static_cast<uint64_t>(min(max(rrow, 0), n_out - 1)) << 31) |
+          static_cast<uint64_t>(rcnt);
+  }
+  if (lane == 0) rflags[seg] = tf;
 }
 
-// One wavefront per kFixTiles consecutive tiles (t0 ..) of one channel
-// block.  One batch of loads brings everything the common case needs: lane
-// l's tail flag of tile t0 + l (64 flags), the head flags of tiles t0 + 1 ..
-// t0 + kFixTiles, and the tail pieces of tiles t0 .. and head pieces of
-// tiles t0 + 1 .. (kFixTiles each, staged in LDS).  An owner is a tile whose
-// tail piece starts a crossing row; a ballot over the through tiles gives
-// the tile te where its row ends.  Each owner's row is folded in tile order
-// from LDS and written; pieces beyond the staged ones (rows that run past
-// the window) are loaded on the way.  Also raises the status word for bad
-// indices.
-#ifndef SSLA_SR_FIX_TILES
-#define SSLA_SR_FIX_TILES 8
-#endif
-constexpr int kFixTiles = SSLA_SR_FIX_TILES;   // tiles per fixup wavefront (<= 64)
-constexpr int kFixWaves = 4;
-// 64-bit value of lane k (a scalar)
-__device__ __forceinline__ uint64_t rl64(uint64_t v, int k) {
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(v), k));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int32_t>(v >> 32), k));
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-template <bool MEAN, bool PERM>
-__global__ __launch_bounds__(64 * kFixWaves) void seg_fixup_kernel(int64_t E, const int32_t *__restrict__ n_valid,
-                                                                   int C, float *__restrict__ out,
-                                                                   int64_t *__restrict__ argmax, int64_t n_seg,
-                                                                   const uint64_t *__restrict__ flags,
-                                                                   const uint64_t *__restrict__ pieces,
-                                                                   int32_t *__restrict__ status) {
-  __shared__ uint64_t st_tail[kFixWaves][kFixTiles][64], st_head[kFixWaves][kFixTiles][64];
+// One wavefront per (range, channel block): a range whose last row
+// continues (state 2) folds the row's pieces -- its tail piece, the ranges
+// the row runs through (state 1) and the head piece of the range where it
+// ends -- in range order and writes the row.  Raises the status word for a
+// bad index.
+template <bool MEAN>
+__global__ __launch_bounds__(64 * kLinkWaves) void seg_link_kernel(int64_t E, int C, int64_t n_out,
+                                                                   float *__restrict__ out,
+                                                                   int64_t *__restrict__ argmax,
+                                                                   const uint64_t *__restrict__ rflags,
+                                                                   const uint64_t *__restrict__ rpieces,
+                                                                   int64_t n_rng, int32_t *__restrict__ status) {
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int ncb = (C + 63) / 64;
-  const int64_t Ev = PERM ? min(max(static_cast<int64_t>(*n_valid), static_cast<int64_t>(0)), E) : E;
-  const int64_t n_tiles = (Ev + kTile - 1) / kTile;
-  const int64_t n_win = (n_tiles + kFixTiles - 1) / kFixTiles;
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * kFixWaves + w;
-  const int64_t win = q / ncb;
-  if (win >= n_win) return;   // wavefront-uniform
-  const int cb = static_cast<int>(q - win * ncb);
-  const int64_t t0 = win * kFixTiles;
-  const uint64_t *tails = pieces, *heads = pieces + n_seg * 64;
-  const uint64_t *tail_f = flags, *head_f = flags + n_seg;
-  auto piece = [&](const uint64_t *base, int64_t tile) { return base + (tile * ncb + cb) * 64 + lane; };
-  // the batch (positions past the last tile re-read the last tile, unused)
-  const int64_t j = t0 + lane;
-  const uint64_t f = j < n_tiles ? tail_f[j * ncb + cb] : 0;
-  uint64_t hf = 0;
-  if constexpr (MEAN) hf = lane < kFixTiles && j + 1 < n_tiles ? head_f[(j + 1) * ncb + cb] : 0;
-  uint64_t pt[kFixTiles], ph[kFixTiles];
-#pragma unroll
-  for (int k = 0; k < kFixTiles; ++k) {
-    pt[k] = *piece(tails, min(t0 + k, n_tiles - 1));
-    ph[k] = *piece(heads, min(t0 + 1 + k, n_tiles - 1));
+  const int64_t n_rseg = n_rng * ncb;
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * kLinkWaves + w;
+  if (E == 0 || q >= n_rseg) return;   // wavefront-uniform
+  const int64_t rg = q / ncb;
+  const int cb = static_cast<int>(q - rg * ncb);
+  const uint64_t f = rflags[q];
+  if ((f & kSegBad) && lane == 0) *status = SSLA_ERR_ARG;
+  if (seg_state(f) != 2) return;
+  const uint64_t *tails = rpieces, *heads = rpieces + n_rseg * 64;
+  // te: the first range after rg that is not wholly the row
+  int64_t te = n_rng - 1;
+  for (int64_t j0 = rg + 1; j0 < n_rng; j0 += 64) {
+    const int64_t j = j0 + lane;
+    const uint64_t fj = j < n_rng ? rflags[j * ncb + cb] : 0;
+    const uint64_t stop = __builtin_amdgcn_ballot_w64(j < n_rng && seg_state(fj) != 1);
+    if (stop) {
+      te = j0 + static_cast<int64_t>(__builtin_ctzll(stop));
+      break;
+    }
   }
-  if (!PERM && __builtin_amdgcn_ballot_w64(lane < kFixTiles && (f & kSegBad)) != 0 && lane == 0)
-    *status = SSLA_ERR_ARG;
-  const uint64_t thr = __builtin_amdgcn_ballot_w64(seg_state(f) == 1);
-  uint32_t own =
-      static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(lane < kFixTiles && j < n_tiles && seg_state(f) == 2));
-  if (own == 0) return;
-#pragma unroll
-  for (int k = 0; k < kFixTiles; ++k) {
-    st_tail[w][k][lane] = pt[k];
-    st_head[w][k][lane] = ph[k];
+  SegAcc<MEAN> a;
+  a.reset();
+  a.merge(tails[q * 64 + lane]);
+  int64_t cnt = seg_count(f);
+  for (int64_t m = rg + 1; m < te; ++m) {
+    a.merge(tails[(m * ncb + cb) * 64 + lane]);
+    cnt += seg_count(rflags[m * ncb + cb]);
   }
-  __builtin_amdgcn_wave_barrier();
-  // te of the owner in lane l: the first tile after it that is not through
-  // (-1: the through tiles run past the 64 flags)
-  const uint64_t rest = lane < 63 ? (~thr >> (lane + 1)) : 0;
-  const int64_t te_l = rest ? j + 1 + static_cast<int64_t>(__builtin_ctzll(rest)) : -1;
+  if (te > rg) {
+    a.merge(heads[(te * ncb + cb) * 64 + lane]);
+    cnt += static_cast<int64_t>(rflags[n_rseg + te * ncb + cb] & kMask31);
+  }
   const int col = cb * 64 + lane;
-  const bool act = col < C;
-  const int64_t staged_end = t0 + kFixTiles;   // tails staged for tiles < staged_end, heads for tiles <= staged_end
-  while (own) {   // wavefront-uniform
-    const int k = __builtin_ctz(own);
-    own &= own - 1;
-    const int64_t ts = t0 + k;
-    int64_t te = static_cast<int64_t>(rl64(te_l, k));
-    if (te < 0) {   // through tiles run past the 64 flags: walk on
-      for (int64_t w0 = t0 + 64;; w0 += 64) {
-        const int64_t jj = w0 + lane;
-        const uint64_t ff = jj < n_tiles ? tail_f[jj * ncb + cb] : 0;
-        const uint64_t stop = __builtin_amdgcn_ballot_w64(seg_state(ff) != 1);
-        if (stop) {
-          te = w0 + static_cast<int64_t>(__builtin_ctzll(stop));
-          break;
+  if (col < C) seg_store<MEAN>(out, argmax, seg_row(f) * C + col, a, cnt, E);
+}
+
+// ------------------------------------------------------- bucket_reduce --
+// One workgroup per (chunk, channel block): the chunk's events (at most
+// kChunk consecutive positions of one bucket) go into a 64-row x 64-channel
+// LDS tile with LDS atomics.  Wavefronts take batches of kRedBatch positions
+// in turn: the batch's (event, row) pairs, then its rows (lane = channel,
+// one coalesced 256-byte row load each, all in flight), then one atomic per
+// position.  Batches of 32 keep the kernel at two workgroups per CU, so
+// every chunk of a config-4 call is resident at once.
+constexpr int kRedBatch = 32;
+template <bool MEAN, int CT>
+__global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
+    const float *__restrict__ src, const int2 *__restrict__ perm, const int32_t *__restrict__ off,
+    const int32_t *__restrict__ coff, int32_t NB, int32_t E, int C, int32_t n_out, float *__restrict__ out,
+    int64_t *__restrict__ argmax, uint64_t *__restrict__ parts, int32_t *__restrict__ pcnt) {
+  __shared__ uint64_t tile[kBucketRows][64];   // max keys, or fp64 sums
+  __shared__ int32_t tcnt[kBucketRows];
+  __shared__ int s_b;
+  const int Cc = CT ? CT : C;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int ncb = CT ? 1 : (C + 63) / 64;
+  const int c = static_cast<int>(blockIdx.x) / ncb;
+  const int cb = static_cast<int>(blockIdx.x) - c * ncb;
+  const int32_t n_chunks = coff[NB];
+  if (c >= n_chunks) return;   // workgroup-uniform
+  if (threadIdx.x == 0) {      // the bucket of chunk c: coff is strictly increasing
+    int lo = 0, hi = NB - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (coff[mid] <= c) lo = mid;
+      else hi = mid - 1;
+    }
+    s_b = lo;
+  }
+  for (int i = threadIdx.x; i < kBucketRows * 64; i += 64 * kRedWaves) (&tile[0][0])[i] = 0ull;
+  if (threadIdx.x < kBucketRows) tcnt[threadIdx.x] = 0;
+  __syncthreads();
+  const int b = s_b;
+  const int pb0 = off[b], pb1 = off[b + 1];
+  const int j = c - coff[b], nch = coff[b + 1] - coff[b];
+  const int p0 = min(max(pb0 + j * kChunk, 0), E);
+  const int p1 = min(max(min(p0 + kChunk, pb1), p0), E);
+  const int row0 = b << kBucketShift;
+  const int col = cb * 64 + lane;
+  const bool act = CT ? true : col < C;
+  // this lane's channel (lanes past C re-read the last one, unused)
+  const float *pc = src + (CT ? col : min(col, Cc - 1));
+  // the (event, row) pairs of this wavefront's next batch are loaded while
+  // the current batch's rows are in flight
+  int s = p0 + w * kRedBatch;
+  int2 pr_next = (s < p1 && lane < min(kRedBatch, p1 - s)) ? perm[s + lane] : make_int2(0, row0);
+  for (; s < p1; s += kRedBatch * kRedWaves) {
+    const int ne = min(kRedBatch, p1 - s);
+    const int2 pr = pr_next;
+    const int sn = s + kRedBatch * kRedWaves;
+    const int32_t ev = min(max(pr.x, 0), E - 1);
+    const int32_t rl = (pr.y - row0) & (kBucketRows - 1);
+    float xr[kRedBatch];
+#pragma unroll
+    for (int e = 0; e < kRedBatch; ++e) {
+      const int32_t id = __builtin_amdgcn_readlane(ev, e);   // uniform: the row address is scalar
+      xr[e] = pc[static_cast<int64_t>(id) * Cc];
+    }
+    pr_next = (sn < p1 && lane < min(kRedBatch, p1 - sn)) ? perm[sn + lane] : make_int2(0, row0);
+#pragma unroll
+    for (int e = 0; e < kRedBatch; ++e) {
+      if (e < ne) {
+        const int32_t r = __builtin_amdgcn_readlane(rl, e);
+        if constexpr (MEAN) {
+          if (act) atomicAdd(reinterpret_cast<double *>(&tile[r][lane]), static_cast<double>(xr[e]));
+          if (lane == 0) atomicAdd(&tcnt[r], 1);
+        } else {
+          const uint64_t key = max_key(xr[e], __builtin_amdgcn_readlane(ev, e));
+          if (act && key != 0ull) atomicMax(reinterpret_cast<unsigned long long *>(&tile[r][lane]),
+                                            static_cast<unsigned long long>(key));
         }
       }
     }
-    te = min(te, n_tiles - 1);   // (bad input only)
-    SegAcc<MEAN> a;
-    a.reset();
-    // tail piece of ts, then the through tiles ts+1 .. te-1: staged ones from
-    // LDS, later ones sixteen loads at a time
-    a.merge(st_tail[w][k][lane]);
-    const int64_t m_end = min(te, staged_end);
-    for (int64_t m = ts + 1; m < m_end; ++m) a.merge(st_tail[w][m - t0][lane]);
-    for (int64_t k0 = m_end > ts + 1 ? m_end : ts + 1; k0 < te; k0 += 16) {
-      uint64_t pv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) pv[i] = *piece(tails, min(k0 + i, te - 1));
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (k0 + i < te) a.merge(pv[i]);
+  }
+  __syncthreads();
+  if (nch == 1) {   // the whole bucket: write its rows
+    for (int rr = w; rr < kBucketRows; rr += kRedWaves) {
+      const int row = row0 + rr;
+      if (row >= n_out || !act) continue;
+      const uint64_t v = tile[rr][lane];
+      const int64_t o = static_cast<int64_t>(row) * Cc + col;
+      if constexpr (MEAN) {
+        const int32_t n = tcnt[rr];
+        out[o] = n > 0 ? static_cast<float>(__longlong_as_double(static_cast<long long>(v)) / n) : 0.f;
+      } else {
+        float x = 0.f;
+        int64_t e = E;
+        if (v != 0ull) key_value(v, x, e);
+        out[o] = x;
+        argmax[o] = e;
+      }
     }
-    // head piece of te
-    if (te > ts) a.merge(te <= staged_end ? st_head[w][te - t0 - 1][lane] : *piece(heads, te));
-    int64_t cnt = 0;
+  } else {          // one chunk of a larger bucket: leave the tile
+    uint64_t *pt = parts + (static_cast<int64_t>(c) * ncb + cb) * (kBucketRows * 64);
+    for (int rr = w; rr < kBucketRows; rr += kRedWaves) pt[rr * 64 + lane] = tile[rr][lane];
+    if (cb == 0 && threadIdx.x < kBucketRows) pcnt[static_cast<int64_t>(c) * kBucketRows + threadIdx.x] = tcnt[threadIdx.x];
+  }
+}
+
+// One workgroup per (bucket, channel block) of a multi-chunk bucket: folds
+// the chunks' tiles (keys by max, sums in chunk order) and writes the rows.
+template <bool MEAN>
+__global__ __launch_bounds__(64 * kRedWaves) void bucket_finalize_kernel(
+    const int32_t *__restrict__ coff, int64_t NB, int64_t E, int C, int64_t n_out, float *__restrict__ out,
+    int64_t *__restrict__ argmax, const uint64_t *__restrict__ parts, const int32_t *__restrict__ pcnt) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int ncb = (C + 63) / 64;
+  const int64_t b = blockIdx.x / ncb;
+  const int cb = static_cast<int>(blockIdx.x - b * ncb);
+  if (b >= NB) return;
+  const int64_t c0 = coff[b], c1 = coff[b + 1];
+  if (c1 - c0 <= 1) return;   // written by bucket_reduce
+  const int64_t row0 = b << kBucketShift;
+  const int col = cb * 64 + lane;
+  if (col >= C) return;
+  for (int rr = w; rr < kBucketRows; rr += kRedWaves) {
+    const int64_t row = row0 + rr;
+    if (row >= n_out) break;
+    uint64_t key = 0ull;
+    double sum = 0.0;
+    int64_t n = 0;
+    for (int64_t cc = c0; cc < c1; cc += 4) {   // four tiles' loads in flight
+      uint64_t v[4];
+      int32_t k[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t ch = min(cc + u, c1 - 1);
+        v[u] = parts[(ch * ncb + cb) * (kBucketRows * 64) + rr * 64 + lane];
+        k[u] = MEAN ? pcnt[ch * kBucketRows + rr] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (cc + u < c1) {
+          if constexpr (MEAN) {
+            sum += __longlong_as_double(static_cast<long long>(v[u]));
+            n += k[u];
+          } else {
+            key = v[u] > key ? v[u] : key;
+          }
+        }
+      }
+    }
     if constexpr (MEAN) {
-      // tail piece + through tiles (kTile events each) + head piece
-      const int64_t hck = te <= staged_end ? static_cast<int64_t>(rl64(hf, static_cast<int>(te - t0 - 1)))
-                                           : static_cast<int64_t>(head_f[te * ncb + cb]);
-      cnt = seg_count(rl64(f, k)) + (te - ts - 1) * kTile + (te > ts ? hck : 0);
+      out[row * C + col] = n > 0 ? static_cast<float>(sum / static_cast<double>(n)) : 0.f;
+    } else {
+      float x = 0.f;
+      int64_t e = E;
+      if (key != 0ull) key_value(key, x, e);
+      out[row * C + col] = x;
+      argmax[row * C + col] = e;
     }
-    const int32_t R = seg_row(rl64(f, k));
-    if (act) seg_store<MEAN>(out, argmax, static_cast<int64_t>(R) * C + col, a, cnt, E);
   }
 }
 
@@ -731,56 +954,76 @@ int run_scatter(const float *src, const int64_t *index, int64_t E, int C, int64_
   SSLA_CHECK_ARG(out && (MEAN || argmax), "%s: null output pointer", name);
   SSLA_CHECK_ARG(E == 0 || (src && index), "%s: null input pointer", name);
   SSLA_CHECK_ARG(aligned(src, 4) && aligned(index, 8), "%s: misaligned src or index", name);
+  const int64_t ncb = (C + 63) / 64;
+  // the sorted path addresses each range's rows through a 32-bit buffer
+  // resource (kRange rows of C channels)
+  SSLA_CHECK_ARG(static_cast<int64_t>(kRange) * C * 4 < 0x7fffffff, "%s: C=%d channels too many", name, C);
+  if (sorted) {
+    const int64_t n_rng = n_ranges(E);
+    uint64_t *rflags = reinterpret_cast<uint64_t *>(base + L.rflags);
+    uint64_t *rpieces = reinterpret_cast<uint64_t *>(base + L.rpieces);
+    SSLA_CHECK_ARG(L.n_rseg < 0x7fffffff, "%s: too many events x channel blocks", name);
+    const int32_t E32 = static_cast<int32_t>(E), n32 = static_cast<int32_t>(n_out), r32 = static_cast<int32_t>(L.n_rseg);
+    if (C == 64)
+      hipLaunchKernelGGL((seg_range_kernel<MEAN, 64>), dim3(static_cast<unsigned>(L.n_rseg)), dim3(64 * kRangeWaves),
+                         0, st, src, index, E32, C, n32, out, argmax, rflags, rpieces, r32, status);
+    else
+      hipLaunchKernelGGL((seg_range_kernel<MEAN, 0>), dim3(static_cast<unsigned>(L.n_rseg)), dim3(64 * kRangeWaves),
+                         0, st, src, index, E32, C, n32, out, argmax, rflags, rpieces, r32, status);
+    hipLaunchKernelGGL(seg_link_kernel<MEAN>, dim3(static_cast<unsigned>((L.n_rseg + kLinkWaves - 1) / kLinkWaves)),
+                       dim3(64 * kLinkWaves), 0, st, E, C, n_out, out, argmax, rflags, rpieces, n_rng, status);
+    return launch_status(name);
+  }
+  // unsorted: bucketing by 64-row buckets, then the LDS reduce per chunk
   int32_t *errs = reinterpret_cast<int32_t *>(base + L.errs);
   int32_t *off = reinterpret_cast<int32_t *>(base + L.off);
+  int32_t *coff = reinterpret_cast<int32_t *>(base + L.coff);
   uint64_t *flags = reinterpret_cast<uint64_t *>(base + L.flags);
   int32_t *hist = reinterpret_cast<int32_t *>(base + L.hist);
   int2 *perm = reinterpret_cast<int2 *>(base + L.perm);
-  const int64_t n_scan = scan_blocks(n_out);
-  const bool lds = n_out <= kLdsCells;
+  uint64_t *parts = reinterpret_cast<uint64_t *>(base + L.parts);
+  int32_t *pcnt = reinterpret_cast<int32_t *>(base + L.pcnt);
+  const int64_t NB = L.NB;
+  const int64_t n_scan = scan_blocks(NB);
+  const bool lds = lds_hist(NB);
+  SSLA_CHECK_ARG(L.n_chunks * ncb < 0x7fffffff && NB * ncb < 0x7fffffff, "%s: too many chunks x channel blocks",
+                 name);
   int n_err = 0;
-
-  uint64_t *pieces = reinterpret_cast<uint64_t *>(base + L.pieces);
-  const int64_t g = std::max<int64_t>(1, (L.n_seg + kSegWaves - 1) / kSegWaves);
-  SSLA_CHECK_ARG(L.n_tiles < (1 << 29) && g < 0x7fffffff, "%s: too many events x channel blocks", name);
-  uint64_t *seg_flags = reinterpret_cast<uint64_t *>(base + L.seg_flags);
-  const int64_t gf =
-      std::max<int64_t>(1, ((L.n_tiles + kFixTiles - 1) / kFixTiles * ((C + 63) / 64) + kFixWaves - 1) / kFixWaves);
-  auto segments = [&](auto red, auto fix, const int2 *perm_p, const int32_t *n_valid) {
-    hipLaunchKernelGGL(red, dim3(static_cast<unsigned>(g)), dim3(64 * kSegWaves), 0, st, src, index, perm_p,
-                       n_valid, E, C, n_out, out, argmax, L.n_seg, seg_flags, pieces, status);
-    hipLaunchKernelGGL(fix, dim3(static_cast<unsigned>(gf)), dim3(64 * kFixWaves), 0, st, E, n_valid, C, out, argmax, L.n_seg,
-                       seg_flags, pieces, status);
-  };
-  if (sorted) {
-    segments(seg_reduce_kernel<MEAN, false>, seg_fixup_kernel<MEAN, false>, nullptr, nullptr);
-    return launch_status(name);
-  }
-  // unsorted: counting sort of the events by row, then the same segments
-  // over the sorted positions
   if (lds) {
-    hipLaunchKernelGGL((hist_kernel<true>), dim3(L.n_hist), dim3(kEvThreads), 0, st, index, E, n_out, L.n_hist,
+    hipLaunchKernelGGL((hist_kernel<true>), dim3(L.n_hist), dim3(kEvThreads), 0, st, index, E, n_out, NB, L.n_hist,
                        hist, errs, ticket, flags, n_scan + 1);
     n_err = L.n_hist;
   } else {
-    hipLaunchKernelGGL(fill_i32, dim3(static_cast<unsigned>(std::min<int64_t>(1024, (n_out + 256) / 256))),
-                       dim3(256), 0, st, hist, n_out + 1, 0);
+    hipLaunchKernelGGL(fill_i32, dim3(static_cast<unsigned>(std::min<int64_t>(1024, (NB + 256) / 256))), dim3(256),
+                       0, st, hist, NB + 1, 0);
     const int nb = global_hist_blocks(E);
-    hipLaunchKernelGGL((hist_kernel<false>), dim3(nb), dim3(kEvThreads), 0, st, index, E, n_out, 1, hist, errs,
+    hipLaunchKernelGGL((hist_kernel<false>), dim3(nb), dim3(kEvThreads), 0, st, index, E, n_out, NB, 1, hist, errs,
                        ticket, flags, n_scan + 1);
     n_err = nb;
   }
   hipLaunchKernelGGL(scan_kernel, dim3(static_cast<unsigned>(n_scan)), dim3(kScanCells * kScanTpc), 0, st, hist,
-                     L.n_hist, n_out, off, ticket, flags, errs, n_err, status);
+                     L.n_hist, NB, off, coff, ticket, flags, errs, n_err, status);
   if (lds) {
-    hipLaunchKernelGGL((bucket_kernel<true>), dim3(L.n_hist), dim3(kEvThreads), 0, st, index, E, n_out, L.n_hist,
-                       off, hist, perm);
+    hipLaunchKernelGGL((bucket_kernel<true>), dim3(L.n_hist), dim3(kEvThreads), 0, st, index, E, n_out, NB,
+                       L.n_hist, off, hist, perm);
   } else {
     const int nb = global_hist_blocks(E);
-    hipLaunchKernelGGL((bucket_kernel<false>), dim3(nb), dim3(kEvThreads), 0, st, index, E, n_out, 1, off, hist,
+    hipLaunchKernelGGL((bucket_kernel<false>), dim3(nb), dim3(kEvThreads), 0, st, index, E, n_out, NB, 1, off, hist,
                        perm);
   }
-  segments(seg_reduce_kernel<MEAN, true>, seg_fixup_kernel<MEAN, true>, perm, off + n_out);
+  {
+    const int32_t E32 = static_cast<int32_t>(E), n32 = static_cast<int32_t>(n_out), NB32 = static_cast<int32_t>(NB);
+    if (C == 64)
+      hipLaunchKernelGGL((bucket_reduce_kernel<MEAN, 64>), dim3(static_cast<unsigned>(L.n_chunks * ncb)),
+                         dim3(64 * kRedWaves), 0, st, src, perm, off, coff, NB32, E32, C, n32, out, argmax, parts,
+                         pcnt);
+    else
+      hipLaunchKernelGGL((bucket_reduce_kernel<MEAN, 0>), dim3(static_cast<unsigned>(L.n_chunks * ncb)),
+                         dim3(64 * kRedWaves), 0, st, src, perm, off, coff, NB32, E32, C, n32, out, argmax, parts,
+                         pcnt);
+  }
+  hipLaunchKernelGGL(bucket_finalize_kernel<MEAN>, dim3(static_cast<unsigned>(NB * ncb)), dim3(64 * kRedWaves), 0,
+                     st, coff, NB, E, C, n_out, out, argmax, parts, pcnt);
   return launch_status(name);
 }
 
