@@ -15,8 +15,8 @@ widths (multiples of 16 up to 256) run as groups of 64 keys, the last one
 zero-padded -- the decay is per key, so each key group is an independent
 GLA whose outputs add up (o = sum of the groups' o, ht = the groups' rows).
 ``chunk_gla`` is differentiable (:class:`ChunkGLAFunction`, backward
-``ssla_gla_chunk_bwd``) for the shapes the backward kernels take (bf16/fp16,
-V a multiple of 16 up to 64); the recurrent form is forward-only.  Layouts are the
+``ssla_gla_chunk_bwd``, run in groups of 64 keys by 64 value columns) for
+K and V multiples of 16 up to 256; the recurrent form is forward-only.  Layouts are the
 reference's packed varlen layouts: q, k, g ``[T, H, K]``, v ``[T, H, V]``,
 ``cu_seqlens`` int64 ``[N + 1]``, states ``[N, H, K, V]`` fp32.
 """
@@ -44,10 +44,14 @@ def chunk_kernel_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
             and v.shape[-1] % 16 == 0 and v.shape[-1] <= 256)
 
 
+VD = 64   # value columns of one chunk-backward call
+
+
 def chunk_backward_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
-    """True when ``ssla_gla_chunk_bwd`` handles this dtype/shape (bf16/fp16,
-    K a multiple of 16 up to 256, V a multiple of 16 up to 64)."""
-    return chunk_kernel_supports(q, v) and v.shape[-1] <= 64
+    """True when the chunk backward handles this dtype/shape (bf16/fp16, K
+    and V multiples of 16 up to 256: ``ssla_gla_chunk_bwd`` runs 64 keys by
+    64 value columns, wider K and V run as groups of those)."""
+    return chunk_kernel_supports(q, v)
 
 
 def _key_groups(K: int):
@@ -129,7 +133,7 @@ def chunk_gla(
     if grad:
         if not chunk_backward_supports(q, v):
             raise NotImplementedError(
-                "chunk_gla backward needs bf16/fp16 inputs with K a multiple of 16 up to 256 and V a multiple of 16 up to 64 "
+                "chunk_gla backward needs K and V multiples of 16 up to 256 "
                 f"(got {q.dtype}, K={q.shape[-1]}, V={v.shape[-1]})")
         return ChunkGLAFunction.apply(q, k, v, g, float(scale), h0, output_final_state, cu)
     return _chunk_fwd(q, k, v, g, cu, float(scale), h0, output_final_state)
@@ -197,19 +201,43 @@ class ChunkGLAFunction(torch.autograd.Function):
         q, k, v, g, h0, cu = ctx.saved_tensors
         do = do.to(v.dtype).contiguous()
         dht = None if dht is None else dht.to(torch.float32).contiguous()
-        K = q.shape[-1]
-        if K == KD:
-            dq, dk, dv, dg, dh0 = _chunk_bwd_call(q, k, v, g, h0, cu, do, dht, ctx.scale)
+        V = v.shape[-1]
+        if V <= VD:
+            dq, dk, dv, dg, dh0 = _bwd_keys(q, k, v, g, h0, cu, do, dht, ctx.scale)
             return dq, dk, dv, dg, None, dh0, None, None
-        # key groups: each group's gradients are its keys' rows; dv adds up
-        parts = [_chunk_bwd_call(_keys_of(q, s, w, 2), _keys_of(k, s, w, 2), v, _keys_of(g, s, w, 2),
-                                 _keys_of(h0, s, w, 2), cu, do, _keys_of(dht, s, w, 2), ctx.scale)
-                 for s, w in _key_groups(K)]
-        widths = [w for _, w in _key_groups(K)]
-        cat = lambda i, dim: torch.cat([p[i].narrow(dim, 0, w) for p, w in zip(parts, widths)], dim=dim)
-        dv = parts[0][2] if len(parts) == 1 else torch.stack([p[2] for p in parts]).float().sum(0).to(v.dtype)
-        dh0 = cat(4, 2) if h0 is not None else None
-        return cat(0, 2), cat(1, 2), dv, cat(3, 2), None, dh0, None, None
+        # value groups: each state column evolves on its own (the decay acts
+        # on keys), so the V groups are independent GLAs sharing q, k, g;
+        # their dq, dk, dg add up (in fp32, rounded once), dv and dh0 are the
+        # groups' columns
+        parts = [_bwd_keys(q, k, v[..., s:s + w].contiguous(), g, None if h0 is None else h0[..., s:s + w].contiguous(),
+                           cu, do[..., s:s + w].contiguous(), None if dht is None else dht[..., s:s + w].contiguous(),
+                           ctx.scale)
+                 for s, w in _value_groups(V)]
+        add = lambda i, like: torch.stack([p[i].float() for p in parts]).sum(0).to(like.dtype)   # noqa: E731
+        dh0 = torch.cat([p[4] for p in parts], dim=3) if h0 is not None else None
+        return (add(0, q), add(1, k), torch.cat([p[2] for p in parts], dim=2), add(3, g), None, dh0, None, None)
+
+
+def _value_groups(V: int):
+    """(first column, columns) of the 64-column groups that cover V."""
+    return [(s, min(VD, V - s)) for s in range(0, V, VD)]
+
+
+def _bwd_keys(q, k, v, g, h0, cu, do, dht, scale):
+    """dq, dk, dv, dg, dh0 of one value group (V <= VD): one
+    ssla_gla_chunk_bwd call per group of 64 keys."""
+    K = q.shape[-1]
+    if K == KD:
+        return _chunk_bwd_call(q, k, v, g, h0, cu, do, dht, scale)
+    # key groups: each group's gradients are its keys' rows; dv adds up
+    parts = [_chunk_bwd_call(_keys_of(q, s, w, 2), _keys_of(k, s, w, 2), v, _keys_of(g, s, w, 2),
+                             _keys_of(h0, s, w, 2), cu, do, _keys_of(dht, s, w, 2), scale)
+             for s, w in _key_groups(K)]
+    widths = [w for _, w in _key_groups(K)]
+    cat = lambda i, dim: torch.cat([p[i].narrow(dim, 0, w) for p, w in zip(parts, widths)], dim=dim)   # noqa: E731
+    dv = parts[0][2] if len(parts) == 1 else torch.stack([p[2] for p in parts]).float().sum(0).to(v.dtype)
+    dh0 = cat(4, 2) if h0 is not None else None
+    return cat(0, 2), cat(1, 2), dv, cat(3, 2), dh0
 
 
 def _chunk_bwd_call(q, k, v, g, h0, cu, do, dht, scale):

@@ -228,8 +228,11 @@ def test_chunk_errors(dev):
     o, _ = chunk_gla(qg, k.to(dev), v.to(dev), g.to(dev), cu.to(dev))
     assert o.requires_grad   # V = 64 has a backward
     v128 = torch.randn(30, 2, 128, dtype=torch.bfloat16, device=dev)
-    with pytest.raises(NotImplementedError):   # V > 64 has none
-        chunk_gla(qg, k.to(dev), v128, g.to(dev), cu.to(dev))
+    o, _ = chunk_gla(qg, k.to(dev), v128, g.to(dev), cu.to(dev))
+    assert o.requires_grad   # so has V = 128 (two value groups)
+    v300 = torch.randn(30, 2, 300, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(NotImplementedError):   # V above 256 has none
+        chunk_gla(qg, k.to(dev), v300, g.to(dev), cu.to(dev))
 
 
 def test_recurrent_returns_sequence_rows(dev):

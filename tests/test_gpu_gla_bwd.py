@@ -41,6 +41,9 @@ BANDS = {
               "dh0": (6.9e-5, 3.7e-6)},
     "16-bit g fp16": {"dq": (0.02, 4.3e-4), "dk": (0.016, 4.1e-4), "dv": (8.4e-3, 4.2e-4), "dg": (0.016, 3.8e-4),
                       "dh0": (3.6e-4, 6.8e-6)},
+    # value groups: the bf16 bands of the logsig case (one more rounding
+    # of dq, dk, dg, which add up over the groups in fp32)
+    "value groups": _B16,
 }
 
 
@@ -121,10 +124,19 @@ def test_chunk_bwd_key_widths(dev, K):
            scale=K ** -0.5)
 
 
+@pytest.mark.parametrize("K,V", [(64, 128), (64, 80), (32, 256), (128, 128)])
+def test_chunk_bwd_value_widths(dev, K, V):
+    """V above 64: the backward runs per group of 64 value columns (each
+    state column evolves on its own), dq, dk, dg add up over the groups and
+    dv, dh0 are their columns; K above 64 adds the key groups inside."""
+    _check(dev, [0, 1, 63, 64, 65, 200, 7], 2, V, torch.bfloat16, seed=K + V, tag=f"K={K} V={V}", case="value groups",
+           K=K, scale=K ** -0.5)
+
+
 def test_chunk_bwd_unsupported_raises(dev):
     from ssla_amd.gla import chunk_gla
     q = torch.randn(10, 1, 64, device=dev, dtype=torch.bfloat16, requires_grad=True)
-    v = torch.randn(10, 1, 128, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(10, 1, 272, device=dev, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
         chunk_gla(q, q.detach(), v, torch.zeros(10, 1, 64, device=dev), torch.tensor([0, 10], device=dev))
 
