@@ -117,6 +117,30 @@ int ssla_gla_chunk_fwd_noalloc(const void *q, const void *k, const void *v,
                                const float *h0, void *o, float *ht, int dtype,
                                void *stream);
 
+/* Chunked GLA in fp32: the forward and backward that chunk_gla runs for
+ * fp32 inputs (reference chunk_gla_fwd / chunk_gla_bwd, ops/gla/chunk.py
+ * 906-960 and 963-1053, which take any float dtype; the reference's dots
+ * use TF32 operands, here every product is fp32).  q, k, g fp32 [T, H, K],
+ * v fp32 [T, H, V], states fp32 [N, H, K, V] (h0 / ht / dht may be NULL),
+ * o, dq, dk, dv, dg fp32 in the input layouts; rows outside
+ * [cu_seqlens[0], cu_seqlens[n_seq]) are not written.  Chunks of 64 rows,
+ * walked in order per (sequence, head): no serial walk over time steps.
+ * Forward: K <= 64, V <= 256 per call (wider K: groups of 64 keys whose o
+ * add up).  Backward: K, V <= 64 per call (wider K or V: groups of 64 keys
+ * or value columns, as for the bf16 backward); dh0 is required with h0.
+ * Workspace of the backward: ssla_gla_chunk_f32_bwd_workspace_size bytes
+ * (every chunk's entering state; no initialisation needed); cu_seqlens
+ * must be non-decreasing. */
+int ssla_gla_chunk_f32_fwd(const float *q, const float *k, const float *v, const float *g,
+                           const int64_t *cu_seqlens, int n_seq, int64_t T, int H, int K, int V,
+                           float scale, const float *h0, float *o, float *ht, void *stream);
+size_t ssla_gla_chunk_f32_bwd_workspace_size(int n_seq, int64_t T, int H);
+int ssla_gla_chunk_f32_bwd(const float *q, const float *k, const float *v, const float *g,
+                           const int64_t *cu_seqlens, int n_seq, int64_t T, int H, int K, int V,
+                           float scale, const float *h0, const float *dout, const float *dht, float *dq,
+                           float *dk, float *dv, float *dg, float *dh0, void *workspace,
+                           size_t workspace_bytes, void *stream);
+
 /* Backward of ssla_gla_chunk_fwd: ChunkGLAFunction.backward /
  * chunk_gla_bwd (reference ops/gla/chunk.py:1096-1116, 963-1053, with
  * chunk_bwd_dh, ops/common/chunk_h.py:145-239).  dout [T, H, V] (dtype of

@@ -43,6 +43,11 @@ SIGNATURES = {
                                   _f32, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
     "ssla_gla_chunk_fwd_noalloc": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32,
                                           _f32, _vp, _vp, _vp, _i32, _vp]),
+    "ssla_gla_chunk_f32_fwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _f32, _vp, _vp, _vp,
+                                       _vp]),
+    "ssla_gla_chunk_f32_bwd_workspace_size": (_sz, [_i32, _i64, _i32]),
+    "ssla_gla_chunk_f32_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _f32, _vp, _vp, _vp,
+                                       _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ssla_gla_chunk_bwd_workspace_size": (_sz, [_i32, _i64, _i32, _i32, _i32]),
     "ssla_gla_chunk_bwd": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i32, _i32, _i32, _f32, _vp,
                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),

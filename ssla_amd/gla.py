@@ -15,8 +15,10 @@ widths (multiples of 16 up to 256) run as groups of 64 keys, the last one
 zero-padded -- the decay is per key, so each key group is an independent
 GLA whose outputs add up (o = sum of the groups' o, ht = the groups' rows).
 ``chunk_gla`` is differentiable (:class:`ChunkGLAFunction`, backward
-``ssla_gla_chunk_bwd``, run in groups of 64 keys by 64 value columns) for
-K and V multiples of 16 up to 256; the recurrent form is forward-only.  Layouts are the
+``ssla_gla_chunk_bwd`` / ``ssla_gla_chunk_f32_bwd``, run in groups of 64
+keys by 64 value columns) for the shapes the chunk kernels take; fp32
+inputs run fp32 chunk kernels in both directions.  The recurrent form is
+forward-only.  Layouts are the
 reference's packed varlen layouts: q, k, g ``[T, H, K]``, v ``[T, H, V]``,
 ``cu_seqlens`` int64 ``[N + 1]``, states ``[N, H, K, V]`` fp32.
 """
@@ -36,12 +38,15 @@ KD = 64   # keys of one chunk-kernel call
 
 
 def chunk_kernel_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
-    """True when the fused MFMA chunk kernels handle this dtype/shape
-    (bf16/fp16, K a multiple of 16 up to 256 -- run in groups of 64 keys --
-    and V a multiple of 16 up to 256)."""
-    K = q.shape[-1]
+    """True when the chunk kernels handle this dtype/shape: bf16/fp16 with K
+    a multiple of 16 up to 256 (run in groups of 64 keys) and V a multiple
+    of 16 up to 256 (the fused MFMA kernels), or fp32 with K and V up to
+    256 (the fp32 chunk kernels, ``ssla_gla_chunk_f32_*``)."""
+    K, V = q.shape[-1], v.shape[-1]
+    if q.dtype == torch.float32:
+        return 0 < K <= 256 and 0 < V <= 256
     return (q.dtype in (torch.bfloat16, torch.float16) and K % 16 == 0 and 0 < K <= 256
-            and v.shape[-1] % 16 == 0 and v.shape[-1] <= 256)
+            and V % 16 == 0 and V <= 256)
 
 
 VD = 64   # value columns of one chunk-backward call
@@ -117,8 +122,9 @@ def chunk_gla(
     reference (``torch.empty_like``).
 
     bf16/fp16 inputs with K a multiple of 16 up to 256 run the fused MFMA
-    chunk kernels (in groups of 64 keys); other shapes and fp32 inputs run
-    the fused recurrent kernel (same math, fp32 state, serial over time).
+    chunk kernels (in groups of 64 keys); fp32 inputs run the fp32 chunk
+    kernels (chunks of 64 rows, fp32 products); other shapes run the fused
+    recurrent kernel (same math, fp32 state, serial over time).
     """
     if initial_state is not None and initial_state.shape[0] != len(cu_seqlens) - 1:
         raise ValueError(
@@ -149,10 +155,10 @@ def _chunk_fwd(q, k, v, g, cu, scale, h0, output_final_state):
         o = torch.empty_like(v)
         ht = torch.empty(N, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
         return _recurrent(q, k, v, g, cu, float(scale), h0, o, ht, None, 0)
-    if K == KD:
+    if K == KD or (q.dtype == torch.float32 and K <= KD):
         return _chunk_call(q, k, v, g, cu, scale, h0, output_final_state)
-    # key groups: o adds up over the groups (in fp32, rounded once more),
-    # ht stacks their key rows
+    # key groups: o adds up over the groups (in fp32, rounded once more for
+    # 16-bit inputs), ht stacks their key rows
     os, hts = [], []
     for s, w in _key_groups(K):
         o_i, ht_i = _chunk_call(_keys_of(q, s, w, 2), _keys_of(k, s, w, 2), v, _keys_of(g, s, w, 2), cu, scale,
@@ -165,13 +171,19 @@ def _chunk_fwd(q, k, v, g, cu, scale, h0, output_final_state):
 
 
 def _chunk_call(q, k, v, g, cu, scale, h0, output_final_state):
-    """One ssla_gla_chunk_fwd call (K == KD)."""
+    """One ssla_gla_chunk_fwd call (K == KD), or one ssla_gla_chunk_f32_fwd
+    call for fp32 inputs (K <= KD)."""
     T, H, K = q.shape
     V = v.shape[-1]
     N = cu.numel() - 1
     o = torch.empty_like(v)
     ht = torch.empty(N, H, K, V, device=q.device, dtype=torch.float32) if output_final_state else None
     lib = _lib.load()
+    if q.dtype == torch.float32:
+        st = lib.ssla_gla_chunk_f32_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(cu), N, T, H, K,
+                                        V, float(scale), _lib.ptr(h0), _lib.ptr(o), _lib.ptr(ht), _lib.stream_of(q))
+        _lib.check(st, "ssla_gla_chunk_f32_fwd")
+        return o, ht
     ws_bytes = lib.ssla_gla_chunk_workspace_size(N, T, H, K, V)
     ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8) if ws_bytes else None
     st = lib.ssla_gla_chunk_fwd(
@@ -227,7 +239,7 @@ def _bwd_keys(q, k, v, g, h0, cu, do, dht, scale):
     """dq, dk, dv, dg, dh0 of one value group (V <= VD): one
     ssla_gla_chunk_bwd call per group of 64 keys."""
     K = q.shape[-1]
-    if K == KD:
+    if K == KD or (q.dtype == torch.float32 and K <= KD):
         return _chunk_bwd_call(q, k, v, g, h0, cu, do, dht, scale)
     # key groups: each group's gradients are its keys' rows; dv adds up
     parts = [_chunk_bwd_call(_keys_of(q, s, w, 2), _keys_of(k, s, w, 2), v, _keys_of(g, s, w, 2),
@@ -241,7 +253,8 @@ def _bwd_keys(q, k, v, g, h0, cu, do, dht, scale):
 
 
 def _chunk_bwd_call(q, k, v, g, h0, cu, do, dht, scale):
-    """One ssla_gla_chunk_bwd call (K == KD): dq, dk, dv, dg, dh0."""
+    """One ssla_gla_chunk_bwd call (K == KD), or one ssla_gla_chunk_f32_bwd
+    call for fp32 inputs: dq, dk, dv, dg, dh0."""
     T, H, K = q.shape
     V = v.shape[-1]
     N = cu.numel() - 1
@@ -249,6 +262,19 @@ def _chunk_bwd_call(q, k, v, g, h0, cu, do, dht, scale):
     dv, dg = torch.empty_like(v), torch.empty_like(g)
     dh0 = torch.empty_like(h0) if h0 is not None else None
     lib = _lib.load()
+    if q.dtype == torch.float32:
+        g32 = g if g.dtype == torch.float32 else g.float()
+        dg32 = dg if dg.dtype == torch.float32 else torch.empty_like(g32)
+        ws_bytes = lib.ssla_gla_chunk_f32_bwd_workspace_size(N, T, H)
+        ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+        st = lib.ssla_gla_chunk_f32_bwd(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g32), _lib.ptr(cu), N, T, H, K, V, float(scale),
+            _lib.ptr(h0), _lib.ptr(do), _lib.ptr(dht), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg32),
+            _lib.ptr(dh0), _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
+        _lib.check(st, "ssla_gla_chunk_f32_bwd")
+        if dg32 is not dg:
+            dg.copy_(dg32)
+        return dq, dk, dv, dg, dh0
     ws_bytes = lib.ssla_gla_chunk_bwd_workspace_size(N, T, H, K, V)
     ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
     st = lib.ssla_gla_chunk_bwd(

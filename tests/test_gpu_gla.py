@@ -308,3 +308,38 @@ def test_chunk_sequence_size_limit(dev):
     print("chunk size limit: one sequence of 131072 rows", flush=True)
     with pytest.raises(NotImplementedError, match="2\\^31"):
         chunk_gla(q, q, q, g, torch.tensor([0, 2 * n], device=dev), scale=1.0, initial_state=h0[:1])
+
+
+@pytest.mark.parametrize("K,V", [(64, 64), (32, 48), (16, 16), (128, 80), (64, 256)])
+@pytest.mark.parametrize("gate", ["logsig", "randn-1", "strong", "zero"])
+def test_chunk_fp32(dev, K, V, gate):
+    """fp32 chunk_gla (ssla_gla_chunk_f32_fwd: chunks of 64 rows restarting
+    at every sequence start, fp32 products) on ragged sequences (empty, 1,
+    chunk - 1, chunk, chunk + 1, long) in every gate regime, with an initial
+    state: o and the final state against the fp64 recurrence at the fp32
+    bar (rtol 1e-4, atol 1e-4 of the RMS)."""
+    from ssla_amd.gla import chunk_gla
+    q, k, v, g, cu, s0 = _inputs([0, 1, 63, 64, 65, 200, 7], 3, K, V, torch.float32, seed=K + V, gate=gate)
+    print(f"fp32 chunk K={K} V={V} gate={gate}", flush=True)
+    o, ht = _run(chunk_gla, q, k, v, g, cu, s0, K ** -0.5, dev)
+    ro, rht = _oracle(q, k, v, g, cu, s0, K ** -0.5)
+    assert_close(o, ro, RTOL_F32, f"fp32 chunk o K={K} V={V} {gate}")
+    assert_close(ht, rht, RTOL_F32, f"fp32 chunk ht K={K} V={V} {gate}")
+
+
+def test_chunk_fp32_c2_shape(dev):
+    """Config 2's shape in fp32 (B=8, H=8, T=4096, K=V=64, h0 ~ N(0, 0.1)):
+    the fp32 chunk kernels walk 64 chunks per sequence instead of 4096
+    steps; o and ht against the fp64 recurrence at the fp32 bar."""
+    from ssla_amd import synthetic
+    from ssla_amd.gla import chunk_gla
+    x = synthetic.chunk_gla_inputs()
+    q, k, v = (x[n].float() for n in ("q", "k", "v"))
+    print("fp32 chunk at the C2 shape", flush=True)
+    with torch.no_grad():
+        o, ht = chunk_gla(q.to(dev), k.to(dev), v.to(dev), x["g"].to(dev), x["cu_seqlens"].to(dev),
+                          scale=x["scale"], initial_state=x["initial_state"].to(dev), output_final_state=True)
+    ro, rht = oracle.gla_recurrent(q.numpy(), k.numpy(), v.numpy(), x["g"].numpy(), x["cu_seqlens"].numpy(),
+                                   x["scale"], x["initial_state"].numpy(), True)
+    assert_close(o.cpu().numpy(), ro, RTOL_F32, "fp32 chunk o (C2 shape)")
+    assert_close(ht.cpu().numpy(), rht, RTOL_F32, "fp32 chunk ht (C2 shape)")

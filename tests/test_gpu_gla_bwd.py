@@ -177,3 +177,33 @@ def test_chunk_bwd_all_sequences_empty(dev):
     o, _ = chunk_gla(z[0], z[1], z[2], g, cu, initial_state=h0b, output_final_state=False)
     torch.autograd.backward([o], [torch.zeros_like(o)])
     assert h0b.grad is not None and not h0b.grad.any()
+
+
+@pytest.mark.parametrize("K,V", [(64, 64), (32, 48), (128, 128)])
+@pytest.mark.parametrize("gate", ["logsig", "randn-1", "strong", "zero"])
+def test_chunk_bwd_fp32(dev, K, V, gate):
+    """fp32 backward (ssla_gla_chunk_f32_bwd, in groups of 64 keys by 64
+    value columns): dq, dk, dv, dg, dh0 of o and the final state against the
+    fp64 recurrent backward at the fp32 bar (rtol 1e-4, atol 1e-4 of each
+    gradient's RMS)."""
+    q, k, v, g, cu, s0, do, dht = _inputs([0, 1, 63, 64, 65, 200, 7], 2, V, torch.float32, seed=K + V, gate=gate, K=K)
+    scale = K ** -0.5
+    print(f"gla bwd fp32 K={K} V={V} gate={gate}", flush=True)
+    got = _gpu_grads(dev, q, k, v, g, cu, s0, do, dht, scale)
+    ref = oracle.gla_recurrent_bwd(q.numpy(), k.numpy(), v.numpy(), g.numpy(), cu.numpy(), do.numpy(), scale,
+                                   s0.numpy(), dht.numpy())
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dh0"), got, ref):
+        assert_close(a, b, 1e-4, f"fp32 {name} K={K} V={V} {gate}")
+
+
+def test_chunk_bwd_fp32_long(dev):
+    """Two 4096-token fp32 sequences (64 chunks each), H = 4, without an
+    initial state: the backward's forward pass and reverse walk carry 64
+    chunks."""
+    q, k, v, g, cu, s0, do, dht = _inputs([4096, 4096], 4, 64, torch.float32, seed=6, h0=False)
+    print("gla bwd fp32 long", flush=True)
+    got = _gpu_grads(dev, q, k, v, g, cu, s0, do, dht, 64 ** -0.5)
+    ref = oracle.gla_recurrent_bwd(q.numpy(), k.numpy(), v.numpy(), g.numpy(), cu.numpy(), do.numpy(), 64 ** -0.5)
+    for name, a, b in zip(("dq", "dk", "dv", "dg"), got, ref):
+        assert_close(a, b, 1e-4, f"fp32 long {name}")
+    assert got[4] is None and ref[4] is None
