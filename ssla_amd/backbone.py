@@ -44,7 +44,7 @@ from . import events as E
 from .layers import SparseMaxPool
 from .scan import sparse_gla_scan
 
-__all__ = ["SiteGLABlock", "DetectionHead", "AsyncSparseGLA", "STAGES"]
+__all__ = ["SiteGLABlock", "DetectionHead", "AsyncSparseGLA", "WindowPlan", "STAGES"]
 
 # (channels, stride) of the four stages
 STAGES: Tuple[Tuple[int, int], ...] = ((32, 4), (64, 8), (128, 16), (256, 32))
@@ -338,6 +338,21 @@ class DetectionHead(nn.Module):
         return torch.cat(outs, 1)
 
 
+class WindowPlan:
+    """The structure of one window (AsyncSparseGLA.plan): the preprocessed
+    pixel groups and the pooling plans of the stem and stages 1-3."""
+    __slots__ = ("grouped", "pools")
+
+    def __init__(self, grouped: Dict[str, torch.Tensor], pools: List["E.PoolPlan"]):
+        self.grouped, self.pools = grouped, pools
+
+    def tensors(self) -> List[torch.Tensor]:
+        out = [v for v in self.grouped.values() if isinstance(v, torch.Tensor)]
+        for p in self.pools:
+            out += p.tensors()
+        return out
+
+
 class AsyncSparseGLA(nn.Module):
     """Stem, four per-site GLA stages with pooling, dense grids and the
     detection head.  ``forward(events, lengths, states)`` runs one window
@@ -377,8 +392,20 @@ class AsyncSparseGLA(nn.Module):
         return [torch.zeros(batch_size * Hg * Wg, self.heads, D, D, dtype=torch.float32, device=device)
                 for Hg, Wg in self.grid_sizes]
 
-    def stem(self, events: torch.Tensor, lengths: torch.Tensor) -> Dict[str, torch.Tensor]:
+    def plan(self, events: torch.Tensor, lengths: torch.Tensor) -> "WindowPlan":
+        """Everything of a window that depends only on its events'
+        coordinates and times: the pixel groups with their <dt, p> features
+        (preprocess_inputs) and the pooling plans and pooled structure of the
+        stem and of stages 1-3 (the per-site stages keep the structure).  All
+        of the window's reads of device counts happen here, so ``forward``
+        with this plan enqueues its work without waiting on the device."""
         gr = E.preprocess_inputs(events, lengths, self.frame_size, self.hot_pixel_thres)
+        pools = [self.stem_pool.plan(gr)]
+        for pool in self.pools:
+            pools.append(pool.plan(pools[-1].structure))
+        return WindowPlan(gr, pools)
+
+    def _embed(self, gr: Dict[str, torch.Tensor]) -> torch.Tensor:
         w = self.embed.weight
         key = (w.data_ptr(), w._version, w.device)
         cache = getattr(self, "_embed_bf16", None)
@@ -388,14 +415,26 @@ class AsyncSparseGLA(nn.Module):
             with torch.no_grad():
                 cache = (key, w.detach().to(torch.bfloat16))
             self._embed_bf16 = cache
-        gr["events"] = F.linear(gr["events"].to(torch.bfloat16), cache[1]).float()
+        return F.linear(gr["events"].to(torch.bfloat16), cache[1]).float()
+
+    def stem(self, events: torch.Tensor, lengths: torch.Tensor) -> Dict[str, torch.Tensor]:
+        gr = E.preprocess_inputs(events, lengths, self.frame_size, self.hot_pixel_thres)
+        gr["events"] = self._embed(gr)
         return self.stem_pool(gr)
 
-    def forward(self, events: torch.Tensor, lengths: torch.Tensor, states: List[torch.Tensor], mark=None):
-        """``mark(name)`` (optional) is called after each piece ("stem",
-        "s<i>.project" / ".scan" / ".finish" / ".pool", "grids", "head"): a
-        timing hook that must not touch the tensors."""
-        x = self.stem(events, lengths)
+    def forward(self, events: torch.Tensor, lengths: torch.Tensor, states: List[torch.Tensor], mark=None,
+                plan: "WindowPlan" = None):
+        """``plan`` (from ``plan`` on this window) supplies the groups and the
+        pooled structure, and the call then reads nothing back from the
+        device; without it every stage is planned as it comes.  ``mark(name)``
+        (optional) is called after each piece ("stem", "s<i>.project" /
+        ".scan" / ".finish" / ".pool", "grids", "head"): a timing hook that
+        must not touch the tensors."""
+        # Without a plan each stage's pooling is planned right after the
+        # stage's block is enqueued, so the plan's read of device counts
+        # waits while the GPU runs that block.
+        x = self.stem(events, lengths) if plan is None else \
+            self.stem_pool.apply_plan(plan.pools[0], self._embed(plan.grouped))
         if mark:
             mark("stem")
         feats = []
@@ -403,7 +442,7 @@ class AsyncSparseGLA(nn.Module):
             x = blk(x, states[i], self.grid_sizes[i], mark=(lambda nm, i=i: mark(f"s{i}.{nm}")) if mark else None)
             feats.append(x)
             if i < len(self.pools):
-                x = self.pools[i](x)
+                x = self.pools[i](x) if plan is None else self.pools[i].apply_plan(plan.pools[i + 1], x["events"])
                 if mark:
                     mark(f"s{i}.pool")
         grids = [E.events_to_grid(feats[i], self.grid_sizes[i], self.stages[i][0]) for i in self.head_levels]

@@ -1264,9 +1264,18 @@ __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C
                                int64_t *__restrict__ o_time, int64_t *__restrict__ o_len, int64_t *__restrict__ o_b,
                                int64_t *__restrict__ o_h, int64_t *__restrict__ o_w) {
   // VW consecutive channels per thread (C / VW threads per row; E_out * C
-  // < 2^31, checked by the caller)
+  // < 2^31, checked by the caller).  A null o_ev skips the values (the
+  // structure alone: times, per-field counts and coordinates); a null o_len
+  // skips the per-field outputs (the values, with the times if o_time).
   const uint32_t CV = static_cast<uint32_t>(C / VW);
-  GRID_STRIDE(t, E_out * CV) {
+  if (!o_ev) {
+    if (o_time) {
+      GRID_STRIDE(r, E_out) {
+        const int64_t s = segx[r];
+        if (head[r] && s >= 0 && s < n_seg) o_time[s] = tim[r];
+      }
+    }
+  } else GRID_STRIDE(t, E_out * CV) {
     const uint32_t t32 = static_cast<uint32_t>(t);
     const int64_t r = static_cast<int64_t>(t32 / CV);
     const int c = static_cast<int>(t32 - static_cast<uint32_t>(r) * CV) * VW;
@@ -1315,9 +1324,9 @@ __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C
       if constexpr (MEAN) o_ev[s * C + c + v] = static_cast<float>(sum[v] / static_cast<double>(r2 - r));
       else o_ev[s * C + c + v] = found[v] ? best[v] : 0.f;
     }
-    if (c == 0) o_time[s] = tim[r];
+    if (c == 0 && o_time) o_time[s] = tim[r];
   }
-  GRID_STRIDE(j, n_act) {
+  if (o_len) GRID_STRIDE(j, n_act) {
     const int64_t f = f_index[j], len = f_len[j];
     const int64_t st = ev_pre[f];
     int64_t segs = 0;
@@ -1456,7 +1465,11 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
 // After ssla_sparse_pool_plan on the same workspace and sizes: out_events
 // [n_seg, C] (mode 0 max, 1 mean), out_time [n_seg], and per active field
 // out_len / out_batch / out_h / out_w [n_act]; outcoord is the [n_rf, 2]
-// (w, h) output coordinate table of the fields.
+// (w, h) output coordinate table of the fields.  The outputs come in two
+// parts that may be emitted by separate calls on the same plan: the values
+// (out_events; events may then be the only input) and the structure
+// (out_time and the per-field outputs); a null out_events skips the values,
+// null per-field outputs skip the structure (out_time is then optional).
 extern "C" int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int64_t E_in, int B, int H, int W,
                                      int64_t n_rf, int A, int64_t E_cap, const int64_t *outcoord, int mode,
                                      int64_t n_act, int64_t n_seg, int64_t E_out, float *out_events, int64_t *out_time,
@@ -1475,14 +1488,16 @@ extern "C" int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int6
     set_error("sparse_pool_emit: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
     return SSLA_ERR_WORKSPACE;
   }
-  SSLA_CHECK_ARG((n_seg == 0 || (events && out_events && out_time)) &&
-                     (n_act == 0 || (outcoord && out_len && out_batch && out_h && out_w)),
+  const bool values = out_events != nullptr, structure = out_len != nullptr;
+  SSLA_CHECK_ARG(values || structure, "sparse_pool_emit: neither values nor structure requested");
+  SSLA_CHECK_ARG((!values || n_seg == 0 || events) && (!structure || n_seg == 0 || out_time) &&
+                     (!structure || n_act == 0 || (outcoord && out_batch && out_h && out_w)),
                  "sparse_pool_emit: null pointer");
   if (E_out * C == 0 && n_act == 0) return SSLA_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   SSLA_CHECK_ARG(E_out * C < 0x7fffffff, "sparse_pool_emit: rows x channels must stay below 2^31");
   const bool vec = C % 4 == 0 && aligned(events, 16) && aligned(out_events, 16);
-  const unsigned grid = grid_for(std::max(E_out * (vec ? C / 4 : C), n_act));
+  const unsigned grid = grid_for(std::max(values ? E_out * (vec ? C / 4 : C) : E_out, n_act));
 #define SSLA_POOL_EMIT(MEANV, VWV)                                                                                \
   hipLaunchKernelGGL((pool_emit_rows<MEANV, VWV>), dim3(grid), dim3(kThreads), 0, st, events, E_in, C, L.src,       \
                      L.tim, L.head, L.segx, E_out, n_seg, L.rf.f_index, L.rf.f_len, L.rf.ev_pre, n_act, n_rf,       \

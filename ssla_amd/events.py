@@ -356,30 +356,28 @@ def pool_segments(time: torch.Tensor, lengths: torch.Tensor):
     return seg[:E], seg_t[:n_seg], new_len
 
 
-def sparse_pool(inputs, frame_size, rf2pixel_lut, rf_outcoord, mean: bool = False,
-                fields_per_pixel: Optional[int] = None) -> Dict[str, torch.Tensor]:
-    """SparsePool.forward on pixel groups (reference layers/sparse_pooling.py:
-    14-48 after gather_receptive_fields) in two library calls, without
-    gradient: the receptive-field rows are never stored as features.  The
-    returned dict equals that of gather_receptive_fields -> pool_segments ->
-    scatter_max / scatter_mean with a sorted index.  ``fields_per_pixel``
-    bounds the fields one pixel belongs to (ceil(kh/sh) * ceil(kw/sw); the
-    kernel positions when not given): it sizes the row capacity."""
+class PoolPlan:
+    """A pooling plan (ssla_sparse_pool_plan) of one window's structure: the
+    workspace that holds it, the call sizes, the counts and, once emitted,
+    the pooled structure (time, lengths, batch_id, h, w, batch_size)."""
+    __slots__ = ("ws", "sizes", "n_act", "n_seg", "E_out", "outc", "stream", "structure")
+
+    def tensors(self):
+        """The device tensors the plan holds (for Tensor.record_stream when
+        another stream consumes it)."""
+        return [self.ws, self.outc] + [v for v in self.structure.values() if isinstance(v, torch.Tensor)]
+
+
+def _pool_plan_call(inputs, frame_size, rf2pixel_lut, rf_outcoord, fields_per_pixel) -> PoolPlan:
     lib = _lib.load()
     gb, gh, gw, gl = (_i64(inputs[k]) for k in ("batch_id", "h", "w", "lengths"))
     time = _i64(inputs["time"])
-    ev = inputs["events"]
-    if ev.dim() != 2 or ev.dtype != torch.float32:
-        raise TypeError("sparse_pool: events must be fp32 [E, C]")
-    ev = ev.contiguous()
-    dev = _lib.require_cuda(gb, gl, time, ev, rf2pixel_lut)
+    dev = _lib.require_cuda(gb, gl, time, rf2pixel_lut)
     B = int(inputs["batch_size"])
     H, W = int(frame_size[0]), int(frame_size[1])
     lut, outc = _i64(rf2pixel_lut), _i64(rf_outcoord)
     n_rf, A = lut.shape
-    G, E_in, C = gl.numel(), time.numel(), ev.shape[1]
-    if ev.shape[0] != E_in:
-        raise ValueError(f"sparse_pool: {ev.shape[0]} event rows for {E_in} times")
+    G, E_in = gl.numel(), time.numel()
     E_cap = E_in * min(A, int(fields_per_pixel) if fields_per_pixel else A)
     ws = _ws(lib.ssla_sparse_pool_workspace_size(G, E_in, B, H, W, n_rf, A, E_cap), dev)
     st = _lib.stream_of(time)
@@ -390,16 +388,74 @@ def sparse_pool(inputs, frame_size, rf2pixel_lut, rf_outcoord, mean: bool = Fals
     n_act, n_seg, E_out, bad = (int(v) for v in cnt)
     if bad:
         raise ValueError("sparse_pool: input indices or coordinates out of range")
-    out_ev = torch.empty(n_seg, C, dtype=torch.float32, device=dev)
-    out_t = torch.empty(n_seg, dtype=torch.int64, device=dev)
-    fl = torch.empty(4, n_act, dtype=torch.int64, device=dev)
-    _lib.check(lib.ssla_sparse_pool_emit(_lib.ptr(ev), C, G, E_in, B, H, W, n_rf, A, E_cap, _lib.ptr(outc),
-                                         1 if mean else 0,
-                                         n_act, n_seg, E_out, _lib.ptr(out_ev), _lib.ptr(out_t), _lib.ptr(fl[0]),
-                                         _lib.ptr(fl[1]), _lib.ptr(fl[2]), _lib.ptr(fl[3]), _lib.ptr(ws), ws.numel(),
-                                         st), "sparse_pool_emit")
-    return {"events": out_ev, "time": out_t, "lengths": fl[0], "batch_id": fl[1], "h": fl[2], "w": fl[3],
-            "batch_size": inputs["batch_size"]}
+    plan = PoolPlan()
+    plan.ws, plan.sizes, plan.outc, plan.stream = ws, (G, E_in, B, H, W, n_rf, A, E_cap), outc, st
+    plan.n_act, plan.n_seg, plan.E_out = n_act, n_seg, E_out
+    plan.structure = {"batch_size": inputs["batch_size"]}
+    return plan
+
+
+def _pool_emit(plan: PoolPlan, ev, mean, structure: bool):
+    """One ssla_sparse_pool_emit call on the plan: the values when ``ev`` is
+    given, the structure when ``structure``."""
+    lib = _lib.load()
+    G, E_in, B, H, W, n_rf, A, E_cap = plan.sizes
+    dev = plan.ws.device
+    out_ev = None
+    if ev is not None:
+        if ev.dim() != 2 or ev.dtype != torch.float32:
+            raise TypeError("sparse_pool: events must be fp32 [E, C]")
+        if ev.shape[0] != E_in:
+            raise ValueError(f"sparse_pool: {ev.shape[0]} event rows for {E_in} times")
+        ev = ev.contiguous()
+        out_ev = torch.empty(plan.n_seg, ev.shape[1], dtype=torch.float32, device=dev)
+    C = ev.shape[1] if ev is not None else 1
+    out_t = fl = None
+    if structure:
+        out_t = torch.empty(plan.n_seg, dtype=torch.int64, device=dev)
+        fl = torch.empty(4, plan.n_act, dtype=torch.int64, device=dev)
+    P = _lib.ptr
+    _lib.check(lib.ssla_sparse_pool_emit(P(ev), C, G, E_in, B, H, W, n_rf, A, E_cap, P(plan.outc),
+                                         1 if mean else 0, plan.n_act, plan.n_seg, plan.E_out, P(out_ev), P(out_t),
+                                         P(fl[0]) if fl is not None else None, P(fl[1]) if fl is not None else None,
+                                         P(fl[2]) if fl is not None else None, P(fl[3]) if fl is not None else None,
+                                         P(plan.ws), plan.ws.numel(), _lib.stream_of(plan.ws)), "sparse_pool_emit")
+    if structure:
+        plan.structure.update({"time": out_t, "lengths": fl[0], "batch_id": fl[1], "h": fl[2], "w": fl[3]})
+    return out_ev
+
+
+def sparse_pool_plan(inputs, frame_size, rf2pixel_lut, rf_outcoord,
+                     fields_per_pixel: Optional[int] = None) -> PoolPlan:
+    """The structure half of sparse_pool: the plan of the groups in
+    ``inputs`` (batch_id, h, w, lengths, time, batch_size; no values needed)
+    and the pooled structure, emitted into ``plan.structure``.  The values
+    follow with sparse_pool_values on the same plan, so the structure of a
+    window can be planned before the values that pass through it exist."""
+    plan = _pool_plan_call(inputs, frame_size, rf2pixel_lut, rf_outcoord, fields_per_pixel)
+    _pool_emit(plan, None, False, True)
+    return plan
+
+
+def sparse_pool_values(plan: PoolPlan, events: torch.Tensor, mean: bool = False) -> torch.Tensor:
+    """The values half of sparse_pool on a plan from sparse_pool_plan:
+    [segments, C] max (or mean) of every pooling segment."""
+    return _pool_emit(plan, events, mean, False)
+
+
+def sparse_pool(inputs, frame_size, rf2pixel_lut, rf_outcoord, mean: bool = False,
+                fields_per_pixel: Optional[int] = None) -> Dict[str, torch.Tensor]:
+    """SparsePool.forward on pixel groups (reference layers/sparse_pooling.py:
+    14-48 after gather_receptive_fields) in two library calls, without
+    gradient: the receptive-field rows are never stored as features.  The
+    returned dict equals that of gather_receptive_fields -> pool_segments ->
+    scatter_max / scatter_mean with a sorted index.  ``fields_per_pixel``
+    bounds the fields one pixel belongs to (ceil(kh/sh) * ceil(kw/sw); the
+    kernel positions when not given): it sizes the row capacity."""
+    _lib.require_cuda(inputs["events"])
+    plan = _pool_plan_call(inputs, frame_size, rf2pixel_lut, rf_outcoord, fields_per_pixel)
+    out_ev = _pool_emit(plan, inputs["events"], mean, True)
+    return {"events": out_ev, **plan.structure}
 
 
 def events_to_grid(x: Dict[str, torch.Tensor], grid_size, channels: int) -> torch.Tensor:

@@ -29,7 +29,7 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Tuple
+from typing import Dict, Tuple
 
 import torch
 import torch.nn as nn
@@ -349,15 +349,37 @@ class SparsePool(AsyncSparseModule):
         if grouped_events and self._one_call(inputs):
             dev = inputs["time"].device
             _ensure_lut(self, "rf2pixel_lut", "rf_outcoord", self.frame_size, self.kernel_size, self.stride, dev)
-            per_px = (-(-self.kernel_size[0] // self.stride[0])) * (-(-self.kernel_size[1] // self.stride[1]))
             return E.sparse_pool(inputs, self.frame_size, self.rf2pixel_lut, self.rf_outcoord,
-                                 mean=self.pool_func is scatter_mean, fields_per_pixel=per_px)
+                                 mean=self.pool_func is scatter_mean, fields_per_pixel=self._fields_per_pixel())
         x = self.prepare_inputs(inputs, grouped_events)
         seg, seg_time, new_len = E.pool_segments(x["time"], x["lengths"])
         res = self.pool_func(x["events"], seg, dim=0, dim_size=int(seg_time.numel()), sorted_index=True)
         new_events = res[0] if isinstance(res, tuple) else res
         return {"events": new_events, "time": seg_time, "lengths": new_len, "batch_id": x["batch_id"],
                 "h": x["h"], "w": x["w"], "batch_size": x["batch_size"]}
+
+    def plan(self, inputs) -> "E.PoolPlan":
+        """The structure half of forward (E.sparse_pool_plan) for grouped
+        device inputs whose values come later: the pooled time, lengths,
+        batch_id, h, w land in ``plan.structure``; ``apply_plan`` then pools
+        the values.  Only for the one-call pooling (max or mean over a field
+        larger than one pixel)."""
+        if self.pool_func not in (scatter_max, scatter_mean) or (self.kernel_size == (1, 1)
+                                                                 and self.stride == (1, 1)):
+            raise ValueError("SparsePool.plan: needs max or mean pooling over fields larger than one pixel")
+        dev = inputs["time"].device
+        _ensure_lut(self, "rf2pixel_lut", "rf_outcoord", self.frame_size, self.kernel_size, self.stride, dev)
+        return E.sparse_pool_plan(inputs, self.frame_size, self.rf2pixel_lut, self.rf_outcoord,
+                                  fields_per_pixel=self._fields_per_pixel())
+
+    def apply_plan(self, plan: "E.PoolPlan", events: torch.Tensor) -> Dict[str, torch.Tensor]:
+        """forward's output for the values ``events`` of the groups ``plan``
+        was made from."""
+        return {"events": E.sparse_pool_values(plan, events, mean=self.pool_func is scatter_mean),
+                **plan.structure}
+
+    def _fields_per_pixel(self) -> int:
+        return (-(-self.kernel_size[0] // self.stride[0])) * (-(-self.kernel_size[1] // self.stride[1]))
 
     def compute_flops(self, inputs, grouped_events=True, elementwise_agg_flops=0):
         """Flops of the aggregation (reference layers/sparse_pooling.py:53-70):

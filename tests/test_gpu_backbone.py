@@ -207,6 +207,34 @@ def test_async_step_full_size_properties(dev):
             assert abs(float(y.mean())) < 0.1 and 0.8 < float(y.std()) < 1.2
 
 
+def test_async_plan_then_forward_matches(dev):
+    """plan() of every window first, then forward(plan=...) window by
+    window: outputs, pooled structure and carried states equal forward()
+    that plans each window itself, bit for bit, over three 50k-event
+    windows."""
+    from ssla_amd import synthetic
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(5)
+    model = AsyncSparseGLA().to(dev).eval()
+    wins = [w.to(dev) for w in synthetic.async_windows(3, 50_000, seed=6)]
+    ln = torch.tensor([50_000], device=dev)
+    print("async plan then forward", flush=True)
+    with torch.no_grad():
+        s_seq = model.init_states(1, dev)
+        seq = [model(w, ln, s_seq) for w in wins]
+        plans = [model.plan(w, ln) for w in wins]
+        s_pl = model.init_states(1, dev)
+        got = [model(w, ln, s_pl, plan=p) for w, p in zip(wins, plans)]
+    for w, ((o1, f1), (o2, f2)) in enumerate(zip(seq, got)):
+        assert torch.equal(o1, o2), f"window {w}: head output differs"
+        for i in range(4):
+            assert torch.equal(f1[i]["events"], f2[i]["events"]), f"window {w} stage {i}: events differ"
+            for key in ("time", "lengths", "batch_id", "h", "w"):
+                assert torch.equal(f1[i][key], f2[i][key]), f"window {w} stage {i}: {key} differs"
+    for i in range(4):
+        assert torch.equal(s_seq[i], s_pl[i]), f"stage {i}: carried states differ"
+
+
 def test_head_kernel_matches_module(dev):
     """ssla_detect_head (all levels in one kernel, fp32 between its two bf16
     GEMMs) against the module's bf16 ops run one by one and against the fp64
