@@ -9,19 +9,19 @@
 //
 // Sorted index (the reference's own call: segment ids from
 // unique_consecutive are non-decreasing):   seg_range -> seg_link
-// * seg_range: one workgroup of 8 wavefronts per range of 2048 positions
+// * seg_range: one workgroup of 8 wavefronts per range of 512 positions
 //   (every workgroup the same size of work, however the rows are spread).
-//   Each wavefront walks a contiguous quarter-kilo of positions in batches of
-//   64 (lane = channel: each position is one coalesced row load, 64 in
-//   flight at once) and writes the rows that start and end inside its part;
+//   Each wavefront walks a contiguous part of 64 positions as one batch
+//   (lane = channel: each position is one coalesced row load, 64 in flight
+//   at once) and writes the rows that start and end inside its part;
 //   rows that cross a wavefront edge are merged through LDS; a row that
 //   crosses the workgroup's start or end leaves one 512-byte piece, and every
 //   workgroup writes its tail flag (state, row, event count, bad-index bit).
 // * seg_link: one wavefront per range; a range whose last row continues
 //   reads the flags of the ranges after it (64 at a time), folds the pieces
 //   of the row in range order and writes it; also raises the status word for
-//   a bad index.  At C4 there are ~500 range edges (against ~16k tile edges
-//   with one 64-position tile per wavefront), so the link is a small pass.
+//   a bad index.  At C4 there are ~2,000 range edges and most rows end
+//   inside their range, so the link is a small pass.
 //
 // Unsorted index:   hist -> scan -> bucket -> bucket_reduce -> bucket_finalize
 // * hist  : LDS histogram of buckets of 64 consecutive rows per event range
@@ -32,7 +32,7 @@
 //           single-pass decoupled look-back; both counts travel in the flag
 //           word.
 // * bucket: (event, row) pairs placed at their bucket-grouped positions.
-// * bucket_reduce: one workgroup per chunk of at most 8192 events of one
+// * bucket_reduce: one workgroup per chunk of at most 4096 events of one
 //           bucket: a 64-row x 64-channel tile in LDS takes every event with
 //           LDS atomics (max: ds_max_u64 on a packed (orderable value,
 //           inverted event id) key, so the result does not depend on the
