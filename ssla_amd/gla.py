@@ -53,9 +53,10 @@ VD = 64   # value columns of one chunk-backward call
 
 
 def chunk_backward_supports(q: torch.Tensor, v: torch.Tensor) -> bool:
-    """True when the chunk backward handles this dtype/shape (bf16/fp16, K
-    and V multiples of 16 up to 256: ``ssla_gla_chunk_bwd`` runs 64 keys by
-    64 value columns, wider K and V run as groups of those)."""
+    """True when the chunk backward handles this dtype/shape: bf16/fp16 with
+    K and V multiples of 16 up to 256, or fp32 with K and V up to 256
+    (``ssla_gla_chunk_bwd`` / ``ssla_gla_chunk_f32_bwd`` run 64 keys by 64
+    value columns; wider K and V run as groups of those)."""
     return chunk_kernel_supports(q, v)
 
 
@@ -139,7 +140,7 @@ def chunk_gla(
     if grad:
         if not chunk_backward_supports(q, v):
             raise NotImplementedError(
-                "chunk_gla backward needs K and V multiples of 16 up to 256 "
+                "chunk_gla backward needs K and V multiples of 16 up to 256 (up to 256 for fp32) "
                 f"(got {q.dtype}, K={q.shape[-1]}, V={v.shape[-1]})")
         return ChunkGLAFunction.apply(q, k, v, g, float(scale), h0, output_final_state, cu)
     return _chunk_fwd(q, k, v, g, cu, float(scale), h0, output_final_state)
