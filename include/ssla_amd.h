@@ -536,8 +536,8 @@ int ssla_pool_segments(const int64_t *time, const int64_t *lengths, int64_t n_f,
  * field) -- the dict SparsePool.forward returns.  The values (out_events)
  * and the structure (out_time and the per-field outputs) may be emitted by
  * two calls on the same plan: a null out_events skips the values, a null
- * out_len skips the structure, so the structure of a window can be planned
- * before its values exist. */
+ * out_len skips the structure (both null: nothing is written), so the
+ * structure of a window can be planned before its values exist. */
 size_t ssla_sparse_pool_workspace_size(int64_t G, int64_t E_in, int B, int H, int W, int64_t n_rf, int A,
                                        int64_t E_cap);
 int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,

@@ -1489,7 +1489,7 @@ extern "C" int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int6
     return SSLA_ERR_WORKSPACE;
   }
   const bool values = out_events != nullptr, structure = out_len != nullptr;
-  SSLA_CHECK_ARG(values || structure, "sparse_pool_emit: neither values nor structure requested");
+  if (!values && !structure) return SSLA_OK;   // nothing requested (or nothing to write: empty outputs)
   SSLA_CHECK_ARG((!values || n_seg == 0 || events) && (!structure || n_seg == 0 || out_time) &&
                      (!structure || n_act == 0 || (outcoord && out_batch && out_h && out_w)),
                  "sparse_pool_emit: null pointer");
