@@ -726,7 +726,9 @@ def calibrate_copy(torch, dev, mib=256, reps=3):
 
 def bench_chunk_bwd(torch, lib, reps, dev):
     """Backward of config 2 (ssla_gla_chunk_bwd): gradients of o and ht for
-    the C2 batch, two input sets alternating."""
+    the C2 batch, three input sets in rotation (369 MB each with their
+    gradients: a call's data was last touched two calls before, more than
+    the 256 MB Infinity Cache holds)."""
     from ssla_amd import _lib, synthetic
     Tt, H, D = C2["B"] * C2["T"], C2["H"], C2["D"]
     sets = []
@@ -752,12 +754,12 @@ def bench_chunk_bwd(torch, lib, reps, dev):
         _lib.check(st, "ssla_gla_chunk_bwd")
 
     for i in range(3):
-        launch(sets[i % 2])
+        launch(sets[i % len(sets)])
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for i in range(reps):
-        launch(sets[i % 2])
+        launch(sets[i % len(sets)])
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps

@@ -203,7 +203,7 @@ __device__ __forceinline__ void seg_pass(SmemP &sm, const int64_t bid, const uin
                                          float xscale, float *__restrict__ loc, float *__restrict__ dec,
                                          float *__restrict__ eloc, float *__restrict__ dtot) {
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wavefront-uniform
   const int col = lane & 15, grp = lane >> 4;
   const int h = static_cast<int>(bid % H);
   const int64_t sg = bid / H;
@@ -438,7 +438,7 @@ __global__ __launch_bounds__(64 * kCW) void bwd_chunk_kernel(
   __shared__ SmemC sm;
   auto X = [](uint16_t b) { return Elt<DT>::f(b); };   // a staged input value
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wavefront-uniform
   const int col = lane & 15, grp = lane >> 4;
   const int I = w & 3, P = w >> 2;
   const int h = static_cast<int>(blockIdx.x % H);
@@ -899,7 +899,7 @@ __device__ __forceinline__ void seg_pass_tiles(SmemT &sm, const int64_t bid, con
                                                float xscale, float *__restrict__ loc, float *__restrict__ dec,
                                                float *__restrict__ eloc, float *__restrict__ dtot) {
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wavefront-uniform
   const int h = static_cast<int>(bid % H);
   const int64_t sg = bid / H;
   if (sg >= sgoff[n_seq]) return;   // workgroup-uniform

@@ -30,10 +30,13 @@
 // * scan  : per-bucket start offsets (and per-workgroup offsets inside each
 //           bucket) and the prefix of each bucket's chunk count, by a
 //           single-pass decoupled look-back; both counts travel in the flag
-//           word.
+//           word.  It also writes one descriptor per chunk (bucket, first
+//           and last position, chunks of the bucket).
 // * bucket: (event, row) pairs placed at their bucket-grouped positions.
-// * bucket_reduce: one workgroup per chunk of at most 4096 events of one
-//           bucket: a 64-row x 64-channel tile in LDS takes every event with
+// * bucket_reduce: one workgroup per chunk of at most 2048 events of one
+//           bucket (its descriptor is one load; 2048 gives config 4 about
+//           two chunks per bucket, so the workgroups fill the chip): a
+//           64-row x 64-channel tile in LDS takes every event with
 //           LDS atomics (max: ds_max_u64 on a packed (orderable value,
 //           inverted event id) key, so the result does not depend on the
 //           order the events arrive in; mean: ds_add_f64 and a row count).
@@ -52,7 +55,7 @@ namespace ssla {
 namespace {
 
 #ifndef SSLA_SR_CHUNK
-#define SSLA_SR_CHUNK 4096
+#define SSLA_SR_CHUNK 2048
 #endif
 #ifndef SSLA_SR_RANGE
 #define SSLA_SR_RANGE 512
@@ -66,7 +69,10 @@ constexpr int kLdsBuckets = 4096;                  // buckets counted in LDS (16
 constexpr int kScanCells = 64;                     // buckets per scan workgroup
 constexpr int kScanTpc = 1024 / kScanCells;        // scan threads per bucket
 constexpr int kChunk = SSLA_SR_CHUNK;              // events per bucket_reduce workgroup at most
-constexpr int kRedWaves = 16;                      // bucket_reduce / finalize wavefronts
+#ifndef SSLA_SR_REDW
+#define SSLA_SR_REDW 16
+#endif
+constexpr int kRedWaves = SSLA_SR_REDW;            // bucket_reduce / finalize wavefronts
 #ifndef SSLA_SR_RWAVES
 #define SSLA_SR_RWAVES 8
 #endif
@@ -81,7 +87,7 @@ inline int64_t n_ranges(int64_t E) { return std::max<int64_t>(1, (E + kRange - 1
 inline int64_t n_chunks_max(int64_t E, int64_t NB) { return NB + (E + kChunk - 1) / kChunk; }
 
 struct WsLayout {
-  size_t status, errs, off, coff, flags, hist, perm, parts, pcnt, rflags, rpieces, total;
+  size_t status, errs, off, coff, cdesc, flags, hist, perm, parts, pcnt, rflags, rpieces, total;
   int n_hist;
   int64_t NB, n_chunks, n_rseg;
 };
@@ -116,6 +122,7 @@ inline WsLayout ws_layout(int64_t E, int C, int64_t n_out) {
   L.errs = p;  p = align256(p + sizeof(int32_t) * n_err);
   L.off = p;   p = align256(p + sizeof(int32_t) * (L.NB + 1));
   L.coff = p;  p = align256(p + sizeof(int32_t) * (L.NB + 1));
+  L.cdesc = p; p = align256(p + sizeof(int4) * static_cast<size_t>(L.n_chunks));   // (bucket, p0, p1, chunks)
   L.flags = p; p = align256(p + sizeof(uint64_t) * (scan_blocks(L.NB) + 1));
   L.hist = p;  p = align256(p + sizeof(int32_t) * static_cast<size_t>(L.n_hist) * (L.NB + 1));
   L.perm = p;  p = align256(p + sizeof(int2) * (E > 0 ? E : 1));   // (event, row) per bucket-grouped position
@@ -228,7 +235,8 @@ __device__ __forceinline__ int64_t bucket_chunks(int64_t n) { return max((n + kC
 // (coff[NB] = chunks).
 __global__ __launch_bounds__(kScanCells *kScanTpc) void scan_kernel(
     int32_t *__restrict__ hist, int n_hist, int64_t NB, int32_t *__restrict__ off, int32_t *__restrict__ coff,
-    int32_t *ticket, uint64_t *flags, const int32_t *__restrict__ errs, int n_err, int32_t *__restrict__ status) {
+    int4 *__restrict__ cdesc, int64_t n_cmax, int32_t *ticket, uint64_t *flags, const int32_t *__restrict__ errs,
+    int n_err, int32_t *__restrict__ status) {
   __shared__ int s_bid;
   __shared__ int32_t s_part[kScanTpc][kScanCells];
   __shared__ int64_t s_cnt[kScanCells], s_chk[kScanCells];
@@ -357,11 +365,21 @@ __global__ __launch_bounds__(kScanCells *kScanTpc) void scan_kernel(
     }
   }
   __syncthreads();
-  if (grp == 0 && live) {
+  if (live) {
     const int64_t mine = lc > 0 ? s_cnt[lc] - s_cnt[lc - 1] : s_cnt[0];
     const int64_t mine_k = lc > 0 ? s_chk[lc] - s_chk[lc - 1] : s_chk[0];
-    off[cell] = static_cast<int32_t>(s_excl + s_cnt[lc] - mine);
-    coff[cell] = static_cast<int32_t>(s_excl_chk + s_chk[lc] - mine_k);
+    const int64_t o = s_excl + s_cnt[lc] - mine, ok = s_excl_chk + s_chk[lc] - mine_k;
+    if (grp == 0) {
+      off[cell] = static_cast<int32_t>(o);
+      coff[cell] = static_cast<int32_t>(ok);
+    }
+    // the bucket's chunk descriptors: a reduce workgroup finds its bucket
+    // and positions in one load
+    for (int64_t j = grp; j < mine_k && ok + j < n_cmax; j += kScanTpc) {
+      const int64_t p0 = o + j * kChunk, p1 = min(p0 + static_cast<int64_t>(kChunk), o + mine);
+      cdesc[ok + j] = make_int4(static_cast<int>(cell), static_cast<int>(p0), static_cast<int>(p1),
+                                static_cast<int>(mine_k));
+    }
   }
 }
 
@@ -773,40 +791,35 @@ __global__ __launch_bounds__(64 * kLinkWaves) void seg_link_kernel(int64_t E, in
 // one coalesced 256-byte row load each, all in flight), then one atomic per
 // position.  Batches of 32 keep the kernel at two workgroups per CU, so
 // every chunk of a config-4 call is resident at once.
-constexpr int kRedBatch = 32;
+#ifndef SSLA_SR_RBATCH
+#define SSLA_SR_RBATCH 32
+#endif
+constexpr int kRedBatch = SSLA_SR_RBATCH;
+static_assert(kRedBatch <= 64, "a batch's (event, row) pairs are one per lane");
 template <bool MEAN, int CT>
 __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
-    const float *__restrict__ src, const int2 *__restrict__ perm, const int32_t *__restrict__ off,
+    const float *__restrict__ src, const int2 *__restrict__ perm, const int4 *__restrict__ cdesc,
     const int32_t *__restrict__ coff, int32_t NB, int32_t E, int C, int32_t n_out, float *__restrict__ out,
     int64_t *__restrict__ argmax, uint64_t *__restrict__ parts, int32_t *__restrict__ pcnt) {
   __shared__ uint64_t tile[kBucketRows][64];   // max keys, or fp64 sums
   __shared__ int32_t tcnt[kBucketRows];
-  __shared__ int s_b;
   const int Cc = CT ? CT : C;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int ncb = CT ? 1 : (C + 63) / 64;
   const int c = static_cast<int>(blockIdx.x) / ncb;
   const int cb = static_cast<int>(blockIdx.x) - c * ncb;
+  // the chunk count and this chunk's descriptor in one round trip (the
+  // grid covers the most chunks there can be; c is checked before use)
   const int32_t n_chunks = coff[NB];
+  const int4 d = cdesc[c];
   if (c >= n_chunks) return;   // workgroup-uniform
-  if (threadIdx.x == 0) {      // the bucket of chunk c: coff is strictly increasing
-    int lo = 0, hi = NB - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (coff[mid] <= c) lo = mid;
-      else hi = mid - 1;
-    }
-    s_b = lo;
-  }
   for (int i = threadIdx.x; i < kBucketRows * 64; i += 64 * kRedWaves) (&tile[0][0])[i] = 0ull;
   if (threadIdx.x < kBucketRows) tcnt[threadIdx.x] = 0;
   __syncthreads();
-  const int b = s_b;
-  const int pb0 = off[b], pb1 = off[b + 1];
-  const int j = c - coff[b], nch = coff[b + 1] - coff[b];
-  const int p0 = min(max(pb0 + j * kChunk, 0), E);
-  const int p1 = min(max(min(p0 + kChunk, pb1), p0), E);
+  const int b = min(max(d.x, 0), NB - 1), nch = d.w;
+  const int p0 = min(max(d.y, 0), E);
+  const int p1 = min(max(d.z, p0), E);
   const int row0 = b << kBucketShift;
   const int col = cb * 64 + lane;
   const bool act = CT ? true : col < C;
@@ -978,6 +991,7 @@ int run_scatter(const float *src, const int64_t *index, int64_t E, int C, int64_
   int32_t *errs = reinterpret_cast<int32_t *>(base + L.errs);
   int32_t *off = reinterpret_cast<int32_t *>(base + L.off);
   int32_t *coff = reinterpret_cast<int32_t *>(base + L.coff);
+  int4 *cdesc = reinterpret_cast<int4 *>(base + L.cdesc);
   uint64_t *flags = reinterpret_cast<uint64_t *>(base + L.flags);
   int32_t *hist = reinterpret_cast<int32_t *>(base + L.hist);
   int2 *perm = reinterpret_cast<int2 *>(base + L.perm);
@@ -1002,7 +1016,7 @@ int run_scatter(const float *src, const int64_t *index, int64_t E, int C, int64_
     n_err = nb;
   }
   hipLaunchKernelGGL(scan_kernel, dim3(static_cast<unsigned>(n_scan)), dim3(kScanCells * kScanTpc), 0, st, hist,
-                     L.n_hist, NB, off, coff, ticket, flags, errs, n_err, status);
+                     L.n_hist, NB, off, coff, cdesc, L.n_chunks, ticket, flags, errs, n_err, status);
   if (lds) {
     hipLaunchKernelGGL((bucket_kernel<true>), dim3(L.n_hist), dim3(kEvThreads), 0, st, index, E, n_out, NB,
                        L.n_hist, off, hist, perm);
@@ -1015,11 +1029,11 @@ int run_scatter(const float *src, const int64_t *index, int64_t E, int C, int64_
     const int32_t E32 = static_cast<int32_t>(E), n32 = static_cast<int32_t>(n_out), NB32 = static_cast<int32_t>(NB);
     if (C == 64)
       hipLaunchKernelGGL((bucket_reduce_kernel<MEAN, 64>), dim3(static_cast<unsigned>(L.n_chunks * ncb)),
-                         dim3(64 * kRedWaves), 0, st, src, perm, off, coff, NB32, E32, C, n32, out, argmax, parts,
+                         dim3(64 * kRedWaves), 0, st, src, perm, cdesc, coff, NB32, E32, C, n32, out, argmax, parts,
                          pcnt);
     else
       hipLaunchKernelGGL((bucket_reduce_kernel<MEAN, 0>), dim3(static_cast<unsigned>(L.n_chunks * ncb)),
-                         dim3(64 * kRedWaves), 0, st, src, perm, off, coff, NB32, E32, C, n32, out, argmax, parts,
+                         dim3(64 * kRedWaves), 0, st, src, perm, cdesc, coff, NB32, E32, C, n32, out, argmax, parts,
                          pcnt);
   }
   hipLaunchKernelGGL(bucket_finalize_kernel<MEAN>, dim3(static_cast<unsigned>(NB * ncb)), dim3(64 * kRedWaves), 0,
