@@ -642,7 +642,10 @@ def bench_async_step(torch, lib, dev, n_windows=20, n_events=50_000, cpu=True):
     n_windows consecutive windows of n_events events, per-stage states
     carried from window to window; raw <x, y, t, p> windows resident on the
     device before the timing.  value = windows/s over the whole timed run
-    (host wall clock, synchronised); a second, instrumented pass over the
+    (host wall clock, synchronised) of AsyncSparseGLA.run, which plans each
+    window while the previous one's stages run; the same windows through
+    forward() one at a time are timed too (ms_per_window_forward_loop).  A
+    second, instrumented pass over the
     same windows (fresh states) times each piece with HIP events (those
     intervals include the GPU's idle time while the host prepares a piece).
     The per-site scan of every stage is priced against HBM from its own
@@ -657,7 +660,9 @@ def bench_async_step(torch, lib, dev, n_windows=20, n_events=50_000, cpu=True):
     ln = torch.tensor([n_events], device=dev)
     stream = torch.cuda.current_stream(dev)
     with torch.no_grad():
+        lns = [ln] * len(wins)
         warm = model.init_states(1, dev)
+        model.run(wins[:3], lns[:3], warm)
         for w in wins[:2]:
             model(w, ln, warm)
         states = model.init_states(1, dev)
@@ -665,6 +670,12 @@ def bench_async_step(torch, lib, dev, n_windows=20, n_events=50_000, cpu=True):
         t0 = time.perf_counter()
         for w in wins:
             model(w, ln, states)
+        torch.cuda.synchronize()
+        wall_loop = time.perf_counter() - t0
+        states = model.init_states(1, dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.run(wins, lns, states)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         # instrumented pass: per-piece HIP events
@@ -696,6 +707,7 @@ def bench_async_step(torch, lib, dev, n_windows=20, n_events=50_000, cpu=True):
                         "bf16 projections and head",
             "metric": "async step windows/s", "value": n_windows / wall, "unit": "windows/s",
             "events_per_s": n_windows * n_events / wall, "ms_per_window": per_window_ms,
+            "ms_per_window_forward_loop": wall_loop * 1e3 / n_windows,
             "ms_per_piece": piece_ms, "scan_kernels": scans,
             "roofline": {"bound": "hbm", "kernel": "ssla_gla_recurrent_fwd with state_idx (per-site scan), "
                                                    "stage 1", **{k: scans[0][k] for k in

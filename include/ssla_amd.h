@@ -361,8 +361,10 @@ int ssla_scatter_check(const void *workspace, int *status_out, void *stream);
  * index-add, truncation, temporal dropout, pooling keys, dense grids).
  *
  * Calls whose output size depends on the data write their counts into the
- * first int64 words of their workspace; ssla_events_counts() copies them to
- * the host (synchronising the stream).  Outputs are capacity-sized.  All
+ * first int64 words of their workspace and their input-error flag as an
+ * int32 at byte 256; ssla_events_counts() copies them to the host
+ * (synchronising the stream), or a caller copies those 260 bytes itself
+ * without waiting.  Outputs are capacity-sized.  All
  * orderings are stable (ties keep enumeration order).
  * ------------------------------------------------------------------------ */
 
@@ -544,6 +546,23 @@ int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_h, const in
                           const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B, int H,
                           int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap, int64_t *counts_out,
                           void *workspace, size_t workspace_bytes, void *stream);
+/* The plan in two halves, for callers that keep the device busy while the
+ * counts travel back: plan_enqueue launches the plan's kernels and reads
+ * nothing (the counts land in the first bytes of the workspace, where
+ * ssla_events_counts reads them; the caller may copy those bytes to host
+ * memory asynchronously on the same stream); plan_finish takes head[0..5]
+ * and bad as ssla_events_counts returns them once the enqueue's kernels are
+ * done, checks them and, when a pixel run is not sorted by time, runs the
+ * sort fill (two more reads).  counts_out as for plan.  The same
+ * reference interface as plan (layers/sparse_pooling.py:14-48). */
+int ssla_sparse_pool_plan_enqueue(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
+                                  const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
+                                  int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
+                                  void *workspace, size_t workspace_bytes, void *stream);
+int ssla_sparse_pool_plan_finish(const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
+                                 int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
+                                 const int64_t *head, int bad, int64_t *counts_out, void *workspace,
+                                 size_t workspace_bytes, void *stream);
 int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int64_t E_in, int B, int H, int W, int64_t n_rf,
                           int A, int64_t E_cap, const int64_t *outcoord, int mode, int64_t n_act, int64_t n_seg,
                           int64_t E_out, float *out_events, int64_t *out_time, int64_t *out_len,

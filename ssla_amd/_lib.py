@@ -101,6 +101,10 @@ SIGNATURES = {
     "ssla_sparse_pool_workspace_size": (_sz, [_i64, _i64, _i32, _i32, _i32, _i64, _i32, _i64]),
     "ssla_sparse_pool_plan": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _i32, _i64,
                                      C.POINTER(_i64), _vp, _sz, _vp]),
+    "ssla_sparse_pool_plan_enqueue": (_i32, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _i32,
+                                             _i64, _vp, _sz, _vp]),
+    "ssla_sparse_pool_plan_finish": (_i32, [_vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _i32, _i64,
+                                            C.POINTER(_i64), _i32, C.POINTER(_i64), _vp, _sz, _vp]),
     "ssla_sparse_pool_emit": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _i32, _i64, _i32, _i64, _vp, _i32, _i64,
                                      _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ssla_pixel_delays": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _sz, _vp]),

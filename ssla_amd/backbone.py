@@ -287,7 +287,18 @@ class DetectionHead(nn.Module):
         fp32 scale and shift, and the predictions as one bf16 [16, 2 width]
         matrix (zero where a prediction does not read a branch) with fp32
         biases; recomputed only when a parameter or buffer changes."""
-        key = tuple((t.data_ptr(), t._version) for t in list(self.parameters()) + list(self.buffers()))
+        # the key covers exactly the tensors read below, each looked up
+        # through its module (a replaced module or parameter changes it);
+        # walking parameters() and buffers() instead cost about 0.2 ms of
+        # host time per call
+        ts = []
+        for lvl in range(len(self.strides)):
+            for seq in (self.cls_convs[lvl], self.reg_convs[lvl]):
+                conv, bn = seq[0], seq[1]
+                ts += (conv.weight, conv.bias, bn.weight, bn.bias, bn.running_mean, bn.running_var)
+            for pred in (self.reg_preds[lvl], self.obj_preds[lvl], self.cls_preds[lvl]):
+                ts += (pred.weight, pred.bias)
+        key = tuple((t.data_ptr(), t._version, t.device) for t in ts)
         cache = getattr(self, "_fused_cache", None)
         if cache is not None and cache[0] == key:
             return cache[1]
@@ -430,6 +441,17 @@ class AsyncSparseGLA(nn.Module):
         (optional) is called after each piece ("stem", "s<i>.project" /
         ".scan" / ".finish" / ".pool", "grids", "head"): a timing hook that
         must not touch the tensors."""
+        pieces = self._pieces(events, lengths, states, mark, plan)
+        while True:
+            try:
+                next(pieces)
+            except StopIteration as done:
+                return done.value
+
+    def _pieces(self, events, lengths, states, mark, plan):
+        """forward as a generator that pauses after the stem and after each
+        of stages 0-2 (block and pooling) and returns (head output, stage
+        outputs)."""
         # Without a plan each stage's pooling is planned right after the
         # stage's block is enqueued, so the plan's read of device counts
         # waits while the GPU runs that block.
@@ -437,6 +459,7 @@ class AsyncSparseGLA(nn.Module):
             self.stem_pool.apply_plan(plan.pools[0], self._embed(plan.grouped))
         if mark:
             mark("stem")
+        yield
         feats = []
         for i, blk in enumerate(self.blocks):
             x = blk(x, states[i], self.grid_sizes[i], mark=(lambda nm, i=i: mark(f"s{i}.{nm}")) if mark else None)
@@ -445,6 +468,7 @@ class AsyncSparseGLA(nn.Module):
                 x = self.pools[i](x) if plan is None else self.pools[i].apply_plan(plan.pools[i + 1], x["events"])
                 if mark:
                     mark(f"s{i}.pool")
+                yield
         grids = [E.events_to_grid(feats[i], self.grid_sizes[i], self.stages[i][0]) for i in self.head_levels]
         if mark:
             mark("grids")
@@ -452,3 +476,69 @@ class AsyncSparseGLA(nn.Module):
         if mark:
             mark("head")
         return out, feats
+
+    def _plan_steps(self, events: torch.Tensor, lengths: torch.Tensor):
+        """``plan`` as a generator: each step queues its kernels and an
+        asynchronous copy of its counts and pauses; resuming waits for those
+        counts only (not for the stream), finishes the step and queues the
+        next.  Returns the WindowPlan."""
+        pending = E.preprocess_enqueue(events, lengths, self.frame_size, self.hot_pixel_thres)
+        yield
+        gr = E.preprocess_finish(pending)
+        pending = self.stem_pool.plan_enqueue(gr)
+        yield
+        pools = [self.stem_pool.plan_finish(pending)]
+        for pool in self.pools:
+            pending = pool.plan_enqueue(pools[-1].structure)
+            yield
+            pools.append(pool.plan_finish(pending))
+        return WindowPlan(gr, pools)
+
+    def run(self, windows: Sequence[torch.Tensor], lengths: Sequence[torch.Tensor],
+            states: List[torch.Tensor]) -> List[tuple]:
+        """``forward`` over consecutive windows with ``states`` carried from
+        one to the next (the same results as calling it on each window in
+        turn), with no wait that drains the device: while window i's stages
+        run, the next window is planned step by step on the same stream,
+        each planning step queued ahead of one of window i's stages, so the
+        device works on that stage while the host waits for the step's
+        counts.  Returns forward's result per window."""
+        outs = []
+        if len(windows) == 0:
+            return outs
+        if not self._can_plan_ahead(windows, lengths):
+            return [self.forward(w, ln, states) for w, ln in zip(windows, lengths)]
+        plan = self.plan(windows[0], lengths[0])
+        for i in range(len(windows)):
+            steps = self._plan_steps(windows[i + 1], lengths[i + 1]) if i + 1 < len(windows) else None
+            nxt = None
+
+            def advance():
+                nonlocal steps, nxt
+                try:
+                    next(steps)
+                except StopIteration as done:
+                    nxt, steps = done.value, None
+
+            if steps is not None:
+                advance()
+            pieces = self._pieces(windows[i], lengths[i], states, None, plan)
+            while True:
+                try:
+                    next(pieces)
+                except StopIteration as done:
+                    outs.append(done.value)
+                    break
+                if steps is not None:
+                    advance()
+            while steps is not None:
+                advance()
+            plan = nxt
+        return outs
+
+    def _can_plan_ahead(self, windows, lengths) -> bool:
+        """Planning ahead takes the one-call preprocessing and pooling: padded
+        fp32 device events and no gradient to record."""
+        return (not torch.is_grad_enabled() and all(
+            w.is_cuda and w.dim() == 3 and w.size(2) >= 4 and ln.dim() == 1 and ln.size(0) == w.size(0)
+            for w, ln in zip(windows, lengths)))

@@ -1338,6 +1338,17 @@ __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C
     o_w[j] = outcoord[rf * 2];
   }
 }
+
+// Segment heads of the filled field rows, their exclusive prefix and the
+// segment count (workspace head, slot 4).
+int pool_segments_pass(const PoolWs &L, int64_t E_cap, hipStream_t st) {
+  hipLaunchKernelGGL(pool_row_heads, dim3(grid_for(E_cap)), dim3(kThreads), 0, st, L.fidx, L.tim, L.rf.counts + 1,
+                     E_cap, L.head);
+  const int r = excl_scan(L.tmp, L.tmp_bytes, L.head, L.segx, E_cap, st);
+  if (r) return r;
+  hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.segx, L.head, E_cap, L.rf.counts + 4);
+  return SSLA_OK;
+}
 }  // namespace
 
 // E_cap bounds the field rows: E_in times the fields a pixel can belong to
@@ -1348,22 +1359,19 @@ extern "C" size_t ssla_sparse_pool_workspace_size(int64_t G, int64_t E_in, int B
   return pool_layout(nullptr, G, B, H, W, n_rf, A, E_cap).total;
 }
 
-// counts_out[0..3] = active fields, segments, field rows, and 1 if a group
-// coordinate or run was out of range (then nothing else was computed).
-// The rows are filled by counting, on the premise that every pixel run is
+// The plan's kernels up to the segment count, with no read back: the
+// counts land in the workspace's head (ssla_events_counts layout).  The
+// rows are filled by counting, on the premise that every pixel run is
 // sorted by time (as group_events and pooled outputs leave them), and the
 // segment heads and their prefix sum run over the capacity E_cap, so one
-// read of the counts covers the plan, the premise and the segments; runs
-// that are not sorted send the call through the sort fill and a second read.
-extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
-                                     const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
-                                     int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
-                                     int64_t *counts_out, void *workspace, size_t workspace_bytes, void *stream) {
+// read of the counts covers the plan, the premise and the segments.
+extern "C" int ssla_sparse_pool_plan_enqueue(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
+                                             const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in,
+                                             int B, int H, int W, const int64_t *lut, int64_t n_rf, int A,
+                                             int64_t E_cap, void *workspace, size_t workspace_bytes, void *stream) {
   clear_error();
-  SSLA_CHECK_ARG(G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 && counts_out &&
-                     E_cap >= E_in,
+  SSLA_CHECK_ARG(G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 && E_cap >= E_in,
                  "sparse_pool_plan: bad arguments");
-  const int64_t n_f = static_cast<int64_t>(B) * n_rf;
   SSLA_CHECK_ARG(E_cap < 0x7fffffff && E_in * A < 0x7fffffff,
                  "sparse_pool_plan: the row capacity and E_in * A must stay below 2^31");
   const PoolWs L = pool_layout(workspace, G, B, H, W, n_rf, A, E_cap);
@@ -1375,7 +1383,7 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
   // the plan with the counting fill's inverse table, without the largest
   // time (only the sort fill needs it)
   // a capacity of one row per event promises one field per pixel (more rows
-  // than that are reported below): one thread per event in the fill
+  // than that are reported at the finish): one thread per event in the fill
   const bool one = E_cap == E_in;
   int s = rf_plan_impl(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, L.inv, one, false,
                        workspace, L.rf.total, st);
@@ -1392,20 +1400,32 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
                          E_in, E_cap, L.src, L.tim, static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr),
                          L.rf.act_pre, L.fidx);
   }
-  auto segments = [&]() -> int {
-    hipLaunchKernelGGL(pool_row_heads, dim3(grid_for(E_cap)), dim3(kThreads), 0, st, L.fidx, L.tim, L.rf.counts + 1,
-                       E_cap, L.head);
-    const int r = excl_scan(L.tmp, L.tmp_bytes, L.head, L.segx, E_cap, st);
-    if (r) return r;
-    hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.segx, L.head, E_cap, L.rf.counts + 4);
-    return SSLA_OK;
-  };
-  s = segments();
+  s = pool_segments_pass(L, E_cap, st);
   if (s) return s;
+  return launch_status("sparse_pool_plan");
+}
+
+// The plan's counts read back after ssla_sparse_pool_plan_enqueue (head[0..5]
+// and bad as ssla_events_counts returns them): checks them and, when a
+// pixel run was not sorted by time, runs the sort fill (which reads the
+// device twice more).  counts_out as for ssla_sparse_pool_plan.
+extern "C" int ssla_sparse_pool_plan_finish(const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in,
+                                            int B, int H, int W, const int64_t *lut, int64_t n_rf, int A,
+                                            int64_t E_cap, const int64_t *head, int bad, int64_t *counts_out,
+                                            void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 && E_cap >= E_in && head &&
+                     counts_out,
+                 "sparse_pool_plan: bad arguments");
+  const int64_t n_f = static_cast<int64_t>(B) * n_rf;
+  const PoolWs L = pool_layout(workspace, G, B, H, W, n_rf, A, E_cap);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("sparse_pool_plan: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
   int64_t c[8] = {};
-  int bad = 0;
-  s = ssla_events_counts(workspace, c, 6, &bad, stream);
-  if (s) return s;
+  for (int i = 0; i < 6; ++i) c[i] = head[i];
   for (int i = 0; i < 4; ++i) counts_out[i] = 0;
   if (bad) {
     counts_out[3] = 1;
@@ -1425,6 +1445,7 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
     set_error("sparse_pool_plan: %lld field rows exceed the capacity %lld", (long long)E_out, (long long)E_cap);
     return SSLA_ERR_ARG;
   }
+  int s = SSLA_OK;
   if (c[3] != 0 && E_out > 0) {   // a pixel run not sorted by time: the sort fill
     hipLaunchKernelGGL(max_i64, dim3(grid_for(std::min<int64_t>(E_in, 1 << 16))), dim3(kThreads), 0, st, time, E_in,
                        L.rf.tmax);
@@ -1446,7 +1467,7 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
     hipLaunchKernelGGL(rf_emit, dim3(grid_for(E_out)), dim3(kThreads), 0, st, L.rf.perm, E_out, L.rf.pre_src,
                        L.rf.pre_pos, time, L.src, L.tim, static_cast<int64_t *>(nullptr), L.rf.skey, t_stride,
                        L.fidx);
-    s = segments();
+    s = pool_segments_pass(L, E_cap, st);
     if (s) return s;
     s = ssla_events_counts(workspace, c, 5, nullptr, stream);
     if (s) return s;
@@ -1460,6 +1481,25 @@ extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_
   counts_out[1] = n_seg;
   counts_out[2] = E_out;
   return launch_status("sparse_pool_plan");
+}
+
+// counts_out[0..3] = active fields, segments, field rows, and 1 if a group
+// coordinate or run was out of range (then nothing else was computed):
+// the enqueue, one read of the counts, the finish.
+extern "C" int ssla_sparse_pool_plan(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w,
+                                     const int64_t *gr_len, int64_t G, const int64_t *time, int64_t E_in, int B,
+                                     int H, int W, const int64_t *lut, int64_t n_rf, int A, int64_t E_cap,
+                                     int64_t *counts_out, void *workspace, size_t workspace_bytes, void *stream) {
+  SSLA_CHECK_ARG(counts_out, "sparse_pool_plan: bad arguments");
+  int s = ssla_sparse_pool_plan_enqueue(gr_batch, gr_h, gr_w, gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap,
+                                        workspace, workspace_bytes, stream);
+  if (s) return s;
+  int64_t c[8] = {};
+  int bad = 0;
+  s = ssla_events_counts(workspace, c, 6, &bad, stream);
+  if (s) return s;
+  return ssla_sparse_pool_plan_finish(gr_len, G, time, E_in, B, H, W, lut, n_rf, A, E_cap, c, bad, counts_out,
+                                      workspace, workspace_bytes, stream);
 }
 
 // After ssla_sparse_pool_plan on the same workspace and sizes: out_events

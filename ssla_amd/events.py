@@ -52,6 +52,32 @@ def _counts(ws: torch.Tensor, n: int, stream: int, what: str, check_bad: bool = 
     return [int(v) for v in out]
 
 
+# Counts of a data-dependent call sit at the head of its workspace: int64
+# words from byte 0 and the input-error flag as an int32 at byte 256.
+_HEAD_BYTES = 260
+
+
+class PendingCounts:
+    """The counts of a data-dependent call on their way to host memory: a
+    copy of the workspace head into pinned memory, queued on the current
+    stream behind the call's kernels, and the event after it.  ``read``
+    waits on that event only, so work queued after the copy keeps the
+    device busy meanwhile."""
+    __slots__ = ("host", "event")
+
+    def __init__(self, ws: torch.Tensor):
+        n = min(_HEAD_BYTES, ws.numel())
+        self.host = torch.zeros(_HEAD_BYTES, dtype=torch.uint8, pin_memory=True)
+        self.host[:n].copy_(ws[:n], non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record(torch.cuda.current_stream(ws.device))
+
+    def read(self, n: int):
+        """(counts[0..n), input-error flag) once the copy has landed."""
+        self.event.synchronize()
+        return self.host[:8 * n].view(torch.int64).tolist(), int(self.host[256:260].view(torch.int32)[0])
+
+
 def _i64(t: torch.Tensor) -> torch.Tensor:
     return t.to(torch.int64).contiguous()
 
@@ -360,7 +386,7 @@ class PoolPlan:
     """A pooling plan (ssla_sparse_pool_plan) of one window's structure: the
     workspace that holds it, the call sizes, the counts and, once emitted,
     the pooled structure (time, lengths, batch_id, h, w, batch_size)."""
-    __slots__ = ("ws", "sizes", "n_act", "n_seg", "E_out", "outc", "stream", "structure")
+    __slots__ = ("ws", "sizes", "n_act", "n_seg", "E_out", "outc", "stream", "structure", "pending", "refs")
 
     def tensors(self):
         """The device tensors the plan holds (for Tensor.record_stream when
@@ -368,7 +394,10 @@ class PoolPlan:
         return [self.ws, self.outc] + [v for v in self.structure.values() if isinstance(v, torch.Tensor)]
 
 
-def _pool_plan_call(inputs, frame_size, rf2pixel_lut, rf_outcoord, fields_per_pixel) -> PoolPlan:
+def _pool_plan_call(inputs, frame_size, rf2pixel_lut, rf_outcoord, fields_per_pixel,
+                    enqueue_only: bool = False) -> PoolPlan:
+    """ssla_sparse_pool_plan, or with ``enqueue_only`` its kernels alone and
+    an asynchronous copy of the counts (finished by _pool_plan_finish)."""
     lib = _lib.load()
     gb, gh, gw, gl = (_i64(inputs[k]) for k in ("batch_id", "h", "w", "lengths"))
     time = _i64(inputs["time"])
@@ -381,18 +410,46 @@ def _pool_plan_call(inputs, frame_size, rf2pixel_lut, rf_outcoord, fields_per_pi
     E_cap = E_in * min(A, int(fields_per_pixel) if fields_per_pixel else A)
     ws = _ws(lib.ssla_sparse_pool_workspace_size(G, E_in, B, H, W, n_rf, A, E_cap), dev)
     st = _lib.stream_of(time)
+    plan = PoolPlan()
+    plan.ws, plan.sizes, plan.outc, plan.stream = ws, (G, E_in, B, H, W, n_rf, A, E_cap), outc, st
+    plan.structure = {"batch_size": inputs["batch_size"]}
+    plan.pending, plan.refs = None, None
+    if enqueue_only:
+        _lib.check(lib.ssla_sparse_pool_plan_enqueue(_lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), _lib.ptr(gl), G,
+                                                     _lib.ptr(time), E_in, B, H, W, _lib.ptr(lut), n_rf, A, E_cap,
+                                                     _lib.ptr(ws), ws.numel(), st), "sparse_pool_plan")
+        plan.pending, plan.refs = PendingCounts(ws), (gl, time, lut)
+        return plan
     cnt = (ctypes.c_int64 * 4)()
     _lib.check(lib.ssla_sparse_pool_plan(_lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), _lib.ptr(gl), G, _lib.ptr(time),
                                          E_in, B, H, W, _lib.ptr(lut), n_rf, A, E_cap, cnt, _lib.ptr(ws), ws.numel(),
                                          st), "sparse_pool_plan")
+    _pool_plan_counts(plan, cnt)
+    return plan
+
+
+def _pool_plan_counts(plan: PoolPlan, cnt):
     n_act, n_seg, E_out, bad = (int(v) for v in cnt)
     if bad:
         raise ValueError("sparse_pool: input indices or coordinates out of range")
-    plan = PoolPlan()
-    plan.ws, plan.sizes, plan.outc, plan.stream = ws, (G, E_in, B, H, W, n_rf, A, E_cap), outc, st
     plan.n_act, plan.n_seg, plan.E_out = n_act, n_seg, E_out
-    plan.structure = {"batch_size": inputs["batch_size"]}
-    return plan
+
+
+def _pool_plan_finish(plan: PoolPlan):
+    """The counts of an enqueued plan (waiting for their copy), checked by
+    ssla_sparse_pool_plan_finish (which runs the sort fill when a pixel run
+    was not sorted by time)."""
+    head, bad = plan.pending.read(6)
+    gl, time, lut = plan.refs
+    G, E_in, B, H, W, n_rf, A, E_cap = plan.sizes
+    hv = (ctypes.c_int64 * 6)(*head)
+    cnt = (ctypes.c_int64 * 4)()
+    _lib.check(_lib.load().ssla_sparse_pool_plan_finish(_lib.ptr(gl), G, _lib.ptr(time), E_in, B, H, W,
+                                                       _lib.ptr(lut), n_rf, A, E_cap, hv, int(bad), cnt,
+                                                       _lib.ptr(plan.ws), plan.ws.numel(), plan.stream),
+               "sparse_pool_plan")
+    plan.pending, plan.refs = None, None
+    _pool_plan_counts(plan, cnt)
 
 
 def _pool_emit(plan: PoolPlan, ev, mean, structure: bool):
@@ -433,6 +490,21 @@ def sparse_pool_plan(inputs, frame_size, rf2pixel_lut, rf_outcoord,
     follow with sparse_pool_values on the same plan, so the structure of a
     window can be planned before the values that pass through it exist."""
     plan = _pool_plan_call(inputs, frame_size, rf2pixel_lut, rf_outcoord, fields_per_pixel)
+    _pool_emit(plan, None, False, True)
+    return plan
+
+
+def sparse_pool_plan_enqueue(inputs, frame_size, rf2pixel_lut, rf_outcoord,
+                             fields_per_pixel: Optional[int] = None) -> PoolPlan:
+    """sparse_pool_plan in two halves: the plan's kernels and an
+    asynchronous copy of its counts now, the counts and the structure in
+    sparse_pool_plan_finish, so that work queued in between keeps the device
+    busy while the host waits."""
+    return _pool_plan_call(inputs, frame_size, rf2pixel_lut, rf_outcoord, fields_per_pixel, enqueue_only=True)
+
+
+def sparse_pool_plan_finish(plan: PoolPlan) -> PoolPlan:
+    _pool_plan_finish(plan)
     _pool_emit(plan, None, False, True)
     return plan
 
@@ -478,10 +550,9 @@ def events_to_grid(x: Dict[str, torch.Tensor], grid_size, channels: int) -> torc
     return grid
 
 
-def _preprocess_one_call(events, lengths, frame_size, hot_pixel_thres, max_events_per_px: int = 512):
-    """preprocess_inputs as one library call (ssla_preprocess_events): the
-    grouping, the delays and the truncation share one device pass and one
-    read of the counts."""
+def _preprocess_launch(events, lengths, frame_size, hot_pixel_thres, max_events_per_px: int = 512):
+    """ssla_preprocess_events into capacity-sized outputs: (workspace,
+    stream, outputs, batch size); the counts stay on the device."""
     ev = events.to(torch.float32).contiguous()
     ln = _i64(lengths)
     dev = _lib.require_cuda(ev, ln)
@@ -498,9 +569,39 @@ def _preprocess_one_call(events, lengths, frame_size, hot_pixel_thres, max_event
                                           int(hot_pixel_thres), _lib.ptr(out_ev), _lib.ptr(out_t), _lib.ptr(grp[0]),
                                           _lib.ptr(grp[1]), _lib.ptr(grp[2]), _lib.ptr(grp[3]), _lib.ptr(ws),
                                           ws.numel(), st), "preprocess_events")
-    G, E, _ = _counts(ws, 3, st, "preprocess_events")
+    return ws, st, (out_ev, out_t, grp), B
+
+
+def _preprocess_result(outs, B, G: int, E: int):
+    out_ev, out_t, grp = outs
     return {"events": out_ev[:E], "time": out_t[:E], "batch_id": grp[0, :G], "h": grp[1, :G], "w": grp[2, :G],
             "lengths": grp[3, :G], "batch_size": B}
+
+
+def _preprocess_one_call(events, lengths, frame_size, hot_pixel_thres, max_events_per_px: int = 512):
+    """preprocess_inputs as one library call (ssla_preprocess_events): the
+    grouping, the delays and the truncation share one device pass and one
+    read of the counts."""
+    ws, st, outs, B = _preprocess_launch(events, lengths, frame_size, hot_pixel_thres, max_events_per_px)
+    G, E, _ = _counts(ws, 3, st, "preprocess_events")
+    return _preprocess_result(outs, B, G, E)
+
+
+def preprocess_enqueue(events, lengths, frame_size, hot_pixel_thres: int = 50):
+    """The first half of preprocess_inputs on a GPU (padded [B, N, >= 4]
+    events): the library call and an asynchronous copy of its counts.
+    preprocess_finish waits for the counts and returns what
+    preprocess_inputs returns."""
+    ws, _st, outs, B = _preprocess_launch(events, lengths, frame_size, hot_pixel_thres)
+    return (PendingCounts(ws), ws, outs, B)
+
+
+def preprocess_finish(pending) -> Dict[str, torch.Tensor]:
+    counts, ws, outs, B = pending
+    (G, E, _), bad = counts.read(3)
+    if bad:
+        raise ValueError("preprocess_events: input indices or coordinates out of range")
+    return _preprocess_result(outs, B, G, E)
 
 
 def preprocess_inputs(events: torch.Tensor, lengths: torch.Tensor, frame_size, hot_pixel_thres: int = 50):

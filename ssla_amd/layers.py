@@ -372,6 +372,22 @@ class SparsePool(AsyncSparseModule):
         return E.sparse_pool_plan(inputs, self.frame_size, self.rf2pixel_lut, self.rf_outcoord,
                                   fields_per_pixel=self._fields_per_pixel())
 
+    def plan_enqueue(self, inputs) -> "E.PoolPlan":
+        """``plan`` in two halves (E.sparse_pool_plan_enqueue): the plan's
+        kernels and an asynchronous copy of its counts; ``plan_finish`` waits
+        for the counts and emits the structure."""
+        if self.pool_func not in (scatter_max, scatter_mean) or (self.kernel_size == (1, 1)
+                                                                 and self.stride == (1, 1)):
+            raise ValueError("SparsePool.plan: needs max or mean pooling over fields larger than one pixel")
+        dev = inputs["time"].device
+        _ensure_lut(self, "rf2pixel_lut", "rf_outcoord", self.frame_size, self.kernel_size, self.stride, dev)
+        return E.sparse_pool_plan_enqueue(inputs, self.frame_size, self.rf2pixel_lut, self.rf_outcoord,
+                                          fields_per_pixel=self._fields_per_pixel())
+
+    @staticmethod
+    def plan_finish(plan: "E.PoolPlan") -> "E.PoolPlan":
+        return E.sparse_pool_plan_finish(plan)
+
     def apply_plan(self, plan: "E.PoolPlan", events: torch.Tensor) -> Dict[str, torch.Tensor]:
         """forward's output for the values ``events`` of the groups ``plan``
         was made from."""

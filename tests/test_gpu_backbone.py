@@ -235,6 +235,74 @@ def test_async_plan_then_forward_matches(dev):
         assert torch.equal(s_seq[i], s_pl[i]), f"stage {i}: carried states differ"
 
 
+def test_async_run_matches_forward(dev):
+    """run() over four 50k-event windows (each window planned step by step
+    while the previous one's stages run, counts copied back without
+    draining the stream) equals forward() window by window, bit for bit:
+    head outputs, every stage's events and structure, the carried states;
+    a second run() on the same states continues them the same way."""
+    from ssla_amd import synthetic
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(7)
+    model = AsyncSparseGLA().to(dev).eval()
+    wins = [w.to(dev) for w in synthetic.async_windows(6, 50_000, seed=8)]
+    lns = [torch.tensor([50_000], device=dev)] * len(wins)
+    print("async run vs forward", flush=True)
+    with torch.no_grad():
+        s_seq = model.init_states(1, dev)
+        seq = [model(w, ln, s_seq) for w, ln in zip(wins, lns)]
+        s_run = model.init_states(1, dev)
+        got = model.run(wins[:4], lns[:4], s_run) + model.run(wins[4:], lns[4:], s_run)
+        assert model.run([], [], s_run) == []
+    assert len(got) == len(seq)
+    for w, ((o1, f1), (o2, f2)) in enumerate(zip(seq, got)):
+        assert torch.equal(o1, o2), f"window {w}: head output differs"
+        for i in range(4):
+            for key in ("events", "time", "lengths", "batch_id", "h", "w"):
+                assert torch.equal(f1[i][key], f2[i][key]), f"window {w} stage {i}: {key} differs"
+    for i in range(4):
+        assert torch.equal(s_seq[i], s_run[i]), f"stage {i}: carried states differ"
+
+
+def test_pool_plan_halves_match_plan(dev):
+    """ssla_sparse_pool_plan_enqueue + an asynchronous copy of the counts +
+    ssla_sparse_pool_plan_finish give the plan, structure and pooled values
+    of ssla_sparse_pool_plan, for runs sorted by time (the counting fill)
+    and for runs that are not (the sort fill inside the finish), and report
+    out-of-range coordinates the same way."""
+    from ssla_amd import events as E
+    from ssla_amd.layers import SparseMaxPool
+    torch.manual_seed(3)
+    frame = (24, 30)
+    pool = SparseMaxPool(frame, kernel_size=(3, 3), stride=(2, 2)).to(dev)
+    print("pool plan halves", flush=True)
+    for sort_times in (True, False):
+        G, B = 200, 2
+        cells = torch.randperm(frame[0] * frame[1] * B)[:G].sort().values
+        lengths = torch.randint(1, 6, (G,))
+        E_in = int(lengths.sum())
+        times = torch.randint(0, 40, (E_in,))
+        if sort_times:   # every pixel run sorted by time
+            starts = torch.cumsum(lengths, 0) - lengths
+            times = torch.cat([times[s:s + n].sort().values for s, n in zip(starts.tolist(), lengths.tolist())])
+        inputs = {"batch_id": (cells // (frame[0] * frame[1])).to(dev),
+                  "h": ((cells % (frame[0] * frame[1])) // frame[1]).to(dev),
+                  "w": (cells % frame[1]).to(dev), "lengths": lengths.to(dev), "time": times.to(dev),
+                  "batch_size": B}
+        ev = torch.randn(E_in, 16, device=dev)
+        with torch.no_grad():
+            ref = pool.plan(dict(inputs))
+            ref_out = pool.apply_plan(ref, ev)
+            got = pool.plan_finish(pool.plan_enqueue(dict(inputs)))
+            got_out = pool.apply_plan(got, ev)
+        assert (ref.n_act, ref.n_seg, ref.E_out) == (got.n_act, got.n_seg, got.E_out)
+        for key in ("events", "time", "lengths", "batch_id", "h", "w"):
+            assert torch.equal(ref_out[key], got_out[key]), f"sorted={sort_times}: {key} differs"
+    bad = dict(inputs, h=inputs["h"] + frame[0])
+    with torch.no_grad(), pytest.raises(ValueError):
+        pool.plan_finish(pool.plan_enqueue(bad))
+
+
 def test_head_kernel_matches_module(dev):
     """ssla_detect_head (all levels in one kernel, fp32 between its two bf16
     GEMMs) against the module's bf16 ops run one by one and against the fp64
