@@ -662,7 +662,7 @@ def bench_async_step(torch, lib, dev, n_windows=20, n_events=50_000, cpu=True):
     with torch.no_grad():
         lns = [ln] * len(wins)
         warm = model.init_states(1, dev)
-        model.run(wins[:3], lns[:3], warm)
+        model.run(wins, lns, warm)   # a whole pass: pinned count buffers and allocator pools warm
         for w in wins[:2]:
             model(w, ln, warm)
         states = model.init_states(1, dev)
