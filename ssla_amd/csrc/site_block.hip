@@ -29,16 +29,6 @@ constexpr int kRows = 16 * kWaves;   // event rows per workgroup
 
 typedef float f32x8v __attribute__((ext_vector_type(8)));
 
-// Eight consecutive fp32 inputs of a row, rounded to bf16 (zeros when the
-// row does not exist).
-__device__ __forceinline__ bf16x8 a_from_f32(const float *x, int64_t row, int ld, int k, bool ok) {
-  if (!ok) return bf16x8{};
-  const float4 u = *reinterpret_cast<const float4 *>(x + row * ld + k);
-  const float4 w = *reinterpret_cast<const float4 *>(x + row * ld + k + 4);
-  const f32x8v v = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
-  return __builtin_convertvector(v, bf16x8);
-}
-
 // Eight consecutive bf16 values of a row of a [rows, ld] bf16 matrix.
 __device__ __forceinline__ bf16x8 bf16_piece(const uint16_t *p, int64_t row, int ld, int k, bool ok) {
   if (!ok) return bf16x8{};
@@ -52,9 +42,11 @@ __device__ __forceinline__ float round_bf16(float x) {
 // grid (row tiles of 64 events, column chunks of 16 NTO); w is [4 hd, cin]
 // (the rows of Wq, Wk, Wv, Wg in turn).  Wavefront w computes output w
 // (q, k, v, g) for all 64 rows of the tile: 4 x NTO MFMA tiles, each weight
-// piece reused by the 4 row tiles.  The tile's inputs are staged once in LDS
-// as bf16 (shared by the 4 wavefronts); the results leave through a
-// wave-private LDS block in 16-byte row pieces.
+// piece reused by the 4 row tiles.  The tile's inputs are staged in LDS one
+// 32-wide reduction step at a time as bf16 (shared by the 4 wavefronts),
+// the next step's inputs loaded while the current step is multiplied (rows
+// past n read row n - 1; their outputs are never stored); the results
+// leave through a wave-private LDS block in 16-byte row pieces.
 template <int NTO>
 __global__ __launch_bounds__(64 * kWaves) void site_project_kernel(const float *__restrict__ x, int64_t n, int cin,
                                                                    const uint16_t *__restrict__ w, int hd,
@@ -77,12 +69,19 @@ __global__ __launch_bounds__(64 * kWaves) void site_project_kernel(const float *
     for (int t = 0; t < NTO; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   // staging: thread -> (row tid / 4, inputs 8 (tid % 4) .. + 7)
   const int sr = tid >> 2, sk = 8 * (tid & 3);
-  const int64_t srow = e0 + sr;
+  const int64_t srow = min(e0 + sr, n - 1);   // n > 0 (the launcher returns before)
+  const float *xrow = x + srow * cin + sk;
+  float4 xa = *reinterpret_cast<const float4 *>(xrow), xb = *reinterpret_cast<const float4 *>(xrow + 4);
   for (int k0 = 0; k0 < cin; k0 += 32) {
-    const bf16x8 xv = a_from_f32(x, srow, cin, k0 + sk, srow < n);
+    const f32x8v xf = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
     bf16x8 bv[NTO];
 #pragma unroll
     for (int t = 0; t < NTO; ++t) bv[t] = bf16_piece(wb, 16 * t + r, cin, k0 + kq, true);
+    if (k0 + 32 < cin) {
+      xa = *reinterpret_cast<const float4 *>(xrow + k0 + 32);
+      xb = *reinterpret_cast<const float4 *>(xrow + k0 + 36);
+    }
+    const bf16x8 xv = __builtin_convertvector(xf, bf16x8);
     __syncthreads();   // the previous step's reads of xs are done
     *reinterpret_cast<bf16x8 *>(&xs[sr][sk]) = xv;
     __syncthreads();
@@ -138,8 +137,11 @@ __global__ __launch_bounds__(64 * kWaves) void site_project_kernel(const float *
 
 // One wavefront: 16 rows x 16 NT output columns, LayerNorm over them.  The
 // weights of each 32-wide reduction step are staged in LDS once per
-// workgroup (shared by its 4 wavefronts); the next step's pieces are
-// loaded while the current one is multiplied.
+// workgroup (shared by its 4 wavefronts); the next step's weight pieces and
+// the next step's row pieces (o, then x) are loaded while the current step
+// is multiplied, so the steps do not each wait on a memory round trip.
+// Rows past n read row n - 1 (their results are never stored, and the
+// LayerNorm sums stay within a row).
 template <int NT>
 __global__ __launch_bounds__(64 * kWaves) void site_finish_kernel(const uint16_t *__restrict__ o, int64_t n, int hd,
                                                                   const uint16_t *__restrict__ wo,
@@ -154,8 +156,7 @@ __global__ __launch_bounds__(64 * kWaves) void site_finish_kernel(const uint16_t
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r = lane & 15, kq = 8 * (lane >> 4);
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kRows + 16 * wv;
-  const int64_t row = e0 + r;
-  const bool rok = row < n;
+  const int64_t row = min(e0 + r, n - 1);   // n > 0 (the launcher returns before)
   f32x4 acc[NT], res[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = res[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -179,13 +180,29 @@ __global__ __launch_bounds__(64 * kWaves) void site_finish_kernel(const uint16_t
     }
     __syncthreads();
   };
+  // this lane's row pieces: o as bf16, x as fp32 (rounded when used)
+  auto o_piece = [&](int k0) __attribute__((always_inline)) {
+    return *reinterpret_cast<const uint4 *>(o + row * hd + k0 + kq);
+  };
+  auto x_piece = [&](int k0, float4 (&xv)[2]) __attribute__((always_inline)) {
+    xv[0] = *reinterpret_cast<const float4 *>(x + row * cin + k0 + kq);
+    xv[1] = *reinterpret_cast<const float4 *>(x + row * cin + k0 + kq + 4);
+  };
   uint4 pcur[PT];
   fetch(wo, hd, 0, pcur);
+  uint4 ocur = o_piece(0);
+  float4 xcur[2];
   for (int k0 = 0; k0 < hd; k0 += 32) {
     stage(pcur);
-    if (k0 + 32 < hd) fetch(wo, hd, k0 + 32, pcur);
-    else if (wr) fetch(wr, cin, 0, pcur);
-    const bf16x8 a = bf16_piece(o, row, hd, k0 + kq, rok);
+    const uint4 a_bits = ocur;
+    if (k0 + 32 < hd) {
+      fetch(wo, hd, k0 + 32, pcur);
+      ocur = o_piece(k0 + 32);
+    } else if (wr) {
+      fetch(wr, cin, 0, pcur);
+      x_piece(0, xcur);
+    }
+    const bf16x8 a = __builtin_bit_cast(bf16x8, a_bits);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, *reinterpret_cast<const bf16x8 *>(&wst[16 * t + r][kq]),
@@ -194,8 +211,12 @@ __global__ __launch_bounds__(64 * kWaves) void site_finish_kernel(const uint16_t
   if (wr) {
     for (int k0 = 0; k0 < cin; k0 += 32) {
       stage(pcur);
-      if (k0 + 32 < cin) fetch(wr, cin, k0 + 32, pcur);
-      const bf16x8 a = a_from_f32(x, row, cin, k0 + kq, rok);
+      const f32x8v xf = {xcur[0].x, xcur[0].y, xcur[0].z, xcur[0].w, xcur[1].x, xcur[1].y, xcur[1].z, xcur[1].w};
+      if (k0 + 32 < cin) {
+        fetch(wr, cin, k0 + 32, pcur);
+        x_piece(k0 + 32, xcur);
+      }
+      const bf16x8 a = __builtin_convertvector(xf, bf16x8);
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         res[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, *reinterpret_cast<const bf16x8 *>(&wst[16 * t + r][kq]),
