@@ -132,6 +132,7 @@ enum { kPlain = 0, kSegState = 1, kSegOut = 2 };
 
 struct SegWs {
   const int64_t *segoff;   // [n_seq + 1]
+  const int4 *segmap;      // [n_segs_max]: (sequence, segment of it, its segment count, 0)
   float *slot;             // [n_segs_max, H, K, V]: L_j
   float *prod;             // [n_segs_max, H, K]: P_j
   float *h0c;              // [n_seq, H, K, V]: copy of the initial states
@@ -139,25 +140,17 @@ struct SegWs {
   int seg_steps;           // steps per segment (the last of a sequence may be shorter)
 };
 
-__device__ __forceinline__ int find_seg_seq(const int64_t *off, int n_seq, int64_t i) {
-  int lo = 0, hi = n_seq - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (off[mid] <= i) lo = mid;
-    else hi = mid - 1;
-  }
-  return lo;
-}
-
-// segoff[n] = segments of sequences 0..n-1 (segoff[n_seq]: the total).  One
-// workgroup of 256 threads.  The grid holds n_segs_max segments, which
+// segoff[n] = segments of sequences 0..n-1 (segoff[n_seq]: the total) and
+// segmap[s] = (sequence, segment of it, its segment count) for every
+// segment s below the total.  One workgroup of 256 threads.  The grid holds n_segs_max segments, which
 // bounds the total when cu_seqlens is non-decreasing (the sequences then
 // share the T rows); with sequences that overlap the total can exceed it,
 // and the segments past the grid would not run: the total is then capped at
 // n_segs_max and SSLA_ERR_ARG goes to the status word (when one is given).
 __global__ __launch_bounds__(256) void seg_offsets_kernel(const int64_t *__restrict__ cu, int n_seq, int64_t T,
                                                           int seg_steps, int64_t n_segs_max,
-                                                          int64_t *__restrict__ segoff, int32_t *__restrict__ status) {
+                                                          int64_t *__restrict__ segoff, int4 *__restrict__ segmap,
+                                                          int32_t *__restrict__ status) {
   __shared__ int64_t ps[256];
   int64_t carry = 0;
   for (int base = 0; base < n_seq; base += 256) {
@@ -176,7 +169,14 @@ __global__ __launch_bounds__(256) void seg_offsets_kernel(const int64_t *__restr
       ps[threadIdx.x] += x;
       __syncthreads();
     }
-    if (n < n_seq) segoff[n] = min(carry + ps[threadIdx.x] - c, n_segs_max);
+    if (n < n_seq) {
+      const int64_t first = carry + ps[threadIdx.x] - c;
+      segoff[n] = min(first, n_segs_max);
+      // each segment's sequence and place in it, so a wavefront finds its
+      // unit with one load instead of a search over segoff
+      for (int64_t j = 0; j < c && first + j < n_segs_max; ++j)
+        segmap[first + j] = make_int4(n, static_cast<int>(j), static_cast<int>(c), 0);
+    }
     carry += ps[255];
     __syncthreads();
   }
@@ -275,10 +275,12 @@ __global__ __launch_bounds__(256, KPL <= 8 ? 4 : 3) void gla_recurrent_staged_ke
     u.seg = 0;
     u.nseg = 1;
     if (MODE != kPlain) {
-      if (un >= sw.segoff[n_seq]) return u;   // past the actual segment count
-      u.n = find_seg_seq(sw.segoff, n_seq, un);
-      u.seg = static_cast<int>(un - sw.segoff[u.n]);
-      u.nseg = static_cast<int>(sw.segoff[u.n + 1] - sw.segoff[u.n]);
+      const int64_t n_segs = sw.segoff[n_seq];
+      const int4 m = sw.segmap[un];   // written for every segment below n_segs
+      if (un >= n_segs) return u;     // past the actual segment count
+      u.n = m.x;
+      u.seg = m.y;
+      u.nseg = m.z;
       if (MODE == kSegState && u.seg == u.nseg - 1) return u;   // the last segment needs no local state
     }
     const int64_t sbos = min(max(cu_seqlens[u.n], (int64_t)0), T);
@@ -432,7 +434,7 @@ __global__ __launch_bounds__(256, KPL <= 8 ? 4 : 3) void gla_recurrent_staged_ke
       float L[kFoldB][KPL], P[kFoldB][KPL];
 #pragma unroll
       for (int u = 0; u < kFoldB; ++u) {
-        const int64_t gj = sw.segoff[cur.n] + j0 + u;
+        const int64_t gj = cur.gseg - cur.seg + j0 + u;   // segment j0 + u of this sequence
         const bool ok = j0 + u < cur.seg;
 #pragma unroll
         for (int i = 0; i < KPL; ++i) {
@@ -601,7 +603,7 @@ __global__ __launch_bounds__(256) void gla_recurrent_kernel(
 // outside the staged kernels, or sequences of fewer than kSegSteps / 4
 // steps on average, where one pass is as fast).
 struct SegLayout {
-  size_t segoff, slot, prod, h0c, total;
+  size_t segoff, segmap, slot, prod, h0c, total;
   int64_t n_segs_max;
   int seg_steps;
 };
@@ -627,6 +629,7 @@ inline SegLayout seg_layout(int n_seq, int64_t T, int H, int K, int V) {
   const size_t hkv = static_cast<size_t>(H) * K * V;
   size_t p = 0;
   L.segoff = p; p = align256(p + sizeof(int64_t) * (n_seq + 1));
+  L.segmap = p; p = align256(p + sizeof(int4) * L.n_segs_max);
   L.slot = p;   p = align256(p + sizeof(float) * L.n_segs_max * hkv);
   L.prod = p;   p = align256(p + sizeof(float) * L.n_segs_max * H * K);
   L.h0c = p;    p = align256(p + sizeof(float) * n_seq * hkv);
@@ -670,6 +673,7 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
     if (segmented) {
       char *w = static_cast<char *>(workspace);
       sw.segoff = reinterpret_cast<const int64_t *>(w + L.segoff);
+      sw.segmap = reinterpret_cast<const int4 *>(w + L.segmap);
       sw.slot = reinterpret_cast<float *>(w + L.slot);
       sw.prod = reinterpret_cast<float *>(w + L.prod);
       sw.h0c = reinterpret_cast<float *>(w + L.h0c);
@@ -677,7 +681,8 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
       sw.seg_steps = L.seg_steps;
       sgrid = dim3(static_cast<unsigned>((L.n_segs_max * H * n_vt + waves_per_block - 1) / waves_per_block));
       hipLaunchKernelGGL(seg_offsets_kernel, dim3(1), dim3(256), 0, st, cu, n_seq, T, L.seg_steps, L.n_segs_max,
-                         reinterpret_cast<int64_t *>(w + L.segoff), status);
+                         reinterpret_cast<int64_t *>(w + L.segoff), reinterpret_cast<int4 *>(w + L.segmap),
+                         status);
     }
 #define SSLA_RECS(KPL_)                                                                                     \
   if (segmented) {                                                                                          \
