@@ -264,6 +264,38 @@ def test_async_run_matches_forward(dev):
         assert torch.equal(s_seq[i], s_run[i]), f"stage {i}: carried states differ"
 
 
+def test_async_run_batched_ragged(dev):
+    """run() on windows of two samples with different lengths (the padded
+    [B, N, 4] batch the reference collates, padding rows never read) equals
+    forward() window by window, bit for bit, states included."""
+    from ssla_amd import synthetic
+    from ssla_amd.backbone import AsyncSparseGLA
+    torch.manual_seed(9)
+    model = AsyncSparseGLA().to(dev).eval()
+    a = synthetic.async_windows(3, 30_000, seed=10)
+    b = synthetic.async_windows(3, 30_000, seed=11)
+    wins, lns = [], []
+    for i, (wa, wb) in enumerate(zip(a, b)):
+        na, nb = 30_000 - 4_000 * i, 21_000 + 3_000 * i
+        w = torch.full((2, 30_000, 4), -7.0)   # padding rows hold junk
+        w[0, :na], w[1, :nb] = wa[0, :na], wb[0, :nb]
+        wins.append(w.to(dev))
+        lns.append(torch.tensor([na, nb], device=dev))
+    print("async run batched ragged", flush=True)
+    with torch.no_grad():
+        s_seq = model.init_states(2, dev)
+        seq = [model(w, ln, s_seq) for w, ln in zip(wins, lns)]
+        s_run = model.init_states(2, dev)
+        got = model.run(wins, lns, s_run)
+    for w, ((o1, f1), (o2, f2)) in enumerate(zip(seq, got)):
+        assert torch.equal(o1, o2), f"window {w}: head output differs"
+        for i in range(4):
+            for key in ("events", "time", "lengths", "batch_id", "h", "w"):
+                assert torch.equal(f1[i][key], f2[i][key]), f"window {w} stage {i}: {key} differs"
+    for i in range(4):
+        assert torch.equal(s_seq[i], s_run[i]), f"stage {i}: carried states differ"
+
+
 def test_pool_plan_halves_match_plan(dev):
     """ssla_sparse_pool_plan_enqueue + an asynchronous copy of the counts +
     ssla_sparse_pool_plan_finish give the plan, structure and pooled values
