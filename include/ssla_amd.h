@@ -581,6 +581,26 @@ int ssla_events_to_grid(const float *events, int64_t E, int C, const int64_t *le
                         const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr_w, int64_t G, int B,
                         int Hg, int Wg, float *grid, void *workspace, size_t workspace_bytes, void *stream);
 
+/* async_event_to_grid (model_mos.py:212-228) for several levels in one
+ * launch, each grid [B, C, Hg, Wg] written whole: the last event of every
+ * group at its cell, 0 elsewhere (the reference's index_add_ into zeros,
+ * one group per cell).  No workspace.  status (optional, device int32) is
+ * set to 1 when a group's cell or last event lies out of range (that group
+ * is skipped).  Each level needs B * Hg * Wg <= SSLA_GRIDS_MAX_CELLS. */
+#define SSLA_GRIDS_MAX_LEVELS 8
+#define SSLA_GRIDS_MAX_CELLS 16384
+typedef struct {
+  const float *events;
+  const int64_t *lengths;
+  const int64_t *batch;
+  const int64_t *h;
+  const int64_t *w;
+  float *grid;
+  int64_t E, G;
+  int C, Hg, Wg;
+} ssla_grid_level;
+int ssla_events_to_grids(const ssla_grid_level *levels, int n_levels, int B, int32_t *status, void *stream);
+
 /* ------------------------------------------------------------------------
  * Event ingestion: Prophesee .dat Event2D records -> the padded batch
  * tensor (reference utils/io/dat_events_tools.py:15,40-47 record decode;

@@ -34,6 +34,15 @@ class HeadLevel(C.Structure):
                 ("w_pred", C.c_void_p), ("b_pred", C.c_void_p), ("c", C.c_int), ("h", C.c_int), ("w", C.c_int),
                 ("stride", C.c_int)]
 
+class GridLevel(C.Structure):
+    """ssla_grid_level of include/ssla_amd.h."""
+    _fields_ = [("events", C.c_void_p), ("lengths", C.c_void_p), ("batch", C.c_void_p), ("h", C.c_void_p),
+                ("w", C.c_void_p), ("grid", C.c_void_p), ("E", C.c_int64), ("G", C.c_int64), ("C", C.c_int),
+                ("Hg", C.c_int), ("Wg", C.c_int)]
+
+
+GRIDS_MAX_LEVELS, GRIDS_MAX_CELLS = 8, 16384
+
 # name -> (restype, argtypes); must match include/ssla_amd.h
 SIGNATURES = {
     "ssla_version": (_i32, []),
@@ -110,6 +119,7 @@ SIGNATURES = {
     "ssla_pixel_delays": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _sz, _vp]),
     "ssla_events_to_grid": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _sz,
                                    _vp]),
+    "ssla_events_to_grids": (_i32, [C.POINTER(GridLevel), _i32, _i32, _vp, _vp]),
     "ssla_dat_decode_batch": (_i32, [_vp, _i64, _vp, _i32, _i64, _i32, _vp, _vp]),
 }
 

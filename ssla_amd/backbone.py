@@ -469,7 +469,7 @@ class AsyncSparseGLA(nn.Module):
                 if mark:
                     mark(f"s{i}.pool")
                 yield
-        grids = [E.events_to_grid(feats[i], self.grid_sizes[i], self.stages[i][0]) for i in self.head_levels]
+        grids = E.events_to_grids([(feats[i], self.grid_sizes[i], self.stages[i][0]) for i in self.head_levels])
         if mark:
             mark("grids")
         out = self.head(grids)

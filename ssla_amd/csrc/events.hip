@@ -50,12 +50,13 @@ struct Carve {
   }
 };
 
-// Radix sorts run rocPRIM's onesweep LSD passes at every size above one
-// block (a merge-sort limit of 0): for the narrow keys sorted here (pixel
-// ids, field x time) a few 8-bit passes beat the merge sort rocPRIM picks by
-// default below 2^20 items of 8-byte keys.
+// Radix sorts of (8-byte key, 4-byte value) pairs: rocPRIM's merge sort up
+// to 2^18 items, its onesweep LSD passes above.  Measured on MI355X
+// (µs per sort, 17-bit / 36-bit keys): 20k items 36 / 39 merge against 74 /
+// 118 onesweep, 50k 40 / 43 against 76 / 123, 200k 67 / 71 against 81 /
+// 131, 500k 138 / 141 against 88 / 140, 1M 183 / 190 against 97 / 155.
 using SortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
-                                              rocprim::default_config, 0>;
+                                              rocprim::default_config, (size_t{1} << 18)>;
 
 // rocPRIM temporary storage sizes (queried with a null buffer).
 size_t sort_temp_bytes(size_t n) {
@@ -681,6 +682,72 @@ __global__ void grid_place(const float *__restrict__ ev, const int64_t *__restri
     // one group per cell, so the reference's index_add_ into zeros is a store
     grid[((b * C + c) * Hg + h) * Wg + w] = ev[last * C + c];
   }
+}
+
+// Several grids in one launch: one workgroup per (level, block of kGridCB
+// channels).  Each workgroup builds its level's cell -> last-event map in
+// LDS from the group lengths (a running prefix over chunks of the block
+// size), then writes its channel planes cell by cell, 0 where no group
+// sits: every element is written once, so the grid needs no clearing and
+// no two workgroups touch the same address.
+constexpr int kGridThreads = 256, kGridCB = 8;
+struct GridArgs {
+  ssla_grid_level lv[SSLA_GRIDS_MAX_LEVELS];
+  int blk0[SSLA_GRIDS_MAX_LEVELS + 1];
+  int n_levels, B;
+};
+
+__global__ __launch_bounds__(kGridThreads) void grids_kernel(GridArgs a, int32_t *status) {
+  extern __shared__ int32_t cell_ev[];
+  __shared__ int64_t wsum[kGridThreads / 64];
+  int L = 0;
+  while (L + 1 < a.n_levels && static_cast<int>(blockIdx.x) >= a.blk0[L + 1]) ++L;
+  const ssla_grid_level &lv = a.lv[L];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t HW = static_cast<int64_t>(lv.Hg) * lv.Wg, cells = a.B * HW;
+  for (int64_t i = tid; i < cells; i += kGridThreads) cell_ev[i] = -1;
+  __syncthreads();
+  bool bad = false;
+  int64_t carry = 0;
+  for (int64_t base = 0; base < lv.G; base += kGridThreads) {
+    const int64_t g = base + tid;
+    const int64_t len = g < lv.G ? lv.lengths[g] : 0;
+    int64_t x = len;   // inclusive scan across the wavefront
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int64_t y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[wv] = x;
+    __syncthreads();
+    int64_t pre = 0, tot = 0;
+#pragma unroll
+    for (int j = 0; j < kGridThreads / 64; ++j) {
+      pre += j < wv ? wsum[j] : 0;
+      tot += wsum[j];
+    }
+    if (g < lv.G) {
+      const int64_t b = lv.batch[g], h = lv.h[g], w = lv.w[g], last = carry + pre + x - 1;
+      if (b < 0 || b >= a.B || h < 0 || h >= lv.Hg || w < 0 || w >= lv.Wg || last < 0 || last >= lv.E) bad = true;
+      else cell_ev[(b * lv.Hg + h) * lv.Wg + w] = static_cast<int32_t>(last);
+    }
+    carry += tot;
+    __syncthreads();   // wsum is rewritten by the next chunk
+  }
+  // (the loop's last barrier orders the map's writes before the reads)
+  const int c0 = (static_cast<int>(blockIdx.x) - a.blk0[L]) * kGridCB;
+  const int nc = min(kGridCB, lv.C - c0);
+  const uint32_t ucells = static_cast<uint32_t>(cells);
+  for (uint32_t t = tid; t < static_cast<uint32_t>(nc) * ucells; t += kGridThreads) {
+    const uint32_t cl = t / ucells, cell = t - cl * ucells;
+    const uint32_t b = cell / static_cast<uint32_t>(HW), hw = cell - b * static_cast<uint32_t>(HW);
+    const int c = c0 + static_cast<int>(cl);
+    const int32_t e = cell_ev[cell];
+    lv.grid[(static_cast<int64_t>(b) * lv.C + c) * HW + hw] = e >= 0 ? lv.events[static_cast<int64_t>(e) * lv.C + c]
+                                                                      : 0.f;
+  }
+  const int any_bad = __syncthreads_or(bad ? 1 : 0);
+  if (status && any_bad && tid == 0) *status = 1;
 }
 
 }  // namespace
@@ -1824,6 +1891,41 @@ extern "C" int ssla_events_to_grid(const float *events, int64_t E, int C, const 
   hipLaunchKernelGGL(grid_place, dim3(grid_for(G * C)), dim3(kThreads), 0, st, events, L.kl, gr_batch, gr_h, gr_w, G,
                      E, C, B, Hg, Wg, grid, L.bad);
   return launch_status("events_to_grid");
+}
+
+extern "C" int ssla_events_to_grids(const ssla_grid_level *levels, int n_levels, int B, int32_t *status,
+                                    void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(levels && n_levels > 0 && n_levels <= SSLA_GRIDS_MAX_LEVELS && B > 0,
+                 "events_to_grids: bad arguments (levels=%d B=%d)", n_levels, B);
+  GridArgs a{};
+  a.n_levels = n_levels;
+  a.B = B;
+  int blocks = 0;
+  int64_t max_cells = 1;
+  for (int l = 0; l < n_levels; ++l) {
+    const ssla_grid_level &lv = levels[l];
+    SSLA_CHECK_ARG(lv.E >= 0 && lv.G >= 0 && lv.C > 0 && lv.Hg > 0 && lv.Wg > 0 && lv.grid,
+                   "events_to_grids: bad level %d", l);
+    SSLA_CHECK_ARG(lv.G == 0 || (lv.events && lv.lengths && lv.batch && lv.h && lv.w),
+                   "events_to_grids: null pointer in level %d", l);
+    SSLA_CHECK_ARG(lv.E < 0x7fffffff, "events_to_grids: level %d has 2^31 events or more", l);
+    const int64_t cells = static_cast<int64_t>(B) * lv.Hg * lv.Wg;
+    if (cells > SSLA_GRIDS_MAX_CELLS) {
+      set_error("events_to_grids: level %d has %lld cells (at most %d)", l, static_cast<long long>(cells),
+                SSLA_GRIDS_MAX_CELLS);
+      return SSLA_ERR_UNSUPPORTED;
+    }
+    a.lv[l] = lv;
+    a.blk0[l] = blocks;
+    blocks += (lv.C + kGridCB - 1) / kGridCB;
+    SSLA_CHECK_ARG(blocks < (1 << 20), "events_to_grids: too many channels");
+    max_cells = std::max(max_cells, cells);
+  }
+  a.blk0[n_levels] = blocks;
+  hipLaunchKernelGGL(grids_kernel, dim3(blocks), dim3(kGridThreads), static_cast<size_t>(max_cells) * sizeof(int32_t),
+                     static_cast<hipStream_t>(stream), a, status);
+  return launch_status("events_to_grids");
 }
 
 // Per-pixel delays in place (MosModel.preprocess_inputs, model_mos.py:195-201):

@@ -13,7 +13,7 @@ names, arguments and dict keys, running the gfx950 kernels of
 * :func:`truncate_packed_sequence`      utils/farsecnn_utils.py:8-33
 * :func:`temporal_dropout_index`        layers/temporal_dropout.py:30-53
 * :func:`pool_segments`                 layers/sparse_pooling.py:26-48
-* :func:`events_to_grid`                model_mos.py:212-228
+* :func:`events_to_grid`                model_mos.py:212-228 (``events_to_grids``: several levels)
 * :func:`preprocess_inputs`             model_mos.py:173-209
 
 Every ordering is stable (ties keep enumeration order).  The reference's
@@ -25,7 +25,7 @@ Calls with data-dependent output sizes synchronise once to read the counts
 from __future__ import annotations
 
 import ctypes
-from typing import Dict, Optional, Tuple
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
@@ -34,8 +34,8 @@ from . import _lib
 __all__ = [
     "group_events", "compute_rf2pixels", "get_patch2pixel_lut", "gather_receptive_fields",
     "scatter_group_events_to_patch", "gather_patch_events_to_group", "truncate_packed_sequence",
-    "temporal_dropout_index", "pool_segments", "events_to_grid", "preprocess_inputs", "gather_rows",
-    "sort_pairs", "expand_segments", "GatherRows", "IndexAddRows", "sparse_pool",
+    "temporal_dropout_index", "pool_segments", "events_to_grid", "events_to_grids", "preprocess_inputs",
+    "gather_rows", "sort_pairs", "expand_segments", "GatherRows", "IndexAddRows", "sparse_pool",
 ]
 
 
@@ -548,6 +548,36 @@ def events_to_grid(x: Dict[str, torch.Tensor], grid_size, channels: int) -> torc
                                        _lib.ptr(gh), _lib.ptr(gw), ln.numel(), B, Hg, Wg, _lib.ptr(grid),
                                        _lib.ptr(ws), ws.numel(), st), "events_to_grid")
     return grid
+
+
+def events_to_grids(levels) -> List[torch.Tensor]:
+    """``events_to_grid`` over several ``(x, grid_size, channels)`` levels of
+    one batch in one launch (ssla_events_to_grids); each grid is written
+    whole, so none is cleared first.  Levels with more than
+    ``GRIDS_MAX_CELLS`` cells (B * Hg * Wg) go through ``events_to_grid``
+    one by one."""
+    if not levels:
+        return []
+    B = int(levels[0][0]["batch_size"])
+    if len(levels) > _lib.GRIDS_MAX_LEVELS or any(
+            B * int(gs[0]) * int(gs[1]) > _lib.GRIDS_MAX_CELLS or int(x["batch_size"]) != B for x, gs, _ in levels):
+        return [events_to_grid(x, gs, c) for x, gs, c in levels]
+    arr = (_lib.GridLevel * len(levels))()
+    grids = []
+    for i, (x, gs, c) in enumerate(levels):
+        ev = x["events"].to(torch.float32).contiguous()
+        ln, gb, gh, gw = (_i64(x[k]) for k in ("lengths", "batch_id", "h", "w"))
+        dev = _lib.require_cuda(ev, ln)
+        if ev.shape[1] != c:
+            raise ValueError(f"events_to_grids: level {i} has {ev.shape[1]} channels, expected {c}")
+        Hg, Wg = int(gs[0]), int(gs[1])
+        grid = torch.empty(B, c, Hg, Wg, dtype=torch.float32, device=dev)
+        arr[i] = _lib.GridLevel(_lib.ptr(ev), _lib.ptr(ln), _lib.ptr(gb), _lib.ptr(gh), _lib.ptr(gw), _lib.ptr(grid),
+                                ev.shape[0], ln.numel(), c, Hg, Wg)
+        grids.append(grid)
+    _lib.check(_lib.load().ssla_events_to_grids(arr, len(levels), B, None, _lib.stream_of(grids[0])),
+               "events_to_grids")
+    return grids
 
 
 def _preprocess_launch(events, lengths, frame_size, hot_pixel_thres, max_events_per_px: int = 512):

@@ -117,3 +117,34 @@ def test_status_read_rejects_null():
     import ctypes
     v = ctypes.c_int(0)
     assert _lib.load().ssla_status_read(None, ctypes.byref(v), None) == _lib.SSLA_ERR_ARG
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """The ctypes mirrors of the header's structs (ssla_head_level,
+    ssla_grid_level) have the C compiler's field offsets and sizes."""
+    import ctypes
+    import shutil
+    import subprocess
+    from ssla_amd import _lib
+    if shutil.which("gcc") is None:
+        pytest.skip("no C compiler")
+    structs = {"ssla_head_level": _lib.HeadLevel, "ssla_grid_level": _lib.GridLevel}
+    lines = ["#include <stddef.h>", "#include <stdio.h>", f'#include "{ROOT / "include" / "ssla_amd.h"}"',
+             "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'  printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-x", "c", "-I", "/opt/rocm/include", str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        name, field, val = line.split()
+        got[(name, field)] = int(val)
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for f, _ in py._fields_:
+            assert got[(cname, f)] == getattr(py, f).offset, f"{cname}.{f}"

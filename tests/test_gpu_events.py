@@ -137,6 +137,36 @@ def test_preprocess_and_fields_synthetic(dev):
     np.testing.assert_array_equal(_np(grid), OE.event_to_grid(ro, (H, W), ro["events"].shape[1]))
 
 
+def test_events_to_grids_levels(dev):
+    """ssla_events_to_grids (all levels in one launch, every element written)
+    against the oracle's index-add into zeros and the one-level call: two
+    samples, one group per occupied cell, a channel count that is not a
+    multiple of the 8-channel block, an empty level, and a level above the
+    one-launch cell limit (taken one level at a time)."""
+    from ssla_amd import events as E
+    rng = np.random.default_rng(12)
+    B = 2
+    levels, ref = [], []
+    for (Hg, Wg, C, n_grp) in ((30, 38, 64, 700), (15, 19, 20, 200), (8, 10, 256, 0), (100, 90, 8, 3000)):
+        cells = rng.choice(B * Hg * Wg, size=n_grp, replace=False)
+        cells.sort()
+        lens = rng.integers(1, 5, size=n_grp).astype(np.int64)
+        x = {"events": rng.standard_normal((int(lens.sum()), C)).astype(np.float32),
+             "lengths": lens, "batch_id": (cells // (Hg * Wg)).astype(np.int64),
+             "h": (cells % (Hg * Wg) // Wg).astype(np.int64), "w": (cells % Wg).astype(np.int64), "batch_size": B}
+        ref.append(OE.event_to_grid(x, (Hg, Wg), C))
+        xd = {k: (_t(v, dev) if isinstance(v, np.ndarray) else v) for k, v in x.items()}
+        levels.append((xd, (Hg, Wg), C))
+    print("events_to_grids: 4 levels", flush=True)
+    grids = E.events_to_grids(levels)
+    for i, (g, r) in enumerate(zip(grids, ref)):
+        np.testing.assert_array_equal(_np(g), r, err_msg=f"level {i}")
+        np.testing.assert_array_equal(_np(g), _np(E.events_to_grid(*levels[i])), err_msg=f"level {i}")
+    grids3 = E.events_to_grids(levels[:3])   # one launch for all three
+    for i in range(3):
+        np.testing.assert_array_equal(_np(grids3[i]), ref[i], err_msg=f"one launch, level {i}")
+
+
 @pytest.mark.parametrize("thres,extra", [(20, 0), (0, 0), (3, 2), (600, 0)])
 def test_preprocess_one_call_vs_composed(dev, thres, extra):
     """ssla_preprocess_events (grouping, delays and truncation in one pass)
