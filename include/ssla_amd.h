@@ -569,6 +569,19 @@ int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int64_t E_in, i
                           int64_t *out_batch, int64_t *out_h, int64_t *out_w, void *workspace,
                           size_t workspace_bytes, void *stream);
 
+/* The values half of ssla_sparse_pool_emit for events that are a bf16
+ * linear map of K = 2 inputs (a stem embedding nn.Linear(2, C, bias=False)
+ * run as F.linear(x.bfloat16(), w.bfloat16()).float() before the pooling):
+ * x fp32 [E_in, 2] (8-byte aligned), w bf16 [C, 2], C a multiple of 4.
+ * out_events [n_seg, C] equals ssla_sparse_pool_emit on the mapped events
+ * bit for bit: inputs and results rounded to bf16 (nearest-even), the two
+ * products exact in fp32 and their sum rounded once.  No reference C
+ * function (the reference runs the embedding and the pooling apart). */
+int ssla_sparse_pool_emit_linear(const float *x, int K, const uint16_t *w, int C, int64_t G, int64_t E_in, int B,
+                                 int H, int W, int64_t n_rf, int A, int64_t E_cap, int mode, int64_t n_act,
+                                 int64_t n_seg, int64_t E_out, float *out_events, void *workspace,
+                                 size_t workspace_bytes, void *stream);
+
 /* Per-pixel delays in place (MosModel.preprocess_inputs, model_mos.py:
  * 195-201): column 0 of feat [E, C] (timestamps) becomes
  * min((t_i - t_(i-1)) / 1e5, 1) within each group, 1 at each group start. */

@@ -116,6 +116,8 @@ SIGNATURES = {
                                             C.POINTER(_i64), _i32, C.POINTER(_i64), _vp, _sz, _vp]),
     "ssla_sparse_pool_emit": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _i32, _i64, _i32, _i64, _vp, _i32, _i64,
                                      _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ssla_sparse_pool_emit_linear": (_i32, [_vp, _i32, _vp, _i32, _i64, _i64, _i32, _i32, _i32, _i64, _i32, _i64,
+                                            _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "ssla_pixel_delays": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp, _sz, _vp]),
     "ssla_events_to_grid": (_i32, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _sz,
                                    _vp]),

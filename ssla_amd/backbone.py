@@ -416,17 +416,35 @@ class AsyncSparseGLA(nn.Module):
             pools.append(pool.plan(pools[-1].structure))
         return WindowPlan(gr, pools)
 
-    def _embed(self, gr: Dict[str, torch.Tensor]) -> torch.Tensor:
+    def _embed_weight(self) -> torch.Tensor:
+        """The embedding weight in bf16, converted again only when it
+        changes (differentiable and not cached while it records a
+        gradient)."""
         w = self.embed.weight
+        if torch.is_grad_enabled() and w.requires_grad:
+            return w.to(torch.bfloat16)
         key = (w.data_ptr(), w._version, w.device)
         cache = getattr(self, "_embed_bf16", None)
-        if torch.is_grad_enabled() and w.requires_grad:
-            cache = (None, w.to(torch.bfloat16))   # differentiable, not cached
-        elif cache is None or cache[0] != key:
+        if cache is None or cache[0] != key:
             with torch.no_grad():
                 cache = (key, w.detach().to(torch.bfloat16))
             self._embed_bf16 = cache
-        return F.linear(gr["events"].to(torch.bfloat16), cache[1]).float()
+        return cache[1]
+
+    def _embed(self, gr: Dict[str, torch.Tensor]) -> torch.Tensor:
+        return F.linear(gr["events"].to(torch.bfloat16), self._embed_weight()).float()
+
+    def _stem_planned(self, plan: "WindowPlan") -> Dict[str, torch.Tensor]:
+        """The stem of a planned window: without a gradient to record, the
+        embedding runs inside the stem pool's value pass
+        (SparsePool.apply_plan_linear, bit-identical); else embedding, then
+        pooling."""
+        x = plan.grouped["events"]
+        w = self._embed_weight()
+        if (not torch.is_grad_enabled() and x.is_cuda and x.dim() == 2 and x.shape[1] == 2
+                and w.shape[0] % 4 == 0):
+            return self.stem_pool.apply_plan_linear(plan.pools[0], x, w)
+        return self.stem_pool.apply_plan(plan.pools[0], self._embed(plan.grouped))
 
     def stem(self, events: torch.Tensor, lengths: torch.Tensor) -> Dict[str, torch.Tensor]:
         gr = E.preprocess_inputs(events, lengths, self.frame_size, self.hot_pixel_thres)
@@ -455,8 +473,7 @@ class AsyncSparseGLA(nn.Module):
         # Without a plan each stage's pooling is planned right after the
         # stage's block is enqueued, so the plan's read of device counts
         # waits while the GPU runs that block.
-        x = self.stem(events, lengths) if plan is None else \
-            self.stem_pool.apply_plan(plan.pools[0], self._embed(plan.grouped))
+        x = self.stem(events, lengths) if plan is None else self._stem_planned(plan)
         if mark:
             mark("stem")
         yield

@@ -90,11 +90,12 @@ int sort_pairs(void *tmp, size_t tmp_bytes, const uint64_t *kin, uint64_t *kout,
 // launch; rocPRIM's scan takes two).  Thread t owns values 8t .. 8t+7; the
 // thread totals are scanned across each wavefront with shuffles and across
 // the 16 wavefronts through LDS.  Every value is read before any is
-// written, so in == out is allowed.
+// written, so in == out is allowed.  total (optional) receives the sum.
 constexpr int kScanThreads = 1024, kScanPer = 8;
 constexpr int64_t kSmallScan = static_cast<int64_t>(kScanThreads) * kScanPer;
 
-__global__ __launch_bounds__(kScanThreads) void small_excl_scan(const int64_t *in, int64_t *out, int64_t n) {
+__global__ __launch_bounds__(kScanThreads) void small_excl_scan(const int64_t *in, int64_t *out, int64_t n,
+                                                                int64_t *total) {
   __shared__ int64_t wsum[kScanThreads / 64];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   int64_t v[kScanPer];
@@ -121,12 +122,120 @@ __global__ __launch_bounds__(kScanThreads) void small_excl_scan(const int64_t *i
     if (i < n) out[i] = run;
     run += v[e];
   }
+  if (total && t == kScanThreads - 1) *total = run;
 }
 
-int excl_scan(void *tmp, size_t tmp_bytes, const int64_t *in, int64_t *out, int64_t n, hipStream_t st) {
-  if (n == 0) return SSLA_OK;
+// Exclusive prefix sum in one launch for any size: tiles of kLbTile values,
+// each tile's workgroup taking its tile index from a ticket (so every tile
+// before it is already resident), publishing its aggregate and then its
+// inclusive prefix in a flag word per tile, and folding its predecessors'
+// words (decoupled look-back: the first wavefront reads 64 flags at a time
+// and stops at the nearest inclusive prefix).  The state -- the ticket and
+// one flag per tile, lb_state_words(n) words -- must be zero at launch: the
+// set-up kernel of each caller clears it.  Flag word: [63:62] state (0 none,
+// 1 aggregate, 2 inclusive prefix), [61:0] the value (two's complement), so
+// the payload travels with its state and relaxed agent-scope atomics
+// suffice.  total (optional) receives the sum.
+constexpr int kLbThreads = 256, kLbPer = 16;
+constexpr int64_t kLbTile = static_cast<int64_t>(kLbThreads) * kLbPer;
+constexpr uint64_t kLbAgg = 1ull << 62, kLbIncl = 2ull << 62, kLbMask = (1ull << 62) - 1;
+
+inline int64_t lb_state_words(int64_t n) { return 1 + (std::max<int64_t>(n, 1) + kLbTile - 1) / kLbTile; }
+
+__device__ __forceinline__ int64_t lb_value(uint64_t w) { return static_cast<int64_t>(w << 2) >> 2; }
+
+__global__ __launch_bounds__(kLbThreads) void lb_excl_scan(const int64_t *__restrict__ in, int64_t *__restrict__ out,
+                                                           int64_t n, uint64_t *state, int64_t *total) {
+  __shared__ int64_t s_tile, s_excl;
+  __shared__ int64_t wsum[kLbThreads / 64];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  if (t == 0) s_tile = static_cast<int64_t>(atomicAdd(reinterpret_cast<unsigned long long *>(state), 1ull));
+  __syncthreads();
+  const int64_t tile = s_tile;
+  uint64_t *flags = state + 1;
+  const int64_t base = tile * kLbTile + static_cast<int64_t>(t) * kLbPer;
+  int64_t v[kLbPer];
+  int64_t s = 0;
+#pragma unroll
+  for (int e = 0; e < kLbPer; ++e) {
+    v[e] = base + e < n ? in[base + e] : 0;
+    s += v[e];
+  }
+  int64_t x = s;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  if (w == 0) {
+    int64_t agg = 0;
+#pragma unroll
+    for (int j = 0; j < kLbThreads / 64; ++j) agg += wsum[j];
+    int64_t ex = 0;
+    if (tile > 0) {
+      if (lane == 0)
+        __hip_atomic_store(&flags[tile], kLbAgg | (static_cast<uint64_t>(agg) & kLbMask), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      int64_t j_end = tile;   // tiles [0, j_end) not folded yet
+      while (true) {
+        const int64_t j = j_end - 1 - lane;
+        const uint64_t fw = j >= 0 ? __hip_atomic_load(&flags[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : kLbIncl;   // before tile 0: inclusive prefix 0
+        const uint64_t st = fw >> 62;
+        const uint64_t incl = __builtin_amdgcn_ballot_w64(st == 2);
+        const uint64_t none = __builtin_amdgcn_ballot_w64(st == 0);
+        const int last = incl ? __builtin_ctzll(incl) : 63;   // lanes [0, last] are needed
+        const uint64_t need = last == 63 ? ~0ull : ((2ull << last) - 1);
+        if (none & need) {
+          __builtin_amdgcn_s_sleep(1);
+          continue;
+        }
+        int64_t val = lane <= last ? lb_value(fw) : 0;
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) val += __shfl_xor(val, d, 64);
+        ex += val;
+        if (incl) break;
+        j_end -= 64;
+      }
+    }
+    if (lane == 0) {
+      __hip_atomic_store(&flags[tile], kLbIncl | (static_cast<uint64_t>(ex + agg) & kLbMask), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      s_excl = ex;
+      if (total && tile == static_cast<int64_t>(gridDim.x) - 1) *total = ex + agg;
+    }
+  }
+  __syncthreads();
+  int64_t run = s_excl + x - s;
+  for (int j = 0; j < w; ++j) run += wsum[j];
+#pragma unroll
+  for (int e = 0; e < kLbPer; ++e) {
+    if (base + e < n) out[base + e] = run;
+    run += v[e];
+  }
+}
+
+__global__ void total_from_scan(const int64_t *excl, const int64_t *val, int64_t n, int64_t *dst);
+
+// out = exclusive prefix sum of in[0..n).  Up to kSmallScan values: one
+// workgroup.  Above: the one-launch look-back scan when the caller hands a
+// zeroed state (lb, lb_state_words(n) words), else rocPRIM's scan.  total
+// (optional) receives the sum (0 for n = 0).
+int excl_scan(void *tmp, size_t tmp_bytes, const int64_t *in, int64_t *out, int64_t n, hipStream_t st,
+              uint64_t *lb = nullptr, int64_t *total = nullptr) {
+  if (n == 0) {
+    if (total) hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, out, in, (int64_t)0, total);
+    return SSLA_OK;
+  }
   if (n <= kSmallScan) {
-    hipLaunchKernelGGL(small_excl_scan, dim3(1), dim3(kScanThreads), 0, st, in, out, n);
+    hipLaunchKernelGGL(small_excl_scan, dim3(1), dim3(kScanThreads), 0, st, in, out, n, total);
+    return SSLA_OK;
+  }
+  if (lb) {
+    hipLaunchKernelGGL(lb_excl_scan, dim3(static_cast<unsigned>((n + kLbTile - 1) / kLbTile)), dim3(kLbThreads), 0, st,
+                       in, out, n, lb, total);
     return SSLA_OK;
   }
   size_t tb = tmp_bytes;
@@ -136,6 +245,7 @@ int excl_scan(void *tmp, size_t tmp_bytes, const int64_t *in, int64_t *out, int6
     set_error("prefix sum failed: %s", hipGetErrorString(e));
     return SSLA_ERR_LAUNCH;
   }
+  if (total) hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, out, in, n, total);
   return SSLA_OK;
 }
 
@@ -145,10 +255,12 @@ __global__ void fill_i32(int32_t *p, int64_t n, int32_t v) { GRID_STRIDE(i, n) p
 __global__ void iota_i32(int32_t *p, int64_t n) { GRID_STRIDE(i, n) p[i] = static_cast<int32_t>(i); }
 
 // One launch for a call's set-up fills: the 8 count words and 8 status
-// flags to zero, a[0..na) = va, b[0..nb) = vb and c[0..nc) = vb (any range
-// may be empty).  Grid: grid_for(max(8, na, nb, nc)).
+// flags to zero, a[0..na) = va, b[0..nb) = vb, c[0..nc) = vb and z[0..nz) =
+// 0 (look-back scan states; any range may be empty).  Grid: grid_for(max(8,
+// na, nb, nc, nz)).
 __global__ void clear_and_fill(int64_t *counts, int32_t *bad, int64_t *a, int64_t na, int64_t va, int32_t *b,
-                               int64_t nb, int32_t vb, int32_t *c, int64_t nc) {
+                               int64_t nb, int32_t vb, int32_t *c, int64_t nc, uint64_t *z = nullptr,
+                               int64_t nz = 0) {
   GRID_STRIDE(i, 8) {
     counts[i] = 0;
     bad[i] = 0;
@@ -156,6 +268,7 @@ __global__ void clear_and_fill(int64_t *counts, int32_t *bad, int64_t *a, int64_
   GRID_STRIDE(i, na) a[i] = va;
   GRID_STRIDE(i, nb) b[i] = vb;
   GRID_STRIDE(i, nc) c[i] = vb;
+  GRID_STRIDE(i, nz) z[i] = 0;
 }
 
 // Sorted-fill set-up in one launch: inv and dst to -1, and the field
@@ -405,6 +518,39 @@ __global__ void rf_count(const int64_t *__restrict__ lut, int64_t n_rf, int A, i
     nev[f] = n;
     act[f] = a_;
     if (pk) pk[f] = (n << kPackBits) | a_;
+  }
+}
+
+// rf_count with one lane per (field, kernel position) when A divides 64:
+// the A lanes of a field sit in one wavefront and sum their events with
+// shuffles, so each lane makes one lookup chain instead of A in a row.
+// Grid: exactly ceil(B * n_rf * A / kThreads) workgroups (every lane takes
+// part in the shuffles; lanes past the end add nothing and write nothing).
+__global__ void rf_count_lanes(const int64_t *__restrict__ lut, int64_t n_rf, int A, int B, int H, int W,
+                               const int32_t *__restrict__ pixmap, const int64_t *__restrict__ glen,
+                               int64_t *__restrict__ nev, int64_t *__restrict__ act, int64_t *__restrict__ pk) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t n_f = static_cast<int64_t>(B) * n_rf;
+  const int64_t f = t / A;
+  const int a = static_cast<int>(t - f * A);
+  int64_t n = 0, on = 0;
+  if (f < n_f) {
+    const int64_t b = f / n_rf, r = f - b * n_rf;
+    const int64_t p = lut[r * A + a];
+    const int32_t g = p >= 0 ? pixmap[b * H * W + p] : -1;
+    if (g >= 0) {
+      n = glen[g];
+      on = 1;
+    }
+  }
+  for (int d = 1; d < A; d <<= 1) {
+    n += __shfl_xor(n, d, 64);
+    on |= __shfl_xor(on, d, 64);
+  }
+  if (f < n_f && a == 0) {
+    nev[f] = n;
+    act[f] = on;
+    if (pk) pk[f] = (n << kPackBits) | on;
   }
 }
 
@@ -686,11 +832,12 @@ __global__ void grid_place(const float *__restrict__ ev, const int64_t *__restri
 
 // Several grids in one launch: one workgroup per (level, block of kGridCB
 // channels).  Each workgroup builds its level's cell -> last-event map in
-// LDS from the group lengths (a running prefix over chunks of the block
-// size), then writes its channel planes cell by cell, 0 where no group
-// sits: every element is written once, so the grid needs no clearing and
-// no two workgroups touch the same address.
-constexpr int kGridThreads = 256, kGridCB = 8;
+// LDS from the group lengths (kGridPer groups per thread, a running prefix
+// over chunks of kGridThreads * kGridPer groups), then writes its channel
+// planes cell by cell, 0 where no group sits: every element is written
+// once, so the grid needs no clearing and no two workgroups touch the same
+// address.  Loads are issued kGridPer at a time ahead of their uses.
+constexpr int kGridThreads = 1024, kGridPer = 4, kGridCB = 4;
 struct GridArgs {
   ssla_grid_level lv[SSLA_GRIDS_MAX_LEVELS];
   int blk0[SSLA_GRIDS_MAX_LEVELS + 1];
@@ -709,10 +856,20 @@ __global__ __launch_bounds__(kGridThreads) void grids_kernel(GridArgs a, int32_t
   __syncthreads();
   bool bad = false;
   int64_t carry = 0;
-  for (int64_t base = 0; base < lv.G; base += kGridThreads) {
-    const int64_t g = base + tid;
-    const int64_t len = g < lv.G ? lv.lengths[g] : 0;
-    int64_t x = len;   // inclusive scan across the wavefront
+  for (int64_t base = 0; base < lv.G; base += kGridThreads * kGridPer) {
+    const int64_t g0 = base + static_cast<int64_t>(tid) * kGridPer;
+    int64_t len[kGridPer], gb[kGridPer], gh[kGridPer], gw[kGridPer];
+    int64_t s = 0;
+#pragma unroll
+    for (int u = 0; u < kGridPer; ++u) {
+      const bool in = g0 + u < lv.G;
+      len[u] = in ? lv.lengths[g0 + u] : 0;
+      gb[u] = in ? lv.batch[g0 + u] : 0;
+      gh[u] = in ? lv.h[g0 + u] : 0;
+      gw[u] = in ? lv.w[g0 + u] : 0;
+      s += len[u];
+    }
+    int64_t x = s;   // inclusive scan of the thread sums across the wavefront
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const int64_t y = __shfl_up(x, d, 64);
@@ -726,10 +883,17 @@ __global__ __launch_bounds__(kGridThreads) void grids_kernel(GridArgs a, int32_t
       pre += j < wv ? wsum[j] : 0;
       tot += wsum[j];
     }
-    if (g < lv.G) {
-      const int64_t b = lv.batch[g], h = lv.h[g], w = lv.w[g], last = carry + pre + x - 1;
-      if (b < 0 || b >= a.B || h < 0 || h >= lv.Hg || w < 0 || w >= lv.Wg || last < 0 || last >= lv.E) bad = true;
-      else cell_ev[(b * lv.Hg + h) * lv.Wg + w] = static_cast<int32_t>(last);
+    int64_t end = carry + pre + x - s;
+#pragma unroll
+    for (int u = 0; u < kGridPer; ++u) {
+      end += len[u];
+      if (g0 + u >= lv.G) continue;
+      const int64_t last = end - 1;
+      if (gb[u] < 0 || gb[u] >= a.B || gh[u] < 0 || gh[u] >= lv.Hg || gw[u] < 0 || gw[u] >= lv.Wg || last < 0 ||
+          last >= lv.E)
+        bad = true;
+      else
+        cell_ev[(gb[u] * lv.Hg + gh[u]) * lv.Wg + gw[u]] = static_cast<int32_t>(last);
     }
     carry += tot;
     __syncthreads();   // wsum is rewritten by the next chunk
@@ -737,14 +901,30 @@ __global__ __launch_bounds__(kGridThreads) void grids_kernel(GridArgs a, int32_t
   // (the loop's last barrier orders the map's writes before the reads)
   const int c0 = (static_cast<int>(blockIdx.x) - a.blk0[L]) * kGridCB;
   const int nc = min(kGridCB, lv.C - c0);
-  const uint32_t ucells = static_cast<uint32_t>(cells);
-  for (uint32_t t = tid; t < static_cast<uint32_t>(nc) * ucells; t += kGridThreads) {
-    const uint32_t cl = t / ucells, cell = t - cl * ucells;
-    const uint32_t b = cell / static_cast<uint32_t>(HW), hw = cell - b * static_cast<uint32_t>(HW);
-    const int c = c0 + static_cast<int>(cl);
-    const int32_t e = cell_ev[cell];
-    lv.grid[(static_cast<int64_t>(b) * lv.C + c) * HW + hw] = e >= 0 ? lv.events[static_cast<int64_t>(e) * lv.C + c]
-                                                                      : 0.f;
+  const uint32_t ucells = static_cast<uint32_t>(cells), uhw = static_cast<uint32_t>(HW);
+  const uint32_t total = static_cast<uint32_t>(nc) * ucells;
+  const float *__restrict__ ev = lv.events;
+  float *__restrict__ grid = lv.grid;
+  for (uint32_t t0 = tid; t0 < total; t0 += kGridThreads * kGridPer) {
+    float v[kGridPer];
+    int64_t o[kGridPer];
+#pragma unroll
+    for (int u = 0; u < kGridPer; ++u) {
+      const uint32_t t = t0 + u * kGridThreads;
+      o[u] = -1;
+      v[u] = 0.f;
+      if (t < total) {
+        const uint32_t cl = t / ucells, cell = t - cl * ucells;
+        const uint32_t b = cell / uhw, hw = cell - b * uhw;
+        const int c = c0 + static_cast<int>(cl);
+        const int32_t e = cell_ev[cell];
+        o[u] = (static_cast<int64_t>(b) * lv.C + c) * HW + hw;
+        if (e >= 0) v[u] = ev[static_cast<int64_t>(e) * lv.C + c];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kGridPer; ++u)
+      if (o[u] >= 0) grid[o[u]] = v[u];
   }
   const int any_bad = __syncthreads_or(bad ? 1 : 0);
   if (status && any_bad && tid == 0) *status = 1;
@@ -788,6 +968,8 @@ struct GeWs {
   int64_t *counts, *off, *head, *gpos, *start, *kept, *kpre, *row_of;
   uint64_t *key, *skey;
   int32_t *val, *order, *bad;
+  uint64_t *lb;   // two look-back scan states of lb_state_words(cap) words
+  int64_t lb_words;
   void *tmp;
   size_t tmp_bytes, total;
 };
@@ -807,6 +989,8 @@ GeWs ge_layout(void *ws, int B, int64_t cap) {
   L.skey = c.take<uint64_t>(cap);
   L.val = c.take<int32_t>(cap);
   L.order = c.take<int32_t>(cap);
+  L.lb_words = lb_state_words(cap);
+  L.lb = c.take<uint64_t>(2 * L.lb_words);
   L.tmp_bytes = std::max(sort_temp_bytes(cap), scan_temp_bytes(std::max<int64_t>(cap, B + 1)));
   L.tmp = c.take<char>(L.tmp_bytes);
   L.total = c.off;
@@ -847,8 +1031,9 @@ int group_events_impl(const char *what, const float *events, const int64_t *leng
     return launch_status(what);
   }
   // sample offsets: exclusive scan of the lengths clamped to [0, N]
-  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max<int64_t>(8, B + 1))), dim3(kThreads), 0, st, L.counts,
-                     L.bad, L.kept, (int64_t)(B + 1), (int64_t)0, nullptr, (int64_t)0, 0, nullptr, (int64_t)0);
+  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max<int64_t>(std::max<int64_t>(8, B + 1), 2 * L.lb_words))),
+                     dim3(kThreads), 0, st, L.counts, L.bad, L.kept, (int64_t)(B + 1), (int64_t)0, nullptr,
+                     (int64_t)0, 0, nullptr, (int64_t)0, L.lb, 2 * L.lb_words);
   hipLaunchKernelGGL(trunc_len, dim3(grid_for(B)), dim3(kThreads), 0, st, lengths, (int64_t)B, N, L.kept);
   int s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.off, B + 1, st);
   if (s) return s;
@@ -862,13 +1047,13 @@ int group_events_impl(const char *what, const float *events, const int64_t *leng
   s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.order, cap, bits_for(static_cast<uint64_t>(n_pix)), st);
   if (s) return s;
   hipLaunchKernelGGL(ge_heads, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.skey, cap, Ep, L.head);
-  s = excl_scan(L.tmp, L.tmp_bytes, L.head, L.gpos, cap, st);
+  s = excl_scan(L.tmp, L.tmp_bytes, L.head, L.gpos, cap, st, L.lb);
   if (s) return s;
   hipLaunchKernelGGL(ge_starts, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, cap, Ep, L.start,
                      L.counts);
   hipLaunchKernelGGL(ge_groups, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.counts, L.start, cap, L.order,
                      L.row_of, events, N, C, max_per_px, keep_first, L.kept, gr_batch, gr_h, gr_w, gr_len);
-  s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.kpre, cap, st);
+  s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.kpre, cap, st, L.lb + L.lb_words);
   if (s) return s;
   if (delays)
     hipLaunchKernelGGL(ge_emit<true>, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, L.start, L.kept,
@@ -1068,6 +1253,11 @@ struct RfWs {
   int32_t *bad, *pixmap, *val, *perm;
   uint64_t *key, *skey;
   unsigned long long *tmax;
+  // look-back scan states (zeroed by the plan's set-up kernel): the group
+  // starts' scan (lb_state_words(G)) and the segment heads' scan of the
+  // pooling plan (lb_state_words(E_cap)), contiguous
+  uint64_t *lb_g, *lb_e;
+  int64_t lb_words;
   void *tmp;
   size_t tmp_bytes, total;
 };
@@ -1091,6 +1281,9 @@ RfWs rf_layout(void *ws, int64_t G, int64_t n_pix, int64_t n_f, int64_t E_cap) {
   L.skey = c.take<uint64_t>(E_cap);
   L.val = c.take<int32_t>(E_cap);
   L.perm = c.take<int32_t>(E_cap);
+  L.lb_words = lb_state_words(G) + lb_state_words(E_cap);
+  L.lb_g = c.take<uint64_t>(L.lb_words);
+  L.lb_e = L.lb_g ? L.lb_g + lb_state_words(G) : nullptr;
   L.tmp_bytes = std::max(sort_temp_bytes(E_cap), scan_temp_bytes(std::max(n_f, G + 1)));
   L.tmp = c.take<char>(L.tmp_bytes);
   L.total = c.off;
@@ -1129,20 +1322,25 @@ int rf_plan_impl(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr
   SSLA_CHECK_ARG(lut && (G == 0 || (gr_batch && gr_h && gr_w && gr_len)) && (E_in == 0 || time),
                  "rf_scatter_plan: null pointer");
   const int64_t n_inv = inv ? static_cast<int64_t>(H) * W * (one_field ? 1 : A) : 0;
-  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max(std::max<int64_t>(8, n_pix), n_inv))), dim3(kThreads), 0,
-                     st, L.counts, L.bad, reinterpret_cast<int64_t *>(L.tmax), (int64_t)1, (int64_t)0, L.pixmap, n_pix,
-                     -1, inv, n_inv);
+  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max(std::max(std::max<int64_t>(8, n_pix), n_inv), L.lb_words))),
+                     dim3(kThreads), 0, st, L.counts, L.bad, reinterpret_cast<int64_t *>(L.tmax), (int64_t)1,
+                     (int64_t)0, L.pixmap, n_pix, -1, inv, n_inv, L.lb_g, L.lb_words);
   if (G > 0 || inv)
     hipLaunchKernelGGL(rf_pixmap, dim3(grid_for(std::max(G, inv ? n_rf * A : 0))), dim3(kThreads), 0, st, gr_batch,
                        gr_h, gr_w, G, H, W, n_pix, L.pixmap, L.bad, lut, n_rf, A, inv, one_field ? 1 : 0,
                        L.counts + 5);
-  int s = excl_scan(L.tmp, L.tmp_bytes, gr_len, L.gstart, G, st);
+  int s = excl_scan(L.tmp, L.tmp_bytes, gr_len, L.gstart, G, st, L.lb_g);
   if (s) return s;
   // one prefix sum of the packed (events, active) pairs while the active
   // count fits 21 bits (f_index / f_len hold the pairs until rf_fields)
   const bool packed = n_f < (int64_t{1} << kPackBits);
-  hipLaunchKernelGGL(rf_count, dim3(grid_for(n_f)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap, gr_len,
-                     L.nev, L.act, packed ? L.f_index : nullptr);
+  if (64 % A == 0 && n_f * A <= (int64_t{1} << 28))
+    hipLaunchKernelGGL(rf_count_lanes, dim3(static_cast<unsigned>((n_f * A + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap, gr_len, L.nev, L.act,
+                       packed ? L.f_index : nullptr);
+  else
+    hipLaunchKernelGGL(rf_count, dim3(grid_for(n_f)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap, gr_len,
+                       L.nev, L.act, packed ? L.f_index : nullptr);
   if (packed) {
     s = excl_scan(L.tmp, L.tmp_bytes, L.f_index, L.f_len, n_f, st);
     if (s) return s;
@@ -1321,7 +1519,11 @@ __global__ void pool_row_heads(const int32_t *__restrict__ fidx, const int64_t *
 // once.  Max: the first row among equal maxima; NaN never wins; a segment
 // whose values are all NaN gives 0 (scatter_max's rule for a row that no
 // event wins).  Then per active field its segment count and coordinates.
-template <bool MEAN, int VW>
+// LIN: ev holds two inputs per event and a row's value is its bf16 linear
+// map by w_lin (bf16 [C, 2]): both inputs and the result rounded to bf16
+// (nearest-even), the two products exact in fp32 and their sum rounded
+// once -- what a bf16 GEMM with fp32 accumulation returns for K = 2.
+template <bool MEAN, int VW, bool LIN = false>
 __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C, const int64_t *__restrict__ src,
                                const int64_t *__restrict__ tim, const int64_t *__restrict__ head,
                                const int64_t *__restrict__ segx, int64_t E_out, int64_t n_seg,
@@ -1329,7 +1531,8 @@ __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C
                                const int64_t *__restrict__ ev_pre, int64_t n_act, int64_t n_rf,
                                const int64_t *__restrict__ outcoord, float *__restrict__ o_ev,
                                int64_t *__restrict__ o_time, int64_t *__restrict__ o_len, int64_t *__restrict__ o_b,
-                               int64_t *__restrict__ o_h, int64_t *__restrict__ o_w) {
+                               int64_t *__restrict__ o_h, int64_t *__restrict__ o_w,
+                               const uint16_t *__restrict__ w_lin = nullptr) {
   // VW consecutive channels per thread (C / VW threads per row; E_out * C
   // < 2^31, checked by the caller).  A null o_ev skips the values (the
   // structure alone: times, per-field counts and coordinates); a null o_len
@@ -1352,18 +1555,28 @@ __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C
     double sum[VW];
     float best[VW];
     bool found[VW];
+    float wl[VW][2];
 #pragma unroll
     for (int v = 0; v < VW; ++v) {
       sum[v] = 0.0;
       best[v] = -INFINITY;
       found[v] = false;
+      if constexpr (LIN) {
+        wl[v][0] = bf16_bits_to_f32(w_lin[(c + v) * 2]);
+        wl[v][1] = bf16_bits_to_f32(w_lin[(c + v) * 2 + 1]);
+      }
     }
     int64_t r2 = r;
     do {
       const int64_t e = src[r2];
       float x[VW];
       if (e >= 0 && e < E_in) {
-        if constexpr (VW == 4) {
+        if constexpr (LIN) {
+          const float2 in = *reinterpret_cast<const float2 *>(ev + e * 2);
+          const float a0 = bf16_bits_to_f32(f32_to_bf16_bits(in.x)), a1 = bf16_bits_to_f32(f32_to_bf16_bits(in.y));
+#pragma unroll
+          for (int v = 0; v < VW; ++v) x[v] = bf16_bits_to_f32(f32_to_bf16_bits(a0 * wl[v][0] + a1 * wl[v][1]));
+        } else if constexpr (VW == 4) {
           const float4 q = *reinterpret_cast<const float4 *>(ev + e * C + c);
           x[0] = q.x, x[1] = q.y, x[2] = q.z, x[3] = q.w;
         } else {
@@ -1407,14 +1620,13 @@ __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C
 }
 
 // Segment heads of the filled field rows, their exclusive prefix and the
-// segment count (workspace head, slot 4).
-int pool_segments_pass(const PoolWs &L, int64_t E_cap, hipStream_t st) {
+// segment count (workspace head, slot 4).  first: the plan's first pass,
+// whose set-up kernel zeroed the look-back scan state (a second pass, after
+// the sort fill, takes rocPRIM's scan).
+int pool_segments_pass(const PoolWs &L, int64_t E_cap, hipStream_t st, bool first) {
   hipLaunchKernelGGL(pool_row_heads, dim3(grid_for(E_cap)), dim3(kThreads), 0, st, L.fidx, L.tim, L.rf.counts + 1,
                      E_cap, L.head);
-  const int r = excl_scan(L.tmp, L.tmp_bytes, L.head, L.segx, E_cap, st);
-  if (r) return r;
-  hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, L.segx, L.head, E_cap, L.rf.counts + 4);
-  return SSLA_OK;
+  return excl_scan(L.tmp, L.tmp_bytes, L.head, L.segx, E_cap, st, first ? L.rf.lb_e : nullptr, L.rf.counts + 4);
 }
 }  // namespace
 
@@ -1467,7 +1679,7 @@ extern "C" int ssla_sparse_pool_plan_enqueue(const int64_t *gr_batch, const int6
                          E_in, E_cap, L.src, L.tim, static_cast<int64_t *>(nullptr), static_cast<int32_t *>(nullptr),
                          L.rf.act_pre, L.fidx);
   }
-  s = pool_segments_pass(L, E_cap, st);
+  s = pool_segments_pass(L, E_cap, st, true);
   if (s) return s;
   return launch_status("sparse_pool_plan");
 }
@@ -1534,7 +1746,7 @@ extern "C" int ssla_sparse_pool_plan_finish(const int64_t *gr_len, int64_t G, co
     hipLaunchKernelGGL(rf_emit, dim3(grid_for(E_out)), dim3(kThreads), 0, st, L.rf.perm, E_out, L.rf.pre_src,
                        L.rf.pre_pos, time, L.src, L.tim, static_cast<int64_t *>(nullptr), L.rf.skey, t_stride,
                        L.fidx);
-    s = pool_segments_pass(L, E_cap, st);
+    s = pool_segments_pass(L, E_cap, st, false);
     if (s) return s;
     s = ssla_events_counts(workspace, c, 5, nullptr, stream);
     if (s) return s;
@@ -1618,6 +1830,46 @@ extern "C" int ssla_sparse_pool_emit(const float *events, int C, int64_t G, int6
   }
 #undef SSLA_POOL_EMIT
   return launch_status("sparse_pool_emit");
+}
+
+extern "C" int ssla_sparse_pool_emit_linear(const float *x, int K, const uint16_t *w, int C, int64_t G, int64_t E_in,
+                                            int B, int H, int W, int64_t n_rf, int A, int64_t E_cap, int mode,
+                                            int64_t n_act, int64_t n_seg, int64_t E_out, float *out_events,
+                                            void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(K == 2, "sparse_pool_emit_linear: K must be 2 (got %d)", K);
+  SSLA_CHECK_ARG(C > 0 && C % 4 == 0 && G >= 0 && E_in >= 0 && B > 0 && H > 0 && W > 0 && n_rf > 0 && A > 0 &&
+                     (mode == 0 || mode == 1),
+                 "sparse_pool_emit_linear: bad arguments (C must be a multiple of 4)");
+  SSLA_CHECK_ARG(E_cap >= E_in && E_cap < 0x7fffffff, "sparse_pool_emit_linear: bad row capacity");
+  SSLA_CHECK_ARG(E_out >= 0 && E_out <= E_cap && n_seg >= 0 && n_seg <= E_out && n_act >= 0 &&
+                     n_act <= static_cast<int64_t>(B) * n_rf,
+                 "sparse_pool_emit_linear: counts outside the plan's bounds");
+  const PoolWs L = pool_layout(workspace, G, B, H, W, n_rf, A, E_cap);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("sparse_pool_emit_linear: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+    return SSLA_ERR_WORKSPACE;
+  }
+  if (E_out == 0 || n_seg == 0) return SSLA_OK;
+  SSLA_CHECK_ARG(x && w && out_events, "sparse_pool_emit_linear: null pointer");
+  SSLA_CHECK_ARG(aligned(x, 8) && aligned(out_events, 16), "sparse_pool_emit_linear: x must be 8-byte and "
+                 "out_events 16-byte aligned");
+  SSLA_CHECK_ARG(E_out * C < 0x7fffffff, "sparse_pool_emit_linear: rows x channels must stay below 2^31");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned grid = grid_for(E_out * (C / 4));
+  if (mode == 1)
+    hipLaunchKernelGGL((pool_emit_rows<true, 4, true>), dim3(grid), dim3(kThreads), 0, st, x, E_in, C, L.src, L.tim,
+                       L.head, L.segx, E_out, n_seg, L.rf.f_index, L.rf.f_len, L.rf.ev_pre, (int64_t)0, n_rf,
+                       static_cast<const int64_t *>(nullptr), out_events, static_cast<int64_t *>(nullptr),
+                       static_cast<int64_t *>(nullptr), static_cast<int64_t *>(nullptr),
+                       static_cast<int64_t *>(nullptr), static_cast<int64_t *>(nullptr), w);
+  else
+    hipLaunchKernelGGL((pool_emit_rows<false, 4, true>), dim3(grid), dim3(kThreads), 0, st, x, E_in, C, L.src, L.tim,
+                       L.head, L.segx, E_out, n_seg, L.rf.f_index, L.rf.f_len, L.rf.ev_pre, (int64_t)0, n_rf,
+                       static_cast<const int64_t *>(nullptr), out_events, static_cast<int64_t *>(nullptr),
+                       static_cast<int64_t *>(nullptr), static_cast<int64_t *>(nullptr),
+                       static_cast<int64_t *>(nullptr), static_cast<int64_t *>(nullptr), w);
+  return launch_status("sparse_pool_emit_linear");
 }
 
 // ---- rows ------------------------------------------------------------------------

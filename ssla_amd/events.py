@@ -36,6 +36,7 @@ __all__ = [
     "scatter_group_events_to_patch", "gather_patch_events_to_group", "truncate_packed_sequence",
     "temporal_dropout_index", "pool_segments", "events_to_grid", "events_to_grids", "preprocess_inputs",
     "gather_rows", "sort_pairs", "expand_segments", "GatherRows", "IndexAddRows", "sparse_pool",
+    "sparse_pool_values_linear",
 ]
 
 
@@ -513,6 +514,30 @@ def sparse_pool_values(plan: PoolPlan, events: torch.Tensor, mean: bool = False)
     """The values half of sparse_pool on a plan from sparse_pool_plan:
     [segments, C] max (or mean) of every pooling segment."""
     return _pool_emit(plan, events, mean, False)
+
+
+def sparse_pool_values_linear(plan: PoolPlan, x: torch.Tensor, weight_bf16: torch.Tensor,
+                              mean: bool = False) -> torch.Tensor:
+    """sparse_pool_values of ``F.linear(x.bfloat16(), weight_bf16).float()``
+    without materialising the mapped events (ssla_sparse_pool_emit_linear):
+    x fp32 [E, 2], weight_bf16 [C, 2] with C a multiple of 4; bit-identical
+    to the two steps."""
+    lib = _lib.load()
+    G, E_in, B, H, W, n_rf, A, E_cap = plan.sizes
+    dev = plan.ws.device
+    if x.dim() != 2 or x.shape[1] != 2 or x.shape[0] != E_in:
+        raise ValueError(f"sparse_pool_values_linear: x must be [{E_in}, 2], got {tuple(x.shape)}")
+    if weight_bf16.dtype != torch.bfloat16 or weight_bf16.dim() != 2 or weight_bf16.shape[1] != 2:
+        raise TypeError("sparse_pool_values_linear: weight must be bf16 [C, 2]")
+    x = x.to(torch.float32).contiguous()
+    w = weight_bf16.contiguous()
+    C = w.shape[0]
+    out = torch.empty(plan.n_seg, C, dtype=torch.float32, device=dev)
+    _lib.check(lib.ssla_sparse_pool_emit_linear(_lib.ptr(x), 2, _lib.ptr(w), C, G, E_in, B, H, W, n_rf, A, E_cap,
+                                                1 if mean else 0, plan.n_act, plan.n_seg, plan.E_out, _lib.ptr(out),
+                                                _lib.ptr(plan.ws), plan.ws.numel(), _lib.stream_of(plan.ws)),
+               "sparse_pool_emit_linear")
+    return out
 
 
 def sparse_pool(inputs, frame_size, rf2pixel_lut, rf_outcoord, mean: bool = False,

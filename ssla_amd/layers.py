@@ -394,6 +394,14 @@ class SparsePool(AsyncSparseModule):
         return {"events": E.sparse_pool_values(plan, events, mean=self.pool_func is scatter_mean),
                 **plan.structure}
 
+    def apply_plan_linear(self, plan: "E.PoolPlan", x: torch.Tensor,
+                          weight_bf16: torch.Tensor) -> Dict[str, torch.Tensor]:
+        """``apply_plan`` of ``F.linear(x.bfloat16(), weight_bf16).float()``
+        (x fp32 [E, 2], weight bf16 [C, 2]) with the linear map folded into
+        the pooling (E.sparse_pool_values_linear): bit-identical outputs."""
+        return {"events": E.sparse_pool_values_linear(plan, x, weight_bf16, mean=self.pool_func is scatter_mean),
+                **plan.structure}
+
     def _fields_per_pixel(self) -> int:
         return (-(-self.kernel_size[0] // self.stride[0])) * (-(-self.kernel_size[1] // self.stride[1]))
 

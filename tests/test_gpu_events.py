@@ -141,13 +141,13 @@ def test_events_to_grids_levels(dev):
     """ssla_events_to_grids (all levels in one launch, every element written)
     against the oracle's index-add into zeros and the one-level call: two
     samples, one group per occupied cell, a channel count that is not a
-    multiple of the 8-channel block, an empty level, and a level above the
+    multiple of the 4-channel block, an empty level, and a level above the
     one-launch cell limit (taken one level at a time)."""
     from ssla_amd import events as E
     rng = np.random.default_rng(12)
     B = 2
     levels, ref = [], []
-    for (Hg, Wg, C, n_grp) in ((30, 38, 64, 700), (15, 19, 20, 200), (8, 10, 256, 0), (100, 90, 8, 3000)):
+    for (Hg, Wg, C, n_grp) in ((30, 38, 64, 700), (15, 19, 22, 200), (8, 10, 256, 0), (100, 90, 8, 3000)):
         cells = rng.choice(B * Hg * Wg, size=n_grp, replace=False)
         cells.sort()
         lens = rng.integers(1, 5, size=n_grp).astype(np.int64)
@@ -165,6 +165,31 @@ def test_events_to_grids_levels(dev):
     grids3 = E.events_to_grids(levels[:3])   # one launch for all three
     for i in range(3):
         np.testing.assert_array_equal(_np(grids3[i]), ref[i], err_msg=f"one launch, level {i}")
+
+
+def test_preprocess_large_vs_oracle(dev):
+    """ssla_preprocess_events at a capacity of 2 x 40,000 events (its prefix
+    sums run as multi-tile look-back scans) against the oracle, bit for
+    bit, on the 304 x 240 sensor with a hot pixel over the 512-event cap."""
+    from ssla_amd import events as E
+    H, W = 240, 304
+    gen = np.random.default_rng(31)
+    N = 40_000
+    lens = np.array([N, 31_000], np.int64)
+    ev = np.zeros((2, N, 4), np.float32)
+    for b in range(2):
+        n = int(lens[b])
+        ev[b, :n, 0] = gen.integers(0, W, n)
+        ev[b, :n, 1] = gen.integers(0, H, n)
+        ev[b, :n, 2] = np.sort(gen.integers(0, 50_000, n))
+        ev[b, :n, 3] = np.where(gen.random(n) < 0.5, -1.0, 1.0)
+    ev[0, :900, 0], ev[0, :900, 1] = 17.0, 9.0
+    print("preprocess large", flush=True)
+    one = E.preprocess_inputs(_t(ev, dev), _t(lens, dev), (H, W), hot_pixel_thres=50)
+    ro = OE.preprocess_events(ev, lens, (H, W), hot_pixel_thres=50)
+    assert ro["lengths"].size > 8192
+    for key in ("events", "time", "batch_id", "h", "w", "lengths"):
+        np.testing.assert_array_equal(_np(one[key]), ro[key], err_msg=key)
 
 
 @pytest.mark.parametrize("thres,extra", [(20, 0), (0, 0), (3, 2), (600, 0)])

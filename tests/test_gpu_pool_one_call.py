@@ -84,6 +84,35 @@ def test_pool_one_call_vs_composed_and_oracle(kind, k, s, t_levels, sorted_runs)
     np.testing.assert_array_equal(one["batch_id"].cpu().numpy(), rf["batch_id"])
 
 
+@pytest.mark.parametrize("kind", ["max", "mean"])
+def test_pool_one_call_large_vs_oracle(kind):
+    """The one-call pooling at 20,000 pixel groups and about 40,000 events
+    on the 304 x 240 sensor (4 x 4 fields): its group-start and
+    segment-head prefix sums run as multi-tile look-back scans.  Against the
+    oracle and the composed path."""
+    from ssla_amd.layers import SparseAvgPool, SparseMaxPool
+    frame = (240, 304)
+    gr = _groups(41, 1, *frame, n_px=20_000, max_len=3, t_levels=50, C=8)
+    layer = (SparseMaxPool if kind == "max" else SparseAvgPool)(frame, kernel_size=(4, 4)).cuda()
+    print(f"pool one-call large {kind}", flush=True)
+    one, comp = _both(layer, _dev(gr))
+    for key in KEYS:
+        a, b = one[key].cpu().numpy(), comp[key].cpu().numpy()
+        if key == "events" and kind == "mean":
+            np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-7)
+        else:
+            np.testing.assert_array_equal(a, b, err_msg=key)
+    lut, outc = OE.rf2pixels(frame, (4, 4), (4, 4))
+    want = OE.sparse_pool(OE.gather_receptive_fields(gr, frame, lut, outc), kind)
+    assert want["time"].size > 8192
+    if kind == "max":
+        np.testing.assert_array_equal(one["events"].cpu().numpy(), want["events"])
+    else:
+        np.testing.assert_allclose(one["events"].cpu().numpy(), want["events"], rtol=1e-6, atol=1e-7)
+    np.testing.assert_array_equal(one["time"].cpu().numpy(), want["time"])
+    np.testing.assert_array_equal(one["lengths"].cpu().numpy(), want["lengths"])
+
+
 @pytest.mark.parametrize("C", [16, 6])
 def test_pool_one_call_special_values(C):
     """NaN never wins, equal maxima keep the first row (+0 / -0 bits), -inf
@@ -136,3 +165,34 @@ def test_pool_one_call_row_capacity():
             E.sparse_pool(_dev(gr), frame, lut, outc, fields_per_pixel=1)
     rf = OE.gather_receptive_fields(gr, frame, lut.cpu().numpy(), outc.cpu().numpy())
     np.testing.assert_array_equal(ok["events"].cpu().numpy(), OE.sparse_pool(rf, "max")["events"])
+
+
+@pytest.mark.parametrize("kind", ["max", "mean"])
+@pytest.mark.parametrize("t_levels", [1000000, 7], ids=["distinct", "ties"])
+def test_pool_values_linear_equals_linear_then_pool(kind, t_levels):
+    """SparsePool.apply_plan_linear (the bf16 linear map of two inputs folded
+    into the value pass, ssla_sparse_pool_emit_linear) equals
+    F.linear(x.bfloat16(), w).float() followed by apply_plan, bit for bit:
+    inputs that need rounding to bf16, repeated rows (ties in the max) and
+    a 4 x 4 field as in the backbone's stem."""
+    import torch.nn.functional as F
+    from ssla_amd.layers import SparseAvgPool, SparseMaxPool
+    frame = (24, 28)
+    gr = _groups(21, 2, *frame, 250, 5, t_levels, 2)
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((gr["time"].size, 2)).astype(np.float32) * np.float32(3.3)
+    rep = np.arange(0, x.shape[0] - 1, 5)
+    x[rep + 1] = x[rep]   # repeated inputs: equal mapped rows
+    gr["events"] = x
+    d = _dev(gr)
+    layer = (SparseMaxPool if kind == "max" else SparseAvgPool)(frame, kernel_size=(4, 4))
+    w = (torch.randn(32, 2, device="cuda") * 0.7).to(torch.bfloat16)
+    print(f"pool values linear {kind} t_levels={t_levels}", flush=True)
+    with torch.no_grad():
+        plan = layer.plan(d)
+        fused = layer.apply_plan_linear(plan, d["events"], w)
+        ref = layer.apply_plan(plan, F.linear(d["events"].to(torch.bfloat16), w).float())
+    for key in KEYS:
+        assert torch.equal(fused[key], ref[key]), key
+    with pytest.raises(ValueError):
+        layer.apply_plan_linear(plan, d["events"][:-1], w)
