@@ -380,6 +380,12 @@ int ssla_rf_lut(int H, int W, int kh, int kw, int sh, int sw, int64_t *lut, int6
 /* Copies counts[0..n_counts) of the last data-dependent call that used
  * `workspace` and its input-error flag (1 if an index was out of range). */
 int ssla_events_counts(const void *workspace, int64_t *counts_out, int n_counts, int *bad_out, void *stream);
+/* ssla_events_counts without waiting: the same 260 bytes (counts as int64
+ * from byte 0, the bad-input flag as int32 at byte 256) copied into
+ * host_head, pinned host memory of at least 260 bytes, in stream order;
+ * they are there once the stream has passed the call (e.g. an event
+ * recorded after it has completed).  No reference C function. */
+int ssla_events_counts_async(const void *workspace, void *host_head, void *stream);
 
 /* Group padded events [B, N, C] (x, y, t, features...) with lengths[B] by
  * pixel b*H*W + y*W + x (stable), keeping the latest max_per_px events of

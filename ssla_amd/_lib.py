@@ -81,6 +81,7 @@ SIGNATURES = {
     "ssla_rf_lut_shape": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, C.POINTER(_i64)]),
     "ssla_rf_lut": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "ssla_events_counts": (_i32, [_vp, C.POINTER(_i64), _i32, C.POINTER(_i32), _vp]),
+    "ssla_events_counts_async": (_i32, [_vp, _vp, _vp]),
     "ssla_group_events_workspace_size": (_sz, [_i32, _i64]),
     "ssla_group_events": (_i32, [_vp, _vp, _i32, _i64, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                  _vp, _sz, _vp]),
@@ -184,7 +185,43 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """The raw handle of the current stream of t's device."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
+
+
+class ParamWatch:
+    """A cheap validity check for values derived from a module's parameters
+    and buffers.  For every tensor read (a dotted path from ``root``) it
+    keeps the dict that holds the tensor (``_parameters`` / ``_buffers`` of
+    its module), the tensor, its version and data pointer, and for every
+    module on the way the ``_modules`` dict that holds it: an in-place
+    update, a reassigned parameter, a move (``.to``) or a replaced submodule
+    fails ``valid()``."""
+    __slots__ = ("items",)
+
+    def __init__(self, root: torch.nn.Module, paths):
+        items, seen = [], set()
+        for path in paths:
+            parts = path.split(".")
+            m = root
+            for name in parts[:-1]:
+                child = m._modules[name]
+                if (id(m._modules), name) not in seen:
+                    seen.add((id(m._modules), name))
+                    items.append((m._modules, name, child, None, None))
+                m = child
+            name = parts[-1]
+            d = m._parameters if name in m._parameters else m._buffers
+            t = d.get(name)
+            items.append((d, name, t, None, None) if t is None else (d, name, t, t._version, t.data_ptr()))
+        self.items = tuple(items)
+
+    def valid(self) -> bool:
+        for d, k, obj, ver, p in self.items:
+            cur = d.get(k)
+            if cur is not obj or (ver is not None and (cur._version != ver or cur.data_ptr() != p)):
+                return False
+        return True
 
 
 def require_cuda(*tensors: torch.Tensor) -> torch.device:

@@ -40,6 +40,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _lib
 from . import events as E
 from .layers import SparseMaxPool
 from .scan import sparse_gla_scan
@@ -84,20 +85,26 @@ class SiteGLABlock(nn.Module):
         """bf16 copies of the projection weights, converted once and again
         only when a weight changes (in-place updates bump its version, a
         move or reassignment changes its storage)."""
+        if torch.is_grad_enabled():
+            mods = self._proj_modules()
+            if any(m.weight.requires_grad for m in mods.values()):
+                return {nm: m.weight.to(torch.bfloat16) for nm, m in mods.items()}   # differentiable, not cached
+        cache = self.__dict__.get("_bf16_cache")
+        if cache is not None and cache[0].valid() and ("r" in cache[1]) == (self._modules.get("res_proj") is not None):
+            return cache[1]
+        mods = self._proj_modules()
+        with torch.no_grad():
+            ws = {nm: m.weight.detach().to(torch.bfloat16).contiguous() for nm, m in mods.items()}
+            ws["qkvg"] = torch.cat([ws[nm] for nm in ("q", "k", "v", "g")], 0).contiguous()
+        names = {"q": "q_proj", "k": "k_proj", "v": "v_proj", "g": "g_proj", "o": "o_proj", "r": "res_proj"}
+        self.__dict__["_bf16_cache"] = (_lib.ParamWatch(self, [f"{names[nm]}.weight" for nm in mods]), ws)
+        return ws
+
+    def _proj_modules(self) -> Dict[str, nn.Linear]:
         mods = {"q": self.q_proj, "k": self.k_proj, "v": self.v_proj, "g": self.g_proj, "o": self.o_proj}
         if self.res_proj is not None:
             mods["r"] = self.res_proj
-        if torch.is_grad_enabled() and any(m.weight.requires_grad for m in mods.values()):
-            return {nm: m.weight.to(torch.bfloat16) for nm, m in mods.items()}   # differentiable, not cached
-        key = tuple((m.weight.data_ptr(), m.weight._version, m.weight.device) for m in mods.values())
-        cache = getattr(self, "_bf16_cache", None)
-        if cache is None or cache[0] != key:
-            with torch.no_grad():
-                ws = {nm: m.weight.detach().to(torch.bfloat16).contiguous() for nm, m in mods.items()}
-                ws["qkvg"] = torch.cat([ws[nm] for nm in ("q", "k", "v", "g")], 0).contiguous()
-                cache = (key, ws)
-            self._bf16_cache = cache
-        return cache[1]
+        return mods
 
     def _fused(self, *tensors) -> bool:
         """The one-launch kernels (ssla_site_project / ssla_site_finish) take
@@ -114,7 +121,6 @@ class SiteGLABlock(nn.Module):
         w = self._bf16()
         shp = (n, self.heads, self.head_dim)
         if self._fused(x):
-            from . import _lib
             hd = self.heads * self.head_dim
             x = x.to(torch.float32).contiguous()
             q, k, v = (torch.empty(n, hd, dtype=torch.bfloat16, device=x.device) for _ in range(3))
@@ -133,7 +139,6 @@ class SiteGLABlock(nn.Module):
         n = x.shape[0]
         w = self._bf16()
         if self._fused(o, x) and o.dtype == torch.bfloat16:
-            from . import _lib
             hd = self.heads * self.head_dim
             o = o.reshape(n, hd).contiguous()
             x = x.to(torch.float32).contiguous()
@@ -182,7 +187,6 @@ class SiteGLABlock(nn.Module):
 
 
     def _forward_one_call(self, inputs, x, state, grid_size, check):
-        from . import _lib
         H, D = self.heads, self.head_dim
         if state.dim() != 4 or state.shape[1:] != (H, D, D) or state.dtype != torch.float32 \
                 or not state.is_contiguous() or not state.is_cuda:
@@ -190,7 +194,7 @@ class SiteGLABlock(nn.Module):
         w = self._bf16()
         n = x.shape[0]
         x = x.contiguous()
-        ln, gb, gh, gw = (inputs[k].to(torch.int64).contiguous() for k in ("lengths", "batch_id", "h", "w"))
+        ln, gb, gh, gw = (E._i64(inputs[k]) for k in ("lengths", "batch_id", "h", "w"))
         G = ln.numel()
         lib = _lib.load()
         ws = torch.empty(max(lib.ssla_site_gla_block_workspace_size(n, G, H, D), 1), dtype=torch.uint8,
@@ -254,7 +258,6 @@ class DetectionHead(nn.Module):
         if not (fused and xin and xin[0].is_cuda and not torch.is_grad_enabled() and self._kernel_fits(xin)):
             dt = self.cls_convs[0][0].weight.dtype
             return self._forward_eager([x.to(dt) for x in xin])
-        from . import _lib
         prm = self._fused_params()
         B = int(xin[0].shape[0])
         grids = [x.to(torch.float32).contiguous() for x in xin]
@@ -287,21 +290,23 @@ class DetectionHead(nn.Module):
         fp32 scale and shift, and the predictions as one bf16 [16, 2 width]
         matrix (zero where a prediction does not read a branch) with fp32
         biases; recomputed only when a parameter or buffer changes."""
-        # the key covers exactly the tensors read below, each looked up
-        # through its module (a replaced module or parameter changes it);
-        # walking parameters() and buffers() instead cost about 0.2 ms of
-        # host time per call
-        ts = []
-        for lvl in range(len(self.strides)):
-            for seq in (self.cls_convs[lvl], self.reg_convs[lvl]):
-                conv, bn = seq[0], seq[1]
-                ts += (conv.weight, conv.bias, bn.weight, bn.bias, bn.running_mean, bn.running_var)
-            for pred in (self.reg_preds[lvl], self.obj_preds[lvl], self.cls_preds[lvl]):
-                ts += (pred.weight, pred.bias)
-        key = tuple((t.data_ptr(), t._version, t.device) for t in ts)
-        cache = getattr(self, "_fused_cache", None)
-        if cache is not None and cache[0] == key:
+        # the watch covers exactly the tensors read below and the modules
+        # that hold them (an in-place update, a replaced parameter or module,
+        # or a move invalidates it); comparing a key built by walking the
+        # modules cost about 40 µs of host time per call
+        cache = self.__dict__.get("_fused_cache")
+        if cache is not None and cache[0].valid():
             return cache[1]
+        paths = []
+        for lvl in range(len(self.strides)):
+            for br in ("cls_convs", "reg_convs"):
+                paths += [f"{br}.{lvl}.0.{n}" for n in ("weight", "bias")]
+                # (batch norm's running statistics change in training
+                # without a version bump; its batch counter does not)
+                paths += [f"{br}.{lvl}.1.{n}" for n in ("weight", "bias", "running_mean", "running_var",
+                                                         "num_batches_tracked")]
+            for pr in ("reg_preds", "obj_preds", "cls_preds"):
+                paths += [f"{pr}.{lvl}.{n}" for n in ("weight", "bias")]
         levels = []
         with torch.no_grad():
             for lvl in range(len(self.strides)):
@@ -323,7 +328,7 @@ class DetectionHead(nn.Module):
                 w_p[5:5 + self.num_classes, :width] = cls.weight.view(self.num_classes, width)
                 b_p[0:4], b_p[4:5], b_p[5:5 + self.num_classes] = reg.bias.float(), obj.bias.float(), cls.bias.float()
                 levels.append((w_br, torch.cat(scs).contiguous(), torch.cat(shs).contiguous(), w_p.contiguous(), b_p))
-        self._fused_cache = (key, levels)
+        self.__dict__["_fused_cache"] = (_lib.ParamWatch(self, paths), levels)
         return levels
 
     def _forward_eager(self, xin: List[torch.Tensor]) -> torch.Tensor:

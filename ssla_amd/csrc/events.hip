@@ -94,8 +94,52 @@ int sort_pairs(void *tmp, size_t tmp_bytes, const uint64_t *kin, uint64_t *kout,
 constexpr int kScanThreads = 1024, kScanPer = 8;
 constexpr int64_t kSmallScan = static_cast<int64_t>(kScanThreads) * kScanPer;
 
-__global__ __launch_bounds__(kScanThreads) void small_excl_scan(const int64_t *in, int64_t *out, int64_t n,
-                                                                int64_t *total) {
+// Scan inputs: an array, or the segment-head flag of a pooling plan's
+// field rows computed on the fly (and stored to head): 1 where row r
+// starts a segment -- the first row, a new field, or a time different from
+// the row before (reference sparse_pooling.py:26-31) -- 0 at rows past the
+// row count *n_rows (read on the device).
+struct ArrayIn {
+  const int64_t *p;
+  __device__ __forceinline__ int64_t operator()(int64_t i) const { return p[i]; }
+};
+struct RowHeadsIn {
+  const int32_t *fidx;
+  const int64_t *tim, *n_rows;
+  int64_t cap;
+  int64_t *head;
+  __device__ __forceinline__ int64_t operator()(int64_t r) const {
+    const int64_t n = min(*n_rows, cap);
+    const int64_t h = (r < n && (r == 0 || fidx[r] != fidx[r - 1] || tim[r] != tim[r - 1])) ? 1 : 0;
+    head[r] = h;
+    return h;
+  }
+};
+
+// The sample lengths clamped to [0, N] (group_events' valid rows per
+// sample), 0 at i >= B.
+struct TruncIn {
+  const int64_t *len;
+  int64_t B, N;
+  __device__ __forceinline__ int64_t operator()(int64_t i) const {
+    return i < B ? min(max(len[i], (int64_t)0), N) : 0;
+  }
+};
+// group_events' group-head flag of sorted slot i (first of its pixel; the
+// slots at or past E = *Ep are padding), also stored to head.
+struct SortedHeadsIn {
+  const uint64_t *key;
+  const int64_t *Ep;
+  int64_t *head;
+  __device__ __forceinline__ int64_t operator()(int64_t i) const {
+    const int64_t h = (i < *Ep && (i == 0 || key[i] != key[i - 1])) ? 1 : 0;
+    head[i] = h;
+    return h;
+  }
+};
+
+template <class In>
+__global__ __launch_bounds__(kScanThreads) void small_excl_scan(In in, int64_t *out, int64_t n, int64_t *total) {
   __shared__ int64_t wsum[kScanThreads / 64];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   int64_t v[kScanPer];
@@ -103,7 +147,7 @@ __global__ __launch_bounds__(kScanThreads) void small_excl_scan(const int64_t *i
 #pragma unroll
   for (int e = 0; e < kScanPer; ++e) {
     const int64_t i = static_cast<int64_t>(t) * kScanPer + e;
-    v[e] = i < n ? in[i] : 0;
+    v[e] = i < n ? in(i) : 0;
     s += v[e];
   }
   int64_t x = s;   // inclusive scan of the thread totals across the wavefront
@@ -144,8 +188,9 @@ inline int64_t lb_state_words(int64_t n) { return 1 + (std::max<int64_t>(n, 1) +
 
 __device__ __forceinline__ int64_t lb_value(uint64_t w) { return static_cast<int64_t>(w << 2) >> 2; }
 
-__global__ __launch_bounds__(kLbThreads) void lb_excl_scan(const int64_t *__restrict__ in, int64_t *__restrict__ out,
-                                                           int64_t n, uint64_t *state, int64_t *total) {
+template <class In>
+__global__ __launch_bounds__(kLbThreads) void lb_excl_scan(In in, int64_t *__restrict__ out, int64_t n, uint64_t *state,
+                                                           int64_t *total) {
   __shared__ int64_t s_tile, s_excl;
   __shared__ int64_t wsum[kLbThreads / 64];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -158,7 +203,7 @@ __global__ __launch_bounds__(kLbThreads) void lb_excl_scan(const int64_t *__rest
   int64_t s = 0;
 #pragma unroll
   for (int e = 0; e < kLbPer; ++e) {
-    v[e] = base + e < n ? in[base + e] : 0;
+    v[e] = base + e < n ? in(base + e) : 0;
     s += v[e];
   }
   int64_t x = s;
@@ -223,19 +268,25 @@ __global__ void total_from_scan(const int64_t *excl, const int64_t *val, int64_t
 // workgroup.  Above: the one-launch look-back scan when the caller hands a
 // zeroed state (lb, lb_state_words(n) words), else rocPRIM's scan.  total
 // (optional) receives the sum (0 for n = 0).
+// One launch of an exclusive scan of in(0..n) (n > 0): a single workgroup up
+// to kSmallScan values, else the look-back scan on the zeroed state lb.
+template <class In>
+void excl_scan_launch(In in, int64_t *out, int64_t n, uint64_t *lb, int64_t *total, hipStream_t st) {
+  if (n <= kSmallScan)
+    hipLaunchKernelGGL((small_excl_scan<In>), dim3(1), dim3(kScanThreads), 0, st, in, out, n, total);
+  else
+    hipLaunchKernelGGL((lb_excl_scan<In>), dim3(static_cast<unsigned>((n + kLbTile - 1) / kLbTile)), dim3(kLbThreads),
+                       0, st, in, out, n, lb, total);
+}
+
 int excl_scan(void *tmp, size_t tmp_bytes, const int64_t *in, int64_t *out, int64_t n, hipStream_t st,
               uint64_t *lb = nullptr, int64_t *total = nullptr) {
   if (n == 0) {
     if (total) hipLaunchKernelGGL(total_from_scan, dim3(1), dim3(64), 0, st, out, in, (int64_t)0, total);
     return SSLA_OK;
   }
-  if (n <= kSmallScan) {
-    hipLaunchKernelGGL(small_excl_scan, dim3(1), dim3(kScanThreads), 0, st, in, out, n, total);
-    return SSLA_OK;
-  }
-  if (lb) {
-    hipLaunchKernelGGL(lb_excl_scan, dim3(static_cast<unsigned>((n + kLbTile - 1) / kLbTile)), dim3(kLbThreads), 0, st,
-                       in, out, n, lb, total);
+  if (n <= kSmallScan || lb) {
+    excl_scan_launch(ArrayIn{in}, out, n, lb, total, st);
     return SSLA_OK;
   }
   size_t tb = tmp_bytes;
@@ -255,12 +306,12 @@ __global__ void fill_i32(int32_t *p, int64_t n, int32_t v) { GRID_STRIDE(i, n) p
 __global__ void iota_i32(int32_t *p, int64_t n) { GRID_STRIDE(i, n) p[i] = static_cast<int32_t>(i); }
 
 // One launch for a call's set-up fills: the 8 count words and 8 status
-// flags to zero, a[0..na) = va, b[0..nb) = vb, c[0..nc) = vb and z[0..nz) =
-// 0 (look-back scan states; any range may be empty).  Grid: grid_for(max(8,
-// na, nb, nc, nz)).
+// flags to zero, a[0..na) = va, b[0..nb) = vb, c[0..nc) = vb, d[0..nd) = vb
+// and z[0..nz) = 0 (look-back scan states; any range may be empty).  Grid:
+// grid_for(max(8, na, nb, nc, nd, nz)).
 __global__ void clear_and_fill(int64_t *counts, int32_t *bad, int64_t *a, int64_t na, int64_t va, int32_t *b,
                                int64_t nb, int32_t vb, int32_t *c, int64_t nc, uint64_t *z = nullptr,
-                               int64_t nz = 0) {
+                               int64_t nz = 0, int32_t *d = nullptr, int64_t nd = 0) {
   GRID_STRIDE(i, 8) {
     counts[i] = 0;
     bad[i] = 0;
@@ -269,6 +320,7 @@ __global__ void clear_and_fill(int64_t *counts, int32_t *bad, int64_t *a, int64_
   GRID_STRIDE(i, nb) b[i] = vb;
   GRID_STRIDE(i, nc) c[i] = vb;
   GRID_STRIDE(i, nz) z[i] = 0;
+  GRID_STRIDE(i, nd) d[i] = vb;
 }
 
 // Sorted-fill set-up in one launch: inv and dst to -1, and the field
@@ -280,15 +332,6 @@ __global__ void rf_sorted_setup(int32_t *inv, int64_t n_inv, int32_t *dst, int64
   GRID_STRIDE(i, n_act) {
     f_index[i] = plan_index[i];
     f_len[i] = plan_len[i];
-  }
-}
-
-// Group-events set-up: key[i] = pad (sorts last), val[i] = i, row[i] = 0.
-__global__ void ge_init(int64_t *key, int32_t *val, int64_t *row, int64_t n, int64_t pad) {
-  GRID_STRIDE(i, n) {
-    key[i] = pad;
-    val[i] = static_cast<int32_t>(i);
-    row[i] = 0;
   }
 }
 
@@ -338,11 +381,20 @@ __global__ void expand_segments(const int64_t *__restrict__ val, const int64_t *
 // Per padded slot (b, j < lengths[b]): the flat event index f = off[b] + j,
 // the pixel id (formed in fp32 as the reference does, exact below 2^24) and
 // the padded row of f.
+// Keys of the valid events at their compacted slots f = off[b] + j and the
+// padding slots [E, cap) (E = off[B]: key n_pix, sorting last; val = the
+// slot, row 0); each slot is written by one thread.
 __global__ void ge_keys(const float *__restrict__ ev, const int64_t *__restrict__ lengths,
                         const int64_t *__restrict__ off, int B, int64_t N, int C, int H, int W,
                         uint64_t *__restrict__ key, int32_t *__restrict__ val, int64_t *__restrict__ row_of,
                         int32_t *__restrict__ bad) {
+  const int64_t E = off[B];
   GRID_STRIDE(s, static_cast<int64_t>(B) * N) {   // B * N < 2^31 (checked by the caller)
+    if (s >= E) {
+      key[s] = static_cast<uint64_t>(B) * H * W;
+      val[s] = static_cast<int32_t>(s);
+      row_of[s] = 0;
+    }
     const uint32_t s32 = static_cast<uint32_t>(s), b32 = s32 / static_cast<uint32_t>(N);
     const int64_t b = b32, j = s32 - b32 * static_cast<uint32_t>(N);
     if (j >= min(max(lengths[b], (int64_t)0), N)) continue;
@@ -356,14 +408,6 @@ __global__ void ge_keys(const float *__restrict__ ev, const int64_t *__restrict_
     val[f] = static_cast<int32_t>(f);
     row_of[f] = s;
   }
-}
-
-// E = off[B] (device).  Heads of the sorted events (first of its pixel);
-// entries at or beyond E are the padding slots, which sort last.
-__global__ void ge_heads(const uint64_t *__restrict__ key, int64_t cap, const int64_t *__restrict__ Ep,
-                         int64_t *__restrict__ head) {
-  const int64_t E = *Ep;
-  GRID_STRIDE(i, cap) head[i] = (i < E && (i == 0 || key[i] != key[i - 1])) ? 1 : 0;
 }
 
 // group starts and the group count (counts[0] = G); start[G] = E
@@ -436,15 +480,6 @@ __global__ void ge_emit(const int64_t *__restrict__ head, const int64_t *__restr
       out_ev[o * F] = d;
     }
     out_t[o] = static_cast<int64_t>(src[2]);
-  }
-}
-
-__global__ void ge_finish(const int64_t *__restrict__ kpre, const int64_t *__restrict__ kept, int64_t *counts,
-                          const int64_t *__restrict__ Ep) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    const int64_t G = counts[0];
-    counts[1] = G > 0 ? kpre[G - 1] + kept[G - 1] : 0;
-    counts[2] = *Ep;
   }
 }
 
@@ -554,14 +589,23 @@ __global__ void rf_count_lanes(const int64_t *__restrict__ lut, int64_t n_rf, in
   }
 }
 
-// act_pre / ev_pre and their totals (counts[0], counts[1]) from the prefix
-// sum of the packed pairs
-__global__ void rf_unpack(const int64_t *__restrict__ pk_pre, const int64_t *__restrict__ pk, int64_t n,
-                          int64_t *__restrict__ act_pre, int64_t *__restrict__ ev_pre, int64_t *__restrict__ counts) {
+// From the prefix sum of the packed pairs, in one launch: act_pre / ev_pre
+// of every field, the flat index and event count of every active field
+// (f_index / f_len at its active index, as rf_fields writes them) and the
+// totals (counts[0], counts[1]).
+__global__ void rf_unpack_fields(const int64_t *__restrict__ pk_pre, const int64_t *__restrict__ pk, int64_t n,
+                                 int64_t *__restrict__ act_pre, int64_t *__restrict__ ev_pre,
+                                 int64_t *__restrict__ counts, int64_t *__restrict__ f_index,
+                                 int64_t *__restrict__ f_len) {
   constexpr int64_t mask = (int64_t{1} << kPackBits) - 1;
   GRID_STRIDE(f, n) {
-    act_pre[f] = pk_pre[f] & mask;
-    ev_pre[f] = pk_pre[f] >> kPackBits;
+    const int64_t pre = pk_pre[f], v = pk[f];
+    act_pre[f] = pre & mask;
+    ev_pre[f] = pre >> kPackBits;
+    if (v & mask) {
+      f_index[pre & mask] = f;
+      f_len[pre & mask] = v >> kPackBits;
+    }
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     const int64_t t = n > 0 ? pk_pre[n - 1] + pk[n - 1] : 0;
@@ -1030,30 +1074,34 @@ int group_events_impl(const char *what, const float *events, const int64_t *leng
                        (int64_t)0, nullptr, (int64_t)0, 0, nullptr, (int64_t)0);
     return launch_status(what);
   }
-  // sample offsets: exclusive scan of the lengths clamped to [0, N]
+  // sample offsets: exclusive scan of the lengths clamped to [0, N], their
+  // sum E in counts[2]
   hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max<int64_t>(std::max<int64_t>(8, B + 1), 2 * L.lb_words))),
                      dim3(kThreads), 0, st, L.counts, L.bad, L.kept, (int64_t)(B + 1), (int64_t)0, nullptr,
                      (int64_t)0, 0, nullptr, (int64_t)0, L.lb, 2 * L.lb_words);
-  hipLaunchKernelGGL(trunc_len, dim3(grid_for(B)), dim3(kThreads), 0, st, lengths, (int64_t)B, N, L.kept);
-  int s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.off, B + 1, st);
-  if (s) return s;
+  int s = SSLA_OK;
+  if (B + 1 <= kSmallScan) {
+    excl_scan_launch(TruncIn{lengths, B, N}, L.off, B + 1, nullptr, L.counts + 2, st);
+  } else {
+    hipLaunchKernelGGL(trunc_len, dim3(grid_for(B)), dim3(kThreads), 0, st, lengths, (int64_t)B, N, L.kept);
+    s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.off, B + 1, st, nullptr, L.counts + 2);
+    if (s) return s;
+  }
   // keys of the valid events (pixel ids < B*H*W); padding slots take the key
   // B*H*W and sort last, so only the bits of B*H*W need sorting
   const int64_t n_pix = static_cast<int64_t>(B) * H * W;
-  hipLaunchKernelGGL(ge_init, dim3(grid_for(cap)), dim3(kThreads), 0, st, reinterpret_cast<int64_t *>(L.key), L.val,
-                     L.row_of, cap, n_pix);
   hipLaunchKernelGGL(ge_keys, dim3(grid_for(cap)), dim3(kThreads), 0, st, events, lengths, L.off, B, N, C, H, W,
                      L.key, L.val, L.row_of, L.bad);
   s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.order, cap, bits_for(static_cast<uint64_t>(n_pix)), st);
   if (s) return s;
-  hipLaunchKernelGGL(ge_heads, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.skey, cap, Ep, L.head);
-  s = excl_scan(L.tmp, L.tmp_bytes, L.head, L.gpos, cap, st, L.lb);
-  if (s) return s;
+  // group heads (computed inside the scan) and their positions
+  excl_scan_launch(SortedHeadsIn{L.skey, Ep, L.head}, L.gpos, cap, L.lb, nullptr, st);
   hipLaunchKernelGGL(ge_starts, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, cap, Ep, L.start,
                      L.counts);
   hipLaunchKernelGGL(ge_groups, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.counts, L.start, cap, L.order,
                      L.row_of, events, N, C, max_per_px, keep_first, L.kept, gr_batch, gr_h, gr_w, gr_len);
-  s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.kpre, cap, st, L.lb + L.lb_words);
+  // kept-event offsets, their sum in counts[1]
+  s = excl_scan(L.tmp, L.tmp_bytes, L.kept, L.kpre, cap, st, L.lb + L.lb_words, L.counts + 1);
   if (s) return s;
   if (delays)
     hipLaunchKernelGGL(ge_emit<true>, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, L.start, L.kept,
@@ -1061,7 +1109,6 @@ int group_events_impl(const char *what, const float *events, const int64_t *leng
   else
     hipLaunchKernelGGL(ge_emit<false>, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, L.start, L.kept,
                        L.kpre, L.order, L.row_of, events, cap, Ep, C, max_per_px, fc, out_events, out_time);
-  hipLaunchKernelGGL(ge_finish, dim3(1), dim3(64), 0, st, L.kpre, L.kept, L.counts, Ep);
   return launch_status(what);
 }
 }  // namespace
@@ -1107,6 +1154,22 @@ extern "C" int ssla_events_counts(const void *workspace, int64_t *counts_out, in
   memcpy(badv, raw + 256, sizeof(badv));
   for (int i = 0; i < n_counts; ++i) counts_out[i] = buf[i];
   if (bad_out) *bad_out = badv[0];
+  return SSLA_OK;
+}
+
+// The counts head of a workspace (the 260 bytes ssla_events_counts reads)
+// copied into host memory in stream order, without waiting: host_head must
+// be pinned (page-locked) memory; the copy has landed once the stream has
+// passed this point (an event recorded after the call).
+extern "C" int ssla_events_counts_async(const void *workspace, void *host_head, void *stream) {
+  clear_error();
+  SSLA_CHECK_ARG(workspace && host_head, "events_counts_async: null pointer");
+  const hipError_t e = hipMemcpyAsync(host_head, workspace, 256 + sizeof(int32_t), hipMemcpyDeviceToHost,
+                                      static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) {
+    set_error("events_counts_async: %s", hipGetErrorString(e));
+    return SSLA_ERR_LAUNCH;
+  }
   return SSLA_OK;
 }
 
@@ -1249,7 +1312,7 @@ __global__ void rf_merge(const int32_t *__restrict__ ev2g, const int64_t *__rest
 // ---- receptive-field / patch scatter ---------------------------------------------
 namespace {
 struct RfWs {
-  int64_t *counts, *gstart, *nev, *act, *act_pre, *ev_pre, *f_index, *f_len, *pre_src, *pre_pos;
+  int64_t *counts, *gstart, *nev, *act, *act_pre, *ev_pre, *f_index, *f_len, *pre_src, *pre_pos, *pk, *pk_pre;
   int32_t *bad, *pixmap, *val, *perm;
   uint64_t *key, *skey;
   unsigned long long *tmax;
@@ -1275,6 +1338,8 @@ RfWs rf_layout(void *ws, int64_t G, int64_t n_pix, int64_t n_f, int64_t E_cap) {
   L.ev_pre = c.take<int64_t>(n_f);
   L.f_index = c.take<int64_t>(n_f);
   L.f_len = c.take<int64_t>(n_f);
+  L.pk = c.take<int64_t>(n_f);
+  L.pk_pre = c.take<int64_t>(n_f);
   L.pre_src = c.take<int64_t>(E_cap);
   L.pre_pos = c.take<int64_t>(E_cap);
   L.key = c.take<uint64_t>(E_cap);
@@ -1322,9 +1387,16 @@ int rf_plan_impl(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr
   SSLA_CHECK_ARG(lut && (G == 0 || (gr_batch && gr_h && gr_w && gr_len)) && (E_in == 0 || time),
                  "rf_scatter_plan: null pointer");
   const int64_t n_inv = inv ? static_cast<int64_t>(H) * W * (one_field ? 1 : A) : 0;
-  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max(std::max(std::max<int64_t>(8, n_pix), n_inv), L.lb_words))),
+  // event -> group table (the sort-free fill's input; kept in the value
+  // buffer of the sort path, which needs E_in <= E_cap): -1 until
+  // rf_groups_scan fills it
+  const int store = E_in <= E_cap;
+  const int64_t n_ev2g = store ? E_in : 0;
+  hipLaunchKernelGGL(clear_and_fill,
+                     dim3(grid_for(std::max(std::max(std::max<int64_t>(8, n_pix), std::max(n_inv, n_ev2g)),
+                                            L.lb_words))),
                      dim3(kThreads), 0, st, L.counts, L.bad, reinterpret_cast<int64_t *>(L.tmax), (int64_t)1,
-                     (int64_t)0, L.pixmap, n_pix, -1, inv, n_inv, L.lb_g, L.lb_words);
+                     (int64_t)0, L.pixmap, n_pix, -1, inv, n_inv, L.lb_g, L.lb_words, L.val, n_ev2g);
   if (G > 0 || inv)
     hipLaunchKernelGGL(rf_pixmap, dim3(grid_for(std::max(G, inv ? n_rf * A : 0))), dim3(kThreads), 0, st, gr_batch,
                        gr_h, gr_w, G, H, W, n_pix, L.pixmap, L.bad, lut, n_rf, A, inv, one_field ? 1 : 0,
@@ -1332,20 +1404,20 @@ int rf_plan_impl(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr
   int s = excl_scan(L.tmp, L.tmp_bytes, gr_len, L.gstart, G, st, L.lb_g);
   if (s) return s;
   // one prefix sum of the packed (events, active) pairs while the active
-  // count fits 21 bits (f_index / f_len hold the pairs until rf_fields)
+  // count fits 21 bits
   const bool packed = n_f < (int64_t{1} << kPackBits);
   if (64 % A == 0 && n_f * A <= (int64_t{1} << 28))
     hipLaunchKernelGGL(rf_count_lanes, dim3(static_cast<unsigned>((n_f * A + kThreads - 1) / kThreads)),
                        dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap, gr_len, L.nev, L.act,
-                       packed ? L.f_index : nullptr);
+                       packed ? L.pk : nullptr);
   else
     hipLaunchKernelGGL(rf_count, dim3(grid_for(n_f)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap, gr_len,
-                       L.nev, L.act, packed ? L.f_index : nullptr);
+                       L.nev, L.act, packed ? L.pk : nullptr);
   if (packed) {
-    s = excl_scan(L.tmp, L.tmp_bytes, L.f_index, L.f_len, n_f, st);
+    s = excl_scan(L.tmp, L.tmp_bytes, L.pk, L.pk_pre, n_f, st);
     if (s) return s;
-    hipLaunchKernelGGL(rf_unpack, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.f_len, L.f_index, n_f, L.act_pre,
-                       L.ev_pre, L.counts);
+    hipLaunchKernelGGL(rf_unpack_fields, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.pk_pre, L.pk, n_f, L.act_pre,
+                       L.ev_pre, L.counts, L.f_index, L.f_len);
   } else {
     s = excl_scan(L.tmp, L.tmp_bytes, L.act, L.act_pre, n_f, st);
     if (s) return s;
@@ -1357,15 +1429,11 @@ int rf_plan_impl(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr
   if (E_in > 0 && with_tmax)
     hipLaunchKernelGGL(max_i64, dim3(grid_for(std::min<int64_t>(E_in, 1 << 16))), dim3(kThreads), 0, st, time, E_in,
                        L.tmax);
-  hipLaunchKernelGGL(rf_fields, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.act, L.act_pre, L.nev, n_f, L.f_index,
-                     L.f_len);
+  if (!packed)
+    hipLaunchKernelGGL(rf_fields, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.act, L.act_pre, L.nev, n_f, L.f_index,
+                       L.f_len);
   if (with_tmax) hipLaunchKernelGGL(store_u64_as_i64, dim3(1), dim3(64), 0, st, L.tmax, L.counts + 2);
-  // event -> group table (the sort-free fill's input; kept in the value
-  // buffer of the sort path, which needs E_in <= E_cap) and the count of
-  // unsorted runs
-  const int store = E_in <= E_cap;
-  if (store && E_in > 0)
-    hipLaunchKernelGGL(fill_i32, dim3(grid_for(E_in)), dim3(kThreads), 0, st, L.val, E_in, -1);
+  // the event -> group table and the count of unsorted runs
   if (G > 0 || !store)
     hipLaunchKernelGGL(rf_groups_scan, dim3(grid_for(std::max<int64_t>(std::max(G, E_in), 1))), dim3(kThreads), 0,
                        st, L.gstart, gr_len, G, time, E_in, L.val, store,
@@ -1624,9 +1692,14 @@ __global__ void pool_emit_rows(const float *__restrict__ ev, int64_t E_in, int C
 // whose set-up kernel zeroed the look-back scan state (a second pass, after
 // the sort fill, takes rocPRIM's scan).
 int pool_segments_pass(const PoolWs &L, int64_t E_cap, hipStream_t st, bool first) {
+  if (first && E_cap > 0) {   // the head flags computed inside the scan's launch
+    excl_scan_launch(RowHeadsIn{L.fidx, L.tim, L.rf.counts + 1, E_cap, L.head}, L.segx, E_cap, L.rf.lb_e,
+                     L.rf.counts + 4, st);
+    return SSLA_OK;
+  }
   hipLaunchKernelGGL(pool_row_heads, dim3(grid_for(E_cap)), dim3(kThreads), 0, st, L.fidx, L.tim, L.rf.counts + 1,
                      E_cap, L.head);
-  return excl_scan(L.tmp, L.tmp_bytes, L.head, L.segx, E_cap, st, first ? L.rf.lb_e : nullptr, L.rf.counts + 4);
+  return excl_scan(L.tmp, L.tmp_bytes, L.head, L.segx, E_cap, st, nullptr, L.rf.counts + 4);
 }
 }  // namespace
 

@@ -27,6 +27,7 @@ from __future__ import annotations
 import ctypes
 from typing import Dict, List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -58,28 +59,63 @@ def _counts(ws: torch.Tensor, n: int, stream: int, what: str, check_bad: bool = 
 _HEAD_BYTES = 260
 
 
+class _CountSlot:
+    """Pinned host memory for one counts head (with int64 / int32 views)
+    and the event that marks its copy."""
+    __slots__ = ("host", "i64", "i32", "event")
+
+    def __init__(self):
+        self.host = torch.zeros(_HEAD_BYTES + 4, dtype=torch.uint8, pin_memory=True)
+        arr = self.host.numpy()
+        self.i64, self.i32 = arr.view(np.int64), arr.view(np.int32)
+        self.event = torch.cuda.Event()
+
+
+# per device index: slots whose counts were read, ready for another copy
+_free_slots: Dict[int, list] = {}
+
+
 class PendingCounts:
     """The counts of a data-dependent call on their way to host memory: a
     copy of the workspace head into pinned memory, queued on the current
     stream behind the call's kernels, and the event after it.  ``read``
     waits on that event only, so work queued after the copy keeps the
-    device busy meanwhile."""
-    __slots__ = ("host", "event")
+    device busy meanwhile; its pinned slot then serves later copies."""
+    __slots__ = ("slot", "dev")
 
     def __init__(self, ws: torch.Tensor):
-        n = min(_HEAD_BYTES, ws.numel())
-        self.host = torch.zeros(_HEAD_BYTES, dtype=torch.uint8, pin_memory=True)
-        self.host[:n].copy_(ws[:n], non_blocking=True)
-        self.event = torch.cuda.Event()
-        self.event.record(torch.cuda.current_stream(ws.device))
+        if ws.numel() < _HEAD_BYTES:
+            raise ValueError(f"PendingCounts: workspace of {ws.numel()} bytes holds no counts head")
+        dev = ws.get_device()
+        free = _free_slots.setdefault(dev, [])
+        if free:
+            slot = free.pop()
+        else:
+            with torch.cuda.device(dev):
+                slot = _CountSlot()
+        _lib.check(_lib.load().ssla_events_counts_async(ws.data_ptr(), slot.host.data_ptr(), _lib.stream_of(ws)),
+                   "events_counts_async")
+        if dev == torch.cuda.current_device():
+            slot.event.record()
+        else:
+            slot.event.record(torch.cuda.current_stream(ws.device))
+        self.slot, self.dev = slot, dev
 
     def read(self, n: int):
         """(counts[0..n), input-error flag) once the copy has landed."""
-        self.event.synchronize()
-        return self.host[:8 * n].view(torch.int64).tolist(), int(self.host[256:260].view(torch.int32)[0])
+        slot = self.slot
+        if slot is None:
+            raise RuntimeError("PendingCounts.read: the counts were read already")
+        slot.event.synchronize()
+        out = slot.i64[:n].tolist(), int(slot.i32[64])
+        self.slot = None
+        _free_slots[self.dev].append(slot)
+        return out
 
 
 def _i64(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype is torch.int64 and t.is_contiguous():
+        return t
     return t.to(torch.int64).contiguous()
 
 
