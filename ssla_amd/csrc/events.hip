@@ -125,6 +125,16 @@ struct TruncIn {
     return i < B ? min(max(len[i], (int64_t)0), N) : 0;
   }
 };
+// A pixel-sort histogram (int32), each counter cleared as it is read so the
+// next pass can count into the same memory.
+struct HistIn {
+  int32_t *h;
+  __device__ __forceinline__ int64_t operator()(int64_t i) const {
+    const int64_t v = h[i];
+    h[i] = 0;
+    return v;
+  }
+};
 // group_events' group-head flag of sorted slot i (first of its pixel; the
 // slots at or past E = *Ep are padding), also stored to head.
 struct SortedHeadsIn {
@@ -180,7 +190,7 @@ __global__ __launch_bounds__(kScanThreads) void small_excl_scan(In in, int64_t *
 // 1 aggregate, 2 inclusive prefix), [61:0] the value (two's complement), so
 // the payload travels with its state and relaxed agent-scope atomics
 // suffice.  total (optional) receives the sum.
-constexpr int kLbThreads = 256, kLbPer = 16;
+constexpr int kLbThreads = 1024, kLbPer = 4;
 constexpr int64_t kLbTile = static_cast<int64_t>(kLbThreads) * kLbPer;
 constexpr uint64_t kLbAgg = 1ull << 62, kLbIncl = 2ull << 62, kLbMask = (1ull << 62) - 1;
 
@@ -216,7 +226,6 @@ __global__ __launch_bounds__(kLbThreads) void lb_excl_scan(In in, int64_t *__res
   __syncthreads();
   if (w == 0) {
     int64_t agg = 0;
-#pragma unroll
     for (int j = 0; j < kLbThreads / 64; ++j) agg += wsum[j];
     int64_t ex = 0;
     if (tile > 0) {
@@ -383,17 +392,23 @@ __global__ void expand_segments(const int64_t *__restrict__ val, const int64_t *
 // the padded row of f.
 // Keys of the valid events at their compacted slots f = off[b] + j and the
 // padding slots [E, cap) (E = off[B]: key n_pix, sorting last; val = the
-// slot, row 0); each slot is written by one thread.
+// slot, row 0); each slot is written by one thread.  hist (optional): the
+// first pass of the pixel sort counts every slot's low digit (key &
+// (2^d1 - 1)) in its tile (slot / kRsTile), hist[digit * n_tiles + tile].
+constexpr int kRsSteps = 16, kRsTile = 64 * kRsSteps;
 __global__ void ge_keys(const float *__restrict__ ev, const int64_t *__restrict__ lengths,
                         const int64_t *__restrict__ off, int B, int64_t N, int C, int H, int W,
                         uint64_t *__restrict__ key, int32_t *__restrict__ val, int64_t *__restrict__ row_of,
-                        int32_t *__restrict__ bad) {
+                        int32_t *__restrict__ bad, int32_t *__restrict__ hist, int d1, int64_t n_tiles) {
   const int64_t E = off[B];
+  const uint64_t mask1 = (uint64_t{1} << d1) - 1;
   GRID_STRIDE(s, static_cast<int64_t>(B) * N) {   // B * N < 2^31 (checked by the caller)
     if (s >= E) {
-      key[s] = static_cast<uint64_t>(B) * H * W;
+      const uint64_t k = static_cast<uint64_t>(B) * H * W;
+      key[s] = k;
       val[s] = static_cast<int32_t>(s);
       row_of[s] = 0;
+      if (hist) atomicAdd(&hist[static_cast<int64_t>(k & mask1) * n_tiles + s / kRsTile], 1);
     }
     const uint32_t s32 = static_cast<uint32_t>(s), b32 = s32 / static_cast<uint32_t>(N);
     const int64_t b = b32, j = s32 - b32 * static_cast<uint32_t>(N);
@@ -404,10 +419,126 @@ __global__ void ge_keys(const float *__restrict__ ev, const int64_t *__restrict_
     if (!(x >= 0.f && x < W && y >= 0.f && y < H)) *bad = 1;
     // out-of-frame events (reported through bad) stay inside the sorted bits
     const uint64_t n_pix = static_cast<uint64_t>(B) * H * W;
-    key[f] = pid >= 0.f ? min(static_cast<uint64_t>(pid), n_pix) : 0;
+    const uint64_t k = pid >= 0.f ? min(static_cast<uint64_t>(pid), n_pix) : 0;
+    key[f] = k;
     val[f] = static_cast<int32_t>(f);
     row_of[f] = s;
+    if (hist) atomicAdd(&hist[static_cast<int64_t>(k & mask1) * n_tiles + f / kRsTile], 1);
   }
+}
+
+// One pass of the pixel sort (a stable LSD counting sort): the digit of a
+// key is (key >> shift) & (2^d - 1); off[digit * n_tiles + tile] is where
+// the tile's keys of that digit start (the exclusive prefix of the pass's
+// histogram in digit-major order).  A workgroup per tile of kRsTile slots,
+// 16 / S wavefronts each taking S rows of 64 in order.  Within a row the
+// lanes with equal digits find each other with one ballot per digit bit and
+// rank by lane; the lowest of them adds their count to the wavefront's LDS
+// counter of the digit (so a lane's rank within its wavefront is that
+// counter's old value plus the lanes below it with its digit).  The
+// counters are then turned into per-digit prefixes over the wavefronts, so
+// a key's place is the digit's start + the keys of that digit in earlier
+// wavefronts + its rank: slot order within the tile, equal keys keep their
+// order.  FIRST: also counts the next pass's digits (shift2, d2) at the
+// destination tiles into hist2.  Destinations outside [0, n) (inconsistent
+// counts) are skipped.  LDS: (16 / S + 1) * 2^d int32.
+template <bool FIRST, int S>
+__global__ __launch_bounds__(64 * (kRsSteps / S)) void rs_scatter(
+    const uint64_t *__restrict__ kin, const int32_t *__restrict__ vin, int64_t n, int64_t n_tiles, int shift, int d,
+    const int64_t *__restrict__ off, uint64_t *__restrict__ kout, int32_t *__restrict__ vout, int shift2, int d2,
+    int32_t *__restrict__ hist2) {
+  constexpr int kW = kRsSteps / S;
+  extern __shared__ int32_t rs_lds[];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t t = blockIdx.x;
+  const uint32_t R = 1u << d;
+  int32_t *rs_base = rs_lds, *rs_cnt = rs_lds + R;   // rs_cnt[w * R + digit]
+  for (uint32_t r = tid; r < R; r += 64 * kW) {
+    rs_base[r] = static_cast<int32_t>(off[static_cast<int64_t>(r) * n_tiles + t]);
+#pragma unroll
+    for (int q = 0; q < kW; ++q) rs_cnt[q * R + r] = 0;
+  }
+  __syncthreads();
+  const int64_t base = t * kRsTile + static_cast<int64_t>(w) * S * 64;
+  uint64_t k[S];
+  int32_t v[S], rank[S];
+  uint32_t dig[S];
+#pragma unroll
+  for (int st = 0; st < S; ++st) {
+    const int64_t i = base + st * 64 + lane;
+    k[st] = i < n ? kin[i] : 0;
+    v[st] = i < n ? vin[i] : 0;
+  }
+  const uint64_t below = (uint64_t{1} << lane) - 1;
+  int32_t *cnt = rs_cnt + static_cast<int64_t>(w) * R;
+#pragma unroll
+  for (int st = 0; st < S; ++st) {
+    const bool valid = base + st * 64 + lane < n;
+    const uint32_t r = static_cast<uint32_t>(k[st] >> shift) & (R - 1);
+    uint64_t m = __builtin_amdgcn_ballot_w64(valid);
+    for (int b = 0; b < d; ++b) {
+      const bool bit = (r >> b) & 1u;
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(bit);
+      m &= bit ? bal : ~bal;
+    }
+    const int leader = valid ? __builtin_ctzll(m) : lane;
+    int32_t old = 0;
+    if (valid && lane == leader) {
+      old = cnt[r];
+      cnt[r] = old + __builtin_popcountll(m);
+    }
+    old = __shfl(old, leader, 64);
+    rank[st] = old + __builtin_popcountll(m & below);
+    dig[st] = r;
+  }
+  __syncthreads();
+  // per digit: the counts of the wavefronts before each one
+  for (uint32_t r = tid; r < R; r += 64 * kW) {
+    int32_t run = 0;
+#pragma unroll
+    for (int q = 0; q < kW; ++q) {
+      const int32_t c = rs_cnt[q * R + r];
+      rs_cnt[q * R + r] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int st = 0; st < S; ++st) {
+    if (base + st * 64 + lane >= n) continue;
+    const uint32_t r = dig[st];
+    const int64_t pos = static_cast<int64_t>(rs_base[r]) + cnt[r] + rank[st];
+    if (pos < 0 || pos >= n) continue;
+    kout[pos] = k[st];
+    vout[pos] = v[st];
+    if constexpr (FIRST) {
+      const uint32_t r2 = static_cast<uint32_t>(k[st] >> shift2) & ((1u << d2) - 1);
+      atomicAdd(&hist2[static_cast<int64_t>(r2) * n_tiles + pos / kRsTile], 1);
+    }
+  }
+}
+
+// A pass of the pixel sort with the widest wavefront split whose counters
+// stay within 50 KB of LDS (S rows per wavefront: 1 up to 2^9 digits, 2 at
+// 2^10, 4 at 2^11, 8 at 2^12).
+template <bool FIRST>
+void rs_pass(const uint64_t *kin, const int32_t *vin, int64_t n, int64_t n_tiles, int shift, int d,
+             const int64_t *off, uint64_t *kout, int32_t *vout, int shift2, int d2, int32_t *hist2, hipStream_t st) {
+  const unsigned tiles = static_cast<unsigned>(n_tiles);
+  const int S = d <= 9 ? 1 : (d == 10 ? 2 : (d == 11 ? 4 : 8));
+  const size_t lds = (static_cast<size_t>(kRsSteps / S) + 1) * (size_t{1} << d) * sizeof(int32_t);
+  if (S == 1)
+    hipLaunchKernelGGL((rs_scatter<FIRST, 1>), dim3(tiles), dim3(64 * kRsSteps), lds, st, kin, vin, n, n_tiles, shift,
+                       d, off, kout, vout, shift2, d2, hist2);
+  else if (S == 2)
+    hipLaunchKernelGGL((rs_scatter<FIRST, 2>), dim3(tiles), dim3(64 * kRsSteps / 2), lds, st, kin, vin, n, n_tiles,
+                       shift, d, off, kout, vout, shift2, d2, hist2);
+  else if (S == 4)
+    hipLaunchKernelGGL((rs_scatter<FIRST, 4>), dim3(tiles), dim3(64 * kRsSteps / 4), lds, st, kin, vin, n, n_tiles,
+                       shift, d, off, kout, vout, shift2, d2, hist2);
+  else
+    hipLaunchKernelGGL((rs_scatter<FIRST, 8>), dim3(tiles), dim3(64 * kRsSteps / 8), lds, st, kin, vin, n, n_tiles,
+                       shift, d, off, kout, vout, shift2, d2, hist2);
 }
 
 // group starts and the group count (counts[0] = G); start[G] = E
@@ -1014,9 +1145,18 @@ struct GeWs {
   int32_t *val, *order, *bad;
   uint64_t *lb;   // two look-back scan states of lb_state_words(cap) words
   int64_t lb_words;
+  // the pixel sort (caps up to kRsMaxCap): one histogram (int32, up to
+  // 2^12 digits per tile), its prefix, the first pass's output and a
+  // look-back state per pass
+  int32_t *rs_hist, *rs_tval;
+  int64_t *rs_off;
+  uint64_t *rs_tkey, *rs_lb;
+  int64_t rs_tiles, rs_counters, rs_lb_words;
   void *tmp;
   size_t tmp_bytes, total;
 };
+constexpr int64_t kRsMaxCap = int64_t{1} << 21;
+constexpr int kRsMaxDigit = 12;   // two passes cover keys up to 24 bits
 GeWs ge_layout(void *ws, int B, int64_t cap) {
   Carve c{static_cast<char *>(ws)};
   GeWs L;
@@ -1034,8 +1174,18 @@ GeWs ge_layout(void *ws, int B, int64_t cap) {
   L.val = c.take<int32_t>(cap);
   L.order = c.take<int32_t>(cap);
   L.lb_words = lb_state_words(cap);
-  L.lb = c.take<uint64_t>(2 * L.lb_words);
-  L.tmp_bytes = std::max(sort_temp_bytes(cap), scan_temp_bytes(std::max<int64_t>(cap, B + 1)));
+  const bool rs = cap <= kRsMaxCap;
+  L.rs_tiles = (cap + kRsTile - 1) / kRsTile;
+  L.rs_counters = rs ? (int64_t{1} << kRsMaxDigit) * L.rs_tiles : 0;
+  L.rs_lb_words = rs ? lb_state_words(L.rs_counters) : 0;
+  // the scan states of the grouping (2) and of the pixel sort (2), contiguous
+  L.lb = c.take<uint64_t>(2 * (L.lb_words + L.rs_lb_words));
+  L.rs_lb = L.lb ? L.lb + 2 * L.lb_words : nullptr;
+  L.rs_hist = c.take<int32_t>(L.rs_counters);
+  L.rs_off = c.take<int64_t>(L.rs_counters);
+  L.rs_tkey = c.take<uint64_t>(rs ? cap : 0);
+  L.rs_tval = c.take<int32_t>(rs ? cap : 0);
+  L.tmp_bytes = std::max(rs ? 0 : sort_temp_bytes(cap), scan_temp_bytes(std::max<int64_t>(cap, B + 1)));
   L.tmp = c.take<char>(L.tmp_bytes);
   L.total = c.off;
   return L;
@@ -1076,9 +1226,18 @@ int group_events_impl(const char *what, const float *events, const int64_t *leng
   }
   // sample offsets: exclusive scan of the lengths clamped to [0, N], their
   // sum E in counts[2]
-  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max<int64_t>(std::max<int64_t>(8, B + 1), 2 * L.lb_words))),
-                     dim3(kThreads), 0, st, L.counts, L.bad, L.kept, (int64_t)(B + 1), (int64_t)0, nullptr,
-                     (int64_t)0, 0, nullptr, (int64_t)0, L.lb, 2 * L.lb_words);
+  // the pixel sort: two stable counting passes over digits of d1 and d2 bits
+  // (keys up to n_pix, below 2^24) while the capacity is at most kRsMaxCap,
+  // else rocPRIM's radix sort
+  const int64_t n_pix = static_cast<int64_t>(B) * H * W;
+  const bool rs = cap <= kRsMaxCap;
+  const int bits = bits_for(static_cast<uint64_t>(n_pix));
+  const int d1 = (bits + 1) / 2, d2 = bits - d1;
+  const int64_t n_hist1 = rs ? (int64_t{1} << d1) * L.rs_tiles : 0;
+  const int64_t n_lb = 2 * (L.lb_words + L.rs_lb_words);
+  hipLaunchKernelGGL(clear_and_fill, dim3(grid_for(std::max(std::max<int64_t>(8, B + 1), std::max(n_lb, n_hist1)))),
+                     dim3(kThreads), 0, st, L.counts, L.bad, L.kept, (int64_t)(B + 1), (int64_t)0, L.rs_hist, n_hist1,
+                     0, nullptr, (int64_t)0, L.lb, n_lb);
   int s = SSLA_OK;
   if (B + 1 <= kSmallScan) {
     excl_scan_launch(TruncIn{lengths, B, N}, L.off, B + 1, nullptr, L.counts + 2, st);
@@ -1089,11 +1248,22 @@ int group_events_impl(const char *what, const float *events, const int64_t *leng
   }
   // keys of the valid events (pixel ids < B*H*W); padding slots take the key
   // B*H*W and sort last, so only the bits of B*H*W need sorting
-  const int64_t n_pix = static_cast<int64_t>(B) * H * W;
   hipLaunchKernelGGL(ge_keys, dim3(grid_for(cap)), dim3(kThreads), 0, st, events, lengths, L.off, B, N, C, H, W,
-                     L.key, L.val, L.row_of, L.bad);
-  s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.order, cap, bits_for(static_cast<uint64_t>(n_pix)), st);
-  if (s) return s;
+                     L.key, L.val, L.row_of, L.bad, rs ? L.rs_hist : nullptr, d1, L.rs_tiles);
+  if (rs) {
+    excl_scan_launch(HistIn{L.rs_hist}, L.rs_off, n_hist1, L.rs_lb, nullptr, st);
+    if (d2 > 0) {
+      rs_pass<true>(L.key, L.val, cap, L.rs_tiles, 0, d1, L.rs_off, L.rs_tkey, L.rs_tval, d1, d2, L.rs_hist, st);
+      excl_scan_launch(HistIn{L.rs_hist}, L.rs_off, (int64_t{1} << d2) * L.rs_tiles, L.rs_lb + L.rs_lb_words, nullptr,
+                       st);
+      rs_pass<false>(L.rs_tkey, L.rs_tval, cap, L.rs_tiles, d1, d2, L.rs_off, L.skey, L.order, 0, 0, nullptr, st);
+    } else {
+      rs_pass<false>(L.key, L.val, cap, L.rs_tiles, 0, d1, L.rs_off, L.skey, L.order, 0, 0, nullptr, st);
+    }
+  } else {
+    s = sort_pairs(L.tmp, L.tmp_bytes, L.key, L.skey, L.val, L.order, cap, bits, st);
+    if (s) return s;
+  }
   // group heads (computed inside the scan) and their positions
   excl_scan_launch(SortedHeadsIn{L.skey, Ep, L.head}, L.gpos, cap, L.lb, nullptr, st);
   hipLaunchKernelGGL(ge_starts, dim3(grid_for(cap)), dim3(kThreads), 0, st, L.head, L.gpos, cap, Ep, L.start,

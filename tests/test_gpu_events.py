@@ -192,6 +192,34 @@ def test_preprocess_large_vs_oracle(dev):
         np.testing.assert_array_equal(_np(one[key]), ro[key], err_msg=key)
 
 
+@pytest.mark.parametrize("B,H,W", [(8, 240, 304), (4, 480, 640), (32, 480, 640), (1, 8, 8), (1, 1, 1)],
+                         ids=["20bit", "21bit", "24bit", "7bit", "1bit"])
+def test_group_events_pixel_sort_widths(dev, B, H, W):
+    """group_events' pixel sort (two stable counting passes; digits of 1 to
+    12 bits, so 1 to 16 wavefronts per tile and a single pass for 1-bit
+    keys) against the oracle's stable argsort, with ragged samples, repeated
+    pixels and a few events outside the frame dropped by the lengths."""
+    from ssla_amd import events as E
+    gen = np.random.default_rng(B * 1000 + H)
+    N = 600
+    lens = gen.integers(0, N + 1, B).astype(np.int64)
+    lens[0] = N
+    ev = np.zeros((B, N, 4), np.float32)
+    for b in range(B):
+        n = int(lens[b])
+        ev[b, :n, 0] = gen.integers(0, W, n)
+        ev[b, :n, 1] = gen.integers(0, H, n)
+        ev[b, :n, 2] = np.sort(gen.integers(0, 10_000, n))
+        ev[b, :n, 3] = 1.0
+        if n > 40:
+            ev[b, 10:40, 0], ev[b, 10:40, 1] = ev[b, 5, 0], ev[b, 5, 1]   # a pixel with many events
+    print(f"group_events pixel sort B={B} H={H} W={W}", flush=True)
+    gr = E.group_events((_t(ev, dev), _t(lens, dev)), (H, W), max_events_per_px=16)
+    ro = OE.group_events(ev, lens, (H, W), max_events_per_px=16)
+    for key in ("events", "time", "batch_id", "h", "w", "lengths"):
+        np.testing.assert_array_equal(_np(gr[key]), ro[key], err_msg=key)
+
+
 @pytest.mark.parametrize("thres,extra", [(20, 0), (0, 0), (3, 2), (600, 0)])
 def test_preprocess_one_call_vs_composed(dev, thres, extra):
     """ssla_preprocess_events (grouping, delays and truncation in one pass)
