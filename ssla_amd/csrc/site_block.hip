@@ -18,7 +18,10 @@
 // elements 8 (l / 16) .. + 7, one 16-byte piece), no LDS and no barriers;
 // the weights are small and shared by every workgroup (cache resident).
 // finish keeps a row's whole output in its wavefront, so LayerNorm reduces
-// over the 16 lanes of a lane group (xor shuffles) with no LDS either.
+// over the 16 lanes of a lane group (xor shuffles) with no LDS either; at
+// the step's four stage shapes it runs with both weight matrices resident
+// in LDS (site_finish_resident_kernel: staged once per workgroup, no
+// barrier per reduction step, the same sums in the same order).
 #include "common.h"
 
 namespace ssla {
@@ -267,6 +270,134 @@ __global__ __launch_bounds__(64 * kWaves) void site_finish_kernel(const uint16_t
 
 unsigned row_tiles(int64_t n) { return static_cast<unsigned>((n + kRows - 1) / kRows); }
 
+// site_finish with both weight matrices resident in LDS for the whole
+// launch (sizes fixed at compile time: the step's stage shapes).  A
+// workgroup of kResWaves wavefronts stages Wo [C, HD] and Wr [C, CIN] once
+// (rows padded by 8 elements, so the 16 lanes of an MFMA operand read
+// spread over the banks), then takes row tiles of 16 kResWaves events
+// blockIdx.x, blockIdx.x + gridDim.x, ... with no barrier between them:
+// each wavefront loads all of its 16 rows' o and x pieces at once, then
+// runs the same MFMA sequence and epilogue as site_finish_kernel (the same
+// sums in the same order: the same bits).
+constexpr int kResWaves = 8;
+constexpr int kResRows = 16 * kResWaves;
+template <int NT, int HD, int CIN, bool WR>
+__global__ __launch_bounds__(64 * kResWaves) void site_finish_resident_kernel(
+    const uint16_t *__restrict__ o, int64_t n, const uint16_t *__restrict__ wo, const float *__restrict__ x,
+    const uint16_t *__restrict__ wr, const float *__restrict__ ln_w, const float *__restrict__ ln_b, float eps,
+    float *__restrict__ y) {
+  constexpr int C = 16 * NT;
+  constexpr int PO = HD + 8, PR = CIN + 8;   // row pitches (elements)
+  __shared__ __align__(16) uint16_t wlo[C * PO];
+  __shared__ __align__(16) uint16_t wlr[WR ? C * PR : 8];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int r = lane & 15, kq = 8 * (lane >> 4);
+  for (int i = tid; i < C * (HD / 8); i += 64 * kResWaves) {
+    const int rw = i / (HD / 8), c8 = i - rw * (HD / 8);
+    *reinterpret_cast<uint4 *>(&wlo[rw * PO + 8 * c8]) = *reinterpret_cast<const uint4 *>(wo + rw * HD + 8 * c8);
+  }
+  if constexpr (WR) {
+    for (int i = tid; i < C * (CIN / 8); i += 64 * kResWaves) {
+      const int rw = i / (CIN / 8), c8 = i - rw * (CIN / 8);
+      *reinterpret_cast<uint4 *>(&wlr[rw * PR + 8 * c8]) = *reinterpret_cast<const uint4 *>(wr + rw * CIN + 8 * c8);
+    }
+  }
+  __syncthreads();
+  const int64_t n_tiles = (n + kResRows - 1) / kResRows;
+  for (int64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+    const int64_t e0 = tile * kResRows + 16 * wv;
+    if (e0 >= n) continue;   // wavefront-uniform; no barrier in the loop
+    const int64_t row = min(e0 + r, n - 1);
+    uint4 op[HD / 32];
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s) op[s] = *reinterpret_cast<const uint4 *>(o + row * HD + 32 * s + kq);
+    float4 xp[WR ? CIN / 32 : 1][2];
+    if constexpr (WR) {
+#pragma unroll
+      for (int s = 0; s < CIN / 32; ++s) {
+        xp[s][0] = *reinterpret_cast<const float4 *>(x + row * CIN + 32 * s + kq);
+        xp[s][1] = *reinterpret_cast<const float4 *>(x + row * CIN + 32 * s + kq + 4);
+      }
+    }
+    f32x4 acc[NT], res[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = res[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s) {
+      const bf16x8 a = __builtin_bit_cast(bf16x8, op[s]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            a, *reinterpret_cast<const bf16x8 *>(&wlo[(16 * t + r) * PO + 32 * s + kq]), acc[t], 0, 0, 0);
+    }
+    if constexpr (WR) {
+#pragma unroll
+      for (int s = 0; s < CIN / 32; ++s) {
+        const f32x8v xf = {xp[s][0].x, xp[s][0].y, xp[s][0].z, xp[s][0].w,
+                           xp[s][1].x, xp[s][1].y, xp[s][1].z, xp[s][1].w};
+        const bf16x8 a = __builtin_convertvector(xf, bf16x8);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          res[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              a, *reinterpret_cast<const bf16x8 *>(&wlr[(16 * t + r) * PR + 32 * s + kq]), res[t], 0, 0, 0);
+      }
+    }
+    float yv[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t ev = e0 + 4 * (lane >> 4) + i;
+        const float rv = WR ? round_bf16(res[t][i]) : (ev < n ? x[ev * CIN + 16 * t + r] : 0.f);
+        yv[t][i] = round_bf16(acc[t][i]) + rv;
+      }
+    float mean[4], rstd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sm = 0.f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) sm += yv[t][i];
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) sm += __shfl_xor(sm, m);
+      mean[i] = sm / static_cast<float>(C);
+      float d = 0.f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) d += (yv[t][i] - mean[i]) * (yv[t][i] - mean[i]);
+#pragma unroll
+      for (int m = 1; m < 16; m <<= 1) d += __shfl_xor(d, m);
+      rstd[i] = 1.f / sqrtf(d / static_cast<float>(C) + eps);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int col = 16 * t + r;
+      const float lw = ln_w[col], lb = ln_b[col];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t ev = e0 + 4 * (lane >> 4) + i;
+        if (ev < n) y[ev * C + col] = (yv[t][i] - mean[i]) * rstd[i] * lw + lb;
+      }
+    }
+  }
+}
+
+// Workgroups of the resident finish that fit the device at once (its LDS
+// decides), for a grid that covers every row tile in one round or less.
+template <int NT, int HD, int CIN, bool WR>
+unsigned resident_grid(int64_t n) {
+  static int per_cu = -1, cus = 0;
+  if (per_cu < 0) {
+    int dev = 0, b = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, site_finish_resident_kernel<NT, HD, CIN, WR>,
+                                                     64 * kResWaves, 0) != hipSuccess)
+      b = 1, cus = 256;
+    per_cu = std::max(b, 1);
+  }
+  const int64_t tiles = (n + kResRows - 1) / kResRows;
+  return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(tiles, static_cast<int64_t>(per_cu) * cus)));
+}
+
 }  // namespace
 }  // namespace ssla
 
@@ -321,6 +452,17 @@ extern "C" int ssla_site_finish(const uint16_t *o, int64_t n, int hd, const uint
   SSLA_CHECK_ARG(aligned(o, 16) && aligned(wo, 16) && aligned(x, 16) && (!wr || aligned(wr, 16)),
                  "site_finish: o, x and the weights must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // the step's stage shapes: weights resident in LDS
+#define SITE_FINISH_RES(NTV, HDV, CINV, WRV)                                                                      \
+  if (cout == 16 * NTV && hd == HDV && cin == CINV && (wr != nullptr) == WRV) {                                  \
+    hipLaunchKernelGGL((site_finish_resident_kernel<NTV, HDV, CINV, WRV>),                                      \
+                       dim3(resident_grid<NTV, HDV, CINV, WRV>(n)), dim3(64 * kResWaves), 0, st, o, n, wo, x, wr, \
+                       ln_w, ln_b, eps, y);                                                                      \
+    return launch_status("site_finish");                                                                         \
+  }
+  SITE_FINISH_RES(2, 128, 32, false) SITE_FINISH_RES(4, 128, 32, true) SITE_FINISH_RES(8, 128, 64, true)
+  SITE_FINISH_RES(16, 128, 128, true)
+#undef SITE_FINISH_RES
 #define SITE_FINISH(NTV)                                                                                           \
   if (cout == 16 * NTV) {                                                                                          \
     hipLaunchKernelGGL((site_finish_kernel<NTV>), dim3(row_tiles(n)), dim3(64 * kWaves), 0, st, o, n, hd, wo, x,   \
