@@ -75,14 +75,20 @@ __global__ __launch_bounds__(64 * kWaves) void site_project_kernel(const float *
   const int64_t srow = min(e0 + sr, n - 1);   // n > 0 (the launcher returns before)
   const float *xrow = x + srow * cin + sk;
   float4 xa = *reinterpret_cast<const float4 *>(xrow), xb = *reinterpret_cast<const float4 *>(xrow + 4);
+  // the weight pieces of a step are loaded with the step before's inputs
+  bf16x8 bn[NTO];
+#pragma unroll
+  for (int t = 0; t < NTO; ++t) bn[t] = bf16_piece(wb, 16 * t + r, cin, kq, true);
   for (int k0 = 0; k0 < cin; k0 += 32) {
     const f32x8v xf = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
     bf16x8 bv[NTO];
 #pragma unroll
-    for (int t = 0; t < NTO; ++t) bv[t] = bf16_piece(wb, 16 * t + r, cin, k0 + kq, true);
+    for (int t = 0; t < NTO; ++t) bv[t] = bn[t];
     if (k0 + 32 < cin) {
       xa = *reinterpret_cast<const float4 *>(xrow + k0 + 32);
       xb = *reinterpret_cast<const float4 *>(xrow + k0 + 36);
+#pragma unroll
+      for (int t = 0; t < NTO; ++t) bn[t] = bf16_piece(wb, 16 * t + r, cin, k0 + 32 + kq, true);
     }
     const bf16x8 xv = __builtin_convertvector(xf, bf16x8);
     __syncthreads();   // the previous step's reads of xs are done
