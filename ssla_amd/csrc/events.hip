@@ -793,6 +793,125 @@ __global__ void rf_fields(const int64_t *__restrict__ act, const int64_t *__rest
   }
 }
 
+// rf_count_lanes, the prefix sum of the packed pairs and rf_unpack_fields
+// in one launch (A divides 64; the packed path): workgroups take tickets in
+// field order, count their 256 / A fields (one lane per (field, position),
+// sums by shuffles), publish the packed total of their fields and find the
+// total before them by decoupled look-back (lb_excl_scan's flag words, whose
+// state the plan's set-up kernel clears), then write every field's act_pre /
+// ev_pre and the compacted index and count of its active fields; the last
+// workgroup writes the totals (counts[0], counts[1]).
+__global__ __launch_bounds__(256) void rf_count_scan(const int64_t *__restrict__ lut, int64_t n_rf, int A, int B,
+                                                     int H, int W, const int32_t *__restrict__ pixmap,
+                                                     const int64_t *__restrict__ glen, int64_t *__restrict__ nev,
+                                                     int64_t *__restrict__ act, int64_t *__restrict__ act_pre,
+                                                     int64_t *__restrict__ ev_pre, int64_t *__restrict__ f_index,
+                                                     int64_t *__restrict__ f_len, int64_t *__restrict__ counts,
+                                                     uint64_t *state) {
+  constexpr int64_t mask = (int64_t{1} << kPackBits) - 1;
+  __shared__ int64_t s_tile, s_excl;
+  __shared__ int64_t s_pk[256];   // packed pair of each of the workgroup's fields
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid == 0) s_tile = static_cast<int64_t>(atomicAdd(reinterpret_cast<unsigned long long *>(state), 1ull));
+  __syncthreads();
+  const int64_t tile = s_tile;
+  uint64_t *flags = state + 1;
+  const int fpw = 256 / A;   // fields per workgroup
+  const int64_t n_f = static_cast<int64_t>(B) * n_rf;
+  const int64_t t = tile * 256 + tid;
+  const int64_t f = t / A;
+  const int a = static_cast<int>(t - f * A);
+  int64_t n = 0, on = 0;
+  if (f < n_f) {
+    const int64_t b = f / n_rf, r = f - b * n_rf;
+    const int64_t p = lut[r * A + a];
+    const int32_t g = p >= 0 ? pixmap[b * H * W + p] : -1;
+    if (g >= 0) {
+      n = glen[g];
+      on = 1;
+    }
+  }
+  for (int d = 1; d < A; d <<= 1) {
+    n += __shfl_xor(n, d, 64);
+    on |= __shfl_xor(on, d, 64);
+  }
+  const int fi = tid / A;   // field of this lane within the workgroup
+  if (a == 0) s_pk[fi] = f < n_f ? (n << kPackBits) | on : 0;
+  __syncthreads();
+  if (tid < 64) {
+    // exclusive prefix of the workgroup's fields (fpw <= 256: four per lane)
+    int64_t v[4], sum = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = 4 * lane + u;
+      v[u] = i < fpw ? s_pk[i] : 0;
+      sum += v[u];
+    }
+    int64_t x = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int64_t y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    const int64_t agg = __shfl(x, 63, 64);
+    int64_t run = x - sum;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = 4 * lane + u;
+      if (i < fpw) s_pk[i] = run;   // now the exclusive prefix within the workgroup
+      run += v[u];
+    }
+    int64_t ex = 0;
+    if (tile > 0) {
+      if (lane == 0)
+        __hip_atomic_store(&flags[tile], kLbAgg | (static_cast<uint64_t>(agg) & kLbMask), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      int64_t j_end = tile;
+      while (true) {
+        const int64_t j = j_end - 1 - lane;
+        const uint64_t fw = j >= 0 ? __hip_atomic_load(&flags[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : kLbIncl;
+        const uint64_t st = fw >> 62;
+        const uint64_t incl = __builtin_amdgcn_ballot_w64(st == 2);
+        const uint64_t none = __builtin_amdgcn_ballot_w64(st == 0);
+        const int last = incl ? __builtin_ctzll(incl) : 63;
+        const uint64_t need = last == 63 ? ~0ull : ((2ull << last) - 1);
+        if (none & need) {
+          __builtin_amdgcn_s_sleep(1);
+          continue;
+        }
+        int64_t val = lane <= last ? lb_value(fw) : 0;
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) val += __shfl_xor(val, d, 64);
+        ex += val;
+        if (incl) break;
+        j_end -= 64;
+      }
+    }
+    if (lane == 0) {
+      __hip_atomic_store(&flags[tile], kLbIncl | (static_cast<uint64_t>(ex + agg) & kLbMask), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      s_excl = ex;
+      if (tile == static_cast<int64_t>(gridDim.x) - 1) {
+        counts[0] = (ex + agg) & mask;
+        counts[1] = (ex + agg) >> kPackBits;
+      }
+    }
+  }
+  __syncthreads();
+  if (a == 0 && f < n_f) {
+    const int64_t pre = s_excl + s_pk[fi];
+    nev[f] = n;
+    act[f] = on;
+    act_pre[f] = pre & mask;
+    ev_pre[f] = pre >> kPackBits;
+    if (on) {
+      f_index[pre & mask] = f;
+      f_len[pre & mask] = n;
+    }
+  }
+}
+
 // o_fidx (optional): the active-field index of every row, the high part of
 // its sorted key (active index * t_stride + time).
 __global__ void rf_emit(const int32_t *__restrict__ perm, int64_t E_out, const int64_t *__restrict__ pre_src,
@@ -1489,7 +1608,7 @@ struct RfWs {
   // look-back scan states (zeroed by the plan's set-up kernel): the group
   // starts' scan (lb_state_words(G)) and the segment heads' scan of the
   // pooling plan (lb_state_words(E_cap)), contiguous
-  uint64_t *lb_g, *lb_e;
+  uint64_t *lb_g, *lb_e, *lb_c;
   int64_t lb_words;
   void *tmp;
   size_t tmp_bytes, total;
@@ -1516,9 +1635,11 @@ RfWs rf_layout(void *ws, int64_t G, int64_t n_pix, int64_t n_f, int64_t E_cap) {
   L.skey = c.take<uint64_t>(E_cap);
   L.val = c.take<int32_t>(E_cap);
   L.perm = c.take<int32_t>(E_cap);
-  L.lb_words = lb_state_words(G) + lb_state_words(E_cap);
+  // (and the fused field count's: one flag per 256 (field, position) lanes)
+  L.lb_words = lb_state_words(G) + lb_state_words(E_cap) + 2 + (n_f * 64 + 255) / 256;
   L.lb_g = c.take<uint64_t>(L.lb_words);
   L.lb_e = L.lb_g ? L.lb_g + lb_state_words(G) : nullptr;
+  L.lb_c = L.lb_e ? L.lb_e + lb_state_words(E_cap) : nullptr;
   L.tmp_bytes = std::max(sort_temp_bytes(E_cap), scan_temp_bytes(std::max(n_f, G + 1)));
   L.tmp = c.take<char>(L.tmp_bytes);
   L.total = c.off;
@@ -1576,14 +1697,21 @@ int rf_plan_impl(const int64_t *gr_batch, const int64_t *gr_h, const int64_t *gr
   // one prefix sum of the packed (events, active) pairs while the active
   // count fits 21 bits
   const bool packed = n_f < (int64_t{1} << kPackBits);
-  if (64 % A == 0 && n_f * A <= (int64_t{1} << 28))
+  const bool lanes = 64 % A == 0 && n_f * A <= (int64_t{1} << 28);
+  if (packed && lanes && n_f > 0) {   // count, prefix and compaction in one launch
+    hipLaunchKernelGGL(rf_count_scan, dim3(static_cast<unsigned>((n_f * A + 255) / 256)), dim3(256), 0, st, lut, n_rf,
+                       A, B, H, W, L.pixmap, gr_len, L.nev, L.act, L.act_pre, L.ev_pre, L.f_index, L.f_len, L.counts,
+                       L.lb_c);
+  } else if (lanes)
     hipLaunchKernelGGL(rf_count_lanes, dim3(static_cast<unsigned>((n_f * A + kThreads - 1) / kThreads)),
                        dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap, gr_len, L.nev, L.act,
                        packed ? L.pk : nullptr);
   else
     hipLaunchKernelGGL(rf_count, dim3(grid_for(n_f)), dim3(kThreads), 0, st, lut, n_rf, A, B, H, W, L.pixmap, gr_len,
                        L.nev, L.act, packed ? L.pk : nullptr);
-  if (packed) {
+  if (packed && lanes && n_f > 0) {
+    // done above
+  } else if (packed) {
     s = excl_scan(L.tmp, L.tmp_bytes, L.pk, L.pk_pre, n_f, st);
     if (s) return s;
     hipLaunchKernelGGL(rf_unpack_fields, dim3(grid_for(n_f)), dim3(kThreads), 0, st, L.pk_pre, L.pk, n_f, L.act_pre,
