@@ -188,7 +188,7 @@ int ssla_gla_chunk_bwd(const void *q, const void *k, const void *v,
  * segment's local end state and decay, then one that folds them into every
  * segment's entering state (fp32 throughout) -- instead of one wavefront
  * walking the whole sequence.  The size query returns 0 for shapes where
- * the single pass is as fast (sequences shorter than 32 steps on average)
+ * the single pass is faster (sequences shorter than 64 steps on average)
  * or not available (K not a multiple of 16 up to 64); then pass NULL, 0. */
 size_t ssla_gla_recurrent_workspace_size(int n_seq, int64_t T, int H, int K, int V);
 int ssla_gla_recurrent_fwd(const void *q, const void *k, const void *v,

@@ -124,10 +124,29 @@ __device__ __forceinline__ void wave_lds_sync() {
 //   steps writing o, and the last segment writes ht.  Multi-segment
 //   sequences read h0 from the copy, so an in-place update (ht == h0) never
 //   races with a segment that has not read it yet.
-constexpr int kSegSteps = 128;   // the longest segment
-constexpr int kSegStepsMin = 32;
-constexpr int64_t kSegUnits = 8192;   // wavefront units the segment length aims at (8 per SIMD)
-constexpr int64_t kSegFoldMax = 8;    // average segments per sequence at most, when halving
+#ifndef SSLA_REC_SEG_STEPS
+#define SSLA_REC_SEG_STEPS 128
+#endif
+#ifndef SSLA_REC_SEG_MIN
+#define SSLA_REC_SEG_MIN 32
+#endif
+#ifndef SSLA_REC_SEG_UNITS
+#define SSLA_REC_SEG_UNITS 8192
+#endif
+#ifndef SSLA_REC_SEG_FOLD
+#define SSLA_REC_SEG_FOLD 8
+#endif
+constexpr int kSegSteps = SSLA_REC_SEG_STEPS;   // the longest segment
+constexpr int kSegStepsMin = SSLA_REC_SEG_MIN;
+constexpr int64_t kSegUnits = SSLA_REC_SEG_UNITS;   // wavefront units the segment length aims at (8 per SIMD)
+constexpr int64_t kSegFoldMax = SSLA_REC_SEG_FOLD;  // average segments per sequence at most, when halving
+#ifndef SSLA_REC_SEG_AVG
+#define SSLA_REC_SEG_AVG (SSLA_REC_SEG_STEPS / 2)
+#endif
+// average steps per sequence below which one pass runs: at the C5 step's
+// stage 2 (1,140 sites, 44 events each on average) one pass takes 83-87 µs,
+// segments of up to 128 (or 64) steps 102-103 (89-91)
+constexpr int64_t kSegAvgMin = SSLA_REC_SEG_AVG;
 enum { kPlain = 0, kSegState = 1, kSegOut = 2 };
 
 struct SegWs {
@@ -600,8 +619,8 @@ __global__ __launch_bounds__(256) void gla_recurrent_kernel(
 }
 
 // Workspace of the segmented schedule (0: not used for this shape -- K
-// outside the staged kernels, or sequences of fewer than kSegSteps / 4
-// steps on average, where one pass is as fast).
+// outside the staged kernels, or sequences of fewer than kSegAvgMin steps
+// on average, where one pass is faster).
 struct SegLayout {
   size_t segoff, segmap, slot, prod, h0c, total;
   int64_t n_segs_max;
@@ -613,7 +632,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 inline SegLayout seg_layout(int n_seq, int64_t T, int H, int K, int V) {
   SegLayout L{};
   if (n_seq <= 0 || T <= 0 || K % 16 != 0 || K > 64 || V <= 0) return L;
-  if (T < static_cast<int64_t>(n_seq) * (kSegSteps / 4)) return L;
+  if (T < static_cast<int64_t>(n_seq) * kSegAvgMin) return L;
   // halve the segments (down to kSegStepsMin steps) while the grid holds
   // fewer than kSegUnits wavefronts -- shorter serial walks, more of them --
   // and sequences keep at most kSegFoldMax segments on average: segment s
