@@ -23,7 +23,7 @@
 //   a bad index.  At C4 there are ~2,000 range edges and most rows end
 //   inside their range, so the link is a small pass.
 //
-// Unsorted index:   hist -> scan -> bucket -> bucket_reduce -> bucket_finalize
+// Unsorted index:   hist -> scan -> bucket -> bucket_reduce
 // * hist  : LDS histogram of buckets of 64 consecutive rows per event range
 //           (a few hundred buckets, so the histogram is small and the
 //           workgroups many).
@@ -41,9 +41,10 @@
 //           inverted event id) key, so the result does not depend on the
 //           order the events arrive in; mean: ds_add_f64 and a row count).
 //           A bucket of one chunk is written out directly; the chunks of a
-//           larger bucket leave their tile.
-// * bucket_finalize: one workgroup per multi-chunk bucket folds its chunks'
-//           tiles and writes the rows.
+//           larger bucket leave their tiles (device-scope stores) and count
+//           themselves in on a per-bucket counter that hist cleared, and
+//           the last to arrive folds the others' tiles into its own and
+//           writes the rows (no spin: nothing ever waits on another chunk).
 // Max/argmax select (value, smallest event id), NaN never wins, -0.0 ties
 // +0.0 and out keeps the sign of the winner's zero: bit-exact and
 // deterministic on both paths.  Mean sums in fp64 and rounds once (the
@@ -72,7 +73,7 @@ constexpr int kChunk = SSLA_SR_CHUNK;              // events per bucket_reduce w
 #ifndef SSLA_SR_REDW
 #define SSLA_SR_REDW 16
 #endif
-constexpr int kRedWaves = SSLA_SR_REDW;            // bucket_reduce / finalize wavefronts
+constexpr int kRedWaves = SSLA_SR_REDW;            // bucket_reduce wavefronts
 #ifndef SSLA_SR_RWAVES
 #define SSLA_SR_RWAVES 8
 #endif
@@ -87,7 +88,7 @@ inline int64_t n_ranges(int64_t E) { return std::max<int64_t>(1, (E + kRange - 1
 inline int64_t n_chunks_max(int64_t E, int64_t NB) { return NB + (E + kChunk - 1) / kChunk; }
 
 struct WsLayout {
-  size_t status, errs, off, coff, cdesc, flags, hist, perm, parts, pcnt, rflags, rpieces, total;
+  size_t status, errs, off, coff, cdesc, flags, hist, perm, parts, pcnt, arrive, rflags, rpieces, total;
   int n_hist;
   int64_t NB, n_chunks, n_rseg;
 };
@@ -130,6 +131,8 @@ inline WsLayout ws_layout(int64_t E, int C, int64_t n_out) {
   // per chunk: 64 row counts
   L.parts = p; p = align256(p + sizeof(uint64_t) * static_cast<size_t>(L.n_chunks) * ncb * 64 * 64);
   L.pcnt = p;  p = align256(p + sizeof(int32_t) * static_cast<size_t>(L.n_chunks) * 64);
+  // per (bucket, channel block): chunks of the bucket that have left their tile
+  L.arrive = p; p = align256(p + sizeof(int32_t) * static_cast<size_t>(L.NB) * ncb);
   // per (range, channel block): tail flag and head count, tail and head pieces
   L.rflags = p; p = align256(p + sizeof(uint64_t) * 2 * static_cast<size_t>(L.n_rseg));
   L.rpieces = p; p = align256(p + sizeof(uint64_t) * 2 * 64 * static_cast<size_t>(L.n_rseg));
@@ -146,13 +149,16 @@ __device__ __forceinline__ void event_range(int64_t E, int n_hist, int b, int64_
   e1 = min(E, e0 + per);
 }
 
-// Clears the scan ticket and look-back flags (kernel 1 of the unsorted
-// pipeline).
-__device__ __forceinline__ void clear_scan_state(int32_t *ticket, uint64_t *flags, int64_t n_flags) {
+// Clears the scan ticket, the look-back flags and the chunk arrival
+// counters (kernel 1 of the unsorted pipeline).
+__device__ __forceinline__ void clear_scan_state(int32_t *ticket, uint64_t *flags, int64_t n_flags,
+                                                 int32_t *arrive, int64_t n_arrive) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *ticket = 0;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_flags; i += stride)
     flags[i] = 0;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_arrive; i += stride)
+    arrive[i] = 0;
 }
 
 // 64-bit value of lane k (a scalar)
@@ -170,8 +176,8 @@ template <bool LDS>
 __global__ __launch_bounds__(kEvThreads) void hist_kernel(
     const int64_t *__restrict__ index, int64_t E, int64_t n_out, int64_t NB, int n_hist,
     int32_t *__restrict__ hist, int32_t *__restrict__ errs, int32_t *ticket, uint64_t *flags,
-    int64_t n_flags) {
-  clear_scan_state(ticket, flags, n_flags);
+    int64_t n_flags, int32_t *arrive, int64_t n_arrive) {
+  clear_scan_state(ticket, flags, n_flags, arrive, n_arrive);
   bool bad = false;
   if constexpr (LDS) {
     __shared__ int32_t lh[kLdsBuckets];
@@ -800,9 +806,11 @@ template <bool MEAN, int CT>
 __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
     const float *__restrict__ src, const int2 *__restrict__ perm, const int4 *__restrict__ cdesc,
     const int32_t *__restrict__ coff, int32_t NB, int32_t E, int C, int32_t n_out, float *__restrict__ out,
-    int64_t *__restrict__ argmax, uint64_t *__restrict__ parts, int32_t *__restrict__ pcnt) {
+    int64_t *__restrict__ argmax, uint64_t *__restrict__ parts, int32_t *__restrict__ pcnt,
+    int32_t *__restrict__ arrive) {
   __shared__ uint64_t tile[kBucketRows][64];   // max keys, or fp64 sums
   __shared__ int32_t tcnt[kBucketRows];
+  __shared__ int32_t s_last;
   const int Cc = CT ? CT : C;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -858,65 +866,55 @@ __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
     }
   }
   __syncthreads();
-  if (nch == 1) {   // the whole bucket: write its rows
-    for (int rr = w; rr < kBucketRows; rr += kRedWaves) {
-      const int row = row0 + rr;
-      if (row >= n_out || !act) continue;
-      const uint64_t v = tile[rr][lane];
-      const int64_t o = static_cast<int64_t>(row) * Cc + col;
-      if constexpr (MEAN) {
-        const int32_t n = tcnt[rr];
-        out[o] = n > 0 ? static_cast<float>(__longlong_as_double(static_cast<long long>(v)) / n) : 0.f;
-      } else {
-        float x = 0.f;
-        int64_t e = E;
-        if (v != 0ull) key_value(v, x, e);
-        out[o] = x;
-        argmax[o] = e;
-      }
-    }
-  } else {          // one chunk of a larger bucket: leave the tile
+  if (nch > 1) {
+    // One chunk of a larger bucket: leave the tile, written through to
+    // device scope (relaxed agent-scope stores), then count this chunk in.
+    // The bucket's last chunk to arrive -- on whichever XCD -- folds the
+    // others' tiles into its own and writes the rows; the stores are
+    // complete before the count, so it reads them all.
     uint64_t *pt = parts + (static_cast<int64_t>(c) * ncb + cb) * (kBucketRows * 64);
-    for (int rr = w; rr < kBucketRows; rr += kRedWaves) pt[rr * 64 + lane] = tile[rr][lane];
-    if (cb == 0 && threadIdx.x < kBucketRows) pcnt[static_cast<int64_t>(c) * kBucketRows + threadIdx.x] = tcnt[threadIdx.x];
+    for (int rr = w; rr < kBucketRows; rr += kRedWaves)
+      __hip_atomic_store(&pt[rr * 64 + lane], tile[rr][lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (MEAN && cb == 0 && threadIdx.x < kBucketRows)
+      __hip_atomic_store(&pcnt[static_cast<int64_t>(c) * kBucketRows + threadIdx.x], tcnt[threadIdx.x],
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this thread's stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(&arrive[static_cast<int64_t>(b) * ncb + cb], 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == nch - 1;
+    __syncthreads();
+    if (!s_last) return;   // workgroup-uniform
   }
-}
-
-// One workgroup per (bucket, channel block) of a multi-chunk bucket: folds
-// the chunks' tiles (keys by max, sums in chunk order) and writes the rows.
-template <bool MEAN>
-__global__ __launch_bounds__(64 * kRedWaves) void bucket_finalize_kernel(
-    const int32_t *__restrict__ coff, int64_t NB, int64_t E, int C, int64_t n_out, float *__restrict__ out,
-    int64_t *__restrict__ argmax, const uint64_t *__restrict__ parts, const int32_t *__restrict__ pcnt) {
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int ncb = (C + 63) / 64;
-  const int64_t b = blockIdx.x / ncb;
-  const int cb = static_cast<int>(blockIdx.x - b * ncb);
-  if (b >= NB) return;
-  const int64_t c0 = coff[b], c1 = coff[b + 1];
-  if (c1 - c0 <= 1) return;   // written by bucket_reduce
-  const int64_t row0 = b << kBucketShift;
-  const int col = cb * 64 + lane;
-  if (col >= C) return;
+  // Write the bucket's rows: this chunk's tile, folded (for a bucket of
+  // several chunks) with the other chunks' tiles in chunk order.
+  const int c0 = nch > 1 ? coff[b] : c;
   for (int rr = w; rr < kBucketRows; rr += kRedWaves) {
-    const int64_t row = row0 + rr;
-    if (row >= n_out) break;
-    uint64_t key = 0ull;
+    const int row = row0 + rr;
+    if (row >= n_out || !act) continue;
+    uint64_t key = MEAN ? 0ull : tile[rr][lane];
     double sum = 0.0;
     int64_t n = 0;
-    for (int64_t cc = c0; cc < c1; cc += 4) {   // four tiles' loads in flight
+    for (int cc = c0; cc < c0 + nch; cc += 4) {   // four tiles' loads in flight
       uint64_t v[4];
       int32_t k[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t ch = min(cc + u, c1 - 1);
-        v[u] = parts[(ch * ncb + cb) * (kBucketRows * 64) + rr * 64 + lane];
-        k[u] = MEAN ? pcnt[ch * kBucketRows + rr] : 0;
+        const int ch = min(cc + u, c0 + nch - 1);
+        if (ch == c) {
+          v[u] = tile[rr][lane];
+          k[u] = MEAN ? tcnt[rr] : 0;
+        } else {
+          v[u] = __hip_atomic_load(&parts[(static_cast<int64_t>(ch) * ncb + cb) * (kBucketRows * 64) + rr * 64 + lane],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          k[u] = MEAN ? __hip_atomic_load(&pcnt[static_cast<int64_t>(ch) * kBucketRows + rr], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT)
+                      : 0;
+        }
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (cc + u < c1) {
+        if (cc + u < c0 + nch) {
           if constexpr (MEAN) {
             sum += __longlong_as_double(static_cast<long long>(v[u]));
             n += k[u];
@@ -926,14 +924,15 @@ __global__ __launch_bounds__(64 * kRedWaves) void bucket_finalize_kernel(
         }
       }
     }
+    const int64_t o = static_cast<int64_t>(row) * Cc + col;
     if constexpr (MEAN) {
-      out[row * C + col] = n > 0 ? static_cast<float>(sum / static_cast<double>(n)) : 0.f;
+      out[o] = n > 0 ? static_cast<float>(sum / static_cast<double>(n)) : 0.f;
     } else {
       float x = 0.f;
       int64_t e = E;
       if (key != 0ull) key_value(key, x, e);
-      out[row * C + col] = x;
-      argmax[row * C + col] = e;
+      out[o] = x;
+      argmax[o] = e;
     }
   }
 }
@@ -997,6 +996,7 @@ int run_scatter(const float *src, const int64_t *index, int64_t E, int C, int64_
   int2 *perm = reinterpret_cast<int2 *>(base + L.perm);
   uint64_t *parts = reinterpret_cast<uint64_t *>(base + L.parts);
   int32_t *pcnt = reinterpret_cast<int32_t *>(base + L.pcnt);
+  int32_t *arrive = reinterpret_cast<int32_t *>(base + L.arrive);
   const int64_t NB = L.NB;
   const int64_t n_scan = scan_blocks(NB);
   const bool lds = lds_hist(NB);
@@ -1005,14 +1005,14 @@ int run_scatter(const float *src, const int64_t *index, int64_t E, int C, int64_
   int n_err = 0;
   if (lds) {
     hipLaunchKernelGGL((hist_kernel<true>), dim3(L.n_hist), dim3(kEvThreads), 0, st, index, E, n_out, NB, L.n_hist,
-                       hist, errs, ticket, flags, n_scan + 1);
+                       hist, errs, ticket, flags, n_scan + 1, arrive, NB * ncb);
     n_err = L.n_hist;
   } else {
     hipLaunchKernelGGL(fill_i32, dim3(static_cast<unsigned>(std::min<int64_t>(1024, (NB + 256) / 256))), dim3(256),
                        0, st, hist, NB + 1, 0);
     const int nb = global_hist_blocks(E);
     hipLaunchKernelGGL((hist_kernel<false>), dim3(nb), dim3(kEvThreads), 0, st, index, E, n_out, NB, 1, hist, errs,
-                       ticket, flags, n_scan + 1);
+                       ticket, flags, n_scan + 1, arrive, NB * ncb);
     n_err = nb;
   }
   hipLaunchKernelGGL(scan_kernel, dim3(static_cast<unsigned>(n_scan)), dim3(kScanCells * kScanTpc), 0, st, hist,
@@ -1030,14 +1030,12 @@ int run_scatter(const float *src, const int64_t *index, int64_t E, int C, int64_
     if (C == 64)
       hipLaunchKernelGGL((bucket_reduce_kernel<MEAN, 64>), dim3(static_cast<unsigned>(L.n_chunks * ncb)),
                          dim3(64 * kRedWaves), 0, st, src, perm, cdesc, coff, NB32, E32, C, n32, out, argmax, parts,
-                         pcnt);
+                         pcnt, arrive);
     else
       hipLaunchKernelGGL((bucket_reduce_kernel<MEAN, 0>), dim3(static_cast<unsigned>(L.n_chunks * ncb)),
                          dim3(64 * kRedWaves), 0, st, src, perm, cdesc, coff, NB32, E32, C, n32, out, argmax, parts,
-                         pcnt);
+                         pcnt, arrive);
   }
-  hipLaunchKernelGGL(bucket_finalize_kernel<MEAN>, dim3(static_cast<unsigned>(NB * ncb)), dim3(64 * kRedWaves), 0,
-                     st, coff, NB, E, C, n_out, out, argmax, parts, pcnt);
   return launch_status(name);
 }
 
