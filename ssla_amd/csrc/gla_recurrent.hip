@@ -13,6 +13,12 @@
 namespace ssla {
 namespace {
 
+#ifndef SSLA_GR_WPB
+#define SSLA_GR_WPB 4
+#endif
+// wavefronts (units) per workgroup of the staged recurrence kernels
+constexpr int kRecWaves = SSLA_GR_WPB;
+
 constexpr int kBV = 16;   // value columns per wavefront
 constexpr int kKG = 4;    // key groups per wavefront (64 / kBV)
 
@@ -260,7 +266,7 @@ struct Unit {
 };
 
 template <int DT, int GDT, int KPL, int MODE>
-__global__ __launch_bounds__(256, KPL <= 8 ? 4 : 3) void gla_recurrent_staged_kernel(
+__global__ __launch_bounds__(64 * kRecWaves, (KPL <= 8 ? 4 : 3) * 4 / kRecWaves) void gla_recurrent_staged_kernel(
     const void *__restrict__ q, const void *__restrict__ k,
     const void *__restrict__ v, const void *__restrict__ g,
     const int64_t *__restrict__ cu_seqlens, int n_seq, int H, int V,
@@ -269,7 +275,7 @@ __global__ __launch_bounds__(256, KPL <= 8 ? 4 : 3) void gla_recurrent_staged_ke
     int64_t T, int32_t *__restrict__ status, SegWs sw) {
   typedef Staged<DT, GDT, KPL> G;
   constexpr int K = G::K;
-  __shared__ __align__(16) unsigned char smem[4][G::BYTES];
+  __shared__ __align__(16) unsigned char smem[kRecWaves][G::BYTES];
   const int lane = threadIdx.x & 63;
   // wavefront-uniform (SGPR): the unit indexing below runs on the scalar unit
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -435,7 +441,7 @@ __global__ __launch_bounds__(256, KPL <= 8 ? 4 : 3) void gla_recurrent_staged_ke
     }
   };
 
-  const Unit cur = unit_at(static_cast<int>(blockIdx.x) * 4 + wv);
+  const Unit cur = unit_at(static_cast<int>(blockIdx.x) * kRecWaves + wv);
   if (cur.bad && MODE != kSegState)
     skip_sequence<DT>(o, cur.bos, cur.eos, H, cur.h, V, col_of(cur), kg == 0 && col_of(cur) < V, lane, status);
   if (!cur.run) return;   // whole wavefront exits (no workgroup barrier)
@@ -666,7 +672,7 @@ int launch_recurrent(const void *q, const void *k, const void *v, const void *g,
   const int n_vt = (V + kBV - 1) / kBV;
   const int64_t items = static_cast<int64_t>(n_seq) * H * n_vt;
   if (items == 0) return SSLA_OK;
-  const int waves_per_block = 4;
+  const int waves_per_block = kRecWaves;
   const int64_t blocks = (items + waves_per_block - 1) / waves_per_block;
   if (blocks > 0x7fffffff) {
     set_error("gla_recurrent_fwd: too many (sequence, head, tile) items");

@@ -777,9 +777,23 @@ __global__ __launch_bounds__(64 * kLinkWaves) void seg_link_kernel(int64_t E, in
   a.reset();
   a.merge(tails[q * 64 + lane]);
   int64_t cnt = seg_count(f);
-  for (int64_t m = rg + 1; m < te; ++m) {
-    a.merge(tails[(m * ncb + cb) * 64 + lane]);
-    cnt += seg_count(rflags[m * ncb + cb]);
+  // the ranges the row runs through, eight pieces in flight per round trip
+  // (folded in range order)
+  for (int64_t m0 = rg + 1; m0 < te; m0 += 8) {
+    uint64_t pc[8], fc[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t m = min(m0 + u, te - 1);
+      pc[u] = tails[(m * ncb + cb) * 64 + lane];
+      fc[u] = rflags[m * ncb + cb];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (m0 + u < te) {
+        a.merge(pc[u]);
+        cnt += seg_count(fc[u]);
+      }
+    }
   }
   if (te > rg) {
     a.merge(heads[(te * ncb + cb) * 64 + lane]);

@@ -21,8 +21,14 @@
 // updating one state tile.
 #include "common.h"
 
+#ifndef SSLA_SS_WPB
+#define SSLA_SS_WPB 1
+#endif
+
 namespace ssla {
 namespace {
+
+constexpr int kStepWaves = SSLA_SS_WPB;   // wavefronts ((site, head) items) per workgroup
 
 // Sum over the lanes l, l ^ VL, l ^ 2 VL, ... (the row groups that hold one
 // float4 column): rotations inside each 16-lane DPP row (by 8, then by 4:
@@ -45,7 +51,7 @@ __device__ __forceinline__ float sum_row_groups(float x) {
 }
 
 template <int K, int V>
-__global__ __launch_bounds__(256) void sparse_gla_step_kernel(
+__global__ __launch_bounds__(64 * kStepWaves) void sparse_gla_step_kernel(
     const int32_t *__restrict__ site_idx, int n_active, const float *__restrict__ q,
     const float *__restrict__ k, const float *__restrict__ v, const float *__restrict__ g,
     float *__restrict__ state, int n_sites, int H, float scale, float *__restrict__ o,
@@ -57,7 +63,7 @@ __global__ __launch_bounds__(256) void sparse_gla_step_kernel(
   const int lane = threadIdx.x & 63;
   // wavefront-uniform: the (site, head) indexing runs on the scalar unit
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int item = static_cast<int>(blockIdx.x) * 4 + wv;   // n_active * H < 2^31 (host check)
+  const int item = static_cast<int>(blockIdx.x) * kStepWaves + wv;   // n_active * H < 2^31 (host check)
   if (item >= n_active * H) return;
   const int i = item / H;
   const int h = item % H;
@@ -129,9 +135,9 @@ extern "C" int ssla_sparse_gla_step(const int32_t *site_idx, int n_active, const
                  "sparse_gla_step: tensors must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t items = static_cast<int64_t>(n_active) * H;
-  const int64_t blocks = (items + 3) / 4;
+  const int64_t blocks = (items + kStepWaves - 1) / kStepWaves;
   SSLA_CHECK_ARG(items <= 0x7fffffff, "sparse_gla_step: too many active sites");
-  dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  dim3 grid(static_cast<unsigned>(blocks)), block(64 * kStepWaves);
 #define SSLA_STEP(KK, VV)                                                                       \
   if (K == KK && V == VV) {                                                                     \
     hipLaunchKernelGGL((sparse_gla_step_kernel<KK, VV>), grid, block, 0, st, site_idx, n_active, \
