@@ -449,6 +449,18 @@ __device__ __forceinline__ uint64_t max_key(float x, int32_t e) {
   const uint64_t key = (static_cast<uint64_t>(ord) << 32) | lo;
   return (x != x) ? 0ull : key;
 }
+// The same key with its event part precomputed (lo_base = (0x7fffffff - e)
+// << 1, a wavefront-uniform value the scalar unit forms) and no NaN test:
+// the caller leaves NaN values out (their key would be 0, which never
+// changes a maximum).  Bit-identical to max_key for every other x.
+__device__ __forceinline__ uint64_t max_key_part(float x, uint32_t lo_base) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t u0 = x != 0.f ? u : 0u;   // -0 folded onto +0
+  const uint32_t m = static_cast<uint32_t>(static_cast<int32_t>(u0) >> 31);
+  const uint32_t ord = u0 ^ (m | 0x80000000u);   // negative: ~u0, else u0 | sign bit
+  const uint32_t lo = lo_base | ((u ^ u0) >> 31);   // the low bit: x was -0
+  return (static_cast<uint64_t>(ord) << 32) | lo;
+}
 // (value, event) of a key != 0
 __device__ __forceinline__ void key_value(uint64_t key, float &x, int64_t &e) {
   const uint32_t ord = static_cast<uint32_t>(key >> 32);
@@ -846,7 +858,10 @@ __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
   const int col = cb * 64 + lane;
   const bool act = CT ? true : col < C;
   // this lane's channel (lanes past C re-read the last one, unused)
-  const float *pc = src + (CT ? col : min(col, Cc - 1));
+  const uint32_t colc = static_cast<uint32_t>(CT ? col : min(col, Cc - 1));
+  // rows through a buffer resource over src when its bytes fit 31-bit offsets
+  const bool rows32 = static_cast<int64_t>(E) * Cc * 4 < 0x7fffffff;
+  const __amdgpu_buffer_rsrc_t rs_rows = make_rsrc(src, static_cast<int64_t>(E) * Cc * 4);
   // the (event, row) pairs of this wavefront's next batch are loaded while
   // the current batch's rows are in flight
   int s = p0 + w * kRedBatch;
@@ -858,10 +873,18 @@ __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
     const int32_t ev = min(max(pr.x, 0), E - 1);
     const int32_t rl = (pr.y - row0) & (kBucketRows - 1);
     float xr[kRedBatch];
+    // event ids are wavefront-uniform (read lane by lane): the row offset
+    // goes in the scalar offset field, with no address arithmetic per lane
+    if (rows32) {
 #pragma unroll
-    for (int e = 0; e < kRedBatch; ++e) {
-      const int32_t id = __builtin_amdgcn_readlane(ev, e);   // uniform: the row address is scalar
-      xr[e] = pc[static_cast<int64_t>(id) * Cc];
+      for (int e = 0; e < kRedBatch; ++e)
+        xr[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            rs_rows, colc * 4u,
+            static_cast<uint32_t>(__builtin_amdgcn_readlane(ev, e)) * static_cast<uint32_t>(Cc * 4), 0));
+    } else {
+#pragma unroll
+      for (int e = 0; e < kRedBatch; ++e)
+        xr[e] = src[static_cast<int64_t>(__builtin_amdgcn_readlane(ev, e)) * Cc + colc];
     }
     pr_next = (sn < p1 && lane < min(kRedBatch, p1 - sn)) ? perm[sn + lane] : make_int2(0, row0);
 #pragma unroll
@@ -872,9 +895,10 @@ __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
           if (act) atomicAdd(reinterpret_cast<double *>(&tile[r][lane]), static_cast<double>(xr[e]));
           if (lane == 0) atomicAdd(&tcnt[r], 1);
         } else {
-          const uint64_t key = max_key(xr[e], __builtin_amdgcn_readlane(ev, e));
-          if (act && key != 0ull) atomicMax(reinterpret_cast<unsigned long long *>(&tile[r][lane]),
-                                            static_cast<unsigned long long>(key));
+          const uint32_t lo_base = (0x7fffffffu - static_cast<uint32_t>(__builtin_amdgcn_readlane(ev, e))) << 1;
+          if (act && !(xr[e] != xr[e]))   // NaN never wins
+            atomicMax(reinterpret_cast<unsigned long long *>(&tile[r][lane]),
+                      static_cast<unsigned long long>(max_key_part(xr[e], lo_base)));
         }
       }
     }
