@@ -230,6 +230,17 @@ __device__ __forceinline__ uint64_t pack_counts(int64_t cnt, int64_t chk) {
   return (b << 31) | a;
 }
 
+// Descriptor slot of chunk j of bucket b (ok: chunks of the buckets before
+// it, nch: its chunks, n_slots: the grid's slots): the full chunks of all
+// buckets at the bottom in bucket order (ok - b counts the full chunks
+// before bucket b), each bucket's last, partial chunk at n_slots - 1 - b.
+// The reduce grid therefore runs the 2048-event chunks first and the
+// partial ones in its last round.
+__host__ __device__ __forceinline__ int64_t chunk_slot(int64_t b, int64_t ok, int64_t j, int64_t nch,
+                                                       int64_t n_slots) {
+  return j + 1 < nch ? ok - b + j : n_slots - 1 - b;
+}
+
 // Chunks of a bucket of n events: at least one (so every bucket, empty or
 // not, has a workgroup that writes its rows).
 __device__ __forceinline__ int64_t bucket_chunks(int64_t n) { return max((n + kChunk - 1) / kChunk, (int64_t)1); }
@@ -380,10 +391,14 @@ __global__ __launch_bounds__(kScanCells *kScanTpc) void scan_kernel(
       coff[cell] = static_cast<int32_t>(ok);
     }
     // the bucket's chunk descriptors: a reduce workgroup finds its bucket
-    // and positions in one load
-    for (int64_t j = grp; j < mine_k && ok + j < n_cmax; j += kScanTpc) {
+    // and positions in one load.  Full chunks fill the slots from the
+    // bottom, every bucket's last (partial) chunk the slots from the top
+    // (chunk_slot), so the reduce grid runs the full chunks first.
+    for (int64_t j = grp; j < mine_k; j += kScanTpc) {
       const int64_t p0 = o + j * kChunk, p1 = min(p0 + static_cast<int64_t>(kChunk), o + mine);
-      cdesc[ok + j] = make_int4(static_cast<int>(cell), static_cast<int>(p0), static_cast<int>(p1),
+      const int64_t slot = chunk_slot(cell, ok, j, mine_k, n_cmax);
+      if (slot >= 0 && slot < n_cmax)
+        cdesc[slot] = make_int4(static_cast<int>(cell), static_cast<int>(p0), static_cast<int>(p1),
                                 static_cast<int>(mine_k));
     }
   }
@@ -833,7 +848,7 @@ __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
     const float *__restrict__ src, const int2 *__restrict__ perm, const int4 *__restrict__ cdesc,
     const int32_t *__restrict__ coff, int32_t NB, int32_t E, int C, int32_t n_out, float *__restrict__ out,
     int64_t *__restrict__ argmax, uint64_t *__restrict__ parts, int32_t *__restrict__ pcnt,
-    int32_t *__restrict__ arrive) {
+    int32_t *__restrict__ arrive, int32_t n_slots) {
   __shared__ uint64_t tile[kBucketRows][64];   // max keys, or fp64 sums
   __shared__ int32_t tcnt[kBucketRows];
   __shared__ int32_t s_last;
@@ -843,11 +858,12 @@ __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
   const int ncb = CT ? 1 : (C + 63) / 64;
   const int c = static_cast<int>(blockIdx.x) / ncb;
   const int cb = static_cast<int>(blockIdx.x) - c * ncb;
-  // the chunk count and this chunk's descriptor in one round trip (the
-  // grid covers the most chunks there can be; c is checked before use)
+  // the chunk count and this slot's descriptor in one round trip (the grid
+  // covers the most chunks there can be; slots between the full chunks and
+  // the buckets' last chunks hold none)
   const int32_t n_chunks = coff[NB];
   const int4 d = cdesc[c];
-  if (c >= n_chunks) return;   // workgroup-uniform
+  if (c >= n_chunks - NB && c < n_slots - NB) return;   // workgroup-uniform
   for (int i = threadIdx.x; i < kBucketRows * 64; i += 64 * kRedWaves) (&tile[0][0])[i] = 0ull;
   if (threadIdx.x < kBucketRows) tcnt[threadIdx.x] = 0;
   __syncthreads();
@@ -926,19 +942,19 @@ __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
   }
   // Write the bucket's rows: this chunk's tile, folded (for a bucket of
   // several chunks) with the other chunks' tiles in chunk order.
-  const int c0 = nch > 1 ? coff[b] : c;
+  const int ok = nch > 1 ? coff[b] : 0;
   for (int rr = w; rr < kBucketRows; rr += kRedWaves) {
     const int row = row0 + rr;
     if (row >= n_out || !act) continue;
     uint64_t key = MEAN ? 0ull : tile[rr][lane];
     double sum = 0.0;
     int64_t n = 0;
-    for (int cc = c0; cc < c0 + nch; cc += 4) {   // four tiles' loads in flight
+    for (int jj = 0; jj < nch; jj += 4) {   // four tiles' loads in flight
       uint64_t v[4];
       int32_t k[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int ch = min(cc + u, c0 + nch - 1);
+        const int ch = nch > 1 ? static_cast<int>(chunk_slot(b, ok, min(jj + u, nch - 1), nch, n_slots)) : c;
         if (ch == c) {
           v[u] = tile[rr][lane];
           k[u] = MEAN ? tcnt[rr] : 0;
@@ -952,7 +968,7 @@ __global__ __launch_bounds__(64 * kRedWaves) void bucket_reduce_kernel(
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (cc + u < c0 + nch) {
+        if (jj + u < nch) {
           if constexpr (MEAN) {
             sum += __longlong_as_double(static_cast<long long>(v[u]));
             n += k[u];
@@ -1068,11 +1084,11 @@ int run_scatter(const float *src, const int64_t *index, int64_t E, int C, int64_
     if (C == 64)
       hipLaunchKernelGGL((bucket_reduce_kernel<MEAN, 64>), dim3(static_cast<unsigned>(L.n_chunks * ncb)),
                          dim3(64 * kRedWaves), 0, st, src, perm, cdesc, coff, NB32, E32, C, n32, out, argmax, parts,
-                         pcnt, arrive);
+                         pcnt, arrive, static_cast<int32_t>(L.n_chunks));
     else
       hipLaunchKernelGGL((bucket_reduce_kernel<MEAN, 0>), dim3(static_cast<unsigned>(L.n_chunks * ncb)),
                          dim3(64 * kRedWaves), 0, st, src, perm, cdesc, coff, NB32, E32, C, n32, out, argmax, parts,
-                         pcnt, arrive);
+                         pcnt, arrive, static_cast<int32_t>(L.n_chunks));
   }
   return launch_status(name);
 }
