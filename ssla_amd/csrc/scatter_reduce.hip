@@ -33,9 +33,9 @@
 //           word.  It also writes one descriptor per chunk (bucket, first
 //           and last position, chunks of the bucket).
 // * bucket: (event, row) pairs placed at their bucket-grouped positions.
-// * bucket_reduce: one workgroup per chunk of at most 2048 events of one
-//           bucket (its descriptor is one load; 2048 gives config 4 about
-//           two chunks per bucket, so the workgroups fill the chip): a
+// * bucket_reduce: one workgroup per chunk of at most 1792 events of one
+//           bucket (its descriptor is one load; full chunks run first and
+//           each bucket's partial last chunk in the grid's last round): a
 //           64-row x 64-channel tile in LDS takes every event with
 //           LDS atomics (max: ds_max_u64 on a packed (orderable value,
 //           inverted event id) key, so the result does not depend on the
@@ -56,7 +56,7 @@ namespace ssla {
 namespace {
 
 #ifndef SSLA_SR_CHUNK
-#define SSLA_SR_CHUNK 2048
+#define SSLA_SR_CHUNK 1792
 #endif
 #ifndef SSLA_SR_RANGE
 #define SSLA_SR_RANGE 512
@@ -234,7 +234,7 @@ __device__ __forceinline__ uint64_t pack_counts(int64_t cnt, int64_t chk) {
 // it, nch: its chunks, n_slots: the grid's slots): the full chunks of all
 // buckets at the bottom in bucket order (ok - b counts the full chunks
 // before bucket b), each bucket's last, partial chunk at n_slots - 1 - b.
-// The reduce grid therefore runs the 2048-event chunks first and the
+// The reduce grid therefore runs the full chunks first and the
 // partial ones in its last round.
 __host__ __device__ __forceinline__ int64_t chunk_slot(int64_t b, int64_t ok, int64_t j, int64_t nch,
                                                        int64_t n_slots) {
