@@ -21,6 +21,9 @@
 // updating one state tile.
 #include "common.h"
 
+#ifndef SSLA_SS_IPW
+#define SSLA_SS_IPW 1
+#endif
 #ifndef SSLA_SS_WPB
 #define SSLA_SS_WPB 1
 #endif
@@ -28,7 +31,8 @@
 namespace ssla {
 namespace {
 
-constexpr int kStepWaves = SSLA_SS_WPB;   // wavefronts ((site, head) items) per workgroup
+constexpr int kStepWaves = SSLA_SS_WPB;   // wavefronts per workgroup
+constexpr int kStepItems = SSLA_SS_IPW;   // (site, head) items per wavefront
 
 // Sum over the lanes l, l ^ VL, l ^ 2 VL, ... (the row groups that hold one
 // float4 column): rotations inside each 16-lane DPP row (by 8, then by 4:
@@ -63,58 +67,77 @@ __global__ __launch_bounds__(64 * kStepWaves) void sparse_gla_step_kernel(
   const int lane = threadIdx.x & 63;
   // wavefront-uniform: the (site, head) indexing runs on the scalar unit
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int item = static_cast<int>(blockIdx.x) * kStepWaves + wv;   // n_active * H < 2^31 (host check)
-  if (item >= n_active * H) return;
-  const int i = item / H;
-  const int h = item % H;
+  const int n_items = n_active * H;   // < 2^31 (host check)
+  const int item0 = (static_cast<int>(blockIdx.x) * kStepWaves + wv) * kStepItems;
+  if (item0 >= n_items) return;
   const int vc = lane % VL;          // float4 column
   const int rg = lane / VL;          // row group: rows rg*RPL .. rg*RPL+RPL-1
-  const int64_t io = static_cast<int64_t>(i) * H + h;
-  // this (site, head)'s inputs first: they do not depend on the site index,
-  // so their loads overlap its load
-  const float4 vv = reinterpret_cast<const float4 *>(v + io * V)[vc];
-  float gg[RPL], kk[RPL], qq[RPL];
+  // every item's inputs first (they do not depend on the site index, so
+  // their loads overlap its load), then every item's state, then the math
+  float4 vv[kStepItems];
+  float gg[kStepItems][RPL], kk[kStepItems][RPL], qq[kStepItems][RPL];
+  int site[kStepItems];
 #pragma unroll
-  for (int r = 0; r < RPL; ++r) {
-    const int row = rg * RPL + r;
-    gg[r] = g[io * K + row];
-    kk[r] = k[io * K + row];
-    qq[r] = q[io * K + row];
+  for (int u = 0; u < kStepItems; ++u) {
+    const int item = min(item0 + u, n_items - 1);
+    const int64_t io = static_cast<int64_t>(item / H) * H + item % H;
+    vv[u] = reinterpret_cast<const float4 *>(v + io * V)[vc];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      const int row = rg * RPL + r;
+      gg[u][r] = g[io * K + row];
+      kk[u][r] = k[io * K + row];
+      qq[u][r] = q[io * K + row];
+    }
+    site[u] = site_idx[item / H];
   }
-  const int site = site_idx[i];
-  if (site < 0 || site >= n_sites || (i > 0 && site_idx[i - 1] >= site)) {
-    if (rg == 0) reinterpret_cast<float4 *>(o + io * V)[vc] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (status && lane == 0) __hip_atomic_store(status, SSLA_ERR_ARG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
-  float4 *S = reinterpret_cast<float4 *>(state + (static_cast<int64_t>(site) * H + h) * K * V);
-
-  float4 s[RPL];
+  float4 s[kStepItems][RPL];
+  bool ok[kStepItems];
 #pragma unroll
-  for (int r = 0; r < RPL; ++r) s[r] = S[(rg * RPL + r) * VL + vc];
-
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int u = 0; u < kStepItems; ++u) {
+    const int item = min(item0 + u, n_items - 1);
+    const int i = item / H, h = item % H;
+    ok[u] = item0 + u < n_items && site[u] >= 0 && site[u] < n_sites && !(i > 0 && site_idx[i - 1] >= site[u]);
+    if (ok[u]) {
+      const float4 *S = reinterpret_cast<const float4 *>(state + (static_cast<int64_t>(site[u]) * H + h) * K * V);
 #pragma unroll
-  for (int r = 0; r < RPL; ++r) {
-    const float d = fast_exp2(gg[r] * kLog2e);
-    const float qs = qq[r] * scale;
-    s[r].x = fmaf(d, s[r].x, kk[r] * vv.x);
-    s[r].y = fmaf(d, s[r].y, kk[r] * vv.y);
-    s[r].z = fmaf(d, s[r].z, kk[r] * vv.z);
-    s[r].w = fmaf(d, s[r].w, kk[r] * vv.w);
-    acc.x = fmaf(qs, s[r].x, acc.x);
-    acc.y = fmaf(qs, s[r].y, acc.y);
-    acc.z = fmaf(qs, s[r].z, acc.z);
-    acc.w = fmaf(qs, s[r].w, acc.w);
+      for (int r = 0; r < RPL; ++r) s[u][r] = S[(rg * RPL + r) * VL + vc];
+    }
   }
 #pragma unroll
-  for (int r = 0; r < RPL; ++r) S[(rg * RPL + r) * VL + vc] = s[r];
-
-  acc.x = sum_row_groups<VL>(acc.x);
-  acc.y = sum_row_groups<VL>(acc.y);
-  acc.z = sum_row_groups<VL>(acc.z);
-  acc.w = sum_row_groups<VL>(acc.w);
-  if (rg == 0) reinterpret_cast<float4 *>(o + io * V)[vc] = acc;
+  for (int u = 0; u < kStepItems; ++u) {
+    if (item0 + u >= n_items) break;   // wavefront-uniform
+    const int item = item0 + u;
+    const int h = item % H;
+    const int64_t io = static_cast<int64_t>(item / H) * H + h;
+    if (!ok[u]) {
+      if (rg == 0) reinterpret_cast<float4 *>(o + io * V)[vc] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (status && lane == 0) __hip_atomic_store(status, SSLA_ERR_ARG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      continue;
+    }
+    float4 *S = reinterpret_cast<float4 *>(state + (static_cast<int64_t>(site[u]) * H + h) * K * V);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      const float d = fast_exp2(gg[u][r] * kLog2e);
+      const float qs = qq[u][r] * scale;
+      s[u][r].x = fmaf(d, s[u][r].x, kk[u][r] * vv[u].x);
+      s[u][r].y = fmaf(d, s[u][r].y, kk[u][r] * vv[u].y);
+      s[u][r].z = fmaf(d, s[u][r].z, kk[u][r] * vv[u].z);
+      s[u][r].w = fmaf(d, s[u][r].w, kk[u][r] * vv[u].w);
+      acc.x = fmaf(qs, s[u][r].x, acc.x);
+      acc.y = fmaf(qs, s[u][r].y, acc.y);
+      acc.z = fmaf(qs, s[u][r].z, acc.z);
+      acc.w = fmaf(qs, s[u][r].w, acc.w);
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) S[(rg * RPL + r) * VL + vc] = s[u][r];
+    acc.x = sum_row_groups<VL>(acc.x);
+    acc.y = sum_row_groups<VL>(acc.y);
+    acc.z = sum_row_groups<VL>(acc.z);
+    acc.w = sum_row_groups<VL>(acc.w);
+    if (rg == 0) reinterpret_cast<float4 *>(o + io * V)[vc] = acc;
+  }
 }
 
 }  // namespace
@@ -135,7 +158,7 @@ extern "C" int ssla_sparse_gla_step(const int32_t *site_idx, int n_active, const
                  "sparse_gla_step: tensors must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t items = static_cast<int64_t>(n_active) * H;
-  const int64_t blocks = (items + kStepWaves - 1) / kStepWaves;
+  const int64_t blocks = (items + kStepWaves * kStepItems - 1) / (kStepWaves * kStepItems);
   SSLA_CHECK_ARG(items <= 0x7fffffff, "sparse_gla_step: too many active sites");
   dim3 grid(static_cast<unsigned>(blocks)), block(64 * kStepWaves);
 #define SSLA_STEP(KK, VV)                                                                       \
