@@ -185,21 +185,18 @@ __global__ __launch_bounds__(kEvThreads) void hist_kernel(
     __syncthreads();
     int64_t e0, e1;
     event_range(E, n_hist, blockIdx.x, e0, e1);
-    int64_t e = e0 + threadIdx.x;
-    for (; e + 7 * kEvThreads < e1; e += 8 * kEvThreads) {
+    // up to eight index loads per thread in flight at once (a range of
+    // 4096 events is four per thread: one round trip, not four)
+    for (int64_t e = e0 + threadIdx.x; e < e1; e += 8 * kEvThreads) {
       int64_t r[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) r[u] = index[e + u * kEvThreads];
+      for (int u = 0; u < 8; ++u) r[u] = e + u * kEvThreads < e1 ? index[e + u * kEvThreads] : 0;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
+        if (e + u * kEvThreads >= e1) break;
         if (bad_row(r[u], n_out)) bad = true;
         else atomicAdd(&lh[r[u] >> kBucketShift], 1);
       }
-    }
-    for (; e < e1; e += kEvThreads) {
-      const int64_t r = index[e];
-      if (bad_row(r, n_out)) bad = true;
-      else atomicAdd(&lh[r >> kBucketShift], 1);
     }
     __syncthreads();
     int32_t *row = hist + static_cast<int64_t>(blockIdx.x) * (NB + 1);
@@ -418,23 +415,18 @@ __global__ __launch_bounds__(kEvThreads) void bucket_kernel(
     __syncthreads();
     int64_t e0, e1;
     event_range(E, n_hist, blockIdx.x, e0, e1);
-    int64_t e = e0 + threadIdx.x;
-    for (; e + 7 * kEvThreads < e1; e += 8 * kEvThreads) {
+    // up to eight index loads per thread in flight at once, as in hist
+    for (int64_t e = e0 + threadIdx.x; e < e1; e += 8 * kEvThreads) {
       int64_t r[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) r[u] = index[e + u * kEvThreads];
+      for (int u = 0; u < 8; ++u) r[u] = e + u * kEvThreads < e1 ? index[e + u * kEvThreads] : -1;
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
+        if (e + u * kEvThreads >= e1) break;
         if (bad_row(r[u], n_out)) continue;
         const int32_t pos = atomicAdd(&lc[r[u] >> kBucketShift], 1);
         if (pos >= 0 && pos < E) perm[pos] = make_int2(static_cast<int32_t>(e + u * kEvThreads), static_cast<int32_t>(r[u]));
       }
-    }
-    for (; e < e1; e += kEvThreads) {
-      const int64_t r = index[e];
-      if (bad_row(r, n_out)) continue;
-      const int32_t pos = atomicAdd(&lc[r >> kBucketShift], 1);
-      if (pos >= 0 && pos < E) perm[pos] = make_int2(static_cast<int32_t>(e), static_cast<int32_t>(r));
     }
   } else {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kEvThreads;
@@ -452,22 +444,11 @@ __global__ __launch_bounds__(kEvThreads) void bucket_kernel(
 // Order-independent max key of (value x, event e): the value's bits made
 // unsigned-orderable (-0.0 taken as +0.0) in the high word; in the low word
 // the inverted event id (so the smallest id wins a tie) above the sign of a
-// zero (so the winner's -0.0 comes back).  NaN gives 0, which every event
-// beats: NaN never wins, and a row with no winner reads 0.  E < 2^31.
-__device__ __forceinline__ uint64_t max_key(float x, int32_t e) {
-  uint32_t u = __float_as_uint(x);
-  const bool zero = (u & 0x7fffffffu) == 0u;
-  const uint32_t neg_zero = (u == 0x80000000u) ? 1u : 0u;
-  if (zero) u = 0u;
-  const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  const uint32_t lo = ((0x7fffffffu - static_cast<uint32_t>(e)) << 1) | neg_zero;
-  const uint64_t key = (static_cast<uint64_t>(ord) << 32) | lo;
-  return (x != x) ? 0ull : key;
-}
-// The same key with its event part precomputed (lo_base = (0x7fffffff - e)
-// << 1, a wavefront-uniform value the scalar unit forms) and no NaN test:
-// the caller leaves NaN values out (their key would be 0, which never
-// changes a maximum).  Bit-identical to max_key for every other x.
+// zero (so the winner's -0.0 comes back).  E < 2^31.  The event part
+// lo_base = (0x7fffffff - e) << 1 is wavefront-uniform (the scalar unit
+// forms it).  NaN values have no key: the caller leaves them out of the
+// maximum (key 0 would mean the same: every event beats it), so NaN never
+// wins and a row with no winner reads 0.
 __device__ __forceinline__ uint64_t max_key_part(float x, uint32_t lo_base) {
   const uint32_t u = __float_as_uint(x);
   const uint32_t u0 = x != 0.f ? u : 0u;   // -0 folded onto +0
