@@ -96,15 +96,20 @@ def test_sorted_special_values(dev):
     assert np.array_equal(a_s.cpu().numpy(), ra)
 
 
-def test_many_rows_global_counting(dev):
-    """More output rows than the LDS histogram holds (global-counter path),
-    plus a row with several pieces."""
+@pytest.mark.parametrize("n_out", [40000, 300000])
+def test_many_rows_global_counting(dev, n_out):
+    """Many output rows: 625 buckets (LDS histogram) and 4688 buckets, more
+    than the LDS histogram holds (global-counter path, whose histogram kernel
+    also clears the chunk arrival counters), plus a row of 5000 events whose
+    bucket spans several reduce chunks (the last one to arrive folds)."""
     gen = torch.Generator().manual_seed(3)
-    E, C, n_out = 60000, 8, 40000
+    E, C = 60000, 8
     src = torch.randn(E, C, generator=gen)
     index = torch.randint(0, n_out, (E,), generator=gen)
-    index[:1000] = 7
+    index[:5000] = 7
     _check(dev, src, index, n_out)
+    # the same workspace shape again: counters left by the first call are cleared
+    _check(dev, src.flip(0).contiguous(), index.flip(0).contiguous(), n_out)
 
 
 def test_repeated_calls_reuse_workspace(dev):
